@@ -1,0 +1,196 @@
+// fp32 matmul on CDNA4 matrix cores with a fused epilogue.
+//
+// C[b] = A[b] · B[b] (A: [M, K], B: [K, N], row-major, batch stride M·K and
+// K·N), then out[i] = Epi(A, i, C[b][row][col]) with i = (b·M + row)·N + col:
+// the epilogue is the fused body of a matmul-epilogue group (bias broadcast,
+// activation, residual), applied while the accumulator is still in registers.
+//
+// Tiling: a workgroup of 256 threads (4 wavefronts in a 2 x 2 grid) owns a
+// BM x BN tile of C; each wavefront owns (TM·16) x (TN·16) of it as TM x TN
+// accumulators of v_mfma_f32_16x16x4f32 (D 16x16 += A 16x4 · B 4x16). K is
+// walked 16 at a time through two LDS buffers: the global loads of the next
+// slice are in flight while the current one feeds the matrix cores, and one
+// barrier per slice separates the two.
+//
+// Operand layout per lane of a 16x16x4 MFMA (lane = 16·q + t, t in 0..15):
+//   A value: row t, k-group q;  B value: column t, k-group q;
+//   D: column t, rows 4q .. 4q+3 (one per accumulator register).
+// Within a 16-wide K slice, lane group q supplies k = 4q + s at step s, so a
+// lane's four A values of a slice are contiguous in LDS (one ds_read_b128);
+// both operands use the same k for the same (q, s), so the product is exact
+// in what it sums, in an order the float32 budget already covers (any order
+// of K terms, gamma(K)).
+
+#pragma once
+
+#include "tcmi_device.h"
+
+namespace tcmi {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+template <int TM, int TN, bool VEC_A, bool VEC_B, class Epi>
+__device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restrict__ a_ptr,
+                                         const float* __restrict__ b_ptr) {
+  constexpr int BM = 2 * TM * 16;
+  constexpr int BN = 2 * TN * 16;
+  constexpr int BK = 16;
+  constexpr int AS = BK + 4;   // padded row stride of the A slice (conflict-free b128 reads)
+  constexpr int BS = BN + 4;   // padded row stride of the B slice
+  __shared__ __attribute__((aligned(16))) float As[2][BM * AS];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BK * BS];
+
+  const uint32_t M = A.P[1], K = A.P[2], N = A.P[3];
+  const uint32_t bz = blockIdx.z;
+  const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const float* __restrict__ Ab = a_ptr + (size_t)bz * M * K;
+  const float* __restrict__ Bb = b_ptr + (size_t)bz * K * N;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int t16 = lane & 15, q = lane >> 4;
+
+  // Per-thread staging registers for one K slice.
+  constexpr int A_VEC = (BM * BK / 4 + 255) / 256;   // float4 loads per thread
+  constexpr int B_VEC = (BK * BN / 4 + 255) / 256;
+  constexpr int A_SC = (BM * BK + 255) / 256;        // scalar loads per thread
+  constexpr int B_SC = (BK * BN + 255) / 256;
+  float4 ra[VEC_A ? A_VEC : 1];
+  float4 rb[VEC_B ? B_VEC : 1];
+  float sa[VEC_A ? 1 : A_SC];
+  float sb[VEC_B ? 1 : B_SC];
+
+  auto load_slice = [&](uint32_t k0) {
+    if (VEC_A) {
+#pragma unroll
+      for (int v = 0; v < A_VEC; ++v) {
+        const int t = tid + v * 256;
+        const uint32_t row = t >> 2, kk = (t & 3) * 4;
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (t < BM * BK / 4 && m0 + row < M && k0 + kk < K)
+          x = *reinterpret_cast<const float4*>(Ab + (size_t)(m0 + row) * K + k0 + kk);
+        ra[v] = x;
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < A_SC; ++v) {
+        const int t = tid + v * 256;
+        const uint32_t row = t / BK, kk = t % BK;
+        float x = 0.f;
+        if (t < BM * BK && m0 + row < M && k0 + kk < K) x = Ab[(size_t)(m0 + row) * K + k0 + kk];
+        sa[v] = x;
+      }
+    }
+    if (VEC_B) {
+#pragma unroll
+      for (int v = 0; v < B_VEC; ++v) {
+        const int t = tid + v * 256;
+        const uint32_t kk = t / (BN / 4), c = (t % (BN / 4)) * 4;
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (t < BK * BN / 4 && k0 + kk < K && n0 + c < N)
+          x = *reinterpret_cast<const float4*>(Bb + (size_t)(k0 + kk) * N + n0 + c);
+        rb[v] = x;
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < B_SC; ++v) {
+        const int t = tid + v * 256;
+        const uint32_t kk = t / BN, c = t % BN;
+        float x = 0.f;
+        if (t < BK * BN && k0 + kk < K && n0 + c < N) x = Bb[(size_t)(k0 + kk) * N + n0 + c];
+        sb[v] = x;
+      }
+    }
+  };
+
+  auto store_slice = [&](int buf) {
+    if (VEC_A) {
+#pragma unroll
+      for (int v = 0; v < A_VEC; ++v) {
+        const int t = tid + v * 256;
+        if (t < BM * BK / 4) {
+          const int row = t >> 2, kk = (t & 3) * 4;
+          *reinterpret_cast<float4*>(&As[buf][row * AS + kk]) = ra[v];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < A_SC; ++v) {
+        const int t = tid + v * 256;
+        if (t < BM * BK) As[buf][(t / BK) * AS + (t % BK)] = sa[v];
+      }
+    }
+    if (VEC_B) {
+#pragma unroll
+      for (int v = 0; v < B_VEC; ++v) {
+        const int t = tid + v * 256;
+        if (t < BK * BN / 4) {
+          const int kk = t / (BN / 4), c = (t % (BN / 4)) * 4;
+          *reinterpret_cast<float4*>(&Bs[buf][kk * BS + c]) = rb[v];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < B_SC; ++v) {
+        const int t = tid + v * 256;
+        if (t < BK * BN) Bs[buf][(t / BN) * BS + (t % BN)] = sb[v];
+      }
+    }
+  };
+
+  f4 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const uint32_t slices = (K + BK - 1) / BK;
+  load_slice(0);
+  store_slice(0);
+  __syncthreads();
+  for (uint32_t ks = 0; ks < slices; ++ks) {
+    const int cur = ks & 1;
+    if (ks + 1 < slices) load_slice((ks + 1) * BK);
+    // A values of this lane for every row tile: k = 4q .. 4q+3 of the slice.
+    float4 av[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      av[i] = *reinterpret_cast<const float4*>(&As[cur][(wm * TM * 16 + i * 16 + t16) * AS + 4 * q]);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      float bv[TN];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) bv[j] = Bs[cur][(4 * q + s) * BS + wn * TN * 16 + j * 16 + t16];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const float a = lane4(av[i], s);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv[j], acc[i][j], 0, 0, 0);
+      }
+    }
+    if (ks + 1 < slices) store_slice(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: the fused body on each accumulator element, then the store.
+  const Epi epi;
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const uint32_t col = n0 + wn * TN * 16 + j * 16 + t16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t row = m0 + wm * TM * 16 + i * 16 + 4 * q + r;
+        if (row < M && col < N) {
+          const uint32_t o = (bz * M + row) * N + col;
+          A.out[o] = epi(A, o, acc[i][j][r]);
+        }
+      }
+    }
+  }
+}
+
+}  // namespace tcmi

@@ -1,0 +1,595 @@
+// The C ABI of the MI355X backend (include/tcmi.h): device selection, checked
+// device memory, hiprtc compilation with an on-disk code-object cache, kernel
+// launches on one in-order stream, events and captured launch sequences.
+//
+// It replaces the WebGPU objects the reference's runner drives
+// (src/gpu/runtime.js:17-128 in abho7/tensor-compiler-webgpu): a buffer is a
+// device allocation whose size is recorded so that every copy can be checked
+// before it is issued; a pipeline is a hiprtc-compiled module; a dispatch is a
+// hipModuleLaunchKernel on the library stream; device.lost is a sticky flag set
+// by any fatal HIP error.
+//
+// Built with hipcc for gfx950: the file also holds the small fixed kernels
+// (canary fill, bandwidth ceilings) as ordinary device code.
+
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <algorithm>
+#include <atomic>
+#include <dirent.h>
+#include <cerrno>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <mutex>
+#include <sstream>
+#include <string>
+#include <sys/stat.h>
+#include <unistd.h>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/tcmi.h"
+
+namespace {
+
+thread_local std::string g_error;
+std::atomic<int> g_lost{0};
+bool g_init = false;
+int g_device = 0;
+hipStream_t g_stream = nullptr;
+hipDeviceProp_t g_props;
+std::string g_arch;        // "gfx950" (features stripped)
+std::string g_cache_dir;
+std::string g_include_dir;
+std::mutex g_mu;
+
+// Live allocations: device address -> size. Every copy is checked against it.
+std::map<uint64_t, uint64_t> g_allocs;
+std::unordered_map<uint64_t, hipModule_t> g_modules;   // handle -> module
+std::unordered_map<uint64_t, hipFunction_t> g_functions;
+std::unordered_map<uint64_t, hipEvent_t> g_events;
+std::unordered_map<uint64_t, std::pair<hipGraph_t, hipGraphExec_t>> g_graphs;
+uint64_t g_next_handle = 1;
+
+// Options every kernel is compiled with. Packed fp32 instructions are turned
+// off (they have produced silent wrong results on this pool), and floating
+// point contraction is off so that a fused body rounds exactly as the unfused
+// kernels do, op by op.
+const char* kBaseOptions =
+    "-O3 -std=c++17 -ffp-contract=off -fno-fast-math "
+    "-Xclang -target-feature -Xclang -packed-fp32-ops";
+
+int fail(int code, const std::string& msg) {
+  g_error = msg;
+  return code;
+}
+
+bool fatal_hip(hipError_t e) {
+  switch (e) {
+    case hipErrorIllegalAddress:
+    case hipErrorLaunchFailure:
+    case hipErrorAssert:
+    case hipErrorECCNotCorrectable:
+    case hipErrorLaunchTimeOut:
+      return true;
+    default:
+      return false;
+  }
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  if (fatal_hip(e)) g_lost = 1;
+  std::ostringstream s;
+  s << what << ": " << hipGetErrorName(e) << " (" << hipGetErrorString(e) << ")";
+  g_error = s.str();
+  return static_cast<int>(e);
+}
+
+#define HIP_TRY(call, what)                      \
+  do {                                           \
+    hipError_t e_ = (call);                      \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+int ready() {
+  if (!g_init) return fail(TCMI_E_NOT_INIT, "tcmi_init has not been called");
+  if (g_lost) return fail(TCMI_E_LOST, "device lost after an earlier fatal error");
+  return TCMI_OK;
+}
+
+// [base, base+size) must hold [addr+off, addr+off+bytes): `addr` may point
+// inside an allocation (a sub-buffer), as long as the whole range fits.
+bool range_ok(uint64_t addr, uint64_t off, uint64_t bytes) {
+  auto it = g_allocs.upper_bound(addr);
+  if (it == g_allocs.begin()) return false;
+  --it;
+  uint64_t base = it->first, size = it->second;
+  if (addr < base) return false;
+  uint64_t start = addr - base + off;
+  if (start < off) return false;  // overflow
+  return start <= size && bytes <= size - start;
+}
+
+// 128-bit FNV-1a style hash over several strings (two independent 64-bit lanes).
+std::string hash_hex(const std::vector<std::string>& parts) {
+  uint64_t h1 = 1469598103934665603ull, h2 = 0x9e3779b97f4a7c15ull;
+  for (const auto& p : parts) {
+    for (unsigned char c : p) {
+      h1 ^= c; h1 *= 1099511628211ull;
+      h2 ^= c + 0x5bu; h2 *= 0x100000001b3ull; h2 ^= h2 >> 29;
+    }
+    h1 ^= 0xff; h1 *= 1099511628211ull;
+    h2 ^= 0xfe; h2 *= 0x100000001b3ull;
+  }
+  char buf[33];
+  std::snprintf(buf, sizeof buf, "%016llx%016llx", (unsigned long long)h1, (unsigned long long)h2);
+  return buf;
+}
+
+bool read_file(const std::string& path, std::vector<char>& out) {
+  std::ifstream f(path, std::ios::binary);
+  if (!f) return false;
+  out.assign(std::istreambuf_iterator<char>(f), std::istreambuf_iterator<char>());
+  return true;
+}
+
+void mkdirs(const std::string& dir) {
+  std::string cur;
+  for (size_t i = 0; i < dir.size(); i++) {
+    cur += dir[i];
+    if (dir[i] == '/' && cur.size() > 1) mkdir(cur.c_str(), 0755);
+  }
+  mkdir(dir.c_str(), 0755);
+}
+
+bool write_file_atomic(const std::string& path, const std::vector<char>& data) {
+  std::string tmp = path + ".tmp" + std::to_string(getpid());
+  {
+    std::ofstream f(tmp, std::ios::binary);
+    if (!f) return false;
+    f.write(data.data(), static_cast<std::streamsize>(data.size()));
+    if (!f) return false;
+  }
+  return std::rename(tmp.c_str(), path.c_str()) == 0;
+}
+
+std::vector<std::string> split_options(const std::string& s) {
+  std::vector<std::string> out;
+  std::istringstream in(s);
+  std::string t;
+  while (in >> t) out.push_back(t);
+  return out;
+}
+
+int hiprtc_version_string(std::string& out) {
+  int major = 0, minor = 0;
+  if (hiprtcVersion(&major, &minor) != HIPRTC_SUCCESS) return fail(TCMI_E_COMPILE, "hiprtcVersion failed");
+  out = std::to_string(major) + "." + std::to_string(minor);
+  return TCMI_OK;
+}
+
+// Compile `source` for `arch`, or take the code object from the cache.
+int compile_code(const std::string& source, const std::string& extra, const std::string& arch,
+                 std::vector<char>& code) {
+  std::string ver;
+  if (int rc = hiprtc_version_string(ver)) return rc;
+  std::string options = std::string(kBaseOptions) + " " + extra;
+  // The include directory's headers are part of the key: read them whole.
+  std::vector<std::string> key_parts = {source, options, arch, ver, TCMI_BUILD_STAMP};
+  if (!g_include_dir.empty()) {
+    // Every header of the include directory, in name order.
+    std::vector<std::string> names;
+    if (DIR* d = opendir(g_include_dir.c_str())) {
+      while (dirent* e = readdir(d)) {
+        std::string nm = e->d_name;
+        if (nm.size() > 2 && nm.compare(nm.size() - 2, 2, ".h") == 0) names.push_back(nm);
+      }
+      closedir(d);
+    }
+    std::sort(names.begin(), names.end());
+    for (const auto& nm : names) {
+      std::vector<char> h;
+      if (read_file(g_include_dir + "/" + nm, h)) {
+        key_parts.push_back(nm);
+        key_parts.emplace_back(h.begin(), h.end());
+      }
+    }
+  }
+  std::string key = hash_hex(key_parts);
+  std::string path;
+  if (!g_cache_dir.empty()) {
+    path = g_cache_dir + "/" + key + ".co";
+    if (read_file(path, code) && !code.empty()) return TCMI_OK;
+  }
+  hiprtcProgram prog;
+  if (hiprtcCreateProgram(&prog, source.c_str(), "tcmi_kernels.hip", 0, nullptr, nullptr) != HIPRTC_SUCCESS)
+    return fail(TCMI_E_COMPILE, "hiprtcCreateProgram failed");
+  std::vector<std::string> opts = split_options(options);
+  opts.push_back("--offload-arch=" + arch);
+  if (!g_include_dir.empty()) opts.push_back("-I" + g_include_dir);
+  std::vector<const char*> copts;
+  for (auto& o : opts) copts.push_back(o.c_str());
+  hiprtcResult r = hiprtcCompileProgram(prog, static_cast<int>(copts.size()), copts.data());
+  size_t log_size = 0;
+  hiprtcGetProgramLogSize(prog, &log_size);
+  std::string log(log_size, '\0');
+  if (log_size) hiprtcGetProgramLog(prog, &log[0]);
+  if (r != HIPRTC_SUCCESS) {
+    hiprtcDestroyProgram(&prog);
+    return fail(TCMI_E_COMPILE, std::string("hiprtc: ") + hiprtcGetErrorString(r) + "\n" + log);
+  }
+  size_t n = 0;
+  hiprtcGetCodeSize(prog, &n);
+  code.resize(n);
+  hiprtcGetCode(prog, code.data());
+  hiprtcDestroyProgram(&prog);
+  if (!path.empty()) {
+    mkdirs(g_cache_dir);
+    write_file_atomic(path, code);  // a cache that cannot be written only costs time
+  }
+  return TCMI_OK;
+}
+
+// ---- fixed kernels ---------------------------------------------------------------
+
+__global__ void __launch_bounds__(256) k_fill32(uint32_t* __restrict__ dst, uint32_t value, uint64_t count) {
+  uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+  for (; i < count; i += stride) dst[i] = value;
+}
+
+__global__ void __launch_bounds__(256) k_copy16(uint4* __restrict__ dst, const uint4* __restrict__ src, uint64_t n16) {
+  uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+  uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256;
+  for (; i < n16; i += stride) dst[i] = src[i];
+}
+
+__global__ void __launch_bounds__(256) k_read16(uint32_t* __restrict__ dst, const uint4* __restrict__ src, uint64_t n16) {
+  uint64_t t = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+  uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256;
+  uint4 acc = make_uint4(0, 0, 0, 0);
+  for (uint64_t i = t; i < n16; i += stride) {
+    uint4 v = src[i];
+    acc.x ^= v.x; acc.y ^= v.y; acc.z ^= v.z; acc.w ^= v.w;
+  }
+  dst[t] = acc.x ^ acc.y ^ acc.z ^ acc.w;
+}
+
+int check_launch_shape(const uint32_t grid[3], const uint32_t block[3], uint32_t lds) {
+  for (int d = 0; d < 3; d++) {
+    if (grid[d] == 0 || block[d] == 0) return fail(TCMI_E_INVALID, "launch: zero grid or block dimension");
+    if (static_cast<int64_t>(grid[d]) > static_cast<int64_t>(g_props.maxGridSize[d]))
+      return fail(TCMI_E_INVALID, "launch: grid dimension above the device limit");
+    if (static_cast<int>(block[d]) > g_props.maxThreadsDim[d])
+      return fail(TCMI_E_INVALID, "launch: block dimension above the device limit");
+  }
+  uint64_t threads = static_cast<uint64_t>(block[0]) * block[1] * block[2];
+  if (threads > static_cast<uint64_t>(g_props.maxThreadsPerBlock))
+    return fail(TCMI_E_INVALID, "launch: more threads per block than the device allows");
+  if (lds > g_props.sharedMemPerBlock) return fail(TCMI_E_INVALID, "launch: dynamic LDS above the device limit");
+  return TCMI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int tcmi_init(void) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  if (g_init) return g_lost ? fail(TCMI_E_LOST, "device lost") : TCMI_OK;
+  int count = 0;
+  HIP_TRY(hipGetDeviceCount(&count), "hipGetDeviceCount");
+  if (count < 1) return fail(TCMI_E_INVALID, "no HIP device");
+  g_device = 0;
+  HIP_TRY(hipSetDevice(g_device), "hipSetDevice");
+  HIP_TRY(hipGetDeviceProperties(&g_props, g_device), "hipGetDeviceProperties");
+  g_arch = g_props.gcnArchName;
+  size_t colon = g_arch.find(':');
+  if (colon != std::string::npos) g_arch = g_arch.substr(0, colon);
+  // Default priority, non-blocking with respect to the null stream.
+  HIP_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+  g_init = true;
+  return TCMI_OK;
+}
+
+int tcmi_device_info_get(tcmi_device_info* out) {
+  if (int rc = ready()) return rc;
+  if (!out) return fail(TCMI_E_INVALID, "null output");
+  std::memset(out, 0, sizeof *out);
+  std::snprintf(out->name, sizeof out->name, "%s", g_props.name);
+  std::snprintf(out->arch, sizeof out->arch, "%s", g_props.gcnArchName);
+  out->compute_units = g_props.multiProcessorCount;
+  out->clock_khz = g_props.clockRate;
+  out->memory_clock_khz = g_props.memoryClockRate;
+  out->memory_bus_width = g_props.memoryBusWidth;
+  out->total_memory = g_props.totalGlobalMem;
+  out->l2_bytes = g_props.l2CacheSize;
+  out->lds_bytes_per_block = static_cast<int32_t>(g_props.sharedMemPerBlock);
+  out->warp_size = g_props.warpSize;
+  out->max_threads_per_block = g_props.maxThreadsPerBlock;
+  return TCMI_OK;
+}
+
+int tcmi_lost(void) { return g_lost.load(); }
+const char* tcmi_last_error(void) { return g_error.c_str(); }
+const char* tcmi_version(void) { return "tcmi 0.1 (" TCMI_BUILD_STAMP ")"; }
+const char* tcmi_compile_options(void) { return kBaseOptions; }
+
+int tcmi_malloc(uint64_t bytes, uint64_t* handle) {
+  if (int rc = ready()) return rc;
+  if (!handle) return fail(TCMI_E_INVALID, "null handle");
+  void* p = nullptr;
+  HIP_TRY(hipMalloc(&p, bytes ? bytes : 4), "hipMalloc");
+  g_allocs[reinterpret_cast<uint64_t>(p)] = bytes ? bytes : 4;
+  *handle = reinterpret_cast<uint64_t>(p);
+  return TCMI_OK;
+}
+
+int tcmi_free(uint64_t handle) {
+  if (!g_init) return fail(TCMI_E_NOT_INIT, "tcmi_init has not been called");
+  auto it = g_allocs.find(handle);
+  if (it == g_allocs.end()) return fail(TCMI_E_INVALID, "tcmi_free: unknown allocation");
+  g_allocs.erase(it);
+  // Work already queued may still read it: free after the stream drains.
+  hipError_t e = hipStreamSynchronize(g_stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize before free");
+  HIP_TRY(hipFree(reinterpret_cast<void*>(handle)), "hipFree");
+  return TCMI_OK;
+}
+
+int tcmi_size(uint64_t handle, uint64_t* bytes) {
+  auto it = g_allocs.find(handle);
+  if (it == g_allocs.end()) return fail(TCMI_E_INVALID, "tcmi_size: unknown allocation");
+  *bytes = it->second;
+  return TCMI_OK;
+}
+
+int tcmi_h2d(uint64_t dst, uint64_t dst_offset, const void* src, uint64_t bytes) {
+  if (int rc = ready()) return rc;
+  if (!bytes) return TCMI_OK;
+  if (!src || !range_ok(dst, dst_offset, bytes)) return fail(TCMI_E_INVALID, "tcmi_h2d: range outside the allocation");
+  HIP_TRY(hipMemcpyAsync(reinterpret_cast<char*>(dst) + dst_offset, src, bytes, hipMemcpyHostToDevice, g_stream),
+          "hipMemcpyAsync H2D");
+  HIP_TRY(hipStreamSynchronize(g_stream), "hipStreamSynchronize after H2D");
+  return TCMI_OK;
+}
+
+int tcmi_d2h(void* dst, uint64_t src, uint64_t src_offset, uint64_t bytes) {
+  if (int rc = ready()) return rc;
+  if (!bytes) return TCMI_OK;
+  if (!dst || !range_ok(src, src_offset, bytes)) return fail(TCMI_E_INVALID, "tcmi_d2h: range outside the allocation");
+  HIP_TRY(hipMemcpyAsync(dst, reinterpret_cast<char*>(src) + src_offset, bytes, hipMemcpyDeviceToHost, g_stream),
+          "hipMemcpyAsync D2H");
+  HIP_TRY(hipStreamSynchronize(g_stream), "hipStreamSynchronize after D2H");
+  return TCMI_OK;
+}
+
+int tcmi_d2d(uint64_t dst, uint64_t dst_offset, uint64_t src, uint64_t src_offset, uint64_t bytes) {
+  if (int rc = ready()) return rc;
+  if (!bytes) return TCMI_OK;
+  if (!range_ok(dst, dst_offset, bytes) || !range_ok(src, src_offset, bytes))
+    return fail(TCMI_E_INVALID, "tcmi_d2d: range outside an allocation");
+  HIP_TRY(hipMemcpyAsync(reinterpret_cast<char*>(dst) + dst_offset, reinterpret_cast<char*>(src) + src_offset, bytes,
+                         hipMemcpyDeviceToDevice, g_stream),
+          "hipMemcpyAsync D2D");
+  return TCMI_OK;
+}
+
+int tcmi_fill32(uint64_t dst, uint64_t offset, uint32_t value, uint64_t count) {
+  if (int rc = ready()) return rc;
+  if (!count) return TCMI_OK;
+  if (offset % 4 || count > (UINT64_MAX / 4) || !range_ok(dst, offset, count * 4))
+    return fail(TCMI_E_INVALID, "tcmi_fill32: range outside the allocation or misaligned");
+  uint64_t blocks = (count + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(k_fill32, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, g_stream,
+                     reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(dst) + offset), value, count);
+  HIP_TRY(hipGetLastError(), "k_fill32 launch");
+  return TCMI_OK;
+}
+
+int tcmi_count_not32(uint64_t src, uint64_t offset, uint32_t value, uint64_t count, uint64_t* mismatches) {
+  if (int rc = ready()) return rc;
+  if (!mismatches) return fail(TCMI_E_INVALID, "null output");
+  *mismatches = 0;
+  if (!count) return TCMI_OK;
+  if (offset % 4 || count > (UINT64_MAX / 4) || !range_ok(src, offset, count * 4))
+    return fail(TCMI_E_INVALID, "tcmi_count_not32: range outside the allocation or misaligned");
+  std::vector<uint32_t> host(count);
+  if (int rc = tcmi_d2h(host.data(), src, offset, count * 4)) return rc;
+  uint64_t bad = 0;
+  for (uint32_t w : host) bad += (w != value);
+  *mismatches = bad;
+  return TCMI_OK;
+}
+
+int tcmi_set_cache_dir(const char* dir) {
+  g_cache_dir = dir ? dir : "";
+  return TCMI_OK;
+}
+
+int tcmi_set_include_dir(const char* dir) {
+  g_include_dir = dir ? dir : "";
+  return TCMI_OK;
+}
+
+int tcmi_module_compile(const char* source, const char* extra_options, uint64_t* module) {
+  if (int rc = ready()) return rc;
+  if (!source || !module) return fail(TCMI_E_INVALID, "null argument");
+  std::vector<char> code;
+  if (int rc = compile_code(source, extra_options ? extra_options : "", g_arch, code)) return rc;
+  hipModule_t m;
+  HIP_TRY(hipModuleLoadData(&m, code.data()), "hipModuleLoadData");
+  uint64_t h = g_next_handle++;
+  g_modules[h] = m;
+  *module = h;
+  return TCMI_OK;
+}
+
+int tcmi_precompile(const char* source, const char* extra_options, const char* arch) {
+  if (!source || !arch) return fail(TCMI_E_INVALID, "null argument");
+  if (g_cache_dir.empty()) return fail(TCMI_E_IO, "tcmi_precompile: no cache directory set");
+  std::vector<char> code;
+  return compile_code(source, extra_options ? extra_options : "", arch, code);
+}
+
+int tcmi_module_function(uint64_t module, const char* name, uint64_t* function) {
+  if (int rc = ready()) return rc;
+  auto it = g_modules.find(module);
+  if (it == g_modules.end() || !name || !function) return fail(TCMI_E_INVALID, "tcmi_module_function: bad module or name");
+  hipFunction_t f;
+  HIP_TRY(hipModuleGetFunction(&f, it->second, name), (std::string("hipModuleGetFunction ") + name).c_str());
+  uint64_t h = g_next_handle++;
+  g_functions[h] = f;
+  *function = h;
+  return TCMI_OK;
+}
+
+int tcmi_module_unload(uint64_t module) {
+  if (!g_init) return fail(TCMI_E_NOT_INIT, "tcmi_init has not been called");
+  auto it = g_modules.find(module);
+  if (it == g_modules.end()) return fail(TCMI_E_INVALID, "tcmi_module_unload: unknown module");
+  hipError_t e = hipStreamSynchronize(g_stream);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize before unload");
+  HIP_TRY(hipModuleUnload(it->second), "hipModuleUnload");
+  g_modules.erase(it);
+  return TCMI_OK;
+}
+
+int tcmi_function_attrs(uint64_t function, int32_t* vgprs, int32_t* sgprs, int32_t* lds_bytes, int32_t* max_threads) {
+  if (int rc = ready()) return rc;
+  auto it = g_functions.find(function);
+  if (it == g_functions.end()) return fail(TCMI_E_INVALID, "tcmi_function_attrs: unknown function");
+  hipFuncAttributes a;
+  HIP_TRY(hipFuncGetAttributes(&a, reinterpret_cast<const void*>(it->second)), "hipFuncGetAttributes");
+  if (vgprs) *vgprs = -1;  // not reported through this API on ROCm
+  if (sgprs) *sgprs = -1;
+  if (lds_bytes) *lds_bytes = static_cast<int32_t>(a.sharedSizeBytes);
+  if (max_threads) *max_threads = a.maxThreadsPerBlock;
+  return TCMI_OK;
+}
+
+int tcmi_launch(uint64_t function, const uint32_t grid[3], const uint32_t block[3], uint32_t lds_bytes,
+                const void* args, uint64_t args_bytes) {
+  if (int rc = ready()) return rc;
+  auto it = g_functions.find(function);
+  if (it == g_functions.end()) return fail(TCMI_E_INVALID, "tcmi_launch: unknown function");
+  if (!grid || !block) return fail(TCMI_E_INVALID, "tcmi_launch: null grid or block");
+  if (int rc = check_launch_shape(grid, block, lds_bytes)) return rc;
+  if (args_bytes > 4096 || (args_bytes && !args)) return fail(TCMI_E_INVALID, "tcmi_launch: bad argument block");
+  size_t size = static_cast<size_t>(args_bytes);
+  void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<void*>(args), HIP_LAUNCH_PARAM_BUFFER_SIZE, &size,
+                    HIP_LAUNCH_PARAM_END};
+  HIP_TRY(hipModuleLaunchKernel(it->second, grid[0], grid[1], grid[2], block[0], block[1], block[2], lds_bytes,
+                                g_stream, nullptr, args_bytes ? config : nullptr),
+          "hipModuleLaunchKernel");
+  return TCMI_OK;
+}
+
+int tcmi_sync(void) {
+  if (int rc = ready()) return rc;
+  HIP_TRY(hipStreamSynchronize(g_stream), "hipStreamSynchronize");
+  return TCMI_OK;
+}
+
+int tcmi_event_create(uint64_t* event) {
+  if (int rc = ready()) return rc;
+  hipEvent_t e;
+  HIP_TRY(hipEventCreate(&e), "hipEventCreate");
+  uint64_t h = g_next_handle++;
+  g_events[h] = e;
+  *event = h;
+  return TCMI_OK;
+}
+
+int tcmi_event_record(uint64_t event) {
+  if (int rc = ready()) return rc;
+  auto it = g_events.find(event);
+  if (it == g_events.end()) return fail(TCMI_E_INVALID, "unknown event");
+  HIP_TRY(hipEventRecord(it->second, g_stream), "hipEventRecord");
+  return TCMI_OK;
+}
+
+int tcmi_event_elapsed(uint64_t start, uint64_t end, float* ms) {
+  if (int rc = ready()) return rc;
+  auto a = g_events.find(start), b = g_events.find(end);
+  if (a == g_events.end() || b == g_events.end() || !ms) return fail(TCMI_E_INVALID, "unknown event");
+  HIP_TRY(hipEventSynchronize(b->second), "hipEventSynchronize");
+  HIP_TRY(hipEventElapsedTime(ms, a->second, b->second), "hipEventElapsedTime");
+  return TCMI_OK;
+}
+
+int tcmi_event_destroy(uint64_t event) {
+  auto it = g_events.find(event);
+  if (it == g_events.end()) return fail(TCMI_E_INVALID, "unknown event");
+  (void)hipEventDestroy(it->second);
+  g_events.erase(it);
+  return TCMI_OK;
+}
+
+int tcmi_capture_begin(void) {
+  if (int rc = ready()) return rc;
+  HIP_TRY(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  return TCMI_OK;
+}
+
+int tcmi_capture_end(uint64_t* graph) {
+  if (int rc = ready()) return rc;
+  hipGraph_t g;
+  HIP_TRY(hipStreamEndCapture(g_stream, &g), "hipStreamEndCapture");
+  hipGraphExec_t x;
+  hipError_t e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(g);
+    return hip_fail(e, "hipGraphInstantiate");
+  }
+  uint64_t h = g_next_handle++;
+  g_graphs[h] = {g, x};
+  *graph = h;
+  return TCMI_OK;
+}
+
+int tcmi_graph_launch(uint64_t graph) {
+  if (int rc = ready()) return rc;
+  auto it = g_graphs.find(graph);
+  if (it == g_graphs.end()) return fail(TCMI_E_INVALID, "unknown graph");
+  HIP_TRY(hipGraphLaunch(it->second.second, g_stream), "hipGraphLaunch");
+  return TCMI_OK;
+}
+
+int tcmi_graph_destroy(uint64_t graph) {
+  auto it = g_graphs.find(graph);
+  if (it == g_graphs.end()) return fail(TCMI_E_INVALID, "unknown graph");
+  (void)hipStreamSynchronize(g_stream);
+  (void)hipGraphExecDestroy(it->second.second);
+  (void)hipGraphDestroy(it->second.first);
+  g_graphs.erase(it);
+  return TCMI_OK;
+}
+
+int tcmi_ceiling_copy(uint64_t dst, uint64_t src, uint64_t bytes, uint32_t blocks) {
+  if (int rc = ready()) return rc;
+  if (bytes % 16 || !blocks || !range_ok(dst, 0, bytes) || !range_ok(src, 0, bytes))
+    return fail(TCMI_E_INVALID, "tcmi_ceiling_copy: bad range");
+  hipLaunchKernelGGL(k_copy16, dim3(blocks), dim3(256), 0, g_stream, reinterpret_cast<uint4*>(dst),
+                     reinterpret_cast<const uint4*>(src), bytes / 16);
+  HIP_TRY(hipGetLastError(), "k_copy16 launch");
+  return TCMI_OK;
+}
+
+int tcmi_ceiling_read(uint64_t dst, uint64_t src, uint64_t bytes, uint32_t blocks) {
+  if (int rc = ready()) return rc;
+  if (bytes % 16 || !blocks || !range_ok(src, 0, bytes) || !range_ok(dst, 0, static_cast<uint64_t>(blocks) * 256 * 4))
+    return fail(TCMI_E_INVALID, "tcmi_ceiling_read: bad range");
+  hipLaunchKernelGGL(k_read16, dim3(blocks), dim3(256), 0, g_stream, reinterpret_cast<uint32_t*>(dst),
+                     reinterpret_cast<const uint4*>(src), bytes / 16);
+  HIP_TRY(hipGetLastError(), "k_read16 launch");
+  return TCMI_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,197 @@
+#!/usr/bin/env node
+'use strict';
+// Command-line entry to the host side, for harnesses in other processes
+// (the Python tests and bench). Usage:
+//
+//   node tool.js <command> [request.json] [--out DIR]
+//
+// CPU commands print one JSON document on stdout:
+//   builder-cases    the hand-built graphs of the reference's exported cases
+//   grad             request {cases: [{name, graph, outputs}]} -> gradient graphs
+//   fuse             request {graphs: [{name, graph, keep, recompute?, sabotage?}]} -> fused graphs
+//   lower            request {graph, fuse?: {keep}} -> launch records (sources omitted)
+//   model-fusion     fusion summaries of the reference's transformer forward pass and Adam step
+//   direct-catalogue the direct adversarial cases: names, kinds, patterns, and what fuse() makes of each
+//   transformer-init the reference transformer (golden config) forward + gradient graph and its inputs
+// GPU commands write a bundle (manifest.json + data.f32) under --out:
+//   gpu-direct       every direct case, fused, canary-padded, on the GPU
+//   gpu-graphs       request {graphs: [{name, graph, inputs, keep, unfused?}]} fused (and unfused) on the GPU
+
+const fs = require('fs');
+const path = require('path');
+const { Graph } = require('../src/ir/graph');
+const { grad } = require('../src/autodiff');
+const { fuse, fusionSummary } = require('../src/fusion/fuse');
+const { lowerMI355X } = require('../src/mi355x/lower');
+const { builderCases } = require('../src/testing/cases');
+const { fusedDirectCases } = require('../src/builders/direct_cases');
+const tf = require('../src/builders/transformer');
+const { Bundle } = require('../src/testing/bundle');
+
+function readRequest(argv) {
+  const file = argv.find((a, i) => i > 0 && !a.startsWith('--') && argv[i - 1] !== '--out');
+  if (!file) return {};
+  return JSON.parse(fs.readFileSync(file, 'utf8'));
+}
+
+function outDir(argv) {
+  const i = argv.indexOf('--out');
+  if (i < 0 || !argv[i + 1]) throw new Error('--out DIR is required');
+  return argv[i + 1];
+}
+
+const fusedOut = (f) => ({
+  graph: f.graph.toJSON(), origin: f.origin,
+  groups: f.groups.map((g) => ({ sink: g.sink, members: Array.from(g.members), kind: g.kind, root: g.root, pattern: g.pattern })),
+});
+
+function modelFusion() {
+  const cfg = tf.REFERENCE_CONFIG;
+  const V = 16, B = 4;
+  const fwd = tf.buildForward(V, B, cfg);
+  const step = tf.buildStep(V, B, cfg, tf.ADAM_3B);
+  const out = [];
+  const cases = [
+    { label: 'forward', graph: fwd.graph, keep: [fwd.logits, fwd.loss] },
+    { label: 'step', graph: step.graph, keep: [step.loss, step.logits].concat(Object.values(step.outputs)) },
+  ];
+  for (const c of cases) {
+    const f = fuse(c.graph, { keep: c.keep });
+    const epilogues = f.groups.filter((g) => g.kind === 'epilogue');
+    const withActivation = epilogues.filter((g) => Array.from(g.members).some((id) => ['tanh', 'relu'].includes(c.graph.nodes[id].op))).length;
+    let threw = null;
+    try { fuse(c.graph, { keep: c.keep, sabotage: 'fusion-absorbs-shared' }); } catch (e) { threw = String(e.message); }
+    out.push(Object.assign({ graph: c.label }, fusionSummary(c.graph, f), { epilogues: epilogues.length, epiloguesWithActivation: withActivation,
+      passSabotageError: threw, unfusedLaunches: lowerMI355X(c.graph).launches.length, fusedLaunches: lowerMI355X(f.graph).launches.length }));
+  }
+  return out;
+}
+
+function directCatalogue() {
+  return fusedDirectCases().map((c) => {
+    const f = fuse(c.graph);
+    const launched = f.graph.nodes.filter((n) => n.op !== 'input' && n.op !== 'const');
+    return { name: c.name, kind: c.kind, pattern: c.pattern, matmul: c.matmul || null,
+      launched: launched.map((n) => ({ op: n.op, kind: n.attrs.kind || null, pattern: n.attrs.pattern || null })),
+      graph: c.graph.toJSON(), inputs: c.inputs };
+  });
+}
+
+function transformerInit(req) {
+  const cfg = Object.assign({}, tf.REFERENCE_CONFIG);
+  const V = req.V || 16, B = req.batch || 4, seed = req.seed || 1;
+  const fwd = tf.buildForward(V, B, cfg);
+  const names = tf.paramSpec(V, cfg).map((s) => s[0]);
+  const G = grad(fwd.graph, [fwd.loss], names.map((n) => fwd.ids[n]));
+  const params = tf.initParams(V, seed, cfg);
+  const { x, y } = tf.encodeBatch(req.firstBatch, V, cfg.T);
+  return { graph: G.graph.toJSON(), logits: fwd.logits, loss: fwd.loss, names, grads: G.grads, cotangent: G.cotangents[0],
+    params, x: Array.from(x), y: Array.from(y) };
+}
+
+/** Compile, offline, the kernels a named group of GPU runs will ask for (same module text as on the box). */
+function precompileGroup(group, arch) {
+  const { precompile } = require('../src/mi355x/runner');
+  if (group === 'direct') return precompile(fusedDirectCases().map((c) => lowerMI355X(fuse(c.graph).graph)), arch);
+  throw new Error(`unknown precompile group '${group}'`);
+}
+
+async function gpuDirect(dir) {
+  const { HipRunner } = require('../src/mi355x/runner');
+  const runner = HipRunner.create();
+  const bundle = new Bundle(dir);
+  const cases = fusedDirectCases();
+  const plans = cases.map((c) => { const f = fuse(c.graph); return { f, lowered: lowerMI355X(f.graph) }; });
+  process.stderr.write(`gpu-direct: compiling ${plans.length} launch lists\n`);
+  runner.functions(plans.map((p) => p.lowered));
+  for (const [k, c] of cases.entries()) {
+    process.stderr.write(`gpu-direct: ${c.name}\n`);
+    const { f, lowered } = plans[k];
+    const inputs = {};
+    for (const n of c.graph.inputs()) inputs[n.attrs.name] = Float32Array.from(c.inputs[n.attrs.name]);
+    const r = await runner.run(f.graph, lowered, inputs, { canary: true });
+    const gpu = {};
+    f.graph.nodes.forEach((n) => { gpu[n.id] = bundle.put(r.values[n.id]); });
+    const ins = {};
+    for (const k of Object.keys(inputs)) ins[k] = bundle.put(inputs[k]);
+    bundle.add({ name: c.name, kind: c.kind, pattern: c.pattern, graph: c.graph.toJSON(), fused: f.graph.toJSON(), origin: f.origin,
+      inputs: ins, gpu, canaryIntact: r.canaryIntact, launches: lowered.launches.map((l) => ({ node: l.node, kind: l.kind, code: l.code })) });
+  }
+  bundle.close({ device: runner.info() });
+}
+
+async function gpuGraphs(req, dir) {
+  const { HipRunner } = require('../src/mi355x/runner');
+  const runner = HipRunner.create();
+  const bundle = new Bundle(dir);
+  for (const c of req.graphs) {
+    process.stderr.write(`gpu-graphs: ${c.name}\n`);
+    const g = Graph.fromJSON(c.graph);
+    const inputs = {};
+    for (const n of g.inputs()) inputs[n.attrs.name] = Float32Array.from(c.inputs[n.attrs.name]);
+    const f = fuse(g, { keep: c.keep || [] });
+    const lf = lowerMI355X(f.graph);
+    const rf = await runner.run(f.graph, lf, inputs, { canary: true });
+    const entry = { name: c.name, fused: f.graph.toJSON(), origin: f.origin, gpuFused: {}, canaryFused: rf.canaryIntact };
+    f.graph.nodes.forEach((n) => { entry.gpuFused[n.id] = bundle.put(rf.values[n.id]); });
+    if (c.unfused) {
+      const lu = lowerMI355X(g);
+      const ru = await runner.run(g, lu, inputs, { canary: true });
+      entry.gpuUnfused = {};
+      g.nodes.forEach((n) => { entry.gpuUnfused[n.id] = bundle.put(ru.values[n.id]); });
+      entry.canaryUnfused = ru.canaryIntact;
+    }
+    bundle.add(entry);
+  }
+  bundle.close({ device: runner.info() });
+}
+
+async function main() {
+  const argv = process.argv.slice(2);
+  const cmd = argv[0];
+  const req = readRequest(argv);
+  let out;
+  switch (cmd) {
+    case 'builder-cases': out = builderCases(); break;
+    case 'grad':
+      out = req.cases.map((c) => {
+        const g = Graph.fromJSON(c.graph);
+        const G = grad(g, c.outputs, g.inputs().map((n) => n.id));
+        return { name: c.name, graph: G.graph.toJSON(), grads: G.grads, cotangents: G.cotangents };
+      });
+      break;
+    case 'fuse':
+      out = req.graphs.map((c) => {
+        const g = Graph.fromJSON(c.graph);
+        try {
+          const f = fuse(g, { keep: c.keep || [], recompute: !!c.recompute, sabotage: c.sabotage });
+          return Object.assign({ name: c.name, summary: fusionSummary(g, f) }, fusedOut(f));
+        } catch (e) {
+          return { name: c.name, error: String(e.message) };
+        }
+      });
+      break;
+    case 'lower': {
+      const g = Graph.fromJSON(req.graph);
+      const target = req.fuse ? fuse(g, { keep: req.fuse.keep || [] }).graph : g;
+      const l = lowerMI355X(target, { sabotage: req.sabotage });
+      out = { workspace: l.workspace, launches: l.launches.map((x) => Object.assign({}, x, { params: Array.from(x.params),
+        kernels: x.kernels.map((k) => ({ name: k.name, grid: k.grid, block: k.block, lds: k.lds, source: req.sources ? k.source : undefined })) })) };
+      break;
+    }
+    case 'model-fusion': out = modelFusion(); break;
+    case 'direct-catalogue': out = directCatalogue(); break;
+    case 'transformer-init': out = transformerInit(req); break;
+    case 'precompile': out = { kernels: precompileGroup(req.group || 'direct', req.arch) }; break;
+    case 'gpu-direct': await gpuDirect(outDir(argv)); out = { ok: true }; break;
+    case 'gpu-graphs': await gpuGraphs(req, outDir(argv)); out = { ok: true }; break;
+    default:
+      throw new Error(`unknown command '${cmd}'`);
+  }
+  process.stdout.write(JSON.stringify(out));
+}
+
+main().catch((e) => {
+  process.stderr.write(`${e.stack || e}\n`);
+  process.exit(1);
+});

@@ -1,0 +1,633 @@
+'use strict';
+// HIP source for every launch the MI355X lowering plans, as text, so it can be
+// generated and inspected without a GPU. The runner compiles it with hiprtc.
+//
+// The reference generates one WGSL kernel per fused node from its body
+// (src/fusion/codegen-fused.js:154-362 in abho7/tensor-compiler-webgpu) and
+// one per plain op (src/gpu/codegen.js). Here the kernel *skeletons* are
+// hand-written for gfx950 and live in csrc/kernels/tcmi_device.h and
+// tcmi_gemm.h; this file writes only what varies per launch:
+//   * the body of the fused node as straight-line float arithmetic, every
+//     value a register, each op through the shared tcmi::op_* helpers (so a
+//     fused body rounds exactly as the chain of unfused kernels does);
+//   * the load of every operand, classified by how its index follows from the
+//     output index (flat, a contiguous `span` of axes, or a general gather),
+//     and hoisted into 128-bit loads where the classification allows;
+//   * the u32 parameter block P (sizes and index maps), so one kernel text
+//     serves every size of the same structure and class.
+//
+// Kernel kinds:
+//   elementwise  grid-stride loop, 4 elements per thread per step (float4)
+//   rowwise      one workgroup per row, the row's operands held in registers
+//                across every reduction phase (read from HBM once), max-shift
+//                and normalisation applied in-kernel
+//   colreduce    sum/max over a non-last axis: split-n partials + a final pass
+//   gemm         fp32 MFMA matmul with the fused epilogue applied at the store
+
+const { size, strides } = require('../ir/shapes');
+
+const MAX_P = 48;
+const MAX_IN = 8;
+const WG = 256;
+
+const f32 = new Float32Array(1);
+const u32 = new Uint32Array(f32.buffer);
+/** The exact float32 bits of `v` (rounded to nearest), as a C++ expression. */
+function literal(v) {
+  f32[0] = v;
+  return `tcmi::f32_bits(0x${u32[0].toString(16).padStart(8, '0')}u)`;
+}
+
+/** FNV-1a over a string, as 8 hex digits (kernel names). */
+function fnv(s) {
+  let h = 0x811c9dc5;
+  for (let i = 0; i < s.length; i++) {
+    h ^= s.charCodeAt(i);
+    h = Math.imul(h, 0x01000193) >>> 0;
+  }
+  return h.toString(16).padStart(8, '0');
+}
+
+const UNARY = { neg: 'op_neg', exp: 'op_exp', log: 'op_log', relu: 'op_relu', tanh: 'op_tanh', sqrt: 'op_sqrt',
+  step: 'op_step', stopGradient: 'op_copy', copy: 'op_copy' };
+const BINARY = { add: 'op_add', sub: 'op_sub', mul: 'op_mul', div: 'op_div' };
+
+/**
+ * How a gather node (broadcast or transpose of its input) maps its output
+ * flat index to its source flat index: { mode: 'zero' | 'span' | 'general', ... }.
+ */
+function classifyGather(node, inShape) {
+  const out = node.shape;
+  if (node.op === 'broadcast') {
+    const lead = out.length - inShape.length;
+    const kept = [];
+    for (let d = 0; d < out.length; d++) if (d >= lead && inShape[d - lead] !== 1) kept.push(d);
+    if (kept.length === 0) return { mode: 'zero' };
+    let contiguous = true;
+    for (let k = 1; k < kept.length; k++) if (kept[k] !== kept[k - 1] + 1) contiguous = false;
+    if (contiguous) {
+      const d0 = kept[0], d1 = kept[kept.length - 1];
+      return { mode: 'span', inner: size(out.slice(d1 + 1)), extent: size(out.slice(d0, d1 + 1)) };
+    }
+  }
+  // General: per output axis, its extent and the source stride (lower.js:31-62's gather strides).
+  const st = gatherStrides(node, inShape);
+  return { mode: 'general', extents: out.slice(), strides: st };
+}
+
+function gatherStrides(node, inShape) {
+  const out = node.shape;
+  const natural = strides(inShape);
+  if (node.op === 'broadcast') {
+    const lead = out.length - inShape.length;
+    return out.map((_, i) => (i < lead || inShape[i - lead] === 1 ? 0 : natural[i - lead]));
+  }
+  if (node.op === 'transpose') return node.attrs.perm.map((p) => natural[p]);
+  if (node.op === 'reshape') return strides(out);
+  throw new Error(`not a gather: ${node.op}`);
+}
+
+/**
+ * The straight-line body writer shared by every kernel kind. A context is an
+ * index expression (the flat index at which values are wanted); every body
+ * value is computed once per context. `hooks` lets a kernel kind supply the
+ * loads of operands and the values of nodes it treats specially (the matmul
+ * root of an epilogue, the reductions of a rowwise body).
+ */
+class Emitter {
+  constructor(body, params, hooks) {
+    this.b = body;
+    this.params = params;
+    this.hooks = hooks;
+    this.memo = new Map();
+    this.counter = 0;
+    this.gatherBase = new Map();
+  }
+
+  fresh(prefix) { return `${prefix}${this.counter++}`; }
+
+  /**
+   * Index expression of the source of gather node `node` read in `ctx`. Every
+   * context carries `limit`, one past the largest index it can produce; the
+   * gather's own output must cover it and its largest source index must fall
+   * inside its source, so every load the kernel makes is proved in bounds here.
+   */
+  gatherIndex(node, ctx) {
+    const inShape = this.b.nodes[node.inputs[0]].shape;
+    const g = classifyGather(node, inShape);
+    if (ctx.limit === undefined || ctx.limit > size(node.shape)) {
+      throw new Error(`gather node ${node.id}: read at ${ctx.limit} indices, has ${size(node.shape)} elements`);
+    }
+    let maxSrc = 0;
+    if (g.mode === 'span') maxSrc = g.extent - 1;
+    else if (g.mode === 'general') g.extents.forEach((e, d) => { maxSrc += (e - 1) * g.strides[d]; });
+    if (maxSrc >= size(inShape)) throw new Error(`gather node ${node.id}: source index ${maxSrc} outside ${size(inShape)} elements`);
+    if (g.mode === 'zero') return { idx: '0u', g };
+    const key = `${node.id}`;
+    let base = this.gatherBase.get(key);
+    if (base === undefined) {
+      base = this.params.length;
+      if (g.mode === 'span') this.params.push(g.inner, g.extent);
+      else {
+        const rank = g.extents.length;
+        this.params.push(rank);
+        for (let d = rank - 1; d >= 0; d--) this.params.push(g.extents[d], g.strides[d]);
+      }
+      if (this.params.length > MAX_P) throw new Error(`kernel parameters exceed ${MAX_P} words`);
+      this.gatherBase.set(key, base);
+    }
+    if (g.mode === 'span') {
+      if (g.inner === 1) return { idx: `((${ctx.idx}) % A.P[${base + 1}])`, g, base };
+      return { idx: `tcmi::idx_span(${ctx.idx}, A.P[${base}], A.P[${base + 1}])`, g, base };
+    }
+    return { idx: `tcmi::idx_general(${ctx.idx}, A.P, ${base}u)`, g, base };
+  }
+
+  value(id, ctx, lines) {
+    const key = `${ctx.key}|${id}`;
+    if (this.memo.has(key)) return this.memo.get(key);
+    const node = this.b.nodes[id];
+    let v;
+    const special = this.hooks.special ? this.hooks.special(id, ctx, lines) : undefined;
+    if (special !== undefined) {
+      v = special;
+    } else if (node.op === 'input') {
+      if (ctx.limit === undefined || ctx.limit > size(node.shape)) {
+        throw new Error(`operand ${node.attrs.name}: read at ${ctx.limit} indices, has ${size(node.shape)} elements`);
+      }
+      v = this.hooks.load(Number(node.attrs.name.slice(1)), ctx, lines, node);
+    } else if (node.op === 'const') {
+      v = literal(typeof node.attrs.value === 'number' ? node.attrs.value : node.attrs.value[0]);
+    } else if (node.op === 'reshape') {
+      v = this.value(node.inputs[0], ctx, lines);
+    } else if (node.op === 'broadcast' || node.op === 'transpose') {
+      const src = this.b.nodes[node.inputs[0]];
+      if (src.op === 'const') {
+        v = this.value(src.id, ctx, lines);
+      } else {
+        const gi = this.gatherIndex(node, ctx);
+        const child = { key: `${ctx.key}>${node.id}`, idx: gi.idx, parent: ctx, gather: gi, root: false, row: ctx.row,
+          limit: size(src.shape) };
+        v = this.value(src.id, child, lines);
+      }
+    } else if (BINARY[node.op]) {
+      const a = this.value(node.inputs[0], ctx, lines);
+      const c = this.value(node.inputs[1], ctx, lines);
+      v = this.fresh('v');
+      lines.push(`const float ${v} = tcmi::${BINARY[node.op]}(${a}, ${c});`);
+    } else if (UNARY[node.op]) {
+      const a = this.value(node.inputs[0], ctx, lines);
+      v = this.fresh('v');
+      lines.push(`const float ${v} = tcmi::${UNARY[node.op]}(${a});`);
+    } else {
+      throw new Error(`mi355x codegen: no rule for '${node.op}' in this kernel kind`);
+    }
+    this.memo.set(key, v);
+    return v;
+  }
+}
+
+const inputCount = (b) => b.nodes.filter((n) => n.op === 'input').length;
+
+function checkOperands(b) {
+  const k = inputCount(b);
+  if (k > MAX_IN) throw new Error(`kernel has ${k} operands; the argument block holds ${MAX_IN}`);
+  return k;
+}
+
+function kernelText(kind, bodyText) {
+  const name = `tcmi_${kind}_${fnv(bodyText)}`;
+  return { name, source: bodyText.replace(/__KERNEL__/g, name) };
+}
+
+const indent = (lines, pad) => lines.map((l) => pad + l).join('\n');
+
+// ---- elementwise ------------------------------------------------------------------
+
+/**
+ * A fused (or one-op) elementwise body over n output elements, output node
+ * `output` of body graph `b`. Grid-stride over float4 groups; a scalar tail
+ * for n % 4. Operands read at the output index are loaded as float4; a span
+ * load is a float4 when its 4 lanes are contiguous in the source, one scalar
+ * when they share an element, else 4 scalars.
+ */
+function elementwiseKernel(b, output, outShape, opts) {
+  const o = opts || {};
+  checkOperands(b);
+  const n = size(outShape);
+  if (n >= 2 ** 31) throw new Error(`elementwise kernel over ${n} elements exceeds the 32-bit index space`);
+  const params = [n];
+
+  // Vector pass: hoisted loads go to `hoist`, lane code to `lane`.
+  const hoist = [];
+  const hoisted = new Map();
+  const vecEmitter = new Emitter(b, params, {
+    load(k, ctx, lines) {
+      if (ctx.root) {
+        const hk = `full${k}`;
+        if (!hoisted.has(hk)) {
+          const h = `H${hoisted.size}`;
+          hoist.push(`const float4 ${h} = reinterpret_cast<const float4*>(A.in[${k}])[v];`);
+          hoisted.set(hk, h);
+        }
+        return `tcmi::lane4(${hoisted.get(hk)}, l)`;
+      }
+      const g = ctx.gather;
+      if (ctx.parent && ctx.parent.root && g) {
+        if (g.g.mode === 'zero') {
+          const hk = `zero${k}`;
+          if (!hoisted.has(hk)) { const h = `H${hoisted.size}`; hoist.push(`const float ${h} = A.in[${k}][0];`); hoisted.set(hk, h); }
+          return hoisted.get(hk);
+        }
+        if (g.g.mode === 'span' && g.g.inner === 1 && g.g.extent % 4 === 0) {
+          const hk = `spanv${k}|${ctx.key}`;
+          if (!hoisted.has(hk)) {
+            const h = `H${hoisted.size}`;
+            hoist.push(`const float4 ${h} = reinterpret_cast<const float4*>(A.in[${k}])[(i0 % A.P[${g.base + 1}]) >> 2];`);
+            hoisted.set(hk, h);
+          }
+          return `tcmi::lane4(${hoisted.get(hk)}, l)`;
+        }
+        if (g.g.mode === 'span' && g.g.inner % 4 === 0) {
+          const hk = `spans${k}|${ctx.key}`;
+          if (!hoisted.has(hk)) {
+            const h = `H${hoisted.size}`;
+            hoist.push(`const float ${h} = A.in[${k}][tcmi::idx_span(i0, A.P[${g.base}], A.P[${g.base + 1}])];`);
+            hoisted.set(hk, h);
+          }
+          return hoisted.get(hk);
+        }
+      }
+      const v = `L${lines.length}_${k}`;
+      lines.push(`const float ${v} = A.in[${k}][${ctx.idx}];`);
+      return v;
+    },
+  });
+  const lane = [];
+  const vout = vecEmitter.value(output, { key: 'i', idx: 'i', root: true, limit: n }, lane);
+
+  // Scalar tail: the same body, every load scalar.
+  const tailEmitter = new Emitter(b, params, {
+    load(k, ctx, lines) {
+      const v = `T${lines.length}_${k}`;
+      lines.push(`const float ${v} = A.in[${k}][${ctx.idx}];`);
+      return v;
+    },
+  });
+  tailEmitter.gatherBase = vecEmitter.gatherBase;  // same parameter offsets
+  const tail = [];
+  const tout = tailEmitter.value(output, { key: 'i', idx: 'i', root: true, limit: n }, tail);
+
+  const guard = o.sabotage === 'fused-bounds-off-by-one' ? 'threadIdx.x <= (n & 3u)' : 'threadIdx.x < (n & 3u)';
+  const text = `extern "C" __global__ void __launch_bounds__(${WG}) __KERNEL__(const TcmiArgs A) {
+  const uint32_t n = A.P[0];
+  const uint32_t nv = n >> 2;
+  const uint32_t stride = gridDim.x * ${WG}u;
+  for (uint32_t v = blockIdx.x * ${WG}u + threadIdx.x; v < nv; v += stride) {
+    const uint32_t i0 = v << 2;
+${indent(hoist, '    ')}
+    float r[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      const uint32_t i = i0 + l;
+${indent(lane, '      ')}
+      r[l] = ${vout};
+    }
+    reinterpret_cast<float4*>(A.out)[v] = make_float4(r[0], r[1], r[2], r[3]);
+  }
+  if (blockIdx.x == 0 && ${guard}) {
+    const uint32_t i = (nv << 2) + threadIdx.x;
+${indent(tail, '    ')}
+    A.out[i] = ${tout};
+  }
+}
+`;
+  const k = kernelText('ew', text);
+  // Enough workgroups to fill 256 CUs several times over; grid-stride covers the rest.
+  const groups = Math.max(1, Math.min(Math.ceil(Math.max(1, n >> 2) / WG), 256 * 16));
+  return { name: k.name, source: k.source, params: Uint32Array.from(params), grid: [groups, 1, 1], block: [WG, 1, 1], lds: 0, workspace: 0 };
+}
+
+// ---- rowwise ------------------------------------------------------------------------
+
+const isReduce = (n) => n.op === 'sum' || n.op === 'max';
+
+/**
+ * A rowwise body: last-axis sum/max reductions of element-tier values ([R, C])
+ * and row-tier values ([R, 1]) built from them, output at element or row tier.
+ * One workgroup per row (grid-stride over rows). Every element-tier operand
+ * load is made once into registers and reused by every phase, so each input
+ * is read from HBM once, whatever the number of reductions.
+ */
+function rowwiseKernel(b, output, opts) {
+  const o = opts || {};
+  checkOperands(b);
+  const reductions = b.nodes.filter(isReduce);
+  if (!reductions.length) throw new Error('rowwise kernel without a reduction');
+  const S = b.nodes[reductions[0].inputs[0]].shape;
+  const C = S[S.length - 1];
+  const R = size(S) / C;
+  if (size(S) >= 2 ** 31) throw new Error('rowwise kernel exceeds the 32-bit index space');
+  const T = C >= 2048 ? 256 : 64;
+  const vec = C % 4 === 0;
+  const W = vec ? 4 : 1;                     // elements per slot
+  const E = Math.max(1, Math.ceil(C / (W * T)));  // slots per thread
+  const params = [R, C];
+  const rowTier = (id) => size(b.nodes[id].shape) === R && size(b.nodes[id].shape) !== R * C;
+  const outRow = rowTier(output) || (R === size(b.nodes[output].shape) && C !== 1 && size(b.nodes[output].shape) !== R * C);
+
+  // Loads at the element index: cached per load site in registers.
+  const cacheDecl = [];   // declarations + fill loops before the phases
+  const caches = new Map();
+  const reduced = new Map();
+  const rowLines = [];    // row-tier statements, emitted as they are first needed
+  let em;
+  const ROW = { key: 'r', idx: 'r', root: false, row: true, limit: R };
+  const elemCtx = () => ({ key: 'e', idx: 'e', root: true, limit: R * C });
+
+  const hooks = {
+    special(id, ctx, lines) {
+      if (reduced.has(id)) return reduced.get(id);
+      const n = b.nodes[id];
+      if (!ctx.row && rowTier(id) && n.op !== 'input' && n.op !== 'const') return em.value(id, ROW, rowLines);
+      if (n.op === 'broadcast' && !ctx.row && rowTier(n.inputs[0])) {
+        const src = b.nodes[n.inputs[0]];
+        if (src.op !== 'input' && src.op !== 'const') return em.value(src.id, ROW, rowLines);
+      }
+      return undefined;
+    },
+    load(k, ctx, lines, node) {
+      if (ctx.row) {
+        // A row-tier operand at the row index.
+        const v = `R${rowLines.length}_${k}`;
+        lines.push(`const float ${v} = A.in[${k}][${ctx.idx}];`);
+        return v;
+      }
+      if (ctx.root) {
+        const ck = `full${k}`;
+        if (!caches.has(ck)) {
+          const c = `X${caches.size}`;
+          caches.set(ck, c);
+          if (vec) {
+            cacheDecl.push(`float4 ${c}[${E}];`,
+              `#pragma unroll`,
+              `for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = (threadIdx.x + s * ${T}u) * 4u;`,
+              `  ${c}[s] = c0 < C ? reinterpret_cast<const float4*>(A.in[${k}] + rowBase)[c0 >> 2] : make_float4(0.f, 0.f, 0.f, 0.f); }`);
+          } else {
+            cacheDecl.push(`float ${c}[${E}];`,
+              `#pragma unroll`,
+              `for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = threadIdx.x + s * ${T}u;`,
+              `  ${c}[s] = c0 < C ? A.in[${k}][rowBase + c0] : 0.f; }`);
+          }
+        }
+        return vec ? `tcmi::lane4(${caches.get(ck)}[s], l)` : `${caches.get(ck)}[s]`;
+      }
+      const g = ctx.gather;
+      if (vec && ctx.parent && ctx.parent.root && g && g.g.mode === 'span' && g.g.inner === 1 && g.g.extent === C) {
+        // A per-column vector (LayerNorm gain/bias): cached like a full operand.
+        const ck = `col${k}`;
+        if (!caches.has(ck)) {
+          const c = `X${caches.size}`;
+          caches.set(ck, c);
+          cacheDecl.push(`float4 ${c}[${E}];`,
+            `#pragma unroll`,
+            `for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = (threadIdx.x + s * ${T}u) * 4u;`,
+            `  ${c}[s] = c0 < C ? reinterpret_cast<const float4*>(A.in[${k}])[c0 >> 2] : make_float4(0.f, 0.f, 0.f, 0.f); }`);
+        }
+        return `tcmi::lane4(${caches.get(ck)}[s], l)`;
+      }
+      const v = `L${lines.length}_${k}`;
+      lines.push(`const float ${v} = A.in[${k}][${ctx.idx}];`);
+      return v;
+    },
+  };
+  em = new Emitter(b, params, hooks);
+
+  // One element loop: `body` runs for every valid element with `e` its flat index.
+  const loop = (bodyLines) => vec
+    ? `#pragma unroll
+for (int s = 0; s < ${E}; ++s) {
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    const uint32_t c = (threadIdx.x + s * ${T}u) * 4u + l;
+    if (c < C) {
+      const uint32_t e = rowBase + c;
+${indent(bodyLines, '      ')}
+    }
+  }
+}`
+    : `#pragma unroll
+for (int s = 0; s < ${E}; ++s) {
+  const uint32_t c = threadIdx.x + s * ${T}u;
+  if (c < C) {
+    const uint32_t e = rowBase + c;
+${indent(bodyLines, '    ')}
+  }
+}`;
+
+  const phases = [];
+  const shortTree = o.sabotage === 'layernorm-tree-short' && o.pattern === 'layernorm';
+  reductions.forEach((rd, k) => {
+    for (const key of Array.from(em.memo.keys())) if (key.startsWith('e')) em.memo.delete(key);
+    const rowBefore = rowLines.length;
+    const inner = [];
+    const v = em.value(rd.inputs[0], elemCtx(), inner);
+    const isMax = rd.op === 'max';
+    const pre = rowLines.splice(rowBefore);
+    const acc = `acc${k}`;
+    let result = `tcmi::block_reduce<${isMax}, ${T}>(${acc}, red)`;
+    if (shortTree) result = `tcmi::block_reduce<${isMax}, ${T}>(threadIdx.x < ${T / 2} ? ${acc} : ${isMax ? '(-TCMI_INF)' : '0.f'}, red)`;
+    if (o.sabotage === 'softmax-no-max' && isMax && (o.pattern === 'softmax' || o.pattern === 'log-softmax')) result = '0.f';
+    phases.push(...pre,
+      `float ${acc} = ${isMax ? '(-TCMI_INF)' : '0.f'};`,
+      loop(inner.concat([`${acc} = tcmi::red_${isMax ? 'max' : 'sum'}(${acc}, ${v});`])),
+      `const float red${k} = ${result};`);
+    reduced.set(rd.id, `red${k}`);
+  });
+  for (const key of Array.from(em.memo.keys())) if (key.startsWith('e')) em.memo.delete(key);
+  let store;
+  if (outRow) {
+    const rowBefore = rowLines.length;
+    const v = em.value(output, ROW, rowLines);
+    const pre = rowLines.splice(rowBefore);
+    store = [...pre, `if (threadIdx.x == 0) A.out[r] = ${v};`];
+  } else {
+    const rowBefore = rowLines.length;
+    const inner = [];
+    const v = em.value(output, elemCtx(), inner);
+    const pre = rowLines.splice(rowBefore);
+    if (vec) {
+      // Compute the 4 lanes of each slot, then one 128-bit store.
+      store = [...pre, `#pragma unroll
+for (int s = 0; s < ${E}; ++s) {
+  const uint32_t c0 = (threadIdx.x + s * ${T}u) * 4u;
+  if (c0 < C) {
+    float o4[4];
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      const uint32_t c = c0 + l;
+      const uint32_t e = rowBase + c;
+${indent(inner, '      ')}
+      o4[l] = ${v};
+    }
+    reinterpret_cast<float4*>(A.out + rowBase)[c0 >> 2] = make_float4(o4[0], o4[1], o4[2], o4[3]);
+  }
+}`];
+    } else {
+      store = [...pre, loop(inner.concat([`A.out[e] = ${v};`]))];
+    }
+  }
+  const text = `extern "C" __global__ void __launch_bounds__(${T}) __KERNEL__(const TcmiArgs A) {
+  __shared__ float red[${T / 64}];
+  const uint32_t R = A.P[0];
+  const uint32_t C = A.P[1];
+  for (uint32_t r = blockIdx.x; r < R; r += gridDim.x) {
+    const uint32_t rowBase = r * C;
+${indent(cacheDecl, '    ')}
+${indent(phases, '    ')}
+${indent(store, '    ')}
+  }
+}
+`;
+  const k = kernelText('row', text);
+  const groups = Math.max(1, Math.min(R, 65536));
+  return { name: k.name, source: k.source, params: Uint32Array.from(params), grid: [groups, 1, 1], block: [T, 1, 1], lds: 0, workspace: 0 };
+}
+
+// ---- column reductions (sum / max over a non-last axis) --------------------------------
+
+/**
+ * out[o, j] = reduce_k x[o, k, j] over [outer, n, inner] with inner > 1.
+ * 256 threads = 64 columns x 4 row groups; the n axis is split across
+ * workgroups when one column block alone would leave the chip idle, the
+ * partials going to the workspace and a second kernel combining them.
+ */
+function colreduceKernels(op, outer, n, inner) {
+  const isMax = op === 'max';
+  const colBlocks = Math.ceil(inner / 64);
+  const want = 2048;
+  let splits = Math.max(1, Math.min(Math.ceil(want / Math.max(1, colBlocks * outer)), Math.ceil(n / 64)));
+  const chunk = Math.ceil(n / splits);
+  splits = Math.ceil(n / chunk);
+  const init = isMax ? '(-TCMI_INF)' : '0.f';
+  const comb = isMax ? 'tcmi::red_max' : 'tcmi::red_sum';
+  const first = `extern "C" __global__ void __launch_bounds__(256) __KERNEL__(const TcmiArgs A) {
+  __shared__ float part[4][64];
+  const uint32_t n = A.P[1], inner = A.P[2], splits = A.P[3], chunk = A.P[4];
+  const uint32_t j = blockIdx.x * 64u + (threadIdx.x & 63u);
+  const uint32_t g = threadIdx.x >> 6;
+  const uint32_t s = blockIdx.y, o = blockIdx.z;
+  const uint32_t k0 = s * chunk;
+  const uint32_t k1 = min(n, k0 + chunk);
+  float acc = ${init};
+  if (j < inner) {
+    const float* __restrict__ x = A.in[0] + (size_t)o * n * inner + j;
+    for (uint32_t k = k0 + g; k < k1; k += 4u) acc = ${comb}(acc, x[(size_t)k * inner]);
+  }
+  part[g][threadIdx.x & 63u] = acc;
+  __syncthreads();
+  if (g == 0 && j < inner) {
+    float r = part[0][threadIdx.x];
+    r = ${comb}(r, part[1][threadIdx.x]);
+    r = ${comb}(r, part[2][threadIdx.x]);
+    r = ${comb}(r, part[3][threadIdx.x]);
+    if (splits == 1u) A.out[(size_t)o * inner + j] = r;
+    else A.ws[((size_t)o * splits + s) * inner + j] = r;
+  }
+}
+`;
+  const k1 = kernelText('colred', first);
+  const launches = [{ name: k1.name, source: k1.source, grid: [colBlocks, splits, outer], block: [256, 1, 1], lds: 0 }];
+  if (splits > 1) {
+    const second = `extern "C" __global__ void __launch_bounds__(256) __KERNEL__(const TcmiArgs A) {
+  const uint32_t inner = A.P[2], splits = A.P[3], outer = A.P[0];
+  const uint32_t total = outer * inner;
+  for (uint32_t t = blockIdx.x * 256u + threadIdx.x; t < total; t += gridDim.x * 256u) {
+    const uint32_t o = t / inner, j = t - o * inner;
+    const float* __restrict__ w = A.ws + (size_t)o * splits * inner + j;
+    float r = w[0];
+    for (uint32_t s = 1; s < splits; ++s) r = ${comb}(r, w[(size_t)s * inner]);
+    A.out[t] = r;
+  }
+}
+`;
+    const k2 = kernelText('colfin', second);
+    launches.push({ name: k2.name, source: k2.source, grid: [Math.max(1, Math.min(Math.ceil(outer * inner / 256), 4096)), 1, 1], block: [256, 1, 1], lds: 0 });
+  }
+  return { launches, params: Uint32Array.from([outer, n, inner, splits, chunk]), workspace: splits > 1 ? outer * splits * inner * 4 : 0 };
+}
+
+// ---- matmul with epilogue ----------------------------------------------------------------
+
+/** MFMA tiles per wavefront for a problem: the largest tile that still gives the chip work. */
+function gemmTiles(batch, M, N) {
+  const blocks = (t) => batch * Math.ceil(M / (32 * t)) * Math.ceil(N / (32 * t));
+  if (M >= 128 && N >= 128 && blocks(4) >= 128) return 4;
+  if (M >= 64 && N >= 64 && blocks(2) >= 64) return 2;
+  return M >= 64 && N >= 64 ? 2 : 1;
+}
+
+/**
+ * A matmul-epilogue body (or a plain matmul): the body's matmul node is the
+ * root, every other body op runs on its accumulator at the store. Epilogue
+ * operands are read at the output's flat index (or through their gathers).
+ */
+function gemmKernel(b, output, opts) {
+  const o = opts || {};
+  checkOperands(b);
+  const root = b.nodes.find((n) => n.op === 'matmul');
+  const ia = Number(b.nodes[root.inputs[0]].attrs.name.slice(1));
+  const ib = Number(b.nodes[root.inputs[1]].attrs.name.slice(1));
+  const as = b.nodes[root.inputs[0]].shape, bs = b.nodes[root.inputs[1]].shape;
+  const batch = size(as.slice(0, -2)), M = as[as.length - 2], K = as[as.length - 1], N = bs[bs.length - 1];
+  if (batch * M * N >= 2 ** 31 || batch * M * K >= 2 ** 31 || batch * K * N >= 2 ** 31) {
+    throw new Error('matmul exceeds the 32-bit index space');
+  }
+  const params = [batch, M, K, N];
+  // Sabotage (the reference's 'epilogue-before-bias', codegen-fused.js:228-243): the
+  // activation sees the bare sum and the bias is added after it.
+  let biasAdd = null;
+  if (o.sabotage === 'epilogue-before-bias') {
+    const add = b.nodes.find((n) => n.op === 'add' && n.inputs.includes(root.id) && !n.inputs.every((i) => i === root.id));
+    if (add && add.id !== output) biasAdd = add;
+  }
+  const em = new Emitter(b, params, {
+    special: (id) => (id === root.id || (biasAdd && id === biasAdd.id) ? 'acc' : undefined),
+    load(k, ctx, lines) {
+      const v = `L${lines.length}_${k}`;
+      lines.push(`const float ${v} = A.in[${k}][${ctx.idx}];`);
+      return v;
+    },
+  });
+  const lines = [];
+  const rootCtx = { key: 'i', idx: 'i', root: true, limit: batch * M * N };
+  let out = em.value(output, rootCtx, lines);
+  if (biasAdd) {
+    const other = biasAdd.inputs.find((i) => i !== root.id);
+    const ov = em.value(other, rootCtx, lines);
+    const t = em.fresh('v');
+    lines.push(`const float ${t} = tcmi::op_add(${out}, ${ov});`);
+    out = t;
+  }
+  const T = gemmTiles(batch, M, N);
+  const vecA = K % 4 === 0, vecB = N % 4 === 0;
+  const text = `#include "tcmi_gemm.h"
+struct __KERNEL___epi {
+  __device__ __forceinline__ float operator()(const TcmiArgs& A, uint32_t i, float acc) const {
+${indent(lines, '    ')}
+    return ${out};
+  }
+};
+extern "C" __global__ void __launch_bounds__(256) __KERNEL__(const TcmiArgs A) {
+  tcmi::gemm_f32<${T}, ${T}, ${vecA}, ${vecB}, __KERNEL___epi>(A, A.in[${ia}], A.in[${ib}]);
+}
+`;
+  const k = kernelText('mm', text);
+  const tile = 32 * T;
+  return { name: k.name, source: k.source, params: Uint32Array.from(params),
+    grid: [Math.ceil(N / tile), Math.ceil(M / tile), batch], block: [256, 1, 1], lds: 0, workspace: 0,
+    flops: 2 * batch * M * N * K };
+}
+
+module.exports = { elementwiseKernel, rowwiseKernel, colreduceKernels, gemmKernel, classifyGather, gatherStrides, literal, fnv,
+  Emitter, WG, MAX_P, MAX_IN };

@@ -1,0 +1,271 @@
+'use strict';
+// Runs MI355X launch lists: the drop-in for the reference's WebGPU runner.
+//
+// HipRunner.run(graph, lowered, inputs, { canary }) has the contract of
+// GpuRunner.run (src/gpu/runtime.js:60-128 in abho7/tensor-compiler-webgpu):
+// one buffer per node, inputs and constants uploaded, every launch in order on
+// one stream, every node read back, and with `canary` each buffer padded past
+// its end with 0xdeadbeef that must survive. It returns { values, canaryIntact }
+// (a Float32Array per node) and throws on any HIP error; a fatal error makes
+// the runner `lost` for good (runtime.js:23,61).
+//
+// runLocal(graph, lowered, values) is the node-local executor
+// (src/gpu/harness-m3b.js:86-140): each launch reads float32-rounded reference
+// operands and writes its own output, so no launch sees another's error.
+//
+// prepare(graph, lowered) makes a Program: buffers, packed argument blocks and
+// function handles made once, then run() issues every launch with one native
+// call (or replays a captured HIP graph) — what the trainer and bench use.
+
+const { size } = require('../ir/shapes');
+const { addon } = require('./addon');
+const { kernelSources } = require('./lower');
+const { MAX_IN, MAX_P } = require('./codegen');
+
+const CANARY_BITS = 0xdeadbeef;
+const CANARY_PAD = 256;           // words past the end of every buffer
+const ARG_BYTES = MAX_IN * 8 + 8 + 8 + MAX_P * 4;
+
+const PRELUDE = '#include "tcmi_device.h"\n';
+
+/** One translation unit holding `sources` (name -> text), in name order so the text is canonical. */
+function translationUnit(sources) {
+  const names = Array.from(sources.keys()).sort();
+  return PRELUDE + names.map((n) => sources.get(n)).join('\n');
+}
+
+/** Compile (into the on-disk cache only; no GPU needed) every kernel of `lists` as one module. */
+function precompile(lists, arch) {
+  const all = new Map();
+  for (const l of lists) for (const [name, src] of kernelSources(l)) all.set(name, src);
+  addon().precompile(translationUnit(all), '', arch || 'gfx950');
+  return all.size;
+}
+
+/** Pack one kernel's argument block (TcmiArgs in tcmi_device.h). */
+function packArgs(view, offset, inPtrs, outPtr, wsPtr, params) {
+  const put64 = (at, v) => {
+    view.setUint32(at, v % 4294967296, true);
+    view.setUint32(at + 4, Math.floor(v / 4294967296), true);
+  };
+  if (inPtrs.length > MAX_IN) throw new Error(`launch has ${inPtrs.length} operands (max ${MAX_IN})`);
+  if (params.length > MAX_P) throw new Error(`launch has ${params.length} parameters (max ${MAX_P})`);
+  for (let k = 0; k < MAX_IN; k++) put64(offset + 8 * k, k < inPtrs.length ? inPtrs[k] : 0);
+  put64(offset + MAX_IN * 8, outPtr);
+  put64(offset + MAX_IN * 8 + 8, wsPtr);
+  for (let k = 0; k < MAX_P; k++) view.setUint32(offset + MAX_IN * 8 + 16 + 4 * k, k < params.length ? params[k] : 0, true);
+}
+
+function constData(node) {
+  const n = size(node.shape);
+  const v = node.attrs.value;
+  if (typeof v === 'number') return new Float32Array(Math.max(1, n)).fill(v);
+  return Float32Array.from(v);
+}
+
+class HipRunner {
+  static create() {
+    const a = addon();
+    a.init();
+    return new HipRunner(a);
+  }
+
+  constructor(a) {
+    this.a = a;
+    this.loaded = new Map();    // kernel name (a hash of its source) -> function handle
+  }
+
+  get lost() { return this.a.lost(); }
+
+  info() { return Object.assign({ version: this.a.version(), compileOptions: this.a.compileOptions() }, this.a.info()); }
+
+  /**
+   * Function handles for every kernel of `lowered` (one launch list, or an
+   * array of them): the kernels not loaded yet are compiled together as one
+   * module (one hiprtc call, cached on disk by its text).
+   */
+  functions(lowered) {
+    const lists = Array.isArray(lowered) ? lowered : [lowered];
+    const missing = new Map();
+    for (const l of lists) for (const [name, src] of kernelSources(l)) if (!this.loaded.has(name)) missing.set(name, src);
+    if (missing.size) {
+      const module = this.a.compile(translationUnit(missing), '');
+      for (const name of missing.keys()) this.loaded.set(name, this.a.function(module, name));
+    }
+    return this.loaded;
+  }
+
+  alloc(bytes) { return this.a.malloc(Math.max(16, Math.ceil(bytes / 16) * 16)); }
+
+  /** Launch every kernel of `lowered` with node buffers `bufs` (node id -> device address). */
+  launchAll(lowered, fns, bufs, outOf, ws) {
+    const argBuf = new ArrayBuffer(ARG_BYTES);
+    const view = new DataView(argBuf);
+    const bytes = new Uint8Array(argBuf);
+    for (const l of lowered.launches) {
+      const out = outOf ? outOf(l) : bufs[l.node];
+      packArgs(view, 0, l.inputs.map((id) => bufs[id]), out, ws, l.params);
+      for (const k of l.kernels) this.a.launch(fns.get(k.name), k.grid, k.block, k.lds, bytes);
+    }
+  }
+
+  async run(graph, lowered, inputs, options) {
+    const canary = !!(options && options.canary);
+    if (this.a.lost()) throw new Error('device lost');
+    const a = this.a;
+    const fns = this.functions(lowered);
+    const n = graph.nodes.map((node) => size(node.shape));
+    const cap = n.map((k) => (canary ? k + CANARY_PAD : k));
+    const bufs = [];
+    let ws = 0;
+    try {
+      for (let i = 0; i < graph.nodes.length; i++) bufs.push(this.alloc(cap[i] * 4));
+      ws = this.alloc(lowered.workspace || 16);
+      for (const node of graph.nodes) {
+        const h = bufs[node.id];
+        if (canary) a.fill32(h, 0, CANARY_BITS, cap[node.id]);
+        if (node.op === 'input') {
+          const v = inputs[node.attrs.name];
+          if (v === undefined) throw new Error(`no value for input '${node.attrs.name}'`);
+          if (v.length !== n[node.id]) throw new Error(`input '${node.attrs.name}' has ${v.length} values, needs ${n[node.id]}`);
+          a.h2d(h, 0, v instanceof Float32Array ? v : Float32Array.from(v));
+        } else if (node.op === 'const') {
+          a.h2d(h, 0, constData(node).subarray(0, n[node.id]));
+        }
+      }
+      this.launchAll(lowered, fns, bufs, null, ws);
+      a.sync();
+      const values = [], canaryIntact = [];
+      for (const node of graph.nodes) {
+        const out = new Float32Array(n[node.id]);
+        a.d2h(bufs[node.id], 0, out);
+        values.push(out);
+        if (canary) canaryIntact.push(a.countNot32(bufs[node.id], n[node.id] * 4, CANARY_BITS, CANARY_PAD) === 0);
+      }
+      return { values, canaryIntact };
+    } finally {
+      for (const h of bufs) a.free(h);
+      if (ws) a.free(ws);
+    }
+  }
+
+  /** Node-local run: every launch on float32 reference operands `values` (per node). */
+  async runLocal(graph, lowered, values, options) {
+    const canary = !!(options && options.canary);
+    const a = this.a;
+    const fns = this.functions(lowered);
+    const n = graph.nodes.map((node) => size(node.shape));
+    const ref = [], outs = new Map();
+    let ws = 0;
+    try {
+      for (const node of graph.nodes) {
+        const h = this.alloc(n[node.id] * 4);
+        ref.push(h);
+        a.h2d(h, 0, Float32Array.from(values[node.id]));
+      }
+      for (const l of lowered.launches) {
+        const cap = n[l.node] + (canary ? CANARY_PAD : 0);
+        const h = this.alloc(cap * 4);
+        outs.set(l.node, h);
+        if (canary) a.fill32(h, 0, CANARY_BITS, cap);
+      }
+      ws = this.alloc(lowered.workspace || 16);
+      this.launchAll(lowered, fns, ref, (l) => outs.get(l.node), ws);
+      a.sync();
+      const result = new Array(graph.nodes.length);
+      const canaryIntact = new Array(graph.nodes.length);
+      for (const [id, h] of outs) {
+        const out = new Float32Array(n[id]);
+        a.d2h(h, 0, out);
+        result[id] = out;
+        if (canary) canaryIntact[id] = a.countNot32(h, n[id] * 4, CANARY_BITS, CANARY_PAD) === 0;
+      }
+      if (canary) result.canaryIntact = canaryIntact;
+      return result;
+    } finally {
+      for (const h of ref) a.free(h);
+      for (const h of outs.values()) a.free(h);
+      if (ws) a.free(ws);
+    }
+  }
+
+  /**
+   * A prepared program: one buffer per node, constants uploaded, every launch's
+   * argument block packed once. `only(l)` keeps a subset of launches.
+   */
+  prepare(graph, lowered, options) {
+    return new Program(this, graph, lowered, options || {});
+  }
+}
+
+class Program {
+  constructor(runner, graph, lowered, { only, buffers } = {}) {
+    const a = runner.a;
+    this.a = a;
+    this.graph = graph;
+    this.lowered = lowered;
+    const fns = runner.functions(lowered);
+    this.n = graph.nodes.map((node) => size(node.shape));
+    this.bufs = buffers ? buffers.slice() : graph.nodes.map((node) => runner.alloc(this.n[node.id] * 4));
+    this.owned = !buffers;
+    this.ws = runner.alloc(lowered.workspace || 16);
+    for (const node of graph.nodes) {
+      if (node.op === 'const' && this.owned) a.h2d(this.bufs[node.id], 0, constData(node).subarray(0, this.n[node.id]));
+    }
+    const launches = lowered.launches.filter((l) => !only || only(l));
+    let count = 0;
+    for (const l of launches) count += l.kernels.length;
+    this.count = count;
+    this.fns = new Float64Array(count);
+    this.dims = new Uint32Array(count * 7);
+    this.args = new Uint8Array(count * ARG_BYTES);
+    this.offsets = new Uint32Array(count + 1);
+    const view = new DataView(this.args.buffer);
+    let i = 0;
+    for (const l of launches) {
+      for (const k of l.kernels) {
+        packArgs(view, i * ARG_BYTES, l.inputs.map((id) => this.bufs[id]), this.bufs[l.node], this.ws, l.params);
+        this.fns[i] = fns.get(k.name);
+        this.dims.set([k.grid[0], k.grid[1], k.grid[2], k.block[0], k.block[1], k.block[2], k.lds], i * 7);
+        this.offsets[i] = i * ARG_BYTES;
+        i++;
+      }
+    }
+    this.offsets[count] = count * ARG_BYTES;
+    this.launches = launches;
+    this.graphHandle = 0;
+  }
+
+  write(id, data) { this.a.h2d(this.bufs[id], 0, data instanceof Float32Array ? data : Float32Array.from(data)); }
+
+  read(id) {
+    const out = new Float32Array(this.n[id]);
+    this.a.d2h(this.bufs[id], 0, out);
+    return out;
+  }
+
+  /** Enqueue every launch once (asynchronous). */
+  run() { this.a.launchMany(this.fns, this.dims, this.args, this.offsets); }
+
+  /** Capture one run() as a HIP graph; later replay() calls enqueue it whole. */
+  capture() {
+    if (this.graphHandle) return;
+    this.a.captureBegin();
+    try { this.run(); } finally { this.graphHandle = this.a.captureEnd(); }
+  }
+
+  replay() {
+    if (!this.graphHandle) this.capture();
+    this.a.graphLaunch(this.graphHandle);
+  }
+
+  sync() { this.a.sync(); }
+
+  destroy() {
+    if (this.graphHandle) this.a.graphDestroy(this.graphHandle);
+    if (this.owned) for (const h of this.bufs) this.a.free(h);
+    this.a.free(this.ws);
+  }
+}
+
+module.exports = { HipRunner, Program, packArgs, translationUnit, precompile, CANARY_BITS, CANARY_PAD, ARG_BYTES, PRELUDE };

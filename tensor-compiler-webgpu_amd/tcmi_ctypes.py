@@ -1,0 +1,101 @@
+"""ctypes binding of the tcmi C ABI (include/tcmi.h) for Python callers.
+
+This is the reference-side binding a Python harness would add: every entry
+point of the header with its prototype, and a status check that raises with
+tcmi_last_error(). There is no fallback — if lib/libtcmi.so is missing, load()
+raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+PKG = pathlib.Path(__file__).resolve().parent
+LIB_PATH = PKG / "lib" / "libtcmi.so"
+
+u64 = ctypes.c_uint64
+u32 = ctypes.c_uint32
+i32 = ctypes.c_int32
+P = ctypes.POINTER
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 256), ("arch", ctypes.c_char * 64), ("compute_units", i32),
+                ("clock_khz", i32), ("memory_clock_khz", i32), ("memory_bus_width", i32), ("total_memory", u64),
+                ("l2_bytes", i32), ("lds_bytes_per_block", i32), ("warp_size", i32), ("max_threads_per_block", i32)]
+
+
+# name -> (argtypes, restype); restype int means a status code.
+PROTOTYPES = {
+    "tcmi_init": ([], ctypes.c_int),
+    "tcmi_device_info_get": ([P(DeviceInfo)], ctypes.c_int),
+    "tcmi_lost": ([], ctypes.c_int),
+    "tcmi_last_error": ([], ctypes.c_char_p),
+    "tcmi_version": ([], ctypes.c_char_p),
+    "tcmi_compile_options": ([], ctypes.c_char_p),
+    "tcmi_malloc": ([u64, P(u64)], ctypes.c_int),
+    "tcmi_free": ([u64], ctypes.c_int),
+    "tcmi_size": ([u64, P(u64)], ctypes.c_int),
+    "tcmi_h2d": ([u64, u64, ctypes.c_void_p, u64], ctypes.c_int),
+    "tcmi_d2h": ([ctypes.c_void_p, u64, u64, u64], ctypes.c_int),
+    "tcmi_d2d": ([u64, u64, u64, u64, u64], ctypes.c_int),
+    "tcmi_fill32": ([u64, u64, u32, u64], ctypes.c_int),
+    "tcmi_count_not32": ([u64, u64, u32, u64, P(u64)], ctypes.c_int),
+    "tcmi_set_cache_dir": ([ctypes.c_char_p], ctypes.c_int),
+    "tcmi_set_include_dir": ([ctypes.c_char_p], ctypes.c_int),
+    "tcmi_module_compile": ([ctypes.c_char_p, ctypes.c_char_p, P(u64)], ctypes.c_int),
+    "tcmi_precompile": ([ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p], ctypes.c_int),
+    "tcmi_module_function": ([u64, ctypes.c_char_p, P(u64)], ctypes.c_int),
+    "tcmi_module_unload": ([u64], ctypes.c_int),
+    "tcmi_function_attrs": ([u64, P(i32), P(i32), P(i32), P(i32)], ctypes.c_int),
+    "tcmi_launch": ([u64, P(u32), P(u32), u32, ctypes.c_void_p, u64], ctypes.c_int),
+    "tcmi_sync": ([], ctypes.c_int),
+    "tcmi_event_create": ([P(u64)], ctypes.c_int),
+    "tcmi_event_record": ([u64], ctypes.c_int),
+    "tcmi_event_elapsed": ([u64, u64, P(ctypes.c_float)], ctypes.c_int),
+    "tcmi_event_destroy": ([u64], ctypes.c_int),
+    "tcmi_capture_begin": ([], ctypes.c_int),
+    "tcmi_capture_end": ([P(u64)], ctypes.c_int),
+    "tcmi_graph_launch": ([u64], ctypes.c_int),
+    "tcmi_graph_destroy": ([u64], ctypes.c_int),
+    "tcmi_ceiling_copy": ([u64, u64, u64, u32], ctypes.c_int),
+    "tcmi_ceiling_read": ([u64, u64, u64, u32], ctypes.c_int),
+}
+
+
+class TcmiError(RuntimeError):
+    pass
+
+
+class Tcmi:
+    """The loaded library; attribute access returns checked callables (status != 0 raises)."""
+
+    def __init__(self, path: pathlib.Path = LIB_PATH):
+        if not path.exists():
+            raise TcmiError(f"the MI355X backend is not built: {path} is missing")
+        self.lib = ctypes.CDLL(str(path))
+        for name, (args, res) in PROTOTYPES.items():
+            f = getattr(self.lib, name)
+            f.argtypes = args
+            f.restype = res
+
+    def __getattr__(self, name):
+        f = getattr(self.lib, "tcmi_" + name)
+        if f.restype is not ctypes.c_int or name in ("lost",):
+            return f
+
+        def checked(*args):
+            rc = f(*args)
+            if rc != 0:
+                raise TcmiError(f"tcmi_{name} failed ({rc}): {self.lib.tcmi_last_error().decode()}")
+            return rc
+        return checked
+
+    def device_info(self) -> dict:
+        d = DeviceInfo()
+        self.device_info_get(ctypes.byref(d))
+        return {k: (getattr(d, k).decode() if isinstance(getattr(d, k), bytes) else getattr(d, k)) for k, _ in d._fields_}
+
+
+def load(path: pathlib.Path = LIB_PATH) -> Tcmi:
+    return Tcmi(path)

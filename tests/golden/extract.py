@@ -1,0 +1,85 @@
+"""Write the fixtures under tests/golden/ from the data files the reference's own
+tests hold (abho7/tensor-compiler-webgpu golden/*.json and golden/torch-m3b.f64).
+
+Run once, in a container where the reference is mounted:
+
+    python tests/golden/extract.py /root/reference
+
+Only data is copied (graphs as node lists, inputs, expected float64 outputs,
+recorded counts); no reference source text. The outputs are committed, so no
+test reads the reference at run time.
+
+  cases.json          golden/cases.json (112 graphs + inputs + cotangents) with
+                      golden/torch.json's float64 outputs and gradients merged in
+  m4_counts.json      golden/measurements.json m4.fusion / m4.semantics.model /
+                      corpus byPattern, and golden/gpu-m4.json direct-case names
+                      with their kind and pattern
+  transformer_init.json + transformer_init.f64
+                      golden/spec-m3b.json golden-seed1 (V, batch, seed, initSha,
+                      the four token sequences of its first batch) and
+                      golden/torch-m3b.f64's init logits, loss and gradients
+"""
+import json
+import pathlib
+import struct
+import sys
+
+HERE = pathlib.Path(__file__).resolve().parent
+
+
+def main(ref_root: str) -> None:
+    ref = pathlib.Path(ref_root) / "golden"
+    cases = json.loads((ref / "cases.json").read_text())["cases"]
+    torch = json.loads((ref / "torch.json").read_text())
+    answers = {c["name"]: c for c in torch["cases"]}
+    out = []
+    for c in cases:
+        a = answers[c["name"]]
+        entry = {k: c[k] for k in ("name", "kind", "graph", "outputs", "inputs", "cotangents")}
+        if "native" in c:
+            entry["native"] = c["native"]
+            entry["torchNative"] = a.get("native")
+        if "set" in c:
+            entry["set"] = c["set"]
+        entry["torchOutputs"] = a["outputs"]
+        entry["torchGrads"] = a["grads"]
+        out.append(entry)
+    (HERE / "cases.json").write_text(json.dumps({"source": "golden/cases.json + golden/torch.json",
+                                                 "torch": torch["torch"], "dtype": torch["dtype"], "cases": out}))
+
+    m = json.loads((ref / "measurements.json").read_text())["m4"]
+    gpu = json.loads((ref / "gpu-m4.json").read_text())
+    direct = [{"name": d["name"], "kind": d["kind"], "pattern": d["pattern"], "matmul": d.get("matmul")}
+              for d in gpu["direct"]]
+    counts = {"source": "golden/measurements.json m4, golden/gpu-m4.json direct",
+              "fusion": m["fusion"], "semanticsModel": m["semantics"]["model"],
+              "corpusByPattern": m["semantics"]["corpus"]["byPattern"],
+              "gpuDirect": m["gpu"]["direct"], "direct": direct}
+    (HERE / "m4_counts.json").write_text(json.dumps(counts, indent=1))
+
+    spec = json.loads((ref / "spec-m3b.json").read_text())
+    g = spec["golden"][0]
+    tm = json.loads((ref / "torch-m3b.json").read_text())
+    init = next(i for i in tm["init"] if i["name"] == g["name"])
+    index = tm["blob"]["index"]
+    blob = (ref / tm["blob"]["file"]).read_bytes()
+    prefix = f"init/{g['name']}/"
+    keys = [k for k in index if k.startswith(prefix)]
+    tensors = {}
+    data = bytearray()
+    for k in keys:
+        off, n = index[k]
+        vals = struct.unpack_from(f"<{n}d", blob, off * 8)
+        tensors[k[len(prefix):]] = [len(data) // 8, n]
+        data += struct.pack(f"<{n}d", *vals)
+    first = [spec["synthetic"]["train"][i] for i in g["schedule"][0]]
+    meta = {"source": "golden/spec-m3b.json golden[0] + golden/torch-m3b.json/.f64 init",
+            "name": g["name"], "seed": g["seed"], "V": g["V"], "batch": g["batch"], "initSha": g["initSha"],
+            "config": spec["config"], "paramOrder": spec["paramOrder"], "firstBatch": first,
+            "loss": init["loss"], "tensors": tensors}
+    (HERE / "transformer_init.json").write_text(json.dumps(meta))
+    (HERE / "transformer_init.f64").write_bytes(bytes(data))
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")

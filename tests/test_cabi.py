@@ -1,0 +1,57 @@
+"""The boundary: the C ABI library loads and exports every entry point
+include/tcmi.h declares, the ctypes binding declares each with a prototype, the
+Node addon loads and exposes its functions, and host-side argument checks fail
+cleanly before any device call. No test here touches a GPU."""
+import ctypes
+import re
+import subprocess
+
+import pytest
+
+from conftest import PKG, ROOT
+
+
+def declared():
+    text = (ROOT / "include" / "tcmi.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(tcmi_[a-z0-9_]+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    import tcmi_ctypes
+    names = declared()
+    assert len(names) >= 30
+    lib = ctypes.CDLL(str(tcmi_ctypes.LIB_PATH))
+    for n in names:
+        assert hasattr(lib, n), n
+    out = subprocess.run(["nm", "-D", "--defined-only", str(tcmi_ctypes.LIB_PATH)], capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (tcmi_[a-z0-9_]+)", out))
+    assert set(names) <= exported
+    assert set(tcmi_ctypes.PROTOTYPES) == set(names)
+
+
+def test_calls_before_init_fail_cleanly():
+    import tcmi_ctypes
+    t = tcmi_ctypes.load()
+    h = tcmi_ctypes.u64()
+    # No tcmi_init in this process: allocation must refuse without touching a device.
+    rc = t.lib.tcmi_malloc(16, ctypes.byref(h))
+    assert rc == 10004
+    assert b"tcmi_init" in t.lib.tcmi_last_error()
+    assert b"packed-fp32-ops" in t.lib.tcmi_compile_options()
+
+
+def test_node_addon_loads_and_exports():
+    js = ("const a=require(process.argv[1]);"
+          "const want=['init','info','malloc','free','h2d','d2h','d2d','fill32','countNot32','compile','precompile',"
+          "'function','launch','launchMany','sync','eventCreate','eventRecord','eventElapsed','captureBegin','captureEnd',"
+          "'graphLaunch','ceilingCopy','ceilingRead'];"
+          "const miss=want.filter((k)=>typeof a[k]!=='function'); if(miss.length){console.log(miss.join());process.exit(2);}"
+          "try{a.malloc(16);process.exit(3);}catch(e){if(!/tcmi_init/.test(e.message))process.exit(4);}")
+    p = subprocess.run(["node", "-e", js, str(PKG / "lib" / "tcmi.node")], capture_output=True, text=True)
+    assert p.returncode == 0, p.stdout + p.stderr
+
+
+def test_kernel_headers_compile_for_gfx950_offline(tool):
+    """The skeletons compile with hiprtc for gfx950 (no GPU): every direct case's kernels as one module."""
+    out = tool("precompile", {"group": "direct", "arch": "gfx950"})
+    assert out["kernels"] > 30

@@ -1,0 +1,134 @@
+"""The host side (JavaScript, run under node) against the reference's recorded
+structure: builder graphs node for node, the fusion pass's counts on the
+reference's own transformer, the direct-case catalogue, bitwise semantic
+preservation of fusion (judged by the float64 oracle), and that every graph
+lowers with every load proved in bounds."""
+import json
+
+import numpy as np
+import pytest
+
+from oracle import interp
+
+
+def test_builder_graphs_equal_reference_cases(golden_cases, tool):
+    ref = {c["name"]: c for c in golden_cases}
+    built = tool("builder-cases")
+    assert len(built) == 12
+    for b in built:
+        assert b["graph"] == ref[b["name"]]["graph"], b["name"]
+        assert b["outputs"] == ref[b["name"]]["outputs"], b["name"]
+
+
+def test_fusion_counts_on_reference_transformer(m4_counts, tool):
+    """measurements.json m4.fusion: forward 212 -> 48 and step 1308 -> 450 launches, by pattern,
+    with 2 and 0 activation epilogues; the pass sabotage throws on both (m4.passSabotage.model)."""
+    got = {g["graph"]: g for g in tool("model-fusion")}
+    for want in m4_counts["fusion"]:
+        g = got[want["graph"]]
+        for k in ("launchesBefore", "launchesAfter", "byPattern", "epilogues", "epiloguesWithActivation"):
+            assert g[k] == want[k], (want["graph"], k, g[k], want[k])
+        assert g["unfusedLaunches"] == want["launchesBefore"] and g["fusedLaunches"] == want["launchesAfter"]
+    assert got["forward"]["passSabotageError"] == "fuse: node 157 used before it is built"
+    assert got["step"]["passSabotageError"] == "fuse: node 597 used before it is built"
+
+
+def test_direct_catalogue_is_the_references(m4_counts, tool):
+    cat = tool("direct-catalogue")
+    want = [(d["name"], d["kind"], d["pattern"]) for d in m4_counts["direct"]]
+    assert [(c["name"], c["kind"], c["pattern"]) for c in cat] == want
+    by = {}
+    for c in cat:
+        # Every case fuses into exactly the one kernel it is meant to test.
+        assert len(c["launched"]) == 1, c["name"]
+        assert c["launched"][0]["op"] == "fused" and c["launched"][0]["kind"] == c["kind"], c["name"]
+        assert c["launched"][0]["pattern"] == c["pattern"], c["name"]
+        by[c["pattern"]] = by.get(c["pattern"], 0) + 1
+    assert by == {k: v["cases"] for k, v in m4_counts["gpuDirect"]["byPattern"].items()}
+
+
+def _semantics(original, fused, origin, inputs):
+    a = interp.evaluate(original, inputs)
+    b = interp.evaluate(fused, inputs)
+    for nid in range(len(fused["nodes"])):
+        x, y = a[origin[nid]], b[nid]
+        if x.size != y.size or not np.array_equal(x.view(np.int64), y.view(np.int64)):
+            return False
+    return True
+
+
+def test_fusion_preserves_semantics_bitwise(golden_cases, tool):
+    """checkSemantics (fuse.js:311-330): the fused graph evaluates bitwise equal at every
+    surviving node, on every golden case's forward and gradient graph."""
+    grads = tool("grad", {"cases": [{"name": c["name"], "graph": c["graph"], "outputs": c["outputs"]} for c in golden_cases]})
+    reqs, feeds = [], []
+    for c, g in zip(golden_cases, grads):
+        reqs.append({"name": c["name"] + "/fwd", "graph": c["graph"], "keep": c["outputs"]})
+        feeds.append(c["inputs"])
+        feed = dict(c["inputs"])
+        for n, cot in zip(g["cotangents"], c["cotangents"]):
+            feed[n] = cot
+        reqs.append({"name": c["name"] + "/grad", "graph": g["graph"], "keep": c["outputs"] + g["grads"]})
+        feeds.append(feed)
+    fused = tool("fuse", {"graphs": reqs})
+    n_fused = 0
+    for r, f, feed in zip(reqs, fused, feeds):
+        assert "error" not in f, (r["name"], f.get("error"))
+        assert _semantics(r["graph"], f["graph"], f["origin"], feed), r["name"]
+        for node in f["graph"]["nodes"]:
+            if node["op"] == "fused":
+                n_fused += 1
+                assert len(node["inputs"]) <= 6
+    assert n_fused > 50
+
+
+def test_fusion_sabotage_is_caught_by_semantics(golden_cases, tool):
+    """The pass sabotage ('fusion-absorbs-shared') either throws or changes some value."""
+    reqs = [{"name": c["name"], "graph": c["graph"], "keep": c["outputs"], "sabotage": "fusion-absorbs-shared"}
+            for c in golden_cases]
+    honest = tool("fuse", {"graphs": [dict(r, sabotage=None) for r in reqs]})
+    bad = tool("fuse", {"graphs": reqs})
+    caught = 0
+    for c, h, b in zip(golden_cases, honest, bad):
+        if "error" in b:
+            caught += 1
+        elif b["graph"] != h["graph"] and not _semantics(c["graph"], b["graph"], b["origin"], c["inputs"]):
+            caught += 1
+    assert caught >= 1
+
+
+def test_recompute_option_recomputes(tool):
+    """A producer feeding a broadcast is stored once by default and recomputed with
+    recompute: true (m4-fusion.test.js:55-63), semantics preserved either way."""
+    nodes = [{"op": "input", "inputs": [], "attrs": {"name": "y", "shape": [16, 256]}, "shape": [16, 256]},
+             {"op": "input", "inputs": [], "attrs": {"name": "p", "shape": [256]}, "shape": [256]}]
+    cyc = ["tanh", "exp", "neg", "exp", "sqrt", "log"]
+    for k in range(16):
+        nodes.append({"op": cyc[k % 6], "inputs": [len(nodes) - 1 if k else 1], "attrs": {}, "shape": [256]})
+    nodes.append({"op": "broadcast", "inputs": [len(nodes) - 1], "attrs": {"shape": [16, 256]}, "shape": [16, 256]})
+    nodes.append({"op": "add", "inputs": [0, len(nodes) - 1], "attrs": {}, "shape": [16, 256]})
+    g = {"nodes": nodes}
+    plain, re = tool("fuse", {"graphs": [{"name": "a", "graph": g, "keep": [len(nodes) - 1]},
+                                          {"name": "b", "graph": g, "keep": [len(nodes) - 1], "recompute": True}]})
+    count = lambda f: sum(1 for n in f["graph"]["nodes"] if n["op"] == "fused")
+    assert count(plain) == 2 and count(re) == 1
+    rng = np.random.default_rng(1)
+    feed = {"y": rng.uniform(-2, 2, 16 * 256), "p": rng.uniform(-2, 2, 256)}
+    assert _semantics(g, plain["graph"], plain["origin"], feed)
+    assert _semantics(g, re["graph"], re["origin"], feed)
+
+
+def test_every_golden_graph_lowers_with_loads_proved_in_bounds(golden_cases, tool):
+    """lowerMI355X proves every gather and operand load in bounds or throws; every golden
+    graph, fused and unfused, must lower."""
+    for c in golden_cases:
+        for fz in (None, {"keep": c["outputs"]}):
+            req = {"graph": c["graph"]}
+            if fz:
+                req["fuse"] = fz
+            out = tool("lower", req)
+            assert len(out["launches"]) >= 1
+            for l in out["launches"]:
+                assert len(l["params"]) <= 48
+                for k in l["kernels"]:
+                    assert all(g >= 1 for g in k["grid"]) and k["block"][0] in (64, 256)
