@@ -157,6 +157,57 @@ def reference_with_bounds(graph, raw_inputs: Dict[str, Sequence[float]], carried
     return {"values": values, "bounds": bounds, "inputs": used}
 
 
+def _node_step(graph, node, values, bounds_, raw_inputs, used):
+    op = node["op"]
+    if op == "input":
+        name = node["attrs"]["name"]
+        raw = np.asarray(raw_inputs[name], dtype=np.float64).reshape(-1)
+        if raw.size != interp.size(node["shape"]):
+            raise ValueError(f"input '{name}' has {raw.size} values, needs {interp.size(node['shape'])}")
+        value = fround(raw)
+        used[name] = value
+        return value, ftz(value)
+    if op == "const":
+        value = fround(interp.kernel(node, [], graph))
+        return value, ftz(value)
+    args = [values[i] for i in node["inputs"]]
+    errs = [bounds_[i] for i in node["inputs"]]
+    value = interp.kernel(node, args, graph)
+    bound = _structured_bound(node, args, errs, graph)
+    if bound is None:
+        bound = _elementwise_bound(op, value, args, errs)
+    return value, bound + ftz(value)
+
+
+def streaming_reference(graph, raw_inputs, outputs):
+    """reference_with_bounds for `outputs` only, holding just the live values
+    (src/fusion/workloads.js:275-301 streamingReference): {id: (value, bound)}.
+    Gives exactly reference_with_bounds' values and bounds for those ids."""
+    last_use = [-1] * len(graph["nodes"])
+    for nid, n in enumerate(graph["nodes"]):
+        for i in n["inputs"]:
+            last_use[i] = nid
+    keep = set(outputs)
+    values: Dict[int, np.ndarray] = {}
+    bnds: Dict[int, np.ndarray] = {}
+    used: Dict[str, np.ndarray] = {}
+    out = {}
+    with np.errstate(all="ignore"):
+        for nid, node in enumerate(graph["nodes"]):
+            v, e = _node_step(graph, node, values, bnds, raw_inputs, used)
+            values[nid], bnds[nid] = v, e
+            if nid in keep:
+                out[nid] = (v, e)
+            for i in set(node["inputs"]):
+                if last_use[i] == nid and i not in keep:
+                    values.pop(i, None)
+                    bnds.pop(i, None)
+            if last_use[nid] == -1 and nid not in keep:
+                values.pop(nid, None)
+                bnds.pop(nid, None)
+    return out
+
+
 def unjudgeable_count(values, bounds) -> int:
     n = 0
     for v, e in zip(values, bounds):

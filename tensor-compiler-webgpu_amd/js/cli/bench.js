@@ -1,0 +1,232 @@
+#!/usr/bin/env node
+'use strict';
+// Measurement of the MI355X backend on BASELINE's configs, printed as one JSON
+// document (bench.py turns it into the driver's one-line record).
+//
+//   node bench.js [--configs c2,c3,c4] [--steps K] [--warmup W] [--programs P]
+//                 [--reps N] [--c4-shapes all|small] [--quick]
+//
+// c2  fused elementwise chains (P programs, forward + gradient) over [8192, 1024]:
+//     the headline step = every fused program run once; K timed steps
+//     bracketed by a sync and hipEvents on both sides.
+// c3  softmax / logSoftmax forward + backward over [16384, 4096]
+// c4  matmul + bias -> relu | tanh at three shapes, and its backward graph
+// For every program: fused and unfused timed against each other (ABBA), every
+// launch timed alone (for per-fusion-group speedups and the dominant kernel's
+// average duration), algorithmic bytes and matmul flops.
+
+const { Graph } = require('../src/ir/graph');
+const { size } = require('../src/ir/shapes');
+const { grad } = require('../src/autodiff');
+const { fuse } = require('../src/fusion/fuse');
+const { lowerMI355X } = require('../src/mi355x/lower');
+const { HipRunner } = require('../src/mi355x/runner');
+const { HipBench, summarize, verdict, median } = require('../src/mi355x/bench');
+const { chainWorkload, chainInputs } = require('../src/builders/chains');
+const { Rng } = require('../src/testing/rng');
+
+const HBM_PEAK_GBS = 8000;
+const FP32_MFMA_PEAK_TFLOPS = 157.3;
+
+function arg(name, dflt) {
+  const i = process.argv.indexOf(`--${name}`);
+  return i >= 0 && process.argv[i + 1] !== undefined ? process.argv[i + 1] : dflt;
+}
+const flag = (name) => process.argv.includes(`--${name}`);
+const log = (m) => process.stderr.write(`bench: ${m}\n`);
+
+/** Prepare a program for `graph` with `inputs` uploaded. */
+function prepared(runner, graph, lowered, inputs, opts) {
+  const p = runner.prepare(graph, lowered, opts);
+  for (const node of graph.nodes) if (node.op === 'input') p.write(node.id, inputs[node.attrs.name]);
+  return p;
+}
+
+/** Time every launch of `program` alone: ms per launch (median of a few repetitions). */
+function timeLaunches(runner, bench, program, reps) {
+  const out = [];
+  for (const l of program.lowered.launches) {
+    const one = runner.prepare(program.graph, { launches: [l], workspace: program.lowered.workspace }, { buffers: program.bufs });
+    const r = bench.time({ one }, { reps: reps || 5, warmup: 1, targetMs: 0.5 });
+    out.push({ node: l.node, kind: l.kind, pattern: l.pattern || null, code: l.code, bytes: l.bytes, flops: l.flops,
+      us: r.stats.one.median });
+    one.destroy();
+  }
+  return out;
+}
+
+/**
+ * One graph, fused and unfused: ABBA timing of the two programs, every launch
+ * alone, per-group speedups. `inputs` by name.
+ */
+function measureGraph(runner, bench, name, graph, keep, inputs, opts) {
+  const o = opts || {};
+  const f = fuse(graph, { keep });
+  const lf = lowerMI355X(f.graph);
+  const lu = lowerMI355X(graph);
+  runner.functions([lf, lu]);
+  const pf = prepared(runner, f.graph, lf, inputs);
+  const pu = prepared(runner, graph, lu, inputs);
+  const t = bench.time({ fused: pf, unfused: pu }, { reps: o.reps });
+  const launchF = timeLaunches(runner, bench, pf, o.launchReps);
+  const launchU = o.skipUnfusedLaunches ? null : timeLaunches(runner, bench, pu, o.launchReps);
+  // Outputs of both variants: bitwise agreement is reported, parity is the tests' job.
+  pf.run(); pu.run(); pf.sync();
+  let same = 0, total = 0;
+  for (const id of keep) {
+    const a = pf.read(f.index.get(id)), b = pu.read(id);
+    total += a.length;
+    for (let i = 0; i < a.length; i++) if (Object.is(a[i], b[i])) same++;
+  }
+  const bytesF = lf.launches.reduce((s, l) => s + l.bytes, 0);
+  const bytesU = lu.launches.reduce((s, l) => s + l.bytes, 0);
+  const flops = lf.launches.reduce((s, l) => s + (l.flops || 0), 0);
+  const unfusedUs = new Map();
+  if (launchU) for (const l of launchU) unfusedUs.set(l.node, l.us);
+  const groups = f.groups.filter((g) => f.index.has(g.sink)).map((g) => {
+    const fusedLaunch = launchF.find((l) => l.node === f.index.get(g.sink));
+    let unfused = 0, count = 0;
+    for (const m of g.members) if (unfusedUs.has(m)) { unfused += unfusedUs.get(m); count++; }
+    return { sink: g.sink, kind: g.kind, pattern: g.pattern, members: g.members.size, unfusedLaunches: count,
+      fusedUs: fusedLaunch ? fusedLaunch.us : null, unfusedUs: launchU ? unfused : null,
+      speedup: launchU && fusedLaunch ? unfused / fusedLaunch.us : null };
+  });
+  const res = {
+    name, launches: { fused: lf.launches.length, unfused: lu.launches.length }, k: t.k,
+    fused: t.stats.fused, unfused: t.stats.unfused, verdict: verdict(t.stats.unfused, t.stats.fused),
+    bytes: { fused: bytesF, unfused: bytesU }, flops,
+    gbs: { fused: bytesF / (t.stats.fused.median * 1e3), unfused: bytesU / (t.stats.unfused.median * 1e3) },
+    tflops: flops ? { fused: flops / (t.stats.fused.median * 1e6), unfused: flops / (t.stats.unfused.median * 1e6) } : null,
+    bitwiseSameOutputs: { same, total }, groups, launchF, launchU,
+  };
+  if (o.keepPrograms) res.programs = { pf, pu };
+  else { pf.destroy(); pu.destroy(); }
+  return res;
+}
+
+/** The dominant kernel (by total time) of a set of launch timings, aggregated by kernel name. */
+function dominant(launches) {
+  const by = new Map();
+  for (const l of launches) {
+    const e = by.get(l.code) || { code: l.code, kind: l.kind, pattern: l.pattern, count: 0, us: 0, bytes: 0, flops: 0 };
+    e.count++; e.us += l.us; e.bytes += l.bytes; e.flops += l.flops || 0;
+    by.set(l.code, e);
+  }
+  let best = null;
+  for (const e of by.values()) if (!best || e.us > best.us) best = e;
+  if (!best) return null;
+  const avgUs = best.us / best.count, bytes = best.bytes / best.count;
+  return Object.assign(best, { avgUs, bytesPerLaunch: bytes, gbs: bytes / (avgUs * 1e3),
+    tflops: best.flops ? best.flops / best.count / (avgUs * 1e6) : null });
+}
+
+// ---- configs -----------------------------------------------------------------------
+
+function c2(runner, bench, opts) {
+  const R = 8192, C = 1024;
+  const P = Number(arg('programs', opts.quick ? 2 : 8));
+  const K = Number(arg('steps', 20)), W = Number(arg('warmup', 3));
+  const programs = [];
+  const results = [];
+  for (let s = 0; s < P; s++) {
+    const w = chainWorkload(s, R, C);
+    const inputs = chainInputs(s, R, C);
+    for (const kind of ['forward', 'gradient']) {
+      const v = w[kind];
+      log(`c2 program ${s} ${kind}`);
+      const r = measureGraph(runner, bench, `c2-p${s}-${kind}`, v.graph, v.keep, inputs, { keepPrograms: true, reps: opts.reps });
+      r.ops = w.ops;
+      programs.push(r.programs.pf);
+      r.programs.pu.destroy();
+      delete r.programs;
+      results.push(r);
+    }
+  }
+  // The headline step: every fused program once; W warm-up steps, then K timed steps.
+  for (const p of programs) p.capture();
+  for (let i = 0; i < W; i++) for (const p of programs) p.replay();
+  runner.a.sync();
+  const t0 = process.hrtime.bigint();
+  runner.a.eventRecord(bench.start);
+  for (let i = 0; i < K; i++) for (const p of programs) p.replay();
+  runner.a.eventRecord(bench.end);
+  const ms = runner.a.eventElapsed(bench.start, bench.end);
+  runner.a.sync();
+  const wallMs = Number(process.hrtime.bigint() - t0) / 1e6;
+  for (const p of programs) p.destroy();
+  const stepBytes = results.reduce((s, r) => s + r.bytes.fused, 0);
+  const all = [].concat.apply([], results.map((r) => r.launchF));
+  return { config: 'c2', shape: [R, C], programs: P, steps: K, warmup: W, msPerStep: ms / K, wallMsPerStep: wallMs / K,
+    stepBytes, gbs: stepBytes / ((ms / K) * 1e6), dominant: dominant(all), results };
+}
+
+function c3(runner, bench, opts) {
+  const R = opts.quick ? 2048 : 16384, C = 4096;
+  const rng = new Rng(3);
+  const x = rng.normalF32(R * C, 2);
+  const rows = rng.shuffle(Array.from({ length: R }, (_, i) => i)).slice(0, Math.round(R / 100));
+  for (const r of rows) for (let c = 0; c < C; c++) x[r * C + c] += 800;
+  const dy = rng.normalF32(R * C, 1);
+  const results = [];
+  for (const fn of ['softmax', 'logSoftmax']) {
+    const g = new Graph();
+    const xi = g.input('x', [R, C]);
+    const y = g[fn](xi, 1);
+    log(`c3 ${fn} forward`);
+    results.push(measureGraph(runner, bench, `c3-${fn}-forward`, g, [y], { x }, { reps: opts.reps }));
+    const G = grad(g, [y], [xi]);
+    log(`c3 ${fn} backward`);
+    results.push(measureGraph(runner, bench, `c3-${fn}-backward`, G.graph, [y, G.grads[0]], { x, d0: dy }, { reps: opts.reps }));
+  }
+  const all = [].concat.apply([], results.map((r) => r.launchF));
+  const bytes = results.reduce((s, r) => s + r.bytes.fused, 0);
+  const us = results.reduce((s, r) => s + r.fused.median, 0);
+  return { config: 'c3', shape: [R, C], shiftedRows: rows.length, gbs: bytes / (us * 1e3), dominant: dominant(all), results };
+}
+
+function c4(runner, bench, opts) {
+  const shapes = opts.quick || arg('c4-shapes', 'all') === 'small' ? [[512, 512, 512]] : [[512, 512, 512], [4096, 4096, 4096], [8192, 1024, 4096]];
+  const results = [];
+  for (const [M, K, N] of shapes) {
+    const rng = new Rng(M * 7 + K * 3 + N);
+    const X = rng.normalF32(M * K, 1 / Math.sqrt(K)), Wt = rng.normalF32(K * N, 1 / Math.sqrt(K));
+    const bias = rng.normalF32(N, Math.sqrt(0.1));
+    const dY = rng.normalF32(M * N, 1);
+    for (const act of ['relu', 'tanh']) {
+      const g = new Graph();
+      const xi = g.input('X', [M, K]), wi = g.input('W', [K, N]), bi = g.input('bias', [N]);
+      const y = g[act](g.add(g.matmul(xi, wi), bi));
+      log(`c4 ${M}x${K}x${N} ${act} forward`);
+      results.push(measureGraph(runner, bench, `c4-${M}x${K}x${N}-${act}-forward`, g, [y], { X, W: Wt, bias }, { reps: opts.reps || 16 }));
+      const G = grad(g, [y], [xi, wi, bi]);
+      log(`c4 ${M}x${K}x${N} ${act} backward`);
+      results.push(measureGraph(runner, bench, `c4-${M}x${K}x${N}-${act}-backward`, G.graph, [y].concat(G.grads),
+        { X, W: Wt, bias, d0: dY }, { reps: opts.reps || 8 }));
+    }
+  }
+  const mm = [].concat.apply([], results.map((r) => r.launchF)).filter((l) => l.flops);
+  return { config: 'c4', shapes, dominant: dominant(mm), results };
+}
+
+async function main() {
+  const runner = HipRunner.create();
+  const bench = new HipBench(runner);
+  const opts = { quick: flag('quick'), reps: arg('reps') ? Number(arg('reps')) : undefined };
+  const which = arg('configs', 'c2,c3,c4').split(',');
+  const out = { device: runner.info(), peaks: { hbmGBs: HBM_PEAK_GBS, fp32MfmaTFLOPs: FP32_MFMA_PEAK_TFLOPS }, configs: {} };
+  const fns = { c2, c3, c4 };
+  for (const c of which) {
+    if (!fns[c]) throw new Error(`unknown config ${c}`);
+    const t0 = Date.now();
+    out.configs[c] = fns[c](runner, bench, opts);
+    out.configs[c].seconds = (Date.now() - t0) / 1e3;
+    log(`${c} done in ${out.configs[c].seconds.toFixed(1)} s`);
+  }
+  bench.destroy();
+  process.stdout.write(JSON.stringify(out));
+}
+
+main().catch((e) => {
+  process.stderr.write(`${e.stack || e}\n`);
+  process.exit(1);
+});

@@ -146,6 +146,43 @@ async function gpuGraphs(req, dir) {
   bundle.close({ device: runner.info() });
 }
 
+/**
+ * Config-2 programs on the GPU: for each seed, forward and gradient graphs at [R, C],
+ * fused (and with `unfused`, unfused), canary-padded; the bundle holds the inputs,
+ * the kept outputs of each variant (by original node id) and the canary verdicts.
+ */
+async function gpuChains(req, dir) {
+  const { HipRunner } = require('../src/mi355x/runner');
+  const { chainWorkload, chainInputs } = require('../src/builders/chains');
+  const runner = HipRunner.create();
+  const bundle = new Bundle(dir);
+  for (const seed of req.seeds) {
+    const w = chainWorkload(seed, req.R, req.C);
+    const inputs = chainInputs(seed, req.R, req.C);
+    const ins = {};
+    for (const k of Object.keys(inputs)) ins[k] = bundle.put(inputs[k]);
+    for (const kind of ['forward', 'gradient']) {
+      process.stderr.write(`gpu-chains: seed ${seed} ${kind}\n`);
+      const v = w[kind];
+      const f = fuse(v.graph, { keep: v.keep });
+      const lf = lowerMI355X(f.graph);
+      const rf = await runner.run(f.graph, lf, inputs, { canary: true });
+      const entry = { name: `c2-p${seed}-${kind}`, seed, kind, graph: v.graph.toJSON(), keep: v.keep, inputs: ins,
+        fusedLaunches: lf.launches.length, canaryFused: rf.canaryIntact.every(Boolean), fused: {} };
+      for (const id of v.keep) entry.fused[id] = bundle.put(rf.values[f.index.get(id)]);
+      if (req.unfused) {
+        const lu = lowerMI355X(v.graph);
+        const ru = await runner.run(v.graph, lu, inputs, { canary: true });
+        entry.unfused = {};
+        for (const id of v.keep) entry.unfused[id] = bundle.put(ru.values[id]);
+        entry.canaryUnfused = ru.canaryIntact.every(Boolean);
+      }
+      bundle.add(entry);
+    }
+  }
+  bundle.close({ device: runner.info() });
+}
+
 async function main() {
   const argv = process.argv.slice(2);
   const cmd = argv[0];
@@ -182,8 +219,23 @@ async function main() {
     case 'model-fusion': out = modelFusion(); break;
     case 'direct-catalogue': out = directCatalogue(); break;
     case 'transformer-init': out = transformerInit(req); break;
+    case 'chain-graphs': {
+      const { chainWorkload } = require('../src/builders/chains');
+      out = req.seeds.map((seed) => {
+        const w = chainWorkload(seed, req.R, req.C);
+        const one = (v) => {
+          const f = fuse(v.graph, { keep: v.keep });
+          const l = lowerMI355X(f.graph);
+          return { graph: v.graph.toJSON(), keep: v.keep, cotangent: v.cotangent || null,
+            fusedBytes: l.launches.reduce((s, x) => s + x.bytes, 0), fusedLaunches: l.launches.length };
+        };
+        return { seed, ops: w.ops, forward: one(w.forward), gradient: one(w.gradient) };
+      });
+      break;
+    }
     case 'precompile': out = { kernels: precompileGroup(req.group || 'direct', req.arch) }; break;
     case 'gpu-direct': await gpuDirect(outDir(argv)); out = { ok: true }; break;
+    case 'gpu-chains': await gpuChains(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-graphs': await gpuGraphs(req, outDir(argv)); out = { ok: true }; break;
     default:
       throw new Error(`unknown command '${cmd}'`);

@@ -1,0 +1,92 @@
+'use strict';
+// Timing on the MI355X: the reference's protocol (src/fusion/bench.js:124-216
+// and src/fusion/measure-m4.js:229-234 in abho7/tensor-compiler-webgpu) on HIP:
+//   * a repetition is k back-to-back runs of a prepared program, bracketed by
+//     two hipEvents on the stream the kernels run on; k is chosen from a
+//     single run so one repetition lasts >= 2 ms (bench.js:178-181);
+//   * every program is captured once as a HIP graph and replayed, so nothing
+//     is created inside a timed region and host launch cost stays off the clock;
+//   * 5 warm-up repetitions per variant, then 32 repetitions in ABBA order;
+//   * summaries are median/min/max microseconds per program run, and two
+//     variants win or lose against each other only when their min-max ranges
+//     do not overlap (verdict), speedup being the ratio of medians.
+
+const WARMUP = 5;
+const REPS = 32;
+const TARGET_MS = 2;
+const MAX_K = 4096;
+
+function median(a) {
+  const s = a.slice().sort((x, y) => x - y);
+  const n = s.length;
+  return n % 2 ? s[(n - 1) / 2] : (s[n / 2 - 1] + s[n / 2]) / 2;
+}
+
+function summarize(msPerRun) {
+  const us = msPerRun.map((x) => x * 1e3);
+  return { median: median(us), min: Math.min.apply(null, us), max: Math.max.apply(null, us), n: us.length };
+}
+
+function verdict(base, other) {
+  const speedup = base.median / other.median;
+  const v = other.max < base.min ? 'win' : other.min > base.max ? 'loss' : 'noise';
+  return { speedup, verdict: v };
+}
+
+class HipBench {
+  constructor(runner) {
+    this.a = runner.a;
+    this.start = this.a.eventCreate();
+    this.end = this.a.eventCreate();
+  }
+
+  /** One repetition: k replays of `program` between two events; ms per run. */
+  rep(program, k) {
+    const a = this.a;
+    a.eventRecord(this.start);
+    for (let i = 0; i < k; i++) program.replay();
+    a.eventRecord(this.end);
+    return a.eventElapsed(this.start, this.end) / k;
+  }
+
+  /** k for `program`: a repetition of at least TARGET_MS. */
+  chooseK(program, opts) {
+    const target = (opts && opts.targetMs) || TARGET_MS;
+    program.capture();
+    this.rep(program, 1);
+    const one = this.rep(program, 1);
+    return Math.max(1, Math.min(MAX_K, Math.ceil(target / Math.max(one, 1e-4))));
+  }
+
+  /**
+   * Time several variants (name -> Program) of one workload: k from the first
+   * variant, warm-ups, then `reps` repetitions in ABBA order.
+   * Returns { k, stats: {name: summary}, msPerRun: {name: [..]} }.
+   */
+  time(variants, opts) {
+    const o = opts || {};
+    const names = Object.keys(variants);
+    const k = o.k || this.chooseK(variants[names[0]], o);
+    for (const n of names) {
+      variants[n].capture();
+      for (let i = 0; i < (o.warmup === undefined ? WARMUP : o.warmup); i++) this.rep(variants[n], k);
+    }
+    const msPerRun = {};
+    for (const n of names) msPerRun[n] = [];
+    const reps = o.reps || REPS;
+    for (let b = 0; b < reps; b++) {
+      const order = b % 2 === 0 ? names : names.slice().reverse();
+      for (const n of order) msPerRun[n].push(this.rep(variants[n], k));
+    }
+    const stats = {};
+    for (const n of names) stats[n] = summarize(msPerRun[n]);
+    return { k, stats, msPerRun };
+  }
+
+  destroy() {
+    this.a.eventDestroy(this.start);
+    this.a.eventDestroy(this.end);
+  }
+}
+
+module.exports = { HipBench, summarize, verdict, median, WARMUP, REPS, TARGET_MS };

@@ -1,0 +1,52 @@
+"""GPU parity of BASELINE config 2 (fused elementwise chains, forward and gradient)
+at its full size [8192, 1024], and of all eight programs at a small row count:
+every kept output of the fused and of the unfused launch list within the float32
+budget of the float64 oracle (streamed, node by node), canaries intact, and the
+fraction of outputs where fused and unfused agree bit for bit reported."""
+import sys
+
+import numpy as np
+import pytest
+
+from oracle import bounds
+
+pytestmark = pytest.mark.gpu
+
+
+def judge_bundle(b):
+    report = []
+    for c in b.cases:
+        inputs = {k: b.arr(v) for k, v in c["inputs"].items()}
+        ref = bounds.streaming_reference(c["graph"], inputs, c["keep"])
+        vals = [ref[k][0] for k in c["keep"]]
+        bnds = [ref[k][1] for k in c["keep"]]
+        jf = bounds.judge_outputs(vals, bnds, [b.arr(c["fused"][str(k)]) for k in c["keep"]])
+        ju = bounds.judge_outputs(vals, bnds, [b.arr(c["unfused"][str(k)]) for k in c["keep"]])
+        same = sum(int(np.sum(b.arr(c["fused"][str(k)]).view(np.uint32) == b.arr(c["unfused"][str(k)]).view(np.uint32)))
+                   for k in c["keep"])
+        total = sum(b.arr(c["fused"][str(k)]).size for k in c["keep"])
+        report.append((c["name"], jf, ju, same / total, c["canaryFused"], c["canaryUnfused"]))
+    return report
+
+
+def check(report):
+    for name, jf, ju, same, cf, cu in report:
+        print(f"{name}: fused worst {jf['worst']:.3g} unfused worst {ju['worst']:.3g} bitwise-same {same:.4f}",
+              file=sys.stderr)
+        assert jf["pass"], (name, "fused", jf["first"], jf["unjudged"])
+        assert ju["pass"], (name, "unfused", ju["first"], ju["unjudged"])
+        assert cf and cu, (name, "canary")
+
+
+def test_c2_all_programs_small(tmp_path, tool):
+    import tcmi_bridge
+    print("gpu step: gpu-chains seeds 0-7 at [64,1024]", flush=True)
+    tool("gpu-chains", {"seeds": list(range(8)), "R": 64, "C": 1024, "unfused": True}, out=str(tmp_path), timeout=300)
+    check(judge_bundle(tcmi_bridge.Bundle(tmp_path)))
+
+
+def test_c2_full_size(tmp_path, tool):
+    import tcmi_bridge
+    print("gpu step: gpu-chains seeds 0,1 at [8192,1024]", flush=True)
+    tool("gpu-chains", {"seeds": [0, 1], "R": 8192, "C": 1024, "unfused": True}, out=str(tmp_path), timeout=300)
+    check(judge_bundle(tcmi_bridge.Bundle(tmp_path)))

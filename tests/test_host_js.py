@@ -132,3 +132,21 @@ def test_every_golden_graph_lowers_with_loads_proved_in_bounds(golden_cases, too
                 assert len(l["params"]) <= 48
                 for k in l["kernels"]:
                     assert all(g >= 1 for g in k["grid"]) and k["block"][0] in (64, 256)
+
+
+def test_c2_programs_are_fully_judgeable(tool):
+    """Config 2's generator keeps every element of every program (forward and gradient)
+    judgeable: finite values inside float32's range and finite bounds."""
+    from oracle import bounds
+    progs = tool("chain-graphs", {"seeds": list(range(16)), "R": 32, "C": 1024})
+    rng = np.random.default_rng(7)
+    for p in progs:
+        feed = {"x0": rng.standard_normal(32 * 1024), "x1": rng.standard_normal(32 * 1024),
+                "r": rng.standard_normal(1024), "d0": rng.standard_normal(32 * 1024)}
+        for kind in ("forward", "gradient"):
+            v = p[kind]
+            ref = bounds.streaming_reference(v["graph"], feed, v["keep"])
+            vals = [ref[k][0] for k in v["keep"]]
+            bnds = [ref[k][1] for k in v["keep"]]
+            assert bounds.unjudgeable_count(vals, bnds) == 0, (p["seed"], kind, p["ops"])
+            assert 8 <= len(p["ops"]) <= 16
