@@ -75,12 +75,29 @@ def cpu_baseline(rows: int, seeds) -> dict:
             "seconds": secs}
 
 
+def profiled_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
+    (profiles/*_traffic.md, a json block), or None when that profile is of another kernel."""
+    for md in sorted((ROOT / "profiles").glob("*_traffic.md")):
+        text = md.read_text()
+        if "```json" not in text:
+            continue
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        try:
+            rec = json.loads(block)
+        except ValueError:
+            continue
+        if rec.get("kernel") == kernel:
+            return rec.get("traffic_bytes_per_launch"), md.name
+    return None, None
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--configs", default="c2,c3,c4")
+    ap.add_argument("--configs", default="ceiling,c2,c3,c4")
     ap.add_argument("--programs", type=int, default=8)
     ap.add_argument("--quick", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -124,6 +141,9 @@ def main() -> None:
                                         "GBs": r["gbs"]["fused"], "bitwise_same_outputs": r["bitwiseSameOutputs"]}
                             for r in c2["results"]}
     extra["device"] = {k: full["device"].get(k) for k in ("name", "arch", "computeUnits", "clockKHz", "totalMemory")}
+    if "ceiling" in cfg:
+        extra["ceiling_1GiB"] = {"copy_GBs": cfg["ceiling"]["copy"]["gbs"], "read_GBs": cfg["ceiling"]["read"]["gbs"]}
+    traffic, traffic_src = profiled_traffic(dom["code"])
     line = {
         "metric": METRIC, "value": c2["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": c2["steps"], "warmup": c2["warmup"],
         "ms_per_step": c2["msPerStep"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -132,7 +152,7 @@ def main() -> None:
                                "over fp32 [8192,1024] with a [1024] row broadcast",
                    "programs": c2["programs"], "shape": c2["shape"], "step_bytes": c2["stepBytes"]},
         "roofline": {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK, "unit": "GB/s", "frac": dom["gbs"] / HBM_PEAK,
-                     "traffic": None, "kernel": dom["code"], "kernel_avg_us": dom["avgUs"],
+                     "traffic": traffic, "traffic_source": traffic_src, "kernel": dom["code"], "kernel_avg_us": dom["avgUs"],
                      "bytes_per_launch": dom["bytesPerLaunch"], "launches_per_step": dom["count"]},
         "extra": extra,
     }

@@ -27,8 +27,6 @@
 
 namespace tcmi {
 
-typedef float f4 __attribute__((ext_vector_type(4)));
-
 template <int TM, int TN, bool VEC_A, bool VEC_B, class Epi>
 __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restrict__ a_ptr,
                                          const float* __restrict__ b_ptr) {

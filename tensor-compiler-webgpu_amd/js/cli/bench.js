@@ -3,8 +3,8 @@
 // Measurement of the MI355X backend on BASELINE's configs, printed as one JSON
 // document (bench.py turns it into the driver's one-line record).
 //
-//   node bench.js [--configs c2,c3,c4] [--steps K] [--warmup W] [--programs P]
-//                 [--reps N] [--c4-shapes all|small] [--quick]
+//   node bench.js [--configs ceiling,c2,c3,c4] [--steps K] [--warmup W] [--programs P]
+//                 [--reps N] [--c4-shapes all|small] [--quick] [--graphs] [--step-only]
 //
 // c2  fused elementwise chains (P programs, forward + gradient) over [8192, 1024]:
 //     the headline step = every fused program run once; K timed steps
@@ -47,7 +47,7 @@ function timeLaunches(runner, bench, program, reps) {
   const out = [];
   for (const l of program.lowered.launches) {
     const one = runner.prepare(program.graph, { launches: [l], workspace: program.lowered.workspace }, { buffers: program.bufs });
-    const r = bench.time({ one }, { reps: reps || 5, warmup: 1, targetMs: 0.5 });
+    const r = bench.time({ one }, { reps: reps || 5, warmup: 1, targetMs: 0.5, direct: true });
     out.push({ node: l.node, kind: l.kind, pattern: l.pattern || null, code: l.code, bytes: l.bytes, flops: l.flops,
       us: r.stats.one.median });
     one.destroy();
@@ -104,7 +104,12 @@ function measureGraph(runner, bench, name, graph, keep, inputs, opts) {
   return res;
 }
 
-/** The dominant kernel (by total time) of a set of launch timings, aggregated by kernel name. */
+/**
+ * The dominant kernel of a set of launch timings, aggregated by kernel name:
+ * the one moving the most algorithmic bytes (or, for matmuls, flops) in all —
+ * a choice that does not depend on timing noise, so a profile of the same
+ * command names the same kernel.
+ */
 function dominant(launches) {
   const by = new Map();
   for (const l of launches) {
@@ -113,7 +118,8 @@ function dominant(launches) {
     by.set(l.code, e);
   }
   let best = null;
-  for (const e of by.values()) if (!best || e.us > best.us) best = e;
+  const weight = (e) => (e.flops || e.bytes);
+  for (const e of by.values()) if (!best || weight(e) > weight(best)) best = e;
   if (!best) return null;
   const avgUs = best.us / best.count, bytes = best.bytes / best.count;
   return Object.assign(best, { avgUs, bytesPerLaunch: bytes, gbs: bytes / (avgUs * 1e3),
@@ -128,12 +134,22 @@ function c2(runner, bench, opts) {
   const K = Number(arg('steps', 20)), W = Number(arg('warmup', 3));
   const programs = [];
   const results = [];
+  const stepOnly = flag('step-only');
   for (let s = 0; s < P; s++) {
     const w = chainWorkload(s, R, C);
     const inputs = chainInputs(s, R, C);
     for (const kind of ['forward', 'gradient']) {
       const v = w[kind];
       log(`c2 program ${s} ${kind}`);
+      if (stepOnly) {
+        // Profiling mode: only the programs of the step, no per-variant timing.
+        const f = fuse(v.graph, { keep: v.keep });
+        const lf = lowerMI355X(f.graph);
+        runner.functions(lf);
+        programs.push(prepared(runner, f.graph, lf, inputs));
+        results.push({ name: `c2-p${s}-${kind}`, bytes: { fused: lf.launches.reduce((q, l) => q + l.bytes, 0) }, launchF: [] });
+        continue;
+      }
       const r = measureGraph(runner, bench, `c2-p${s}-${kind}`, v.graph, v.keep, inputs, { keepPrograms: true, reps: opts.reps });
       r.ops = w.ops;
       programs.push(r.programs.pf);
@@ -143,21 +159,24 @@ function c2(runner, bench, opts) {
     }
   }
   // The headline step: every fused program once; W warm-up steps, then K timed steps.
-  for (const p of programs) p.capture();
-  for (let i = 0; i < W; i++) for (const p of programs) p.replay();
+  const go = bench.graphs ? (p) => p.replay() : (p) => p.run();
+  for (const p of programs) if (bench.graphs) p.capture();
+  for (let i = 0; i < W; i++) for (const p of programs) go(p);
   runner.a.sync();
   const t0 = process.hrtime.bigint();
   runner.a.eventRecord(bench.start);
-  for (let i = 0; i < K; i++) for (const p of programs) p.replay();
+  for (let i = 0; i < K; i++) for (const p of programs) go(p);
   runner.a.eventRecord(bench.end);
   const ms = runner.a.eventElapsed(bench.start, bench.end);
   runner.a.sync();
   const wallMs = Number(process.hrtime.bigint() - t0) / 1e6;
   for (const p of programs) p.destroy();
   const stepBytes = results.reduce((s, r) => s + r.bytes.fused, 0);
-  const all = [].concat.apply([], results.map((r) => r.launchF));
+  // The roofline kernel: the fused kernel taking the most time in the step (each
+  // fused body is its own kernel, at one size, so its average is well defined).
+  const all = [].concat.apply([], results.map((r) => r.launchF)).filter((l) => l.kind.startsWith('fused-'));
   return { config: 'c2', shape: [R, C], programs: P, steps: K, warmup: W, msPerStep: ms / K, wallMsPerStep: wallMs / K,
-    stepBytes, gbs: stepBytes / ((ms / K) * 1e6), dominant: dominant(all), results };
+    stepBytes, gbs: stepBytes / ((ms / K) * 1e6), dominant: stepOnly ? null : dominant(all), results };
 }
 
 function c3(runner, bench, opts) {
@@ -208,13 +227,37 @@ function c4(runner, bench, opts) {
   return { config: 'c4', shapes, dominant: dominant(mm), results };
 }
 
+/** The bandwidth ceiling (workloads.js:312-345): copy and pure read of 1 GiB, grid-strided, 1024 x 256 threads. */
+function ceiling(runner, bench) {
+  const a = runner.a;
+  const bytes = 2 ** 30;
+  const src = a.malloc(bytes), dst = a.malloc(bytes);
+  a.fill32(src, 0, 0x3f800000, bytes / 4);
+  const out = {};
+  for (const mode of ['copy', 'read']) {
+    const run = () => (mode === 'copy' ? a.ceilingCopy(dst, src, bytes, 1024) : a.ceilingRead(dst, src, bytes, 1024));
+    for (let i = 0; i < 3; i++) run();
+    const ms = [];
+    for (let r = 0; r < 10; r++) {
+      a.eventRecord(bench.start);
+      for (let i = 0; i < 5; i++) run();
+      a.eventRecord(bench.end);
+      ms.push(a.eventElapsed(bench.start, bench.end) / 5);
+    }
+    const med = median(ms);
+    out[mode] = { bytes: mode === 'copy' ? 2 * bytes : bytes, us: med * 1e3, gbs: (mode === 'copy' ? 2 * bytes : bytes) / (med * 1e6) };
+  }
+  a.free(src); a.free(dst);
+  return Object.assign({ config: 'ceiling', kernel: { copy: 'k_copy16', read: 'k_read16' }, blocks: 1024 }, out);
+}
+
 async function main() {
   const runner = HipRunner.create();
-  const bench = new HipBench(runner);
+  const bench = new HipBench(runner, { graphs: flag('graphs') });
   const opts = { quick: flag('quick'), reps: arg('reps') ? Number(arg('reps')) : undefined };
-  const which = arg('configs', 'c2,c3,c4').split(',');
+  const which = arg('configs', 'ceiling,c2,c3,c4').split(',');
   const out = { device: runner.info(), peaks: { hbmGBs: HBM_PEAK_GBS, fp32MfmaTFLOPs: FP32_MFMA_PEAK_TFLOPS }, configs: {} };
-  const fns = { c2, c3, c4 };
+  const fns = { c2, c3, c4, ceiling };
   for (const c of which) {
     if (!fns[c]) throw new Error(`unknown config ${c}`);
     const t0 = Date.now();

@@ -4,8 +4,9 @@
 //   * a repetition is k back-to-back runs of a prepared program, bracketed by
 //     two hipEvents on the stream the kernels run on; k is chosen from a
 //     single run so one repetition lasts >= 2 ms (bench.js:178-181);
-//   * every program is captured once as a HIP graph and replayed, so nothing
-//     is created inside a timed region and host launch cost stays off the clock;
+//   * every buffer, argument block and function handle is made before the
+//     timed region; a program run is one native call issuing all its launches
+//     (or, with `graphs`, the replay of a HIP graph captured once);
 //   * 5 warm-up repetitions per variant, then 32 repetitions in ABBA order;
 //   * summaries are median/min/max microseconds per program run, and two
 //     variants win or lose against each other only when their min-max ranges
@@ -34,17 +35,24 @@ function verdict(base, other) {
 }
 
 class HipBench {
-  constructor(runner) {
+  constructor(runner, options) {
     this.a = runner.a;
+    this.graphs = !!(options && options.graphs);
     this.start = this.a.eventCreate();
     this.end = this.a.eventCreate();
   }
 
-  /** One repetition: k replays of `program` between two events; ms per run. */
-  rep(program, k) {
+  /**
+   * One repetition: k runs of `program` between two events; ms per run. By
+   * default the k runs' launches are issued directly, all in one native call,
+   * so the GPU runs them back to back; with `graphs` the program is captured
+   * once as a HIP graph and replayed k times.
+   */
+  rep(program, k, direct) {
     const a = this.a;
     a.eventRecord(this.start);
-    for (let i = 0; i < k; i++) program.replay();
+    if (direct) program.runTimes(k);
+    else for (let i = 0; i < k; i++) program.replay();
     a.eventRecord(this.end);
     return a.eventElapsed(this.start, this.end) / k;
   }
@@ -52,9 +60,10 @@ class HipBench {
   /** k for `program`: a repetition of at least TARGET_MS. */
   chooseK(program, opts) {
     const target = (opts && opts.targetMs) || TARGET_MS;
-    program.capture();
-    this.rep(program, 1);
-    const one = this.rep(program, 1);
+    const direct = !this.graphs || !!(opts && opts.direct);
+    if (!direct) program.capture();
+    this.rep(program, 1, direct);
+    const one = this.rep(program, 1, direct);
     return Math.max(1, Math.min(MAX_K, Math.ceil(target / Math.max(one, 1e-4))));
   }
 
@@ -66,17 +75,18 @@ class HipBench {
   time(variants, opts) {
     const o = opts || {};
     const names = Object.keys(variants);
+    const direct = !this.graphs || !!o.direct;
     const k = o.k || this.chooseK(variants[names[0]], o);
     for (const n of names) {
-      variants[n].capture();
-      for (let i = 0; i < (o.warmup === undefined ? WARMUP : o.warmup); i++) this.rep(variants[n], k);
+      if (!direct) variants[n].capture();
+      for (let i = 0; i < (o.warmup === undefined ? WARMUP : o.warmup); i++) this.rep(variants[n], k, direct);
     }
     const msPerRun = {};
     for (const n of names) msPerRun[n] = [];
     const reps = o.reps || REPS;
     for (let b = 0; b < reps; b++) {
       const order = b % 2 === 0 ? names : names.slice().reverse();
-      for (const n of order) msPerRun[n].push(this.rep(variants[n], k));
+      for (const n of order) msPerRun[n].push(this.rep(variants[n], k, direct));
     }
     const stats = {};
     for (const n of names) stats[n] = summarize(msPerRun[n]);

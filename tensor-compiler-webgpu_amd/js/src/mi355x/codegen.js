@@ -136,11 +136,23 @@ class Emitter {
       if (this.params.length > MAX_P) throw new Error(`kernel parameters exceed ${MAX_P} words`);
       this.gatherBase.set(key, base);
     }
+    // The index maps are baked into the kernel text as constants (the lowering
+    // knows every shape): divisions and remainders by powers of two become
+    // shifts and masks, the rest multiplications. P keeps them for inspection.
     if (g.mode === 'span') {
-      if (g.inner === 1) return { idx: `((${ctx.idx}) % A.P[${base + 1}])`, g, base };
-      return { idx: `tcmi::idx_span(${ctx.idx}, A.P[${base}], A.P[${base + 1}])`, g, base };
+      if (g.inner === 1) return { idx: `((${ctx.idx}) % ${g.extent}u)`, g, base };
+      return { idx: `(((${ctx.idx}) / ${g.inner}u) % ${g.extent}u)`, g, base };
     }
-    return { idx: `tcmi::idx_general(${ctx.idx}, A.P, ${base}u)`, g, base };
+    let e = '0u';
+    let rem = `(${ctx.idx})`;
+    const terms = [];
+    for (let d = g.extents.length - 1; d >= 0; d--) {
+      const ext = g.extents[d], st = g.strides[d];
+      if (st !== 0 && ext > 1) terms.push(`((${rem}) % ${ext}u) * ${st}u`);
+      rem = `(${rem}) / ${ext}u`;
+    }
+    if (terms.length) e = terms.join(' + ');
+    return { idx: `(${e})`, g, base };
   }
 
   value(id, ctx, lines) {
@@ -206,56 +218,52 @@ const indent = (lines, pad) => lines.map((l) => pad + l).join('\n');
 
 /**
  * A fused (or one-op) elementwise body over n output elements, output node
- * `output` of body graph `b`. Grid-stride over float4 groups; a scalar tail
- * for n % 4. Operands read at the output index are loaded as float4; a span
- * load is a float4 when its 4 lanes are contiguous in the source, one scalar
- * when they share an element, else 4 scalars.
+ * `output` of body graph `b`. A grid-stride loop over float4 groups with a
+ * fixed, modest number of long-lived workgroups (`blocks`, default 2048 = 8
+ * per CU): each trip a thread loads U groups spaced one grid apart (every
+ * operand load of all U issued before any arithmetic), computes, and stores
+ * (non-temporally by default: the output is not re-read by this kernel). A
+ * scalar tail handles n % 4. Operands read at the output index are float4
+ * loads; a span load is a float4 when its 4 lanes are contiguous in the source,
+ * one scalar when they share an element, else 4 scalars.
+ * `tuning`: { unroll (U, default 1), nt (default true), blocks (default 2048) }.
  */
 function elementwiseKernel(b, output, outShape, opts) {
   const o = opts || {};
+  const tune = o.tuning || {};
+  const U = tune.unroll || 1;
+  const nt = tune.nt === undefined ? true : !!tune.nt;
+  const maxBlocks = tune.blocks || 2048;
   checkOperands(b);
   const n = size(outShape);
   if (n >= 2 ** 31) throw new Error(`elementwise kernel over ${n} elements exceeds the 32-bit index space`);
   const params = [n];
 
-  // Vector pass: hoisted loads go to `hoist`, lane code to `lane`.
+  // Vector pass: hoisted loads fill per-group arrays in `hoist`; lane code in `lane`.
+  const decl = [];
   const hoist = [];
   const hoisted = new Map();
+  const hoistAs = (key, type, expr) => {
+    if (!hoisted.has(key)) {
+      const h = `H${hoisted.size}`;
+      decl.push(`${type} ${h}[${U}];`);
+      hoist.push(`${h}[j] = ${expr};`);
+      hoisted.set(key, h);
+    }
+    return hoisted.get(key);
+  };
   const vecEmitter = new Emitter(b, params, {
     load(k, ctx, lines) {
-      if (ctx.root) {
-        const hk = `full${k}`;
-        if (!hoisted.has(hk)) {
-          const h = `H${hoisted.size}`;
-          hoist.push(`const float4 ${h} = reinterpret_cast<const float4*>(A.in[${k}])[v];`);
-          hoisted.set(hk, h);
-        }
-        return `tcmi::lane4(${hoisted.get(hk)}, l)`;
-      }
+      if (ctx.root) return `${hoistAs(`full${k}`, 'tcmi::f4', `reinterpret_cast<const tcmi::f4*>(A.in[${k}])[v]`)}[j][l]`;
       const g = ctx.gather;
       if (ctx.parent && ctx.parent.root && g) {
-        if (g.g.mode === 'zero') {
-          const hk = `zero${k}`;
-          if (!hoisted.has(hk)) { const h = `H${hoisted.size}`; hoist.push(`const float ${h} = A.in[${k}][0];`); hoisted.set(hk, h); }
-          return hoisted.get(hk);
-        }
+        if (g.g.mode === 'zero') return `${hoistAs(`zero${k}`, 'float', `A.in[${k}][0]`)}[j]`;
         if (g.g.mode === 'span' && g.g.inner === 1 && g.g.extent % 4 === 0) {
-          const hk = `spanv${k}|${ctx.key}`;
-          if (!hoisted.has(hk)) {
-            const h = `H${hoisted.size}`;
-            hoist.push(`const float4 ${h} = reinterpret_cast<const float4*>(A.in[${k}])[(i0 % A.P[${g.base + 1}]) >> 2];`);
-            hoisted.set(hk, h);
-          }
-          return `tcmi::lane4(${hoisted.get(hk)}, l)`;
+          return `${hoistAs(`spanv${k}|${ctx.key}`, 'tcmi::f4',
+            `reinterpret_cast<const tcmi::f4*>(A.in[${k}])[(i0 % ${g.g.extent}u) >> 2]`)}[j][l]`;
         }
         if (g.g.mode === 'span' && g.g.inner % 4 === 0) {
-          const hk = `spans${k}|${ctx.key}`;
-          if (!hoisted.has(hk)) {
-            const h = `H${hoisted.size}`;
-            hoist.push(`const float ${h} = A.in[${k}][tcmi::idx_span(i0, A.P[${g.base}], A.P[${g.base + 1}])];`);
-            hoisted.set(hk, h);
-          }
-          return hoisted.get(hk);
+          return `${hoistAs(`spans${k}|${ctx.key}`, 'float', `A.in[${k}][(i0 / ${g.g.inner}u) % ${g.g.extent}u]`)}[j]`;
         }
       }
       const v = `L${lines.length}_${k}`;
@@ -279,21 +287,38 @@ function elementwiseKernel(b, output, outShape, opts) {
   const tout = tailEmitter.value(output, { key: 'i', idx: 'i', root: true, limit: n }, tail);
 
   const guard = o.sabotage === 'fused-bounds-off-by-one' ? 'threadIdx.x <= (n & 3u)' : 'threadIdx.x < (n & 3u)';
+  const store = nt ? '__builtin_nontemporal_store(o4, reinterpret_cast<tcmi::f4*>(A.out) + v);'
+    : 'reinterpret_cast<tcmi::f4*>(A.out)[v] = o4;';
   const text = `extern "C" __global__ void __launch_bounds__(${WG}) __KERNEL__(const TcmiArgs A) {
-  const uint32_t n = A.P[0];
+  const uint32_t n = ${n}u;
   const uint32_t nv = n >> 2;
   const uint32_t stride = gridDim.x * ${WG}u;
-  for (uint32_t v = blockIdx.x * ${WG}u + threadIdx.x; v < nv; v += stride) {
-    const uint32_t i0 = v << 2;
-${indent(hoist, '    ')}
-    float r[4];
+  for (uint32_t base = blockIdx.x * ${WG}u + threadIdx.x; base < nv; base += ${U}u * stride) {
+${indent(decl, '    ')}
 #pragma unroll
-    for (int l = 0; l < 4; ++l) {
-      const uint32_t i = i0 + l;
-${indent(lane, '      ')}
-      r[l] = ${vout};
+    for (int j = 0; j < ${U}; ++j) {
+      const uint32_t v = base + j * stride;
+      if (v < nv) {
+        const uint32_t i0 = v << 2;
+${indent(hoist, '        ')}
+      }
     }
-    reinterpret_cast<float4*>(A.out)[v] = make_float4(r[0], r[1], r[2], r[3]);
+#pragma unroll
+    for (int j = 0; j < ${U}; ++j) {
+      const uint32_t v = base + j * stride;
+      if (v < nv) {
+        const uint32_t i0 = v << 2;
+        float r[4];
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+          const uint32_t i = i0 + l;
+${indent(lane, '          ')}
+          r[l] = ${vout};
+        }
+        const tcmi::f4 o4 = {r[0], r[1], r[2], r[3]};
+        ${store}
+      }
+    }
   }
   if (blockIdx.x == 0 && ${guard}) {
     const uint32_t i = (nv << 2) + threadIdx.x;
@@ -303,8 +328,7 @@ ${indent(tail, '    ')}
 }
 `;
   const k = kernelText('ew', text);
-  // Enough workgroups to fill 256 CUs several times over; grid-stride covers the rest.
-  const groups = Math.max(1, Math.min(Math.ceil(Math.max(1, n >> 2) / WG), 256 * 16));
+  const groups = Math.max(1, Math.min(Math.ceil(Math.max(1, n >> 2) / WG), maxBlocks));
   return { name: k.name, source: k.source, params: Uint32Array.from(params), grid: [groups, 1, 1], block: [WG, 1, 1], lds: 0, workspace: 0 };
 }
 
@@ -479,8 +503,8 @@ ${indent(inner, '      ')}
   }
   const text = `extern "C" __global__ void __launch_bounds__(${T}) __KERNEL__(const TcmiArgs A) {
   __shared__ float red[${T / 64}];
-  const uint32_t R = A.P[0];
-  const uint32_t C = A.P[1];
+  const uint32_t R = ${R}u;
+  const uint32_t C = ${C}u;
   for (uint32_t r = blockIdx.x; r < R; r += gridDim.x) {
     const uint32_t rowBase = r * C;
 ${indent(cacheDecl, '    ')}
@@ -497,62 +521,98 @@ ${indent(store, '    ')}
 // ---- column reductions (sum / max over a non-last axis) --------------------------------
 
 /**
- * out[o, j] = reduce_k x[o, k, j] over [outer, n, inner] with inner > 1.
- * 256 threads = 64 columns x 4 row groups; the n axis is split across
- * workgroups when one column block alone would leave the chip idle, the
- * partials going to the workspace and a second kernel combining them.
+ * out[o, j] = reduce_k x[o, k, j] over [outer, n, inner] with inner > 1: the
+ * column sums autodiff emits for every broadcast operand (bias gradients).
+ * Vector form (inner % 4 == 0): a workgroup owns 256 columns (each lane a
+ * float4 of them) and a chunk of rows; its 4 wavefronts take every 4th row of
+ * the chunk, 128-bit loads, and their partials meet in LDS. Enough row chunks
+ * are made to give every CU work; each chunk's partial goes to the workspace,
+ * and a second kernel combines the chunks, again 4 wavefronts per column tile.
+ * Every output sums its terms in a fixed order (deterministic). Scalar form
+ * (inner % 4 != 0): the same with one column per lane.
  */
-function colreduceKernels(op, outer, n, inner) {
+function colreduceKernels(op, outer, n, inner, tuning) {
+  const tune = tuning || {};
   const isMax = op === 'max';
-  const colBlocks = Math.ceil(inner / 64);
-  const want = 2048;
-  let splits = Math.max(1, Math.min(Math.ceil(want / Math.max(1, colBlocks * outer)), Math.ceil(n / 64)));
-  const chunk = Math.ceil(n / splits);
-  splits = Math.ceil(n / chunk);
   const init = isMax ? '(-TCMI_INF)' : '0.f';
   const comb = isMax ? 'tcmi::red_max' : 'tcmi::red_sum';
+  const vec = inner % 4 === 0;
+  const W = vec ? 4 : 1;
+  const colsPerBlock = 64 * W;
+  const colBlocks = Math.ceil(inner / colsPerBlock);
+  const want = tune.blocks || 1024;
+  let splits = Math.max(1, Math.min(Math.ceil(want / Math.max(1, colBlocks * outer)), Math.ceil(n / 32)));
+  const chunk = Math.ceil(n / splits);
+  splits = Math.ceil(n / chunk);
+  const T = vec ? 'tcmi::f4' : 'float';
+  const zero = vec ? `tcmi::f4{${init}, ${init}, ${init}, ${init}}` : init;
+  const combV = vec
+    ? (a, b) => `tcmi::f4{${comb}(${a}[0], ${b}[0]), ${comb}(${a}[1], ${b}[1]), ${comb}(${a}[2], ${b}[2]), ${comb}(${a}[3], ${b}[3])}`
+    : (a, b) => `${comb}(${a}, ${b})`;
+  const ld = (ptr, idx) => (vec ? `reinterpret_cast<const tcmi::f4*>(${ptr})[(${idx}) >> 2]` : `(${ptr})[${idx}]`);
+  const st = (ptr, idx, v) => (vec ? `reinterpret_cast<tcmi::f4*>(${ptr})[(${idx}) >> 2] = ${v};` : `(${ptr})[${idx}] = ${v};`);
   const first = `extern "C" __global__ void __launch_bounds__(256) __KERNEL__(const TcmiArgs A) {
-  __shared__ float part[4][64];
-  const uint32_t n = A.P[1], inner = A.P[2], splits = A.P[3], chunk = A.P[4];
-  const uint32_t j = blockIdx.x * 64u + (threadIdx.x & 63u);
-  const uint32_t g = threadIdx.x >> 6;
+  __shared__ ${T} part[4][64];
+  const uint32_t n = ${n}u, inner = ${inner}u, splits = ${splits}u, chunk = ${chunk}u;
+  const uint32_t lane = threadIdx.x & 63u, g = threadIdx.x >> 6;
+  const uint32_t j = blockIdx.x * ${colsPerBlock}u + lane * ${W}u;
   const uint32_t s = blockIdx.y, o = blockIdx.z;
   const uint32_t k0 = s * chunk;
   const uint32_t k1 = min(n, k0 + chunk);
-  float acc = ${init};
+  ${T} acc = ${zero};
   if (j < inner) {
-    const float* __restrict__ x = A.in[0] + (size_t)o * n * inner + j;
-    for (uint32_t k = k0 + g; k < k1; k += 4u) acc = ${comb}(acc, x[(size_t)k * inner]);
+    const float* __restrict__ x = A.in[0] + (size_t)o * n * inner;
+#pragma unroll 8
+    for (uint32_t k = k0 + g; k < k1; k += 4u) {
+      const ${T} v = ${ld('x', '(size_t)k * inner + j')};
+      acc = ${combV('acc', 'v')};
+    }
   }
-  part[g][threadIdx.x & 63u] = acc;
+  part[g][lane] = acc;
   __syncthreads();
   if (g == 0 && j < inner) {
-    float r = part[0][threadIdx.x];
-    r = ${comb}(r, part[1][threadIdx.x]);
-    r = ${comb}(r, part[2][threadIdx.x]);
-    r = ${comb}(r, part[3][threadIdx.x]);
-    if (splits == 1u) A.out[(size_t)o * inner + j] = r;
-    else A.ws[((size_t)o * splits + s) * inner + j] = r;
+    ${T} r = part[0][lane];
+    r = ${combV('r', 'part[1][lane]')};
+    r = ${combV('r', 'part[2][lane]')};
+    r = ${combV('r', 'part[3][lane]')};
+    if (splits == 1u) { ${st('A.out', '(size_t)o * inner + j', 'r')} }
+    else { ${st('A.ws', '((size_t)o * splits + s) * inner + j', 'r')} }
   }
 }
 `;
   const k1 = kernelText('colred', first);
   const launches = [{ name: k1.name, source: k1.source, grid: [colBlocks, splits, outer], block: [256, 1, 1], lds: 0 }];
   if (splits > 1) {
+    // 16 column groups x 16 split groups per workgroup: every CU of a good share of
+    // the chip reads a slice of the partials, 16 split rows per thread at most.
+    const groupsPerBlock = 16;
     const second = `extern "C" __global__ void __launch_bounds__(256) __KERNEL__(const TcmiArgs A) {
-  const uint32_t inner = A.P[2], splits = A.P[3], outer = A.P[0];
-  const uint32_t total = outer * inner;
-  for (uint32_t t = blockIdx.x * 256u + threadIdx.x; t < total; t += gridDim.x * 256u) {
-    const uint32_t o = t / inner, j = t - o * inner;
-    const float* __restrict__ w = A.ws + (size_t)o * splits * inner + j;
-    float r = w[0];
-    for (uint32_t s = 1; s < splits; ++s) r = ${comb}(r, w[(size_t)s * inner]);
-    A.out[t] = r;
+  __shared__ ${T} part[16][${groupsPerBlock}];
+  const uint32_t inner = ${inner}u, splits = ${splits}u;
+  const uint32_t c = threadIdx.x & ${groupsPerBlock - 1}u, g = threadIdx.x / ${groupsPerBlock}u;
+  const uint32_t j = (blockIdx.x * ${groupsPerBlock}u + c) * ${W}u;
+  const uint32_t o = blockIdx.y;
+  ${T} acc = ${zero};
+  if (j < inner) {
+    const float* __restrict__ w = A.ws + (size_t)o * splits * inner;
+#pragma unroll 8
+    for (uint32_t s = g; s < splits; s += 16u) {
+      const ${T} v = ${ld('w', '(size_t)s * inner + j')};
+      acc = ${combV('acc', 'v')};
+    }
+  }
+  part[g][c] = acc;
+  __syncthreads();
+  if (g == 0 && j < inner) {
+    ${T} r = part[0][c];
+#pragma unroll
+    for (int q = 1; q < 16; ++q) r = ${combV('r', 'part[q][c]')};
+    ${st('A.out', '(size_t)o * inner + j', 'r')}
   }
 }
 `;
     const k2 = kernelText('colfin', second);
-    launches.push({ name: k2.name, source: k2.source, grid: [Math.max(1, Math.min(Math.ceil(outer * inner / 256), 4096)), 1, 1], block: [256, 1, 1], lds: 0 });
+    launches.push({ name: k2.name, source: k2.source, grid: [Math.ceil(inner / (W * groupsPerBlock)), outer, 1], block: [256, 1, 1], lds: 0 });
   }
   return { launches, params: Uint32Array.from([outer, n, inner, splits, chunk]), workspace: splits > 1 ? outer * splits * inner * 4 : 0 };
 }

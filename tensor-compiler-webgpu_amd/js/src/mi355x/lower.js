@@ -52,8 +52,11 @@ function lowerNode(graph, node, opts) {
     const b = bodyOf(node);
     const out = node.attrs.output;
     const kind = node.attrs.kind;
+    const tuning = opts.tuning || {};
     const sab = { sabotage: opts.sabotage, pattern: node.attrs.pattern };
-    if (kind === 'elementwise') return Object.assign({ kind: 'fused-elementwise' }, single(cg.elementwiseKernel(b, out, node.shape, sab)));
+    if (kind === 'elementwise') {
+      return Object.assign({ kind: 'fused-elementwise' }, single(cg.elementwiseKernel(b, out, node.shape, Object.assign({ tuning: tuning.ew }, sab))));
+    }
     if (kind === 'rowwise') return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(b, out, sab)));
     if (kind === 'epilogue') return Object.assign({ kind: 'fused-epilogue' }, single(cg.gemmKernel(b, out, sab)));
     throw new Error(`no MI355X kernel for fused kind '${kind}'`);
@@ -61,7 +64,7 @@ function lowerNode(graph, node, opts) {
   if (ELEMENTWISE_OPS.has(node.op) || GATHERS.has(node.op)) {
     const { body, output } = oneOpBody(graph, node);
     const kind = GATHERS.has(node.op) ? 'gather' : 'elementwise';
-    return Object.assign({ kind }, single(cg.elementwiseKernel(body, output, node.shape, {})));
+    return Object.assign({ kind }, single(cg.elementwiseKernel(body, output, node.shape, { tuning: (opts.tuning || {}).ew })));
   }
   if (node.op === 'sum' || node.op === 'max') {
     const inShape = graph.nodes[node.inputs[0]].shape;
@@ -72,7 +75,7 @@ function lowerNode(graph, node, opts) {
       const { body, output } = oneOpBody(graph, node, [[outer, n]], { axis: 1, keepDims: true });
       return Object.assign({ kind: 'rowreduce' }, single(cg.rowwiseKernel(body, output, {})));
     }
-    const c = cg.colreduceKernels(node.op, outer, n, inner);
+    const c = cg.colreduceKernels(node.op, outer, n, inner, (opts.tuning || {}).colreduce);
     return { kind: 'colreduce', kernels: c.launches, params: c.params, workspace: c.workspace, flops: 0 };
   }
   if (node.op === 'matmul') {
@@ -86,7 +89,8 @@ function lowerNode(graph, node, opts) {
  * Lower `graph` for the MI355X runner. Options: sabotage (one of the
  * reference's fused-kernel sabotages: 'epilogue-before-bias',
  * 'layernorm-tree-short', 'softmax-no-max', 'fused-bounds-off-by-one'),
- * applied to fused kernels only.
+ * applied to fused kernels only; tuning ({ ew: { unroll, nt, blocks }, colreduce: { blocks } })
+ * overrides the kernels' launch-shape defaults (used by sweeps).
  * Returns { launches, workspace } (workspace: bytes of scratch the largest launch needs).
  */
 function lowerMI355X(graph, options) {
@@ -98,7 +102,7 @@ function lowerMI355X(graph, options) {
     if (node.op === 'input' || node.op === 'const') continue;
     // Kernels depend on structure and shapes only: reuse across identical nodes.
     const key = JSON.stringify([node.op, node.inputs.map((id) => graph.nodes[id].shape), node.attrs, node.shape,
-      node.op === 'fused' ? opts.sabotage : null]);
+      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null]);
     let k = cache.get(key);
     if (!k) { k = lowerNode(graph, node, opts); cache.set(key, k); }
     workspace = Math.max(workspace, k.workspace);

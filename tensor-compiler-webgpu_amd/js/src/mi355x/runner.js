@@ -247,6 +247,24 @@ class Program {
   /** Enqueue every launch once (asynchronous). */
   run() { this.a.launchMany(this.fns, this.dims, this.args, this.offsets); }
 
+  /** Enqueue every launch `k` times over, in one native call (timing back-to-back runs). */
+  runTimes(k) {
+    if (!this.repeated || this.repeated.k !== k) {
+      const n = this.count;
+      const fns = new Float64Array(n * k), dims = new Uint32Array(n * k * 7);
+      const args = new Uint8Array(n * k * ARG_BYTES), offsets = new Uint32Array(n * k + 1);
+      for (let r = 0; r < k; r++) {
+        fns.set(this.fns, r * n);
+        dims.set(this.dims, r * n * 7);
+        args.set(this.args, r * n * ARG_BYTES);
+      }
+      for (let i = 0; i <= n * k; i++) offsets[i] = i * ARG_BYTES;
+      this.repeated = { k, fns, dims, args, offsets };
+    }
+    const r = this.repeated;
+    this.a.launchMany(r.fns, r.dims, r.args, r.offsets);
+  }
+
   /** Capture one run() as a HIP graph; later replay() calls enqueue it whole. */
   capture() {
     if (this.graphHandle) return;
