@@ -69,7 +69,7 @@ def check_node_loads() -> None:
           LIB / "tcmi.node"])
 
 
-PRECOMPILE_GROUPS = ["direct"]
+PRECOMPILE_GROUPS = ["direct", "models"]
 
 
 def precompile(groups=None) -> None:

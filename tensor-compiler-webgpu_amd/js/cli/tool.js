@@ -18,6 +18,7 @@
 //   gpu-graphs       request {graphs: [{name, graph, inputs, keep, unfused?}]} fused (and unfused) on the GPU
 
 const fs = require('fs');
+const fs_ = fs;
 const path = require('path');
 const { Graph } = require('../src/ir/graph');
 const { grad } = require('../src/autodiff');
@@ -93,6 +94,15 @@ function transformerInit(req) {
 function precompileGroup(group, arch) {
   const { precompile } = require('../src/mi355x/runner');
   if (group === 'direct') return precompile(fusedDirectCases().map((c) => lowerMI355X(fuse(c.graph).graph)), arch);
+  if (group === 'models') {
+    // The trainer compiles a step's kernels as one module: the same text here.
+    const { modelStep } = require('../src/builders/models');
+    const { fusedStep } = require('../src/mi355x/trainer');
+    const reqs = [{ model: 'mlp' }, { model: 'transformer', B: 1 }, { model: 'transformer', B: 64 }, { model: 'transformer-ref' }];
+    let n = 0;
+    for (const r of reqs) n += precompile([fusedStep(modelStep(r).step).lowered], arch);
+    return n;
+  }
   throw new Error(`unknown precompile group '${group}'`);
 }
 
@@ -183,6 +193,107 @@ async function gpuChains(req, dir) {
   bundle.close({ device: runner.info() });
 }
 
+/**
+ * The step graph of a model request as a bundle: the original and fused graphs,
+ * the origin map, the ids that matter, and the step's inputs (parameters, state,
+ * batch k, cotangent 1) as float32 arrays. No GPU.
+ */
+function stepGraph(req, dir) {
+  const { modelStep } = require('../src/builders/models');
+  const { fusedStep } = require('../src/mi355x/trainer');
+  const m = modelStep(req);
+  const fs = fusedStep(m.step);
+  const bundle = new Bundle(dir);
+  const b = m.batch(req.batchIndex || 0);
+  const values = Object.assign({}, m.params, m.state, { x: b.x, y: b.y });
+  values[m.step.cotangent] = [1];
+  const inputs = {};
+  for (const k of Object.keys(values)) inputs[k] = bundle.put(values[k]);
+  bundle.add({ name: req.model, graph: m.step.graph.toJSON(), fused: fs.graph.toJSON(), origin: fs.fusion.origin, inputs,
+    loss: m.step.loss, logits: m.step.logits, outputs: m.step.outputs, stepInputs: m.step.inputs, names: m.step.names,
+    launchesFused: fs.lowered.launches.length, info: m.info });
+  bundle.close();
+}
+
+/**
+ * Node-local run of a model's fused step: every launch reads the float32
+ * reference operands given in `values.f32` (all fused-graph nodes, in node
+ * order, as the checker computed them) and writes its own output (with canaries).
+ */
+async function gpuLocal(req, dir) {
+  const { modelStep } = require('../src/builders/models');
+  const { fusedStep } = require('../src/mi355x/trainer');
+  const { HipRunner } = require('../src/mi355x/runner');
+  const m = modelStep(req);
+  const fs = fusedStep(m.step, { sabotage: req.sabotage });
+  const raw = fs_.readFileSync(req.valuesFile);
+  const data = new Float32Array(raw.buffer, raw.byteOffset, raw.byteLength / 4);
+  const values = [];
+  let off = 0;
+  for (const node of fs.graph.nodes) {
+    const n = node.shape.reduce((a, c) => a * c, 1);
+    values.push(data.subarray(off, off + n));
+    off += n;
+  }
+  if (off !== data.length) throw new Error(`values file holds ${data.length} floats, the fused graph needs ${off}`);
+  const runner = HipRunner.create();
+  const out = await runner.runLocal(fs.graph, fs.lowered, values, { canary: true });
+  const bundle = new Bundle(dir);
+  const gpu = {};
+  for (const l of fs.lowered.launches) gpu[l.node] = bundle.put(out[l.node]);
+  bundle.add({ name: req.model, gpu, canaryIntact: fs.lowered.launches.every((l) => out.canaryIntact[l.node]),
+    launches: fs.lowered.launches.length });
+  bundle.close({ device: runner.info() });
+}
+
+/**
+ * Train a model for `steps` steps on the GPU with the fused trainer; with
+ * `consistency`, also run the first steps through runner.run on the same fused
+ * graph and compare loss and parameters bit for bit (the trainer's feedback
+ * against the checked path, harness-m4.js:310-330).
+ */
+async function gpuTrain(req) {
+  const { modelStep } = require('../src/builders/models');
+  const { fusedStep, HipTrainer } = require('../src/mi355x/trainer');
+  const { HipRunner } = require('../src/mi355x/runner');
+  const m = modelStep(req);
+  const fs = fusedStep(m.step);
+  const runner = HipRunner.create();
+  const trainer = new HipTrainer(runner, fs, m.params, m.state);
+  const losses = [];
+  let identical = null;
+  const names = Object.keys(Object.assign({}, m.params, m.state));
+  let inputs = null;
+  if (req.consistency) {
+    identical = true;
+    inputs = {};
+    for (const n of names) inputs[n] = Float32Array.from(Object.assign({}, m.params, m.state)[n]);
+  }
+  for (let t = 0; t < req.steps; t++) {
+    const b = m.batch(req.sameBatch ? 0 : t);
+    const loss = trainer.train(b.x, b.y);
+    losses.push(loss);
+    if (req.consistency && t < (req.consistencySteps || 3)) {
+      const feed = Object.assign({}, inputs, { x: b.x, y: b.y });
+      feed[fs.cotangent] = [1];
+      const r = await runner.run(fs.graph, fs.lowered, feed);
+      if (!Object.is(r.values[fs.loss][0], loss)) identical = false;
+      for (const n of names) inputs[n] = r.values[fs.outputs[n]];
+    }
+  }
+  if (req.consistency) {
+    const now = trainer.read(names);
+    for (const n of names) {
+      const a = now[n], b = inputs[n];
+      if ((req.consistencySteps || 3) >= req.steps) for (let i = 0; i < a.length; i++) if (!Object.is(a[i], b[i])) { identical = false; break; }
+    }
+  }
+  const params = req.returnParams ? trainer.read(Object.keys(m.params)) : null;
+  if (params) for (const k of Object.keys(params)) params[k] = Array.from(params[k]);
+  trainer.destroy();
+  return { losses, identical, params, launches: fs.lowered.launches.length, unfusedNodes: m.step.graph.nodes.length, info: m.info };
+}
+
 async function main() {
   const argv = process.argv.slice(2);
   const cmd = argv[0];
@@ -235,6 +346,9 @@ async function main() {
     }
     case 'precompile': out = { kernels: precompileGroup(req.group || 'direct', req.arch) }; break;
     case 'gpu-direct': await gpuDirect(outDir(argv)); out = { ok: true }; break;
+    case 'step-graph': stepGraph(req, outDir(argv)); out = { ok: true }; break;
+    case 'gpu-local': await gpuLocal(req, outDir(argv)); out = { ok: true }; break;
+    case 'gpu-train': out = await gpuTrain(req); break;
     case 'gpu-chains': await gpuChains(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-graphs': await gpuGraphs(req, outDir(argv)); out = { ok: true }; break;
     default:
