@@ -97,7 +97,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--configs", default="ceiling,c2,c3,c4")
+    ap.add_argument("--configs", default="ceiling,c2,c3,c4,c1,c5")
     ap.add_argument("--programs", type=int, default=8)
     ap.add_argument("--quick", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -133,6 +133,14 @@ def main() -> None:
         extra["matmul_c4"] = {r["name"]: {"fused_us": r["fused"]["median"], "TFLOPs": (r["tflops"] or {}).get("fused"),
                                           "frac_mfma": ((r["tflops"] or {}).get("fused") or 0) / MFMA_FP32_PEAK,
                                           "speedup_vs_unfused": r["verdict"]["speedup"]} for r in c4["results"]}
+    for key, label in (("c1", "mlp_step_c1"), ("c5", "transformer_step_c5")):
+        if key in cfg:
+            t = cfg[key]
+            extra[label] = {"steps_per_sec": t["stepsPerSec"], "ms_per_step": t["msPerStep"],
+                            "resident_steps_per_sec": t["residentStepsPerSec"], "resident_ms_per_step": t["residentMsPerStep"],
+                            "launches": t["launches"], "fused_us": t["fused"]["median"], "unfused_us": t["unfused"]["median"],
+                            "speedup_vs_unfused": t["verdict"]["speedup"], "matmul_TFLOPs_resident": t["matmulTflopsResident"],
+                            "loss": t["lossLast"], "time_by_kind_us": {k: round(v["us"], 1) for k, v in t["byKind"].items()}}
     if c2 is None:
         raise SystemExit("bench.py: the headline needs config c2")
     dom = c2["dominant"]

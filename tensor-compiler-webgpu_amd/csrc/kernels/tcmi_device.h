@@ -33,7 +33,8 @@ typedef unsigned long long uint64_t;
 #define TCMI_MAX_P 48
 
 // The one kernel argument: operand pointers, the output, an optional
-// workspace, and the u32 parameter block (sizes, strides, per-launch facts).
+// workspace, and a u32 block P that carries the launch's sizes and index maps
+// for inspection (kernels have them as constants of their text and never read P).
 struct TcmiArgs {
   const float* in[TCMI_MAX_IN];
   float* out;
@@ -103,28 +104,11 @@ __device__ __forceinline__ float lane4(const float4& v, int l) {
 //
 // A load through a broadcast or transpose reads its source at an index
 // computed from the output's flat index. The lowering classifies each such
-// load and gives this header the cheapest form:
-//   span:    src = (i / inner) % extent   (any broadcast whose kept axes are one
-//            contiguous run of the output's axes: row vectors, columns, scalars)
-//   general: up to six axes, src = Σ ((i / outStride_d) % extent_d) · srcStride_d
-// Parameters live in TcmiArgs::P at the offset the lowering records.
-
-__device__ __forceinline__ uint32_t idx_span(uint32_t i, uint32_t inner, uint32_t extent) {
-  return (inner == 1 ? i : i / inner) % extent;
-}
-
-// P[base] = rank, P[base+1..] = (extent_d, srcStride_d) pairs from the last axis to the first.
-__device__ __forceinline__ uint32_t idx_general(uint32_t i, const uint32_t* __restrict__ P, uint32_t base) {
-  const uint32_t rank = P[base];
-  uint32_t rem = i, src = 0;
-  for (uint32_t k = 0; k < rank; k++) {
-    const uint32_t extent = P[base + 1 + 2 * k];
-    const uint32_t st = P[base + 2 + 2 * k];
-    src += (rem % extent) * st;
-    rem /= extent;
-  }
-  return src;
-}
+// load and writes the index as an expression of constants (it knows every
+// shape): `(i / inner) % extent` for any broadcast whose kept axes are one
+// contiguous run of the output's axes (row vectors, columns, scalars), and a
+// sum over axes of `((i / outStride_d) % extent_d) · srcStride_d` otherwise.
+// Each map is proved in bounds by the lowering before the kernel is emitted.
 
 // ---- reductions across a workgroup ---------------------------------------------------
 

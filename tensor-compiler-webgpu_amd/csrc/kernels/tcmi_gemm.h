@@ -27,9 +27,17 @@
 
 namespace tcmi {
 
-template <int TM, int TN, bool VEC_A, bool VEC_B, class Epi>
+// Sizes are compile-time constants of the generated kernel (batch, M, K, N, and
+// for SPLIT the number of K chunks and their length, a multiple of 16). SPLIT:
+// blockIdx.z enumerates (batch, chunk) pairs, and each workgroup stores its raw
+// partial tile to the workspace at ((chunk·batch + b)·M + row)·N + col; a
+// second kernel (gemm_splitk_reduce) sums the chunks in order and applies the
+// epilogue.
+template <int TM, int TN, bool VEC_A, bool VEC_B, bool SPLIT, class Epi>
 __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restrict__ a_ptr,
-                                         const float* __restrict__ b_ptr) {
+                                         const float* __restrict__ b_ptr, const uint32_t batch, const uint32_t M,
+                                         const uint32_t K, const uint32_t N, const uint32_t chunks,
+                                         const uint32_t chunkK) {
   constexpr int BM = 2 * TM * 16;
   constexpr int BN = 2 * TN * 16;
   constexpr int BK = 16;
@@ -38,8 +46,10 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
   __shared__ __attribute__((aligned(16))) float As[2][BM * AS];
   __shared__ __attribute__((aligned(16))) float Bs[2][BK * BS];
 
-  const uint32_t M = A.P[1], K = A.P[2], N = A.P[3];
-  const uint32_t bz = blockIdx.z;
+  const uint32_t kz = SPLIT ? blockIdx.z % chunks : 0u;
+  const uint32_t bz = SPLIT ? blockIdx.z / chunks : blockIdx.z;
+  const uint32_t kbeg = SPLIT ? kz * chunkK : 0u;
+  const uint32_t kend = SPLIT ? min(K, kbeg + chunkK) : K;
   const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const float* __restrict__ Ab = a_ptr + (size_t)bz * M * K;
   const float* __restrict__ Bb = b_ptr + (size_t)bz * K * N;
@@ -67,7 +77,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
         const int t = tid + v * 256;
         const uint32_t row = t >> 2, kk = (t & 3) * 4;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (t < BM * BK / 4 && m0 + row < M && k0 + kk < K)
+        if (t < BM * BK / 4 && m0 + row < M && k0 + kk < kend)
           x = *reinterpret_cast<const float4*>(Ab + (size_t)(m0 + row) * K + k0 + kk);
         ra[v] = x;
       }
@@ -77,7 +87,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
         const int t = tid + v * 256;
         const uint32_t row = t / BK, kk = t % BK;
         float x = 0.f;
-        if (t < BM * BK && m0 + row < M && k0 + kk < K) x = Ab[(size_t)(m0 + row) * K + k0 + kk];
+        if (t < BM * BK && m0 + row < M && k0 + kk < kend) x = Ab[(size_t)(m0 + row) * K + k0 + kk];
         sa[v] = x;
       }
     }
@@ -87,7 +97,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
         const int t = tid + v * 256;
         const uint32_t kk = t / (BN / 4), c = (t % (BN / 4)) * 4;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (t < BK * BN / 4 && k0 + kk < K && n0 + c < N)
+        if (t < BK * BN / 4 && k0 + kk < kend && n0 + c < N)
           x = *reinterpret_cast<const float4*>(Bb + (size_t)(k0 + kk) * N + n0 + c);
         rb[v] = x;
       }
@@ -97,7 +107,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
         const int t = tid + v * 256;
         const uint32_t kk = t / BN, c = t % BN;
         float x = 0.f;
-        if (t < BK * BN && k0 + kk < K && n0 + c < N) x = Bb[(size_t)(k0 + kk) * N + n0 + c];
+        if (t < BK * BN && k0 + kk < kend && n0 + c < N) x = Bb[(size_t)(k0 + kk) * N + n0 + c];
         sb[v] = x;
       }
     }
@@ -144,13 +154,13 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-  const uint32_t slices = (K + BK - 1) / BK;
-  load_slice(0);
+  const uint32_t slices = (kend - kbeg + BK - 1) / BK;
+  load_slice(kbeg);
   store_slice(0);
   __syncthreads();
   for (uint32_t ks = 0; ks < slices; ++ks) {
     const int cur = ks & 1;
-    if (ks + 1 < slices) load_slice((ks + 1) * BK);
+    if (ks + 1 < slices) load_slice(kbeg + (ks + 1) * BK);
     // A values of this lane for every row tile: k = 4q .. 4q+3 of the slice.
     float4 av[TM];
 #pragma unroll
@@ -172,6 +182,21 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
     __syncthreads();
   }
 
+  if (SPLIT) {
+    float* __restrict__ part = A.ws + (size_t)(kz * batch + bz) * M * N;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const uint32_t col = n0 + wn * TN * 16 + j * 16 + t16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t row = m0 + wm * TM * 16 + i * 16 + 4 * q + r;
+          if (row < M && col < N) part[(size_t)row * N + col] = acc[i][j][r];
+        }
+      }
+    return;
+  }
   // Epilogue: the fused body on each accumulator element, then the store.
   const Epi epi;
 #pragma unroll
@@ -187,6 +212,32 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
           A.out[o] = epi(A, o, acc[i][j][r]);
         }
       }
+    }
+  }
+}
+
+// The second half of a split-K matmul: out[i] = Epi(A, i, Σ_chunk ws[chunk·total + i]),
+// the chunks summed in order; `total` = batch·M·N. Four outputs per thread when N % 4 == 0.
+template <bool VEC, class Epi>
+__device__ __forceinline__ void gemm_splitk_reduce(const TcmiArgs& A, uint32_t total, uint32_t chunks) {
+  const Epi epi;
+  const uint32_t stride = gridDim.x * blockDim.x;
+  if (VEC) {
+    const uint32_t nv = total >> 2;
+    const f4* __restrict__ ws = reinterpret_cast<const f4*>(A.ws);
+    for (uint32_t v = blockIdx.x * blockDim.x + threadIdx.x; v < nv; v += stride) {
+      f4 acc = ws[v];
+      for (uint32_t c = 1; c < chunks; ++c) acc += ws[(size_t)c * nv + v];
+      f4 o;
+#pragma unroll
+      for (int l = 0; l < 4; ++l) o[l] = epi(A, 4 * v + l, acc[l]);
+      reinterpret_cast<f4*>(A.out)[v] = o;
+    }
+  } else {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+      float acc = A.ws[i];
+      for (uint32_t c = 1; c < chunks; ++c) acc += A.ws[(size_t)c * total + i];
+      A.out[i] = epi(A, i, acc);
     }
   }
 }

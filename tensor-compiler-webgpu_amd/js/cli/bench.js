@@ -227,6 +227,70 @@ function c4(runner, bench, opts) {
   return { config: 'c4', shapes, dominant: dominant(mm), results };
 }
 
+/**
+ * A training step (configs 1 and 5) through the fused trainer: K timed steps of
+ * train(x, y) — batch upload, every launch, device-side parameter feedback, loss
+ * readback — after W warm-up steps, timed by the wall clock (the contract of
+ * FusedTrainer.train, one sync per step); the same K steps with the batch already
+ * in HBM timed by hipEvents; fused against unfused step time; launches per step;
+ * time by kernel kind from every launch timed alone.
+ */
+function trainStep(runner, bench, name, req, opts) {
+  const { modelStep } = require('../src/builders/models');
+  const { fusedStep, HipTrainer } = require('../src/mi355x/trainer');
+  const m = modelStep(req);
+  const fs = fusedStep(m.step);
+  const lu = lowerMI355X(m.step.graph);
+  runner.functions([fs.lowered, lu]);
+  const K = Number(arg('train-steps', opts.quick ? 3 : 10)), W = 2;
+  const batch = m.batch(0);
+  const trainer = new HipTrainer(runner, fs, m.params, m.state);
+  for (let i = 0; i < W; i++) trainer.train(batch.x, batch.y);
+  const t0 = process.hrtime.bigint();
+  let loss = 0;
+  for (let i = 0; i < K; i++) loss = trainer.train(batch.x, batch.y);
+  const wallMs = Number(process.hrtime.bigint() - t0) / 1e6 / K;
+  // Batch resident: launches + feedback only, K steps between two events.
+  const p = trainer.program;
+  runner.a.sync();
+  runner.a.eventRecord(bench.start);
+  for (let i = 0; i < K; i++) {
+    p.run();
+    for (const [from, to, bytes] of trainer.feedback) runner.a.d2d(to, 0, from, 0, bytes);
+  }
+  runner.a.eventRecord(bench.end);
+  const residentMs = runner.a.eventElapsed(bench.start, bench.end) / K;
+  // Unfused step (same graph, no fusion), batch resident.
+  const pu = runner.prepare(m.step.graph, lu);
+  const all = Object.assign({}, m.params, m.state, { x: batch.x, y: batch.y });
+  all[m.step.cotangent] = [1];
+  for (const node of m.step.graph.nodes) if (node.op === 'input') pu.write(node.id, all[node.attrs.name]);
+  const t = bench.time({ fused: p, unfused: pu }, { reps: opts.quick ? 3 : 8, warmup: 2 });
+  // Time by kind (each launch alone).
+  const launches = timeLaunches(runner, bench, p, 3);
+  const byKind = {};
+  for (const l of launches) {
+    const e = byKind[l.kind] || (byKind[l.kind] = { launches: 0, us: 0, bytes: 0, flops: 0 });
+    e.launches++; e.us += l.us; e.bytes += l.bytes; e.flops += l.flops || 0;
+  }
+  for (const k of Object.keys(byKind)) {
+    const e = byKind[k];
+    e.gbs = e.bytes / (e.us * 1e3);
+    if (e.flops) e.tflops = e.flops / (e.us * 1e6);
+  }
+  pu.destroy();
+  trainer.destroy();
+  const flops = fs.lowered.launches.reduce((q, l) => q + (l.flops || 0), 0);
+  return { config: name, info: m.info, steps: K, warmup: W, lossLast: loss,
+    stepsPerSec: 1e3 / wallMs, msPerStep: wallMs, residentMsPerStep: residentMs, residentStepsPerSec: 1e3 / residentMs,
+    launches: { fused: fs.lowered.launches.length, unfused: lu.launches.length },
+    fused: t.stats.fused, unfused: t.stats.unfused, verdict: verdict(t.stats.unfused, t.stats.fused),
+    matmulFlopsPerStep: flops, matmulTflopsResident: flops / (residentMs * 1e9), byKind };
+}
+
+function c1(runner, bench, opts) { return trainStep(runner, bench, 'c1', { model: 'mlp' }, opts); }
+function c5(runner, bench, opts) { return trainStep(runner, bench, 'c5', { model: 'transformer', B: opts.quick ? 8 : 64 }, opts); }
+
 /** The bandwidth ceiling (workloads.js:312-345): copy and pure read of 1 GiB, grid-strided, 1024 x 256 threads. */
 function ceiling(runner, bench) {
   const a = runner.a;
@@ -255,9 +319,9 @@ async function main() {
   const runner = HipRunner.create();
   const bench = new HipBench(runner, { graphs: flag('graphs') });
   const opts = { quick: flag('quick'), reps: arg('reps') ? Number(arg('reps')) : undefined };
-  const which = arg('configs', 'ceiling,c2,c3,c4').split(',');
+  const which = arg('configs', 'ceiling,c2,c3,c4,c1,c5').split(',');
   const out = { device: runner.info(), peaks: { hbmGBs: HBM_PEAK_GBS, fp32MfmaTFLOPs: FP32_MFMA_PEAK_TFLOPS }, configs: {} };
-  const fns = { c2, c3, c4, ceiling };
+  const fns = { c2, c3, c4, c1, c5, ceiling };
   for (const c of which) {
     if (!fns[c]) throw new Error(`unknown config ${c}`);
     const t0 = Date.now();

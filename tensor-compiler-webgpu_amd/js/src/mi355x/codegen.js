@@ -619,12 +619,26 @@ function colreduceKernels(op, outer, n, inner, tuning) {
 
 // ---- matmul with epilogue ----------------------------------------------------------------
 
-/** MFMA tiles per wavefront for a problem: the largest tile that still gives the chip work. */
-function gemmTiles(batch, M, N) {
-  const blocks = (t) => batch * Math.ceil(M / (32 * t)) * Math.ceil(N / (32 * t));
-  if (M >= 128 && N >= 128 && blocks(4) >= 128) return 4;
-  if (M >= 64 && N >= 64 && blocks(2) >= 64) return 2;
-  return M >= 64 && N >= 64 ? 2 : 1;
+/**
+ * Tiling of a matmul: MFMA tiles per wavefront (T: the workgroup owns 32T x 32T of
+ * the output) and K chunks (split-K). The largest tile that still gives every
+ * CU of the 256 a workgroup; when even the smallest leaves CUs idle and K is
+ * long, K is split (chunks of at least 256, at most 16 of them).
+ */
+function gemmTiling(batch, M, N, K, tuning) {
+  const t = tuning || {};
+  const blocks = (T) => batch * Math.ceil(M / (32 * T)) * Math.ceil(N / (32 * T));
+  let T;
+  if (t.tile) T = t.tile;
+  else if (M >= 128 && N >= 128 && blocks(4) >= 256) T = 4;
+  else if (M >= 64 && N >= 64) T = 2;
+  else T = M >= 32 && N >= 32 ? 1 : 1;
+  let chunks = 1;
+  if (t.splitk !== undefined) chunks = t.splitk;
+  else if (blocks(T) < 256 && K >= 512) chunks = Math.max(1, Math.min(Math.ceil(512 / blocks(T)), Math.floor(K / 256), 16));
+  let chunkK = Math.ceil(Math.ceil(K / chunks) / 16) * 16;
+  chunks = Math.ceil(K / chunkK);
+  return { T, chunks, chunkK, blocks: blocks(T) * chunks };
 }
 
 /**
@@ -669,25 +683,42 @@ function gemmKernel(b, output, opts) {
     lines.push(`const float ${t} = tcmi::op_add(${out}, ${ov});`);
     out = t;
   }
-  const T = gemmTiles(batch, M, N);
+  const tl = gemmTiling(batch, M, N, K, o.tuning);
+  const T = tl.T;
+  const split = tl.chunks > 1;
   const vecA = K % 4 === 0, vecB = N % 4 === 0;
-  const text = `#include "tcmi_gemm.h"
-struct __KERNEL___epi {
+  const total = batch * M * N;
+  const epi = `struct __KERNEL___epi {
   __device__ __forceinline__ float operator()(const TcmiArgs& A, uint32_t i, float acc) const {
 ${indent(lines, '    ')}
     return ${out};
   }
 };
-extern "C" __global__ void __launch_bounds__(256) __KERNEL__(const TcmiArgs A) {
-  tcmi::gemm_f32<${T}, ${T}, ${vecA}, ${vecB}, __KERNEL___epi>(A, A.in[${ia}], A.in[${ib}]);
+`;
+  const main = `extern "C" __global__ void __launch_bounds__(256) __KERNEL__(const TcmiArgs A) {
+  tcmi::gemm_f32<${T}, ${T}, ${vecA}, ${vecB}, ${split}, __KERNEL___epi>(A, A.in[${ia}], A.in[${ib}],
+      ${batch}u, ${M}u, ${K}u, ${N}u, ${tl.chunks}u, ${tl.chunkK}u);
 }
 `;
+  const text = `#include "tcmi_gemm.h"\n${epi}${main}`;
   const k = kernelText('mm', text);
   const tile = 32 * T;
-  return { name: k.name, source: k.source, params: Uint32Array.from(params),
-    grid: [Math.ceil(N / tile), Math.ceil(M / tile), batch], block: [256, 1, 1], lds: 0, workspace: 0,
-    flops: 2 * batch * M * N * K };
+  const kernels = [{ name: k.name, source: k.source, grid: [Math.ceil(N / tile), Math.ceil(M / tile), batch * tl.chunks], block: [256, 1, 1], lds: 0 }];
+  let workspace = 0;
+  if (split) {
+    // The reduction kernel shares the epilogue struct of the partial kernel's text.
+    const red = `#include "tcmi_gemm.h"\n${epi}extern "C" __global__ void __launch_bounds__(256) __KERNEL___red(const TcmiArgs A) {
+  tcmi::gemm_splitk_reduce<${vecB}, __KERNEL___epi>(A, ${total}u, ${tl.chunks}u);
+}
+`;
+    const rk = kernelText('mmred', red);
+    const rname = `${rk.name}_red`;
+    kernels.push({ name: rname, source: rk.source, grid: [Math.max(1, Math.min(Math.ceil(total / (vecB ? 4 : 1) / 256), 2048)), 1, 1], block: [256, 1, 1], lds: 0 });
+    workspace = tl.chunks * total * 4;
+  }
+  return { name: k.name, source: k.source, kernels, params: Uint32Array.from(params), grid: kernels[0].grid, block: [256, 1, 1],
+    lds: 0, workspace, flops: 2 * batch * M * N * K, tiling: tl };
 }
 
-module.exports = { elementwiseKernel, rowwiseKernel, colreduceKernels, gemmKernel, classifyGather, gatherStrides, literal, fnv,
+module.exports = { elementwiseKernel, rowwiseKernel, colreduceKernels, gemmKernel, gemmTiling, classifyGather, gatherStrides, literal, fnv,
   Emitter, WG, MAX_P, MAX_IN };

@@ -42,8 +42,8 @@ function algorithmicBytes(graph, node) {
 }
 
 function single(k) {
-  return { kernels: [{ name: k.name, source: k.source, grid: k.grid, block: k.block, lds: k.lds }],
-    params: k.params, workspace: k.workspace || 0, flops: k.flops || 0 };
+  const kernels = k.kernels || [{ name: k.name, source: k.source, grid: k.grid, block: k.block, lds: k.lds }];
+  return { kernels, params: k.params, workspace: k.workspace || 0, flops: k.flops || 0 };
 }
 
 /** Kernels for one node. */
@@ -58,7 +58,7 @@ function lowerNode(graph, node, opts) {
       return Object.assign({ kind: 'fused-elementwise' }, single(cg.elementwiseKernel(b, out, node.shape, Object.assign({ tuning: tuning.ew }, sab))));
     }
     if (kind === 'rowwise') return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(b, out, sab)));
-    if (kind === 'epilogue') return Object.assign({ kind: 'fused-epilogue' }, single(cg.gemmKernel(b, out, sab)));
+    if (kind === 'epilogue') return Object.assign({ kind: 'fused-epilogue' }, single(cg.gemmKernel(b, out, Object.assign({ tuning: tuning.gemm }, sab))));
     throw new Error(`no MI355X kernel for fused kind '${kind}'`);
   }
   if (ELEMENTWISE_OPS.has(node.op) || GATHERS.has(node.op)) {
@@ -80,7 +80,7 @@ function lowerNode(graph, node, opts) {
   }
   if (node.op === 'matmul') {
     const { body, output } = oneOpBody(graph, node);
-    return Object.assign({ kind: 'matmul' }, single(cg.gemmKernel(body, output, {})));
+    return Object.assign({ kind: 'matmul' }, single(cg.gemmKernel(body, output, { tuning: (opts.tuning || {}).gemm })));
   }
   throw new Error(`no MI355X lowering for '${node.op}'`);
 }

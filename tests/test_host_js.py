@@ -150,3 +150,19 @@ def test_c2_programs_are_fully_judgeable(tool):
             bnds = [ref[k][1] for k in v["keep"]]
             assert bounds.unjudgeable_count(vals, bnds) == 0, (p["seed"], kind, p["ops"])
             assert 8 <= len(p["ops"]) <= 16
+
+
+def test_generated_kernels_read_no_parameter_block(golden_cases, tool):
+    """Every size a kernel uses is a constant of its text: no generated source reads the
+    parameter block (a layout mismatch there once sent a split-K matmul out of bounds)."""
+    import re
+    graphs = [{"graph": c["graph"]} for c in golden_cases[:40]]
+    graphs.append({"graph": golden_cases[0]["graph"], "fuse": {"keep": golden_cases[0]["outputs"]}})
+    progs = tool("chain-graphs", {"seeds": [0, 1], "R": 64, "C": 1024})
+    for p in progs:
+        graphs.append({"graph": p["gradient"]["graph"], "fuse": {"keep": p["gradient"]["keep"]}})
+    for req in graphs:
+        out = tool("lower", dict(req, sources=True))
+        for l in out["launches"]:
+            for k in l["kernels"]:
+                assert not re.search(r"\.P\[", k["source"]), k["name"]
