@@ -69,7 +69,7 @@ def check_node_loads() -> None:
           LIB / "tcmi.node"])
 
 
-PRECOMPILE_GROUPS = ["direct", "models"]
+PRECOMPILE_GROUPS = ["direct", "models", "configs"]
 
 
 def precompile(groups=None) -> None:

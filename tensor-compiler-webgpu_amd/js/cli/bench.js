@@ -15,15 +15,13 @@
 // launch timed alone (for per-fusion-group speedups and the dominant kernel's
 // average duration), algorithmic bytes and matmul flops.
 
-const { Graph } = require('../src/ir/graph');
 const { size } = require('../src/ir/shapes');
-const { grad } = require('../src/autodiff');
 const { fuse } = require('../src/fusion/fuse');
 const { lowerMI355X } = require('../src/mi355x/lower');
 const { HipRunner } = require('../src/mi355x/runner');
 const { HipBench, summarize, verdict, median } = require('../src/mi355x/bench');
 const { chainWorkload, chainInputs } = require('../src/builders/chains');
-const { Rng } = require('../src/testing/rng');
+const cfg = require('../src/builders/configs');
 
 const HBM_PEAK_GBS = 8000;
 const FP32_MFMA_PEAK_TFLOPS = 157.3;
@@ -180,47 +178,35 @@ function c2(runner, bench, opts) {
 }
 
 function c3(runner, bench, opts) {
-  const R = opts.quick ? 2048 : 16384, C = 4096;
-  const rng = new Rng(3);
-  const x = rng.normalF32(R * C, 2);
-  const rows = rng.shuffle(Array.from({ length: R }, (_, i) => i)).slice(0, Math.round(R / 100));
-  for (const r of rows) for (let c = 0; c < C; c++) x[r * C + c] += 800;
-  const dy = rng.normalF32(R * C, 1);
+  const R = opts.quick ? 2048 : cfg.C3_SHAPE[0], C = cfg.C3_SHAPE[1];
+  const { x, dy, shifted } = cfg.c3Inputs(R, C);
   const results = [];
   for (const fn of ['softmax', 'logSoftmax']) {
-    const g = new Graph();
-    const xi = g.input('x', [R, C]);
-    const y = g[fn](xi, 1);
+    const g = cfg.c3Graphs(fn, R, C);
     log(`c3 ${fn} forward`);
-    results.push(measureGraph(runner, bench, `c3-${fn}-forward`, g, [y], { x }, { reps: opts.reps }));
-    const G = grad(g, [y], [xi]);
+    results.push(measureGraph(runner, bench, `c3-${fn}-forward`, g.forward.graph, g.forward.keep, { x }, { reps: opts.reps }));
     log(`c3 ${fn} backward`);
-    results.push(measureGraph(runner, bench, `c3-${fn}-backward`, G.graph, [y, G.grads[0]], { x, d0: dy }, { reps: opts.reps }));
+    results.push(measureGraph(runner, bench, `c3-${fn}-backward`, g.gradient.graph, g.gradient.keep, { x, d0: dy }, { reps: opts.reps }));
   }
   const all = [].concat.apply([], results.map((r) => r.launchF));
   const bytes = results.reduce((s, r) => s + r.bytes.fused, 0);
   const us = results.reduce((s, r) => s + r.fused.median, 0);
-  return { config: 'c3', shape: [R, C], shiftedRows: rows.length, gbs: bytes / (us * 1e3), dominant: dominant(all), results };
+  return { config: 'c3', shape: [R, C], shiftedRows: shifted.length, gbs: bytes / (us * 1e3), dominant: dominant(all), results };
 }
 
 function c4(runner, bench, opts) {
-  const shapes = opts.quick || arg('c4-shapes', 'all') === 'small' ? [[512, 512, 512]] : [[512, 512, 512], [4096, 4096, 4096], [8192, 1024, 4096]];
+  const shapes = opts.quick || arg('c4-shapes', 'all') === 'small' ? [cfg.C4_SHAPES[0]] : cfg.C4_SHAPES;
   const results = [];
   for (const [M, K, N] of shapes) {
-    const rng = new Rng(M * 7 + K * 3 + N);
-    const X = rng.normalF32(M * K, 1 / Math.sqrt(K)), Wt = rng.normalF32(K * N, 1 / Math.sqrt(K));
-    const bias = rng.normalF32(N, Math.sqrt(0.1));
-    const dY = rng.normalF32(M * N, 1);
+    const { X, W, bias, dY } = cfg.c4Inputs(M, K, N);
     for (const act of ['relu', 'tanh']) {
-      const g = new Graph();
-      const xi = g.input('X', [M, K]), wi = g.input('W', [K, N]), bi = g.input('bias', [N]);
-      const y = g[act](g.add(g.matmul(xi, wi), bi));
+      const g = cfg.c4Graphs(act, M, K, N);
       log(`c4 ${M}x${K}x${N} ${act} forward`);
-      results.push(measureGraph(runner, bench, `c4-${M}x${K}x${N}-${act}-forward`, g, [y], { X, W: Wt, bias }, { reps: opts.reps || 16 }));
-      const G = grad(g, [y], [xi, wi, bi]);
+      results.push(measureGraph(runner, bench, `c4-${M}x${K}x${N}-${act}-forward`, g.forward.graph, g.forward.keep,
+        { X, W, bias }, { reps: opts.reps || 16 }));
       log(`c4 ${M}x${K}x${N} ${act} backward`);
-      results.push(measureGraph(runner, bench, `c4-${M}x${K}x${N}-${act}-backward`, G.graph, [y].concat(G.grads),
-        { X, W: Wt, bias, d0: dY }, { reps: opts.reps || 8 }));
+      results.push(measureGraph(runner, bench, `c4-${M}x${K}x${N}-${act}-backward`, g.gradient.graph, g.gradient.keep,
+        { X, W, bias, d0: dY }, { reps: opts.reps || 8 }));
     }
   }
   const mm = [].concat.apply([], results.map((r) => r.launchF)).filter((l) => l.flops);

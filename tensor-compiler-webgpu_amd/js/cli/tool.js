@@ -13,9 +13,11 @@
 //   model-fusion     fusion summaries of the reference's transformer forward pass and Adam step
 //   direct-catalogue the direct adversarial cases: names, kinds, patterns, and what fuse() makes of each
 //   transformer-init the reference transformer (golden config) forward + gradient graph and its inputs
+//   config-graphs    request {c3: [{fn, R, C}], c4: [{act, M, K, N}]} -> forward and gradient graphs of configs 3 and 4
 // GPU commands write a bundle (manifest.json + data.f32) under --out:
 //   gpu-direct       every direct case, fused, canary-padded, on the GPU
 //   gpu-graphs       request {graphs: [{name, graph, inputs, keep, unfused?}]} fused (and unfused) on the GPU
+//   gpu-configs      request {c3: [...], c4: [...], unfused} configs 3 and 4, kept outputs as oracle-computable slices
 
 const fs = require('fs');
 const fs_ = fs;
@@ -103,6 +105,21 @@ function precompileGroup(group, arch) {
     for (const r of reqs) n += precompile([fusedStep(modelStep(r).step).lowered], arch);
     return n;
   }
+  if (group === 'configs') {
+    // Configs 2, 3 and 4 as the bench and the GPU tests run them: fused and unfused.
+    const { chainWorkload } = require('../src/builders/chains');
+    const cfg = require('../src/builders/configs');
+    const lists = [];
+    const both = (v) => { lists.push(lowerMI355X(fuse(v.graph, { keep: v.keep }).graph), lowerMI355X(v.graph)); };
+    for (const R of [8192, 64]) {
+      for (let seed = 0; seed < 8; seed++) { const w = chainWorkload(seed, R, 1024); both(w.forward); both(w.gradient); }
+    }
+    for (const fn of ['softmax', 'logSoftmax']) { const g = cfg.c3Graphs(fn, cfg.C3_SHAPE[0], cfg.C3_SHAPE[1]); both(g.forward); both(g.gradient); }
+    for (const [M, K, N] of cfg.C4_SHAPES) {
+      for (const act of ['relu', 'tanh']) { const g = cfg.c4Graphs(act, M, K, N); both(g.forward); both(g.gradient); }
+    }
+    return precompile(lists, arch);
+  }
   throw new Error(`unknown precompile group '${group}'`);
 }
 
@@ -152,6 +169,164 @@ async function gpuGraphs(req, dir) {
       entry.canaryUnfused = ru.canaryIntact;
     }
     bundle.add(entry);
+  }
+  bundle.close({ device: runner.info() });
+}
+
+/** Sorted unique indices in [0, n): the two first and two last, `must`, and random ones up to `count` in all. */
+function sampleIndices(n, must, count, seed) {
+  const { Rng } = require('../src/testing/rng');
+  const set = new Set([0, 1, n - 2, n - 1].filter((i) => i >= 0 && i < n).concat(must || []));
+  const rng = new Rng(seed >>> 0);
+  while (set.size < Math.min(count, n)) set.add(rng.int(0, n - 1));
+  return Array.from(set).sort((a, b) => a - b);
+}
+
+function takeRows(a, C, rows) {
+  const out = new Float32Array(rows.length * C);
+  rows.forEach((r, k) => out.set(a.subarray(r * C, (r + 1) * C), k * C));
+  return out;
+}
+
+function takeCols(a, R, C, cols) {
+  const out = new Float32Array(R * cols.length);
+  for (let r = 0; r < R; r++) for (let k = 0; k < cols.length; k++) out[r * cols.length + k] = a[r * C + cols[k]];
+  return out;
+}
+
+/** The two graphs have the same nodes (op, inputs, attrs other than shapes) in the same order. */
+function sameStructure(a, b) {
+  if (a.nodes.length !== b.nodes.length) return false;
+  return a.nodes.every((n, i) => n.op === b.nodes[i].op && n.inputs.join() === b.nodes[i].inputs.join());
+}
+
+/** Full-tensor properties of one kept output: non-finite counts and fused/unfused bitwise agreement. */
+function tensorProps(f, u) {
+  let nfF = 0, nfU = 0, same = 0;
+  for (let i = 0; i < f.length; i++) if (!Number.isFinite(f[i])) nfF++;
+  if (u) {
+    const fb = new Uint32Array(f.buffer, f.byteOffset, f.length), ub = new Uint32Array(u.buffer, u.byteOffset, u.length);
+    for (let i = 0; i < u.length; i++) { if (!Number.isFinite(u[i])) nfU++; if (fb[i] === ub[i]) same++; }
+  }
+  return { n: f.length, nonfiniteFused: nfF, nonfiniteUnfused: u ? nfU : null, bitwiseSame: u ? same : null };
+}
+
+/** Fused (and unfused) run of `graph` with canaries; the kept outputs of each, by kept position. */
+async function runVariants(runner, graph, keep, inputs, unfused) {
+  const f = fuse(graph, { keep });
+  const lf = lowerMI355X(f.graph);
+  let r = await runner.run(f.graph, lf, inputs, { canary: true });
+  const out = { fused: keep.map((id) => r.values[f.index.get(id)]), canaryFused: r.canaryIntact.every(Boolean),
+    fusedKinds: lf.launches.map((l) => l.kind), unfused: null, canaryUnfused: null, unfusedLaunches: null };
+  r = null;
+  if (unfused) {
+    const lu = lowerMI355X(graph);
+    const ru = await runner.run(graph, lu, inputs, { canary: true });
+    out.unfused = keep.map((id) => ru.values[id]);
+    out.canaryUnfused = ru.canaryIntact.every(Boolean);
+    out.unfusedLaunches = lu.launches.length;
+  }
+  return out;
+}
+
+/**
+ * Configs 3 and 4 on the GPU at the requested sizes, fused and unfused, with
+ * canaries. Every kept output is returned through slices the oracle can compute
+ * exactly: whole rows (config 3; config 4's y and dX) and whole columns
+ * (config 4's y, dW and dbias), each with the graph the same builder makes at
+ * the slice's size and the inputs restricted to it (rows of a row-wise softmax
+ * depend only on their own inputs; row i of X·W on row i of X; column j of
+ * X·W, of dW = Xᵀ·dZ and of dbias on column j of W, bias and dY). Full-tensor
+ * properties over every element are computed here: non-finite counts,
+ * fused/unfused bitwise agreement, the row sums of softmax and the row
+ * log-sum-exp of logSoftmax.
+ * Request: { c3: [{fn, R, C, rows}], c4: [{act, M, K, N, rows, cols}], unfused }.
+ */
+async function gpuConfigs(req, dir) {
+  const cfg = require('../src/builders/configs');
+  const { HipRunner } = require('../src/mi355x/runner');
+  const runner = HipRunner.create();
+  const bundle = new Bundle(dir);
+  for (const c of req.c3 || []) {
+    const { R, C } = c;
+    const ins = cfg.c3Inputs(R, C);
+    const rows = c.rows === 'all' ? Array.from({ length: R }, (_, i) => i) : sampleIndices(R, ins.shifted, ins.shifted.length + c.rows, 31);
+    const full = cfg.c3Graphs(c.fn, R, C), sub = cfg.c3Graphs(c.fn, rows.length, C);
+    for (const kind of ['forward', 'gradient']) {
+      const v = full[kind], s = sub[kind];
+      if (!sameStructure(v.graph, s.graph)) throw new Error('config 3 sub-graph differs in structure');
+      process.stderr.write(`gpu-configs: c3 ${c.fn} ${kind} [${R},${C}], ${rows.length} rows sampled\n`);
+      const inputs = kind === 'forward' ? { x: ins.x } : { x: ins.x, d0: ins.dy };
+      const r = await runVariants(runner, v.graph, v.keep, inputs, req.unfused);
+      const props = v.keep.map((id, k) => tensorProps(r.fused[k], r.unfused && r.unfused[k]));
+      // Row property of y over every row: sum of softmax = 1, log-sum-exp of logSoftmax = 0.
+      const y = r.fused[0];
+      let worstRow = 0;
+      for (let row = 0; row < R; row++) {
+        let acc = 0;
+        for (let col = 0; col < C; col++) acc += c.fn === 'softmax' ? y[row * C + col] : Math.exp(y[row * C + col]);
+        const dev = c.fn === 'softmax' ? Math.abs(acc - 1) : Math.abs(Math.log(acc));
+        if (!(dev <= worstRow)) worstRow = dev;
+      }
+      const subInputs = {};
+      for (const name of Object.keys(inputs)) subInputs[name] = bundle.put(takeRows(inputs[name], C, rows));
+      const compare = v.keep.map((id, k) => ({ id, fused: bundle.put(takeRows(r.fused[k], C, rows)),
+        unfused: r.unfused ? bundle.put(takeRows(r.unfused[k], C, rows)) : null }));
+      bundle.add({ name: `c3-${c.fn}-${kind}-${R}x${C}`, config: 'c3', fn: c.fn, kind, shape: [R, C], rows: rows.length,
+        shifted: ins.shifted.length, sample: { graph: s.graph.toJSON(), inputs: subInputs, compare },
+        props, rowProperty: worstRow, canaryFused: r.canaryFused, canaryUnfused: r.canaryUnfused, fusedKinds: r.fusedKinds,
+        unfusedLaunches: r.unfusedLaunches });
+    }
+  }
+  for (const c of req.c4 || []) {
+    const { M, K, N } = c;
+    const ins = cfg.c4Inputs(M, K, N);
+    const all = c.rows === 'all';
+    const rows = all ? Array.from({ length: M }, (_, i) => i) : sampleIndices(M, [], c.rows, 41);
+    const cols = all ? [] : sampleIndices(N, [], c.cols, 43);
+    const full = cfg.c4Graphs(c.act, M, K, N);
+    const byRows = cfg.c4Graphs(c.act, rows.length, K, N);
+    const byCols = all ? null : cfg.c4Graphs(c.act, M, K, cols.length);
+    for (const kind of ['forward', 'gradient']) {
+      const v = full[kind];
+      if (!sameStructure(v.graph, byRows[kind].graph) || (byCols && !sameStructure(v.graph, byCols[kind].graph))) {
+        throw new Error('config 4 sub-graph differs in structure');
+      }
+      process.stderr.write(`gpu-configs: c4 ${c.act} ${kind} ${M}x${K}x${N}, ${all ? 'all' : rows.length} rows, ${cols.length} cols sampled\n`);
+      const inputs = kind === 'forward' ? { X: ins.X, W: ins.W, bias: ins.bias } : { X: ins.X, W: ins.W, bias: ins.bias, d0: ins.dY };
+      const r = await runVariants(runner, v.graph, v.keep, inputs, req.unfused);
+      const props = v.keep.map((id, k) => tensorProps(r.fused[k], r.unfused && r.unfused[k]));
+      let outOfRange = 0;
+      for (const t of [r.fused[0]].concat(r.unfused ? [r.unfused[0]] : [])) {
+        for (let i = 0; i < t.length; i++) if (c.act === 'relu' ? !(t[i] >= 0) : !(Math.abs(t[i]) <= 1)) outOfRange++;
+      }
+      const samples = [];
+      // Row slice: y and dX (kept as [y, dX, dW, dbias]); everything when all rows are taken.
+      {
+        const shapes = v.keep.map((id) => v.graph.nodes[id].shape);
+        const take = (a, shape) => takeRows(a, shape[shape.length - 1], rows);
+        const sel = all ? v.keep.map((id, k) => k) : (kind === 'forward' ? [0] : [0, 1]);
+        const subInputs = { X: bundle.put(takeRows(ins.X, K, rows)), W: bundle.put(ins.W), bias: bundle.put(ins.bias) };
+        if (kind === 'gradient') subInputs.d0 = bundle.put(takeRows(ins.dY, N, rows));
+        samples.push({ slice: 'rows', n: rows.length, graph: byRows[kind].graph.toJSON(), inputs: subInputs,
+          compare: sel.map((k) => ({ id: v.keep[k], fused: bundle.put(all ? r.fused[k] : take(r.fused[k], shapes[k])),
+            unfused: r.unfused ? bundle.put(all ? r.unfused[k] : take(r.unfused[k], shapes[k])) : null })) });
+      }
+      // Column slice: y, dW and dbias.
+      if (!all) {
+        const shapes = v.keep.map((id) => v.graph.nodes[id].shape);
+        const take = (a, shape) => (shape.length === 1 ? Float32Array.from(cols.map((j) => a[j])) : takeCols(a, shape[0], N, cols));
+        const sel = kind === 'forward' ? [0] : [0, 2, 3];
+        const subInputs = { X: bundle.put(ins.X), W: bundle.put(takeCols(ins.W, K, N, cols)), bias: bundle.put(Float32Array.from(cols.map((j) => ins.bias[j]))) };
+        if (kind === 'gradient') subInputs.d0 = bundle.put(takeCols(ins.dY, M, N, cols));
+        samples.push({ slice: 'cols', n: cols.length, graph: byCols[kind].graph.toJSON(), inputs: subInputs,
+          compare: sel.map((k) => ({ id: v.keep[k], fused: bundle.put(take(r.fused[k], shapes[k])),
+            unfused: r.unfused ? bundle.put(take(r.unfused[k], shapes[k])) : null })) });
+      }
+      bundle.add({ name: `c4-${c.act}-${kind}-${M}x${K}x${N}`, config: 'c4', act: c.act, kind, shape: [M, K, N],
+        samples, props, outOfRange, canaryFused: r.canaryFused, canaryUnfused: r.canaryUnfused, fusedKinds: r.fusedKinds,
+        unfusedLaunches: r.unfusedLaunches });
+    }
   }
   bundle.close({ device: runner.info() });
 }
@@ -344,6 +519,16 @@ async function main() {
       });
       break;
     }
+    case 'config-graphs': {
+      // Forward and gradient graphs of configs 3 and 4 at the requested sizes.
+      const cfg = require('../src/builders/configs');
+      const one = (v) => ({ graph: v.graph.toJSON(), keep: v.keep });
+      out = {
+        c3: (req.c3 || []).map((c) => { const g = cfg.c3Graphs(c.fn, c.R, c.C); return { fn: c.fn, R: c.R, C: c.C, forward: one(g.forward), gradient: one(g.gradient) }; }),
+        c4: (req.c4 || []).map((c) => { const g = cfg.c4Graphs(c.act, c.M, c.K, c.N); return { act: c.act, M: c.M, K: c.K, N: c.N, forward: one(g.forward), gradient: one(g.gradient) }; }),
+      };
+      break;
+    }
     case 'precompile': out = { kernels: precompileGroup(req.group || 'direct', req.arch) }; break;
     case 'gpu-direct': await gpuDirect(outDir(argv)); out = { ok: true }; break;
     case 'step-graph': stepGraph(req, outDir(argv)); out = { ok: true }; break;
@@ -351,6 +536,7 @@ async function main() {
     case 'gpu-train': out = await gpuTrain(req); break;
     case 'gpu-chains': await gpuChains(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-graphs': await gpuGraphs(req, outDir(argv)); out = { ok: true }; break;
+    case 'gpu-configs': await gpuConfigs(req, outDir(argv)); out = { ok: true }; break;
     default:
       throw new Error(`unknown command '${cmd}'`);
   }

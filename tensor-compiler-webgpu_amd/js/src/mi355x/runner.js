@@ -17,8 +17,11 @@
 // function handles made once, then run() issues every launch with one native
 // call (or replays a captured HIP graph) — what the trainer and bench use.
 
+const crypto = require('crypto');
+const fs = require('fs');
+const path = require('path');
 const { size } = require('../ir/shapes');
-const { addon } = require('./addon');
+const { addon, CACHE } = require('./addon');
 const { kernelSources } = require('./lower');
 const { MAX_IN, MAX_P } = require('./codegen');
 
@@ -34,11 +37,51 @@ function translationUnit(sources) {
   return PRELUDE + names.map((n) => sources.get(n)).join('\n');
 }
 
+// The kernel index: for every kernel compiled before (here or at build time),
+// the translation unit it was compiled in, so a later process loads that unit's
+// cached code object instead of compiling the kernel again in a new unit.
+// <cache>/index/<kernel>.ref holds the unit's key, <cache>/index/<key>.tu its text.
+const INDEX = path.join(CACHE, 'index');
+
+function unitKey(text) { return crypto.createHash('sha256').update(text).digest('hex').slice(0, 32); }
+
+function writeAtomic(file, text) {
+  const tmp = `${file}.${process.pid}.tmp`;
+  fs.writeFileSync(tmp, text);
+  fs.renameSync(tmp, file);
+}
+
+/** Record that the kernels `names` are in unit `text`; an index that cannot be written only costs compile time. */
+function indexUnit(names, text) {
+  try {
+    fs.mkdirSync(INDEX, { recursive: true });
+    const key = unitKey(text);
+    const tu = path.join(INDEX, `${key}.tu`);
+    if (!fs.existsSync(tu)) writeAtomic(tu, text);
+    for (const n of names) writeAtomic(path.join(INDEX, `${n}.ref`), key);
+  } catch (e) {
+    // read-only cache: nothing to record
+  }
+}
+
+/** The text of the unit that holds kernel `name`, or null. */
+function indexedUnit(name) {
+  try {
+    const key = fs.readFileSync(path.join(INDEX, `${name}.ref`), 'utf8').trim();
+    const text = fs.readFileSync(path.join(INDEX, `${key}.tu`), 'utf8');
+    return text.includes(` ${name}(const TcmiArgs`) ? { key, text } : null;
+  } catch (e) {
+    return null;
+  }
+}
+
 /** Compile (into the on-disk cache only; no GPU needed) every kernel of `lists` as one module. */
 function precompile(lists, arch) {
   const all = new Map();
   for (const l of lists) for (const [name, src] of kernelSources(l)) all.set(name, src);
-  addon().precompile(translationUnit(all), '', arch || 'gfx950');
+  const text = translationUnit(all);
+  addon().precompile(text, '', arch || 'gfx950');
+  indexUnit(Array.from(all.keys()), text);
   return all.size;
 }
 
@@ -88,9 +131,26 @@ class HipRunner {
     const lists = Array.isArray(lowered) ? lowered : [lowered];
     const missing = new Map();
     for (const l of lists) for (const [name, src] of kernelSources(l)) if (!this.loaded.has(name)) missing.set(name, src);
+    // Kernels compiled before in some unit: load those units (code-object cache hits).
+    const units = new Map();
+    for (const name of missing.keys()) {
+      const u = indexedUnit(name);
+      if (!u) continue;
+      if (!units.has(u.key)) units.set(u.key, { text: u.text, names: [] });
+      units.get(u.key).names.push(name);
+    }
+    for (const u of units.values()) {
+      const module = this.a.compile(u.text, '');
+      for (const name of u.names) {
+        this.loaded.set(name, this.a.function(module, name));
+        missing.delete(name);
+      }
+    }
     if (missing.size) {
-      const module = this.a.compile(translationUnit(missing), '');
+      const text = translationUnit(missing);
+      const module = this.a.compile(text, '');
       for (const name of missing.keys()) this.loaded.set(name, this.a.function(module, name));
+      indexUnit(Array.from(missing.keys()), text);
     }
     return this.loaded;
   }

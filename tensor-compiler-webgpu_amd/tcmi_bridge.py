@@ -14,6 +14,7 @@ import pathlib
 import subprocess
 import sys
 import tempfile
+import threading
 from typing import Any, Dict, Optional
 
 import numpy as np
@@ -28,8 +29,14 @@ class ToolError(RuntimeError):
 
 
 def node_tool(cmd: str, request: Optional[Dict[str, Any]] = None, out: Optional[str] = None,
-              timeout: float = 600, echo_stderr: bool = False) -> Any:
-    """Run `node tool.js cmd [request.json] [--out out]` and return its parsed stdout."""
+              timeout: float = 600, echo_stderr: Optional[bool] = None) -> Any:
+    """Run `node tool.js cmd [request.json] [--out out]` and return its parsed stdout.
+
+    The child's stderr (its progress lines) is forwarded line by line as it comes
+    when `echo_stderr` is true (the default for the GPU commands, `gpu-*`), and
+    its tail is kept for the error raised if the child fails."""
+    if echo_stderr is None:
+        echo_stderr = cmd.startswith("gpu-")
     args = [NODE, str(TOOL), cmd]
     tmp = None
     try:
@@ -40,12 +47,35 @@ def node_tool(cmd: str, request: Optional[Dict[str, Any]] = None, out: Optional[
             args.append(tmp.name)
         if out is not None:
             args += ["--out", str(out)]
-        p = subprocess.run(args, stdout=subprocess.PIPE, stderr=None if echo_stderr else subprocess.PIPE,
-                           timeout=timeout)
+        tail: list = []
+
+        def pump(stream):
+            for raw in iter(stream.readline, b""):
+                line = raw.decode(errors="replace")
+                tail.append(line)
+                del tail[:-200]
+                if echo_stderr:
+                    sys.stderr.write(line)
+                    sys.stderr.flush()
+
+        chunks: list = []
+        p = subprocess.Popen(args, stdout=subprocess.PIPE, stderr=subprocess.PIPE)
+        readers = [threading.Thread(target=pump, args=(p.stderr,), daemon=True),
+                   threading.Thread(target=lambda: chunks.append(p.stdout.read()), daemon=True)]
+        for t in readers:
+            t.start()
+        try:
+            p.wait(timeout=timeout)
+        except subprocess.TimeoutExpired:
+            p.kill()
+            p.wait()
+            raise
+        for t in readers:
+            t.join(timeout=10)
+        stdout = b"".join(chunks)
         if p.returncode != 0:
-            err = "" if echo_stderr else p.stderr.decode(errors="replace")[-4000:]
-            raise ToolError(f"node tool.js {cmd} exited {p.returncode}:\n{err}")
-        return json.loads(p.stdout.decode()) if p.stdout else None
+            raise ToolError(f"node tool.js {cmd} exited {p.returncode}:\n{''.join(tail)[-4000:]}")
+        return json.loads(stdout.decode()) if stdout else None
     finally:
         if tmp is not None:
             os.unlink(tmp.name)
