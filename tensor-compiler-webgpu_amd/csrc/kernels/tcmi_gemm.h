@@ -1,9 +1,21 @@
 // fp32 matmul on CDNA4 matrix cores with a fused epilogue.
 //
-// C[b] = A[b] · B[b] (A: [M, K], B: [K, N], row-major, batch stride M·K and
-// K·N), then out[i] = Epi(A, i, C[b][row][col]) with i = (b·M + row)·N + col:
-// the epilogue is the fused body of a matmul-epilogue group (bias broadcast,
-// activation, residual), applied while the accumulator is still in registers.
+// C[b] = A[b] · B[b] (A: [M, K], B: [K, N]), then out[i] = Epi(A, i, C[b][row][col])
+// with i = (b·M + row)·N + col: the epilogue is the fused body of a
+// matmul-epilogue group (bias broadcast, activation, residual), applied while
+// the accumulator is still in registers.
+//
+// Operands are strided views: element (b, r, c) of an operand is at
+// V::batch(b) + r·V::SR + c·V::SC of its buffer, so a transposed operand
+// (autodiff's transpose(W) and transpose(X), attention's transposed keys, a
+// head split) is read in place instead of being materialised first. The load
+// path per operand (MODE) follows its layout:
+//   MODE_C  c contiguous (SC = 1): 128-bit loads along c (the row-major case)
+//   MODE_R  r contiguous (SR = 1): 128-bit loads along r (the transposed case),
+//           scattered into the LDS tile as four 32-bit writes
+//   MODE_S  anything else: one 32-bit load per element
+// (for A, r is the output row and c the K index; for B, r is K and c the
+// output column).
 //
 // Tiling: a workgroup of 256 threads (4 wavefronts in a 2 x 2 grid) owns a
 // BM x BN tile of C; each wavefront owns (TM·16) x (TN·16) of it as TM x TN
@@ -19,7 +31,8 @@
 // lane's four A values of a slice are contiguous in LDS (one ds_read_b128);
 // both operands use the same k for the same (q, s), so the product is exact
 // in what it sums, in an order the float32 budget already covers (any order
-// of K terms, gamma(K)).
+// of K terms, gamma(K)). The order does not depend on the operands' layouts:
+// a view and a materialised copy of the same operand give the same bits.
 
 #pragma once
 
@@ -27,13 +40,24 @@
 
 namespace tcmi {
 
+enum { MODE_C = 0, MODE_R = 1, MODE_S = 2 };
+
+// The contiguous row-major view of a [batch, R, C] operand.
+template <uint32_t R, uint32_t C>
+struct DenseView {
+  static constexpr size_t SR = C, SC = 1;
+  static __device__ __forceinline__ size_t batch(uint32_t b) { return (size_t)b * R * C; }
+};
+
 // Sizes are compile-time constants of the generated kernel (batch, M, K, N, and
 // for SPLIT the number of K chunks and their length, a multiple of 16). SPLIT:
 // blockIdx.z enumerates (batch, chunk) pairs, and each workgroup stores its raw
 // partial tile to the workspace at ((chunk·batch + b)·M + row)·N + col; a
 // second kernel (gemm_splitk_reduce) sums the chunks in order and applies the
-// epilogue.
-template <int TM, int TN, bool VEC_A, bool VEC_B, bool SPLIT, class Epi>
+// epilogue. MODE_C needs C % 4 == 0 and MODE_R needs R % 4 == 0 (R, C: the
+// operand's extents), and both need every other stride a multiple of 4, so a
+// 128-bit load is aligned and either wholly inside the operand or wholly out.
+template <int TM, int TN, int AMODE, int BMODE, bool SPLIT, class AV, class BV, class Epi>
 __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restrict__ a_ptr,
                                          const float* __restrict__ b_ptr, const uint32_t batch, const uint32_t M,
                                          const uint32_t K, const uint32_t N, const uint32_t chunks,
@@ -51,8 +75,8 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
   const uint32_t kbeg = SPLIT ? kz * chunkK : 0u;
   const uint32_t kend = SPLIT ? min(K, kbeg + chunkK) : K;
   const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const float* __restrict__ Ab = a_ptr + (size_t)bz * M * K;
-  const float* __restrict__ Bb = b_ptr + (size_t)bz * K * N;
+  const float* __restrict__ Ab = a_ptr + AV::batch(bz);
+  const float* __restrict__ Bb = b_ptr + BV::batch(bz);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -65,20 +89,31 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
   constexpr int B_VEC = (BK * BN / 4 + 255) / 256;
   constexpr int A_SC = (BM * BK + 255) / 256;        // scalar loads per thread
   constexpr int B_SC = (BK * BN + 255) / 256;
-  float4 ra[VEC_A ? A_VEC : 1];
-  float4 rb[VEC_B ? B_VEC : 1];
-  float sa[VEC_A ? 1 : A_SC];
-  float sb[VEC_B ? 1 : B_SC];
+  constexpr bool VA = AMODE != MODE_S, VB = BMODE != MODE_S;
+  float4 ra[VA ? A_VEC : 1];
+  float4 rb[VB ? B_VEC : 1];
+  float sa[VA ? 1 : A_SC];
+  float sb[VB ? 1 : B_SC];
 
   auto load_slice = [&](uint32_t k0) {
-    if (VEC_A) {
+    if (AMODE == MODE_C) {
 #pragma unroll
       for (int v = 0; v < A_VEC; ++v) {
         const int t = tid + v * 256;
         const uint32_t row = t >> 2, kk = (t & 3) * 4;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t < BM * BK / 4 && m0 + row < M && k0 + kk < kend)
-          x = *reinterpret_cast<const float4*>(Ab + (size_t)(m0 + row) * K + k0 + kk);
+          x = *reinterpret_cast<const float4*>(Ab + (size_t)(m0 + row) * AV::SR + k0 + kk);
+        ra[v] = x;
+      }
+    } else if (AMODE == MODE_R) {
+#pragma unroll
+      for (int v = 0; v < A_VEC; ++v) {
+        const int t = tid + v * 256;
+        const uint32_t kk = t / (BM / 4), row = (t % (BM / 4)) * 4;
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (t < BM * BK / 4 && m0 + row < M && k0 + kk < kend)
+          x = *reinterpret_cast<const float4*>(Ab + (size_t)(k0 + kk) * AV::SC + m0 + row);
         ra[v] = x;
       }
     } else {
@@ -87,18 +122,28 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
         const int t = tid + v * 256;
         const uint32_t row = t / BK, kk = t % BK;
         float x = 0.f;
-        if (t < BM * BK && m0 + row < M && k0 + kk < kend) x = Ab[(size_t)(m0 + row) * K + k0 + kk];
+        if (t < BM * BK && m0 + row < M && k0 + kk < kend) x = Ab[(size_t)(m0 + row) * AV::SR + (size_t)(k0 + kk) * AV::SC];
         sa[v] = x;
       }
     }
-    if (VEC_B) {
+    if (BMODE == MODE_C) {
 #pragma unroll
       for (int v = 0; v < B_VEC; ++v) {
         const int t = tid + v * 256;
         const uint32_t kk = t / (BN / 4), c = (t % (BN / 4)) * 4;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t < BK * BN / 4 && k0 + kk < kend && n0 + c < N)
-          x = *reinterpret_cast<const float4*>(Bb + (size_t)(k0 + kk) * N + n0 + c);
+          x = *reinterpret_cast<const float4*>(Bb + (size_t)(k0 + kk) * BV::SR + n0 + c);
+        rb[v] = x;
+      }
+    } else if (BMODE == MODE_R) {
+#pragma unroll
+      for (int v = 0; v < B_VEC; ++v) {
+        const int t = tid + v * 256;
+        const uint32_t c = t / (BK / 4), kk = (t % (BK / 4)) * 4;
+        float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (t < BK * BN / 4 && k0 + kk < kend && n0 + c < N)
+          x = *reinterpret_cast<const float4*>(Bb + (size_t)(n0 + c) * BV::SC + k0 + kk);
         rb[v] = x;
       }
     } else {
@@ -107,20 +152,32 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
         const int t = tid + v * 256;
         const uint32_t kk = t / BN, c = t % BN;
         float x = 0.f;
-        if (t < BK * BN && k0 + kk < kend && n0 + c < N) x = Bb[(size_t)(k0 + kk) * N + n0 + c];
+        if (t < BK * BN && k0 + kk < kend && n0 + c < N) x = Bb[(size_t)(k0 + kk) * BV::SR + (size_t)(n0 + c) * BV::SC];
         sb[v] = x;
       }
     }
   };
 
   auto store_slice = [&](int buf) {
-    if (VEC_A) {
+    if (AMODE == MODE_C) {
 #pragma unroll
       for (int v = 0; v < A_VEC; ++v) {
         const int t = tid + v * 256;
         if (t < BM * BK / 4) {
           const int row = t >> 2, kk = (t & 3) * 4;
           *reinterpret_cast<float4*>(&As[buf][row * AS + kk]) = ra[v];
+        }
+      }
+    } else if (AMODE == MODE_R) {
+#pragma unroll
+      for (int v = 0; v < A_VEC; ++v) {
+        const int t = tid + v * 256;
+        if (t < BM * BK / 4) {
+          const int kk = t / (BM / 4), row = (t % (BM / 4)) * 4;
+          As[buf][(row + 0) * AS + kk] = ra[v].x;
+          As[buf][(row + 1) * AS + kk] = ra[v].y;
+          As[buf][(row + 2) * AS + kk] = ra[v].z;
+          As[buf][(row + 3) * AS + kk] = ra[v].w;
         }
       }
     } else {
@@ -130,13 +187,25 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
         if (t < BM * BK) As[buf][(t / BK) * AS + (t % BK)] = sa[v];
       }
     }
-    if (VEC_B) {
+    if (BMODE == MODE_C) {
 #pragma unroll
       for (int v = 0; v < B_VEC; ++v) {
         const int t = tid + v * 256;
         if (t < BK * BN / 4) {
           const int kk = t / (BN / 4), c = (t % (BN / 4)) * 4;
           *reinterpret_cast<float4*>(&Bs[buf][kk * BS + c]) = rb[v];
+        }
+      }
+    } else if (BMODE == MODE_R) {
+#pragma unroll
+      for (int v = 0; v < B_VEC; ++v) {
+        const int t = tid + v * 256;
+        if (t < BK * BN / 4) {
+          const int c = t / (BK / 4), kk = (t % (BK / 4)) * 4;
+          Bs[buf][(kk + 0) * BS + c] = rb[v].x;
+          Bs[buf][(kk + 1) * BS + c] = rb[v].y;
+          Bs[buf][(kk + 2) * BS + c] = rb[v].z;
+          Bs[buf][(kk + 3) * BS + c] = rb[v].w;
         }
       }
     } else {

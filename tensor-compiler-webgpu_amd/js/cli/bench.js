@@ -59,9 +59,11 @@ function timeLaunches(runner, bench, program, reps) {
  */
 function measureGraph(runner, bench, name, graph, keep, inputs, opts) {
   const o = opts || {};
+  // Both variants in the perf lowering (reshapes share buffers, transposes read in
+  // place by their matmuls): what the trainer runs; outputs equal the plain lowering's.
   const f = fuse(graph, { keep });
-  const lf = lowerMI355X(f.graph);
-  const lu = lowerMI355X(graph);
+  const lf = lowerMI355X(f.graph, { perf: true, keep: keep.map((id) => f.index.get(id)) });
+  const lu = lowerMI355X(graph, { perf: true, keep });
   runner.functions([lf, lu]);
   const pf = prepared(runner, f.graph, lf, inputs);
   const pu = prepared(runner, graph, lu, inputs);
@@ -142,7 +144,7 @@ function c2(runner, bench, opts) {
       if (stepOnly) {
         // Profiling mode: only the programs of the step, no per-variant timing.
         const f = fuse(v.graph, { keep: v.keep });
-        const lf = lowerMI355X(f.graph);
+        const lf = lowerMI355X(f.graph, { perf: true, keep: v.keep.map((id) => f.index.get(id)) });
         runner.functions(lf);
         programs.push(prepared(runner, f.graph, lf, inputs));
         results.push({ name: `c2-p${s}-${kind}`, bytes: { fused: lf.launches.reduce((q, l) => q + l.bytes, 0) }, launchF: [] });
@@ -226,7 +228,8 @@ function trainStep(runner, bench, name, req, opts) {
   const { fusedStep, HipTrainer } = require('../src/mi355x/trainer');
   const m = modelStep(req);
   const fs = fusedStep(m.step);
-  const lu = lowerMI355X(m.step.graph);
+  // The unfused step in the same perf lowering the fused trainer runs.
+  const lu = lowerMI355X(m.step.graph, { perf: true, keep: [m.step.loss, m.step.logits].concat(Object.values(m.step.outputs)) });
   runner.functions([fs.lowered, lu]);
   const K = Number(arg('train-steps', opts.quick ? 3 : 10)), W = 2;
   const batch = m.batch(0);

@@ -102,7 +102,7 @@ function precompileGroup(group, arch) {
     const { fusedStep } = require('../src/mi355x/trainer');
     const reqs = [{ model: 'mlp' }, { model: 'transformer', B: 1 }, { model: 'transformer', B: 64 }, { model: 'transformer-ref' }];
     let n = 0;
-    for (const r of reqs) n += precompile([fusedStep(modelStep(r).step).lowered], arch);
+    for (const r of reqs) { const fs = fusedStep(modelStep(r).step); n += precompile([fs.lowered], arch) + precompile([fs.checked], arch); }
     return n;
   }
   if (group === 'configs') {
@@ -110,7 +110,11 @@ function precompileGroup(group, arch) {
     const { chainWorkload } = require('../src/builders/chains');
     const cfg = require('../src/builders/configs');
     const lists = [];
-    const both = (v) => { lists.push(lowerMI355X(fuse(v.graph, { keep: v.keep }).graph), lowerMI355X(v.graph)); };
+    const both = (v) => {
+      const f = fuse(v.graph, { keep: v.keep });
+      const fk = v.keep.map((id) => f.index.get(id));
+      lists.push(lowerMI355X(f.graph), lowerMI355X(v.graph), lowerMI355X(f.graph, { perf: true, keep: fk }), lowerMI355X(v.graph, { perf: true, keep: v.keep }));
+    };
     for (const R of [8192, 64]) {
       for (let seed = 0; seed < 8; seed++) { const w = chainWorkload(seed, R, 1024); both(w.forward); both(w.gradient); }
     }
@@ -219,6 +223,18 @@ async function runVariants(runner, graph, keep, inputs, unfused) {
   const out = { fused: keep.map((id) => r.values[f.index.get(id)]), canaryFused: r.canaryIntact.every(Boolean),
     fusedKinds: lf.launches.map((l) => l.kind), unfused: null, canaryUnfused: null, unfusedLaunches: null };
   r = null;
+  // The perf lowering of the fused graph (transposes read in place, reshapes sharing
+  // buffers): its kept outputs must equal the plain lowering's bit for bit.
+  const lp = lowerMI355X(f.graph, { perf: true, keep: keep.map((id) => f.index.get(id)) });
+  const rp = await runner.run(f.graph, lp, inputs, { canary: true });
+  let perfSame = 0, perfTotal = 0;
+  keep.forEach((id, k) => {
+    const a = new Uint32Array(rp.values[f.index.get(id)].buffer), b = new Uint32Array(out.fused[k].buffer);
+    perfTotal += a.length;
+    for (let i = 0; i < a.length; i++) if (a[i] === b[i]) perfSame++;
+  });
+  Object.assign(out, { perfSame, perfTotal, perfLaunches: lp.launches.length, perfFolded: lp.folded.length,
+    canaryPerf: rp.canaryIntact.every(Boolean) });
   if (unfused) {
     const lu = lowerMI355X(graph);
     const ru = await runner.run(graph, lu, inputs, { canary: true });
@@ -275,7 +291,7 @@ async function gpuConfigs(req, dir) {
       bundle.add({ name: `c3-${c.fn}-${kind}-${R}x${C}`, config: 'c3', fn: c.fn, kind, shape: [R, C], rows: rows.length,
         shifted: ins.shifted.length, sample: { graph: s.graph.toJSON(), inputs: subInputs, compare },
         props, rowProperty: worstRow, canaryFused: r.canaryFused, canaryUnfused: r.canaryUnfused, fusedKinds: r.fusedKinds,
-        unfusedLaunches: r.unfusedLaunches });
+        unfusedLaunches: r.unfusedLaunches, perf: { same: r.perfSame, total: r.perfTotal, launches: r.perfLaunches, folded: r.perfFolded, canary: r.canaryPerf } });
     }
   }
   for (const c of req.c4 || []) {
@@ -325,7 +341,7 @@ async function gpuConfigs(req, dir) {
       }
       bundle.add({ name: `c4-${c.act}-${kind}-${M}x${K}x${N}`, config: 'c4', act: c.act, kind, shape: [M, K, N],
         samples, props, outOfRange, canaryFused: r.canaryFused, canaryUnfused: r.canaryUnfused, fusedKinds: r.fusedKinds,
-        unfusedLaunches: r.unfusedLaunches });
+        unfusedLaunches: r.unfusedLaunches, perf: { same: r.perfSame, total: r.perfTotal, launches: r.perfLaunches, folded: r.perfFolded, canary: r.canaryPerf } });
     }
   }
   bundle.close({ device: runner.info() });
@@ -412,12 +428,20 @@ async function gpuLocal(req, dir) {
   }
   if (off !== data.length) throw new Error(`values file holds ${data.length} floats, the fused graph needs ${off}`);
   const runner = HipRunner.create();
-  const out = await runner.runLocal(fs.graph, fs.lowered, values, { canary: true });
   const bundle = new Bundle(dir);
-  const gpu = {};
-  for (const l of fs.lowered.launches) gpu[l.node] = bundle.put(out[l.node]);
-  bundle.add({ name: req.model, gpu, canaryIntact: fs.lowered.launches.every((l) => out.canaryIntact[l.node]),
-    launches: fs.lowered.launches.length });
+  // The checked lowering (every node launched) and the trainer's perf lowering.
+  const entry = { name: req.model };
+  for (const [key, lowered] of [['gpu', fs.checked], ['gpuPerf', fs.lowered]]) {
+    const out = await runner.runLocal(fs.graph, lowered, values, { canary: true });
+    entry[key] = {};
+    for (const l of lowered.launches) entry[key][l.node] = bundle.put(out[l.node]);
+    entry[`${key}Canary`] = lowered.launches.every((l) => out.canaryIntact[l.node]);
+    entry[`${key}Launches`] = lowered.launches.length;
+  }
+  entry.canaryIntact = entry.gpuCanary && entry.gpuPerfCanary;
+  entry.aliases = fs.lowered.aliases;
+  entry.folded = fs.lowered.folded;
+  bundle.add(entry);
   bundle.close({ device: runner.info() });
 }
 
@@ -451,7 +475,8 @@ async function gpuTrain(req) {
     if (req.consistency && t < (req.consistencySteps || 3)) {
       const feed = Object.assign({}, inputs, { x: b.x, y: b.y });
       feed[fs.cotangent] = [1];
-      const r = await runner.run(fs.graph, fs.lowered, feed);
+      // The checked path: the plain lowering (one launch per node), against the trainer's perf lowering.
+      const r = await runner.run(fs.graph, fs.checked, feed);
       if (!Object.is(r.values[fs.loss][0], loss)) identical = false;
       for (const n of names) inputs[n] = r.values[fs.outputs[n]];
     }
@@ -466,7 +491,8 @@ async function gpuTrain(req) {
   const params = req.returnParams ? trainer.read(Object.keys(m.params)) : null;
   if (params) for (const k of Object.keys(params)) params[k] = Array.from(params[k]);
   trainer.destroy();
-  return { losses, identical, params, launches: fs.lowered.launches.length, unfusedNodes: m.step.graph.nodes.length, info: m.info };
+  return { losses, identical, params, launches: fs.lowered.launches.length, checkedLaunches: fs.checked.launches.length,
+    folded: fs.lowered.folded.length, aliases: fs.lowered.aliases.length, unfusedNodes: m.step.graph.nodes.length, info: m.info };
 }
 
 async function main() {
@@ -527,6 +553,24 @@ async function main() {
         c3: (req.c3 || []).map((c) => { const g = cfg.c3Graphs(c.fn, c.R, c.C); return { fn: c.fn, R: c.R, C: c.C, forward: one(g.forward), gradient: one(g.gradient) }; }),
         c4: (req.c4 || []).map((c) => { const g = cfg.c4Graphs(c.act, c.M, c.K, c.N); return { act: c.act, M: c.M, K: c.K, N: c.N, forward: one(g.forward), gradient: one(g.gradient) }; }),
       };
+      break;
+    }
+    case 'perf-lower': {
+      // The perf lowering of a model step or of a graph: launches, aliases, folded nodes, operand views.
+      let g, keep;
+      if (req.model) {
+        const { modelStep } = require('../src/builders/models');
+        const { fusedStep } = require('../src/mi355x/trainer');
+        const fs = fusedStep(modelStep(req).step);
+        g = fs.graph;
+        keep = [fs.loss, fs.logits].concat(Object.values(fs.outputs));
+      } else {
+        g = Graph.fromJSON(req.graph);
+        keep = req.keep || [];
+      }
+      const l = lowerMI355X(g, { perf: true, keep });
+      out = { graph: g.toJSON(), keep, aliases: l.aliases, folded: l.folded,
+        launches: l.launches.map((x) => ({ node: x.node, kind: x.kind, inputs: x.inputs, views: x.views || null, modes: x.kernels[0].source.match(/gemm_f32<\d+, \d+, (\d), (\d)/) ? x.kernels[0].source.match(/gemm_f32<\d+, \d+, (\d), (\d)/).slice(1).map(Number) : null })) };
       break;
     }
     case 'precompile': out = { kernels: precompileGroup(req.group || 'direct', req.arch) }; break;

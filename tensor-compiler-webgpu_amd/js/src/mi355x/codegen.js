@@ -642,9 +642,46 @@ function gemmTiling(batch, M, N, K, tuning) {
 }
 
 /**
+ * The view struct of a matmul operand (tcmi_gemm.h): element (b, r, c) at
+ * batch(b) + r·SR + c·SC of its buffer, and the load mode its layout allows.
+ * `view` = { batch: [[extent, stride], ...], sr, sc } (null: dense row-major
+ * [batch, R, C]); R, C the operand's extents.
+ */
+function operandView(name, view, batchDims, R, C) {
+  const v = view || { batch: batchDims.map((e, d) => [e, R * C * size(batchDims.slice(d + 1))]), sr: C, sc: 1 };
+  const strides = v.batch.map((x) => x[1]);
+  const others4 = (x) => strides.every((s) => s % 4 === 0) && x % 4 === 0;
+  let mode = 2;
+  if (v.sc === 1 && C % 4 === 0 && others4(v.sr)) mode = 0;
+  else if (v.sr === 1 && R % 4 === 0 && others4(v.sc)) mode = 1;
+  const terms = [];
+  let inner = 1;
+  for (let d = v.batch.length - 1; d >= 0; d--) {
+    const [e, st] = v.batch[d];
+    if (e > 1 && st !== 0) {
+      const idx = inner === 1 ? 'b' : `(b / ${inner}u)`;
+      terms.push(`(size_t)(${d === 0 ? idx : `${idx} % ${e}u`}) * ${st}u`);
+    }
+    inner *= e;
+  }
+  const text = `struct ${name} {
+  static constexpr size_t SR = ${v.sr}, SC = ${v.sc};
+  static __device__ __forceinline__ size_t batch(uint32_t b) { return ${terms.length ? terms.join(' + ') : '0'}; }
+};
+`;
+  // One past the largest element offset the kernel can address.
+  const limit = 1 + v.batch.reduce((t, [e, st]) => t + (e - 1) * st, 0) + (R - 1) * v.sr + (C - 1) * v.sc;
+  return { text, mode, limit };
+}
+
+/**
  * A matmul-epilogue body (or a plain matmul): the body's matmul node is the
  * root, every other body op runs on its accumulator at the store. Epilogue
  * operands are read at the output's flat index (or through their gathers).
+ * `views` ({ a, b }, optional): the matmul operands are read in place through
+ * these strided views of other buffers (a transposed operand not materialised);
+ * `sizes` ({ a, b }) are those buffers' element counts, against which every
+ * view is proved in bounds.
  */
 function gemmKernel(b, output, opts) {
   const o = opts || {};
@@ -653,10 +690,12 @@ function gemmKernel(b, output, opts) {
   const ia = Number(b.nodes[root.inputs[0]].attrs.name.slice(1));
   const ib = Number(b.nodes[root.inputs[1]].attrs.name.slice(1));
   const as = b.nodes[root.inputs[0]].shape, bs = b.nodes[root.inputs[1]].shape;
-  const batch = size(as.slice(0, -2)), M = as[as.length - 2], K = as[as.length - 1], N = bs[bs.length - 1];
+  const batchDims = as.slice(0, -2);
+  const batch = size(batchDims), M = as[as.length - 2], K = as[as.length - 1], N = bs[bs.length - 1];
   if (batch * M * N >= 2 ** 31 || batch * M * K >= 2 ** 31 || batch * K * N >= 2 ** 31) {
     throw new Error('matmul exceeds the 32-bit index space');
   }
+  const views = o.views || {};
   const params = [batch, M, K, N];
   // Sabotage (the reference's 'epilogue-before-bias', codegen-fused.js:228-243): the
   // activation sees the bare sum and the bias is added after it.
@@ -686,7 +725,11 @@ function gemmKernel(b, output, opts) {
   const tl = gemmTiling(batch, M, N, K, o.tuning);
   const T = tl.T;
   const split = tl.chunks > 1;
-  const vecA = K % 4 === 0, vecB = N % 4 === 0;
+  const av = operandView('__KERNEL___av', views.a, batchDims, M, K);
+  const bv = operandView('__KERNEL___bv', views.b, bs.slice(0, -2), K, N);
+  const sizes = o.sizes || {};
+  const need = { a: sizes.a !== undefined ? sizes.a : batch * M * K, b: sizes.b !== undefined ? sizes.b : batch * K * N };
+  if (av.limit > need.a || bv.limit > need.b) throw new Error(`matmul operand view out of bounds (${av.limit}/${need.a}, ${bv.limit}/${need.b})`);
   const total = batch * M * N;
   const epi = `struct __KERNEL___epi {
   __device__ __forceinline__ float operator()(const TcmiArgs& A, uint32_t i, float acc) const {
@@ -696,28 +739,29 @@ ${indent(lines, '    ')}
 };
 `;
   const main = `extern "C" __global__ void __launch_bounds__(256) __KERNEL__(const TcmiArgs A) {
-  tcmi::gemm_f32<${T}, ${T}, ${vecA}, ${vecB}, ${split}, __KERNEL___epi>(A, A.in[${ia}], A.in[${ib}],
+  tcmi::gemm_f32<${T}, ${T}, ${av.mode}, ${bv.mode}, ${split}, __KERNEL___av, __KERNEL___bv, __KERNEL___epi>(A, A.in[${ia}], A.in[${ib}],
       ${batch}u, ${M}u, ${K}u, ${N}u, ${tl.chunks}u, ${tl.chunkK}u);
 }
 `;
-  const text = `#include "tcmi_gemm.h"\n${epi}${main}`;
+  const text = `#include "tcmi_gemm.h"\n${av.text}${bv.text}${epi}${main}`;
   const k = kernelText('mm', text);
   const tile = 32 * T;
   const kernels = [{ name: k.name, source: k.source, grid: [Math.ceil(N / tile), Math.ceil(M / tile), batch * tl.chunks], block: [256, 1, 1], lds: 0 }];
   let workspace = 0;
   if (split) {
     // The reduction kernel shares the epilogue struct of the partial kernel's text.
+    const vecOut = N % 4 === 0;
     const red = `#include "tcmi_gemm.h"\n${epi}extern "C" __global__ void __launch_bounds__(256) __KERNEL___red(const TcmiArgs A) {
-  tcmi::gemm_splitk_reduce<${vecB}, __KERNEL___epi>(A, ${total}u, ${tl.chunks}u);
+  tcmi::gemm_splitk_reduce<${vecOut}, __KERNEL___epi>(A, ${total}u, ${tl.chunks}u);
 }
 `;
     const rk = kernelText('mmred', red);
     const rname = `${rk.name}_red`;
-    kernels.push({ name: rname, source: rk.source, grid: [Math.max(1, Math.min(Math.ceil(total / (vecB ? 4 : 1) / 256), 2048)), 1, 1], block: [256, 1, 1], lds: 0 });
+    kernels.push({ name: rname, source: rk.source, grid: [Math.max(1, Math.min(Math.ceil(total / (vecOut ? 4 : 1) / 256), 2048)), 1, 1], block: [256, 1, 1], lds: 0 });
     workspace = tl.chunks * total * 4;
   }
   return { name: k.name, source: k.source, kernels, params: Uint32Array.from(params), grid: kernels[0].grid, block: [256, 1, 1],
-    lds: 0, workspace, flops: 2 * batch * M * N * K, tiling: tl };
+    lds: 0, workspace, flops: 2 * batch * M * N * K, tiling: tl, modes: [av.mode, bv.mode] };
 }
 
 module.exports = { elementwiseKernel, rowwiseKernel, colreduceKernels, gemmKernel, gemmTiling, classifyGather, gatherStrides, literal, fnv,

@@ -17,6 +17,17 @@
 // Every record also carries `bytes` — each unique operand read once at its own
 // size plus the output, the reference's byte count (workloads.js:171-172) —
 // and `flops` (2·batch·M·N·K) for matmuls.
+//
+// With `perf` (the trainer's and the bench's lowering; results are bit for bit
+// those of the plain lowering, only fewer bytes move):
+//   - a reshape launches nothing: its node shares its input's buffer (a
+//     row-major reshape is the same bytes), listed in `aliases`;
+//   - a transpose whose every consumer is a matmul operand (directly, through
+//     further such transposes, or as an epilogue group's operand that only its
+//     matmul reads) launches nothing either (`folded`): the matmuls read its
+//     source in place through a strided view (tcmi_gemm.h). The records of
+//     those matmuls name the source as their input.
+// Nodes in `keep` are never folded, so their values stay readable.
 
 const { Graph } = require('../ir/graph');
 const { size } = require('../ir/shapes');
@@ -47,7 +58,7 @@ function single(k) {
 }
 
 /** Kernels for one node. */
-function lowerNode(graph, node, opts) {
+function lowerNode(graph, node, opts, mmViews) {
   if (node.op === 'fused') {
     const b = bodyOf(node);
     const out = node.attrs.output;
@@ -58,7 +69,7 @@ function lowerNode(graph, node, opts) {
       return Object.assign({ kind: 'fused-elementwise' }, single(cg.elementwiseKernel(b, out, node.shape, Object.assign({ tuning: tuning.ew }, sab))));
     }
     if (kind === 'rowwise') return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(b, out, sab)));
-    if (kind === 'epilogue') return Object.assign({ kind: 'fused-epilogue' }, single(cg.gemmKernel(b, out, Object.assign({ tuning: tuning.gemm }, sab))));
+    if (kind === 'epilogue') return Object.assign({ kind: 'fused-epilogue' }, single(cg.gemmKernel(b, out, Object.assign({ tuning: tuning.gemm }, sab, mmViews))));
     throw new Error(`no MI355X kernel for fused kind '${kind}'`);
   }
   if (ELEMENTWISE_OPS.has(node.op) || GATHERS.has(node.op)) {
@@ -80,9 +91,86 @@ function lowerNode(graph, node, opts) {
   }
   if (node.op === 'matmul') {
     const { body, output } = oneOpBody(graph, node);
-    return Object.assign({ kind: 'matmul' }, single(cg.gemmKernel(body, output, { tuning: (opts.tuning || {}).gemm })));
+    return Object.assign({ kind: 'matmul' }, single(cg.gemmKernel(body, output, Object.assign({ tuning: (opts.tuning || {}).gemm }, mmViews))));
   }
   throw new Error(`no MI355X lowering for '${node.op}'`);
+}
+
+/** Contiguous strides of `shape`. */
+function stridesOf(shape) {
+  const st = new Array(shape.length);
+  let acc = 1;
+  for (let d = shape.length - 1; d >= 0; d--) { st[d] = acc; acc *= shape[d]; }
+  return st;
+}
+
+/** Consumers of every node: id -> [consumer ids] (with repeats per operand slot). */
+function consumersOf(graph) {
+  const c = graph.nodes.map(() => []);
+  for (const n of graph.nodes) for (const i of n.inputs) c[i].push(n.id);
+  return c;
+}
+
+/**
+ * The matmul operand slots of node `n`: [[slot ('a'|'b'), operand position in
+ * n.inputs]] for the operands only its matmul reads.
+ */
+function matmulSlots(n) {
+  if (n.op === 'matmul') return [['a', 0], ['b', 1]];
+  if (n.op !== 'fused' || n.attrs.kind !== 'epilogue') return [];
+  const b = n.attrs.body;
+  const root = b.nodes.find((x) => x.op === 'matmul');
+  const slots = [];
+  root.inputs.forEach((bodyId, k) => {
+    const users = b.nodes.filter((x) => x.inputs.includes(bodyId));
+    if (users.length === 1 && users[0].id === root.id && root.inputs[0] !== root.inputs[1]) {
+      slots.push([k === 0 ? 'a' : 'b', Number(b.nodes[bodyId].attrs.name.slice(1))]);
+    }
+  });
+  return slots;
+}
+
+/** Perf-mode plan: { aliases: id -> source, folded: Set, views: id -> {a, b} of { source, view } }. */
+function perfPlan(graph, keep) {
+  const cons = consumersOf(graph);
+  const aliases = new Map();
+  for (const n of graph.nodes) {
+    if (n.op === 'reshape' && !keep.has(n.id)) {
+      const src = n.inputs[0];
+      aliases.set(n.id, aliases.has(src) ? aliases.get(src) : src);
+    }
+  }
+  // Which (consumer, operand position) pairs are matmul-only operand slots.
+  const slotOf = new Map();
+  for (const n of graph.nodes) for (const [slot, pos] of matmulSlots(n)) slotOf.set(`${n.id}:${pos}`, slot);
+  const folded = new Set();
+  for (let id = graph.nodes.length - 1; id >= 0; id--) {
+    const n = graph.nodes[id];
+    if (n.op !== 'transpose' || keep.has(id) || cons[id].length === 0) continue;
+    const ok = cons[id].every((c) => folded.has(c) || graph.nodes[c].inputs.every((i, pos) => i !== id || slotOf.has(`${c}:${pos}`)));
+    if (ok) folded.add(id);
+  }
+  const views = new Map();
+  for (const n of graph.nodes) {
+    for (const [slot, pos] of matmulSlots(n)) {
+      let cur = n.inputs[pos];
+      if (!folded.has(cur)) continue;
+      const shape = graph.nodes[cur].shape;
+      let perm = shape.map((_, d) => d);
+      while (folded.has(cur)) {
+        const t = graph.nodes[cur];
+        perm = perm.map((d) => t.attrs.perm[d]);
+        cur = t.inputs[0];
+      }
+      const st = stridesOf(graph.nodes[cur].shape);
+      const s = perm.map((d) => st[d]);
+      const r = shape.length;
+      const view = { batch: shape.slice(0, r - 2).map((e, d) => [e, s[d]]), sr: s[r - 2], sc: s[r - 1] };
+      if (!views.has(n.id)) views.set(n.id, {});
+      views.get(n.id)[slot] = { pos, source: cur, view, size: size(graph.nodes[cur].shape) };
+    }
+  }
+  return { aliases, folded, views };
 }
 
 /**
@@ -90,29 +178,42 @@ function lowerNode(graph, node, opts) {
  * reference's fused-kernel sabotages: 'epilogue-before-bias',
  * 'layernorm-tree-short', 'softmax-no-max', 'fused-bounds-off-by-one'),
  * applied to fused kernels only; tuning ({ ew: { unroll, nt, blocks }, colreduce: { blocks } })
- * overrides the kernels' launch-shape defaults (used by sweeps).
- * Returns { launches, workspace } (workspace: bytes of scratch the largest launch needs).
+ * overrides the kernels' launch-shape defaults (used by sweeps); perf and
+ * keep (node ids) as described at the top of this file.
+ * Returns { launches, workspace, aliases, folded } (workspace: bytes of scratch
+ * the largest launch needs; aliases: [[node, source]]; folded: node ids).
  */
 function lowerMI355X(graph, options) {
   const opts = options || {};
+  const plan = opts.perf ? perfPlan(graph, new Set(opts.keep || [])) : { aliases: new Map(), folded: new Set(), views: new Map() };
   const cache = new Map();
   const launches = [];
   let workspace = 0;
   for (const node of graph.nodes) {
     if (node.op === 'input' || node.op === 'const') continue;
-    // Kernels depend on structure and shapes only: reuse across identical nodes.
+    if (plan.aliases.has(node.id) || plan.folded.has(node.id)) continue;
+    const v = plan.views.get(node.id);
+    const mmViews = v ? { views: { a: v.a && v.a.view, b: v.b && v.b.view }, sizes: { a: v.a && v.a.size, b: v.b && v.b.size } } : null;
+    // Kernels depend on structure, shapes and operand views only: reuse across identical nodes.
     const key = JSON.stringify([node.op, node.inputs.map((id) => graph.nodes[id].shape), node.attrs, node.shape,
-      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null]);
+      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews]);
     let k = cache.get(key);
-    if (!k) { k = lowerNode(graph, node, opts); cache.set(key, k); }
+    if (!k) { k = lowerNode(graph, node, opts, mmViews); cache.set(key, k); }
     workspace = Math.max(workspace, k.workspace);
+    const inputs = node.inputs.map((id) => (plan.aliases.has(id) ? plan.aliases.get(id) : id));
+    if (v) for (const s of [v.a, v.b]) if (s) inputs[s.pos] = plan.aliases.has(s.source) ? plan.aliases.get(s.source) : s.source;
     launches.push({
       node: node.id, op: node.op, kind: k.kind, pattern: node.op === 'fused' ? node.attrs.pattern : undefined,
-      inputs: node.inputs.slice(), params: k.params, grid: k.kernels[0].grid, code: k.kernels[0].name,
+      inputs, params: k.params, grid: k.kernels[0].grid, code: k.kernels[0].name,
       kernels: k.kernels, workspace: k.workspace, bytes: algorithmicBytes(graph, node), flops: k.flops,
     });
+    if (v) {
+      // Operands read in place: for each folded slot, the node it stands for and the view of its source.
+      launches[launches.length - 1].views = {};
+      for (const slot of ['a', 'b']) if (v[slot]) launches[launches.length - 1].views[slot] = { pos: v[slot].pos, operand: node.inputs[v[slot].pos], source: v[slot].source, view: v[slot].view };
+    }
   }
-  return { launches, workspace };
+  return { launches, workspace, aliases: Array.from(plan.aliases.entries()), folded: Array.from(plan.folded) };
 }
 
 /** Every distinct kernel source of a launch list, in first-use order. */

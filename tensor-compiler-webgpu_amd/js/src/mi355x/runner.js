@@ -99,6 +99,13 @@ function packArgs(view, offset, inPtrs, outPtr, wsPtr, params) {
   for (let k = 0; k < MAX_P; k++) view.setUint32(offset + MAX_IN * 8 + 16 + 4 * k, k < params.length ? params[k] : 0, true);
 }
 
+/** The perf lowering's buffer sharing: alias (node -> node whose buffer it uses) and folded (no buffer). */
+function sharing(lowered) {
+  const alias = new Map(lowered.aliases || []);
+  for (const [k, v] of alias) if (alias.has(v)) throw new Error(`alias chain ${k} -> ${v} is not resolved`);
+  return { alias, folded: new Set(lowered.folded || []) };
+}
+
 function constData(node) {
   const n = size(node.shape);
   const v = node.attrs.value;
@@ -176,13 +183,20 @@ class HipRunner {
     const fns = this.functions(lowered);
     const n = graph.nodes.map((node) => size(node.shape));
     const cap = n.map((k) => (canary ? k + CANARY_PAD : k));
+    const { alias, folded } = sharing(lowered);
     const bufs = [];
+    const owned = [];
     let ws = 0;
     try {
-      for (let i = 0; i < graph.nodes.length; i++) bufs.push(this.alloc(cap[i] * 4));
+      for (let i = 0; i < graph.nodes.length; i++) {
+        if (alias.has(i)) bufs.push(bufs[alias.get(i)]);
+        else if (folded.has(i)) bufs.push(0);
+        else { const h = this.alloc(cap[i] * 4); bufs.push(h); owned.push(h); }
+      }
       ws = this.alloc(lowered.workspace || 16);
       for (const node of graph.nodes) {
         const h = bufs[node.id];
+        if (!h || alias.has(node.id)) continue;
         if (canary) a.fill32(h, 0, CANARY_BITS, cap[node.id]);
         if (node.op === 'input') {
           const v = inputs[node.attrs.name];
@@ -197,6 +211,7 @@ class HipRunner {
       a.sync();
       const values = [], canaryIntact = [];
       for (const node of graph.nodes) {
+        if (!bufs[node.id]) { values.push(null); canaryIntact.push(true); continue; }
         const out = new Float32Array(n[node.id]);
         a.d2h(bufs[node.id], 0, out);
         values.push(out);
@@ -204,7 +219,7 @@ class HipRunner {
       }
       return { values, canaryIntact };
     } finally {
-      for (const h of bufs) a.free(h);
+      for (const h of owned) a.free(h);
       if (ws) a.free(ws);
     }
   }
@@ -266,11 +281,20 @@ class Program {
     this.lowered = lowered;
     const fns = runner.functions(lowered);
     this.n = graph.nodes.map((node) => size(node.shape));
-    this.bufs = buffers ? buffers.slice() : graph.nodes.map((node) => runner.alloc(this.n[node.id] * 4));
-    this.owned = !buffers;
+    const { alias, folded } = sharing(lowered);
+    this.owned = [];
+    if (buffers) this.bufs = buffers.slice();
+    else {
+      this.bufs = [];
+      for (const node of graph.nodes) {
+        if (alias.has(node.id)) this.bufs.push(this.bufs[alias.get(node.id)]);
+        else if (folded.has(node.id)) this.bufs.push(0);
+        else { const h = runner.alloc(this.n[node.id] * 4); this.bufs.push(h); this.owned.push(h); }
+      }
+    }
     this.ws = runner.alloc(lowered.workspace || 16);
     for (const node of graph.nodes) {
-      if (node.op === 'const' && this.owned) a.h2d(this.bufs[node.id], 0, constData(node).subarray(0, this.n[node.id]));
+      if (node.op === 'const' && !buffers) a.h2d(this.bufs[node.id], 0, constData(node).subarray(0, this.n[node.id]));
     }
     const launches = lowered.launches.filter((l) => !only || only(l));
     let count = 0;
@@ -299,6 +323,7 @@ class Program {
   write(id, data) { this.a.h2d(this.bufs[id], 0, data instanceof Float32Array ? data : Float32Array.from(data)); }
 
   read(id) {
+    if (!this.bufs[id]) throw new Error(`node ${id} is not materialised (a transpose folded into its matmuls)`);
     const out = new Float32Array(this.n[id]);
     this.a.d2h(this.bufs[id], 0, out);
     return out;
@@ -341,7 +366,7 @@ class Program {
 
   destroy() {
     if (this.graphHandle) this.a.graphDestroy(this.graphHandle);
-    if (this.owned) for (const h of this.bufs) this.a.free(h);
+    for (const h of this.owned) this.a.free(h);
     this.a.free(this.ws);
   }
 }

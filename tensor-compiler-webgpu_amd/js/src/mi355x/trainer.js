@@ -14,18 +14,26 @@
 const { fuse } = require('../fusion/fuse');
 const { lowerMI355X } = require('./lower');
 
-/** Fuse and lower a step from the builders ({ graph, loss, logits, inputs, outputs, cotangent, ... }). */
+/**
+ * Fuse and lower a step from the builders ({ graph, loss, logits, inputs, outputs, cotangent, ... }).
+ * `lowered` is the perf lowering the trainer runs (reshapes share buffers,
+ * transposes read in place by their matmuls; `perf: false` turns it off);
+ * `checked` is the plain lowering, one launch per node, for node-by-node checks.
+ */
 function fusedStep(step, options) {
   const o = options || {};
   const keep = [step.loss, step.logits].concat(Object.values(step.outputs));
   const f = fuse(step.graph, { keep, sabotage: o.passSabotage });
   const at = (id) => f.index.get(id);
   const remap = (m) => { const r = {}; for (const k of Object.keys(m)) r[k] = at(m[k]); return r; };
+  const checked = lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning });
+  const lowered = o.perf === false ? checked
+    : lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning, perf: true, keep: keep.map(at) });
   return Object.assign({}, step, {
     graph: f.graph, fusion: f, original: step.graph,
     loss: at(step.loss), logits: at(step.logits),
     inputs: remap(step.inputs), outputs: remap(step.outputs),
-    lowered: lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning }),
+    lowered, checked,
   });
 }
 

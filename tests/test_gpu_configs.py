@@ -7,7 +7,9 @@ Every kept output is judged against the float64 oracle within the float32 budget
 through slices the oracle computes exactly (tests/test_config_slices.py shows
 they are exact): all 164 shifted rows plus sampled rows of config 3; sampled
 rows (y, dX) and columns (y, dW, dbias) of config 4 — every element at
-512x512x512. Over every element of the full tensors: no non-finite values,
+512x512x512. The perf lowering (config 4's transposed operands read in place by
+the matmuls) equals the plain lowering bit for bit on every kept output. Over
+every element of the full tensors: no non-finite values,
 relu outputs >= 0 and tanh outputs in [-1, 1], and each softmax row summing to 1
 (each logSoftmax row's log-sum-exp 0) within ROW_TOL. ROW_TOL: each float32 y
 carries at most ~48 ulp of relative error from exp (|x - max| < 24 here), the
@@ -40,7 +42,9 @@ def _judge_sample(b, graph, inputs, compare):
 def _check_props(c):
     for p in c["props"]:
         assert p["nonfiniteFused"] == 0 and p["nonfiniteUnfused"] == 0, (c["name"], p)
-    assert c["canaryFused"] and c["canaryUnfused"], (c["name"], "canary")
+    assert c["canaryFused"] and c["canaryUnfused"] and c["perf"]["canary"], (c["name"], "canary")
+    # The perf lowering (transposes read in place by the matmuls) gives the same bits.
+    assert c["perf"]["same"] == c["perf"]["total"], (c["name"], c["perf"])
     same = sum(p["bitwiseSame"] for p in c["props"]) / sum(p["n"] for p in c["props"])
     return same
 
@@ -101,3 +105,5 @@ def test_c4_full_size_within_budget(c4_bundle):
             assert ju["pass"], (c["name"], s["slice"], "unfused", ju["first"], ju["unjudged"])
         if c["kind"] == "forward":
             assert c["fusedKinds"] == ["fused-epilogue"], c["fusedKinds"]
+        else:
+            assert c["perf"]["folded"] == 2, c["perf"]   # transpose(W) and transpose(X)

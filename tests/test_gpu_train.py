@@ -34,11 +34,22 @@ def node_local(tool, tmp_path, req):
     gc = g.cases[0]
     expected, bound = bounds.local_reference_fused(c["fused"], fused_vals)
     gpu = {int(k): g.arr(v) for k, v in gc["gpu"].items()}
+    assert set(gpu) == set(expected)
     j = bounds.judge_local(c["fused"], gpu, expected, bound)
     print(f"{req['model']}: node-local worst {j['worst']:.3g} over {j['elements']} elements, "
           f"unjudgeable {j['unjudgeable']}, by kind {j['byKind']}", file=sys.stderr)
     assert gc["canaryIntact"]
     assert j["pass"], (j["first"], j["unjudged"])
+    # The perf lowering: every node it launches (all but the shared reshapes and the
+    # transposes its matmuls read in place), on the same reference operands.
+    perf = {int(k): g.arr(v) for k, v in gc["gpuPerf"].items()}
+    skipped = set(expected) - set(perf)
+    assert skipped == {a for a, _ in gc["aliases"]} | set(gc["folded"])
+    assert all(c["fused"]["nodes"][i]["op"] in ("reshape", "transpose") for i in skipped)
+    jp = bounds.judge_local(c["fused"], perf, {k: expected[k] for k in perf}, {k: bound[k] for k in perf})
+    print(f"{req['model']}: perf lowering node-local worst {jp['worst']:.3g} over {jp['elements']} elements, "
+          f"{len(skipped)} nodes shared or folded", file=sys.stderr)
+    assert jp["pass"], (jp["first"], jp["unjudged"])
     return j
 
 
@@ -77,8 +88,10 @@ def test_c1_first_step_against_composed_budget(tool):
 
 
 def test_c1_trainer_consistency_and_learning(tool):
-    """20 fused-trainer steps on one batch: each equals the checked path (runner.run with the
-    new values fed back by the host) bit for bit, and the loss falls at every step."""
+    """20 fused-trainer steps on one batch: each equals the checked path (runner.run of the
+    plain lowering, one launch per node, with the new values fed back by the host) bit for
+    bit — the trainer runs the perf lowering, whose matmuls read transposed operands in
+    place — and the loss falls at every step."""
     r = tool("gpu-train", {"model": "mlp", "steps": 20, "consistency": True, "consistencySteps": 20, "sameBatch": True})
     assert r["identical"] is True
     losses = r["losses"]
@@ -89,9 +102,12 @@ def test_c1_trainer_consistency_and_learning(tool):
 
 
 def test_c5_full_size_trainer(tool):
-    """Config 5 at full size (B 64): the fused trainer's first 2 steps equal the checked path bit
-    for bit, and the initial loss is near ln(96) (small initial weights, uniform tokens)."""
+    """Config 5 at full size (B 64): the fused trainer's first 2 steps (perf lowering: 88
+    transposes read in place by their matmuls, 37 reshapes sharing buffers) equal the checked
+    path (plain lowering) bit for bit, and the initial loss is near ln(96) (small initial
+    weights, uniform tokens)."""
     r = tool("gpu-train", {"model": "transformer", "B": 64, "steps": 2, "consistency": True, "consistencySteps": 2},
              timeout=600)
     assert r["identical"] is True
+    assert r["folded"] > 0 and r["aliases"] > 0 and r["launches"] < r["checkedLaunches"]
     assert abs(r["losses"][0] - np.log(96)) < 0.1, r["losses"]

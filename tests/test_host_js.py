@@ -166,3 +166,63 @@ def test_generated_kernels_read_no_parameter_block(golden_cases, tool):
         for l in out["launches"]:
             for k in l["kernels"]:
                 assert not re.search(r"\.P\[", k["source"]), k["name"]
+
+
+def _chain_value(graph, operand, source, src_value):
+    """The operand's value from its source through the transpose/reshape chain between them (oracle kernels)."""
+    from oracle import interp
+    chain = []
+    cur = operand
+    while cur != source:
+        node = graph["nodes"][cur]
+        assert node["op"] in ("transpose", "reshape"), node["op"]
+        chain.append(node)
+        cur = node["inputs"][0]
+    v = src_value
+    for node in reversed(chain):
+        v = interp.kernel(node, [v], graph)
+    return v
+
+
+@pytest.mark.parametrize("req", [{"model": "mlp"}, {"model": "transformer", "B": 2}, {"model": "transformer-ref"}])
+def test_perf_lowering_views_address_the_operands(tool, req):
+    """The perf lowering skips only reshapes (sharing their input's buffer) and transposes
+    whose every consumer is a matmul operand slot; each matmul operand it reads in place
+    is addressed by its strided view exactly as the transpose chain would have laid it out
+    (checked element by element on distinct values), and the load mode matches the view."""
+    d = tool("perf-lower", req)
+    g = d["graph"]
+    nodes = g["nodes"]
+    for a, src in d["aliases"]:
+        assert nodes[a]["op"] == "reshape" and nodes[src]["op"] != "reshape"
+    assert all(nodes[i]["op"] == "transpose" for i in d["folded"])
+    launched = {l["node"] for l in d["launches"]}
+    skipped = {a for a, _ in d["aliases"]} | set(d["folded"])
+    assert launched.isdisjoint(skipped)
+    assert launched | skipped == {n_id for n_id, n in enumerate(nodes) if n["op"] not in ("input", "const")}
+    checked = 0
+    for l in d["launches"]:
+        for i in l["inputs"]:
+            assert i not in skipped, (l["node"], i)
+        for slot, v in (l["views"] or {}).items():
+            shape = nodes[v["operand"]]["shape"]
+            src_shape = nodes[v["source"]]["shape"]
+            src = np.arange(int(np.prod(src_shape)), dtype=np.float64)
+            want = _chain_value(g, v["operand"], v["source"], src).reshape(shape)
+            view = v["view"]
+            idx = np.zeros(shape, dtype=np.int64)
+            strides = [s for _, s in view["batch"]] + [view["sr"], view["sc"]]
+            for axis, st in enumerate(strides):
+                sh = [1] * len(shape)
+                sh[axis] = shape[axis]
+                idx = idx + np.arange(shape[axis]).reshape(sh) * st
+            assert np.array_equal(src[idx], want), (l["node"], slot)
+            mode = l["modes"][0 if slot == "a" else 1]
+            R, C = shape[-2], shape[-1]
+            if view["sc"] == 1 and C % 4 == 0:
+                assert mode == 0
+            elif view["sr"] == 1 and R % 4 == 0 and view["sc"] % 4 == 0:
+                assert mode == 1
+            checked += 1
+    if req["model"] != "mlp":
+        assert checked > 10
