@@ -125,6 +125,17 @@ __device__ __forceinline__ float wave_reduce(float v) {
   return v;
 }
 
+// Reduce within aligned groups of L lanes (L = 16, 32 or 64) of a wavefront:
+// butterfly over the group, then every lane takes the group's first lane's
+// value, so all lanes of a group hold the same bits.
+template <bool IsMax, int L>
+__device__ __forceinline__ float group_reduce(float v) {
+  static_assert(L == 16 || L == 32 || L == 64, "group width");
+#pragma unroll
+  for (int off = L / 2; off >= 1; off >>= 1) v = combine<IsMax>(v, __shfl_xor(v, off, L));
+  return __shfl(v, 0, L);
+}
+
 // Reduce over a workgroup of THREADS (a multiple of 64); every thread gets the
 // result. `scratch` holds THREADS/64 floats of LDS; it is reused across calls,
 // hence the barrier before returning.

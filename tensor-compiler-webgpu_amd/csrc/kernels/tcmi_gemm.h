@@ -20,19 +20,22 @@
 // Tiling: a workgroup of 256 threads (4 wavefronts in a 2 x 2 grid) owns a
 // BM x BN tile of C; each wavefront owns (TM·16) x (TN·16) of it as TM x TN
 // accumulators of v_mfma_f32_16x16x4f32 (D 16x16 += A 16x4 · B 4x16). K is
-// walked 16 at a time through two LDS buffers: the global loads of the next
-// slice are in flight while the current one feeds the matrix cores, and one
-// barrier per slice separates the two.
+// walked BK (16, 32 or 64) at a time through two LDS buffers: the global loads
+// of the next slice are in flight while the current one feeds the matrix
+// cores, and one barrier per slice separates the two. A deeper slice gives the
+// matrix cores more work per round trip to memory, which is what a long-K,
+// few-tile matmul (a weight gradient) needs when there is one workgroup per CU.
 //
 // Operand layout per lane of a 16x16x4 MFMA (lane = 16·q + t, t in 0..15):
 //   A value: row t, k-group q;  B value: column t, k-group q;
 //   D: column t, rows 4q .. 4q+3 (one per accumulator register).
-// Within a 16-wide K slice, lane group q supplies k = 4q + s at step s, so a
-// lane's four A values of a slice are contiguous in LDS (one ds_read_b128);
+// Within each 16-wide part of a slice, lane group q supplies k = 4q + s at step
+// s, so a lane's four A values of a part are contiguous in LDS (one ds_read_b128);
 // both operands use the same k for the same (q, s), so the product is exact
 // in what it sums, in an order the float32 budget already covers (any order
-// of K terms, gamma(K)). The order does not depend on the operands' layouts:
-// a view and a materialised copy of the same operand give the same bits.
+// of K terms, gamma(K)). The order depends on neither BK, the tile size nor
+// the operands' layouts (k ascends 16 at a time whatever the slice depth): a
+// view and a materialised copy of the same operand give the same bits.
 
 #pragma once
 
@@ -57,14 +60,14 @@ struct DenseView {
 // epilogue. MODE_C needs C % 4 == 0 and MODE_R needs R % 4 == 0 (R, C: the
 // operand's extents), and both need every other stride a multiple of 4, so a
 // 128-bit load is aligned and either wholly inside the operand or wholly out.
-template <int TM, int TN, int AMODE, int BMODE, bool SPLIT, class AV, class BV, class Epi>
+template <int TM, int TN, int BK, int AMODE, int BMODE, bool SPLIT, class AV, class BV, class Epi>
 __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restrict__ a_ptr,
                                          const float* __restrict__ b_ptr, const uint32_t batch, const uint32_t M,
                                          const uint32_t K, const uint32_t N, const uint32_t chunks,
                                          const uint32_t chunkK) {
   constexpr int BM = 2 * TM * 16;
   constexpr int BN = 2 * TN * 16;
-  constexpr int BK = 16;
+  static_assert(BK == 16 || BK == 32 || BK == 64, "slice depth");
   constexpr int AS = BK + 4;   // padded row stride of the A slice (conflict-free b128 reads)
   constexpr int BS = BN + 4;   // padded row stride of the B slice
   __shared__ __attribute__((aligned(16))) float As[2][BM * AS];
@@ -100,7 +103,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
 #pragma unroll
       for (int v = 0; v < A_VEC; ++v) {
         const int t = tid + v * 256;
-        const uint32_t row = t >> 2, kk = (t & 3) * 4;
+        const uint32_t row = t / (BK / 4), kk = (t % (BK / 4)) * 4;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t < BM * BK / 4 && m0 + row < M && k0 + kk < kend)
           x = *reinterpret_cast<const float4*>(Ab + (size_t)(m0 + row) * AV::SR + k0 + kk);
@@ -164,7 +167,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
       for (int v = 0; v < A_VEC; ++v) {
         const int t = tid + v * 256;
         if (t < BM * BK / 4) {
-          const int row = t >> 2, kk = (t & 3) * 4;
+          const int row = t / (BK / 4), kk = (t % (BK / 4)) * 4;
           *reinterpret_cast<float4*>(&As[buf][row * AS + kk]) = ra[v];
         }
       }
@@ -230,21 +233,24 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
   for (uint32_t ks = 0; ks < slices; ++ks) {
     const int cur = ks & 1;
     if (ks + 1 < slices) load_slice(kbeg + (ks + 1) * BK);
-    // A values of this lane for every row tile: k = 4q .. 4q+3 of the slice.
-    float4 av[TM];
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
-      av[i] = *reinterpret_cast<const float4*>(&As[cur][(wm * TM * 16 + i * 16 + t16) * AS + 4 * q]);
+    for (int g = 0; g < BK / 16; ++g) {
+      // A values of this lane for every row tile: k = 16g + 4q .. 16g + 4q + 3 of the slice.
+      float4 av[TM];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      float bv[TN];
+      for (int i = 0; i < TM; ++i)
+        av[i] = *reinterpret_cast<const float4*>(&As[cur][(wm * TM * 16 + i * 16 + t16) * AS + 16 * g + 4 * q]);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) bv[j] = Bs[cur][(4 * q + s) * BS + wn * TN * 16 + j * 16 + t16];
+      for (int s = 0; s < 4; ++s) {
+        float bv[TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        const float a = lane4(av[i], s);
+        for (int j = 0; j < TN; ++j) bv[j] = Bs[cur][(16 * g + 4 * q + s) * BS + wn * TN * 16 + j * 16 + t16];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < TM; ++i) {
+          const float a = lane4(av[i], s);
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv[j], acc[i][j], 0, 0, 0);
+        }
       }
     }
     if (ks + 1 < slices) store_slice(cur ^ 1);

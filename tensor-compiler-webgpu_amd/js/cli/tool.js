@@ -15,7 +15,7 @@
 //   transformer-init the reference transformer (golden config) forward + gradient graph and its inputs
 //   config-graphs    request {c3: [{fn, R, C}], c4: [{act, M, K, N}]} -> forward and gradient graphs of configs 3 and 4
 // GPU commands write a bundle (manifest.json + data.f32) under --out:
-//   gpu-direct       every direct case, fused, canary-padded, on the GPU
+//   gpu-direct       request {sabotage?}: every direct case, fused, canary-padded, on the GPU
 //   gpu-graphs       request {graphs: [{name, graph, inputs, keep, unfused?}]} fused (and unfused) on the GPU
 //   gpu-configs      request {c3: [...], c4: [...], unfused} configs 3 and 4, kept outputs as oracle-computable slices
 
@@ -95,7 +95,12 @@ function transformerInit(req) {
 /** Compile, offline, the kernels a named group of GPU runs will ask for (same module text as on the box). */
 function precompileGroup(group, arch) {
   const { precompile } = require('../src/mi355x/runner');
-  if (group === 'direct') return precompile(fusedDirectCases().map((c) => lowerMI355X(fuse(c.graph).graph)), arch);
+  if (group === 'direct') {
+    const fused = fusedDirectCases().map((c) => fuse(c.graph).graph);
+    let n = precompile(fused.map((g) => lowerMI355X(g)), arch);
+    for (const sabotage of KERNEL_SABOTAGES) n += precompile(fused.map((g) => lowerMI355X(g, { sabotage })), arch);
+    return n;
+  }
   if (group === 'models') {
     // The trainer compiles a step's kernels as one module: the same text here.
     const { modelStep } = require('../src/builders/models');
@@ -127,12 +132,23 @@ function precompileGroup(group, arch) {
   throw new Error(`unknown precompile group '${group}'`);
 }
 
-async function gpuDirect(dir) {
+/** The load modes (A, B) of a matmul launch's kernel, or null. */
+function gemmModes(l) {
+  const m = l.kernels[0].source.match(/gemm_f32<\d+, \d+, \d+, (\d), (\d)/);
+  return m ? [Number(m[1]), Number(m[2])] : null;
+}
+
+/** The reference's four kernel sabotages (codegen-fused.js:22), as lowerMI355X applies them. */
+const KERNEL_SABOTAGES = ['epilogue-before-bias', 'layernorm-tree-short', 'softmax-no-max', 'fused-bounds-off-by-one'];
+
+async function gpuDirect(dir, req) {
   const { HipRunner } = require('../src/mi355x/runner');
+  const sabotage = (req && req.sabotage) || undefined;
+  if (sabotage && !KERNEL_SABOTAGES.includes(sabotage)) throw new Error(`unknown kernel sabotage '${sabotage}'`);
   const runner = HipRunner.create();
   const bundle = new Bundle(dir);
   const cases = fusedDirectCases();
-  const plans = cases.map((c) => { const f = fuse(c.graph); return { f, lowered: lowerMI355X(f.graph) }; });
+  const plans = cases.map((c) => { const f = fuse(c.graph); return { f, lowered: lowerMI355X(f.graph, { sabotage }) }; });
   process.stderr.write(`gpu-direct: compiling ${plans.length} launch lists\n`);
   runner.functions(plans.map((p) => p.lowered));
   for (const [k, c] of cases.entries()) {
@@ -148,7 +164,7 @@ async function gpuDirect(dir) {
     bundle.add({ name: c.name, kind: c.kind, pattern: c.pattern, graph: c.graph.toJSON(), fused: f.graph.toJSON(), origin: f.origin,
       inputs: ins, gpu, canaryIntact: r.canaryIntact, launches: lowered.launches.map((l) => ({ node: l.node, kind: l.kind, code: l.code })) });
   }
-  bundle.close({ device: runner.info() });
+  bundle.close({ device: runner.info(), sabotage: sabotage || null });
 }
 
 async function gpuGraphs(req, dir) {
@@ -570,11 +586,11 @@ async function main() {
       }
       const l = lowerMI355X(g, { perf: true, keep });
       out = { graph: g.toJSON(), keep, aliases: l.aliases, folded: l.folded,
-        launches: l.launches.map((x) => ({ node: x.node, kind: x.kind, inputs: x.inputs, views: x.views || null, modes: x.kernels[0].source.match(/gemm_f32<\d+, \d+, (\d), (\d)/) ? x.kernels[0].source.match(/gemm_f32<\d+, \d+, (\d), (\d)/).slice(1).map(Number) : null })) };
+        launches: l.launches.map((x) => ({ node: x.node, kind: x.kind, inputs: x.inputs, views: x.views || null, modes: gemmModes(x) })) };
       break;
     }
     case 'precompile': out = { kernels: precompileGroup(req.group || 'direct', req.arch) }; break;
-    case 'gpu-direct': await gpuDirect(outDir(argv)); out = { ok: true }; break;
+    case 'gpu-direct': await gpuDirect(outDir(argv), req); out = { ok: true }; break;
     case 'step-graph': stepGraph(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-local': await gpuLocal(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-train': out = await gpuTrain(req); break;

@@ -95,13 +95,16 @@ function gatherStrides(node, inShape) {
  * root of an epilogue, the reductions of a rowwise body).
  */
 class Emitter {
-  constructor(body, params, hooks) {
+  constructor(body, params, hooks, slack) {
     this.b = body;
     this.params = params;
     this.hooks = hooks;
     this.memo = new Map();
     this.counter = 0;
     this.gatherBase = new Map();
+    // Elements an operand may be read past its end (only the deliberately broken
+    // bounds check of a sabotaged kernel reads one past, into the canary pad).
+    this.slack = slack || 0;
   }
 
   fresh(prefix) { return `${prefix}${this.counter++}`; }
@@ -115,7 +118,7 @@ class Emitter {
   gatherIndex(node, ctx) {
     const inShape = this.b.nodes[node.inputs[0]].shape;
     const g = classifyGather(node, inShape);
-    if (ctx.limit === undefined || ctx.limit > size(node.shape)) {
+    if (ctx.limit === undefined || ctx.limit > size(node.shape) + this.slack) {
       throw new Error(`gather node ${node.id}: read at ${ctx.limit} indices, has ${size(node.shape)} elements`);
     }
     let maxSrc = 0;
@@ -164,7 +167,7 @@ class Emitter {
     if (special !== undefined) {
       v = special;
     } else if (node.op === 'input') {
-      if (ctx.limit === undefined || ctx.limit > size(node.shape)) {
+      if (ctx.limit === undefined || ctx.limit > size(node.shape) + this.slack) {
         throw new Error(`operand ${node.attrs.name}: read at ${ctx.limit} indices, has ${size(node.shape)} elements`);
       }
       v = this.hooks.load(Number(node.attrs.name.slice(1)), ctx, lines, node);
@@ -274,19 +277,25 @@ function elementwiseKernel(b, output, outShape, opts) {
   const lane = [];
   const vout = vecEmitter.value(output, { key: 'i', idx: 'i', root: true, limit: n }, lane);
 
-  // Scalar tail: the same body, every load scalar.
+  // Scalar tail: the same body, every load scalar. The reference's sabotage
+  // 'fused-bounds-off-by-one' (codegen-fused.js:160) lets one thread past the
+  // end: it reads every flat operand and writes the output at index n, one
+  // element into the canary pad that check-mode buffers carry (the record is
+  // marked so the runner refuses it without canaries); gathers stay in range
+  // (every axis index is taken modulo its extent).
+  const offByOne = o.sabotage === 'fused-bounds-off-by-one';
   const tailEmitter = new Emitter(b, params, {
     load(k, ctx, lines) {
       const v = `T${lines.length}_${k}`;
       lines.push(`const float ${v} = A.in[${k}][${ctx.idx}];`);
       return v;
     },
-  });
+  }, offByOne ? 1 : 0);
   tailEmitter.gatherBase = vecEmitter.gatherBase;  // same parameter offsets
   const tail = [];
-  const tout = tailEmitter.value(output, { key: 'i', idx: 'i', root: true, limit: n }, tail);
+  const tout = tailEmitter.value(output, { key: 'i', idx: 'i', root: true, limit: offByOne ? n + 1 : n }, tail);
 
-  const guard = o.sabotage === 'fused-bounds-off-by-one' ? 'threadIdx.x <= (n & 3u)' : 'threadIdx.x < (n & 3u)';
+  const guard = offByOne ? 'threadIdx.x <= (n & 3u)' : 'threadIdx.x < (n & 3u)';
   const store = nt ? '__builtin_nontemporal_store(o4, reinterpret_cast<tcmi::f4*>(A.out) + v);'
     : 'reinterpret_cast<tcmi::f4*>(A.out)[v] = o4;';
   const text = `extern "C" __global__ void __launch_bounds__(${WG}) __KERNEL__(const TcmiArgs A) {
@@ -329,7 +338,8 @@ ${indent(tail, '    ')}
 `;
   const k = kernelText('ew', text);
   const groups = Math.max(1, Math.min(Math.ceil(Math.max(1, n >> 2) / WG), maxBlocks));
-  return { name: k.name, source: k.source, params: Uint32Array.from(params), grid: [groups, 1, 1], block: [WG, 1, 1], lds: 0, workspace: 0 };
+  return { name: k.name, source: k.source, params: Uint32Array.from(params), grid: [groups, 1, 1], block: [WG, 1, 1], lds: 0, workspace: 0,
+    needsPad: offByOne };
 }
 
 // ---- rowwise ------------------------------------------------------------------------
@@ -339,9 +349,14 @@ const isReduce = (n) => n.op === 'sum' || n.op === 'max';
 /**
  * A rowwise body: last-axis sum/max reductions of element-tier values ([R, C])
  * and row-tier values ([R, 1]) built from them, output at element or row tier.
- * One workgroup per row (grid-stride over rows). Every element-tier operand
- * load is made once into registers and reused by every phase, so each input
- * is read from HBM once, whatever the number of reductions.
+ * Every element-tier operand load is made once into registers and reused by
+ * every phase, so each input is read from HBM once, whatever the number of
+ * reductions. A row is owned by L lanes: for C >= 2048 a whole workgroup of
+ * 256 (reduced through LDS), otherwise a group of 16, 32 or 64 lanes of one
+ * wavefront — the fewest that leave no lane idle for the row's float4 slots —
+ * reduced by butterfly shuffles, with 256 / L rows per workgroup, so short
+ * rows (attention's 128, LayerNorm's 256) still move a full workgroup's worth
+ * of data per launch slot. Rows are walked grid-stride.
  */
 function rowwiseKernel(b, output, opts) {
   const o = opts || {};
@@ -352,9 +367,12 @@ function rowwiseKernel(b, output, opts) {
   const C = S[S.length - 1];
   const R = size(S) / C;
   if (size(S) >= 2 ** 31) throw new Error('rowwise kernel exceeds the 32-bit index space');
-  const T = C >= 2048 ? 256 : 64;
   const vec = C % 4 === 0;
   const W = vec ? 4 : 1;                     // elements per slot
+  const pow2 = (x) => 2 ** Math.ceil(Math.log2(Math.max(1, x)));
+  const T = C >= 2048 ? 256 : Math.min(64, Math.max(16, pow2(Math.ceil(C / W))));   // lanes per row
+  const BLOCK = 256;
+  const G = BLOCK / T;                        // rows per workgroup
   const E = Math.max(1, Math.ceil(C / (W * T)));  // slots per thread
   const params = [R, C];
   const rowTier = (id) => size(b.nodes[id].shape) === R && size(b.nodes[id].shape) !== R * C;
@@ -395,12 +413,12 @@ function rowwiseKernel(b, output, opts) {
           if (vec) {
             cacheDecl.push(`float4 ${c}[${E}];`,
               `#pragma unroll`,
-              `for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = (threadIdx.x + s * ${T}u) * 4u;`,
+              `for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = (ln + s * ${T}u) * 4u;`,
               `  ${c}[s] = c0 < C ? reinterpret_cast<const float4*>(A.in[${k}] + rowBase)[c0 >> 2] : make_float4(0.f, 0.f, 0.f, 0.f); }`);
           } else {
             cacheDecl.push(`float ${c}[${E}];`,
               `#pragma unroll`,
-              `for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = threadIdx.x + s * ${T}u;`,
+              `for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = ln + s * ${T}u;`,
               `  ${c}[s] = c0 < C ? A.in[${k}][rowBase + c0] : 0.f; }`);
           }
         }
@@ -415,7 +433,7 @@ function rowwiseKernel(b, output, opts) {
           caches.set(ck, c);
           cacheDecl.push(`float4 ${c}[${E}];`,
             `#pragma unroll`,
-            `for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = (threadIdx.x + s * ${T}u) * 4u;`,
+            `for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = (ln + s * ${T}u) * 4u;`,
             `  ${c}[s] = c0 < C ? reinterpret_cast<const float4*>(A.in[${k}])[c0 >> 2] : make_float4(0.f, 0.f, 0.f, 0.f); }`);
         }
         return `tcmi::lane4(${caches.get(ck)}[s], l)`;
@@ -433,7 +451,7 @@ function rowwiseKernel(b, output, opts) {
 for (int s = 0; s < ${E}; ++s) {
 #pragma unroll
   for (int l = 0; l < 4; ++l) {
-    const uint32_t c = (threadIdx.x + s * ${T}u) * 4u + l;
+    const uint32_t c = (ln + s * ${T}u) * 4u + l;
     if (c < C) {
       const uint32_t e = rowBase + c;
 ${indent(bodyLines, '      ')}
@@ -442,7 +460,7 @@ ${indent(bodyLines, '      ')}
 }`
     : `#pragma unroll
 for (int s = 0; s < ${E}; ++s) {
-  const uint32_t c = threadIdx.x + s * ${T}u;
+  const uint32_t c = ln + s * ${T}u;
   if (c < C) {
     const uint32_t e = rowBase + c;
 ${indent(bodyLines, '    ')}
@@ -459,8 +477,9 @@ ${indent(bodyLines, '    ')}
     const isMax = rd.op === 'max';
     const pre = rowLines.splice(rowBefore);
     const acc = `acc${k}`;
-    let result = `tcmi::block_reduce<${isMax}, ${T}>(${acc}, red)`;
-    if (shortTree) result = `tcmi::block_reduce<${isMax}, ${T}>(threadIdx.x < ${T / 2} ? ${acc} : ${isMax ? '(-TCMI_INF)' : '0.f'}, red)`;
+    const reduce = (v) => (T === 256 ? `tcmi::block_reduce<${isMax}, 256>(${v}, red)` : `tcmi::group_reduce<${isMax}, ${T}>(${v})`);
+    let result = reduce(acc);
+    if (shortTree) result = reduce(`ln < ${T / 2}u ? ${acc} : ${isMax ? '(-TCMI_INF)' : '0.f'}`);
     if (o.sabotage === 'softmax-no-max' && isMax && (o.pattern === 'softmax' || o.pattern === 'log-softmax')) result = '0.f';
     phases.push(...pre,
       `float ${acc} = ${isMax ? '(-TCMI_INF)' : '0.f'};`,
@@ -474,7 +493,7 @@ ${indent(bodyLines, '    ')}
     const rowBefore = rowLines.length;
     const v = em.value(output, ROW, rowLines);
     const pre = rowLines.splice(rowBefore);
-    store = [...pre, `if (threadIdx.x == 0) A.out[r] = ${v};`];
+    store = [...pre, `if (ln == 0) A.out[r] = ${v};`];
   } else {
     const rowBefore = rowLines.length;
     const inner = [];
@@ -484,7 +503,7 @@ ${indent(bodyLines, '    ')}
       // Compute the 4 lanes of each slot, then one 128-bit store.
       store = [...pre, `#pragma unroll
 for (int s = 0; s < ${E}; ++s) {
-  const uint32_t c0 = (threadIdx.x + s * ${T}u) * 4u;
+  const uint32_t c0 = (ln + s * ${T}u) * 4u;
   if (c0 < C) {
     float o4[4];
 #pragma unroll
@@ -501,11 +520,11 @@ ${indent(inner, '      ')}
       store = [...pre, loop(inner.concat([`A.out[e] = ${v};`]))];
     }
   }
-  const text = `extern "C" __global__ void __launch_bounds__(${T}) __KERNEL__(const TcmiArgs A) {
-  __shared__ float red[${T / 64}];
-  const uint32_t R = ${R}u;
+  const text = `extern "C" __global__ void __launch_bounds__(${BLOCK}) __KERNEL__(const TcmiArgs A) {
+${T === 256 ? '  __shared__ float red[4];\n' : ''}  const uint32_t R = ${R}u;
   const uint32_t C = ${C}u;
-  for (uint32_t r = blockIdx.x; r < R; r += gridDim.x) {
+  const uint32_t ln = threadIdx.x % ${T}u;     // lane within the row's group
+  for (uint32_t r = blockIdx.x * ${G}u + threadIdx.x / ${T}u; r < R; r += gridDim.x * ${G}u) {
     const uint32_t rowBase = r * C;
 ${indent(cacheDecl, '    ')}
 ${indent(phases, '    ')}
@@ -514,8 +533,8 @@ ${indent(store, '    ')}
 }
 `;
   const k = kernelText('row', text);
-  const groups = Math.max(1, Math.min(R, 65536));
-  return { name: k.name, source: k.source, params: Uint32Array.from(params), grid: [groups, 1, 1], block: [T, 1, 1], lds: 0, workspace: 0 };
+  const groups = Math.max(1, Math.min(Math.ceil(R / G), 65536));
+  return { name: k.name, source: k.source, params: Uint32Array.from(params), grid: [groups, 1, 1], block: [BLOCK, 1, 1], lds: 0, workspace: 0 };
 }
 
 // ---- column reductions (sum / max over a non-last axis) --------------------------------
@@ -620,25 +639,38 @@ function colreduceKernels(op, outer, n, inner, tuning) {
 // ---- matmul with epilogue ----------------------------------------------------------------
 
 /**
- * Tiling of a matmul: MFMA tiles per wavefront (T: the workgroup owns 32T x 32T of
- * the output) and K chunks (split-K). The largest tile that still gives every
- * CU of the 256 a workgroup; when even the smallest leaves CUs idle and K is
- * long, K is split (chunks of at least 256, at most 16 of them).
+ * Tiling of a matmul: MFMA tiles per wavefront (T: the workgroup owns 32T x 32T
+ * of the output), K chunks (split-K) and the LDS slice depth (bk). Rules, from
+ * a sweep of every (T, bk, chunks) on the MI355X over the configs' shapes:
+ *   - T = 4 when M, N >= 128 and that still gives the 256 CUs a workgroup each,
+ *     except for an A operand read transposed (MODE_R) when T = 2 gives two
+ *     workgroups per CU (its scattered LDS stores cost more at T = 4);
+ *     T = 2 when that gives every CU a workgroup (or when K is long, see below);
+ *     T = 1 otherwise;
+ *   - K is split only when it is long (>= 2048) and the output leaves fewer than
+ *     two workgroups per CU: into chunks of >= 256 (at most 32) so that about
+ *     1024 workgroups run — a few per CU hide each other's memory latency; a
+ *     short K is never split (the partial-sum traffic costs more than it saves);
+ *   - bk = 64 for T = 1, 32 for T = 2, 16 for T = 4 (the deeper slice feeds the
+ *     small tiles more work per round trip to memory).
+ * `aTransposed`: A is read through a view whose rows are contiguous (MODE_R).
  */
-function gemmTiling(batch, M, N, K, tuning) {
+function gemmTiling(batch, M, N, K, tuning, aTransposed) {
   const t = tuning || {};
   const blocks = (T) => batch * Math.ceil(M / (32 * T)) * Math.ceil(N / (32 * T));
+  const longK = K >= 2048;
   let T;
   if (t.tile) T = t.tile;
-  else if (M >= 128 && N >= 128 && blocks(4) >= 256) T = 4;
-  else if (M >= 64 && N >= 64) T = 2;
-  else T = M >= 32 && N >= 32 ? 1 : 1;
+  else if (M >= 128 && N >= 128 && blocks(4) >= 256 && !(aTransposed && blocks(2) >= 512)) T = 4;
+  else if (M >= 64 && N >= 64 && (blocks(2) >= 256 || longK)) T = 2;
+  else T = 1;
   let chunks = 1;
   if (t.splitk !== undefined) chunks = t.splitk;
-  else if (blocks(T) < 256 && K >= 512) chunks = Math.max(1, Math.min(Math.ceil(512 / blocks(T)), Math.floor(K / 256), 16));
+  else if (longK && blocks(T) < 512) chunks = Math.max(1, Math.min(Math.ceil(1024 / blocks(T)), Math.floor(K / 256), 32));
   let chunkK = Math.ceil(Math.ceil(K / chunks) / 16) * 16;
   chunks = Math.ceil(K / chunkK);
-  return { T, chunks, chunkK, blocks: blocks(T) * chunks };
+  const bk = t.bk || (T === 1 ? 64 : T === 2 ? 32 : 16);
+  return { T, chunks, chunkK, bk, blocks: blocks(T) * chunks };
 }
 
 /**
@@ -722,11 +754,11 @@ function gemmKernel(b, output, opts) {
     lines.push(`const float ${t} = tcmi::op_add(${out}, ${ov});`);
     out = t;
   }
-  const tl = gemmTiling(batch, M, N, K, o.tuning);
-  const T = tl.T;
-  const split = tl.chunks > 1;
   const av = operandView('__KERNEL___av', views.a, batchDims, M, K);
   const bv = operandView('__KERNEL___bv', views.b, bs.slice(0, -2), K, N);
+  const tl = gemmTiling(batch, M, N, K, o.tuning, av.mode === 1);
+  const T = tl.T;
+  const split = tl.chunks > 1;
   const sizes = o.sizes || {};
   const need = { a: sizes.a !== undefined ? sizes.a : batch * M * K, b: sizes.b !== undefined ? sizes.b : batch * K * N };
   if (av.limit > need.a || bv.limit > need.b) throw new Error(`matmul operand view out of bounds (${av.limit}/${need.a}, ${bv.limit}/${need.b})`);
@@ -739,7 +771,7 @@ ${indent(lines, '    ')}
 };
 `;
   const main = `extern "C" __global__ void __launch_bounds__(256) __KERNEL__(const TcmiArgs A) {
-  tcmi::gemm_f32<${T}, ${T}, ${av.mode}, ${bv.mode}, ${split}, __KERNEL___av, __KERNEL___bv, __KERNEL___epi>(A, A.in[${ia}], A.in[${ib}],
+  tcmi::gemm_f32<${T}, ${T}, ${tl.bk}, ${av.mode}, ${bv.mode}, ${split}, __KERNEL___av, __KERNEL___bv, __KERNEL___epi>(A, A.in[${ia}], A.in[${ib}],
       ${batch}u, ${M}u, ${K}u, ${N}u, ${tl.chunks}u, ${tl.chunkK}u);
 }
 `;

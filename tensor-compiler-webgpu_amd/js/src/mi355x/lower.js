@@ -53,7 +53,7 @@ function algorithmicBytes(graph, node) {
 }
 
 function single(k) {
-  const kernels = k.kernels || [{ name: k.name, source: k.source, grid: k.grid, block: k.block, lds: k.lds }];
+  const kernels = k.kernels || [{ name: k.name, source: k.source, grid: k.grid, block: k.block, lds: k.lds, needsPad: !!k.needsPad }];
   return { kernels, params: k.params, workspace: k.workspace || 0, flops: k.flops || 0 };
 }
 

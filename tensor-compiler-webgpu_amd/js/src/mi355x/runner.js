@@ -106,6 +106,17 @@ function sharing(lowered) {
   return { alias, folded: new Set(lowered.folded || []) };
 }
 
+/**
+ * Refuse a launch list with a kernel that reads and writes one element past its
+ * buffers (the off-by-one sabotage) unless every buffer carries a canary pad.
+ */
+function requirePad(lowered, padded) {
+  if (padded) return;
+  for (const l of lowered.launches) for (const k of l.kernels) {
+    if (k.needsPad) throw new Error(`launch of node ${l.node} (${k.name}) runs past its buffers: run it with canaries`);
+  }
+}
+
 function constData(node) {
   const n = size(node.shape);
   const v = node.attrs.value;
@@ -179,6 +190,7 @@ class HipRunner {
   async run(graph, lowered, inputs, options) {
     const canary = !!(options && options.canary);
     if (this.a.lost()) throw new Error('device lost');
+    requirePad(lowered, canary);
     const a = this.a;
     const fns = this.functions(lowered);
     const n = graph.nodes.map((node) => size(node.shape));
@@ -228,13 +240,14 @@ class HipRunner {
   async runLocal(graph, lowered, values, options) {
     const canary = !!(options && options.canary);
     const a = this.a;
+    requirePad(lowered, canary);
     const fns = this.functions(lowered);
     const n = graph.nodes.map((node) => size(node.shape));
     const ref = [], outs = new Map();
     let ws = 0;
     try {
       for (const node of graph.nodes) {
-        const h = this.alloc(n[node.id] * 4);
+        const h = this.alloc((n[node.id] + (canary ? CANARY_PAD : 0)) * 4);
         ref.push(h);
         a.h2d(h, 0, Float32Array.from(values[node.id]));
       }
@@ -275,6 +288,7 @@ class HipRunner {
 
 class Program {
   constructor(runner, graph, lowered, { only, buffers } = {}) {
+    requirePad(lowered, false);
     const a = runner.a;
     this.a = a;
     this.graph = graph;
