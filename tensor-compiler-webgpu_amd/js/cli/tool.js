@@ -138,6 +138,12 @@ function gemmModes(l) {
   return m ? [Number(m[1]), Number(m[2])] : null;
 }
 
+/** The K split (chunks, chunk length) of a matmul launch's kernel, or null. */
+function gemmSplit(l) {
+  const m = l.kernels[0].source.match(/(\d+)u, (\d+)u\);\s*}\s*$/);
+  return l.flops && m ? [Number(m[1]), Number(m[2])] : null;
+}
+
 /** The reference's four kernel sabotages (codegen-fused.js:22), as lowerMI355X applies them. */
 const KERNEL_SABOTAGES = ['epilogue-before-bias', 'layernorm-tree-short', 'softmax-no-max', 'fused-bounds-off-by-one'];
 
@@ -585,8 +591,10 @@ async function main() {
         keep = req.keep || [];
       }
       const l = lowerMI355X(g, { perf: true, keep });
+      const plain = new Map(lowerMI355X(g).launches.map((x) => [x.node, x]));
       out = { graph: g.toJSON(), keep, aliases: l.aliases, folded: l.folded,
-        launches: l.launches.map((x) => ({ node: x.node, kind: x.kind, inputs: x.inputs, views: x.views || null, modes: gemmModes(x) })) };
+        launches: l.launches.map((x) => ({ node: x.node, kind: x.kind, inputs: x.inputs, views: x.views || null, modes: gemmModes(x),
+          split: gemmSplit(x), plainSplit: gemmSplit(plain.get(x.node)) })) };
       break;
     }
     case 'precompile': out = { kernels: precompileGroup(req.group || 'direct', req.arch) }; break;

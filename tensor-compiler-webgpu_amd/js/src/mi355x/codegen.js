@@ -653,20 +653,26 @@ function colreduceKernels(op, outer, n, inner, tuning) {
  *     short K is never split (the partial-sum traffic costs more than it saves);
  *   - bk = 64 for T = 1, 32 for T = 2, 16 for T = 4 (the deeper slice feeds the
  *     small tiles more work per round trip to memory).
+ * The split — the only choice that changes the order of the K sum, hence the
+ * bits — depends on (batch, M, N, K) alone (it is set from the tile the rules
+ * give without the layout exception), so a matmul gives the same bits whether
+ * its operands are materialised or read through views.
  * `aTransposed`: A is read through a view whose rows are contiguous (MODE_R).
  */
 function gemmTiling(batch, M, N, K, tuning, aTransposed) {
   const t = tuning || {};
   const blocks = (T) => batch * Math.ceil(M / (32 * T)) * Math.ceil(N / (32 * T));
   const longK = K >= 2048;
-  let T;
-  if (t.tile) T = t.tile;
-  else if (M >= 128 && N >= 128 && blocks(4) >= 256 && !(aTransposed && blocks(2) >= 512)) T = 4;
-  else if (M >= 64 && N >= 64 && (blocks(2) >= 256 || longK)) T = 2;
-  else T = 1;
+  const tileFor = (transposed) => {
+    if (M >= 128 && N >= 128 && blocks(4) >= 256 && !(transposed && blocks(2) >= 512)) return 4;
+    if (M >= 64 && N >= 64 && (blocks(2) >= 256 || longK)) return 2;
+    return 1;
+  };
+  const T = t.tile || tileFor(!!aTransposed);
+  const T0 = t.tile || tileFor(false);
   let chunks = 1;
   if (t.splitk !== undefined) chunks = t.splitk;
-  else if (longK && blocks(T) < 512) chunks = Math.max(1, Math.min(Math.ceil(1024 / blocks(T)), Math.floor(K / 256), 32));
+  else if (longK && blocks(T0) < 512) chunks = Math.max(1, Math.min(Math.ceil(1024 / blocks(T0)), Math.floor(K / 256), 32));
   let chunkK = Math.ceil(Math.ceil(K / chunks) / 16) * 16;
   chunks = Math.ceil(K / chunkK);
   const bk = t.bk || (T === 1 ? 64 : T === 2 ? 32 : 16);

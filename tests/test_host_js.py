@@ -226,3 +226,18 @@ def test_perf_lowering_views_address_the_operands(tool, req):
             checked += 1
     if req["model"] != "mlp":
         assert checked > 10
+    # Every matmul splits K exactly as in the plain lowering (the same order of the K sum).
+    for l in d["launches"]:
+        assert l["split"] == l["plainSplit"], (l["node"], l["split"], l["plainSplit"])
+
+
+def test_perf_lowering_keeps_the_split_of_config4_backward(tool):
+    """Config 4's gradient graphs at full size: the transposed weight-gradient matmuls read in
+    place keep the plain lowering's K split, so their bits are the same."""
+    graphs = tool("config-graphs", {"c4": [{"act": "relu", "M": M, "K": K, "N": N}
+                                           for M, K, N in ((512, 512, 512), (4096, 4096, 4096), (8192, 1024, 4096))]})["c4"]
+    for g in graphs:
+        d = tool("perf-lower", {"graph": g["gradient"]["graph"], "keep": g["gradient"]["keep"]})
+        assert len(d["folded"]) == 2
+        for l in d["launches"]:
+            assert l["split"] == l["plainSplit"], (g["M"], g["K"], g["N"], l["node"])
