@@ -6,6 +6,9 @@
 //   node bench.js [--configs ceiling,c2,c3,c4] [--steps K] [--warmup W] [--programs P]
 //                 [--reps N] [--c4-shapes all|small] [--quick] [--graphs] [--step-only]
 //
+// --step-only (for profilers): c2 runs its headline step only; c3 and c4 run each
+// fused program --steps times after --warmup runs, with no timing loops.
+//
 // c2  fused elementwise chains (P programs, forward + gradient) over [8192, 1024]:
 //     the headline step = every fused program run once; K timed steps
 //     bracketed by a sync and hipEvents on both sides.
@@ -179,17 +182,42 @@ function c2(runner, bench, opts) {
     stepBytes, gbs: stepBytes / ((ms / K) * 1e6), dominant: stepOnly ? null : dominant(all), results };
 }
 
+/**
+ * Profiling mode (--step-only): the fused program of `graph` in the perf lowering
+ * run `--steps` times after `--warmup` runs, nothing else timed, so a profiler
+ * sees each of its kernels a known number of times. Returns every launch's kernel
+ * names with its algorithmic bytes and flops.
+ */
+function runOnly(runner, name, graph, keep, inputs) {
+  const K = Number(arg('steps', 20)), W = Number(arg('warmup', 3));
+  const f = fuse(graph, { keep });
+  const lf = lowerMI355X(f.graph, { perf: true, keep: keep.map((id) => f.index.get(id)) });
+  runner.functions(lf);
+  const p = prepared(runner, f.graph, lf, inputs);
+  for (let i = 0; i < W + K; i++) p.run();
+  p.sync();
+  p.destroy();
+  return { name, runs: W + K, launches: lf.launches.map((l) => ({ node: l.node, kind: l.kind, pattern: l.pattern || null,
+    kernels: l.kernels.map((k) => k.name), bytes: l.bytes, flops: l.flops || 0 })) };
+}
+
 function c3(runner, bench, opts) {
   const R = opts.quick ? 2048 : cfg.C3_SHAPE[0], C = cfg.C3_SHAPE[1];
   const { x, dy, shifted } = cfg.c3Inputs(R, C);
   const results = [];
   for (const fn of ['softmax', 'logSoftmax']) {
     const g = cfg.c3Graphs(fn, R, C);
+    if (flag('step-only')) {
+      results.push(runOnly(runner, `c3-${fn}-forward`, g.forward.graph, g.forward.keep, { x }));
+      results.push(runOnly(runner, `c3-${fn}-backward`, g.gradient.graph, g.gradient.keep, { x, d0: dy }));
+      continue;
+    }
     log(`c3 ${fn} forward`);
     results.push(measureGraph(runner, bench, `c3-${fn}-forward`, g.forward.graph, g.forward.keep, { x }, { reps: opts.reps }));
     log(`c3 ${fn} backward`);
     results.push(measureGraph(runner, bench, `c3-${fn}-backward`, g.gradient.graph, g.gradient.keep, { x, d0: dy }, { reps: opts.reps }));
   }
+  if (flag('step-only')) return { config: 'c3', shape: [R, C], results };
   const all = [].concat.apply([], results.map((r) => r.launchF));
   const bytes = results.reduce((s, r) => s + r.bytes.fused, 0);
   const us = results.reduce((s, r) => s + r.fused.median, 0);
@@ -203,6 +231,11 @@ function c4(runner, bench, opts) {
     const { X, W, bias, dY } = cfg.c4Inputs(M, K, N);
     for (const act of ['relu', 'tanh']) {
       const g = cfg.c4Graphs(act, M, K, N);
+      if (flag('step-only')) {
+        results.push(runOnly(runner, `c4-${M}x${K}x${N}-${act}-forward`, g.forward.graph, g.forward.keep, { X, W, bias }));
+        results.push(runOnly(runner, `c4-${M}x${K}x${N}-${act}-backward`, g.gradient.graph, g.gradient.keep, { X, W, bias, d0: dY }));
+        continue;
+      }
       log(`c4 ${M}x${K}x${N} ${act} forward`);
       results.push(measureGraph(runner, bench, `c4-${M}x${K}x${N}-${act}-forward`, g.forward.graph, g.forward.keep,
         { X, W, bias }, { reps: opts.reps || 16 }));
@@ -211,6 +244,7 @@ function c4(runner, bench, opts) {
         { X, W, bias, d0: dY }, { reps: opts.reps || 8 }));
     }
   }
+  if (flag('step-only')) return { config: 'c4', shapes, results };
   const mm = [].concat.apply([], results.map((r) => r.launchF)).filter((l) => l.flops);
   return { config: 'c4', shapes, dominant: dominant(mm), results };
 }
