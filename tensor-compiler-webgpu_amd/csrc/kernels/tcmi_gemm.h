@@ -11,11 +11,20 @@
 // head split) is read in place instead of being materialised first. The load
 // path per operand (MODE) follows its layout:
 //   MODE_C  c contiguous (SC = 1): 128-bit loads along c (the row-major case)
-//   MODE_R  r contiguous (SR = 1): 128-bit loads along r (the transposed case),
-//           scattered into the LDS tile as four 32-bit writes
+//   MODE_R  r contiguous (SR = 1): 128-bit loads along r (the transposed case)
 //   MODE_S  anything else: one 32-bit load per element
 // (for A, r is the output row and c the K index; for B, r is K and c the
-// output column).
+// output column). The LDS tile keeps the layout of the loads, so every
+// 128-bit load is one 128-bit LDS store, and the reads adapt instead:
+//   A row-major  As[row][k]: a lane's 4 k values in one ds_read_b128
+//   A k-major    As[k][row]: 4 ds_read_b32 (MODE_R)
+//   B k-major    Bs[k][col]: one ds_read_b32 per k
+//   B col-major  Bs[col][k]: a lane's 4 k values in one ds_read_b128 (MODE_R)
+// Every tile's row stride is padded by 4 floats, which puts the four lane
+// groups q of a read (or the 16 lanes of a 128-bit read) on disjoint banks.
+// (Storing a transposed tile in the other layout would scatter each 128-bit
+// load into four 32-bit LDS writes that collide on the same banks; measured
+// on the MI355X, that stalled LDS for a third of the kernel's time.)
 //
 // Tiling: a workgroup of 256 threads (4 wavefronts in a 2 x 2 grid) owns a
 // BM x BN tile of C; each wavefront owns (TM·16) x (TN·16) of it as TM x TN
@@ -68,10 +77,12 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
   constexpr int BM = 2 * TM * 16;
   constexpr int BN = 2 * TN * 16;
   static_assert(BK == 16 || BK == 32 || BK == 64, "slice depth");
-  constexpr int AS = BK + 4;   // padded row stride of the A slice (conflict-free b128 reads)
-  constexpr int BS = BN + 4;   // padded row stride of the B slice
-  __shared__ __attribute__((aligned(16))) float As[2][BM * AS];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BK * BS];
+  constexpr bool A_KMAJOR = AMODE == MODE_R;   // As[k][row] instead of As[row][k]
+  constexpr bool B_NMAJOR = BMODE == MODE_R;   // Bs[col][k] instead of Bs[k][col]
+  constexpr int AS = A_KMAJOR ? BM + 4 : BK + 4;   // padded row stride of the A tile
+  constexpr int BS = B_NMAJOR ? BK + 4 : BN + 4;   // padded row stride of the B tile
+  __shared__ __attribute__((aligned(16))) float As[2][(A_KMAJOR ? BK : BM) * AS];
+  __shared__ __attribute__((aligned(16))) float Bs[2][(B_NMAJOR ? BN : BK) * BS];
 
   const uint32_t kz = SPLIT ? blockIdx.z % chunks : 0u;
   const uint32_t bz = SPLIT ? blockIdx.z / chunks : blockIdx.z;
@@ -177,10 +188,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
         const int t = tid + v * 256;
         if (t < BM * BK / 4) {
           const int kk = t / (BM / 4), row = (t % (BM / 4)) * 4;
-          As[buf][(row + 0) * AS + kk] = ra[v].x;
-          As[buf][(row + 1) * AS + kk] = ra[v].y;
-          As[buf][(row + 2) * AS + kk] = ra[v].z;
-          As[buf][(row + 3) * AS + kk] = ra[v].w;
+          *reinterpret_cast<float4*>(&As[buf][kk * AS + row]) = ra[v];
         }
       }
     } else {
@@ -205,10 +213,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
         const int t = tid + v * 256;
         if (t < BK * BN / 4) {
           const int c = t / (BK / 4), kk = (t % (BK / 4)) * 4;
-          Bs[buf][(kk + 0) * BS + c] = rb[v].x;
-          Bs[buf][(kk + 1) * BS + c] = rb[v].y;
-          Bs[buf][(kk + 2) * BS + c] = rb[v].z;
-          Bs[buf][(kk + 3) * BS + c] = rb[v].w;
+          *reinterpret_cast<float4*>(&Bs[buf][c * BS + kk]) = rb[v];
         }
       }
     } else {
@@ -238,13 +243,28 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
       // A values of this lane for every row tile: k = 16g + 4q .. 16g + 4q + 3 of the slice.
       float4 av[TM];
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-        av[i] = *reinterpret_cast<const float4*>(&As[cur][(wm * TM * 16 + i * 16 + t16) * AS + 16 * g + 4 * q]);
+      for (int i = 0; i < TM; ++i) {
+        const int row = wm * TM * 16 + i * 16 + t16;
+        if (A_KMAJOR) {
+          const float* a = &As[cur][(16 * g + 4 * q) * AS + row];
+          av[i] = make_float4(a[0], a[AS], a[2 * AS], a[3 * AS]);
+        } else {
+          av[i] = *reinterpret_cast<const float4*>(&As[cur][row * AS + 16 * g + 4 * q]);
+        }
+      }
+      // B values of a column-major tile: the same 4 k values of each column tile at once.
+      float4 bq[B_NMAJOR ? TN : 1];
+      if (B_NMAJOR) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          bq[j] = *reinterpret_cast<const float4*>(&Bs[cur][(wn * TN * 16 + j * 16 + t16) * BS + 16 * g + 4 * q]);
+      }
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         float bv[TN];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) bv[j] = Bs[cur][(16 * g + 4 * q + s) * BS + wn * TN * 16 + j * 16 + t16];
+        for (int j = 0; j < TN; ++j)
+          bv[j] = B_NMAJOR ? lane4(bq[j], s) : Bs[cur][(16 * g + 4 * q + s) * BS + wn * TN * 16 + j * 16 + t16];
 #pragma unroll
         for (int i = 0; i < TM; ++i) {
           const float a = lane4(av[i], s);

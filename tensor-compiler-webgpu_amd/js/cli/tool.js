@@ -16,7 +16,7 @@
 //   config-graphs    request {c3: [{fn, R, C}], c4: [{act, M, K, N}]} -> forward and gradient graphs of configs 3 and 4
 // GPU commands write a bundle (manifest.json + data.f32) under --out:
 //   gpu-direct       request {sabotage?}: every direct case, fused, canary-padded, on the GPU
-//   gpu-graphs       request {graphs: [{name, graph, inputs, keep, unfused?}]} fused (and unfused) on the GPU
+//   gpu-graphs       request {graphs: [{name, graph, inputs, keep, unfused?, perf?}]} fused (and unfused, and in the perf lowering) on the GPU
 //   gpu-configs      request {c3: [...], c4: [...], unfused} configs 3 and 4, kept outputs as oracle-computable slices
 
 const fs = require('fs');
@@ -187,6 +187,17 @@ async function gpuGraphs(req, dir) {
     const rf = await runner.run(f.graph, lf, inputs, { canary: true });
     const entry = { name: c.name, fused: f.graph.toJSON(), origin: f.origin, gpuFused: {}, canaryFused: rf.canaryIntact };
     f.graph.nodes.forEach((n) => { entry.gpuFused[n.id] = bundle.put(rf.values[n.id]); });
+    if (c.perf) {
+      // The perf lowering: transposes read in place by the matmuls, reshapes sharing buffers.
+      const keepF = (c.keep || []).map((id) => f.index.get(id));
+      const lp = lowerMI355X(f.graph, { perf: true, keep: keepF });
+      const rp = await runner.run(f.graph, lp, inputs, { canary: true });
+      entry.gpuPerf = {};
+      for (const id of keepF) entry.gpuPerf[id] = bundle.put(rp.values[id]);
+      entry.perfFolded = lp.folded;
+      entry.perfModes = lp.launches.filter((l) => l.flops).map(gemmModes);
+      entry.canaryPerf = rp.canaryIntact.every(Boolean);
+    }
     if (c.unfused) {
       const lu = lowerMI355X(g);
       const ru = await runner.run(g, lu, inputs, { canary: true });
