@@ -642,9 +642,7 @@ function colreduceKernels(op, outer, n, inner, tuning) {
  * Tiling of a matmul: MFMA tiles per wavefront (T: the workgroup owns 32T x 32T
  * of the output), K chunks (split-K) and the LDS slice depth (bk). Rules, from
  * a sweep of every (T, bk, chunks) on the MI355X over the configs' shapes:
- *   - T = 4 when M, N >= 128 and that still gives the 256 CUs a workgroup each,
- *     except for an A operand read transposed (MODE_R) when T = 2 gives two
- *     workgroups per CU (its scattered LDS stores cost more at T = 4);
+ *   - T = 4 when M, N >= 128 and that still gives the 256 CUs a workgroup each;
  *     T = 2 when that gives every CU a workgroup (or when K is long, see below);
  *     T = 1 otherwise;
  *   - K is split only when it is long (>= 2048) and the output leaves fewer than
@@ -653,26 +651,22 @@ function colreduceKernels(op, outer, n, inner, tuning) {
  *     short K is never split (the partial-sum traffic costs more than it saves);
  *   - bk = 64 for T = 1, 32 for T = 2, 16 for T = 4 (the deeper slice feeds the
  *     small tiles more work per round trip to memory).
- * The split — the only choice that changes the order of the K sum, hence the
- * bits — depends on (batch, M, N, K) alone (it is set from the tile the rules
- * give without the layout exception), so a matmul gives the same bits whether
- * its operands are materialised or read through views.
- * `aTransposed`: A is read through a view whose rows are contiguous (MODE_R).
+ * Every choice depends on (batch, M, N, K) alone, not on the operands' layouts,
+ * so a matmul gives the same bits (the split fixes the order of the K sum)
+ * whether its operands are materialised or read through views.
  */
-function gemmTiling(batch, M, N, K, tuning, aTransposed) {
+function gemmTiling(batch, M, N, K, tuning) {
   const t = tuning || {};
   const blocks = (T) => batch * Math.ceil(M / (32 * T)) * Math.ceil(N / (32 * T));
   const longK = K >= 2048;
-  const tileFor = (transposed) => {
-    if (M >= 128 && N >= 128 && blocks(4) >= 256 && !(transposed && blocks(2) >= 512)) return 4;
-    if (M >= 64 && N >= 64 && (blocks(2) >= 256 || longK)) return 2;
-    return 1;
-  };
-  const T = t.tile || tileFor(!!aTransposed);
-  const T0 = t.tile || tileFor(false);
+  let T;
+  if (t.tile) T = t.tile;
+  else if (M >= 128 && N >= 128 && blocks(4) >= 256) T = 4;
+  else if (M >= 64 && N >= 64 && (blocks(2) >= 256 || longK)) T = 2;
+  else T = 1;
   let chunks = 1;
   if (t.splitk !== undefined) chunks = t.splitk;
-  else if (longK && blocks(T0) < 512) chunks = Math.max(1, Math.min(Math.ceil(1024 / blocks(T0)), Math.floor(K / 256), 32));
+  else if (longK && blocks(T) < 512) chunks = Math.max(1, Math.min(Math.ceil(1024 / blocks(T)), Math.floor(K / 256), 32));
   let chunkK = Math.ceil(Math.ceil(K / chunks) / 16) * 16;
   chunks = Math.ceil(K / chunkK);
   const bk = t.bk || (T === 1 ? 64 : T === 2 ? 32 : 16);
@@ -762,7 +756,7 @@ function gemmKernel(b, output, opts) {
   }
   const av = operandView('__KERNEL___av', views.a, batchDims, M, K);
   const bv = operandView('__KERNEL___bv', views.b, bs.slice(0, -2), K, N);
-  const tl = gemmTiling(batch, M, N, K, o.tuning, av.mode === 1);
+  const tl = gemmTiling(batch, M, N, K, o.tuning);
   const T = tl.T;
   const split = tl.chunks > 1;
   const sizes = o.sizes || {};
