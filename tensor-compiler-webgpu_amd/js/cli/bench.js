@@ -267,21 +267,18 @@ function trainStep(runner, bench, name, req, opts) {
   runner.functions([fs.lowered, lu]);
   const K = Number(arg('train-steps', opts.quick ? 3 : 10)), W = 2;
   const batch = m.batch(0);
-  const trainer = new HipTrainer(runner, fs, m.params, m.state);
+  const trainer = new HipTrainer(runner, fs, m.params, m.state, { graph: bench.graphs });
   for (let i = 0; i < W; i++) trainer.train(batch.x, batch.y);
   const t0 = process.hrtime.bigint();
   let loss = 0;
   for (let i = 0; i < K; i++) loss = trainer.train(batch.x, batch.y);
   const wallMs = Number(process.hrtime.bigint() - t0) / 1e6 / K;
-  // Batch resident: launches + feedback only, K steps between two events.
-  const p = trainer.program;
+  // Batch resident: the steps' launches only, K steps between two events.
   runner.a.sync();
   runner.a.eventRecord(bench.start);
-  for (let i = 0; i < K; i++) {
-    p.run();
-    for (const [from, to, bytes] of trainer.feedback) runner.a.d2d(to, 0, from, 0, bytes);
-  }
+  for (let i = 0; i < K; i++) trainer.advance();
   runner.a.eventRecord(bench.end);
+  const p = trainer.program;
   const residentMs = runner.a.eventElapsed(bench.start, bench.end) / K;
   // Unfused step (same graph, no fusion), batch resident.
   const pu = runner.prepare(m.step.graph, lu);

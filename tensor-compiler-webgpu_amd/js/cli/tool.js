@@ -491,7 +491,7 @@ async function gpuTrain(req) {
   const m = modelStep(req);
   const fs = fusedStep(m.step);
   const runner = HipRunner.create();
-  const trainer = new HipTrainer(runner, fs, m.params, m.state);
+  const trainer = new HipTrainer(runner, fs, m.params, m.state, { graph: !!req.graph });
   const losses = [];
   let identical = null;
   const names = Object.keys(Object.assign({}, m.params, m.state));

@@ -5,11 +5,17 @@
 //
 // fusedStep(step) fuses a step graph keeping the loss, the logits and every
 // new parameter and state value, renumbers the step's ids into the fused graph
-// and lowers it. HipTrainer makes every buffer, constant and packed launch
-// once; train(x, y) writes the batch, enqueues every launch, copies each new
-// parameter/state value back into its input buffer on the device, and reads
-// back only the loss (one sync per step). read(names) returns current values;
-// destroy() frees everything.
+// and lowers it (the perf lowering, and the plain one for node-by-node checks).
+//
+// HipTrainer makes every buffer, constant and packed launch once. Where the
+// reference copies each new parameter back onto its input buffer after every
+// step (trainer-fused.js:72), this trainer keeps two programs over the same
+// buffers with each parameter's input and output buffers exchanged: step t
+// runs program t mod 2, which reads the parameters the previous step wrote, so
+// a step is its launches alone — no copies — and, with `graph`, the replay of
+// one captured HIP graph. train(x, y) writes the batch, enqueues the step and
+// reads back only the loss (one sync per step); read(names) returns current
+// values; destroy() frees everything.
 
 const { fuse } = require('../fusion/fuse');
 const { lowerMI355X } = require('./lower');
@@ -38,43 +44,63 @@ function fusedStep(step, options) {
 }
 
 class HipTrainer {
-  /** `step` from fusedStep (or an unfused step with `lowered`); `params`/`state` map names to values. */
-  constructor(runner, step, params, state) {
+  /**
+   * `step` from fusedStep (or an unfused step with `lowered`); `params`/`state`
+   * map names to values; options.graph: replay each step as a captured HIP graph.
+   */
+  constructor(runner, step, params, state, options) {
     this.runner = runner;
     this.a = runner.a;
     this.step = step;
-    this.program = runner.prepare(step.graph, step.lowered);
-    const p = this.program;
+    this.graph = !!(options && options.graph);
+    const first = runner.prepare(step.graph, step.lowered);
     const cot = step.graph.inputId(step.cotangent);
     if (cot === undefined) throw new Error(`the step has no cotangent input '${step.cotangent}'`);
-    p.write(cot, new Float32Array([1]));
+    first.write(cot, new Float32Array([1]));
     const all = Object.assign({}, params, state || {});
-    for (const name of Object.keys(all)) {
-      if (step.inputs[name] === undefined) throw new Error(`the step has no input '${name}'`);
-      p.write(step.inputs[name], all[name]);
-    }
     this.names = Object.keys(all);
-    this.feedback = this.names.map((name) => {
+    // The second program: every parameter's input and output buffers exchanged,
+    // and the nodes sharing a buffer (aliases) re-pointed at the exchanged one.
+    const bufs = first.bufs.slice();
+    for (const name of this.names) {
       const from = step.outputs[name], to = step.inputs[name];
+      if (to === undefined) throw new Error(`the step has no input '${name}'`);
       if (from === undefined) throw new Error(`the step has no output for '${name}'`);
-      return [p.bufs[from], p.bufs[to], p.n[to] * 4];
-    });
+      if (from === to) throw new Error(`'${name}' is its own output`);
+      first.write(to, all[name]);
+      bufs[to] = first.bufs[from];
+      bufs[from] = first.bufs[to];
+    }
+    for (const [node, source] of step.lowered.aliases || []) bufs[node] = bufs[source];
+    const second = runner.prepare(step.graph, step.lowered, { buffers: bufs });
+    this.programs = [first, second];
+    this.turn = 0;   // the program the next step runs; its parameter inputs hold the current values
     this.lossBuf = new Float32Array(1);
   }
 
-  /** Enqueue one step (no sync): batch, every launch, the feedback copies. */
+  /** The program the next step runs. */
+  get program() { return this.programs[this.turn]; }
+
+  /** Enqueue one step on the resident batch (no sync): every launch, then the buffers' roles swap. */
+  advance() {
+    const p = this.programs[this.turn];
+    if (this.graph) p.replay(); else p.run();
+    this.lossAt = p.bufs[this.step.loss];
+    this.turn ^= 1;
+  }
+
+  /** Enqueue one step (no sync): the batch, then every launch. */
   enqueue(x, y) {
-    const { step, program: p } = this;
-    p.write(step.inputs.x, x);
-    p.write(step.inputs.y, y);
-    p.run();
-    for (const [from, to, bytes] of this.feedback) this.a.d2d(to, 0, from, 0, bytes);
+    const p = this.programs[this.turn];
+    p.write(this.step.inputs.x, x);
+    p.write(this.step.inputs.y, y);
+    this.advance();
   }
 
   /** One training step; returns the loss computed from the parameters before the update. */
   train(x, y) {
     this.enqueue(x, y);
-    this.a.d2h(this.program.bufs[this.step.loss], 0, this.lossBuf);
+    this.a.d2h(this.lossAt, 0, this.lossBuf);
     return this.lossBuf[0];
   }
 
@@ -84,7 +110,10 @@ class HipTrainer {
     return out;
   }
 
-  destroy() { this.program.destroy(); }
+  destroy() {
+    this.programs[1].destroy();
+    this.programs[0].destroy();
+  }
 }
 
 module.exports = { fusedStep, HipTrainer };

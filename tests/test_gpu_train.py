@@ -87,12 +87,16 @@ def test_c1_first_step_against_composed_budget(tool):
     assert j["pass"], j["first"]
 
 
-def test_c1_trainer_consistency_and_learning(tool):
+@pytest.mark.parametrize("graph", [False, True])
+def test_c1_trainer_consistency_and_learning(tool, graph):
     """20 fused-trainer steps on one batch: each equals the checked path (runner.run of the
     plain lowering, one launch per node, with the new values fed back by the host) bit for
     bit — the trainer runs the perf lowering, whose matmuls read transposed operands in
-    place — and the loss falls at every step."""
-    r = tool("gpu-train", {"model": "mlp", "steps": 20, "consistency": True, "consistencySteps": 20, "sameBatch": True})
+    place — and the loss falls at every step. With `graph`, each step is the replay of a
+    captured HIP graph (two graphs, the parameters' buffers exchanging roles), and every
+    replay is checked against the eager path, with the host's synchronisation between."""
+    r = tool("gpu-train", {"model": "mlp", "steps": 20, "consistency": True, "consistencySteps": 20, "sameBatch": True,
+                           "graph": graph})
     assert r["identical"] is True
     losses = r["losses"]
     assert all(np.isfinite(losses))
@@ -101,13 +105,14 @@ def test_c1_trainer_consistency_and_learning(tool):
     assert losses[-1] < losses[0] - 0.2, losses
 
 
-def test_c5_full_size_trainer(tool):
-    """Config 5 at full size (B 64): the fused trainer's first 2 steps (perf lowering: 88
+@pytest.mark.parametrize("graph", [False, True])
+def test_c5_full_size_trainer(tool, graph):
+    """Config 5 at full size (B 64): the fused trainer's first 3 steps (perf lowering: 88
     transposes read in place by their matmuls, 37 reshapes sharing buffers) equal the checked
     path (plain lowering) bit for bit, and the initial loss is near ln(96) (small initial
     weights, uniform tokens)."""
-    r = tool("gpu-train", {"model": "transformer", "B": 64, "steps": 2, "consistency": True, "consistencySteps": 2},
-             timeout=600)
+    r = tool("gpu-train", {"model": "transformer", "B": 64, "steps": 3, "consistency": True, "consistencySteps": 3,
+                           "graph": graph}, timeout=600)
     assert r["identical"] is True
     assert r["folded"] > 0 and r["aliases"] > 0 and r["launches"] < r["checkedLaunches"]
     assert abs(r["losses"][0] - np.log(96)) < 0.1, r["losses"]
