@@ -38,6 +38,9 @@
 // Operand layout per lane of a 16x16x4 MFMA (lane = 16·q + t, t in 0..15):
 //   A value: row t, k-group q;  B value: column t, k-group q;
 //   D: column t, rows 4q .. 4q+3 (one per accumulator register).
+// The kernel passes the B value as the MFMA's first operand and the A value as
+// its second, so each 16 x 16 accumulator holds its output tile transposed:
+// lane (t, q) has row t, columns 4q .. 4q+3 — four consecutive outputs.
 // Within each 16-wide part of a slice, lane group q supplies k = 4q + s at step
 // s, so a lane's four A values of a part are contiguous in LDS (one ds_read_b128);
 // both operands use the same k for the same (q, s), so the product is exact
@@ -69,7 +72,7 @@ struct DenseView {
 // epilogue. MODE_C needs C % 4 == 0 and MODE_R needs R % 4 == 0 (R, C: the
 // operand's extents), and both need every other stride a multiple of 4, so a
 // 128-bit load is aligned and either wholly inside the operand or wholly out.
-template <int TM, int TN, int BK, int AMODE, int BMODE, bool SPLIT, class AV, class BV, class Epi>
+template <int TM, int TN, int BK, int PF, int AMODE, int BMODE, bool SPLIT, class AV, class BV, class Epi>
 __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restrict__ a_ptr,
                                          const float* __restrict__ b_ptr, const uint32_t batch, const uint32_t M,
                                          const uint32_t K, const uint32_t N, const uint32_t chunks,
@@ -77,6 +80,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
   constexpr int BM = 2 * TM * 16;
   constexpr int BN = 2 * TN * 16;
   static_assert(BK == 16 || BK == 32 || BK == 64, "slice depth");
+  static_assert(PF == 1 || PF == 2, "prefetch depth");
   constexpr bool A_KMAJOR = AMODE == MODE_R;   // As[k][row] instead of As[row][k]
   constexpr bool B_NMAJOR = BMODE == MODE_R;   // Bs[col][k] instead of Bs[k][col]
   constexpr int AS = A_KMAJOR ? BM + 4 : BK + 4;   // padded row stride of the A tile
@@ -104,12 +108,22 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
   constexpr int A_SC = (BM * BK + 255) / 256;        // scalar loads per thread
   constexpr int B_SC = (BK * BN + 255) / 256;
   constexpr bool VA = AMODE != MODE_S, VB = BMODE != MODE_S;
-  float4 ra[VA ? A_VEC : 1];
-  float4 rb[VB ? B_VEC : 1];
-  float sa[VA ? 1 : A_SC];
-  float sb[VB ? 1 : B_SC];
+  // Staging registers for a slice in flight: one set, or two for PF = 2 (the
+  // global loads of slice k + 2 are issued while slice k is computed, so each
+  // load has two slices' compute to arrive before it is stored to LDS).
+  struct Stage {
+    float4 ra[VA ? A_VEC : 1];
+    float4 rb[VB ? B_VEC : 1];
+    float sa[VA ? 1 : A_SC];
+    float sb[VB ? 1 : B_SC];
+  };
+  Stage st0, st1;
 
-  auto load_slice = [&](uint32_t k0) {
+  auto load_slice = [&](Stage& S, uint32_t k0) {
+    float4* ra = S.ra;
+    float4* rb = S.rb;
+    float* sa = S.sa;
+    float* sb = S.sb;
     if (AMODE == MODE_C) {
 #pragma unroll
       for (int v = 0; v < A_VEC; ++v) {
@@ -172,7 +186,11 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
     }
   };
 
-  auto store_slice = [&](int buf) {
+  auto store_slice = [&](const Stage& S, int buf) {
+    const float4* ra = S.ra;
+    const float4* rb = S.rb;
+    const float* sa = S.sa;
+    const float* sb = S.sb;
     if (AMODE == MODE_C) {
 #pragma unroll
       for (int v = 0; v < A_VEC; ++v) {
@@ -231,13 +249,11 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
-  const uint32_t slices = (kend - kbeg + BK - 1) / BK;
-  load_slice(kbeg);
-  store_slice(0);
-  __syncthreads();
-  for (uint32_t ks = 0; ks < slices; ++ks) {
-    const int cur = ks & 1;
-    if (ks + 1 < slices) load_slice(kbeg + (ks + 1) * BK);
+  // One K slice from LDS buffer `cur` into the accumulators. The MFMA takes the
+  // B value as its first operand and the A value as its second, so it computes
+  // the tile transposed: lane (t16, q) holds row t16, columns 4q .. 4q+3 of each
+  // 16 x 16 output tile — four consecutive outputs, stored with one 128-bit write.
+  auto compute = [&](const int cur) {
 #pragma unroll
     for (int g = 0; g < BK / 16; ++g) {
       // A values of this lane for every row tile: k = 16g + 4q .. 16g + 4q + 3 of the slice.
@@ -269,25 +285,58 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
         for (int i = 0; i < TM; ++i) {
           const float a = lane4(av[i], s);
 #pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bv[j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j], a, acc[i][j], 0, 0, 0);
         }
       }
     }
-    if (ks + 1 < slices) store_slice(cur ^ 1);
-    __syncthreads();
+  };
+
+  const uint32_t slices = (kend - kbeg + BK - 1) / BK;
+  load_slice(st0, kbeg);
+  store_slice(st0, 0);
+  if (PF == 2 && slices > 1) load_slice(st1, kbeg + BK);
+  __syncthreads();
+  if (PF == 1) {
+    for (uint32_t ks = 0; ks < slices; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < slices) load_slice(st0, kbeg + (ks + 1) * BK);
+      compute(cur);
+      if (ks + 1 < slices) store_slice(st0, cur ^ 1);
+      __syncthreads();
+    }
+  } else {
+    // Slice s travels in set s & 1 and is computed from LDS buffer s & 1; the loop
+    // is unrolled by two so that every set and buffer index is a constant.
+    for (uint32_t ks = 0; ks < slices; ks += 2) {
+      if (ks + 2 < slices) load_slice(st0, kbeg + (ks + 2) * BK);
+      compute(0);
+      if (ks + 1 < slices) store_slice(st1, 1);
+      __syncthreads();
+      if (ks + 1 >= slices) break;
+      if (ks + 3 < slices) load_slice(st1, kbeg + (ks + 3) * BK);
+      compute(1);
+      if (ks + 2 < slices) store_slice(st0, 0);
+      __syncthreads();
+    }
   }
 
+  // Store: lane (t16, q) of tile (i, j) holds row t16, columns 4q .. 4q+3.
+  constexpr bool VOUT = true;
   if (SPLIT) {
     float* __restrict__ part = A.ws + (size_t)(kz * batch + bz) * M * N;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        const uint32_t col = n0 + wn * TN * 16 + j * 16 + t16;
+        const uint32_t row = m0 + wm * TM * 16 + i * 16 + t16;
+        const uint32_t col0 = n0 + wn * TN * 16 + j * 16 + 4 * q;
+        if (row >= M) continue;
+        if (N % 4 == 0 && VOUT) {
+          if (col0 < N) *reinterpret_cast<f4*>(part + (size_t)row * N + col0) = acc[i][j];
+        } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t row = m0 + wm * TM * 16 + i * 16 + 4 * q + r;
-          if (row < M && col < N) part[(size_t)row * N + col] = acc[i][j][r];
+          for (int r = 0; r < 4; ++r)
+            if (col0 + r < N) part[(size_t)row * N + col0 + r] = acc[i][j][r];
         }
       }
     return;
@@ -298,14 +347,21 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
   for (int i = 0; i < TM; ++i) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-      const uint32_t col = n0 + wn * TN * 16 + j * 16 + t16;
+      const uint32_t row = m0 + wm * TM * 16 + i * 16 + t16;
+      const uint32_t col0 = n0 + wn * TN * 16 + j * 16 + 4 * q;
+      if (row >= M) continue;
+      const uint32_t o = (bz * M + row) * N + col0;
+      if (N % 4 == 0 && VOUT) {
+        if (col0 < N) {
+          f4 v;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint32_t row = m0 + wm * TM * 16 + i * 16 + 4 * q + r;
-        if (row < M && col < N) {
-          const uint32_t o = (bz * M + row) * N + col;
-          A.out[o] = epi(A, o, acc[i][j][r]);
+          for (int r = 0; r < 4; ++r) v[r] = epi(A, o + r, acc[i][j][r]);
+          *reinterpret_cast<f4*>(A.out + o) = v;
         }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (col0 + r < N) A.out[o + r] = epi(A, o + r, acc[i][j][r]);
       }
     }
   }

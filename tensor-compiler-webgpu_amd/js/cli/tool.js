@@ -107,7 +107,13 @@ function precompileGroup(group, arch) {
     const { fusedStep } = require('../src/mi355x/trainer');
     const reqs = [{ model: 'mlp' }, { model: 'transformer', B: 1 }, { model: 'transformer', B: 64 }, { model: 'transformer-ref' }];
     let n = 0;
-    for (const r of reqs) { const fs = fusedStep(modelStep(r).step); n += precompile([fs.lowered], arch) + precompile([fs.checked], arch); }
+    for (const r of reqs) {
+      const m = modelStep(r);
+      const fs = fusedStep(m.step);
+      // The bench's unfused step runs in the perf lowering as well.
+      const unfused = lowerMI355X(m.step.graph, { perf: true, keep: [m.step.loss, m.step.logits].concat(Object.values(m.step.outputs)) });
+      n += precompile([fs.lowered], arch) + precompile([fs.checked], arch) + precompile([unfused], arch);
+    }
     return n;
   }
   if (group === 'configs') {
@@ -134,8 +140,11 @@ function precompileGroup(group, arch) {
 
 /** The load modes (A, B) of a matmul launch's kernel, or null. */
 function gemmModes(l) {
-  const m = l.kernels[0].source.match(/gemm_f32<\d+, \d+, \d+, (\d), (\d)/);
-  return m ? [Number(m[1]), Number(m[2])] : null;
+  // gemm_f32<TM, TN, BK, PF, AMODE, BMODE, SPLIT, ...>
+  const m = l.kernels[0].source.match(/gemm_f32<([^>]*)>/);
+  if (!m) return null;
+  const a = m[1].split(',').map((x) => x.trim());
+  return [Number(a[4]), Number(a[5])];
 }
 
 /** The K split (chunks, chunk length) of a matmul launch's kernel, or null. */

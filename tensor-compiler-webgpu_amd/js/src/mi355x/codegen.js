@@ -670,7 +670,8 @@ function gemmTiling(batch, M, N, K, tuning) {
   let chunkK = Math.ceil(Math.ceil(K / chunks) / 16) * 16;
   chunks = Math.ceil(K / chunkK);
   const bk = t.bk || (T === 1 ? 64 : T === 2 ? 32 : 16);
-  return { T, chunks, chunkK, bk, blocks: blocks(T) * chunks };
+  const pf = t.pf || 2;
+  return { T, chunks, chunkK, bk, pf, blocks: blocks(T) * chunks };
 }
 
 /**
@@ -771,7 +772,7 @@ ${indent(lines, '    ')}
 };
 `;
   const main = `extern "C" __global__ void __launch_bounds__(256) __KERNEL__(const TcmiArgs A) {
-  tcmi::gemm_f32<${T}, ${T}, ${tl.bk}, ${av.mode}, ${bv.mode}, ${split}, __KERNEL___av, __KERNEL___bv, __KERNEL___epi>(A, A.in[${ia}], A.in[${ib}],
+  tcmi::gemm_f32<${T}, ${T}, ${tl.bk}, ${tl.pf}, ${av.mode}, ${bv.mode}, ${split}, __KERNEL___av, __KERNEL___bv, __KERNEL___epi>(A, A.in[${ia}], A.in[${ib}],
       ${batch}u, ${M}u, ${K}u, ${N}u, ${tl.chunks}u, ${tl.chunkK}u);
 }
 `;
