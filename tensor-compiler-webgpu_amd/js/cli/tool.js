@@ -13,6 +13,8 @@
 //   model-fusion     fusion summaries of the reference's transformer forward pass and Adam step
 //   direct-catalogue the direct adversarial cases: names, kinds, patterns, and what fuse() makes of each
 //   transformer-init the reference transformer (golden config) forward + gradient graph and its inputs
+//   random-programs  request {programs: [{seed, focus?, f32?}]} -> the reference's v2 random programs
+//   corpus-fusion    request {from, to, sabotageTo?} -> fusion counts over corpus programs
 //   config-graphs    request {c3: [{fn, R, C}], c4: [{act, M, K, N}]} -> forward and gradient graphs of configs 3 and 4
 // GPU commands write a bundle (manifest.json + data.f32) under --out:
 //   gpu-direct       request {sabotage?}: every direct case, fused, canary-padded, on the GPU
@@ -585,6 +587,52 @@ async function main() {
         };
         return { seed, ops: w.ops, forward: one(w.forward), gradient: one(w.gradient) };
       });
+      break;
+    }
+    case 'random-programs': {
+      // The reference's v2 random programs (the fuzzing corpus generator), as graphs and outputs.
+      const { randomProgram } = require('../src/testing/random_graph');
+      out = req.programs.map((r) => {
+        const p = randomProgram(r.seed, { focus: r.focus || undefined, f32: !!r.f32 });
+        return { seed: r.seed, focus: p.focus, graph: p.graph.toJSON(), outputs: p.outputs, inputs: p.inputs, bounds: p.bounds };
+      });
+      break;
+    }
+    case 'corpus-fusion': {
+      // The fusion pass over corpus programs [from, to]: the counts the reference records
+      // (measurements.json m4.semantics.corpus, m4.passSabotage, gpu-m4.json fuzz structure).
+      const { corpusGraphs } = require('../src/testing/random_graph');
+      const sem = { graphs: 0, withFused: 0, fusedNodes: 0, byPattern: {} };
+      const fz = { runs: 0, fusedRuns: 0, byKind: {}, byPattern: {} };
+      const sab = { graphs: 0, changed: 0, threw: 0 };
+      for (let i = req.from; i <= req.to; i++) {
+        for (const c of corpusGraphs(i)) {
+          const f = fuse(c.graph, { keep: c.keep });
+          const fusedNodes = f.graph.nodes.filter((n) => n.op === 'fused');
+          sem.graphs++;
+          if (fusedNodes.length) sem.withFused++;
+          sem.fusedNodes += fusedNodes.length;
+          for (const n of fusedNodes) sem.byPattern[n.attrs.pattern] = (sem.byPattern[n.attrs.pattern] || 0) + 1;
+          // The GPU fuzzer runs a matmul program twice (the reference's naive and tiled matmuls).
+          const reps = c.graph.nodes.some((n) => n.op === 'matmul') ? 2 : 1;
+          const kinds = new Set(fusedNodes.map((n) => n.attrs.kind)), patterns = new Set(fusedNodes.map((n) => n.attrs.pattern));
+          fz.runs += reps;
+          if (fusedNodes.length) fz.fusedRuns += reps;
+          for (const k of kinds) fz.byKind[k] = (fz.byKind[k] || 0) + reps;
+          for (const q of patterns) fz.byPattern[q] = (fz.byPattern[q] || 0) + reps;
+          if (i <= (req.sabotageTo || 0)) {
+            sab.graphs++;
+            try {
+              const bad = fuse(c.graph, { keep: c.keep, sabotage: 'fusion-absorbs-shared' });
+              if (JSON.stringify(bad.graph.toJSON().nodes) !== JSON.stringify(f.graph.toJSON().nodes)) sab.changed++;
+            } catch (e) {
+              sab.threw++;
+              sab.changed++;
+            }
+          }
+        }
+      }
+      out = { semantics: sem, fuzz: fz, passSabotage: sab };
       break;
     }
     case 'config-graphs': {

@@ -12,8 +12,9 @@ test reads the reference at run time.
   cases.json          golden/cases.json (112 graphs + inputs + cotangents) with
                       golden/torch.json's float64 outputs and gradients merged in
   m4_counts.json      golden/measurements.json m4.fusion / m4.semantics.model /
-                      corpus byPattern, and golden/gpu-m4.json direct-case names
-                      with their kind and pattern
+                      m4.semantics.corpus counts / m4.passSabotage counts, and
+                      golden/gpu-m4.json direct-case names with their kind and
+                      pattern and the fuzzer's structural counts
   transformer_init.json + transformer_init.f64
                       golden/spec-m3b.json golden-seed1 (V, batch, seed, initSha,
                       the four token sequences of its first batch) and
@@ -51,9 +52,15 @@ def main(ref_root: str) -> None:
     gpu = json.loads((ref / "gpu-m4.json").read_text())
     direct = [{"name": d["name"], "kind": d["kind"], "pattern": d["pattern"], "matmul": d.get("matmul")}
               for d in gpu["direct"]]
-    counts = {"source": "golden/measurements.json m4, golden/gpu-m4.json direct",
+    corpus = m["semantics"]["corpus"]
+    fuzz = gpu["fuzz"]
+    sab = m["passSabotage"]
+    counts = {"source": "golden/measurements.json m4, golden/gpu-m4.json direct and fuzz",
               "fusion": m["fusion"], "semanticsModel": m["semantics"]["model"],
-              "corpusByPattern": m["semantics"]["corpus"]["byPattern"],
+              "corpusByPattern": corpus["byPattern"],
+              "corpus": {k: corpus[k] for k in ("programs", "graphs", "withFused", "fusedNodes", "byPattern")},
+              "fuzz": {k: fuzz[k] for k in ("programs", "skipped", "runs", "fusedRuns", "byKind", "byPattern")},
+              "passSabotage": {k: sab[k] for k in ("programs", "graphs", "changed", "threw")},
               "gpuDirect": m["gpu"]["direct"], "direct": direct}
     (HERE / "m4_counts.json").write_text(json.dumps(counts, indent=1))
 
