@@ -13,11 +13,13 @@ keyed by their exact text), so a GPU box starts without compiling.
 from __future__ import annotations
 
 import hashlib
+import json
 import os
 import pathlib
 import shutil
 import subprocess
 import sys
+import time
 
 PKG = pathlib.Path(__file__).resolve().parent
 ROOT = PKG.parent
@@ -69,15 +71,43 @@ def check_node_loads() -> None:
           LIB / "tcmi.node"])
 
 
-PRECOMPILE_GROUPS = ["direct", "models", "configs"]
+# (group, shard, shards): the fuzz corpus's ~7500 kernels are compiled in 6 parts.
+PRECOMPILE_JOBS = [("direct", 0, 1), ("models", 0, 1), ("configs", 0, 1)] + [("fuzz", k, 6) for k in range(6)]
+KCACHE = PKG / "_build" / "kcache"
 
 
-def precompile(groups=None) -> None:
-    for g in groups or PRECOMPILE_GROUPS:
-        req = PKG / "_build" / f"precompile-{g}.json"
-        req.parent.mkdir(exist_ok=True)
-        req.write_text('{"group": "%s", "arch": "gfx950"}' % g)
-        _run(["node", JS / "cli" / "tool.js", "precompile", req])
+def precompile(jobs=None, workers=None) -> None:
+    """Compile the code objects of the standard runs into a fresh cache, several
+    groups at a time (each job is one hiprtc translation unit in its own node
+    process)."""
+    jobs = jobs or PRECOMPILE_JOBS
+    if KCACHE.exists():
+        shutil.rmtree(KCACHE)   # only what this build's kernels need travels to a GPU box
+    KCACHE.mkdir(parents=True)
+    workers = workers or max(1, min(len(jobs), os.cpu_count() or 1, 8))
+    pending = list(jobs)
+    running = []
+    failed = []
+    while pending or running:
+        while pending and len(running) < workers:
+            group, shard, shards = pending.pop(0)
+            req = PKG / "_build" / f"precompile-{group}-{shard}.json"
+            req.write_text(json.dumps({"group": group, "arch": "gfx950", "shard": shard, "shards": shards}))
+            cmd = ["node", str(JS / "cli" / "tool.js"), "precompile", str(req)]
+            print("+", " ".join(cmd), flush=True)
+            running.append((group, shard, subprocess.Popen(cmd, stdout=subprocess.PIPE)))
+        time.sleep(0.2)
+        for job in list(running):
+            group, shard, proc = job
+            if proc.poll() is None:
+                continue
+            running.remove(job)
+            out = proc.stdout.read().decode()
+            print(f"  {group}[{shard}]: {out.strip()}", flush=True)
+            if proc.returncode != 0:
+                failed.append(f"{group}[{shard}]")
+    if failed:
+        raise SystemExit(f"precompile failed: {', '.join(failed)}")
 
 
 def main(argv) -> None:

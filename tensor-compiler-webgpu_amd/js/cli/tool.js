@@ -19,6 +19,7 @@
 // GPU commands write a bundle (manifest.json + data.f32) under --out:
 //   gpu-direct       request {sabotage?}: every direct case, fused, canary-padded, on the GPU
 //   gpu-graphs       request {graphs: [{name, graph, inputs, keep, unfused?, perf?}]} fused (and unfused, and in the perf lowering) on the GPU
+//   gpu-fuzz         request {from, to}: the reference's corpus programs, fused / perf / unfused, on the GPU
 //   gpu-configs      request {c3: [...], c4: [...], unfused} configs 3 and 4, kept outputs as oracle-computable slices
 
 const fs = require('fs');
@@ -95,7 +96,7 @@ function transformerInit(req) {
 }
 
 /** Compile, offline, the kernels a named group of GPU runs will ask for (same module text as on the box). */
-function precompileGroup(group, arch) {
+function precompileGroup(group, arch, shard, shards) {
   const { precompile } = require('../src/mi355x/runner');
   if (group === 'direct') {
     const fused = fusedDirectCases().map((c) => fuse(c.graph).graph);
@@ -136,6 +137,21 @@ function precompileGroup(group, arch) {
       for (const act of ['relu', 'tanh']) { const g = cfg.c4Graphs(act, M, K, N); both(g.forward); both(g.gradient); }
     }
     return precompile(lists, arch);
+  }
+  if (group === 'fuzz') {
+    // The GPU fuzzer's kernels (corpus programs 1..2000, fused and unfused), in
+    // `shards` disjoint parts by kernel name so several processes can compile them.
+    const { corpusGraphs } = require('../src/testing/random_graph');
+    const { fnv } = require('../src/mi355x/codegen');
+    const lists = [];
+    for (let i = 1; i <= 2000; i++) {
+      for (const c of corpusGraphs(i)) {
+        const f = fuse(c.graph, { keep: c.keep });
+        lists.push(lowerMI355X(f.graph), lowerMI355X(f.graph, { perf: true, keep: c.keep.map((id) => f.index.get(id)) }), lowerMI355X(c.graph));
+      }
+    }
+    const k = shards || 1, me = shard || 0;
+    return precompile(lists, arch, (name) => parseInt(fnv(name), 16) % k === me);
   }
   throw new Error(`unknown precompile group '${group}'`);
 }
@@ -389,6 +405,41 @@ async function gpuConfigs(req, dir) {
     }
   }
   bundle.close({ device: runner.info() });
+}
+
+/**
+ * The reference's GPU fuzzer over its corpus (src/gpu/harness-m4.js:126-172): for
+ * corpus programs [from, to], the program and its gradient graph, each fused
+ * (plain lowering), fused in the perf lowering, and unfused, on the GPU with
+ * canaries. The bundle holds each graph, its fused graph and origin map, the
+ * inputs, and every node's GPU value of each variant (the perf variant's kept
+ * outputs only) for the checker.
+ */
+async function gpuFuzz(req, dir) {
+  const { corpusGraphs } = require('../src/testing/random_graph');
+  const { HipRunner } = require('../src/mi355x/runner');
+  const runner = HipRunner.create();
+  const bundle = new Bundle(dir);
+  for (let i = req.from; i <= req.to; i++) {
+    for (const c of corpusGraphs(i)) {
+      const inputs = {}, ins = {};
+      for (const name of Object.keys(c.inputs)) { inputs[name] = Float32Array.from(c.inputs[name]); ins[name] = bundle.put(inputs[name]); }
+      const f = fuse(c.graph, { keep: c.keep });
+      const keepF = c.keep.map((id) => f.index.get(id));
+      const rf = await runner.run(f.graph, lowerMI355X(f.graph), inputs, { canary: true });
+      const rp = await runner.run(f.graph, lowerMI355X(f.graph, { perf: true, keep: keepF }), inputs, { canary: true });
+      const ru = await runner.run(c.graph, lowerMI355X(c.graph), inputs, { canary: true });
+      const entry = { program: i, label: c.label, graph: c.graph.toJSON(), fused: f.graph.toJSON(), origin: f.origin, keep: c.keep,
+        inputs: ins, gpuFused: {}, gpuUnfused: {}, gpuPerf: {},
+        canary: rf.canaryIntact.every(Boolean) && rp.canaryIntact.every(Boolean) && ru.canaryIntact.every(Boolean) };
+      f.graph.nodes.forEach((n) => { entry.gpuFused[n.id] = bundle.put(rf.values[n.id]); });
+      c.graph.nodes.forEach((n) => { entry.gpuUnfused[n.id] = bundle.put(ru.values[n.id]); });
+      for (const id of keepF) entry.gpuPerf[id] = bundle.put(rp.values[id]);
+      bundle.add(entry);
+    }
+    if (i % 100 === 0) process.stderr.write(`gpu-fuzz: program ${i}\n`);
+  }
+  bundle.close({ device: runner.info(), from: req.from, to: req.to });
 }
 
 /**
@@ -665,7 +716,7 @@ async function main() {
           split: gemmSplit(x), plainSplit: gemmSplit(plain.get(x.node)) })) };
       break;
     }
-    case 'precompile': out = { kernels: precompileGroup(req.group || 'direct', req.arch) }; break;
+    case 'precompile': out = { kernels: precompileGroup(req.group || 'direct', req.arch, req.shard, req.shards) }; break;
     case 'gpu-direct': await gpuDirect(outDir(argv), req); out = { ok: true }; break;
     case 'step-graph': stepGraph(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-local': await gpuLocal(req, outDir(argv)); out = { ok: true }; break;
@@ -673,6 +724,7 @@ async function main() {
     case 'gpu-chains': await gpuChains(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-graphs': await gpuGraphs(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-configs': await gpuConfigs(req, outDir(argv)); out = { ok: true }; break;
+    case 'gpu-fuzz': await gpuFuzz(req, outDir(argv)); out = { ok: true }; break;
     default:
       throw new Error(`unknown command '${cmd}'`);
   }

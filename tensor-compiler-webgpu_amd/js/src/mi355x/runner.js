@@ -40,8 +40,9 @@ function translationUnit(sources) {
 // The kernel index: for every kernel compiled before (here or at build time),
 // the translation unit it was compiled in, so a later process loads that unit's
 // cached code object instead of compiling the kernel again in a new unit.
-// <cache>/index/<kernel>.ref holds the unit's key, <cache>/index/<key>.tu its text.
+// <cache>/index/<key>.tu holds a unit's text, <key>.names its kernels' names.
 const INDEX = path.join(CACHE, 'index');
+let indexMap = null;   // kernel name -> unit key, read once per process
 
 function unitKey(text) { return crypto.createHash('sha256').update(text).digest('hex').slice(0, 32); }
 
@@ -51,34 +52,51 @@ function writeAtomic(file, text) {
   fs.renameSync(tmp, file);
 }
 
+function loadIndex() {
+  if (indexMap) return indexMap;
+  indexMap = new Map();
+  let files = [];
+  try { files = fs.readdirSync(INDEX); } catch (e) { return indexMap; }
+  for (const f of files) {
+    if (!f.endsWith('.names')) continue;
+    const key = f.slice(0, -'.names'.length);
+    for (const name of fs.readFileSync(path.join(INDEX, f), 'utf8').split('\n')) if (name) indexMap.set(name, key);
+  }
+  return indexMap;
+}
+
 /** Record that the kernels `names` are in unit `text`; an index that cannot be written only costs compile time. */
 function indexUnit(names, text) {
+  const key = unitKey(text);
+  const map = loadIndex();
+  for (const n of names) map.set(n, key);
   try {
     fs.mkdirSync(INDEX, { recursive: true });
-    const key = unitKey(text);
     const tu = path.join(INDEX, `${key}.tu`);
     if (!fs.existsSync(tu)) writeAtomic(tu, text);
-    for (const n of names) writeAtomic(path.join(INDEX, `${n}.ref`), key);
+    writeAtomic(path.join(INDEX, `${key}.names`), names.join('\n') + '\n');
   } catch (e) {
     // read-only cache: nothing to record
   }
 }
 
-/** The text of the unit that holds kernel `name`, or null. */
-function indexedUnit(name) {
+/** The text of indexed unit `key`, or null. */
+function unitText(key) {
   try {
-    const key = fs.readFileSync(path.join(INDEX, `${name}.ref`), 'utf8').trim();
-    const text = fs.readFileSync(path.join(INDEX, `${key}.tu`), 'utf8');
-    return text.includes(` ${name}(const TcmiArgs`) ? { key, text } : null;
+    return fs.readFileSync(path.join(INDEX, `${key}.tu`), 'utf8');
   } catch (e) {
     return null;
   }
 }
 
-/** Compile (into the on-disk cache only; no GPU needed) every kernel of `lists` as one module. */
-function precompile(lists, arch) {
+/**
+ * Compile (into the on-disk cache only; no GPU needed) every kernel of `lists`
+ * as one module; with `select(name)`, only the kernels it accepts.
+ */
+function precompile(lists, arch, select) {
   const all = new Map();
-  for (const l of lists) for (const [name, src] of kernelSources(l)) all.set(name, src);
+  for (const l of lists) for (const [name, src] of kernelSources(l)) if (!select || select(name)) all.set(name, src);
+  if (!all.size) return 0;
   const text = translationUnit(all);
   addon().precompile(text, '', arch || 'gfx950');
   indexUnit(Array.from(all.keys()), text);
@@ -134,6 +152,7 @@ class HipRunner {
   constructor(a) {
     this.a = a;
     this.loaded = new Map();    // kernel name (a hash of its source) -> function handle
+    this.units = new Map();     // indexed unit key -> its loaded module (null: unreadable)
   }
 
   get lost() { return this.a.lost(); }
@@ -149,20 +168,20 @@ class HipRunner {
     const lists = Array.isArray(lowered) ? lowered : [lowered];
     const missing = new Map();
     for (const l of lists) for (const [name, src] of kernelSources(l)) if (!this.loaded.has(name)) missing.set(name, src);
-    // Kernels compiled before in some unit: load those units (code-object cache hits).
-    const units = new Map();
-    for (const name of missing.keys()) {
-      const u = indexedUnit(name);
-      if (!u) continue;
-      if (!units.has(u.key)) units.set(u.key, { text: u.text, names: [] });
-      units.get(u.key).names.push(name);
-    }
-    for (const u of units.values()) {
-      const module = this.a.compile(u.text, '');
-      for (const name of u.names) {
-        this.loaded.set(name, this.a.function(module, name));
-        missing.delete(name);
+    // Kernels compiled before in some unit: load that unit's module once per
+    // process (a code-object cache hit) and take their functions from it.
+    const index = loadIndex();
+    for (const name of Array.from(missing.keys())) {
+      const key = index.get(name);
+      if (!key) continue;
+      if (!this.units.has(key)) {
+        const text = unitText(key);
+        this.units.set(key, text === null ? null : this.a.compile(text, ''));
       }
+      const module = this.units.get(key);
+      if (module === null) continue;
+      this.loaded.set(name, this.a.function(module, name));
+      missing.delete(name);
     }
     if (missing.size) {
       const text = translationUnit(missing);
