@@ -106,7 +106,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--configs", default="ceiling,c2,c3,c4,c1,c5")
+    ap.add_argument("--configs", default="ceiling,c2,c3,c4,c1,c5,sweep")
     ap.add_argument("--programs", type=int, default=8)
     ap.add_argument("--quick", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -149,6 +149,14 @@ def main() -> None:
                             "launches": t["launches"], "fused_us": t["fused"]["median"], "unfused_us": t["unfused"]["median"],
                             "speedup_vs_unfused": t["verdict"]["speedup"], "matmul_TFLOPs_resident": t["matmulTflopsResident"],
                             "loss": t["lossLast"], "time_by_kind_us": {k: round(v["us"], 1) for k, v in t["byKind"].items()}}
+    if "sweep" in cfg:
+        sw = cfg["sweep"]
+        extra["workload_sweep"] = {
+            "workloads": len(sw["workloads"]), "families": sw["families"],
+            "fusion_loses_by_design": {r["id"]: {"fused_vs_unfused": round(r["fused"]["speedup"], 3), "verdict": r["fused"]["verdict"],
+                                                 **({"recompute_vs_fused": round(r["recompute"]["speedup"], 3),
+                                                     "recompute_verdict": r["recompute"]["verdict"]} if "recompute" in r else {})}
+                                       for r in sw["workloads"] if r["family"] in ("broadcast-recompute", "lost-reuse")}}
     if c2 is None:
         raise SystemExit("bench.py: the headline needs config c2")
     dom = c2["dominant"]

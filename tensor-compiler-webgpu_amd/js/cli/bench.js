@@ -14,6 +14,7 @@
 //     bracketed by a sync and hipEvents on both sides.
 // c3  softmax / logSoftmax forward + backward over [16384, 4096]
 // c4  matmul + bias -> relu | tanh at three shapes, and its backward graph
+// sweep  the reference's workload sweep: fused vs unfused (and recompute) per workload
 // For every program: fused and unfused timed against each other (ABBA), every
 // launch timed alone (for per-fusion-group speedups and the dominant kernel's
 // average duration), algorithmic bytes and matmul flops.
@@ -311,6 +312,65 @@ function trainStep(runner, bench, name, req, opts) {
 function c1(runner, bench, opts) { return trainStep(runner, bench, 'c1', { model: 'mlp' }, opts); }
 function c5(runner, bench, opts) { return trainStep(runner, bench, 'c5', { model: 'transformer', B: opts.quick ? 8 : 64 }, opts); }
 
+/**
+ * The reference's workload sweep (src/fusion/workloads.js:71-120): every graph
+ * workload's variants (unfused, fused, recompute, matmul-only) in the perf
+ * lowering, timed against each other in ABBA order; per workload the median and
+ * range of each variant, its launches and algorithmic bytes, and the fused-vs-
+ * unfused (and recompute-vs-fused) speedup and win / loss / noise verdict,
+ * including the workloads built so that fusion loses.
+ */
+function sweep(runner, bench, opts) {
+  const { workloads } = require('../src/builders/workloads');
+  const rows = [];
+  for (const w of workloads()) {
+    const m = w.make();
+    const variants = {}, info = {};
+    for (const v of w.variants) {
+      let graph, lowered, only;
+      if (v === 'unfused') {
+        graph = m.graph;
+        lowered = lowerMI355X(m.graph, { perf: true, keep: m.outputs });
+      } else {
+        const f = fuse(m.graph, { keep: m.outputs, recompute: v === 'recompute' });
+        graph = f.graph;
+        lowered = lowerMI355X(f.graph, { perf: true, keep: m.outputs.map((id) => f.index.get(id)) });
+        if (v === 'matmul-only') only = (l) => !!l.flops;
+      }
+      runner.functions(lowered);
+      const launches = lowered.launches.filter((l) => !only || only(l));
+      variants[v] = prepared(runner, graph, lowered, m.inputs, only ? { only } : undefined);
+      info[v] = { launches: launches.length, bytes: launches.reduce((q, l) => q + l.bytes, 0), flops: launches.reduce((q, l) => q + (l.flops || 0), 0) };
+    }
+    const t = bench.time(variants, { reps: opts.reps || 16 });
+    const row = { id: w.id, family: w.family, params: w.params, k: t.k, variants: {} };
+    for (const v of w.variants) {
+      const st = t.stats[v];
+      row.variants[v] = Object.assign({ medianUs: st.median * 1e3, minUs: st.min * 1e3, maxUs: st.max * 1e3, gbs: info[v].bytes / (st.median * 1e6) }, info[v]);
+    }
+    if (t.stats.fused) row.fused = verdict(t.stats.unfused, t.stats.fused);
+    if (t.stats.recompute) row.recompute = verdict(t.stats.fused, t.stats.recompute);
+    rows.push(row);
+    for (const v of w.variants) variants[v].destroy();
+    log(`sweep ${w.id}: ${row.fused ? `fused ${row.fused.speedup.toFixed(2)}x ${row.fused.verdict}` : ''}`);
+  }
+  // Per family: workloads, fused wins / losses / noise, median and range of the speedup.
+  const families = {};
+  for (const r of rows) {
+    if (!r.fused) continue;
+    const f = families[r.family] || (families[r.family] = { workloads: 0, win: 0, loss: 0, noise: 0, speedups: [] });
+    f.workloads++;
+    f[r.fused.verdict] = (f[r.fused.verdict] || 0) + 1;
+    f.speedups.push(r.fused.speedup);
+  }
+  for (const f of Object.values(families)) {
+    f.speedups.sort((a, b) => a - b);
+    f.speedup = { median: median(f.speedups), min: f.speedups[0], max: f.speedups[f.speedups.length - 1] };
+    delete f.speedups;
+  }
+  return { config: 'sweep', workloads: rows, families };
+}
+
 /** The bandwidth ceiling (workloads.js:312-345): copy and pure read of 1 GiB, grid-strided, 1024 x 256 threads. */
 function ceiling(runner, bench) {
   const a = runner.a;
@@ -341,7 +401,7 @@ async function main() {
   const opts = { quick: flag('quick'), reps: arg('reps') ? Number(arg('reps')) : undefined };
   const which = arg('configs', 'ceiling,c2,c3,c4,c1,c5').split(',');
   const out = { device: runner.info(), peaks: { hbmGBs: HBM_PEAK_GBS, fp32MfmaTFLOPs: FP32_MFMA_PEAK_TFLOPS }, configs: {} };
-  const fns = { c2, c3, c4, c1, c5, ceiling };
+  const fns = { c2, c3, c4, c1, c5, ceiling, sweep };
   for (const c of which) {
     if (!fns[c]) throw new Error(`unknown config ${c}`);
     const t0 = Date.now();

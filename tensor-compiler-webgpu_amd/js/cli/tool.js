@@ -138,6 +138,20 @@ function precompileGroup(group, arch, shard, shards) {
     }
     return precompile(lists, arch);
   }
+  if (group === 'sweep') {
+    // The workload sweep's variants as the bench lowers them.
+    const { workloads } = require('../src/builders/workloads');
+    const lists = [];
+    for (const w of workloads()) {
+      const m = w.make();
+      for (const v of w.variants) {
+        if (v === 'unfused') { lists.push(lowerMI355X(m.graph, { perf: true, keep: m.outputs })); continue; }
+        const f = fuse(m.graph, { keep: m.outputs, recompute: v === 'recompute' });
+        lists.push(lowerMI355X(f.graph, { perf: true, keep: m.outputs.map((id) => f.index.get(id)) }));
+      }
+    }
+    return precompile(lists, arch);
+  }
   if (group === 'fuzz') {
     // The GPU fuzzer's kernels (corpus programs 1..2000, fused and unfused), in
     // `shards` disjoint parts by kernel name so several processes can compile them.
