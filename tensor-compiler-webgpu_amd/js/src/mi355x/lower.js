@@ -27,6 +27,10 @@
 //     matmul reads) launches nothing either (`folded`): the matmuls read its
 //     source in place through a strided view (tcmi_gemm.h). The records of
 //     those matmuls name the source as their input.
+//   - a broadcast whose every consumer reads it in an elementwise, rowwise or
+//     epilogue body (not as a matmul operand, not through a reduction or another
+//     gather) launches nothing: each consumer's kernel reads the broadcast's
+//     source through the broadcast's index map instead of a materialised copy.
 // Nodes in `keep` are never folded, so their values stay readable.
 
 const { Graph } = require('../ir/graph');
@@ -46,9 +50,10 @@ function oneOpBody(graph, node, inputShapes, attrs) {
   return { body: g, output: out };
 }
 
-function algorithmicBytes(graph, node) {
+/** Each unique operand buffer read once at its own size, plus the output (workloads.js:171-172). */
+function algorithmicBytes(graph, node, inputs) {
   let bytes = size(node.shape) * 4;
-  for (const id of new Set(node.inputs)) bytes += size(graph.nodes[id].shape) * 4;
+  for (const id of new Set(inputs || node.inputs)) bytes += size(graph.nodes[id].shape) * 4;
   return bytes;
 }
 
@@ -57,11 +62,34 @@ function single(k) {
   return { kernels, params: k.params, workspace: k.workspace || 0, flops: k.flops || 0 };
 }
 
+/**
+ * `body` with the inputs at positions `folds` (pos -> {from, to} shapes) taking
+ * the broadcast's source shape `from`, each followed by a broadcast to `to` that
+ * stands for the input in the rest of the body. Returns { body, output }.
+ */
+function widenInputs(body, output, folds) {
+  if (!folds || folds.size === 0) return { body, output };
+  const g = new Graph();
+  const map = new Map();
+  for (const n of body.nodes) {
+    if (n.op === 'input') {
+      const pos = Number(n.attrs.name.slice(1));
+      const f = folds.get(pos);
+      const id = g.input(n.attrs.name, f ? f.from : n.shape);
+      map.set(n.id, f ? g.broadcast(id, f.to) : id);
+    } else {
+      map.set(n.id, g.emit(n.op, n.inputs.map((i) => map.get(i)), n.attrs));
+    }
+  }
+  return { body: g, output: map.get(output) };
+}
+
 /** Kernels for one node. */
-function lowerNode(graph, node, opts, mmViews) {
+function lowerNode(graph, node, opts, mmViews, folds) {
   if (node.op === 'fused') {
-    const b = bodyOf(node);
-    const out = node.attrs.output;
+    const w = widenInputs(bodyOf(node), node.attrs.output, folds);
+    const b = w.body;
+    const out = w.output;
     const kind = node.attrs.kind;
     const tuning = opts.tuning || {};
     const sab = { sabotage: opts.sabotage, pattern: node.attrs.pattern };
@@ -73,7 +101,8 @@ function lowerNode(graph, node, opts, mmViews) {
     throw new Error(`no MI355X kernel for fused kind '${kind}'`);
   }
   if (ELEMENTWISE_OPS.has(node.op) || GATHERS.has(node.op)) {
-    const { body, output } = oneOpBody(graph, node);
+    const one = oneOpBody(graph, node);
+    const { body, output } = widenInputs(one.body, one.output, folds);
     const kind = GATHERS.has(node.op) ? 'gather' : 'elementwise';
     return Object.assign({ kind }, single(cg.elementwiseKernel(body, output, node.shape, { tuning: (opts.tuning || {}).ew })));
   }
@@ -150,6 +179,29 @@ function perfPlan(graph, keep) {
     const ok = cons[id].every((c) => folded.has(c) || graph.nodes[c].inputs.every((i, pos) => i !== id || slotOf.has(`${c}:${pos}`)));
     if (ok) folded.add(id);
   }
+  // Broadcasts read in place by every consumer's body (never through a matmul
+  // operand slot, a plain reduction or another gather).
+  const bodyReader = (c, pos) => {
+    const n = graph.nodes[c];
+    if (ELEMENTWISE_OPS.has(n.op)) return true;
+    if (n.op !== 'fused') return false;
+    return !slotOf.has(`${c}:${pos}`);
+  };
+  const broadcasts = new Map();   // consumer id -> Map(pos -> { source, from, to })
+  for (const n of graph.nodes) {
+    if (n.op !== 'broadcast' || keep.has(n.id) || cons[n.id].length === 0) continue;
+    const ok = cons[n.id].every((c) => graph.nodes[c].inputs.every((i, pos) => i !== n.id || bodyReader(c, pos)));
+    if (!ok) continue;
+    folded.add(n.id);
+    const src = n.inputs[0];
+    for (const c of new Set(cons[n.id])) {
+      graph.nodes[c].inputs.forEach((i, pos) => {
+        if (i !== n.id) return;
+        if (!broadcasts.has(c)) broadcasts.set(c, new Map());
+        broadcasts.get(c).set(pos, { source: src, from: graph.nodes[src].shape, to: n.shape });
+      });
+    }
+  }
   const views = new Map();
   for (const n of graph.nodes) {
     for (const [slot, pos] of matmulSlots(n)) {
@@ -170,7 +222,7 @@ function perfPlan(graph, keep) {
       views.get(n.id)[slot] = { pos, source: cur, view, size: size(graph.nodes[cur].shape) };
     }
   }
-  return { aliases, folded, views };
+  return { aliases, folded, views, broadcasts };
 }
 
 /**
@@ -185,7 +237,7 @@ function perfPlan(graph, keep) {
  */
 function lowerMI355X(graph, options) {
   const opts = options || {};
-  const plan = opts.perf ? perfPlan(graph, new Set(opts.keep || [])) : { aliases: new Map(), folded: new Set(), views: new Map() };
+  const plan = opts.perf ? perfPlan(graph, new Set(opts.keep || [])) : { aliases: new Map(), folded: new Set(), views: new Map(), broadcasts: new Map() };
   const cache = new Map();
   const launches = [];
   let workspace = 0;
@@ -194,18 +246,22 @@ function lowerMI355X(graph, options) {
     if (plan.aliases.has(node.id) || plan.folded.has(node.id)) continue;
     const v = plan.views.get(node.id);
     const mmViews = v ? { views: { a: v.a && v.a.view, b: v.b && v.b.view }, sizes: { a: v.a && v.a.size, b: v.b && v.b.size } } : null;
-    // Kernels depend on structure, shapes and operand views only: reuse across identical nodes.
+    const folds = plan.broadcasts.get(node.id) || null;
+    const foldKey = folds ? Array.from(folds.entries()).map(([pos, f]) => [pos, f.from, f.to]) : null;
+    // Kernels depend on structure, shapes, operand views and folded broadcasts only: reuse across identical nodes.
     const key = JSON.stringify([node.op, node.inputs.map((id) => graph.nodes[id].shape), node.attrs, node.shape,
-      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews]);
+      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey]);
     let k = cache.get(key);
-    if (!k) { k = lowerNode(graph, node, opts, mmViews); cache.set(key, k); }
+    if (!k) { k = lowerNode(graph, node, opts, mmViews, folds); cache.set(key, k); }
     workspace = Math.max(workspace, k.workspace);
-    const inputs = node.inputs.map((id) => (plan.aliases.has(id) ? plan.aliases.get(id) : id));
-    if (v) for (const s of [v.a, v.b]) if (s) inputs[s.pos] = plan.aliases.has(s.source) ? plan.aliases.get(s.source) : s.source;
+    const resolve = (id) => (plan.aliases.has(id) ? plan.aliases.get(id) : id);
+    const inputs = node.inputs.map(resolve);
+    if (v) for (const s of [v.a, v.b]) if (s) inputs[s.pos] = resolve(s.source);
+    if (folds) for (const [pos, f] of folds) inputs[pos] = resolve(f.source);
     launches.push({
       node: node.id, op: node.op, kind: k.kind, pattern: node.op === 'fused' ? node.attrs.pattern : undefined,
       inputs, params: k.params, grid: k.kernels[0].grid, code: k.kernels[0].name,
-      kernels: k.kernels, workspace: k.workspace, bytes: algorithmicBytes(graph, node), flops: k.flops,
+      kernels: k.kernels, workspace: k.workspace, bytes: algorithmicBytes(graph, node, inputs), flops: k.flops,
     });
     if (v) {
       // Operands read in place: for each folded slot, the node it stands for and the view of its source.

@@ -186,8 +186,8 @@ def _chain_value(graph, operand, source, src_value):
 
 @pytest.mark.parametrize("req", [{"model": "mlp"}, {"model": "transformer", "B": 2}, {"model": "transformer-ref"}])
 def test_perf_lowering_views_address_the_operands(tool, req):
-    """The perf lowering skips only reshapes (sharing their input's buffer) and transposes
-    whose every consumer is a matmul operand slot; each matmul operand it reads in place
+    """The perf lowering skips only reshapes (sharing their input's buffer), transposes
+    whose every consumer is a matmul operand slot and broadcasts read by bodies; each matmul operand it reads in place
     is addressed by its strided view exactly as the transpose chain would have laid it out
     (checked element by element on distinct values), and the load mode matches the view."""
     d = tool("perf-lower", req)
@@ -195,7 +195,18 @@ def test_perf_lowering_views_address_the_operands(tool, req):
     nodes = g["nodes"]
     for a, src in d["aliases"]:
         assert nodes[a]["op"] == "reshape" and nodes[src]["op"] != "reshape"
-    assert all(nodes[i]["op"] == "transpose" for i in d["folded"])
+    assert all(nodes[i]["op"] in ("transpose", "broadcast") for i in d["folded"])
+    # A folded broadcast is read by elementwise, rowwise or epilogue bodies only (never
+    # by a reduction, a gather or as a matmul operand), through the broadcast's source.
+    consumers = {}
+    for n_id, n in enumerate(nodes):
+        for i in n["inputs"]:
+            consumers.setdefault(i, set()).add(n_id)
+    for i in d["folded"]:
+        if nodes[i]["op"] == "broadcast":
+            for c in consumers[i]:
+                assert nodes[c]["op"] == "fused" or nodes[c]["op"] in ("add", "sub", "mul", "div", "neg", "exp", "log",
+                                                                      "relu", "tanh", "sqrt", "step", "stopGradient"), nodes[c]["op"]
     launched = {l["node"] for l in d["launches"]}
     skipped = {a for a, _ in d["aliases"]} | set(d["folded"])
     assert launched.isdisjoint(skipped)
@@ -238,6 +249,7 @@ def test_perf_lowering_keeps_the_split_of_config4_backward(tool):
                                            for M, K, N in ((512, 512, 512), (4096, 4096, 4096), (8192, 1024, 4096))]})["c4"]
     for g in graphs:
         d = tool("perf-lower", {"graph": g["gradient"]["graph"], "keep": g["gradient"]["keep"]})
-        assert len(d["folded"]) == 2
+        nodes = d["graph"]["nodes"]
+        assert sum(nodes[i]["op"] == "transpose" for i in d["folded"]) == 2   # transpose(W), transpose(X)
         for l in d["launches"]:
             assert l["split"] == l["plainSplit"], (g["M"], g["K"], g["N"], l["node"])
