@@ -57,7 +57,7 @@ std::unordered_map<uint64_t, std::pair<hipGraph_t, hipGraphExec_t>> g_graphs;
 uint64_t g_next_handle = 1;
 
 // Options every kernel is compiled with. Packed fp32 instructions are turned
-// off (they have produced silent wrong results on this pool), and floating
+// off (some of their forms have produced silent wrong results on MI355X), and floating
 // point contraction is off so that a fused body rounds exactly as the unfused
 // kernels do, op by op.
 const char* kBaseOptions =

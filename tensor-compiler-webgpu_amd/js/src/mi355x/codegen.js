@@ -353,8 +353,8 @@ const isReduce = (n) => n.op === 'sum' || n.op === 'max';
  * every phase, so each input is read from HBM once, whatever the number of
  * reductions. A row is owned by L lanes: for C >= 2048 a whole workgroup of
  * 256 (reduced through LDS), otherwise a group of 16, 32 or 64 lanes of one
- * wavefront — the fewest that leave no lane idle for the row's float4 slots —
- * reduced by butterfly shuffles, with 256 / L rows per workgroup, so short
+ * wavefront — enough for about two float4 slots per lane — reduced by
+ * butterfly shuffles, with 256 / L rows per workgroup, so short
  * rows (attention's 128, LayerNorm's 256) still move a full workgroup's worth
  * of data per launch slot. Rows are walked grid-stride.
  */
@@ -370,7 +370,11 @@ function rowwiseKernel(b, output, opts) {
   const vec = C % 4 === 0;
   const W = vec ? 4 : 1;                     // elements per slot
   const pow2 = (x) => 2 ** Math.ceil(Math.log2(Math.max(1, x)));
-  const T = C >= 2048 ? 256 : Math.min(64, Math.max(16, pow2(Math.ceil(C / W))));   // lanes per row
+  const lanes = o.tuning && o.tuning.lanes;
+  // Lanes per row: 256 (the workgroup) for long rows; otherwise enough for two
+  // slots per lane, 16 to 64 (an on-device sweep: one slot per lane left short
+  // rows' loads too thin, more than four made the register cache too large).
+  const T = lanes || (C >= 2048 ? 256 : Math.min(64, Math.max(16, pow2(Math.ceil(C / (2 * W))))));
   const BLOCK = 256;
   const G = BLOCK / T;                        // rows per workgroup
   const E = Math.max(1, Math.ceil(C / (W * T)));  // slots per thread

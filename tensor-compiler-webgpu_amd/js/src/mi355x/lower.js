@@ -96,7 +96,7 @@ function lowerNode(graph, node, opts, mmViews, folds) {
     if (kind === 'elementwise') {
       return Object.assign({ kind: 'fused-elementwise' }, single(cg.elementwiseKernel(b, out, node.shape, Object.assign({ tuning: tuning.ew }, sab))));
     }
-    if (kind === 'rowwise') return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(b, out, sab)));
+    if (kind === 'rowwise') return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(b, out, Object.assign({ tuning: tuning.row }, sab))));
     if (kind === 'epilogue') return Object.assign({ kind: 'fused-epilogue' }, single(cg.gemmKernel(b, out, Object.assign({ tuning: tuning.gemm }, sab, mmViews))));
     throw new Error(`no MI355X kernel for fused kind '${kind}'`);
   }
@@ -113,7 +113,7 @@ function lowerNode(graph, node, opts, mmViews, folds) {
     if (inner === 1) {
       // A reduction over the last non-trivial axis: the rowwise kernel on [outer, n].
       const { body, output } = oneOpBody(graph, node, [[outer, n]], { axis: 1, keepDims: true });
-      return Object.assign({ kind: 'rowreduce' }, single(cg.rowwiseKernel(body, output, {})));
+      return Object.assign({ kind: 'rowreduce' }, single(cg.rowwiseKernel(body, output, { tuning: (opts.tuning || {}).row })));
     }
     const c = cg.colreduceKernels(node.op, outer, n, inner, (opts.tuning || {}).colreduce);
     return { kind: 'colreduce', kernels: c.launches, params: c.params, workspace: c.workspace, flops: 0 };
