@@ -85,9 +85,10 @@ def cpu_baseline(rows: int, seeds, min_seconds: float = 10.0) -> dict:
 
 
 def profiled_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
-    (profiles/*_traffic.md, a json block), or None when that profile is of another kernel."""
-    for md in sorted((ROOT / "profiles").glob("*_traffic.md")):
+    """HBM bytes per launch of `kernel` from a committed rocprofv3 --pmc summary
+    (profiles/*.md, the json block profile_summary.py writes: {"traffic_bytes_per_launch":
+    {kernel: bytes}}), or None when no profile covers that kernel."""
+    for md in sorted((ROOT / "profiles").glob("*.md")):
         text = md.read_text()
         if "```json" not in text:
             continue
@@ -96,8 +97,9 @@ def profiled_traffic(kernel: str):
             rec = json.loads(block)
         except ValueError:
             continue
-        if rec.get("kernel") == kernel:
-            return rec.get("traffic_bytes_per_launch"), md.name
+        traffic = rec.get("traffic_bytes_per_launch")
+        if isinstance(traffic, dict) and kernel in traffic:
+            return traffic[kernel], md.name
     return None, None
 
 

@@ -151,7 +151,8 @@ function c2(runner, bench, opts) {
         const lf = lowerMI355X(f.graph, { perf: true, keep: v.keep.map((id) => f.index.get(id)) });
         runner.functions(lf);
         programs.push(prepared(runner, f.graph, lf, inputs));
-        results.push({ name: `c2-p${s}-${kind}`, bytes: { fused: lf.launches.reduce((q, l) => q + l.bytes, 0) }, launchF: [] });
+        results.push({ name: `c2-p${s}-${kind}`, bytes: { fused: lf.launches.reduce((q, l) => q + l.bytes, 0) }, launchF: [],
+          launches: launchRecords(lf) });
         continue;
       }
       const r = measureGraph(runner, bench, `c2-p${s}-${kind}`, v.graph, v.keep, inputs, { keepPrograms: true, reps: opts.reps });
@@ -176,7 +177,8 @@ function c2(runner, bench, opts) {
   const wallMs = Number(process.hrtime.bigint() - t0) / 1e6;
   for (const p of programs) p.destroy();
   const stepBytes = results.reduce((s, r) => s + r.bytes.fused, 0);
-  // The roofline kernel: the fused kernel taking the most time in the step (each
+  // The roofline kernel: the fused kernel moving the most algorithmic bytes per step,
+  // chosen without timing so a profile of the same step names the same kernel (each
   // fused body is its own kernel, at one size, so its average is well defined).
   const all = [].concat.apply([], results.map((r) => r.launchF)).filter((l) => l.kind.startsWith('fused-'));
   return { config: 'c2', shape: [R, C], programs: P, steps: K, warmup: W, msPerStep: ms / K, wallMsPerStep: wallMs / K,
@@ -198,8 +200,13 @@ function runOnly(runner, name, graph, keep, inputs) {
   for (let i = 0; i < W + K; i++) p.run();
   p.sync();
   p.destroy();
-  return { name, runs: W + K, launches: lf.launches.map((l) => ({ node: l.node, kind: l.kind, pattern: l.pattern || null,
-    kernels: l.kernels.map((k) => k.name), bytes: l.bytes, flops: l.flops || 0 })) };
+  return { name, runs: W + K, launches: launchRecords(lf) };
+}
+
+/** Every launch of a lowering with its kernel names, algorithmic bytes and flops (for profile summaries). */
+function launchRecords(lowered) {
+  return lowered.launches.map((l) => ({ node: l.node, kind: l.kind, pattern: l.pattern || null,
+    kernels: l.kernels.map((k) => k.name), bytes: l.bytes, flops: l.flops || 0 }));
 }
 
 function c3(runner, bench, opts) {

@@ -537,7 +537,8 @@ ${indent(store, '    ')}
 }
 `;
   const k = kernelText('row', text);
-  const groups = Math.max(1, Math.min(Math.ceil(R / G), 65536));
+  const cap = (o.tuning && o.tuning.blocks) || 65536;
+  const groups = Math.max(1, Math.min(Math.ceil(R / G), cap));
   return { name: k.name, source: k.source, params: Uint32Array.from(params), grid: [groups, 1, 1], block: [BLOCK, 1, 1], lds: 0, workspace: 0 };
 }
 
