@@ -150,7 +150,10 @@ def main() -> None:
                             "resident_steps_per_sec": t["residentStepsPerSec"], "resident_ms_per_step": t["residentMsPerStep"],
                             "launches": t["launches"], "fused_us": t["fused"]["median"], "unfused_us": t["unfused"]["median"],
                             "speedup_vs_unfused": t["verdict"]["speedup"], "matmul_TFLOPs_resident": t["matmulTflopsResident"],
-                            "loss": t["lossLast"], "time_by_kind_us": {k: round(v["us"], 1) for k, v in t["byKind"].items()}}
+                            "loss": t["lossLast"], "time_by_kind_us": {k: round(v["us"], 1) for k, v in t["byKind"].items()},
+                            "arena": {"bytes": t["arena"]["bytes"], "unshared_bytes": t["arena"]["unshared"],
+                                      "steps_per_sec": t["arena"]["stepsPerSec"],
+                                      "resident_steps_per_sec": t["arena"]["residentStepsPerSec"]}}
     if "sweep" in cfg:
         sw = cfg["sweep"]
         extra["workload_sweep"] = {

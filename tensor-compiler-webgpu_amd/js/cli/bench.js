@@ -308,8 +308,23 @@ function trainStep(runner, bench, name, req, opts) {
   }
   pu.destroy();
   trainer.destroy();
+  // The same trainer with its intermediate buffers in a liveness arena.
+  const ta = new HipTrainer(runner, fs, m.params, m.state, { graph: bench.graphs, arena: true });
+  for (let i = 0; i < W; i++) ta.train(batch.x, batch.y);
+  const ta0 = process.hrtime.bigint();
+  for (let i = 0; i < K; i++) ta.train(batch.x, batch.y);
+  const arenaWallMs = Number(process.hrtime.bigint() - ta0) / 1e6 / K;
+  runner.a.sync();
+  runner.a.eventRecord(bench.start);
+  for (let i = 0; i < K; i++) ta.advance();
+  runner.a.eventRecord(bench.end);
+  const arenaResidentMs = runner.a.eventElapsed(bench.start, bench.end) / K;
+  const plan = ta.program.arena;
+  const arena = { bytes: plan.size, unshared: plan.unshared, msPerStep: arenaWallMs, residentMsPerStep: arenaResidentMs,
+    stepsPerSec: 1e3 / arenaWallMs, residentStepsPerSec: 1e3 / arenaResidentMs };
+  ta.destroy();
   const flops = fs.lowered.launches.reduce((q, l) => q + (l.flops || 0), 0);
-  return { config: name, info: m.info, steps: K, warmup: W, lossLast: loss,
+  return { config: name, info: m.info, steps: K, warmup: W, lossLast: loss, arena,
     stepsPerSec: 1e3 / wallMs, msPerStep: wallMs, residentMsPerStep: residentMs, residentStepsPerSec: 1e3 / residentMs,
     launches: { fused: fs.lowered.launches.length, unfused: lu.launches.length },
     fused: t.stats.fused, unfused: t.stats.unfused, verdict: verdict(t.stats.unfused, t.stats.fused),

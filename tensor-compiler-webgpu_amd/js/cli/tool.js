@@ -567,7 +567,8 @@ async function gpuTrain(req) {
   const m = modelStep(req);
   const fs = fusedStep(m.step);
   const runner = HipRunner.create();
-  const trainer = new HipTrainer(runner, fs, m.params, m.state, { graph: !!req.graph });
+  const trainer = new HipTrainer(runner, fs, m.params, m.state, { graph: !!req.graph, arena: !!req.arena });
+  const plan = trainer.program.arena;
   const losses = [];
   let identical = null;
   const names = Object.keys(Object.assign({}, m.params, m.state));
@@ -601,7 +602,8 @@ async function gpuTrain(req) {
   if (params) for (const k of Object.keys(params)) params[k] = Array.from(params[k]);
   trainer.destroy();
   return { losses, identical, params, launches: fs.lowered.launches.length, checkedLaunches: fs.checked.launches.length,
-    folded: fs.lowered.folded.length, aliases: fs.lowered.aliases.length, unfusedNodes: m.step.graph.nodes.length, info: m.info };
+    folded: fs.lowered.folded.length, aliases: fs.lowered.aliases.length, unfusedNodes: m.step.graph.nodes.length, info: m.info,
+    arena: plan ? { bytes: plan.size, unshared: plan.unshared, buffers: plan.buffers.length } : null };
 }
 
 async function main() {
@@ -708,6 +710,54 @@ async function main() {
         c3: (req.c3 || []).map((c) => { const g = cfg.c3Graphs(c.fn, c.R, c.C); return { fn: c.fn, R: c.R, C: c.C, forward: one(g.forward), gradient: one(g.gradient) }; }),
         c4: (req.c4 || []).map((c) => { const g = cfg.c4Graphs(c.act, c.M, c.K, c.N); return { act: c.act, M: c.M, K: c.K, N: c.N, forward: one(g.forward), gradient: one(g.gradient) }; }),
       };
+      break;
+    }
+    case 'arena-check': {
+      // Arena plans of model steps and corpus programs (perf lowering), checked by running
+      // each launch list abstractly over the arena's bytes.
+      const { planArena } = require('../src/mi355x/arena');
+      const { simulateArena, peakLive } = require('../src/testing/arena_check');
+      const one = (name, graph, keep) => {
+        const lowered = lowerMI355X(graph, { perf: true, keep });
+        const plan = planArena(graph, lowered, { keep });
+        const res = { name, launches: lowered.launches.length, buffers: plan.buffers.length, bytes: plan.size,
+          unshared: plan.unshared, peak: peakLive(lowered, plan), check: simulateArena(graph, lowered, plan) };
+        if (req.plant) {
+          // A planted mistake: one buffer moved onto another that is live at the same
+          // time (the first such pair); the simulation must refuse the plan.
+          const bs = plan.buffers;
+          let pair = null;
+          for (const a of bs) {
+            if (a.pinned) continue;
+            const b = bs.find((x) => x !== a && x.lo <= a.hi && a.lo <= x.hi && x.bytes >= a.bytes);
+            if (b) { pair = [a, b]; break; }
+          }
+          if (pair) {
+            const saved = pair[0].offset;
+            pair[0].offset = pair[1].offset;
+            res.planted = { moved: pair[0].id, onto: pair[1].id, check: simulateArena(graph, lowered, plan) };
+            pair[0].offset = saved;
+          }
+        }
+        return res;
+      };
+      out = [];
+      const { modelStep } = require('../src/builders/models');
+      const { fusedStep } = require('../src/mi355x/trainer');
+      for (const r of req.models || []) {
+        const m = modelStep(r);
+        const f = fusedStep(m.step);
+        out.push(one(`${r.model}-${r.B || ''}`, f.graph, [f.loss, f.logits].concat(Object.values(f.outputs))));
+      }
+      if (req.corpus) {
+        const { corpusGraphs } = require('../src/testing/random_graph');
+        for (let i = req.corpus.from; i <= req.corpus.to; i++) {
+          for (const c of corpusGraphs(i)) {
+            const f = fuse(c.graph, { keep: c.keep });
+            out.push(one(`corpus-${i}-${c.label}`, f.graph, c.keep.map((id) => f.index.get(id))));
+          }
+        }
+      }
       break;
     }
     case 'perf-lower': {

@@ -16,6 +16,8 @@
 // prepare(graph, lowered) makes a Program: buffers, packed argument blocks and
 // function handles made once, then run() issues every launch with one native
 // call (or replays a captured HIP graph) — what the trainer and bench use.
+// With { arena: { keep } } its node buffers are placed by live range in one
+// allocation (arena.js): only inputs, constants and `keep` stay readable.
 
 const crypto = require('crypto');
 const fs = require('fs');
@@ -24,6 +26,7 @@ const { size } = require('../ir/shapes');
 const { addon, CACHE } = require('./addon');
 const { kernelSources } = require('./lower');
 const { MAX_IN, MAX_P } = require('./codegen');
+const { planArena } = require('./arena');
 
 const CANARY_BITS = 0xdeadbeef;
 const CANARY_PAD = 256;           // words past the end of every buffer
@@ -306,7 +309,12 @@ class HipRunner {
 }
 
 class Program {
-  constructor(runner, graph, lowered, { only, buffers } = {}) {
+  /**
+   * options.only: launch filter; options.buffers: node buffers to use (device addresses,
+   * owned by the caller); options.arena: { keep } to place the buffers by live range in
+   * one allocation, or an arena plan of the same launch list that `buffers` follows.
+   */
+  constructor(runner, graph, lowered, { only, buffers, arena } = {}) {
     requirePad(lowered, false);
     const a = runner.a;
     this.a = a;
@@ -316,8 +324,23 @@ class Program {
     this.n = graph.nodes.map((node) => size(node.shape));
     const { alias, folded } = sharing(lowered);
     this.owned = [];
-    if (buffers) this.bufs = buffers.slice();
-    else {
+    this.arena = null;
+    if (buffers) {
+      this.bufs = buffers.slice();
+      if (arena && arena.offsets) this.arena = arena;
+    } else if (arena) {
+      if (only) throw new Error('an arena is planned over the whole launch list: no launch filter');
+      const plan = planArena(graph, lowered, { keep: arena.keep });
+      const base = runner.alloc(plan.size);
+      this.owned.push(base);
+      this.arena = plan;
+      this.bufs = [];
+      for (const node of graph.nodes) {
+        if (alias.has(node.id)) this.bufs.push(this.bufs[alias.get(node.id)]);
+        else if (folded.has(node.id)) this.bufs.push(0);
+        else this.bufs.push(base + plan.offsets.get(node.id));
+      }
+    } else {
       this.bufs = [];
       for (const node of graph.nodes) {
         if (alias.has(node.id)) this.bufs.push(this.bufs[alias.get(node.id)]);
@@ -353,10 +376,21 @@ class Program {
     this.graphHandle = 0;
   }
 
-  write(id, data) { this.a.h2d(this.bufs[id], 0, data instanceof Float32Array ? data : Float32Array.from(data)); }
+  /** Throw unless node `id` keeps its own bytes across the launches (always, without an arena). */
+  persistent(id, what) {
+    if (this.arena && !this.arena.pinned.has(this.arena.owner(id))) {
+      throw new Error(`node ${id} cannot be ${what}: its arena bytes are reused by later launches (add it to keep)`);
+    }
+  }
+
+  write(id, data) {
+    this.persistent(id, 'written');
+    this.a.h2d(this.bufs[id], 0, data instanceof Float32Array ? data : Float32Array.from(data));
+  }
 
   read(id) {
     if (!this.bufs[id]) throw new Error(`node ${id} is not materialised (a transpose folded into its matmuls)`);
+    this.persistent(id, 'read');
     const out = new Float32Array(this.n[id]);
     this.a.d2h(this.bufs[id], 0, out);
     return out;

@@ -15,7 +15,9 @@
 // a step is its launches alone — no copies — and, with `graph`, the replay of
 // one captured HIP graph. train(x, y) writes the batch, enqueues the step and
 // reads back only the loss (one sync per step); read(names) returns current
-// values; destroy() frees everything.
+// values; destroy() frees everything. With `arena`, every buffer but the
+// parameters, state, batch, loss and logits is placed by live range in one
+// allocation (arena.js), shared by both programs.
 
 const { fuse } = require('../fusion/fuse');
 const { lowerMI355X } = require('./lower');
@@ -46,14 +48,17 @@ function fusedStep(step, options) {
 class HipTrainer {
   /**
    * `step` from fusedStep (or an unfused step with `lowered`); `params`/`state`
-   * map names to values; options.graph: replay each step as a captured HIP graph.
+   * map names to values; options.graph: replay each step as a captured HIP graph;
+   * options.arena: place the step's other buffers by live range in one allocation.
    */
   constructor(runner, step, params, state, options) {
+    const o = options || {};
     this.runner = runner;
     this.a = runner.a;
     this.step = step;
-    this.graph = !!(options && options.graph);
-    const first = runner.prepare(step.graph, step.lowered);
+    this.graph = !!o.graph;
+    const keep = [step.loss, step.logits].concat(Object.values(step.outputs));
+    const first = runner.prepare(step.graph, step.lowered, o.arena ? { arena: { keep } } : {});
     const cot = step.graph.inputId(step.cotangent);
     if (cot === undefined) throw new Error(`the step has no cotangent input '${step.cotangent}'`);
     first.write(cot, new Float32Array([1]));
@@ -72,7 +77,7 @@ class HipTrainer {
       bufs[from] = first.bufs[to];
     }
     for (const [node, source] of step.lowered.aliases || []) bufs[node] = bufs[source];
-    const second = runner.prepare(step.graph, step.lowered, { buffers: bufs });
+    const second = runner.prepare(step.graph, step.lowered, { buffers: bufs, arena: first.arena });
     this.programs = [first, second];
     this.turn = 0;   // the program the next step runs; its parameter inputs hold the current values
     this.lossBuf = new Float32Array(1);

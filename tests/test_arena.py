@@ -1,0 +1,34 @@
+"""The liveness arena of the perf path (js/src/mi355x/arena.js), checked on the CPU.
+
+Every plan is run abstractly over the arena's bytes (js/src/testing/arena_check.js):
+each launch must find its operands still holding their own values, must not write over
+an operand it reads, and every pinned buffer (inputs, constants, kept outputs) must
+survive to the end. The plan's size is compared with the peak of live bytes over the
+launch list, which no placement can go under. The GPU side (the trainer with an arena,
+bit for bit the checked path) is in test_gpu_train.py."""
+
+MODELS = [{"model": "transformer", "B": 64}, {"model": "transformer", "B": 1}, {"model": "mlp"},
+          {"model": "transformer-ref"}]
+
+
+def test_arena_plans_keep_every_value_until_its_last_use(tool):
+    res = tool("arena-check", {"models": MODELS, "corpus": {"from": 1, "to": 300}})
+    assert len(res) == len(MODELS) + 600
+    bad = [r for r in res if not r["check"]["ok"]]
+    assert not bad, bad[:3]
+    for r in res:
+        # First fit by decreasing size lands within a few granules of the lower bound here.
+        assert r["peak"] <= r["bytes"] <= max(256, r["peak"]) * 1.01 + 4096, r
+        assert r["bytes"] <= r["unshared"]
+    c5 = next(r for r in res if r["name"] == "transformer-64")
+    # Config 5's step: 2.42 GB of node buffers in 0.90 GB.
+    assert c5["bytes"] < 0.4 * c5["unshared"], c5
+
+
+def test_a_planted_overlap_is_caught(tool):
+    """One buffer moved onto another that is live at the same time: the simulation refuses
+    every such plan (the check is not the planner's own interval arithmetic)."""
+    res = tool("arena-check", {"models": MODELS[:1] + MODELS[2:3], "corpus": {"from": 1, "to": 50}, "plant": True})
+    planted = [r for r in res if "planted" in r]
+    assert len(planted) > 50
+    assert all(not r["planted"]["check"]["ok"] for r in planted), [r["name"] for r in planted if r["planted"]["check"]["ok"]]

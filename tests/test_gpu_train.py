@@ -88,17 +88,19 @@ def test_c1_first_step_against_composed_budget(tool):
     assert j["pass"], j["first"]
 
 
-@pytest.mark.parametrize("graph", [False, True])
-def test_c1_trainer_consistency_and_learning(tool, graph):
+@pytest.mark.parametrize("graph,arena", [(False, False), (True, False), (False, True)])
+def test_c1_trainer_consistency_and_learning(tool, graph, arena):
     """20 fused-trainer steps on one batch: each equals the checked path (runner.run of the
     plain lowering, one launch per node, with the new values fed back by the host) bit for
     bit — the trainer runs the perf lowering, whose matmuls read transposed operands in
     place — and the loss falls at every step. With `graph`, each step is the replay of a
     captured HIP graph (two graphs, the parameters' buffers exchanging roles), and every
-    replay is checked against the eager path, with the host's synchronisation between."""
+    replay is checked against the eager path, with the host's synchronisation between.
+    With `arena`, the step's intermediate buffers share one allocation by live range."""
     r = tool("gpu-train", {"model": "mlp", "steps": 20, "consistency": True, "consistencySteps": 20, "sameBatch": True,
-                           "graph": graph})
+                           "graph": graph, "arena": arena})
     assert r["identical"] is True
+    assert (r["arena"] is not None) == arena
     losses = r["losses"]
     assert all(np.isfinite(losses))
     # Plain SGD at lr 0.1 on one batch: every step lowers the loss, by 0.2 over the 20.
@@ -106,14 +108,18 @@ def test_c1_trainer_consistency_and_learning(tool, graph):
     assert losses[-1] < losses[0] - 0.2, losses
 
 
-@pytest.mark.parametrize("graph", [False, True])
-def test_c5_full_size_trainer(tool, graph):
-    """Config 5 at full size (B 64): the fused trainer's first 3 steps (perf lowering: 88
-    transposes read in place by their matmuls, 37 reshapes sharing buffers) equal the checked
+@pytest.mark.parametrize("graph,arena", [(False, False), (True, False), (False, True), (True, True)])
+def test_c5_full_size_trainer(tool, graph, arena):
+    """Config 5 at full size (B 64): the fused trainer's first 3 steps (perf lowering:
+    transposes read in place by their matmuls, reshapes sharing buffers) equal the checked
     path (plain lowering) bit for bit, and the initial loss is near ln(96) (small initial
-    weights, uniform tokens)."""
+    weights, uniform tokens). With `arena`, every buffer but the parameters, batch, loss
+    and logits is placed by live range in one allocation (2.4 GB of node buffers in
+    0.9 GB), and the steps are still bit for bit the checked path's."""
     r = tool("gpu-train", {"model": "transformer", "B": 64, "steps": 3, "consistency": True, "consistencySteps": 3,
-                           "graph": graph}, timeout=600)
+                           "graph": graph, "arena": arena}, timeout=600)
     assert r["identical"] is True
     assert r["folded"] > 0 and r["aliases"] > 0 and r["launches"] < r["checkedLaunches"]
     assert abs(r["losses"][0] - np.log(96)) < 0.1, r["losses"]
+    if arena:
+        assert r["arena"]["bytes"] < 0.5 * r["arena"]["unshared"], r["arena"]
