@@ -108,7 +108,7 @@ def main() -> None:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--configs", default="ceiling,c2,c3,c4,c1,c5,sweep")
+    ap.add_argument("--configs", default="ceiling,c2,c3,c4,c1,c5,attention,sweep")
     ap.add_argument("--programs", type=int, default=8)
     ap.add_argument("--quick", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -154,6 +154,15 @@ def main() -> None:
                             "arena": {"bytes": t["arena"]["bytes"], "unshared_bytes": t["arena"]["unshared"],
                                       "steps_per_sec": t["arena"]["stepsPerSec"],
                                       "resident_steps_per_sec": t["arena"]["residentStepsPerSec"]}}
+    if "attention" in cfg:
+        extra["attention_extension"] = {
+            r["name"]: {"contract_us": r["contract"]["median"], "attention_us": r["attention"]["median"],
+                        "speedup": r["verdict"]["speedup"], "verdict": r["verdict"]["verdict"], "launches": r["launches"],
+                        "max_abs_diff_logits": r["maxAbsDiffLogits"],
+                        "kernel_us": sum(g["kernelUs"] for g in r["groups"]) / len(r["groups"]),
+                        "replaced_launches_us": sum(g["replacedUs"] for g in r["groups"]) / len(r["groups"]),
+                        "kernel_TFLOPs": sum(g["tflops"] for g in r["groups"]) / len(r["groups"])}
+            for r in cfg["attention"]["results"]}
     if "sweep" in cfg:
         sw = cfg["sweep"]
         extra["workload_sweep"] = {

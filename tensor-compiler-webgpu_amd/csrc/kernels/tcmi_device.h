@@ -136,6 +136,16 @@ __device__ __forceinline__ float group_reduce(float v) {
   return __shfl(v, 0, L);
 }
 
+// Reduce across the four lanes t, t + 16, t + 32, t + 48 of a wavefront: the
+// lane groups of a 16 x 16 matrix-core tile that together hold one row of it.
+// Every one of the four takes lane t's result, so all hold the same bits.
+template <bool IsMax>
+__device__ __forceinline__ float quad16_reduce(float v) {
+  v = combine<IsMax>(v, __shfl_xor(v, 16, 64));
+  v = combine<IsMax>(v, __shfl_xor(v, 32, 64));
+  return __shfl(v, static_cast<int>(threadIdx.x & 15u), 64);
+}
+
 // Reduce over a workgroup of THREADS (a multiple of 64); every thread gets the
 // result. `scratch` holds THREADS/64 floats of LDS; it is reused across calls,
 // hence the barrier before returning.

@@ -209,6 +209,60 @@ function launchRecords(lowered) {
     kernels: l.kernels.map((k) => k.name), bytes: l.bytes, flops: l.flops || 0 }));
 }
 
+/**
+ * The attention extension on the transformer's forward pass (config 5's structure
+ * at batch 64, and the reference's at batch 16): the contract's fusion (matmul,
+ * softmax group, matmul per attention) against fuse(..., { attention: true }) (one
+ * kernel per attention), ABBA-timed in the perf lowering, with each attention
+ * kernel's own duration against the three launches it replaces.
+ */
+function attention(runner, bench, opts) {
+  const tf = require('../src/builders/transformer');
+  const { Rng } = require('../src/testing/rng');
+  const results = [];
+  const cases = [['c5-forward', tf.C5_CONFIG, 96, opts.quick ? 8 : 64], ['reference-forward', tf.REFERENCE_CONFIG, 16, 16]];
+  for (const [name, cfg, V, B] of cases) {
+    log(`attention ${name}`);
+    const fwd = tf.buildForward(V, B, cfg);
+    const keep = [fwd.logits, fwd.loss];
+    const inputs = {};
+    const init = tf.initParams(V, 1, cfg);
+    for (const k of Object.keys(init)) inputs[k] = Float32Array.from(init[k]);
+    const rng = new Rng(V * 1000 + B);
+    const rows = B * cfg.T;
+    const onehot = () => { const a = new Float32Array(rows * V); for (let i = 0; i < rows; i++) a[i * V + rng.int(0, V - 1)] = 1; return a; };
+    inputs.x = onehot();
+    inputs.y = onehot();
+    const fc = fuse(fwd.graph, { keep });
+    const fa = fuse(fwd.graph, { keep, attention: true });
+    const lc = lowerMI355X(fc.graph, { perf: true, keep: keep.map((id) => fc.index.get(id)) });
+    const la = lowerMI355X(fa.graph, { perf: true, keep: keep.map((id) => fa.index.get(id)) });
+    runner.functions([lc, la]);
+    const pc = prepared(runner, fc.graph, lc, inputs);
+    const pa = prepared(runner, fa.graph, la, inputs);
+    const t = bench.time({ contract: pc, attention: pa }, { reps: opts.reps });
+    const tc = timeLaunches(runner, bench, pc), ta = timeLaunches(runner, bench, pa);
+    pc.run(); pa.run(); pc.sync();
+    const yc = pc.read(fc.index.get(fwd.logits)), ya = pa.read(fa.index.get(fwd.logits));
+    let maxDiff = 0;
+    for (let i = 0; i < yc.length; i++) maxDiff = Math.max(maxDiff, Math.abs(yc[i] - ya[i]));
+    const usOf = (launches, node) => { const l = launches.find((x) => x.node === node); return l ? l.us : 0; };
+    const groups = fa.attention.map((g) => {
+      const kernel = ta.find((x) => x.node === fa.index.get(g.sink));
+      let replaced = 0;
+      for (const m of g.members) if (fc.index.has(m)) replaced += usOf(tc, fc.index.get(m));
+      return { sink: g.sink, kernelUs: kernel.us, replacedUs: replaced, speedup: replaced / kernel.us,
+        tflops: kernel.flops / (kernel.us * 1e6), code: kernel.code };
+    });
+    pc.destroy();
+    pa.destroy();
+    results.push({ name, B, launches: { contract: lc.launches.length, attention: la.launches.length },
+      contract: t.stats.contract, attention: t.stats.attention, verdict: verdict(t.stats.contract, t.stats.attention),
+      maxAbsDiffLogits: maxDiff, groups });
+  }
+  return { config: 'attention', results };
+}
+
 function c3(runner, bench, opts) {
   const R = opts.quick ? 2048 : cfg.C3_SHAPE[0], C = cfg.C3_SHAPE[1];
   const { x, dy, shifted } = cfg.c3Inputs(R, C);
@@ -423,7 +477,7 @@ async function main() {
   const opts = { quick: flag('quick'), reps: arg('reps') ? Number(arg('reps')) : undefined };
   const which = arg('configs', 'ceiling,c2,c3,c4,c1,c5').split(',');
   const out = { device: runner.info(), peaks: { hbmGBs: HBM_PEAK_GBS, fp32MfmaTFLOPs: FP32_MFMA_PEAK_TFLOPS }, configs: {} };
-  const fns = { c2, c3, c4, c1, c5, ceiling, sweep };
+  const fns = { c2, c3, c4, c1, c5, ceiling, sweep, attention };
   for (const c of which) {
     if (!fns[c]) throw new Error(`unknown config ${c}`);
     const t0 = Date.now();

@@ -26,6 +26,7 @@ const fs = require('fs');
 const fs_ = fs;
 const path = require('path');
 const { Graph } = require('../src/ir/graph');
+const { size } = require('../src/ir/shapes');
 const { grad } = require('../src/autodiff');
 const { fuse, fusionSummary } = require('../src/fusion/fuse');
 const { lowerMI355X } = require('../src/mi355x/lower');
@@ -95,6 +96,64 @@ function transformerInit(req) {
     params, x: Array.from(x), y: Array.from(y) };
 }
 
+// Attention graphs of the GPU tests: [B, H, TQ, TK, DH, DV], options, and whether the
+// attention kernel takes them (the last is past its key limit and stays three launches).
+const ATTENTION_CASES = [
+  { name: 'ragged', dims: [2, 3, 37, 45, 20, 12], scale: 0.2, mask: true, fuses: true },
+  { name: 'per-element', dims: [1, 2, 19, 33, 18, 10], scale: 0.25, mask: true, fuses: true },
+  { name: 'query-blocks', dims: [2, 2, 130, 256, 32, 32], scale: 0.18, fuses: true },
+  { name: 'pre-transposed', dims: [2, 2, 64, 64, 32, 32], scale: 0.18, mask: true, kTransposed: true, vTransposed: true, fuses: true },
+  { name: 'too-many-keys', dims: [1, 1, 8, 1024, 16, 16], scale: 0.25, fuses: false },
+];
+
+/**
+ * Scaled-dot-product attention graphs built with the IR builder:
+ * o = softmax(q · kᵀ · scale + mask) · v, k (and v) optionally given already
+ * transposed; inputs uniform in [-2, 2] from a seeded generator.
+ */
+function attentionGraphs(cases) {
+  const { Rng } = require('../src/testing/rng');
+  return cases.map((c) => {
+    const g = new Graph();
+    const [B, H, TQ, TK, DH, DV] = c.dims;
+    const q = g.input('q', [B, H, TQ, DH]);
+    const kt = c.kTransposed ? g.input('kt', [B, H, DH, TK]) : g.transpose(g.input('k', [B, H, TK, DH]), [0, 1, 3, 2]);
+    const v = c.vTransposed ? g.transpose(g.input('vt', [B, H, DV, TK]), [0, 1, 3, 2]) : g.input('v', [B, H, TK, DV]);
+    let s = g.matmul(q, kt);
+    if (c.scale) s = g.mul(s, g.const(c.scale));
+    if (c.mask) {
+      const m = [];
+      for (let i = 0; i < TQ; i++) for (let j = 0; j < TK; j++) m.push(j > i + (TK - TQ) ? -1e4 : 0);
+      s = g.add(s, g.const(m, [TQ, TK]));
+    }
+    const o = g.matmul(g.softmax(s, 3), v);
+    const rng = new Rng(c.seed || 7);
+    const inputs = {};
+    for (const n of g.inputs()) inputs[n.attrs.name] = rng.array(size(n.shape), -2, 2);
+    return { name: c.name, fuses: c.fuses, graph: g.toJSON(), keep: [o], inputs };
+  });
+}
+
+/**
+ * The transformer's forward graph (reference or config-5 structure) with its
+ * parameters (initParams) and one batch of one-hot tokens and targets.
+ */
+function transformerForward(req) {
+  const cfg = req.config === 'c5' ? tf.C5_CONFIG : tf.REFERENCE_CONFIG;
+  const V = req.V || 16, B = req.B || 2;
+  const fwd = tf.buildForward(V, B, cfg);
+  const inputs = {};
+  const init = tf.initParams(V, req.seed || 1, cfg);
+  for (const k of Object.keys(init)) inputs[k] = Array.from(init[k]);
+  const { Rng } = require('../src/testing/rng');
+  const rng = new Rng(req.seed || 1);
+  const rows = B * cfg.T;
+  const onehot = () => { const a = new Array(rows * V).fill(0); for (let i = 0; i < rows; i++) a[i * V + rng.int(0, V - 1)] = 1; return a; };
+  inputs.x = onehot();
+  inputs.y = onehot();
+  return { graph: fwd.graph.toJSON(), keep: [fwd.logits, fwd.loss], inputs };
+}
+
 /** Compile, offline, the kernels a named group of GPU runs will ask for (same module text as on the box). */
 function precompileGroup(group, arch, shard, shards) {
   const { precompile } = require('../src/mi355x/runner');
@@ -149,6 +208,26 @@ function precompileGroup(group, arch, shard, shards) {
         const f = fuse(m.graph, { keep: m.outputs, recompute: v === 'recompute' });
         lists.push(lowerMI355X(f.graph, { perf: true, keep: m.outputs.map((id) => f.index.get(id)) }));
       }
+    }
+    return precompile(lists, arch);
+  }
+  if (group === 'attention') {
+    // The attention GPU tests' graphs (fused with and without the extension, plain and
+    // perf lowerings) and the bench's forward passes.
+    const graphs = attentionGraphs(ATTENTION_CASES).map((c) => ({ graph: Graph.fromJSON(c.graph), keep: c.keep }));
+    const att = builderCases().find((c) => c.name === 'attention');
+    graphs.push({ graph: Graph.fromJSON(att.graph), keep: att.outputs });
+    for (const [config, V, B] of [['reference', 16, 2], ['reference', 16, 16], ['c5', 96, 2], ['c5', 96, 64]]) {
+      const fw = transformerForward({ config, V, B });
+      graphs.push({ graph: Graph.fromJSON(fw.graph), keep: fw.keep });
+    }
+    const lists = [];
+    for (const { graph, keep } of graphs) {
+      for (const attention of [false, true]) {
+        const f = fuse(graph, { keep, attention });
+        lists.push(lowerMI355X(f.graph), lowerMI355X(f.graph, { perf: true, keep: keep.map((id) => f.index.get(id)) }));
+      }
+      lists.push(lowerMI355X(graph, { perf: true, keep }));
     }
     return precompile(lists, arch);
   }
@@ -223,10 +302,11 @@ async function gpuGraphs(req, dir) {
     const g = Graph.fromJSON(c.graph);
     const inputs = {};
     for (const n of g.inputs()) inputs[n.attrs.name] = Float32Array.from(c.inputs[n.attrs.name]);
-    const f = fuse(g, { keep: c.keep || [] });
+    const f = fuse(g, { keep: c.keep || [], attention: !!c.attention });
     const lf = lowerMI355X(f.graph);
     const rf = await runner.run(f.graph, lf, inputs, { canary: true });
-    const entry = { name: c.name, fused: f.graph.toJSON(), origin: f.origin, gpuFused: {}, canaryFused: rf.canaryIntact };
+    const entry = { name: c.name, fused: f.graph.toJSON(), origin: f.origin, gpuFused: {}, canaryFused: rf.canaryIntact,
+      kinds: lf.launches.map((l) => l.kind) };
     f.graph.nodes.forEach((n) => { entry.gpuFused[n.id] = bundle.put(rf.values[n.id]); });
     if (c.perf) {
       // The perf lowering: transposes read in place by the matmuls, reshapes sharing buffers.
@@ -236,7 +316,8 @@ async function gpuGraphs(req, dir) {
       entry.gpuPerf = {};
       for (const id of keepF) entry.gpuPerf[id] = bundle.put(rp.values[id]);
       entry.perfFolded = lp.folded;
-      entry.perfModes = lp.launches.filter((l) => l.flops).map(gemmModes);
+      entry.perfModes = lp.launches.filter((l) => l.flops && l.kind !== 'fused-attention').map(gemmModes);
+      entry.perfViews = lp.launches.filter((l) => l.kind === 'fused-attention').map((l) => Object.keys(l.views || {}).sort());
       entry.canaryPerf = rp.canaryIntact.every(Boolean);
     }
     if (c.unfused) {
@@ -624,7 +705,7 @@ async function main() {
       out = req.graphs.map((c) => {
         const g = Graph.fromJSON(c.graph);
         try {
-          const f = fuse(g, { keep: c.keep || [], recompute: !!c.recompute, sabotage: c.sabotage });
+          const f = fuse(g, { keep: c.keep || [], recompute: !!c.recompute, sabotage: c.sabotage, attention: !!c.attention });
           return Object.assign({ name: c.name, summary: fusionSummary(g, f) }, fusedOut(f));
         } catch (e) {
           return { name: c.name, error: String(e.message) };
@@ -760,6 +841,8 @@ async function main() {
       }
       break;
     }
+    case 'attention-graphs': out = attentionGraphs(req.cases || ATTENTION_CASES); break;
+    case 'transformer-forward': out = transformerForward(req); break;
     case 'perf-lower': {
       // The perf lowering of a model step or of a graph: launches, aliases, folded nodes, operand views.
       let g, keep;

@@ -205,11 +205,20 @@ function bodyOf(node) {
 
 /**
  * Fuse `graph`. Options: patterns, recompute (false), keep (ids that must
- * survive), maxOperands (6), sabotage ('fusion-absorbs-shared').
+ * survive), maxOperands (6), sabotage ('fusion-absorbs-shared'), and
+ * attention (false: this backend's extension, attention.js, applied after the
+ * contract's own pass).
  * Returns { graph, origin, index, groups }: origin[newId] = original id, and
  * index maps each surviving original id to its new id (fuse.js:215-292).
  */
 function fuse(graph, options) {
+  const o = options || {};
+  const fused = fuseContract(graph, o);
+  if (!o.attention) return fused;
+  return require('./attention').fuseAttention(fused, { keep: o.keep });
+}
+
+function fuseContract(graph, options) {
   const o = options || {};
   const patterns = o.patterns || PATTERNS;
   const recompute = !!o.recompute;

@@ -802,5 +802,193 @@ ${indent(lines, '    ')}
     lds: 0, workspace, flops: 2 * batch * M * N * K, tiling: tl, modes: [av.mode, bv.mode] };
 }
 
-module.exports = { elementwiseKernel, rowwiseKernel, colreduceKernels, gemmKernel, gemmTiling, classifyGather, gatherStrides, literal, fnv,
-  Emitter, WG, MAX_P, MAX_IN };
+// ---- attention (the fusion extension of fusion/attention.js) ------------------------
+
+/**
+ * A fused attention node's body: a0 = Q [batch, TQ, DH], a1 = Kt [batch, DH, TK],
+ * scores = matmul(a0, a1), the score body (elementwise ops and last-axis
+ * reductions over the scores and further operands), then matmul(P, V) with V the
+ * last operand — the body's output. One workgroup per (16·W query rows, batch
+ * index), W = min(8, ceil(TQ / 16)) wavefronts, over tcmi_attention.h: the body below runs on the score registers, its
+ * reductions across each row's four lanes. `views` ({ q, k, v }) read those
+ * operands in place through strided views of other buffers (`sizes`: their
+ * element counts, against which every view is proved in bounds).
+ */
+function attentionKernel(b, output, opts) {
+  const o = opts || {};
+  checkOperands(b);
+  const m2 = b.nodes[output];
+  const m1 = b.nodes.find((n) => n.op === 'matmul' && n.id !== output);
+  if (m2.op !== 'matmul' || !m1) throw new Error('attention body: expected matmul(body(matmul(Q, Kt)), V)');
+  const operandOf = (id) => {
+    const n = b.nodes[id];
+    if (n.op !== 'input') throw new Error('attention body: the products\' operands must be body inputs');
+    return Number(n.attrs.name.slice(1));
+  };
+  const iq = operandOf(m1.inputs[0]), ik = operandOf(m1.inputs[1]), iv = operandOf(m2.inputs[1]);
+  const qs = b.nodes[m1.inputs[0]].shape, ks = b.nodes[m1.inputs[1]].shape, vs = b.nodes[m2.inputs[1]].shape;
+  const r = qs.length;
+  const batchDims = qs.slice(0, r - 2);
+  const batch = size(batchDims), TQ = qs[r - 2], DH = qs[r - 1], TK = ks[r - 1], DV = vs[r - 1];
+  if (batch * TQ * TK >= 2 ** 31 || batch * TQ * DV >= 2 ** 31) throw new Error('attention exceeds the 32-bit index space');
+  if (batch > 65535) throw new Error(`attention batch ${batch} exceeds the grid`);
+  const sOut = m2.inputs[0];
+  const reductions = b.nodes.filter((n) => isReduce(n) && n.id > m1.id && n.id < m2.id);
+  for (const rd of reductions) {
+    const src = b.nodes[rd.inputs[0]].shape;
+    if (rd.attrs.axis !== src.length - 1 || size(src) !== batch * TQ * TK) throw new Error('attention body: reductions must be over the keys');
+  }
+  const R = batch * TQ, C = TK;
+  const params = [batch, TQ, DH, TK, DV];
+  const rowTier = (id) => size(b.nodes[id].shape) === R && size(b.nodes[id].shape) !== R * C;
+  if (size(b.nodes[sOut].shape) !== R * C) throw new Error('attention body: P must cover every score');
+
+  const reduced = new Map();
+  const rowLines = [];
+  const caches = new Map();
+  const cacheFill = [];
+  const NT = Math.ceil(TK / 16);
+  let em;
+  const ROW = { key: 'r', idx: 'r', root: false, row: true, limit: R };
+  const elemCtx = () => ({ key: 'e', idx: 'e', root: true, limit: R * C });
+  em = new Emitter(b, params, {
+    special(id, ctx) {
+      if (id === m1.id) {
+        if (ctx.row || !ctx.root) throw new Error('attention body: the scores are read at their own index only');
+        return 'sacc[jt][l]';
+      }
+      if (reduced.has(id)) return reduced.get(id);
+      const n = b.nodes[id];
+      if (!ctx.row && rowTier(id) && n.op !== 'input' && n.op !== 'const') return em.value(id, ROW, rowLines);
+      if (n.op === 'broadcast' && !ctx.row && rowTier(n.inputs[0])) {
+        const src = b.nodes[n.inputs[0]];
+        if (src.op !== 'input' && src.op !== 'const') return em.value(src.id, ROW, rowLines);
+      }
+      return undefined;
+    },
+    load(k, ctx, lines) {
+      if (ctx.key.startsWith('e')) {
+        // An operand read at a score's index (directly or through gathers): loaded once,
+        // for every score of the lane, into registers that every phase reads.
+        const ck = `${k}|${ctx.idx}`;
+        if (!caches.has(ck)) {
+          const c = `C${caches.size}`;
+          caches.set(ck, c);
+          cacheFill.push(`float ${c}[${NT}][4];`, `#pragma unroll
+for (int jt = 0; jt < ${NT}; ++jt) {
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    const uint32_t c = 16u * jt + 4u * q + l;
+    const uint32_t e = rowBase + c;
+    ${c}[jt][l] = rowOk && c < ${TK}u ? A.in[${k}][${ctx.idx}] : 0.f;
+  }
+}`);
+        }
+        return `${caches.get(ck)}[jt][l]`;
+      }
+      const v = `L${lines.length}_${k}`;
+      lines.push(`const float ${v} = A.in[${k}][${ctx.idx}];`);
+      return v;
+    },
+  });
+  // One pass over this lane's scores of its row: `e` the flat index in [batch·TQ, TK].
+  const loop = (bodyLines) => `#pragma unroll
+for (int jt = 0; jt < ${Math.ceil(TK / 16)}; ++jt) {
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    const uint32_t c = 16u * jt + 4u * q + l;
+    if (rowOk && c < ${TK}u) {
+      const uint32_t e = rowBase + c;
+${indent(bodyLines, '      ')}
+    }
+  }
+}`;
+  const phases = [];
+  reductions.forEach((rd, k) => {
+    for (const key of Array.from(em.memo.keys())) if (key.startsWith('e')) em.memo.delete(key);
+    const rowBefore = rowLines.length;
+    const inner = [];
+    const v = em.value(rd.inputs[0], elemCtx(), inner);
+    const isMax = rd.op === 'max';
+    const pre = rowLines.splice(rowBefore);
+    phases.push(...pre,
+      `float acc${k} = ${isMax ? '(-TCMI_INF)' : '0.f'};`,
+      loop(inner.concat([`acc${k} = tcmi::red_${isMax ? 'max' : 'sum'}(acc${k}, ${v});`])),
+      `const float red${k} = tcmi::quad16_reduce<${isMax}>(acc${k});`);
+    reduced.set(rd.id, `red${k}`);
+  });
+  for (const key of Array.from(em.memo.keys())) if (key.startsWith('e')) em.memo.delete(key);
+  const rowBefore = rowLines.length;
+  const inner = [];
+  const pv = em.value(sOut, elemCtx(), inner);
+  const pre = rowLines.splice(rowBefore);
+  const pLoop = `#pragma unroll
+for (int jt = 0; jt < ${Math.ceil(TK / 16)}; ++jt) {
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    const uint32_t c = 16u * jt + 4u * q + l;
+    float pe = 0.f;
+    if (rowOk && c < ${TK}u) {
+      const uint32_t e = rowBase + c;
+${indent(inner, '      ')}
+      pe = ${pv};
+    }
+    p[jt][l] = pe;
+  }
+}`;
+  const views = o.views || {};
+  const sizes = o.sizes || {};
+  const qv = operandView('__KERNEL___qv', views.q, batchDims, TQ, DH);
+  const kv = operandView('__KERNEL___kv', views.k, batchDims, DH, TK);
+  const vv = operandView('__KERNEL___vv', views.v, batchDims, TK, DV);
+  const need = (slot, dense) => (sizes[slot] !== undefined ? sizes[slot] : dense);
+  if (qv.limit > need('q', batch * TQ * DH) || kv.limit > need('k', batch * DH * TK) || vv.limit > need('v', batch * TK * DV)) {
+    throw new Error('attention operand view out of bounds');
+  }
+  // Wavefronts per workgroup: one per 16 query rows, up to 8 (128 rows share one K and V tile).
+  const WAVES = Math.min(8, Math.ceil(TQ / 16));
+  const THREADS = 64 * WAVES;
+  const text = `#include "tcmi_attention.h"
+${qv.text}${kv.text}${vv.text}extern "C" __global__ void __launch_bounds__(${THREADS}) __KERNEL__(const TcmiArgs A) {
+  using G = tcmi::AttnTiles<${TK}, ${DH}, ${DV}>;
+  __shared__ __attribute__((aligned(16))) float Ks[G::ROWS * G::KS];
+  __shared__ __attribute__((aligned(16))) float Vs[G::ROWS * G::VS];
+  const uint32_t b = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t16 = lane & 15, q = lane >> 4;
+  const uint32_t row = blockIdx.x * ${16 * WAVES}u + wave * 16u + t16;   // this lane's query row
+  tcmi::attn_zero_padding<${TK}, ${DH}, ${DV}, ${THREADS}>(Ks, Vs);
+  // Every global load of the K and V tiles issued at once; V lands in LDS after the scores.
+  tcmi::AttnStage<${TK}, ${DH}, G::KS, ${kv.mode}, true, __KERNEL___kv, ${THREADS}> kst;
+  tcmi::AttnStage<${TK}, ${DV}, G::VS, ${vv.mode}, false, __KERNEL___vv, ${THREADS}> vst;
+  kst.load(A.in[${ik}], b);
+  vst.load(A.in[${iv}], b);
+  tcmi::f4 qf[G::DH16];
+  tcmi::attn_q<${TQ}, ${DH}, G::DH16, ${qv.mode}, __KERNEL___qv>(qf, A.in[${iq}], b, row, q);
+  const bool rowOk = row < ${TQ}u;
+  const uint32_t r = b * ${TQ}u + (rowOk ? row : 0u);   // the score row (rows past TQ compute nothing)
+  const uint32_t rowBase = r * ${TK}u;
+${indent(cacheFill, '  ')}
+  kst.store(Ks);
+  __syncthreads();
+  tcmi::f4 sacc[G::NT];
+  tcmi::attn_scores<G::NT, G::DH16, G::KS>(sacc, qf, Ks, t16, q);
+  vst.store(Vs);
+${indent(phases, '  ')}
+  tcmi::f4 p[${NT}];
+${indent(pre.concat([pLoop]), '  ')}
+  __syncthreads();
+  tcmi::f4 oacc[G::DV16];
+  tcmi::attn_pv<G::NT, G::DV16, G::VS>(oacc, p, Vs, t16, q);
+  tcmi::attn_store<${TQ}, ${DV}, G::DV16>(A.out, oacc, b, row, q);
+}
+`;
+  const k = kernelText('attn', text);
+  const lds = 4 * (NT * 16) * (Math.ceil(DH / 16) * 16 + 4 + Math.ceil(DV / 16) * 16 + 4);
+  return { name: k.name, source: k.source, params: Uint32Array.from(params), grid: [Math.ceil(TQ / (16 * WAVES)), batch, 1],
+    block: [THREADS, 1, 1], lds: 0, ldsStatic: lds, workspace: 0, flops: 2 * batch * TQ * TK * (DH + DV),
+    modes: [qv.mode, kv.mode, vv.mode] };
+}
+
+module.exports = { elementwiseKernel, rowwiseKernel, colreduceKernels, gemmKernel, gemmTiling, attentionKernel, classifyGather, gatherStrides,
+  literal, fnv, Emitter, WG, MAX_P, MAX_IN };

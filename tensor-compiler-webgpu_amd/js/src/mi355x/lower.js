@@ -98,6 +98,7 @@ function lowerNode(graph, node, opts, mmViews, folds) {
     }
     if (kind === 'rowwise') return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(b, out, Object.assign({ tuning: tuning.row }, sab))));
     if (kind === 'epilogue') return Object.assign({ kind: 'fused-epilogue' }, single(cg.gemmKernel(b, out, Object.assign({ tuning: tuning.gemm }, sab, mmViews))));
+    if (kind === 'attention') return Object.assign({ kind: 'fused-attention' }, single(cg.attentionKernel(b, out, Object.assign({}, mmViews))));
     throw new Error(`no MI355X kernel for fused kind '${kind}'`);
   }
   if (ELEMENTWISE_OPS.has(node.op) || GATHERS.has(node.op)) {
@@ -141,11 +142,27 @@ function consumersOf(graph) {
 }
 
 /**
- * The matmul operand slots of node `n`: [[slot ('a'|'b'), operand position in
- * n.inputs]] for the operands only its matmul reads.
+ * The matmul operand slots of node `n`: [[slot, operand position in n.inputs]]
+ * for the operands only its matmuls read — 'a' and 'b' of a matmul or an
+ * epilogue group's matmul; 'q', 'k' and 'v' of a fused attention (Q and Kt of
+ * the scores, V of the output product).
  */
 function matmulSlots(n) {
   if (n.op === 'matmul') return [['a', 0], ['b', 1]];
+  if (n.op === 'fused' && n.attrs.kind === 'attention') {
+    const b = n.attrs.body;
+    const m2 = b.nodes[n.attrs.output];
+    const m1 = b.nodes.find((x, i) => x.op === 'matmul' && i !== n.attrs.output);
+    const only = (bodyId, user) => b.nodes.every((x, i) => i === user || !x.inputs.includes(bodyId));
+    const slots = [];
+    const m1Id = b.nodes.indexOf(m1);
+    if (m1.inputs[0] !== m1.inputs[1]) {
+      if (only(m1.inputs[0], m1Id)) slots.push(['q', Number(b.nodes[m1.inputs[0]].attrs.name.slice(1))]);
+      if (only(m1.inputs[1], m1Id)) slots.push(['k', Number(b.nodes[m1.inputs[1]].attrs.name.slice(1))]);
+    }
+    if (only(m2.inputs[1], n.attrs.output)) slots.push(['v', Number(b.nodes[m2.inputs[1]].attrs.name.slice(1))]);
+    return slots;
+  }
   if (n.op !== 'fused' || n.attrs.kind !== 'epilogue') return [];
   const b = n.attrs.body;
   const root = b.nodes.find((x) => x.op === 'matmul');
@@ -245,7 +262,11 @@ function lowerMI355X(graph, options) {
     if (node.op === 'input' || node.op === 'const') continue;
     if (plan.aliases.has(node.id) || plan.folded.has(node.id)) continue;
     const v = plan.views.get(node.id);
-    const mmViews = v ? { views: { a: v.a && v.a.view, b: v.b && v.b.view }, sizes: { a: v.a && v.a.size, b: v.b && v.b.size } } : null;
+    let mmViews = null;
+    if (v) {
+      mmViews = { views: {}, sizes: {} };
+      for (const slot of Object.keys(v)) { mmViews.views[slot] = v[slot].view; mmViews.sizes[slot] = v[slot].size; }
+    }
     const folds = plan.broadcasts.get(node.id) || null;
     const foldKey = folds ? Array.from(folds.entries()).map(([pos, f]) => [pos, f.from, f.to]) : null;
     // Kernels depend on structure, shapes, operand views and folded broadcasts only: reuse across identical nodes.
@@ -256,7 +277,7 @@ function lowerMI355X(graph, options) {
     workspace = Math.max(workspace, k.workspace);
     const resolve = (id) => (plan.aliases.has(id) ? plan.aliases.get(id) : id);
     const inputs = node.inputs.map(resolve);
-    if (v) for (const s of [v.a, v.b]) if (s) inputs[s.pos] = resolve(s.source);
+    if (v) for (const s of Object.values(v)) inputs[s.pos] = resolve(s.source);
     if (folds) for (const [pos, f] of folds) inputs[pos] = resolve(f.source);
     launches.push({
       node: node.id, op: node.op, kind: k.kind, pattern: node.op === 'fused' ? node.attrs.pattern : undefined,
@@ -266,7 +287,7 @@ function lowerMI355X(graph, options) {
     if (v) {
       // Operands read in place: for each folded slot, the node it stands for and the view of its source.
       launches[launches.length - 1].views = {};
-      for (const slot of ['a', 'b']) if (v[slot]) launches[launches.length - 1].views[slot] = { pos: v[slot].pos, operand: node.inputs[v[slot].pos], source: v[slot].source, view: v[slot].view };
+      for (const slot of Object.keys(v)) launches[launches.length - 1].views[slot] = { pos: v[slot].pos, operand: node.inputs[v[slot].pos], source: v[slot].source, view: v[slot].view };
     }
   }
   return { launches, workspace, aliases: Array.from(plan.aliases.entries()), folded: Array.from(plan.folded) };

@@ -253,3 +253,40 @@ def test_perf_lowering_keeps_the_split_of_config4_backward(tool):
         assert sum(nodes[i]["op"] == "transpose" for i in d["folded"]) == 2   # transpose(W), transpose(X)
         for l in d["launches"]:
             assert l["split"] == l["plainSplit"], (g["M"], g["K"], g["N"], l["node"])
+
+
+@pytest.mark.parametrize("config,V,B,layers", [("reference", 16, 2, 2), ("c5", 96, 1, 4)])
+def test_attention_fusion_preserves_semantics(tool, config, V, B, layers):
+    """The attention extension (fuse(..., {attention: true}), off by default): every
+    attention of the transformer's forward pass (matmul(Q, Kt) -> the softmax group ->
+    matmul(P, V)) becomes one fused node, the float64 interpreter evaluates the fused
+    graph bitwise equal at every surviving node, and the contract's own fusion of the
+    same graph is unchanged by the option being available."""
+    fw = tool("transformer-forward", {"config": config, "V": V, "B": B})
+    plain, att = tool("fuse", {"graphs": [{"name": "p", "graph": fw["graph"], "keep": fw["keep"]},
+                                          {"name": "a", "graph": fw["graph"], "keep": fw["keep"], "attention": True}]})
+    kinds = lambda f: [n["attrs"]["kind"] for n in f["graph"]["nodes"] if n["op"] == "fused"]
+    assert kinds(att).count("attention") == layers
+    assert "attention" not in kinds(plain)
+    assert kinds(plain).count("rowwise") - kinds(att).count("rowwise") == layers   # each softmax group absorbed
+    launched = lambda f: sum(1 for n in f["graph"]["nodes"] if n["op"] not in ("input", "const"))
+    assert launched(plain) - launched(att) == 2 * layers
+    assert _semantics(fw["graph"], att["graph"], att["origin"], fw["inputs"])
+    for n in att["graph"]["nodes"]:
+        if n["op"] == "fused" and n["attrs"]["kind"] == "attention":
+            ops = [b["op"] for b in n["attrs"]["body"]["nodes"]]
+            assert ops.count("matmul") == 2 and ops.count("max") == 1 and ops.count("exp") == 1
+
+
+def test_attention_fusion_leaves_training_steps_and_golden_cases_alone(golden_cases, tool):
+    """In a training step the probabilities also feed the backward pass, so no attention
+    fuses there; on every golden case the option keeps fusion semantics bitwise."""
+    fw = tool("transformer-forward", {"config": "reference", "V": 16, "B": 1})
+    g = tool("grad", {"cases": [{"name": "t", "graph": fw["graph"], "outputs": [fw["keep"][1]]}]})[0]
+    step = tool("fuse", {"graphs": [{"name": "s", "graph": g["graph"], "keep": [fw["keep"][1]] + g["grads"], "attention": True}]})[0]
+    assert not any(n["op"] == "fused" and n["attrs"]["kind"] == "attention" for n in step["graph"]["nodes"])
+    reqs = [{"name": c["name"], "graph": c["graph"], "keep": c["outputs"], "attention": True} for c in golden_cases]
+    fused = tool("fuse", {"graphs": reqs})
+    for c, f in zip(golden_cases, fused):
+        assert "error" not in f, (c["name"], f.get("error"))
+        assert _semantics(c["graph"], f["graph"], f["origin"], c["inputs"]), c["name"]
