@@ -8,6 +8,9 @@
 //   runner.runLocal(graph, lowered, values)     for harness-m3b.js runLocal
 //   fusedStep(step); new HipTrainer(...)        for fusedStep / FusedTrainer
 //   new HipBench(runner); bench.time(...)       for Bench.time; verdict, summarize
+// and this backend's own additions: fuseAttention(fused, { keep }) (attention
+// as one fused node, after the reference's fuse) and planArena (the liveness
+// placement Program uses with { arena: { keep } }).
 // Graphs are the reference's own (its Graph objects, or their toJSON form with
 // fused nodes from its fuse()).
 
@@ -15,5 +18,8 @@ const { lowerMI355X, kernelSources } = require('./lower');
 const { HipRunner, Program, precompile } = require('./runner');
 const { fusedStep, HipTrainer } = require('./trainer');
 const { HipBench, summarize, verdict } = require('./bench');
+const { fuseAttention } = require('../fusion/attention');
+const { planArena } = require('./arena');
 
-module.exports = { lowerMI355X, kernelSources, HipRunner, Program, precompile, fusedStep, HipTrainer, HipBench, summarize, verdict };
+module.exports = { lowerMI355X, kernelSources, HipRunner, Program, precompile, fusedStep, HipTrainer, HipBench, summarize, verdict,
+  fuseAttention, planArena };
