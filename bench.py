@@ -146,7 +146,7 @@ def main() -> None:
     for key, label in (("c1", "mlp_step_c1"), ("c5", "transformer_step_c5")):
         if key in cfg:
             t = cfg[key]
-            extra[label] = {"steps_per_sec": t["stepsPerSec"], "ms_per_step": t["msPerStep"],
+            extra[label] = {"steps_per_sec": t["stepsPerSec"], "ms_per_step": t["msPerStep"], "hip_graph_replay": t["graphReplay"],
                             "resident_steps_per_sec": t["residentStepsPerSec"], "resident_ms_per_step": t["residentMsPerStep"],
                             "launches": t["launches"], "fused_us": t["fused"]["median"], "unfused_us": t["unfused"]["median"],
                             "speedup_vs_unfused": t["verdict"]["speedup"], "matmul_TFLOPs_resident": t["matmulTflopsResident"],

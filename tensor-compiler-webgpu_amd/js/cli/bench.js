@@ -4,7 +4,11 @@
 // document (bench.py turns it into the driver's one-line record).
 //
 //   node bench.js [--configs ceiling,c2,c3,c4] [--steps K] [--warmup W] [--programs P]
-//                 [--reps N] [--c4-shapes all|small] [--quick] [--graphs] [--step-only]
+//                 [--reps N] [--c4-shapes all|small] [--quick] [--graphs] [--no-trainer-graphs] [--step-only]
+//
+// --graphs: the c2 step's programs replayed as captured HIP graphs. The trainers
+// of c1 and c5 replay each step as a captured HIP graph by default (a step is
+// launch-bound at c1's size); --no-trainer-graphs issues their launches directly.
 //
 // --step-only (for profilers): c2 runs its headline step only; c3 and c4 run each
 // fused program --steps times after --warmup runs, with no timing loops.
@@ -329,7 +333,8 @@ function trainStep(runner, bench, name, req, opts) {
   runner.functions([fs.lowered, lu]);
   const K = Number(arg('train-steps', opts.quick ? 3 : 10)), W = 2;
   const batch = m.batch(0);
-  const trainer = new HipTrainer(runner, fs, m.params, m.state, { graph: bench.graphs });
+  const graph = !flag('no-trainer-graphs');
+  const trainer = new HipTrainer(runner, fs, m.params, m.state, { graph });
   for (let i = 0; i < W; i++) trainer.train(batch.x, batch.y);
   const t0 = process.hrtime.bigint();
   let loss = 0;
@@ -363,7 +368,7 @@ function trainStep(runner, bench, name, req, opts) {
   pu.destroy();
   trainer.destroy();
   // The same trainer with its intermediate buffers in a liveness arena.
-  const ta = new HipTrainer(runner, fs, m.params, m.state, { graph: bench.graphs, arena: true });
+  const ta = new HipTrainer(runner, fs, m.params, m.state, { graph, arena: true });
   for (let i = 0; i < W; i++) ta.train(batch.x, batch.y);
   const ta0 = process.hrtime.bigint();
   for (let i = 0; i < K; i++) ta.train(batch.x, batch.y);
@@ -378,7 +383,7 @@ function trainStep(runner, bench, name, req, opts) {
     stepsPerSec: 1e3 / arenaWallMs, residentStepsPerSec: 1e3 / arenaResidentMs };
   ta.destroy();
   const flops = fs.lowered.launches.reduce((q, l) => q + (l.flops || 0), 0);
-  return { config: name, info: m.info, steps: K, warmup: W, lossLast: loss, arena,
+  return { config: name, info: m.info, steps: K, warmup: W, lossLast: loss, arena, graphReplay: graph,
     stepsPerSec: 1e3 / wallMs, msPerStep: wallMs, residentMsPerStep: residentMs, residentStepsPerSec: 1e3 / residentMs,
     launches: { fused: fs.lowered.launches.length, unfused: lu.launches.length },
     fused: t.stats.fused, unfused: t.stats.unfused, verdict: verdict(t.stats.unfused, t.stats.fused),
