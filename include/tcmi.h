@@ -113,6 +113,30 @@ int tcmi_launch(uint64_t function, const uint32_t grid[3], const uint32_t block[
 /* Wait for all work on the library stream; reports (and latches) asynchronous faults. */
 int tcmi_sync(void);
 
+/* --- launch graphs over several streams ----------------------------------------
+ * No counterpart in the reference, whose launches go to one in-order WebGPU queue
+ * (runtime.js:86-101); here independent launches of a launch list may overlap.
+ * The scheduler (js/src/mi355x/schedule.js) assigns each launch a stream and the
+ * events it must wait for. */
+
+#define TCMI_MAX_STREAMS 4
+
+/* Make at least `events` event slots for tcmi_launch_dag (do it before a capture). */
+int tcmi_dag_reserve(uint32_t events);
+/* Enqueue `count` launches (functions, dims: 7 u32 per launch = grid xyz, block xyz,
+ * dynamic LDS; args/offsets: packed argument blocks, offsets[count + 1]) over
+ * `streams` (1..TCMI_MAX_STREAMS) in-order streams of default priority: launch i
+ * goes on stream stream_of[i] (0 = the library stream) after waiting for the event
+ * slots waits[wait_begin[i] .. wait_begin[i + 1]), and records slot record_event[i]
+ * after it (-1: none). The side streams first wait for all work already on the
+ * library stream, and the library stream waits for every side stream at the end,
+ * so the whole sequence is ordered against other work like one launch list (and is
+ * captured into a HIP graph like one). Everything is checked before anything is
+ * enqueued. */
+int tcmi_launch_dag(uint32_t count, const uint64_t* functions, const uint32_t* dims, const uint8_t* args,
+                    const uint32_t* offsets, uint32_t streams, const uint8_t* stream_of, const int32_t* record_event,
+                    const uint32_t* wait_begin, const uint32_t* waits);
+
 /* --- timing (bench.js:124-153) ----------------------------------------------- */
 
 int tcmi_event_create(uint64_t* event);

@@ -334,6 +334,40 @@ napi_value LaunchMany(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+// launchDag(fns, dims, args, offsets, streams, streamOf: Uint8Array, recordEvent: Int32Array,
+//           waitBegin: Uint32Array (n + 1), waits: Uint32Array): a launch list over several streams.
+napi_value LaunchDag(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  void *fns, *dims, *args, *offs, *sof, *rec, *wb, *ws;
+  size_t nf, nd, na, no, ns, nr, nwb, nw;
+  uint32_t streams;
+  if (!a.bytes(0, &fns, &nf) || !a.bytes(1, &dims, &nd) || !a.bytes(2, &args, &na) || !a.bytes(3, &offs, &no) ||
+      !a.u32(4, &streams) || !a.bytes(5, &sof, &ns) || !a.bytes(6, &rec, &nr) || !a.bytes(7, &wb, &nwb) ||
+      !a.bytes(8, &ws, &nw))
+    return throw_type(env, "launchDag(fns, dims, args, offsets, streams, streamOf, recordEvent, waitBegin, waits)");
+  size_t count = nf / 8;
+  if (nd != count * 7 * 4 || no != (count + 1) * 4 || ns != count || nr != count * 4 || nwb != (count + 1) * 4)
+    return throw_type(env, "launchDag: array lengths disagree");
+  const uint32_t* O = static_cast<const uint32_t*>(offs);
+  const uint32_t* WB = static_cast<const uint32_t*>(wb);
+  if (count && (O[count] > na || WB[count] > nw / 4)) return throw_type(env, "launchDag: offsets past the arrays");
+  std::vector<uint64_t> F(count);
+  for (size_t i = 0; i < count; i++) F[i] = static_cast<uint64_t>(static_cast<const double*>(fns)[i]);
+  CHECK(tcmi_launch_dag(static_cast<uint32_t>(count), F.data(), static_cast<const uint32_t*>(dims),
+                        static_cast<const uint8_t*>(args), O, streams, static_cast<const uint8_t*>(sof),
+                        static_cast<const int32_t*>(rec), WB, static_cast<const uint32_t*>(ws)),
+        "tcmi_launch_dag");
+  return undef(env);
+}
+
+napi_value DagReserve(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  uint32_t n;
+  if (!a.u32(0, &n)) return throw_type(env, "dagReserve(events)");
+  CHECK(tcmi_dag_reserve(n), "tcmi_dag_reserve");
+  return undef(env);
+}
+
 napi_value Sync(napi_env env, napi_callback_info) {
   CHECK(tcmi_sync(), "tcmi_sync");
   return undef(env);
@@ -428,7 +462,8 @@ napi_value Register(napi_env env, napi_value exports) {
       {"malloc", Malloc}, {"free", Free}, {"h2d", H2D}, {"d2h", D2H}, {"d2d", D2D}, {"fill32", Fill32},
       {"countNot32", CountNot32}, {"setCacheDir", SetCacheDir}, {"setIncludeDir", SetIncludeDir},
       {"compile", Compile}, {"precompile", Precompile}, {"function", Function}, {"unload", Unload},
-      {"launch", Launch}, {"launchMany", LaunchMany}, {"sync", Sync}, {"eventCreate", EventCreate},
+      {"launch", Launch}, {"launchMany", LaunchMany}, {"launchDag", LaunchDag}, {"dagReserve", DagReserve},
+      {"sync", Sync}, {"eventCreate", EventCreate},
       {"eventRecord", EventRecord}, {"eventElapsed", EventElapsed}, {"eventDestroy", EventDestroy},
       {"captureBegin", CaptureBegin}, {"captureEnd", CaptureEnd}, {"graphLaunch", GraphLaunch},
       {"graphDestroy", GraphDestroy}, {"ceilingCopy", CeilingCopy}, {"ceilingRead", CeilingRead},

@@ -42,6 +42,14 @@ std::atomic<int> g_lost{0};
 bool g_init = false;
 int g_device = 0;
 hipStream_t g_stream = nullptr;
+// Side streams for launch graphs (tcmi_launch_dag), default priority like the
+// library stream, and the events that order them: one fork and one join per
+// side stream, and a pool of per-launch event slots.
+constexpr int kSideStreams = TCMI_MAX_STREAMS - 1;
+hipStream_t g_side[kSideStreams] = {};
+hipEvent_t g_fork = nullptr;
+hipEvent_t g_join[kSideStreams] = {};
+std::vector<hipEvent_t> g_dag_events;
 hipDeviceProp_t g_props;
 std::string g_arch;        // "gfx950" (features stripped)
 std::string g_cache_dir;
@@ -293,6 +301,11 @@ int tcmi_init(void) {
   if (colon != std::string::npos) g_arch = g_arch.substr(0, colon);
   // Default priority, non-blocking with respect to the null stream.
   HIP_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+  for (int k = 0; k < kSideStreams; ++k) {
+    HIP_TRY(hipStreamCreateWithFlags(&g_side[k], hipStreamNonBlocking), "hipStreamCreateWithFlags (side)");
+    HIP_TRY(hipEventCreateWithFlags(&g_join[k], hipEventDisableTiming), "hipEventCreateWithFlags");
+  }
+  HIP_TRY(hipEventCreateWithFlags(&g_fork, hipEventDisableTiming), "hipEventCreateWithFlags");
   g_init = true;
   return TCMI_OK;
 }
@@ -488,6 +501,65 @@ int tcmi_launch(uint64_t function, const uint32_t grid[3], const uint32_t block[
   HIP_TRY(hipModuleLaunchKernel(it->second, grid[0], grid[1], grid[2], block[0], block[1], block[2], lds_bytes,
                                 g_stream, nullptr, args_bytes ? config : nullptr),
           "hipModuleLaunchKernel");
+  return TCMI_OK;
+}
+
+int tcmi_dag_reserve(uint32_t events) {
+  if (int rc = ready()) return rc;
+  if (events > (1u << 20)) return fail(TCMI_E_INVALID, "tcmi_dag_reserve: too many events");
+  while (g_dag_events.size() < events) {
+    hipEvent_t e;
+    HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming), "hipEventCreateWithFlags");
+    g_dag_events.push_back(e);
+  }
+  return TCMI_OK;
+}
+
+int tcmi_launch_dag(uint32_t count, const uint64_t* functions, const uint32_t* dims, const uint8_t* args,
+                    const uint32_t* offsets, uint32_t streams, const uint8_t* stream_of, const int32_t* record_event,
+                    const uint32_t* wait_begin, const uint32_t* waits) {
+  if (int rc = ready()) return rc;
+  if (streams < 1 || streams > TCMI_MAX_STREAMS) return fail(TCMI_E_INVALID, "tcmi_launch_dag: streams out of range");
+  if (count && (!functions || !dims || !offsets || !stream_of || !record_event || !wait_begin))
+    return fail(TCMI_E_INVALID, "tcmi_launch_dag: null array");
+  const uint32_t nev = static_cast<uint32_t>(g_dag_events.size());
+  // Check everything before enqueueing anything.
+  for (uint32_t i = 0; i < count; ++i) {
+    if (stream_of[i] >= streams) return fail(TCMI_E_INVALID, "tcmi_launch_dag: stream index out of range");
+    if (record_event[i] >= 0 && static_cast<uint32_t>(record_event[i]) >= nev)
+      return fail(TCMI_E_INVALID, "tcmi_launch_dag: event slot not reserved");
+    if (wait_begin[i] > wait_begin[i + 1]) return fail(TCMI_E_INVALID, "tcmi_launch_dag: bad wait ranges");
+    for (uint32_t w = wait_begin[i]; w < wait_begin[i + 1]; ++w)
+      if (!waits || waits[w] >= nev) return fail(TCMI_E_INVALID, "tcmi_launch_dag: waited event not reserved");
+    if (offsets[i] > offsets[i + 1] || offsets[i + 1] - offsets[i] > 4096)
+      return fail(TCMI_E_INVALID, "tcmi_launch_dag: bad argument offsets");
+    if (g_functions.find(functions[i]) == g_functions.end()) return fail(TCMI_E_INVALID, "tcmi_launch_dag: unknown function");
+    if (int rc = check_launch_shape(dims + 7 * i, dims + 7 * i + 3, dims[7 * i + 6])) return rc;
+  }
+  auto stream = [&](uint32_t k) { return k == 0 ? g_stream : g_side[k - 1]; };
+  // Fork: the side streams start after everything already on the library stream.
+  if (streams > 1) {
+    HIP_TRY(hipEventRecord(g_fork, g_stream), "hipEventRecord (fork)");
+    for (uint32_t k = 1; k < streams; ++k) HIP_TRY(hipStreamWaitEvent(g_side[k - 1], g_fork, 0), "hipStreamWaitEvent (fork)");
+  }
+  for (uint32_t i = 0; i < count; ++i) {
+    hipStream_t st = stream(stream_of[i]);
+    for (uint32_t w = wait_begin[i]; w < wait_begin[i + 1]; ++w)
+      HIP_TRY(hipStreamWaitEvent(st, g_dag_events[waits[w]], 0), "hipStreamWaitEvent");
+    size_t size = offsets[i + 1] - offsets[i];
+    void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, const_cast<uint8_t*>(args + offsets[i]), HIP_LAUNCH_PARAM_BUFFER_SIZE,
+                      &size, HIP_LAUNCH_PARAM_END};
+    const uint32_t* d = dims + 7 * i;
+    HIP_TRY(hipModuleLaunchKernel(g_functions[functions[i]], d[0], d[1], d[2], d[3], d[4], d[5], d[6], st, nullptr,
+                                  size ? config : nullptr),
+            "hipModuleLaunchKernel");
+    if (record_event[i] >= 0) HIP_TRY(hipEventRecord(g_dag_events[record_event[i]], st), "hipEventRecord");
+  }
+  // Join: the library stream continues after every side stream's launches.
+  for (uint32_t k = 1; k < streams; ++k) {
+    HIP_TRY(hipEventRecord(g_join[k - 1], g_side[k - 1]), "hipEventRecord (join)");
+    HIP_TRY(hipStreamWaitEvent(g_stream, g_join[k - 1], 0), "hipStreamWaitEvent (join)");
+  }
   return TCMI_OK;
 }
 

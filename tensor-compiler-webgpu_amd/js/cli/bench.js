@@ -382,8 +382,28 @@ function trainStep(runner, bench, name, req, opts) {
   const arena = { bytes: plan.size, unshared: plan.unshared, msPerStep: arenaWallMs, residentMsPerStep: arenaResidentMs,
     stepsPerSec: 1e3 / arenaWallMs, residentStepsPerSec: 1e3 / arenaResidentMs };
   ta.destroy();
+  // Independent launches on several streams (--streams N, issued directly: multi-stream
+  // programs are not captured into graphs). Measured slower than one stream here: each
+  // cross-stream wait costs more than the overlap it buys.
+  const streamRuns = {};
+  const nStreams = Number(arg('streams', 1));
+  if (nStreams > 1) {
+    const ts = new HipTrainer(runner, fs, m.params, m.state, { streams: nStreams });
+    for (let i = 0; i < W; i++) ts.train(batch.x, batch.y);
+    const ts0 = process.hrtime.bigint();
+    for (let i = 0; i < K; i++) ts.train(batch.x, batch.y);
+    const wall = Number(process.hrtime.bigint() - ts0) / 1e6 / K;
+    runner.a.sync();
+    runner.a.eventRecord(bench.start);
+    for (let i = 0; i < K; i++) ts.advance();
+    runner.a.eventRecord(bench.end);
+    const resident = runner.a.eventElapsed(bench.start, bench.end) / K;
+    streamRuns[nStreams] = { msPerStep: wall, residentMsPerStep: resident, stepsPerSec: 1e3 / wall, residentStepsPerSec: 1e3 / resident,
+      criticalPath: ts.program.dag.criticalPath, waits: ts.program.dag.waits.length };
+    ts.destroy();
+  }
   const flops = fs.lowered.launches.reduce((q, l) => q + (l.flops || 0), 0);
-  return { config: name, info: m.info, steps: K, warmup: W, lossLast: loss, arena, graphReplay: graph,
+  return { config: name, info: m.info, steps: K, warmup: W, lossLast: loss, arena, streams: streamRuns, graphReplay: graph,
     stepsPerSec: 1e3 / wallMs, msPerStep: wallMs, residentMsPerStep: residentMs, residentStepsPerSec: 1e3 / residentMs,
     launches: { fused: fs.lowered.launches.length, unfused: lu.launches.length },
     fused: t.stats.fused, unfused: t.stats.unfused, verdict: verdict(t.stats.unfused, t.stats.fused),

@@ -648,7 +648,7 @@ async function gpuTrain(req) {
   const m = modelStep(req);
   const fs = fusedStep(m.step);
   const runner = HipRunner.create();
-  const trainer = new HipTrainer(runner, fs, m.params, m.state, { graph: !!req.graph, arena: !!req.arena });
+  const trainer = new HipTrainer(runner, fs, m.params, m.state, { graph: !!req.graph, arena: !!req.arena, streams: req.streams || 1 });
   const plan = trainer.program.arena;
   const losses = [];
   let identical = null;
@@ -791,6 +791,49 @@ async function main() {
         c3: (req.c3 || []).map((c) => { const g = cfg.c3Graphs(c.fn, c.R, c.C); return { fn: c.fn, R: c.R, C: c.C, forward: one(g.forward), gradient: one(g.gradient) }; }),
         c4: (req.c4 || []).map((c) => { const g = cfg.c4Graphs(c.act, c.M, c.K, c.N); return { act: c.act, M: c.M, K: c.K, N: c.N, forward: one(g.forward), gradient: one(g.gradient) }; }),
       };
+      break;
+    }
+    case 'schedule-check': {
+      // Stream schedules of model steps and corpus programs (perf lowering) at 2..4 streams,
+      // checked by replaying them with vector clocks; with `plant`, one wait dropped.
+      const { scheduleLaunches } = require('../src/mi355x/schedule');
+      const { checkSchedule } = require('../src/testing/schedule_check');
+      out = [];
+      const one = (name, graph, keep) => {
+        const lw = lowerMI355X(graph, { perf: true, keep });
+        const alias = new Map(lw.aliases);
+        const owner = (id) => (alias.has(id) ? alias.get(id) : id);
+        for (const streams of [2, 3, 4]) {
+          const sc = scheduleLaunches(lw.launches, streams, owner);
+          const rec = { name, streams, launches: lw.launches.length, criticalPath: sc.criticalPath, waits: sc.waits.length,
+            used: new Set(sc.streamOf).size, check: checkSchedule(lw.launches, sc, owner) };
+          if (req.plant && sc.waits.length) {
+            const k = sc.waitBegin.findIndex((b, i) => i < sc.streamOf.length && sc.waitBegin[i + 1] > b);
+            const broken = Object.assign({}, sc, { waits: sc.waits.slice(), waitBegin: sc.waitBegin.slice() });
+            // Drop the first wait of kernel k: shift the later ranges down by one.
+            broken.waits = Uint32Array.from([...sc.waits.slice(0, sc.waitBegin[k]), ...sc.waits.slice(sc.waitBegin[k] + 1)]);
+            for (let i = k + 1; i < broken.waitBegin.length; i++) broken.waitBegin[i]--;
+            rec.planted = checkSchedule(lw.launches, broken, owner);
+          }
+          out.push(rec);
+        }
+      };
+      const { modelStep } = require('../src/builders/models');
+      const { fusedStep } = require('../src/mi355x/trainer');
+      for (const r of req.models || []) {
+        const m = modelStep(r);
+        const f = fusedStep(m.step);
+        one(`${r.model}-${r.B || ''}`, f.graph, [f.loss, f.logits].concat(Object.values(f.outputs)));
+      }
+      if (req.corpus) {
+        const { corpusGraphs } = require('../src/testing/random_graph');
+        for (let i = req.corpus.from; i <= req.corpus.to; i++) {
+          for (const c of corpusGraphs(i)) {
+            const f = fuse(c.graph, { keep: c.keep });
+            one(`corpus-${i}-${c.label}`, f.graph, c.keep.map((id) => f.index.get(id)));
+          }
+        }
+      }
       break;
     }
     case 'arena-check': {

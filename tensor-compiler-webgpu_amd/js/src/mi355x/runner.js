@@ -17,7 +17,9 @@
 // function handles made once, then run() issues every launch with one native
 // call (or replays a captured HIP graph) — what the trainer and bench use.
 // With { arena: { keep } } its node buffers are placed by live range in one
-// allocation (arena.js): only inputs, constants and `keep` stay readable.
+// allocation (arena.js): only inputs, constants and `keep` stay readable. With
+// { streams: n } (2..4) independent launches are issued on n streams
+// (schedule.js), one native call per run as before.
 
 const crypto = require('crypto');
 const fs = require('fs');
@@ -27,6 +29,7 @@ const { addon, CACHE } = require('./addon');
 const { kernelSources } = require('./lower');
 const { MAX_IN, MAX_P } = require('./codegen');
 const { planArena } = require('./arena');
+const { scheduleLaunches } = require('./schedule');
 
 const CANARY_BITS = 0xdeadbeef;
 const CANARY_PAD = 256;           // words past the end of every buffer
@@ -312,9 +315,10 @@ class Program {
   /**
    * options.only: launch filter; options.buffers: node buffers to use (device addresses,
    * owned by the caller); options.arena: { keep } to place the buffers by live range in
-   * one allocation, or an arena plan of the same launch list that `buffers` follows.
+   * one allocation, or an arena plan of the same launch list that `buffers` follows;
+   * options.streams: issue independent launches on up to 4 streams.
    */
-  constructor(runner, graph, lowered, { only, buffers, arena } = {}) {
+  constructor(runner, graph, lowered, { only, buffers, arena, streams } = {}) {
     requirePad(lowered, false);
     const a = runner.a;
     this.a = a;
@@ -374,6 +378,13 @@ class Program {
     this.offsets[count] = count * ARG_BYTES;
     this.launches = launches;
     this.graphHandle = 0;
+    this.dag = null;
+    if (streams && streams > 1) {
+      // Buffers an arena reuses would add write-after-read hazards the schedule does not track.
+      if (this.arena) throw new Error('streams > 1 is not supported with an arena');
+      this.dag = scheduleLaunches(launches, streams, (id) => (alias.has(id) ? alias.get(id) : id));
+      a.dagReserve(this.dag.events);
+    }
   }
 
   /** Throw unless node `id` keeps its own bytes across the launches (always, without an arena). */
@@ -397,10 +408,18 @@ class Program {
   }
 
   /** Enqueue every launch once (asynchronous). */
-  run() { this.a.launchMany(this.fns, this.dims, this.args, this.offsets); }
+  run() {
+    const d = this.dag;
+    if (d) this.a.launchDag(this.fns, this.dims, this.args, this.offsets, d.streams, d.streamOf, d.recordEvent, d.waitBegin, d.waits);
+    else this.a.launchMany(this.fns, this.dims, this.args, this.offsets);
+  }
 
   /** Enqueue every launch `k` times over, in one native call (timing back-to-back runs). */
   runTimes(k) {
+    if (this.dag) {
+      for (let r = 0; r < k; r++) this.run();
+      return;
+    }
     if (!this.repeated || this.repeated.k !== k) {
       const n = this.count;
       const fns = new Float64Array(n * k), dims = new Uint32Array(n * k * 7);
@@ -420,6 +439,12 @@ class Program {
   /** Capture one run() as a HIP graph; later replay() calls enqueue it whole. */
   capture() {
     if (this.graphHandle) return;
+    if (this.dag) {
+      // Switched off: capturing config 5's step over three streams ended the process with
+      // a segmentation fault inside the runtime (config 1's step captured and replayed
+      // correctly); until its cause is known, multi-stream programs run eagerly only.
+      throw new Error('a program issued over several streams is not captured into a HIP graph');
+    }
     this.a.captureBegin();
     try { this.run(); } finally { this.graphHandle = this.a.captureEnd(); }
   }

@@ -49,7 +49,8 @@ class HipTrainer {
   /**
    * `step` from fusedStep (or an unfused step with `lowered`); `params`/`state`
    * map names to values; options.graph: replay each step as a captured HIP graph;
-   * options.arena: place the step's other buffers by live range in one allocation.
+   * options.arena: place the step's other buffers by live range in one allocation;
+   * options.streams: issue the step's independent launches on up to 4 streams.
    */
   constructor(runner, step, params, state, options) {
     const o = options || {};
@@ -57,8 +58,9 @@ class HipTrainer {
     this.a = runner.a;
     this.step = step;
     this.graph = !!o.graph;
+    if (this.graph && o.streams > 1) throw new Error('graph replay and several streams are not combined (multi-stream capture is switched off)');
     const keep = [step.loss, step.logits].concat(Object.values(step.outputs));
-    const first = runner.prepare(step.graph, step.lowered, o.arena ? { arena: { keep } } : {});
+    const first = runner.prepare(step.graph, step.lowered, Object.assign(o.arena ? { arena: { keep } } : {}, { streams: o.streams }));
     const cot = step.graph.inputId(step.cotangent);
     if (cot === undefined) throw new Error(`the step has no cotangent input '${step.cotangent}'`);
     first.write(cot, new Float32Array([1]));
@@ -77,7 +79,7 @@ class HipTrainer {
       bufs[from] = first.bufs[to];
     }
     for (const [node, source] of step.lowered.aliases || []) bufs[node] = bufs[source];
-    const second = runner.prepare(step.graph, step.lowered, { buffers: bufs, arena: first.arena });
+    const second = runner.prepare(step.graph, step.lowered, { buffers: bufs, arena: first.arena, streams: o.streams });
     this.programs = [first, second];
     this.turn = 0;   // the program the next step runs; its parameter inputs hold the current values
     this.lossBuf = new Float32Array(1);

@@ -1,0 +1,27 @@
+"""The stream schedule of the perf path (js/src/mi355x/schedule.js), checked on the CPU.
+
+Every schedule (configs 1 and 5, the reference transformer, 400 corpus graphs, at 2, 3
+and 4 streams) is replayed with vector clocks (js/src/testing/schedule_check.js), the
+way in-order streams and event waits order work: each launch must run after the launch
+that wrote each operand it reads and after the previous workspace user. Dropping any
+one wait must be caught. The GPU side (trainers on several streams, bit for bit the
+single-stream results) is in test_gpu_train.py."""
+
+
+def test_schedules_order_every_dependency(tool):
+    res = tool("schedule-check", {"models": [{"model": "transformer", "B": 64}, {"model": "mlp"},
+                                             {"model": "transformer-ref"}], "corpus": {"from": 1, "to": 200}})
+    assert len(res) == 3 * (3 + 400)
+    bad = [r for r in res if not r["check"]["ok"]]
+    assert not bad, bad[:3]
+    c5 = [r for r in res if r["name"] == "transformer-64"]
+    # Config 5's step: 432 launches on a dependency chain of 285; every stream gets work.
+    assert all(r["launches"] == 432 and r["criticalPath"] < 300 and r["used"] == r["streams"] for r in c5), c5
+
+
+def test_a_dropped_wait_is_caught(tool):
+    res = tool("schedule-check", {"models": [{"model": "transformer", "B": 64}, {"model": "mlp"}],
+                                  "corpus": {"from": 1, "to": 60}, "plant": True})
+    planted = [r for r in res if "planted" in r]
+    assert len(planted) > 100
+    assert all(not r["planted"]["ok"] for r in planted), [r["name"] for r in planted if r["planted"]["ok"]][:5]
