@@ -26,8 +26,8 @@
 // load into four 32-bit LDS writes that collide on the same banks; measured
 // on the MI355X, that stalled LDS for a third of the kernel's time.)
 //
-// Tiling: a workgroup of 256 threads (4 wavefronts in a 2 x 2 grid) owns a
-// BM x BN tile of C; each wavefront owns (TM·16) x (TN·16) of it as TM x TN
+// Tiling: a workgroup of 2 x WN wavefronts (WN = 2: 256 threads, WN = 4: 512)
+// owns a BM x BN tile of C; each wavefront owns (TM·16) x (TN·16) of it as TM x TN
 // accumulators of v_mfma_f32_16x16x4f32 (D 16x16 += A 16x4 · B 4x16). K is
 // walked BK (16, 32 or 64) at a time through two LDS buffers: the global loads
 // of the next slice are in flight while the current one feeds the matrix
@@ -72,13 +72,16 @@ struct DenseView {
 // epilogue. MODE_C needs C % 4 == 0 and MODE_R needs R % 4 == 0 (R, C: the
 // operand's extents), and both need every other stride a multiple of 4, so a
 // 128-bit load is aligned and either wholly inside the operand or wholly out.
-template <int TM, int TN, int BK, int PF, int AMODE, int BMODE, bool SPLIT, class AV, class BV, class Epi>
+template <int TM, int TN, int BK, int PF, int AMODE, int BMODE, bool SPLIT, class AV, class BV, class Epi, int WN = 2,
+          bool PRIO = false>
 __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restrict__ a_ptr,
                                          const float* __restrict__ b_ptr, const uint32_t batch, const uint32_t M,
                                          const uint32_t K, const uint32_t N, const uint32_t chunks,
                                          const uint32_t chunkK) {
+  // 2 x WN wavefronts; each owns (TM·16) x (TN·16) of the BM x BN tile.
+  constexpr int THREADS = 64 * 2 * WN;
   constexpr int BM = 2 * TM * 16;
-  constexpr int BN = 2 * TN * 16;
+  constexpr int BN = WN * TN * 16;
   static_assert(BK == 16 || BK == 32 || BK == 64, "slice depth");
   static_assert(PF == 1 || PF == 2, "prefetch depth");
   constexpr bool A_KMAJOR = AMODE == MODE_R;   // As[k][row] instead of As[row][k]
@@ -99,14 +102,14 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int t16 = lane & 15, q = lane >> 4;
 
   // Per-thread staging registers for one K slice.
-  constexpr int A_VEC = (BM * BK / 4 + 255) / 256;   // float4 loads per thread
-  constexpr int B_VEC = (BK * BN / 4 + 255) / 256;
-  constexpr int A_SC = (BM * BK + 255) / 256;        // scalar loads per thread
-  constexpr int B_SC = (BK * BN + 255) / 256;
+  constexpr int A_VEC = (BM * BK / 4 + THREADS - 1) / THREADS;   // float4 loads per thread
+  constexpr int B_VEC = (BK * BN / 4 + THREADS - 1) / THREADS;
+  constexpr int A_SC = (BM * BK + THREADS - 1) / THREADS;        // scalar loads per thread
+  constexpr int B_SC = (BK * BN + THREADS - 1) / THREADS;
   constexpr bool VA = AMODE != MODE_S, VB = BMODE != MODE_S;
   // Staging registers for a slice in flight: one set, or two for PF = 2 (the
   // global loads of slice k + 2 are issued while slice k is computed, so each
@@ -127,7 +130,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
     if (AMODE == MODE_C) {
 #pragma unroll
       for (int v = 0; v < A_VEC; ++v) {
-        const int t = tid + v * 256;
+        const int t = tid + v * THREADS;
         const uint32_t row = t / (BK / 4), kk = (t % (BK / 4)) * 4;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t < BM * BK / 4 && m0 + row < M && k0 + kk < kend)
@@ -137,7 +140,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
     } else if (AMODE == MODE_R) {
 #pragma unroll
       for (int v = 0; v < A_VEC; ++v) {
-        const int t = tid + v * 256;
+        const int t = tid + v * THREADS;
         const uint32_t kk = t / (BM / 4), row = (t % (BM / 4)) * 4;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t < BM * BK / 4 && m0 + row < M && k0 + kk < kend)
@@ -147,7 +150,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
     } else {
 #pragma unroll
       for (int v = 0; v < A_SC; ++v) {
-        const int t = tid + v * 256;
+        const int t = tid + v * THREADS;
         const uint32_t row = t / BK, kk = t % BK;
         float x = 0.f;
         if (t < BM * BK && m0 + row < M && k0 + kk < kend) x = Ab[(size_t)(m0 + row) * AV::SR + (size_t)(k0 + kk) * AV::SC];
@@ -157,7 +160,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
     if (BMODE == MODE_C) {
 #pragma unroll
       for (int v = 0; v < B_VEC; ++v) {
-        const int t = tid + v * 256;
+        const int t = tid + v * THREADS;
         const uint32_t kk = t / (BN / 4), c = (t % (BN / 4)) * 4;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t < BK * BN / 4 && k0 + kk < kend && n0 + c < N)
@@ -167,7 +170,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
     } else if (BMODE == MODE_R) {
 #pragma unroll
       for (int v = 0; v < B_VEC; ++v) {
-        const int t = tid + v * 256;
+        const int t = tid + v * THREADS;
         const uint32_t c = t / (BK / 4), kk = (t % (BK / 4)) * 4;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t < BK * BN / 4 && k0 + kk < kend && n0 + c < N)
@@ -177,7 +180,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
     } else {
 #pragma unroll
       for (int v = 0; v < B_SC; ++v) {
-        const int t = tid + v * 256;
+        const int t = tid + v * THREADS;
         const uint32_t kk = t / BN, c = t % BN;
         float x = 0.f;
         if (t < BK * BN && k0 + kk < kend && n0 + c < N) x = Bb[(size_t)(k0 + kk) * BV::SR + (size_t)(n0 + c) * BV::SC];
@@ -194,7 +197,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
     if (AMODE == MODE_C) {
 #pragma unroll
       for (int v = 0; v < A_VEC; ++v) {
-        const int t = tid + v * 256;
+        const int t = tid + v * THREADS;
         if (t < BM * BK / 4) {
           const int row = t / (BK / 4), kk = (t % (BK / 4)) * 4;
           *reinterpret_cast<float4*>(&As[buf][row * AS + kk]) = ra[v];
@@ -203,7 +206,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
     } else if (AMODE == MODE_R) {
 #pragma unroll
       for (int v = 0; v < A_VEC; ++v) {
-        const int t = tid + v * 256;
+        const int t = tid + v * THREADS;
         if (t < BM * BK / 4) {
           const int kk = t / (BM / 4), row = (t % (BM / 4)) * 4;
           *reinterpret_cast<float4*>(&As[buf][kk * AS + row]) = ra[v];
@@ -212,14 +215,14 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
     } else {
 #pragma unroll
       for (int v = 0; v < A_SC; ++v) {
-        const int t = tid + v * 256;
+        const int t = tid + v * THREADS;
         if (t < BM * BK) As[buf][(t / BK) * AS + (t % BK)] = sa[v];
       }
     }
     if (BMODE == MODE_C) {
 #pragma unroll
       for (int v = 0; v < B_VEC; ++v) {
-        const int t = tid + v * 256;
+        const int t = tid + v * THREADS;
         if (t < BK * BN / 4) {
           const int kk = t / (BN / 4), c = (t % (BN / 4)) * 4;
           *reinterpret_cast<float4*>(&Bs[buf][kk * BS + c]) = rb[v];
@@ -228,7 +231,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
     } else if (BMODE == MODE_R) {
 #pragma unroll
       for (int v = 0; v < B_VEC; ++v) {
-        const int t = tid + v * 256;
+        const int t = tid + v * THREADS;
         if (t < BK * BN / 4) {
           const int c = t / (BK / 4), kk = (t % (BK / 4)) * 4;
           *reinterpret_cast<float4*>(&Bs[buf][c * BS + kk]) = rb[v];
@@ -237,7 +240,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
     } else {
 #pragma unroll
       for (int v = 0; v < B_SC; ++v) {
-        const int t = tid + v * 256;
+        const int t = tid + v * THREADS;
         if (t < BK * BN) Bs[buf][(t / BN) * BS + (t % BN)] = sb[v];
       }
     }
@@ -254,6 +257,8 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
   // the tile transposed: lane (t16, q) holds row t16, columns 4q .. 4q+3 of each
   // 16 x 16 output tile — four consecutive outputs, stored with one 128-bit write.
   auto compute = [&](const int cur) {
+    // PRIO: a wavefront in its MFMA phase is issued ahead of wavefronts loading or storing.
+    if (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int g = 0; g < BK / 16; ++g) {
       // A values of this lane for every row tile: k = 16g + 4q .. 16g + 4q + 3 of the slice.
@@ -289,6 +294,7 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
         }
       }
     }
+    if (PRIO) __builtin_amdgcn_s_setprio(0);
   };
 
   const uint32_t slices = (kend - kbeg + BK - 1) / BK;

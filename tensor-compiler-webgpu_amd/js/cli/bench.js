@@ -73,8 +73,9 @@ function measureGraph(runner, bench, name, graph, keep, inputs, opts) {
   const lf = lowerMI355X(f.graph, { perf: true, keep: keep.map((id) => f.index.get(id)) });
   const lu = lowerMI355X(graph, { perf: true, keep });
   runner.functions([lf, lu]);
-  const pf = prepared(runner, f.graph, lf, inputs);
-  const pu = prepared(runner, graph, lu, inputs);
+  // With o.arena, each program's node buffers share one allocation by live range.
+  const pf = prepared(runner, f.graph, lf, inputs, o.arena ? { arena: { keep: keep.map((id) => f.index.get(id)) } } : undefined);
+  const pu = prepared(runner, graph, lu, inputs, o.arena ? { arena: { keep } } : undefined);
   const t = bench.time({ fused: pf, unfused: pu }, { reps: o.reps });
   const launchF = timeLaunches(runner, bench, pf, o.launchReps);
   const launchU = o.skipUnfusedLaunches ? null : timeLaunches(runner, bench, pu, o.launchReps);
@@ -143,6 +144,7 @@ function c2(runner, bench, opts) {
   const programs = [];
   const results = [];
   const stepOnly = flag('step-only');
+  const arena = flag('arena');
   for (let s = 0; s < P; s++) {
     const w = chainWorkload(s, R, C);
     const inputs = chainInputs(s, R, C);
@@ -154,12 +156,12 @@ function c2(runner, bench, opts) {
         const f = fuse(v.graph, { keep: v.keep });
         const lf = lowerMI355X(f.graph, { perf: true, keep: v.keep.map((id) => f.index.get(id)) });
         runner.functions(lf);
-        programs.push(prepared(runner, f.graph, lf, inputs));
+        programs.push(prepared(runner, f.graph, lf, inputs, arena ? { arena: { keep: v.keep.map((id) => f.index.get(id)) } } : undefined));
         results.push({ name: `c2-p${s}-${kind}`, bytes: { fused: lf.launches.reduce((q, l) => q + l.bytes, 0) }, launchF: [],
           launches: launchRecords(lf) });
         continue;
       }
-      const r = measureGraph(runner, bench, `c2-p${s}-${kind}`, v.graph, v.keep, inputs, { keepPrograms: true, reps: opts.reps });
+      const r = measureGraph(runner, bench, `c2-p${s}-${kind}`, v.graph, v.keep, inputs, { keepPrograms: true, reps: opts.reps, arena });
       r.ops = w.ops;
       programs.push(r.programs.pf);
       r.programs.pu.destroy();
@@ -185,7 +187,7 @@ function c2(runner, bench, opts) {
   // chosen without timing so a profile of the same step names the same kernel (each
   // fused body is its own kernel, at one size, so its average is well defined).
   const all = [].concat.apply([], results.map((r) => r.launchF)).filter((l) => l.kind.startsWith('fused-'));
-  return { config: 'c2', shape: [R, C], programs: P, steps: K, warmup: W, msPerStep: ms / K, wallMsPerStep: wallMs / K,
+  return { config: 'c2', shape: [R, C], programs: P, steps: K, warmup: W, arena, msPerStep: ms / K, wallMsPerStep: wallMs / K,
     stepBytes, gbs: stepBytes / ((ms / K) * 1e6), dominant: stepOnly ? null : dominant(all), results };
 }
 
