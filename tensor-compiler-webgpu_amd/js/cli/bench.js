@@ -197,9 +197,9 @@ function c2(runner, bench, opts) {
  * sees each of its kernels a known number of times. Returns every launch's kernel
  * names with its algorithmic bytes and flops.
  */
-function runOnly(runner, name, graph, keep, inputs) {
+function runOnly(runner, name, graph, keep, inputs, fuseOptions) {
   const K = Number(arg('steps', 20)), W = Number(arg('warmup', 3));
-  const f = fuse(graph, { keep });
+  const f = fuse(graph, Object.assign({ keep }, fuseOptions || {}));
   const lf = lowerMI355X(f.graph, { perf: true, keep: keep.map((id) => f.index.get(id)) });
   runner.functions(lf);
   const p = prepared(runner, f.graph, lf, inputs);
@@ -239,6 +239,11 @@ function attention(runner, bench, opts) {
     const onehot = () => { const a = new Float32Array(rows * V); for (let i = 0; i < rows; i++) a[i * V + rng.int(0, V - 1)] = 1; return a; };
     inputs.x = onehot();
     inputs.y = onehot();
+    if (flag('step-only')) {
+      // Profiling mode: the forward pass with attention fused, nothing else timed.
+      results.push(runOnly(runner, `attention-${name}`, fwd.graph, keep, inputs, { attention: true }));
+      continue;
+    }
     const fc = fuse(fwd.graph, { keep });
     const fa = fuse(fwd.graph, { keep, attention: true });
     const lc = lowerMI355X(fc.graph, { perf: true, keep: keep.map((id) => fc.index.get(id)) });
@@ -266,7 +271,7 @@ function attention(runner, bench, opts) {
       contract: t.stats.contract, attention: t.stats.attention, verdict: verdict(t.stats.contract, t.stats.attention),
       maxAbsDiffLogits: maxDiff, groups });
   }
-  return { config: 'attention', results };
+  return { config: 'attention', results, stepOnly: flag('step-only') };
 }
 
 function c3(runner, bench, opts) {
