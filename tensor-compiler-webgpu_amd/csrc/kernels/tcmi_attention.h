@@ -43,10 +43,13 @@ struct AttnTiles {
 
 // Staging of one operand tile (K as Ks[key][d], V as Vs[key][d]) through
 // registers: load() issues every global load of this thread's share at once
-// (128-bit where the layout allows), store() writes them to LDS. Splitting the
-// two lets the V loads fly while the scores are computed. View V_ element
-// (b, r, c) is at V_::batch(b) + r·SR + c·SC; the tile's LDS row is `key`,
-// its column `d`: for K (Kt's view) key = c and d = r, for V key = r and d = c.
+// (128-bit where the layout allows) into `r`, store() writes `r` to LDS.
+// Splitting the two lets the V loads fly while the scores are computed. The
+// registers are native 4-vectors, which the compiler keeps in VGPRs (an array
+// of the HIP float4 struct, live across the scores, was placed in scratch).
+// View V_ element (b, r, c) is at V_::batch(b) + r·SR + c·SC; the tile's LDS
+// row is `key`, its column `d`: for K (Kt's view) key = c and d = r, for V
+// key = r and d = c.
 template <int KEYS, int D, int STRIDE, int MODE, bool KEY_IS_C, class V_, int THREADS>
 struct AttnStage {
   // 128-bit along d (one 128-bit LDS store), along the keys (four 32-bit stores), or per element.
@@ -54,43 +57,42 @@ struct AttnStage {
   static constexpr int VEC = MODE != MODE_S ? 4 : 1;
   static constexpr int TOTAL = KEYS * D / VEC;
   static constexpr int PER = (TOTAL + THREADS - 1) / THREADS;
-  float4 r[PER];
 
-  __device__ __forceinline__ void load(const float* __restrict__ base, uint32_t b) {
+  static __device__ __forceinline__ void load(f4 (&r)[PER], const float* __restrict__ base, uint32_t b) {
     const float* __restrict__ p = base + V_::batch(b);
 #pragma unroll
     for (int v = 0; v < PER; ++v) {
       const int t = threadIdx.x + v * THREADS;
-      if (t >= TOTAL) continue;
+      if (TOTAL % THREADS != 0 && t >= TOTAL) continue;
       if (MODE == MODE_S) {
         const int key = t / D, d = t % D;
-        r[v].x = KEY_IS_C ? p[(size_t)d * V_::SR + (size_t)key * V_::SC] : p[(size_t)key * V_::SR + (size_t)d * V_::SC];
+        r[v][0] = KEY_IS_C ? p[(size_t)d * V_::SR + (size_t)key * V_::SC] : p[(size_t)key * V_::SR + (size_t)d * V_::SC];
       } else if (ALONG_D) {
         const int key = t / (D / 4), d = (t % (D / 4)) * 4;
-        r[v] = *reinterpret_cast<const float4*>(p + (size_t)key * (KEY_IS_C ? V_::SC : V_::SR) + d);
+        r[v] = *reinterpret_cast<const f4*>(p + (size_t)key * (KEY_IS_C ? V_::SC : V_::SR) + d);
       } else {
         const int d = t / (KEYS / 4), key = (t % (KEYS / 4)) * 4;
-        r[v] = *reinterpret_cast<const float4*>(p + (size_t)d * (KEY_IS_C ? V_::SR : V_::SC) + key);
+        r[v] = *reinterpret_cast<const f4*>(p + (size_t)d * (KEY_IS_C ? V_::SR : V_::SC) + key);
       }
     }
   }
 
-  __device__ __forceinline__ void store(float* tile) const {
+  static __device__ __forceinline__ void store(const f4 (&r)[PER], float* tile) {
 #pragma unroll
     for (int v = 0; v < PER; ++v) {
       const int t = threadIdx.x + v * THREADS;
-      if (t >= TOTAL) continue;
+      if (TOTAL % THREADS != 0 && t >= TOTAL) continue;
       if (MODE == MODE_S) {
-        tile[(t / D) * STRIDE + t % D] = r[v].x;
+        tile[(t / D) * STRIDE + t % D] = r[v][0];
       } else if (ALONG_D) {
         const int key = t / (D / 4), d = (t % (D / 4)) * 4;
-        *reinterpret_cast<float4*>(&tile[key * STRIDE + d]) = r[v];
+        *reinterpret_cast<f4*>(&tile[key * STRIDE + d]) = r[v];
       } else {
         const int d = t / (KEYS / 4), key = (t % (KEYS / 4)) * 4;
-        tile[(key + 0) * STRIDE + d] = r[v].x;
-        tile[(key + 1) * STRIDE + d] = r[v].y;
-        tile[(key + 2) * STRIDE + d] = r[v].z;
-        tile[(key + 3) * STRIDE + d] = r[v].w;
+        tile[(key + 0) * STRIDE + d] = r[v][0];
+        tile[(key + 1) * STRIDE + d] = r[v][1];
+        tile[(key + 2) * STRIDE + d] = r[v][2];
+        tile[(key + 3) * STRIDE + d] = r[v][3];
       }
     }
   }

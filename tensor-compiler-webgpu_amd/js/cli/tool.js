@@ -793,6 +793,32 @@ async function main() {
       };
       break;
     }
+    case 'kernel-unit': {
+      // One translation unit of every kernel the standard runs launch (config 5's step in
+      // both lowerings, configs 2-4 fused in the perf lowering, the forward pass with
+      // attention fused), as the runner compiles them: for resource checks of the code.
+      const { translationUnit } = require('../src/mi355x/runner');
+      const { modelStep } = require('../src/builders/models');
+      const { fusedStep } = require('../src/mi355x/trainer');
+      const { chainWorkload } = require('../src/builders/chains');
+      const cfg = require('../src/builders/configs');
+      const m = new Map();
+      const add = (lw) => { for (const l of lw.launches) for (const k of l.kernels) m.set(k.name, k.source); };
+      const perf = (v, fuseOpts) => {
+        const f = fuse(v.graph, Object.assign({ keep: v.keep }, fuseOpts || {}));
+        add(lowerMI355X(f.graph, { perf: true, keep: v.keep.map((id) => f.index.get(id)) }));
+      };
+      const fs = fusedStep(modelStep({ model: 'transformer', B: 64 }).step);
+      add(fs.lowered);
+      add(fs.checked);
+      for (let s2 = 0; s2 < 8; s2++) { const w = chainWorkload(s2, 8192, 1024); perf(w.forward); perf(w.gradient); }
+      for (const fn of ['softmax', 'logSoftmax']) { const g = cfg.c3Graphs(fn, cfg.C3_SHAPE[0], cfg.C3_SHAPE[1]); perf(g.forward); perf(g.gradient); }
+      for (const [M, K, N] of cfg.C4_SHAPES) for (const act of ['relu', 'tanh']) { const g = cfg.c4Graphs(act, M, K, N); perf(g.forward); perf(g.gradient); }
+      const fw = transformerForward({ config: 'c5', V: 96, B: 64 });
+      perf({ graph: Graph.fromJSON(fw.graph), keep: fw.keep }, { attention: true });
+      out = { kernels: Array.from(m.keys()), unit: translationUnit(m) };
+      break;
+    }
     case 'schedule-check': {
       // Stream schedules of model steps and corpus programs (perf lowering) at 2..4 streams,
       // checked by replaying them with vector clocks; with `plant`, one wait dropped.

@@ -969,21 +969,22 @@ ${qv.text}${kv.text}${vv.text}extern "C" __global__ void __launch_bounds__(${THR
   const uint32_t row = blockIdx.x * ${16 * WAVES}u + wave * 16u + t16;   // this lane's query row
   tcmi::attn_zero_padding<${TK}, ${DH}, ${DV}, ${THREADS}>(Ks, Vs);
   // Every global load of the K and V tiles issued at once; V lands in LDS after the scores.
-  tcmi::AttnStage<${TK}, ${DH}, G::KS, ${kv.mode}, true, __KERNEL___kv, ${THREADS}> kst;
-  tcmi::AttnStage<${TK}, ${DV}, G::VS, ${vv.mode}, false, __KERNEL___vv, ${THREADS}> vst;
-  kst.load(A.in[${ik}], b);
-  vst.load(A.in[${iv}], b);
+  using Kst = tcmi::AttnStage<${TK}, ${DH}, G::KS, ${kv.mode}, true, __KERNEL___kv, ${THREADS}>;
+  using Vst = tcmi::AttnStage<${TK}, ${DV}, G::VS, ${vv.mode}, false, __KERNEL___vv, ${THREADS}>;
+  tcmi::f4 kr[Kst::PER], vr[Vst::PER];
+  Kst::load(kr, A.in[${ik}], b);
+  Vst::load(vr, A.in[${iv}], b);
   tcmi::f4 qf[G::DH16];
   tcmi::attn_q<${TQ}, ${DH}, G::DH16, ${qv.mode}, __KERNEL___qv>(qf, A.in[${iq}], b, row, q);
   const bool rowOk = row < ${TQ}u;
   const uint32_t r = b * ${TQ}u + (rowOk ? row : 0u);   // the score row (rows past TQ compute nothing)
   const uint32_t rowBase = r * ${TK}u;
 ${indent(cacheFill, '  ')}
-  kst.store(Ks);
+  Kst::store(kr, Ks);
   __syncthreads();
   tcmi::f4 sacc[G::NT];
   tcmi::attn_scores<G::NT, G::DH16, G::KS>(sacc, qf, Ks, t16, q);
-  vst.store(Vs);
+  Vst::store(vr, Vs);
 ${indent(phases, '  ')}
   tcmi::f4 p[${NT}];
 ${indent(pre.concat([pLoop]), '  ')}
