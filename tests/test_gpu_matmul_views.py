@@ -16,9 +16,12 @@ from oracle import bounds
 
 pytestmark = pytest.mark.gpu
 
-# (name, batch dims, M, K, N); the K and N of the last two exercise the per-element path.
+# (name, batch dims, M, K, N); the K and N of "odd" and "odd-batched" exercise the
+# per-element path; "wide-split" takes the 2 x 4-wavefront tiles with a ragged last
+# column tile and a K split, "wide-odd" those tiles with N not a multiple of 4.
 SHAPES = [("ragged", [], 100, 72, 132), ("tiles", [], 256, 512, 192), ("batched", [3], 40, 64, 56),
-          ("odd", [], 33, 17, 29), ("odd-batched", [2], 9, 30, 11)]
+          ("odd", [], 33, 17, 29), ("odd-batched", [2], 9, 30, 11), ("wide-split", [], 1000, 2100, 260),
+          ("wide-odd", [], 4100, 96, 262)]
 
 
 def _graph(tool, bd, M, K, N, ta, tb, act):
