@@ -631,6 +631,7 @@ async function gpuLocal(req, dir) {
   entry.canaryIntact = entry.gpuCanary && entry.gpuPerfCanary;
   entry.aliases = fs.lowered.aliases;
   entry.folded = fs.lowered.folded;
+  entry.dead = fs.lowered.dead;
   bundle.add(entry);
   bundle.close({ device: runner.info() });
 }
@@ -927,7 +928,7 @@ async function main() {
       }
       const l = lowerMI355X(g, { perf: true, keep });
       const plain = new Map(lowerMI355X(g).launches.map((x) => [x.node, x]));
-      out = { graph: g.toJSON(), keep, aliases: l.aliases, folded: l.folded,
+      out = { graph: g.toJSON(), keep, aliases: l.aliases, folded: l.folded, dead: l.dead,
         launches: l.launches.map((x) => ({ node: x.node, kind: x.kind, inputs: x.inputs, views: x.views || null, modes: gemmModes(x),
           split: gemmSplit(x), plainSplit: gemmSplit(plain.get(x.node)) })) };
       break;

@@ -29,7 +29,7 @@ function planArena(graph, lowered, options) {
   const o = options || {};
   const align = o.align || 256;
   const alias = new Map(lowered.aliases || []);
-  const folded = new Set(lowered.folded || []);
+  const folded = new Set((lowered.folded || []).concat(lowered.dead || []));   // no buffer
   const owner = (id) => (alias.has(id) ? alias.get(id) : id);
   const bytes = (id) => Math.max(16, Math.ceil(graph.nodes[id].shape.reduce((p, d) => p * d, 1) * 4 / align) * align);
   const INF = Number.MAX_SAFE_INTEGER;

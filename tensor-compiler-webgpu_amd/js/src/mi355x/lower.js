@@ -176,9 +176,20 @@ function matmulSlots(n) {
   return slots;
 }
 
-/** Perf-mode plan: { aliases: id -> source, folded: Set, views: id -> {a, b} of { source, view } }. */
+/**
+ * Perf-mode plan: { aliases: id -> source, folded: Set, views: id -> {slot: { source, view }},
+ * broadcasts, dead: Set }. `dead`: nodes whose values nothing kept depends on (autodiff leaves
+ * such sinks, e.g. the gradient flowing into the max shift's stopGradient, or the dX of a
+ * one-hot input): no launch, no buffer. Inputs and constants are never dead.
+ */
 function perfPlan(graph, keep) {
   const cons = consumersOf(graph);
+  const live = new Set();
+  for (let id = graph.nodes.length - 1; id >= 0; id--) {
+    const n = graph.nodes[id];
+    if (keep.has(id) || n.op === 'input' || n.op === 'const' || cons[id].some((c) => live.has(c))) live.add(id);
+  }
+  const dead = new Set(graph.nodes.filter((n) => !live.has(n.id)).map((n) => n.id));
   const aliases = new Map();
   for (const n of graph.nodes) {
     if (n.op === 'reshape' && !keep.has(n.id)) {
@@ -239,7 +250,7 @@ function perfPlan(graph, keep) {
       views.get(n.id)[slot] = { pos, source: cur, view, size: size(graph.nodes[cur].shape) };
     }
   }
-  return { aliases, folded, views, broadcasts };
+  return { aliases, folded, views, broadcasts, dead };
 }
 
 /**
@@ -249,18 +260,21 @@ function perfPlan(graph, keep) {
  * applied to fused kernels only; tuning ({ ew: { unroll, nt, blocks }, colreduce: { blocks } })
  * overrides the kernels' launch-shape defaults (used by sweeps); perf and
  * keep (node ids) as described at the top of this file.
- * Returns { launches, workspace, aliases, folded } (workspace: bytes of scratch
- * the largest launch needs; aliases: [[node, source]]; folded: node ids).
+ * Returns { launches, workspace, aliases, folded, dead } (workspace: bytes of scratch
+ * the largest launch needs; aliases: [[node, source]]; folded and dead: node ids with
+ * neither a launch nor a buffer).
  */
 function lowerMI355X(graph, options) {
   const opts = options || {};
-  const plan = opts.perf ? perfPlan(graph, new Set(opts.keep || [])) : { aliases: new Map(), folded: new Set(), views: new Map(), broadcasts: new Map() };
+  if (opts.perf && !opts.keep) throw new Error('the perf lowering needs `keep`: the nodes whose values are read');
+  const plan = opts.perf ? perfPlan(graph, new Set(opts.keep))
+    : { aliases: new Map(), folded: new Set(), views: new Map(), broadcasts: new Map(), dead: new Set() };
   const cache = new Map();
   const launches = [];
   let workspace = 0;
   for (const node of graph.nodes) {
     if (node.op === 'input' || node.op === 'const') continue;
-    if (plan.aliases.has(node.id) || plan.folded.has(node.id)) continue;
+    if (plan.aliases.has(node.id) || plan.folded.has(node.id) || plan.dead.has(node.id)) continue;
     const v = plan.views.get(node.id);
     let mmViews = null;
     if (v) {
@@ -290,7 +304,7 @@ function lowerMI355X(graph, options) {
       for (const slot of Object.keys(v)) launches[launches.length - 1].views[slot] = { pos: v[slot].pos, operand: node.inputs[v[slot].pos], source: v[slot].source, view: v[slot].view };
     }
   }
-  return { launches, workspace, aliases: Array.from(plan.aliases.entries()), folded: Array.from(plan.folded) };
+  return { launches, workspace, aliases: Array.from(plan.aliases.entries()), folded: Array.from(plan.folded), dead: Array.from(plan.dead) };
 }
 
 /** Every distinct kernel source of a launch list, in first-use order. */

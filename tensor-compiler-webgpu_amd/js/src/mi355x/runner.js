@@ -123,11 +123,14 @@ function packArgs(view, offset, inPtrs, outPtr, wsPtr, params) {
   for (let k = 0; k < MAX_P; k++) view.setUint32(offset + MAX_IN * 8 + 16 + 4 * k, k < params.length ? params[k] : 0, true);
 }
 
-/** The perf lowering's buffer sharing: alias (node -> node whose buffer it uses) and folded (no buffer). */
+/**
+ * The perf lowering's buffer sharing: alias (node -> node whose buffer it uses) and
+ * folded (no buffer: folded into its consumers, or dead).
+ */
 function sharing(lowered) {
   const alias = new Map(lowered.aliases || []);
   for (const [k, v] of alias) if (alias.has(v)) throw new Error(`alias chain ${k} -> ${v} is not resolved`);
-  return { alias, folded: new Set(lowered.folded || []) };
+  return { alias, folded: new Set((lowered.folded || []).concat(lowered.dead || [])) };
 }
 
 /**
@@ -400,7 +403,7 @@ class Program {
   }
 
   read(id) {
-    if (!this.bufs[id]) throw new Error(`node ${id} is not materialised (a transpose folded into its matmuls)`);
+    if (!this.bufs[id]) throw new Error(`node ${id} is not materialised (folded into its consumers, or nothing kept reads it)`);
     this.persistent(id, 'read');
     const out = new Float32Array(this.n[id]);
     this.a.d2h(this.bufs[id], 0, out);

@@ -187,7 +187,8 @@ def _chain_value(graph, operand, source, src_value):
 @pytest.mark.parametrize("req", [{"model": "mlp"}, {"model": "transformer", "B": 2}, {"model": "transformer-ref"}])
 def test_perf_lowering_views_address_the_operands(tool, req):
     """The perf lowering skips only reshapes (sharing their input's buffer), transposes
-    whose every consumer is a matmul operand slot and broadcasts read by bodies; each matmul operand it reads in place
+    whose every consumer is a matmul operand slot, broadcasts read by bodies, and the
+    nodes no kept value depends on (dead); each matmul operand it reads in place
     is addressed by its strided view exactly as the transpose chain would have laid it out
     (checked element by element on distinct values), and the load mode matches the view."""
     d = tool("perf-lower", req)
@@ -207,8 +208,14 @@ def test_perf_lowering_views_address_the_operands(tool, req):
             for c in consumers[i]:
                 assert nodes[c]["op"] == "fused" or nodes[c]["op"] in ("add", "sub", "mul", "div", "neg", "exp", "log",
                                                                       "relu", "tanh", "sqrt", "step", "stopGradient"), nodes[c]["op"]
+    # Dead nodes: exactly those no kept node depends on (liveness recomputed here).
+    live = set()
+    for n_id in range(len(nodes) - 1, -1, -1):
+        if n_id in d["keep"] or nodes[n_id]["op"] in ("input", "const") or consumers.get(n_id, set()) & live:
+            live.add(n_id)
+    assert set(d["dead"]) == {n_id for n_id in range(len(nodes)) if n_id not in live}
     launched = {l["node"] for l in d["launches"]}
-    skipped = {a for a, _ in d["aliases"]} | set(d["folded"])
+    skipped = {a for a, _ in d["aliases"]} | set(d["folded"]) | set(d["dead"])
     assert launched.isdisjoint(skipped)
     assert launched | skipped == {n_id for n_id, n in enumerate(nodes) if n["op"] not in ("input", "const")}
     checked = 0
