@@ -153,7 +153,11 @@ def main() -> None:
                             "loss": t["lossLast"], "time_by_kind_us": {k: round(v["us"], 1) for k, v in t["byKind"].items()},
                             "arena": {"bytes": t["arena"]["bytes"], "unshared_bytes": t["arena"]["unshared"],
                                       "steps_per_sec": t["arena"]["stepsPerSec"],
-                                      "resident_steps_per_sec": t["arena"]["residentStepsPerSec"]}}
+                                      "resident_steps_per_sec": t["arena"]["residentStepsPerSec"]},
+                            "dispatches": t["dispatches"], "batched_launches": t["batches"],
+                            "unbatched": {"dispatches": t["unbatched"]["dispatches"],
+                                          "steps_per_sec": t["unbatched"]["stepsPerSec"],
+                                          "resident_steps_per_sec": t["unbatched"]["residentStepsPerSec"]}}
     if "attention" in cfg:
         extra["attention_extension"] = {
             r["name"]: {"contract_us": r["contract"]["median"], "attention_us": r["attention"]["median"],

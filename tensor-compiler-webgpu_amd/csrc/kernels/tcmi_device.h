@@ -42,6 +42,20 @@ struct TcmiArgs {
   uint32_t P[TCMI_MAX_P];
 };
 
+// A batched launch of one kernel over N independent launches of it (same
+// sizes, different buffers): member z's pointers, read by the workgroups with
+// blockIdx.z == z. The kernel body is the member kernel's, with A bound to
+// B.m[blockIdx.z]; only kernels whose own grid has one z-slice are batched.
+struct TcmiPtrs {
+  const float* in[TCMI_MAX_IN];
+  float* out;
+  float* ws;
+};
+template <int N>
+struct TcmiBatch {
+  TcmiPtrs m[N];
+};
+
 namespace tcmi {
 
 // A native 4-wide float vector (128-bit loads and stores, non-temporal stores).

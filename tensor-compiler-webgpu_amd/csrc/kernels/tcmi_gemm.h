@@ -73,8 +73,8 @@ struct DenseView {
 // operand's extents), and both need every other stride a multiple of 4, so a
 // 128-bit load is aligned and either wholly inside the operand or wholly out.
 template <int TM, int TN, int BK, int PF, int AMODE, int BMODE, bool SPLIT, class AV, class BV, class Epi, int WN = 2,
-          bool PRIO = false>
-__device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restrict__ a_ptr,
+          bool PRIO = false, class Args = TcmiArgs>
+__device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict__ a_ptr,
                                          const float* __restrict__ b_ptr, const uint32_t batch, const uint32_t M,
                                          const uint32_t K, const uint32_t N, const uint32_t chunks,
                                          const uint32_t chunkK) {
@@ -92,7 +92,8 @@ __device__ __forceinline__ void gemm_f32(const TcmiArgs& A, const float* __restr
   __shared__ __attribute__((aligned(16))) float Bs[2][(B_NMAJOR ? BN : BK) * BS];
 
   const uint32_t kz = SPLIT ? blockIdx.z % chunks : 0u;
-  const uint32_t bz = SPLIT ? blockIdx.z / chunks : blockIdx.z;
+  // One batch: z is 0 here, or the member index of a batched launch (TcmiBatch).
+  const uint32_t bz = SPLIT ? blockIdx.z / chunks : (batch > 1u ? blockIdx.z : 0u);
   const uint32_t kbeg = SPLIT ? kz * chunkK : 0u;
   const uint32_t kend = SPLIT ? min(K, kbeg + chunkK) : K;
   const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;

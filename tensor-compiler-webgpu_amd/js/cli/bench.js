@@ -11,7 +11,8 @@
 // launch-bound at c1's size); --no-trainer-graphs issues their launches directly.
 //
 // --step-only (for profilers): c2 runs its headline step only; c3 and c4 run each
-// fused program --steps times after --warmup runs, with no timing loops.
+// fused program --steps times after --warmup runs, with no timing loops; c1 and c5
+// run --warmup + --steps trainer steps.
 //
 // c2  fused elementwise chains (P programs, forward + gradient) over [8192, 1024]:
 //     the headline step = every fused program run once; K timed steps
@@ -209,10 +210,19 @@ function runOnly(runner, name, graph, keep, inputs, fuseOptions) {
   return { name, runs: W + K, launches: launchRecords(lf) };
 }
 
-/** Every launch of a lowering with its kernel names, algorithmic bytes and flops (for profile summaries). */
+/**
+ * Every launch of a lowering with its kernel names, algorithmic bytes and flops (for
+ * profile summaries); each batched launch as one more record, its members' work summed.
+ */
 function launchRecords(lowered) {
-  return lowered.launches.map((l) => ({ node: l.node, kind: l.kind, pattern: l.pattern || null,
+  const recs = lowered.launches.map((l) => ({ node: l.node, kind: l.kind, pattern: l.pattern || null,
     kernels: l.kernels.map((k) => k.name), bytes: l.bytes, flops: l.flops || 0 }));
+  for (const b of lowered.batches || []) {
+    const ms = lowered.launches.slice(b.start, b.start + b.count);
+    recs.push({ node: ms[0].node, kind: `batched ${ms[0].kind} x${b.count}`, pattern: ms[0].pattern || null, kernels: [b.kernel.name],
+      bytes: ms.reduce((q, l) => q + l.bytes, 0), flops: ms.reduce((q, l) => q + (l.flops || 0), 0), members: ms.map((l) => l.node) });
+  }
+  return recs;
 }
 
 /**
@@ -342,6 +352,14 @@ function trainStep(runner, bench, name, req, opts) {
   const batch = m.batch(0);
   const graph = !flag('no-trainer-graphs');
   const trainer = new HipTrainer(runner, fs, m.params, m.state, { graph });
+  if (flag('step-only')) {
+    // Profiling mode: --warmup + --steps trainer steps, nothing else run.
+    const n = Number(arg('warmup', 3)) + Number(arg('steps', 20));
+    for (let i = 0; i < n; i++) trainer.train(batch.x, batch.y);
+    trainer.destroy();
+    return { config: name, info: m.info, stepOnly: true, runs: n, graphReplay: graph,
+      results: [{ name: `${name}-step`, launches: launchRecords(fs.lowered) }] };
+  }
   for (let i = 0; i < W; i++) trainer.train(batch.x, batch.y);
   const t0 = process.hrtime.bigint();
   let loss = 0;
@@ -409,10 +427,26 @@ function trainStep(runner, bench, name, req, opts) {
       criticalPath: ts.program.dag.criticalPath, waits: ts.program.dag.waits.length };
     ts.destroy();
   }
+  // The same step with every launch dispatched by itself (no batched launches).
+  const fsPlain = fusedStep(m.step, { batch: false });
+  const tp = new HipTrainer(runner, fsPlain, m.params, m.state, { graph });
+  for (let i = 0; i < W; i++) tp.train(batch.x, batch.y);
+  const tp0 = process.hrtime.bigint();
+  for (let i = 0; i < K; i++) tp.train(batch.x, batch.y);
+  const plainWall = Number(process.hrtime.bigint() - tp0) / 1e6 / K;
+  runner.a.sync();
+  runner.a.eventRecord(bench.start);
+  for (let i = 0; i < K; i++) tp.advance();
+  runner.a.eventRecord(bench.end);
+  const plainResident = runner.a.eventElapsed(bench.start, bench.end) / K;
+  const unbatched = { dispatches: tp.program.dispatches, msPerStep: plainWall, residentMsPerStep: plainResident,
+    stepsPerSec: 1e3 / plainWall, residentStepsPerSec: 1e3 / plainResident };
+  tp.destroy();
   const flops = fs.lowered.launches.reduce((q, l) => q + (l.flops || 0), 0);
   return { config: name, info: m.info, steps: K, warmup: W, lossLast: loss, arena, streams: streamRuns, graphReplay: graph,
     stepsPerSec: 1e3 / wallMs, msPerStep: wallMs, residentMsPerStep: residentMs, residentStepsPerSec: 1e3 / residentMs,
     launches: { fused: fs.lowered.launches.length, unfused: lu.launches.length },
+    dispatches: p.dispatches, batches: (fs.lowered.batches || []).length, unbatched,
     fused: t.stats.fused, unfused: t.stats.unfused, verdict: verdict(t.stats.unfused, t.stats.fused),
     matmulFlopsPerStep: flops, matmulTflopsResident: flops / (residentMs * 1e9), byKind };
 }

@@ -29,7 +29,7 @@ const { Graph } = require('../src/ir/graph');
 const { size } = require('../src/ir/shapes');
 const { grad } = require('../src/autodiff');
 const { fuse, fusionSummary } = require('../src/fusion/fuse');
-const { lowerMI355X } = require('../src/mi355x/lower');
+const { lowerMI355X, kernelSources } = require('../src/mi355x/lower');
 const { builderCases } = require('../src/testing/cases');
 const { fusedDirectCases } = require('../src/builders/direct_cases');
 const tf = require('../src/builders/transformer');
@@ -651,6 +651,7 @@ async function gpuTrain(req) {
   const runner = HipRunner.create();
   const trainer = new HipTrainer(runner, fs, m.params, m.state, { graph: !!req.graph, arena: !!req.arena, streams: req.streams || 1 });
   const plan = trainer.program.arena;
+  const dispatches = trainer.program.dispatches;
   const losses = [];
   let identical = null;
   const names = Object.keys(Object.assign({}, m.params, m.state));
@@ -685,7 +686,9 @@ async function gpuTrain(req) {
   trainer.destroy();
   return { losses, identical, params, launches: fs.lowered.launches.length, checkedLaunches: fs.checked.launches.length,
     folded: fs.lowered.folded.length, aliases: fs.lowered.aliases.length, unfusedNodes: m.step.graph.nodes.length, info: m.info,
-    arena: plan ? { bytes: plan.size, unshared: plan.unshared, buffers: plan.buffers.length } : null };
+    arena: plan ? { bytes: plan.size, unshared: plan.unshared, buffers: plan.buffers.length } : null,
+    batches: (fs.lowered.batches || []).length, batchedLaunches: (fs.lowered.batches || []).reduce((c, b) => c + b.count, 0), dispatches,
+    kernels: fs.lowered.launches.reduce((c, l) => c + l.kernels.length, 0) };
 }
 
 async function main() {
@@ -804,7 +807,7 @@ async function main() {
       const { chainWorkload } = require('../src/builders/chains');
       const cfg = require('../src/builders/configs');
       const m = new Map();
-      const add = (lw) => { for (const l of lw.launches) for (const k of l.kernels) m.set(k.name, k.source); };
+      const add = (lw) => { for (const [name, src] of kernelSources(lw)) m.set(name, src); };
       const perf = (v, fuseOpts) => {
         const f = fuse(v.graph, Object.assign({ keep: v.keep }, fuseOpts || {}));
         add(lowerMI355X(f.graph, { perf: true, keep: v.keep.map((id) => f.index.get(id)) }));
@@ -889,6 +892,12 @@ async function main() {
             res.planted = { moved: pair[0].id, onto: pair[1].id, check: simulateArena(graph, lowered, plan) };
             pair[0].offset = saved;
           }
+          // A plan that takes the members of each batched launch one after another:
+          // its reuse of a member's last operand for a later member's output is a race.
+          if ((lowered.batches || []).length) {
+            const blind = planArena(graph, Object.assign({}, lowered, { batches: [] }), { keep });
+            res.batchBlind = simulateArena(graph, lowered, blind);
+          }
         }
         return res;
       };
@@ -898,6 +907,40 @@ async function main() {
       for (const r of req.models || []) {
         const m = modelStep(r);
         const f = fusedStep(m.step);
+        out.push(one(`${r.model}-${r.B || ''}`, f.graph, [f.loss, f.logits].concat(Object.values(f.outputs))));
+      }
+      if (req.corpus) {
+        const { corpusGraphs } = require('../src/testing/random_graph');
+        for (let i = req.corpus.from; i <= req.corpus.to; i++) {
+          for (const c of corpusGraphs(i)) {
+            const f = fuse(c.graph, { keep: c.keep });
+            out.push(one(`corpus-${i}-${c.label}`, f.graph, c.keep.map((id) => f.index.get(id))));
+          }
+        }
+      }
+      break;
+    }
+    case 'batch-check': {
+      // Batched launches of model steps and corpus programs (perf lowering), checked against
+      // the plain order; with `plant`, the two planted mistakes of batch_check.js as well.
+      const { checkBatches, plantBatchMistake } = require('../src/testing/batch_check');
+      const one = (name, graph, keep) => {
+        const plain = lowerMI355X(graph, { perf: true, keep, batch: false });
+        const batched = lowerMI355X(graph, { perf: true, keep });
+        const res = { name, launches: batched.launches.length, check: checkBatches(plain, batched) };
+        if (req.plant) {
+          for (const kind of ['dependent', 'early']) {
+            const bad = plantBatchMistake(batched, kind);
+            if (bad) res[kind] = checkBatches(plain, bad);
+          }
+        }
+        return res;
+      };
+      out = [];
+      const { modelStep } = require('../src/builders/models');
+      const { fusedStep } = require('../src/mi355x/trainer');
+      for (const r of req.models || []) {
+        const f = fusedStep(modelStep(r).step);
         out.push(one(`${r.model}-${r.B || ''}`, f.graph, [f.loss, f.logits].concat(Object.values(f.outputs))));
       }
       if (req.corpus) {

@@ -8,7 +8,8 @@
 // A launch list runs in order on one stream, so a buffer is live from the
 // launch that writes it to the last launch that reads it (a launch's operands
 // and its output are live together at that launch: no kernel here runs in
-// place). Buffers whose values must outlive the launches — inputs and
+// place). The members of a batched launch run as one dispatch, so they count
+// as one position: every operand and output of the batch is live together. Buffers whose values must outlive the launches — inputs and
 // constants the host writes before running, and the nodes the caller reads or
 // feeds back (`keep`) — are pinned for the whole program. Two buffers may
 // share bytes only when their live ranges are disjoint. Placement is first fit
@@ -45,15 +46,19 @@ function planArena(graph, lowered, options) {
     if (node.op === 'input' || node.op === 'const') pinned.add(node.id);
   }
   for (const id of o.keep || []) pin(id);
-  lowered.launches.forEach((l, i) => {
+  // The members of a batched launch run together: they share their first member's position.
+  const step = lowered.launches.map((_, i) => i);
+  for (const b of lowered.batches || []) for (let k = 1; k < b.count; k++) step[b.start + k] = b.start;
+  lowered.launches.forEach((l, li) => {
+    const i = step[li];
     for (const id of l.inputs) {
       const w = owner(id);
-      if (folded.has(w)) throw new Error(`launch ${i} (node ${l.node}) reads folded node ${id}`);
+      if (folded.has(w)) throw new Error(`launch ${li} (node ${l.node}) reads folded node ${id}`);
       end.set(w, Math.max(end.has(w) ? end.get(w) : -1, i));
       if (!firstRead.has(w)) firstRead.set(w, i);
     }
     const w = owner(l.node);
-    if (w !== l.node) throw new Error(`launch ${i} writes node ${l.node}, an alias of ${w}`);
+    if (w !== l.node) throw new Error(`launch ${li} writes node ${l.node}, an alias of ${w}`);
     if (start.has(w)) throw new Error(`node ${w} is written by two launches`);
     start.set(w, i);
     end.set(w, Math.max(end.has(w) ? end.get(w) : i, i));

@@ -778,7 +778,8 @@ function gemmKernel(b, output, opts) {
   if (av.limit > need.a || bv.limit > need.b) throw new Error(`matmul operand view out of bounds (${av.limit}/${need.a}, ${bv.limit}/${need.b})`);
   const total = batch * M * N;
   const epi = `struct __KERNEL___epi {
-  __device__ __forceinline__ float operator()(const TcmiArgs& A, uint32_t i, float acc) const {
+  template <class Args>
+  __device__ __forceinline__ float operator()(const Args& A, uint32_t i, float acc) const {
 ${indent(lines, '    ')}
     return ${out};
   }
@@ -1001,5 +1002,39 @@ ${indent(pre.concat([pLoop]), '  ')}
     modes: [qv.mode, kv.mode, vv.mode] };
 }
 
+// ---- batched launches ----------------------------------------------------------------
+
+// Members of one batched launch at most: its argument block (TcmiBatch, 80 bytes
+// a member) stays well inside the 4 KiB a launch's arguments may take.
+const MAX_BATCH = 32;
+// Kernel families whose text reads its launch only through A.in / A.out / A.ws
+// and blockIdx.x / blockIdx.y (a one-batch matmul pins its batch index to 0).
+const BATCHABLE = /^tcmi_(ew|row|mm)_[0-9a-f]+$/;
+
+/** Whether kernel `k` (a launch's only kernel) may run as a member of a batched launch. */
+function batchable(k) {
+  return BATCHABLE.test(k.name) && k.grid[2] === 1 && !k.needsPad;
+}
+
+/**
+ * One launch of kernel `k` over `count` independent sets of buffers: the same
+ * body with A bound to member blockIdx.z of a TcmiBatch argument block, and the
+ * grid's z extent `count`. Identical launches (same text: same sizes, same
+ * operand views) of independent nodes become one dispatch, so a step of many
+ * small launches (a parameter update per tensor, the three projections of an
+ * attention layer) fills the chip with one launch's workgroups instead of
+ * paying a launch's ramp and drain each.
+ */
+function batchedKernel(k, count) {
+  if (!batchable(k)) throw new Error(`kernel ${k.name} cannot be batched`);
+  if (!(Number.isInteger(count) && count >= 2 && count <= MAX_BATCH)) throw new Error(`batch of ${count} launches (2..${MAX_BATCH})`);
+  const sig = `${k.name}(const TcmiArgs A) {`;
+  if (k.source.split(sig).length !== 2) throw new Error(`kernel ${k.name}: no single entry point to batch`);
+  const text = k.source.replace(sig, `__KERNEL__(const TcmiBatch<${count}> B) {\n  const TcmiPtrs& A = B.m[blockIdx.z];`)
+    .split(k.name).join('__KERNEL__');
+  const b = kernelText(`b${k.name.split('_')[1]}`, text);
+  return { name: b.name, source: b.source, grid: [k.grid[0], k.grid[1], count], block: k.block.slice(), lds: k.lds, members: count };
+}
+
 module.exports = { elementwiseKernel, rowwiseKernel, colreduceKernels, gemmKernel, gemmTiling, attentionKernel, classifyGather, gatherStrides,
-  literal, fnv, Emitter, WG, MAX_P, MAX_IN };
+  literal, fnv, Emitter, WG, MAX_P, MAX_IN, MAX_BATCH, batchable, batchedKernel };

@@ -31,6 +31,10 @@
 //     epilogue body (not as a matmul operand, not through a reduction or another
 //     gather) launches nothing: each consumer's kernel reads the broadcast's
 //     source through the broadcast's index map instead of a materialised copy.
+//   - launches of one kernel text with no data path between them (the three
+//     projections of an attention layer, the per-tensor parameter updates) are
+//     placed together and listed in `batches`: the runner issues each batch as
+//     one dispatch of the kernel's batched form (batchPlan below).
 // Nodes in `keep` are never folded, so their values stay readable.
 
 const { Graph } = require('../ir/graph');
@@ -259,10 +263,11 @@ function perfPlan(graph, keep) {
  * 'layernorm-tree-short', 'softmax-no-max', 'fused-bounds-off-by-one'),
  * applied to fused kernels only; tuning ({ ew: { unroll, nt, blocks }, colreduce: { blocks } })
  * overrides the kernels' launch-shape defaults (used by sweeps); perf and
- * keep (node ids) as described at the top of this file.
- * Returns { launches, workspace, aliases, folded, dead } (workspace: bytes of scratch
- * the largest launch needs; aliases: [[node, source]]; folded and dead: node ids with
- * neither a launch nor a buffer).
+ * keep (node ids) as described at the top of this file; batch: false keeps the
+ * perf lowering's launches one dispatch each, in graph order.
+ * Returns { launches, workspace, aliases, folded, dead, batches } (workspace: bytes of
+ * scratch the largest launch needs; aliases: [[node, source]]; folded and dead: node
+ * ids with neither a launch nor a buffer; batches, perf only: [{ start, count, kernel }]).
  */
 function lowerMI355X(graph, options) {
   const opts = options || {};
@@ -304,14 +309,53 @@ function lowerMI355X(graph, options) {
       for (const slot of Object.keys(v)) launches[launches.length - 1].views[slot] = { pos: v[slot].pos, operand: node.inputs[v[slot].pos], source: v[slot].source, view: v[slot].view };
     }
   }
-  return { launches, workspace, aliases: Array.from(plan.aliases.entries()), folded: Array.from(plan.folded), dead: Array.from(plan.dead) };
+  const out = { launches, workspace, aliases: Array.from(plan.aliases.entries()), folded: Array.from(plan.folded), dead: Array.from(plan.dead) };
+  if (opts.perf && opts.batch !== false) Object.assign(out, batchPlan(launches, plan.aliases));
+  return out;
 }
 
-/** Every distinct kernel source of a launch list, in first-use order. */
+/**
+ * Batched launches (perf lowering): launches of one kernel text (same sizes and
+ * operand views) with no data path between them run as one dispatch of its
+ * batched form (codegen.js batchedKernel). Walking the list in order, a
+ * batchable launch opens a batch, and every later launch of the same kernel
+ * whose operands are all written by launches already placed joins it (up to
+ * MAX_BATCH); the members are placed together where the first one was. A
+ * member is only moved earlier, past launches it does not read, and writes its
+ * own node's buffer, so every launch still reads exactly the values it read in
+ * graph order. Returns { launches (the new order), batches: [{ start, count,
+ * kernel }] } with each batch's members at launches[start .. start + count).
+ */
+function batchPlan(launches, aliases) {
+  const owner = (id) => (aliases.has(id) ? aliases.get(id) : id);
+  const n = launches.length;
+  const writer = new Map();
+  launches.forEach((l, i) => writer.set(owner(l.node), i));
+  const one = (l) => (l.kernels.length === 1 && !l.workspace && cg.batchable(l.kernels[0]) ? l.kernels[0].name : null);
+  const placed = new Uint8Array(n);
+  const ready = (l) => l.inputs.every((id) => { const w = writer.get(owner(id)); return w === undefined || placed[w] === 1; });
+  const order = [], batches = [];
+  for (let i = 0; i < n; i++) {
+    if (placed[i]) continue;
+    const group = [i];
+    const name = one(launches[i]);
+    if (name) {
+      for (let j = i + 1; j < n && group.length < cg.MAX_BATCH; j++) {
+        if (!placed[j] && one(launches[j]) === name && ready(launches[j])) group.push(j);
+      }
+    }
+    if (group.length > 1) batches.push({ start: order.length, count: group.length, kernel: cg.batchedKernel(launches[i].kernels[0], group.length) });
+    for (const j of group) { placed[j] = 1; order.push(launches[j]); }
+  }
+  return { launches: order, batches };
+}
+
+/** Every distinct kernel source of a launch list (its batched kernels included), in first-use order. */
 function kernelSources(lowered) {
   const seen = new Map();
   for (const l of lowered.launches) for (const k of l.kernels) if (!seen.has(k.name)) seen.set(k.name, k.source);
+  for (const b of lowered.batches || []) if (!seen.has(b.kernel.name)) seen.set(b.kernel.name, b.kernel.source);
   return seen;
 }
 
-module.exports = { lowerMI355X, kernelSources, lowerNode, oneOpBody, algorithmicBytes };
+module.exports = { lowerMI355X, kernelSources, batchPlan, lowerNode, oneOpBody, algorithmicBytes };

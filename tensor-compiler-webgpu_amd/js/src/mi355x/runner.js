@@ -34,6 +34,7 @@ const { scheduleLaunches } = require('./schedule');
 const CANARY_BITS = 0xdeadbeef;
 const CANARY_PAD = 256;           // words past the end of every buffer
 const ARG_BYTES = MAX_IN * 8 + 8 + 8 + MAX_P * 4;
+const PTR_BYTES = MAX_IN * 8 + 8 + 8;     // one member of a batched launch's block
 
 const PRELUDE = '#include "tcmi_device.h"\n';
 
@@ -123,6 +124,18 @@ function packArgs(view, offset, inPtrs, outPtr, wsPtr, params) {
   for (let k = 0; k < MAX_P; k++) view.setUint32(offset + MAX_IN * 8 + 16 + 4 * k, k < params.length ? params[k] : 0, true);
 }
 
+/** Pack one member of a batched launch's argument block (TcmiPtrs in tcmi_device.h). */
+function packPtrs(view, offset, inPtrs, outPtr, wsPtr) {
+  const put64 = (at, v) => {
+    view.setUint32(at, v % 4294967296, true);
+    view.setUint32(at + 4, Math.floor(v / 4294967296), true);
+  };
+  if (inPtrs.length > MAX_IN) throw new Error(`launch has ${inPtrs.length} operands (max ${MAX_IN})`);
+  for (let k = 0; k < MAX_IN; k++) put64(offset + 8 * k, k < inPtrs.length ? inPtrs[k] : 0);
+  put64(offset + MAX_IN * 8, outPtr);
+  put64(offset + MAX_IN * 8 + 8, wsPtr);
+}
+
 /**
  * The perf lowering's buffer sharing: alias (node -> node whose buffer it uses) and
  * folded (no buffer: folded into its consumers, or dead).
@@ -203,12 +216,30 @@ class HipRunner {
 
   alloc(bytes) { return this.a.malloc(Math.max(16, Math.ceil(bytes / 16) * 16)); }
 
-  /** Launch every kernel of `lowered` with node buffers `bufs` (node id -> device address). */
+  /**
+   * Launch every kernel of `lowered` with node buffers `bufs` (node id -> device address),
+   * each batch of the perf lowering as one launch of its batched kernel.
+   */
   launchAll(lowered, fns, bufs, outOf, ws) {
     const argBuf = new ArrayBuffer(ARG_BYTES);
     const view = new DataView(argBuf);
     const bytes = new Uint8Array(argBuf);
-    for (const l of lowered.launches) {
+    const batchAt = new Map((lowered.batches || []).map((b) => [b.start, b]));
+    const L = lowered.launches;
+    for (let i = 0; i < L.length;) {
+      const b = batchAt.get(i);
+      if (b) {
+        const block = new ArrayBuffer(b.count * PTR_BYTES);
+        const bv = new DataView(block);
+        for (let m = 0; m < b.count; m++) {
+          const l = L[i + m];
+          packPtrs(bv, m * PTR_BYTES, l.inputs.map((id) => bufs[id]), outOf ? outOf(l) : bufs[l.node], ws);
+        }
+        this.a.launch(fns.get(b.kernel.name), b.kernel.grid, b.kernel.block, b.kernel.lds, new Uint8Array(block));
+        i += b.count;
+        continue;
+      }
+      const l = L[i++];
       const out = outOf ? outOf(l) : bufs[l.node];
       packArgs(view, 0, l.inputs.map((id) => bufs[id]), out, ws, l.params);
       for (const k of l.kernels) this.a.launch(fns.get(k.name), k.grid, k.block, k.lds, bytes);
@@ -360,26 +391,47 @@ class Program {
       if (node.op === 'const' && !buffers) a.h2d(this.bufs[node.id], 0, constData(node).subarray(0, this.n[node.id]));
     }
     const launches = lowered.launches.filter((l) => !only || only(l));
-    let count = 0;
-    for (const l of launches) count += l.kernels.length;
+    // Dispatch units: a batch's members go as one launch of its batched kernel
+    // (whole launch lists on one stream; a filtered or multi-stream program
+    // launches every member by itself, in the same order).
+    const batchAt = new Map(!only && !(streams > 1) ? (lowered.batches || []).map((b) => [b.start, b]) : []);
+    const units = [];
+    for (let i = 0; i < launches.length;) {
+      const b = batchAt.get(i);
+      const members = launches.slice(i, i + (b ? b.count : 1));
+      units.push({ kernels: b ? [b.kernel] : members[0].kernels, members });
+      i += members.length;
+    }
+    let count = 0, argBytes = 0;
+    for (const u of units) for (const k of u.kernels) { count++; argBytes += u.members.length > 1 ? u.members.length * PTR_BYTES : ARG_BYTES; }
     this.count = count;
     this.fns = new Float64Array(count);
     this.dims = new Uint32Array(count * 7);
-    this.args = new Uint8Array(count * ARG_BYTES);
+    this.args = new Uint8Array(argBytes);
     this.offsets = new Uint32Array(count + 1);
     const view = new DataView(this.args.buffer);
-    let i = 0;
-    for (const l of launches) {
-      for (const k of l.kernels) {
-        packArgs(view, i * ARG_BYTES, l.inputs.map((id) => this.bufs[id]), this.bufs[l.node], this.ws, l.params);
+    let i = 0, at = 0;
+    for (const u of units) {
+      for (const k of u.kernels) {
+        this.offsets[i] = at;
+        if (u.members.length > 1) {
+          for (const l of u.members) {
+            packPtrs(view, at, l.inputs.map((id) => this.bufs[id]), this.bufs[l.node], this.ws);
+            at += PTR_BYTES;
+          }
+        } else {
+          const l = u.members[0];
+          packArgs(view, at, l.inputs.map((id) => this.bufs[id]), this.bufs[l.node], this.ws, l.params);
+          at += ARG_BYTES;
+        }
         this.fns[i] = fns.get(k.name);
         this.dims.set([k.grid[0], k.grid[1], k.grid[2], k.block[0], k.block[1], k.block[2], k.lds], i * 7);
-        this.offsets[i] = i * ARG_BYTES;
         i++;
       }
     }
-    this.offsets[count] = count * ARG_BYTES;
+    this.offsets[count] = at;
     this.launches = launches;
+    this.dispatches = count;
     this.graphHandle = 0;
     this.dag = null;
     if (streams && streams > 1) {
@@ -424,15 +476,16 @@ class Program {
       return;
     }
     if (!this.repeated || this.repeated.k !== k) {
-      const n = this.count;
+      const n = this.count, bytes = this.args.length;
       const fns = new Float64Array(n * k), dims = new Uint32Array(n * k * 7);
-      const args = new Uint8Array(n * k * ARG_BYTES), offsets = new Uint32Array(n * k + 1);
+      const args = new Uint8Array(bytes * k), offsets = new Uint32Array(n * k + 1);
       for (let r = 0; r < k; r++) {
         fns.set(this.fns, r * n);
         dims.set(this.dims, r * n * 7);
-        args.set(this.args, r * n * ARG_BYTES);
+        args.set(this.args, r * bytes);
+        for (let i = 0; i < n; i++) offsets[r * n + i] = r * bytes + this.offsets[i];
       }
-      for (let i = 0; i <= n * k; i++) offsets[i] = i * ARG_BYTES;
+      offsets[n * k] = k * bytes;
       this.repeated = { k, fns, dims, args, offsets };
     }
     const r = this.repeated;
@@ -466,4 +519,4 @@ class Program {
   }
 }
 
-module.exports = { HipRunner, Program, packArgs, translationUnit, precompile, CANARY_BITS, CANARY_PAD, ARG_BYTES, PRELUDE };
+module.exports = { HipRunner, Program, packArgs, packPtrs, translationUnit, precompile, CANARY_BITS, CANARY_PAD, ARG_BYTES, PTR_BYTES, PRELUDE };

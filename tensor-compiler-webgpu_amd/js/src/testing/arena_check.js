@@ -4,7 +4,8 @@
 // (and untagging whatever it overlapped), and require every launch's operands,
 // and at the end every pinned buffer, to still hold their own node intact. A plan
 // that lets a buffer be overwritten while a later launch (or the caller) still
-// needs it fails here, whatever the live-range arithmetic claimed.
+// needs it fails here, whatever the live-range arithmetic claimed. The members
+// of a batched launch read and write as one step.
 
 function simulateArena(graph, lowered, plan) {
   const owner = plan.owner;
@@ -27,16 +28,23 @@ function simulateArena(graph, lowered, plan) {
     return extents.some((e) => e.tag === id && e.lo === b.offset && e.hi === b.offset + b.bytes);
   };
   for (const b of plan.buffers) if (b.pinned) write(b.id);   // the host's uploads
-  for (let i = 0; i < lowered.launches.length; i++) {
-    const l = lowered.launches[i];
-    for (const id of l.inputs) {
-      if (!holds(owner(id))) return { ok: false, launch: i, node: l.node, operand: id };
+  // The members of a batched launch run concurrently: all of them read, then all write.
+  const unit = new Map((lowered.batches || []).map((b) => [b.start, b.count]));
+  for (let i = 0; i < lowered.launches.length;) {
+    const members = lowered.launches.slice(i, i + (unit.get(i) || 1));
+    for (const l of members) {
+      for (const id of l.inputs) {
+        if (!holds(owner(id))) return { ok: false, launch: i, node: l.node, operand: id };
+      }
     }
-    write(owner(l.node));
-    // No kernel here runs in place: its output must not land on an operand it reads.
-    for (const id of l.inputs) {
-      if (owner(id) !== owner(l.node) && !holds(owner(id))) return { ok: false, launch: i, node: l.node, overwrote: id };
+    for (const l of members) write(owner(l.node));
+    // No kernel here runs in place: no output of the unit may land on an operand it reads.
+    for (const l of members) {
+      for (const id of l.inputs) {
+        if (!members.some((m) => owner(m.node) === owner(id)) && !holds(owner(id))) return { ok: false, launch: i, node: l.node, overwrote: id };
+      }
     }
+    i += members.length;
   }
   for (const b of plan.buffers) if (b.pinned && !holds(b.id)) return { ok: false, launch: 'end', operand: b.id };
   return { ok: true };

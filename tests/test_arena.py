@@ -32,3 +32,16 @@ def test_a_planted_overlap_is_caught(tool):
     planted = [r for r in res if "planted" in r]
     assert len(planted) > 50
     assert all(not r["planted"]["check"]["ok"] for r in planted), [r["name"] for r in planted if r["planted"]["check"]["ok"]]
+
+
+def test_batched_launches_share_one_position(tool):
+    """The members of a batched launch run concurrently, so the arena places them at one
+    position. A plan that takes them one after another lets a later member's output reuse
+    the bytes of an earlier member's last operand: the simulation, which reads and writes
+    a batch as one step, refuses that plan for config 5's step and some corpus programs."""
+    res = tool("arena-check", {"models": MODELS[:1], "corpus": {"from": 1, "to": 50}, "plant": True})
+    blind = [r for r in res if "batchBlind" in r]
+    assert any(r["name"] == "transformer-64" for r in blind)
+    assert all(r["check"]["ok"] for r in blind)
+    caught = [r["name"] for r in blind if not r["batchBlind"]["ok"]]
+    assert "transformer-64" in caught and len(caught) >= 3, caught

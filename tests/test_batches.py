@@ -1,0 +1,32 @@
+"""Batched launches of the perf lowering (js/src/mi355x/lower.js batchPlan), checked on the
+CPU by js/src/testing/batch_check.js from the launch records alone: the batched list holds
+the plain list's launches, every launch reads only buffers written before it, a batch's
+members are launches of one kernel text with no data path between them, the batched grid
+has one z-slice per member, and launches that share the workspace keep their order. Two
+planted mistakes (a batch whose second member reads the first's output; a launch moved in
+front of its operand's writer) must be refused. The GPU side — batched runs bit for bit the
+plain ones — is in test_gpu_train.py (config 5's step) and test_gpu_fuzz.py (corpus programs)."""
+
+MODELS = [{"model": "transformer", "B": 64}, {"model": "transformer", "B": 1}, {"model": "mlp"},
+          {"model": "transformer-ref"}]
+
+
+def test_batched_launch_lists_are_valid_orders(tool):
+    res = tool("batch-check", {"models": MODELS, "corpus": {"from": 1, "to": 300}})
+    assert len(res) == len(MODELS) + 600
+    bad = [r for r in res if not r["check"]["ok"]]
+    assert not bad, bad[:3]
+    c5 = next(r for r in res if r["name"] == "transformer-64")
+    # Config 5's step: the q/k/v projections and their head transposes per layer, the
+    # score-gradient matmul pairs and the per-tensor parameter updates batch.
+    assert c5["check"]["batches"] >= 12 and c5["check"]["saved"] >= 40, c5
+    assert sum(1 for r in res if r["check"]["batches"]) > 100
+
+
+def test_planted_batch_mistakes_are_caught(tool):
+    res = tool("batch-check", {"models": MODELS[:1], "corpus": {"from": 1, "to": 100}, "plant": True})
+    dep = [r for r in res if "dependent" in r]
+    early = [r for r in res if "early" in r]
+    assert len(dep) >= 10 and len(early) >= 100
+    assert all(not r["dependent"]["ok"] for r in dep)
+    assert all(not r["early"]["ok"] for r in early)

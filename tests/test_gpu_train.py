@@ -98,8 +98,6 @@ MULTI_STREAM_CAPTURE_OFF = "multi-stream capture is switched off: capturing conf
 @pytest.mark.parametrize("graph,arena,streams", [(False, False, 1), (True, False, 1), (False, True, 1), (False, False, 3),
                                                  (True, False, 3)])
 def test_c1_trainer_consistency_and_learning(tool, graph, arena, streams):
-    if graph and streams > 1:
-        pytest.skip(MULTI_STREAM_CAPTURE_OFF)
     """20 fused-trainer steps on one batch: each equals the checked path (runner.run of the
     plain lowering, one launch per node, with the new values fed back by the host) bit for
     bit — the trainer runs the perf lowering, whose matmuls read transposed operands in
@@ -107,8 +105,10 @@ def test_c1_trainer_consistency_and_learning(tool, graph, arena, streams):
     captured HIP graph (two graphs, the parameters' buffers exchanging roles), and every
     replay is checked against the eager path, with the host's synchronisation between.
     With `arena`, the step's intermediate buffers share one allocation by live range; with
-    `streams`, independent launches run on several streams (and the graph captures them
-    as parallel branches)."""
+    `streams`, independent launches run on several streams (eagerly: a program issued
+    over several streams is not captured)."""
+    if graph and streams > 1:
+        pytest.skip(MULTI_STREAM_CAPTURE_OFF)
     r = tool("gpu-train", {"model": "mlp", "steps": 20, "consistency": True, "consistencySteps": 20, "sameBatch": True,
                            "graph": graph, "arena": arena, "streams": streams})
     assert r["identical"] is True
@@ -123,19 +123,24 @@ def test_c1_trainer_consistency_and_learning(tool, graph, arena, streams):
 @pytest.mark.parametrize("graph,arena,streams", [(False, False, 1), (True, False, 1), (False, True, 1), (True, True, 1),
                                                  (False, False, 3), (True, False, 3)])
 def test_c5_full_size_trainer(tool, graph, arena, streams):
+    """Config 5 at full size (B 64): the fused trainer's first 3 steps (perf lowering:
+    transposes read in place by their matmuls, reshapes sharing buffers, identical
+    independent launches batched into one dispatch) equal the checked path (plain
+    lowering) bit for bit, and the initial loss is near ln(96) (small initial weights,
+    uniform tokens). With `arena`, every buffer but the parameters, batch, loss and logits
+    is placed by live range in one allocation (2.4 GB of node buffers in 0.9 GB), the
+    members of a batch at one position, and the steps are still bit for bit the checked
+    path's; so they are with the step's independent launches on three streams (each
+    batch member then launched by itself)."""
     if graph and streams > 1:
         pytest.skip(MULTI_STREAM_CAPTURE_OFF)
-    """Config 5 at full size (B 64): the fused trainer's first 3 steps (perf lowering:
-    transposes read in place by their matmuls, reshapes sharing buffers) equal the checked
-    path (plain lowering) bit for bit, and the initial loss is near ln(96) (small initial
-    weights, uniform tokens). With `arena`, every buffer but the parameters, batch, loss
-    and logits is placed by live range in one allocation (2.4 GB of node buffers in
-    0.9 GB), and the steps are still bit for bit the checked path's; so they are with the
-    step's independent launches on three streams."""
     r = tool("gpu-train", {"model": "transformer", "B": 64, "steps": 3, "consistency": True, "consistencySteps": 3,
                            "graph": graph, "arena": arena, "streams": streams}, timeout=600)
     assert r["identical"] is True
     assert r["folded"] > 0 and r["aliases"] > 0 and r["launches"] < r["checkedLaunches"]
     assert abs(r["losses"][0] - np.log(96)) < 0.1, r["losses"]
+    assert r["batches"] >= 12, r["batches"]
+    saved = r["batchedLaunches"] - r["batches"]
+    assert r["dispatches"] == (r["kernels"] - saved if streams == 1 else r["kernels"]), r
     if arena:
         assert r["arena"]["bytes"] < 0.5 * r["arena"]["unshared"], r["arena"]
