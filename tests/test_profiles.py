@@ -27,7 +27,7 @@ def test_profiles_name_their_commands_and_carry_traffic():
         block = _json_block(text)
         traffic = block["traffic_bytes_per_launch"]
         assert traffic and all(isinstance(v, int) and v > 0 for v in traffic.values()), md.name
-        assert abs(block["factors"]["FETCH_SIZE"] - 2.0) < 1e-3 and block["factors"]["WRITE_SIZE"] == 1.0
+        assert abs(block["factors"]["FETCH_SIZE"] - 2.0) < 1e-3 and abs(block["factors"]["WRITE_SIZE"] - 1.0) < 1e-3
 
 
 def test_bench_reads_the_traffic_of_a_profiled_kernel():
