@@ -43,9 +43,10 @@ struct TcmiArgs {
 };
 
 // A batched launch of one kernel over N independent launches of it (same
-// sizes, different buffers): member z's pointers, read by the workgroups with
-// blockIdx.z == z. The kernel body is the member kernel's, with A bound to
-// B.m[blockIdx.z]; only kernels whose own grid has one z-slice are batched.
+// sizes, different buffers): the member kernel's grid repeated N times along z,
+// its body run with A bound to member blockIdx.z / Z (Z: the member grid's z
+// extent) and blockIdx.z % Z in place of its own z index. Kernel texts read z
+// only in their own text, never in these headers, so the rewrite is complete.
 struct TcmiPtrs {
   const float* in[TCMI_MAX_IN];
   float* out;

@@ -65,8 +65,9 @@ struct DenseView {
 };
 
 // Sizes are compile-time constants of the generated kernel (batch, M, K, N, and
-// for SPLIT the number of K chunks and their length, a multiple of 16). SPLIT:
-// blockIdx.z enumerates (batch, chunk) pairs, and each workgroup stores its raw
+// for SPLIT the number of K chunks and their length, a multiple of 16). The
+// workgroup's z index `zid` enumerates batches, or for SPLIT (batch, chunk)
+// pairs, and each SPLIT workgroup stores its raw
 // partial tile to the workspace at ((chunk·batch + b)·M + row)·N + col; a
 // second kernel (gemm_splitk_reduce) sums the chunks in order and applies the
 // epilogue. MODE_C needs C % 4 == 0 and MODE_R needs R % 4 == 0 (R, C: the
@@ -77,7 +78,7 @@ template <int TM, int TN, int BK, int PF, int AMODE, int BMODE, bool SPLIT, clas
 __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict__ a_ptr,
                                          const float* __restrict__ b_ptr, const uint32_t batch, const uint32_t M,
                                          const uint32_t K, const uint32_t N, const uint32_t chunks,
-                                         const uint32_t chunkK) {
+                                         const uint32_t chunkK, const uint32_t zid) {
   // 2 x WN wavefronts; each owns (TM·16) x (TN·16) of the BM x BN tile.
   constexpr int THREADS = 64 * 2 * WN;
   constexpr int BM = 2 * TM * 16;
@@ -91,9 +92,10 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
   __shared__ __attribute__((aligned(16))) float As[2][(A_KMAJOR ? BK : BM) * AS];
   __shared__ __attribute__((aligned(16))) float Bs[2][(B_NMAJOR ? BN : BK) * BS];
 
-  const uint32_t kz = SPLIT ? blockIdx.z % chunks : 0u;
-  // One batch: z is 0 here, or the member index of a batched launch (TcmiBatch).
-  const uint32_t bz = SPLIT ? blockIdx.z / chunks : (batch > 1u ? blockIdx.z : 0u);
+  // zid: the workgroup's z index within this launch (blockIdx.z, or its part
+  // below the member index in a batched launch).
+  const uint32_t kz = SPLIT ? zid % chunks : 0u;
+  const uint32_t bz = SPLIT ? zid / chunks : zid;
   const uint32_t kbeg = SPLIT ? kz * chunkK : 0u;
   const uint32_t kend = SPLIT ? min(K, kbeg + chunkK) : K;
   const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
@@ -376,8 +378,8 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
 
 // The second half of a split-K matmul: out[i] = Epi(A, i, Σ_chunk ws[chunk·total + i]),
 // the chunks summed in order; `total` = batch·M·N. Four outputs per thread when N % 4 == 0.
-template <bool VEC, class Epi>
-__device__ __forceinline__ void gemm_splitk_reduce(const TcmiArgs& A, uint32_t total, uint32_t chunks) {
+template <bool VEC, class Epi, class Args>
+__device__ __forceinline__ void gemm_splitk_reduce(const Args& A, uint32_t total, uint32_t chunks) {
   const Epi epi;
   const uint32_t stride = gridDim.x * blockDim.x;
   if (VEC) {

@@ -219,7 +219,7 @@ function launchRecords(lowered) {
     kernels: l.kernels.map((k) => k.name), bytes: l.bytes, flops: l.flops || 0 }));
   for (const b of lowered.batches || []) {
     const ms = lowered.launches.slice(b.start, b.start + b.count);
-    recs.push({ node: ms[0].node, kind: `batched ${ms[0].kind} x${b.count}`, pattern: ms[0].pattern || null, kernels: [b.kernel.name],
+    recs.push({ node: ms[0].node, kind: `batched ${ms[0].kind} x${b.count}`, pattern: ms[0].pattern || null, kernels: b.kernels.map((k) => k.name),
       bytes: ms.reduce((q, l) => q + l.bytes, 0), flops: ms.reduce((q, l) => q + (l.flops || 0), 0), members: ms.map((l) => l.node) });
   }
   return recs;

@@ -687,7 +687,8 @@ async function gpuTrain(req) {
   return { losses, identical, params, launches: fs.lowered.launches.length, checkedLaunches: fs.checked.launches.length,
     folded: fs.lowered.folded.length, aliases: fs.lowered.aliases.length, unfusedNodes: m.step.graph.nodes.length, info: m.info,
     arena: plan ? { bytes: plan.size, unshared: plan.unshared, buffers: plan.buffers.length } : null,
-    batches: (fs.lowered.batches || []).length, batchedLaunches: (fs.lowered.batches || []).reduce((c, b) => c + b.count, 0), dispatches,
+    batches: (fs.lowered.batches || []).length, dispatches,
+    batchSaves: (fs.lowered.batches || []).reduce((c, b) => c + (b.count - 1) * b.kernels.length, 0),
     kernels: fs.lowered.launches.reduce((c, l) => c + l.kernels.length, 0) };
 }
 
@@ -929,7 +930,7 @@ async function main() {
         const batched = lowerMI355X(graph, { perf: true, keep });
         const res = { name, launches: batched.launches.length, check: checkBatches(plain, batched) };
         if (req.plant) {
-          for (const kind of ['dependent', 'early']) {
+          for (const kind of ['dependent', 'early', 'grid']) {
             const bad = plantBatchMistake(batched, kind);
             if (bad) res[kind] = checkBatches(plain, bad);
           }

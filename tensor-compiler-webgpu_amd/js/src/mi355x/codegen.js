@@ -789,7 +789,7 @@ ${indent(lines, '    ')}
   const variant = tl.wn === 2 && !tl.prio ? '' : `, ${tl.wn}, ${tl.prio}`;
   const main = `extern "C" __global__ void __launch_bounds__(${threads}) __KERNEL__(const TcmiArgs A) {
   tcmi::gemm_f32<${T}, ${T}, ${tl.bk}, ${tl.pf}, ${av.mode}, ${bv.mode}, ${split}, __KERNEL___av, __KERNEL___bv, __KERNEL___epi${variant}>(A, A.in[${ia}], A.in[${ib}],
-      ${batch}u, ${M}u, ${K}u, ${N}u, ${tl.chunks}u, ${tl.chunkK}u);
+      ${batch}u, ${M}u, ${K}u, ${N}u, ${tl.chunks}u, ${tl.chunkK}u, blockIdx.z);
 }
 `;
   const text = `#include "tcmi_gemm.h"\n${av.text}${bv.text}${epi}${main}`;
@@ -1007,33 +1007,41 @@ ${indent(pre.concat([pLoop]), '  ')}
 // Members of one batched launch at most: its argument block (TcmiBatch, 80 bytes
 // a member) stays well inside the 4 KiB a launch's arguments may take.
 const MAX_BATCH = 32;
-// Kernel families whose text reads its launch only through A.in / A.out / A.ws
-// and blockIdx.x / blockIdx.y (a one-batch matmul pins its batch index to 0).
-const BATCHABLE = /^tcmi_(ew|row|mm)_[0-9a-f]+$/;
+// Kernel families generated here: each reads its launch only through A.in /
+// A.out / A.ws, and its z index only in its own text (the headers never read
+// blockIdx.z or gridDim.z). `_red`: a split-K matmul's second kernel.
+const BATCHABLE = /^(tcmi_(ew|row|mm|mmred|colred|colfin|attn)_[0-9a-f]+)(_red)?$/;
+const MAX_GRID_Z = 65535;
 
-/** Whether kernel `k` (a launch's only kernel) may run as a member of a batched launch. */
-function batchable(k) {
-  return BATCHABLE.test(k.name) && k.grid[2] === 1 && !k.needsPad;
+/** Whether kernel `k` may run as a member of a batched launch of `count` members. */
+function batchable(k, count) {
+  return BATCHABLE.test(k.name) && !k.needsPad && k.grid[2] * (count || 2) <= MAX_GRID_Z;
 }
 
 /**
- * One launch of kernel `k` over `count` independent sets of buffers: the same
- * body with A bound to member blockIdx.z of a TcmiBatch argument block, and the
- * grid's z extent `count`. Identical launches (same text: same sizes, same
- * operand views) of independent nodes become one dispatch, so a step of many
- * small launches (a parameter update per tensor, the three projections of an
- * attention layer) fills the chip with one launch's workgroups instead of
- * paying a launch's ramp and drain each.
+ * One launch of kernel `k` over `count` independent sets of buffers: the member
+ * grid repeated `count` times along z, the body run with A bound to member
+ * blockIdx.z / Z of a TcmiBatch argument block (Z: the member grid's z extent)
+ * and blockIdx.z % Z as its own z index. Identical launches (same text: same
+ * sizes, same operand views) of independent nodes become one dispatch, so a step
+ * of many small launches (a parameter update per tensor, the three projections
+ * of an attention layer and their weight gradients) fills the chip with one
+ * launch's workgroups instead of paying a launch's ramp and drain each.
  */
 function batchedKernel(k, count) {
-  if (!batchable(k)) throw new Error(`kernel ${k.name} cannot be batched`);
+  if (!batchable(k, count)) throw new Error(`kernel ${k.name} cannot be batched ${count} times`);
   if (!(Number.isInteger(count) && count >= 2 && count <= MAX_BATCH)) throw new Error(`batch of ${count} launches (2..${MAX_BATCH})`);
+  const [, base, , suffix] = k.name.match(BATCHABLE);
   const sig = `${k.name}(const TcmiArgs A) {`;
   if (k.source.split(sig).length !== 2) throw new Error(`kernel ${k.name}: no single entry point to batch`);
-  const text = k.source.replace(sig, `__KERNEL__(const TcmiBatch<${count}> B) {\n  const TcmiPtrs& A = B.m[blockIdx.z];`)
-    .split(k.name).join('__KERNEL__');
+  if (/gridDim\.z/.test(k.source)) throw new Error(`kernel ${k.name} reads gridDim.z`);
+  const Z = k.grid[2];
+  const entry = `__KERNEL__${suffix || ''}(const TcmiBatch<${count}> B) {\n  const TcmiPtrs& A = B.m[blockIdx.z / ${Z}u];`;
+  const text = k.source.split(sig).map((part) => part.split('blockIdx.z').join(`(blockIdx.z % ${Z}u)`)).join('\u0000')
+    .replace('\u0000', entry).split(base).join('__KERNEL__');
   const b = kernelText(`b${k.name.split('_')[1]}`, text);
-  return { name: b.name, source: b.source, grid: [k.grid[0], k.grid[1], count], block: k.block.slice(), lds: k.lds, members: count };
+  return { name: b.name + (suffix || ''), source: b.source, grid: [k.grid[0], k.grid[1], Z * count], block: k.block.slice(), lds: k.lds,
+    members: count };
 }
 
 module.exports = { elementwiseKernel, rowwiseKernel, colreduceKernels, gemmKernel, gemmTiling, attentionKernel, classifyGather, gatherStrides,

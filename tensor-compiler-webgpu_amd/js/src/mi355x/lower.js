@@ -32,9 +32,10 @@
 //     gather) launches nothing: each consumer's kernel reads the broadcast's
 //     source through the broadcast's index map instead of a materialised copy.
 //   - launches of one kernel text with no data path between them (the three
-//     projections of an attention layer, the per-tensor parameter updates) are
-//     placed together and listed in `batches`: the runner issues each batch as
-//     one dispatch of the kernel's batched form (batchPlan below).
+//     projections of an attention layer and their weight gradients, the
+//     per-tensor parameter updates) are placed together and listed in
+//     `batches`: the runner issues each batch as one dispatch per kernel of the
+//     kernels' batched forms (batchPlan below).
 // Nodes in `keep` are never folded, so their values stay readable.
 
 const { Graph } = require('../ir/graph');
@@ -267,7 +268,7 @@ function perfPlan(graph, keep) {
  * perf lowering's launches one dispatch each, in graph order.
  * Returns { launches, workspace, aliases, folded, dead, batches } (workspace: bytes of
  * scratch the largest launch needs; aliases: [[node, source]]; folded and dead: node
- * ids with neither a launch nor a buffer; batches, perf only: [{ start, count, kernel }]).
+ * ids with neither a launch nor a buffer; batches, perf only: [{ start, count, kernels, wsStride }]).
  */
 function lowerMI355X(graph, options) {
   const opts = options || {};
@@ -310,7 +311,12 @@ function lowerMI355X(graph, options) {
     }
   }
   const out = { launches, workspace, aliases: Array.from(plan.aliases.entries()), folded: Array.from(plan.folded), dead: Array.from(plan.dead) };
-  if (opts.perf && opts.batch !== false) Object.assign(out, batchPlan(launches, plan.aliases));
+  if (opts.perf && opts.batch !== false) {
+    const b = batchPlan(launches, plan.aliases);
+    out.launches = b.launches;
+    out.batches = b.batches;
+    for (const x of b.batches) out.workspace = Math.max(out.workspace, x.count * x.wsStride);
+  }
   return out;
 }
 
@@ -323,15 +329,21 @@ function lowerMI355X(graph, options) {
  * MAX_BATCH); the members are placed together where the first one was. A
  * member is only moved earlier, past launches it does not read, and writes its
  * own node's buffer, so every launch still reads exactly the values it read in
- * graph order. Returns { launches (the new order), batches: [{ start, count,
- * kernel }] } with each batch's members at launches[start .. start + count).
+ * graph order. A batch runs each of its launches' kernels over all members in
+ * turn (all first kernels, then all second kernels), member k with the
+ * workspace slice [k·wsStride, (k + 1)·wsStride). Returns { launches (the new
+ * order), batches: [{ start, count, kernels, wsStride }] } with each batch's
+ * members at launches[start .. start + count).
  */
 function batchPlan(launches, aliases) {
   const owner = (id) => (aliases.has(id) ? aliases.get(id) : id);
   const n = launches.length;
   const writer = new Map();
   launches.forEach((l, i) => writer.set(owner(l.node), i));
-  const one = (l) => (l.kernels.length === 1 && !l.workspace && cg.batchable(l.kernels[0]) ? l.kernels[0].name : null);
+  // A launch's kernels as run: a kernel's text does not always fix its grid (a
+  // column sum's outer extent is its grid's z extent only).
+  const one = (l) => (l.kernels.every((k) => cg.batchable(k))
+    ? l.kernels.map((k) => `${k.name}@${k.grid.join(',')}/${k.block.join(',')}/${k.lds}`).join(' ') : null);
   const placed = new Uint8Array(n);
   const ready = (l) => l.inputs.every((id) => { const w = writer.get(owner(id)); return w === undefined || placed[w] === 1; });
   const order = [], batches = [];
@@ -343,8 +355,13 @@ function batchPlan(launches, aliases) {
       for (let j = i + 1; j < n && group.length < cg.MAX_BATCH; j++) {
         if (!placed[j] && one(launches[j]) === name && ready(launches[j])) group.push(j);
       }
+      while (group.length > 1 && !launches[i].kernels.every((k) => cg.batchable(k, group.length))) group.pop();
     }
-    if (group.length > 1) batches.push({ start: order.length, count: group.length, kernel: cg.batchedKernel(launches[i].kernels[0], group.length) });
+    if (group.length > 1) {
+      const l = launches[i];
+      batches.push({ start: order.length, count: group.length, kernels: l.kernels.map((k) => cg.batchedKernel(k, group.length)),
+        wsStride: l.workspace ? Math.ceil(l.workspace / 256) * 256 : 0 });
+    }
     for (const j of group) { placed[j] = 1; order.push(launches[j]); }
   }
   return { launches: order, batches };
@@ -354,7 +371,7 @@ function batchPlan(launches, aliases) {
 function kernelSources(lowered) {
   const seen = new Map();
   for (const l of lowered.launches) for (const k of l.kernels) if (!seen.has(k.name)) seen.set(k.name, k.source);
-  for (const b of lowered.batches || []) if (!seen.has(b.kernel.name)) seen.set(b.kernel.name, b.kernel.source);
+  for (const b of lowered.batches || []) for (const k of b.kernels) if (!seen.has(k.name)) seen.set(k.name, k.source);
   return seen;
 }
 

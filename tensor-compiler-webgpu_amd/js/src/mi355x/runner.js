@@ -233,9 +233,9 @@ class HipRunner {
         const bv = new DataView(block);
         for (let m = 0; m < b.count; m++) {
           const l = L[i + m];
-          packPtrs(bv, m * PTR_BYTES, l.inputs.map((id) => bufs[id]), outOf ? outOf(l) : bufs[l.node], ws);
+          packPtrs(bv, m * PTR_BYTES, l.inputs.map((id) => bufs[id]), outOf ? outOf(l) : bufs[l.node], ws + m * b.wsStride);
         }
-        this.a.launch(fns.get(b.kernel.name), b.kernel.grid, b.kernel.block, b.kernel.lds, new Uint8Array(block));
+        for (const k of b.kernels) this.a.launch(fns.get(k.name), k.grid, k.block, k.lds, new Uint8Array(block));
         i += b.count;
         continue;
       }
@@ -399,7 +399,7 @@ class Program {
     for (let i = 0; i < launches.length;) {
       const b = batchAt.get(i);
       const members = launches.slice(i, i + (b ? b.count : 1));
-      units.push({ kernels: b ? [b.kernel] : members[0].kernels, members });
+      units.push({ kernels: b ? b.kernels : members[0].kernels, members, wsStride: b ? b.wsStride : 0 });
       i += members.length;
     }
     let count = 0, argBytes = 0;
@@ -415,10 +415,10 @@ class Program {
       for (const k of u.kernels) {
         this.offsets[i] = at;
         if (u.members.length > 1) {
-          for (const l of u.members) {
-            packPtrs(view, at, l.inputs.map((id) => this.bufs[id]), this.bufs[l.node], this.ws);
+          u.members.forEach((l, m) => {
+            packPtrs(view, at, l.inputs.map((id) => this.bufs[id]), this.bufs[l.node], this.ws + m * u.wsStride);
             at += PTR_BYTES;
-          }
+          });
         } else {
           const l = u.members[0];
           packArgs(view, at, l.inputs.map((id) => this.bufs[id]), this.bufs[l.node], this.ws, l.params);

@@ -2,10 +2,12 @@
 // An independent check of the perf lowering's batched launches (lower.js
 // batchPlan): the batched launch list must hold the same launches as the plain
 // order, every launch must read only buffers already written (or written by no
-// launch), the members of a batch must be launches of one single-kernel text
-// with no data path between them, and a batched kernel's grid must carry one
-// z-slice per member. Checked from the launch records alone, not from the
-// planner's own bookkeeping.
+// launch), the members of a batch must be launches of the same kernel texts
+// over the same grids (a column sum's text leaves its outer extent to the
+// grid) with no data path between them, each batched kernel's grid must repeat the
+// member kernel's grid once per member along z, and the members' workspace
+// slices must be disjoint and inside the workspace. Checked from the launch
+// records alone, not from the planner's own bookkeeping.
 
 function checkBatches(plain, batched) {
   const alias = new Map(batched.aliases || []);
@@ -21,15 +23,21 @@ function checkBatches(plain, batched) {
     if (b.start < next || b.count < 2 || b.start + b.count > L.length) return { ok: false, why: `batch at ${b.start} overlaps or is out of range` };
     next = b.start + b.count;
     const first = L[b.start];
-    if (first.kernels.length !== 1) return { ok: false, why: `batch at ${b.start}: a multi-kernel launch` };
-    if (b.kernel.grid[2] !== b.count || b.kernel.grid[0] !== first.kernels[0].grid[0] || b.kernel.grid[1] !== first.kernels[0].grid[1]) {
-      return { ok: false, why: `batch at ${b.start}: grid ${b.kernel.grid} for ${b.count} members` };
+    if (b.kernels.length !== first.kernels.length) return { ok: false, why: `batch at ${b.start}: ${b.kernels.length} batched kernels for ${first.kernels.length}` };
+    for (let j = 0; j < b.kernels.length; j++) {
+      const g = b.kernels[j].grid, m = first.kernels[j].grid;
+      if (g[0] !== m[0] || g[1] !== m[1] || g[2] !== m[2] * b.count) return { ok: false, why: `batch at ${b.start}: grid ${g} for ${b.count} x ${m}` };
+    }
+    if (first.workspace && (b.wsStride < first.workspace || b.count * b.wsStride > batched.workspace)) {
+      return { ok: false, why: `batch at ${b.start}: workspace slices of ${b.wsStride} bytes for ${first.workspace}` };
     }
     for (let k = 0; k < b.count; k++) {
       const l = L[b.start + k];
-      if (l.kernels.length !== 1 || l.kernels[0].name !== first.kernels[0].name || l.workspace) {
-        return { ok: false, why: `batch at ${b.start}: member ${k} is not a launch of the same kernel` };
-      }
+      const same = l.kernels.length === first.kernels.length && l.kernels.every((x, j) => {
+        const y = first.kernels[j];
+        return x.name === y.name && x.grid.join() === y.grid.join() && x.block.join() === y.block.join() && x.lds === y.lds;
+      });
+      if (!same || l.workspace !== first.workspace) return { ok: false, why: `batch at ${b.start}: member ${k} is not a launch of the same kernels` };
       unitOf[b.start + k] = b.start;
     }
   }
@@ -41,19 +49,27 @@ function checkBatches(plain, batched) {
       if (w > i) return { ok: false, why: `launch ${i} reads node ${id} before launch ${w} writes it` };
     }
   }
-  // Launches that use the workspace keep their order (they share its bytes).
-  const ws = (ls) => ls.filter((l) => l.workspace).map((l) => l.node).join(',');
-  if (ws(L) !== ws(plain.launches)) return { ok: false, why: 'workspace users reordered' };
   return { ok: true, batches: (batched.batches || []).length, saved: (batched.batches || []).reduce((s, b) => s + b.count - 1, 0) };
 }
 
 /**
  * Planted mistakes for the check to refuse: `dependent` makes a batch of a launch
  * and a later launch of the same kernel that reads its output (placed right after
- * it); `early` moves a launch in front of the launch that writes its first operand.
+ * it); `early` moves a launch in front of the launch that writes its first operand;
+ * `grid` gives a batch's last member its kernel over twice the z extent (the same
+ * text over another grid, as a column sum of another outer extent has).
  * Returns the modified lowering, or null when the list has no such pair.
  */
 function plantBatchMistake(lowered, kind) {
+  if (kind === 'grid') {
+    const b = (lowered.batches || [])[0];
+    if (!b) return null;
+    const launches = lowered.launches.slice();
+    const last = launches[b.start + b.count - 1];
+    launches[b.start + b.count - 1] = Object.assign({}, last, {
+      kernels: last.kernels.map((k, j) => (j ? k : Object.assign({}, k, { grid: [k.grid[0], k.grid[1], 2 * k.grid[2]] }))) });
+    return Object.assign({}, lowered, { launches });
+  }
   const alias = new Map(lowered.aliases || []);
   const owner = (id) => (alias.has(id) ? alias.get(id) : id);
   const L = lowered.launches;
@@ -65,7 +81,7 @@ function plantBatchMistake(lowered, kind) {
     for (const id of L[j].inputs) {
       const i = pos.get(owner(id));
       if (i === undefined || i >= j || inBatch.has(i)) continue;
-      if (kind === 'dependent' && !(L[i].kernels.length === 1 && L[j].kernels.length === 1 && L[i].kernels[0].name === L[j].kernels[0].name)) continue;
+      if (kind === 'dependent' && L[i].kernels.map((k) => k.name).join(' ') !== L[j].kernels.map((k) => k.name).join(' ')) continue;
       // Move launch j to position i + 1 (dependent) or i (early); batches past the move shift.
       const to = kind === 'dependent' ? i + 1 : i;
       if ((lowered.batches || []).some((b) => b.start < to && to < b.start + b.count)) continue;
@@ -74,8 +90,8 @@ function plantBatchMistake(lowered, kind) {
       order.splice(to, 0, moved);
       const batches = (lowered.batches || []).map((b) => Object.assign({}, b, { start: b.start >= to && b.start < j ? b.start + 1 : b.start }));
       if (kind === 'dependent') {
-        const k = L[i].kernels[0];
-        batches.push({ start: i, count: 2, kernel: { name: `planted_${k.name}`, source: '', grid: [k.grid[0], k.grid[1], 2], block: k.block, lds: k.lds } });
+        const kernels = L[i].kernels.map((k) => ({ name: `planted_${k.name}`, source: '', grid: [k.grid[0], k.grid[1], 2 * k.grid[2]], block: k.block, lds: k.lds }));
+        batches.push({ start: i, count: 2, kernels, wsStride: L[i].workspace ? Math.ceil(L[i].workspace / 256) * 256 : 0 });
         batches.sort((a, b) => a.start - b.start);
       }
       return Object.assign({}, lowered, { launches: order, batches });

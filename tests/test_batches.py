@@ -24,9 +24,38 @@ def test_batched_launch_lists_are_valid_orders(tool):
 
 
 def test_planted_batch_mistakes_are_caught(tool):
+    """Three planted mistakes: a batch whose second member reads the first's output; a
+    launch moved in front of its operand's writer; a member whose kernel has the same
+    text over another grid (a column sum's text leaves its outer extent to the grid:
+    batching two such launches by name alone once ran one member over the other's grid,
+    which the GPU fuzz test caught as a canary overwrite and as perf-lowering
+    differences in 3 of 4000 corpus graphs)."""
     res = tool("batch-check", {"models": MODELS[:1], "corpus": {"from": 1, "to": 100}, "plant": True})
     dep = [r for r in res if "dependent" in r]
     early = [r for r in res if "early" in r]
-    assert len(dep) >= 10 and len(early) >= 100
+    grid = [r for r in res if "grid" in r]
+    assert len(dep) >= 10 and len(early) >= 100 and len(grid) >= 20
     assert all(not r["dependent"]["ok"] for r in dep)
     assert all(not r["early"]["ok"] for r in early)
+    assert all(not r["grid"]["ok"] and "member" in r["grid"]["why"] for r in grid), [r["grid"] for r in grid if r["grid"]["ok"]]
+
+
+def test_same_text_over_another_grid_is_not_batched(tool):
+    """Corpus programs 935, 1101 and 1391 (gradient) hold column sums of one kernel text
+    over different outer extents (grids): no batch mixes them."""
+    res = tool("batch-check", {"corpus": {"from": 935, "to": 935}})
+    res += tool("batch-check", {"corpus": {"from": 1101, "to": 1101}})
+    res += tool("batch-check", {"corpus": {"from": 1391, "to": 1391}})
+    assert all(r["check"]["ok"] for r in res), res
+
+
+def test_headers_never_read_the_z_index():
+    """A batched kernel is the member kernel's text with its z index rewritten to
+    blockIdx.z % Z: that is complete only if no device header reads blockIdx.z or
+    gridDim.z itself (the matmul takes its z index as an argument)."""
+    import pathlib
+    import re
+    kernels = pathlib.Path(__file__).resolve().parents[1] / "tensor-compiler-webgpu_amd" / "csrc" / "kernels"
+    for h in sorted(kernels.glob("*.h")):
+        code = "\n".join(line.split("//")[0] for line in h.read_text().splitlines())
+        assert not re.search(r"\b(blockIdx|gridDim)\.z\b", code), h.name

@@ -140,7 +140,6 @@ def test_c5_full_size_trainer(tool, graph, arena, streams):
     assert r["folded"] > 0 and r["aliases"] > 0 and r["launches"] < r["checkedLaunches"]
     assert abs(r["losses"][0] - np.log(96)) < 0.1, r["losses"]
     assert r["batches"] >= 12, r["batches"]
-    saved = r["batchedLaunches"] - r["batches"]
-    assert r["dispatches"] == (r["kernels"] - saved if streams == 1 else r["kernels"]), r
+    assert r["dispatches"] == (r["kernels"] - r["batchSaves"] if streams == 1 else r["kernels"]), r
     if arena:
         assert r["arena"]["bytes"] < 0.5 * r["arena"]["unshared"], r["arena"]
