@@ -321,19 +321,27 @@ function lowerMI355X(graph, options) {
 }
 
 /**
- * Batched launches (perf lowering): launches of one kernel text (same sizes and
- * operand views) with no data path between them run as one dispatch of its
- * batched form (codegen.js batchedKernel). Walking the list in order, a
- * batchable launch opens a batch, and every later launch of the same kernel
- * whose operands are all written by launches already placed joins it (up to
- * MAX_BATCH); the members are placed together where the first one was. A
- * member is only moved earlier, past launches it does not read, and writes its
- * own node's buffer, so every launch still reads exactly the values it read in
- * graph order. A batch runs each of its launches' kernels over all members in
- * turn (all first kernels, then all second kernels), member k with the
- * workspace slice [k·wsStride, (k + 1)·wsStride). Returns { launches (the new
- * order), batches: [{ start, count, kernels, wsStride }] } with each batch's
- * members at launches[start .. start + count).
+ * Batched launches (perf lowering): launches of one kernel text over the same
+ * grids with no data path between them run as one dispatch per kernel of the
+ * kernels' batched forms (codegen.js batchedKernel). Two passes over the list:
+ *   1. walking it in order, a batchable launch opens a batch, and every later
+ *      launch of the same kernels whose operands are all written by launches
+ *      already placed joins it (up to MAX_BATCH); the members are placed
+ *      together where the first one was, each moved only earlier;
+ *   2. launches of one kernel still alone are grouped where their windows meet:
+ *      a launch may sit anywhere after the last launch writing one of its
+ *      operands and before the first launch reading its output, so launches
+ *      whose windows share a point (and none of which reads another's output)
+ *      are moved together to the first such point (the bias gradients of every
+ *      layer, read only by the parameter updates at the end of a step).
+ * Every launch thus stays after its operands' writers and before its output's
+ * readers, so it reads exactly the values it read in graph order, and writes its
+ * own node's buffer (a batch's members each their own workspace slice). A batch
+ * runs its launches' kernels over all members in turn (all first kernels, then
+ * all second kernels), member k with the workspace slice
+ * [k·wsStride, (k + 1)·wsStride). Returns { launches (the new order), batches:
+ * [{ start, count, kernels, wsStride }] } with each batch's members at
+ * launches[start .. start + count).
  */
 function batchPlan(launches, aliases) {
   const owner = (id) => (aliases.has(id) ? aliases.get(id) : id);
@@ -344,9 +352,11 @@ function batchPlan(launches, aliases) {
   // column sum's outer extent is its grid's z extent only).
   const one = (l) => (l.kernels.every((k) => cg.batchable(k))
     ? l.kernels.map((k) => `${k.name}@${k.grid.join(',')}/${k.block.join(',')}/${k.lds}`).join(' ') : null);
+  const fits = (l, count) => l.kernels.every((k) => cg.batchable(k, count));
+  // Pass 1: units (arrays of launches; two or more: a batch), in order.
   const placed = new Uint8Array(n);
   const ready = (l) => l.inputs.every((id) => { const w = writer.get(owner(id)); return w === undefined || placed[w] === 1; });
-  const order = [], batches = [];
+  let units = [];
   for (let i = 0; i < n; i++) {
     if (placed[i]) continue;
     const group = [i];
@@ -355,14 +365,76 @@ function batchPlan(launches, aliases) {
       for (let j = i + 1; j < n && group.length < cg.MAX_BATCH; j++) {
         if (!placed[j] && one(launches[j]) === name && ready(launches[j])) group.push(j);
       }
-      while (group.length > 1 && !launches[i].kernels.every((k) => cg.batchable(k, group.length))) group.pop();
+      while (group.length > 1 && !fits(launches[i], group.length)) group.pop();
     }
-    if (group.length > 1) {
-      const l = launches[i];
-      batches.push({ start: order.length, count: group.length, kernels: l.kernels.map((k) => cg.batchedKernel(k, group.length)),
+    for (const j of group) placed[j] = 1;
+    units.push(group.map((j) => launches[j]));
+  }
+  // Pass 2: group the launches still alone by their windows.
+  for (let changed = true; changed;) {
+    changed = false;
+    const unitOf = new Map();   // buffer owner -> index of the unit writing it
+    units.forEach((u, x) => { for (const l of u) unitOf.set(owner(l.node), x); });
+    const lo = [], hi = [];     // window: after unit lo, before unit hi
+    units.forEach((u) => { lo.push(-1); hi.push(units.length); });
+    units.forEach((u, x) => {
+      for (const l of u) {
+        for (const id of l.inputs) {
+          const w = unitOf.get(owner(id));
+          if (w === undefined) continue;
+          lo[x] = Math.max(lo[x], w);
+          hi[w] = Math.min(hi[w], x);
+        }
+      }
+    });
+    const byKey = new Map();
+    units.forEach((u, x) => {
+      const k = u.length === 1 ? one(u[0]) : null;
+      if (k) { if (!byKey.has(k)) byKey.set(k, []); byKey.get(k).push(x); }
+    });
+    for (const xs of byKey.values()) {
+      if (xs.length < 2) continue;
+      // A lone launch may follow any unit from lo (its operands' last writer) up to,
+      // not including, hi (its output's first reader); grow a group from the
+      // earliest-opening window while the windows still share an anchor.
+      const cand = xs.slice().sort((a, b) => lo[a] - lo[b] || a - b);
+      const group = [cand[0]];
+      let from = lo[cand[0]], to = hi[cand[0]];
+      const reads = (x, y) => units[y][0].inputs.some((id) => unitOf.get(owner(id)) === x);
+      for (const x of cand.slice(1)) {
+        if (group.length >= cg.MAX_BATCH) break;
+        // Anchors a (insert after unit a) with lo <= a < hi, for every member.
+        const f = Math.max(from, lo[x]), t = Math.min(to, hi[x]);
+        if (f >= t) continue;
+        if (group.some((g) => reads(g, x) || reads(x, g))) continue;
+        group.push(x);
+        from = f; to = t;
+      }
+      while (group.length > 1 && !fits(units[group[0]][0], group.length)) group.pop();
+      if (group.length < 2) continue;
+      // Place the group right after unit `from` (the latest writer of any member's
+      // operand): every member's readers come after it, at `to` or later.
+      const members = group.slice().sort((a, b) => a - b).map((x) => units[x][0]);
+      const inGroup = new Set(group);
+      const next = [];
+      if (from < 0) next.push(members);
+      units.forEach((u, x) => {
+        if (!inGroup.has(x)) next.push(u);
+        if (x === from) next.push(members);
+      });
+      units = next;
+      changed = true;
+      break;
+    }
+  }
+  const order = [], batches = [];
+  for (const u of units) {
+    if (u.length > 1) {
+      const l = u[0];
+      batches.push({ start: order.length, count: u.length, kernels: l.kernels.map((k) => cg.batchedKernel(k, u.length)),
         wsStride: l.workspace ? Math.ceil(l.workspace / 256) * 256 : 0 });
     }
-    for (const j of group) { placed[j] = 1; order.push(launches[j]); }
+    order.push(...u);
   }
   return { launches: order, batches };
 }
