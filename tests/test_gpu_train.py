@@ -128,7 +128,7 @@ def test_c5_full_size_trainer(tool, graph, arena, streams):
     independent launches batched into one dispatch) equal the checked path (plain
     lowering) bit for bit, and the initial loss is near ln(96) (small initial weights,
     uniform tokens). With `arena`, every buffer but the parameters, batch, loss and logits
-    is placed by live range in one allocation (2.4 GB of node buffers in 0.9 GB), the
+    is placed by live range in one allocation (2.3 GB of node buffers in 0.9 GB), the
     members of a batch at one position, and the steps are still bit for bit the checked
     path's; so they are with the step's independent launches on three streams (each
     batch member then launched by itself)."""
