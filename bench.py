@@ -182,6 +182,10 @@ def main() -> None:
                                         "speedup": r["verdict"]["speedup"], "verdict": r["verdict"]["verdict"],
                                         "GBs": r["gbs"]["fused"], "bitwise_same_outputs": r["bitwiseSameOutputs"]}
                             for r in c2["results"]}
+    seq = c2["schedule"].get("sequential")
+    if seq:
+        extra["c2_step_sequential"] = {"GBs": seq["gbs"], "ms_per_step": seq["msPerStep"],
+                                       "note": "every program after the previous on one stream"}
     extra["device"] = {k: full["device"].get(k) for k in ("name", "arch", "computeUnits", "clockKHz", "totalMemory")}
     if "ceiling" in cfg:
         extra["ceiling_1GiB"] = {"copy_GBs": cfg["ceiling"]["copy"]["gbs"], "read_GBs": cfg["ceiling"]["read"]["gbs"]}
@@ -192,7 +196,9 @@ def main() -> None:
         "dtype": "f32", "data": "synthetic",
         "config": {"workload": "C2: fused elementwise chains, seeded programs of 8-16 ops (forward + autodiff gradient) "
                                "over fp32 [8192,1024] with a [1024] row broadcast",
-                   "programs": c2["programs"], "shape": c2["shape"], "step_bytes": c2["stepBytes"]},
+                   "programs": c2["programs"], "shape": c2["shape"], "step_bytes": c2["stepBytes"],
+                   "schedule": f"the {2 * c2['programs']} independent programs issued over {c2['schedule']['streams']} "
+                               "streams, balanced by bytes"},
         "roofline": {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK, "unit": "GB/s", "frac": dom["gbs"] / HBM_PEAK,
                      "traffic": traffic, "traffic_source": traffic_src, "kernel": dom["code"], "kernel_avg_us": dom["avgUs"],
                      "bytes_per_launch": dom["bytesPerLaunch"], "launches_per_step": dom["count"]},

@@ -10,7 +10,8 @@
 // of c1 and c5 replay each step as a captured HIP graph by default (a step is
 // launch-bound at c1's size); --no-trainer-graphs issues their launches directly.
 //
-// --step-only (for profilers): c2 runs its headline step only; c3 and c4 run each
+// --step-only (for profilers): c2 runs its step only, every program after the
+// previous on one stream (the headline issues them over --c2-streams); c3 and c4 run each
 // fused program --steps times after --warmup runs, with no timing loops; c1 and c5
 // run --warmup + --steps trainer steps.
 //
@@ -27,7 +28,7 @@
 const { size } = require('../src/ir/shapes');
 const { fuse } = require('../src/fusion/fuse');
 const { lowerMI355X } = require('../src/mi355x/lower');
-const { HipRunner } = require('../src/mi355x/runner');
+const { HipRunner, Concurrent } = require('../src/mi355x/runner');
 const { HipBench, summarize, verdict, median } = require('../src/mi355x/bench');
 const { chainWorkload, chainInputs } = require('../src/builders/chains');
 const cfg = require('../src/builders/configs');
@@ -170,25 +171,40 @@ function c2(runner, bench, opts) {
       results.push(r);
     }
   }
-  // The headline step: every fused program once; W warm-up steps, then K timed steps.
+  // The headline step: every fused program once; W warm-up steps, then K timed steps
+  // bracketed by hipEvents. The 16 programs are independent (each its own buffers), so
+  // the step issues them as one concurrent group over --c2-streams streams (default 2:
+  // 1 to 4 measured, 2 fastest), balanced by bytes; the sequential step, every program
+  // after the previous on one stream (with --graphs: each a replayed HIP graph), is
+  // timed beside it.
+  const timeSteps = (issue) => {
+    for (let i = 0; i < W; i++) issue();
+    runner.a.sync();
+    const t0 = process.hrtime.bigint();
+    runner.a.eventRecord(bench.start);
+    for (let i = 0; i < K; i++) issue();
+    runner.a.eventRecord(bench.end);
+    const ms = runner.a.eventElapsed(bench.start, bench.end);
+    runner.a.sync();
+    return { msPerStep: ms / K, wallMsPerStep: Number(process.hrtime.bigint() - t0) / 1e6 / K };
+  };
   const go = bench.graphs ? (p) => p.replay() : (p) => p.run();
   for (const p of programs) if (bench.graphs) p.capture();
-  for (let i = 0; i < W; i++) for (const p of programs) go(p);
-  runner.a.sync();
-  const t0 = process.hrtime.bigint();
-  runner.a.eventRecord(bench.start);
-  for (let i = 0; i < K; i++) for (const p of programs) go(p);
-  runner.a.eventRecord(bench.end);
-  const ms = runner.a.eventElapsed(bench.start, bench.end);
-  runner.a.sync();
-  const wallMs = Number(process.hrtime.bigint() - t0) / 1e6;
+  const sequential = timeSteps(() => { for (const p of programs) go(p); });
+  // Profiling mode runs the sequential step only, so each kernel's traced duration is its own.
+  const S = Number(arg('c2-streams', 2));
+  const group = stepOnly ? null : new Concurrent(runner, programs, S);
+  const headline = stepOnly ? sequential : timeSteps(() => group.run());
+  const ms = headline.msPerStep * K, wallMs = headline.wallMsPerStep * K;
   for (const p of programs) p.destroy();
   const stepBytes = results.reduce((s, r) => s + r.bytes.fused, 0);
   // The roofline kernel: the fused kernel moving the most algorithmic bytes per step,
   // chosen without timing so a profile of the same step names the same kernel (each
   // fused body is its own kernel, at one size, so its average is well defined).
   const all = [].concat.apply([], results.map((r) => r.launchF)).filter((l) => l.kind.startsWith('fused-'));
-  return { config: 'c2', shape: [R, C], programs: P, steps: K, warmup: W, arena, msPerStep: ms / K, wallMsPerStep: wallMs / K,
+  sequential.gbs = stepBytes / (sequential.msPerStep * 1e6);
+  const schedule = stepOnly ? { streams: 1 } : { streams: S, bytesPerStream: group.load, sequential };
+  return { config: 'c2', shape: [R, C], programs: P, steps: K, warmup: W, arena, schedule, msPerStep: ms / K, wallMsPerStep: wallMs / K,
     stepBytes, gbs: stepBytes / ((ms / K) * 1e6), dominant: stepOnly ? null : dominant(all), results };
 }
 

@@ -642,6 +642,57 @@ async function gpuLocal(req, dir) {
  * graph and compare loss and parameters bit for bit (the trainer's feedback
  * against the checked path, harness-m4.js:310-330).
  */
+/**
+ * Config 2's programs (seeds 0..P-1, forward and gradient, perf lowering) run one after
+ * another on one stream, then, with every kept output a launch writes overwritten
+ * first, as one concurrent group over each of `streams`: the outputs must be the same
+ * bits.
+ */
+async function gpuConcurrent(req) {
+  const { HipRunner, Concurrent, CANARY_BITS } = require('../src/mi355x/runner');
+  const { chainWorkload, chainInputs } = require('../src/builders/chains');
+  const runner = HipRunner.create();
+  const programs = [], kept = [];
+  for (let seed = 0; seed < req.programs; seed++) {
+    const w = chainWorkload(seed, req.R, req.C);
+    const inputs = chainInputs(seed, req.R, req.C);
+    for (const kind of ['forward', 'gradient']) {
+      const v = w[kind];
+      const f = fuse(v.graph, { keep: v.keep });
+      const keep = v.keep.map((id) => f.index.get(id));
+      const p = runner.prepare(f.graph, lowerMI355X(f.graph, { perf: true, keep }));
+      for (const n of f.graph.nodes) if (n.op === 'input') p.write(n.id, inputs[n.attrs.name]);
+      programs.push(p);
+      kept.push(keep);
+    }
+  }
+  const readAll = () => programs.map((p, i) => kept[i].map((id) => p.read(id)));
+  for (const p of programs) p.run();
+  runner.a.sync();
+  const want = readAll();
+  const out = { programs: programs.length, streams: {} };
+  for (const S of req.streams) {
+    // Overwrite every kept output a launch writes (kept constants stay: no launch writes them).
+    programs.forEach((p, i) => {
+      const written = new Set(p.launches.map((l) => l.node));
+      for (const id of kept[i]) if (written.has(id)) runner.a.fill32(p.bufs[id], 0, CANARY_BITS, p.n[id]);
+    });
+    const g = new Concurrent(runner, programs, S);
+    g.run();
+    runner.a.sync();
+    const got = readAll();
+    let same = 0, total = 0;
+    got.forEach((outs, i) => outs.forEach((a, k) => {
+      const x = new Uint32Array(a.buffer), y = new Uint32Array(want[i][k].buffer);
+      total += x.length;
+      for (let q = 0; q < x.length; q++) if (x[q] === y[q]) same++;
+    }));
+    out.streams[S] = { same, total, load: g.load };
+  }
+  for (const p of programs) p.destroy();
+  return out;
+}
+
 async function gpuTrain(req) {
   const { modelStep } = require('../src/builders/models');
   const { fusedStep, HipTrainer } = require('../src/mi355x/trainer');
@@ -955,6 +1006,26 @@ async function main() {
       }
       break;
     }
+    case 'concurrent-check': {
+      // A concurrent group over stand-in programs (no device): stream assignment, the
+      // concatenated launch arrays, and the refusal of programs that share a written buffer.
+      const { Concurrent } = require('../src/mi355x/runner');
+      const fake = (i, bytes, kernels, shareWith) => {
+        const launches = bytes.map((b, j) => ({ node: j + 1, inputs: [0], bytes: b }));
+        const bufs = [1000 * (i + 1)].concat(bytes.map((_, j) => (shareWith !== undefined && j === 0 ? 1000 * (shareWith + 1) + 1 : 1000 * (i + 1) + j + 1)));
+        const args = new Uint8Array(kernels * 16).map((_, q) => (i * 16 + q) % 256);
+        return { dag: null, launches, bufs, ws: 900000 + i, count: kernels, fns: new Float64Array(kernels).fill(i + 1),
+          dims: new Uint32Array(kernels * 7).fill(i), args, offsets: Uint32Array.from({ length: kernels + 1 }, (_, q) => q * 16) };
+      };
+      const runner = { a: {} };
+      const programs = (req.bytes || [[5], [3, 3], [4], [1], [2, 2]]).map((b, i) => fake(i, b, b.length + 1));
+      const g = new Concurrent(runner, programs, req.streams || 2);
+      let refused = null;
+      try { new Concurrent(runner, [fake(0, [1], 1), fake(1, [1], 1, 0)], 2); } catch (e) { refused = String(e.message); }
+      out = { load: g.load, streamOf: Array.from(g.streamOf), fns: Array.from(g.fns), offsets: Array.from(g.offsets),
+        args: Array.from(g.args), refused };
+      break;
+    }
     case 'attention-graphs': out = attentionGraphs(req.cases || ATTENTION_CASES); break;
     case 'transformer-forward': out = transformerForward(req); break;
     case 'perf-lower': {
@@ -982,6 +1053,7 @@ async function main() {
     case 'step-graph': stepGraph(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-local': await gpuLocal(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-train': out = await gpuTrain(req); break;
+    case 'gpu-concurrent': out = await gpuConcurrent(req); break;
     case 'gpu-chains': await gpuChains(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-graphs': await gpuGraphs(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-configs': await gpuConfigs(req, outDir(argv)); out = { ok: true }; break;

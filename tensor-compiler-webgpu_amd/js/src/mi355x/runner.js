@@ -519,4 +519,77 @@ class Program {
   }
 }
 
-module.exports = { HipRunner, Program, packArgs, packPtrs, translationUnit, precompile, CANARY_BITS, CANARY_PAD, ARG_BYTES, PTR_BYTES, PRELUDE };
+/**
+ * Independent programs issued together over `streams` streams (1..4), every
+ * program's launches in order on its stream, in one native call that forks the
+ * side streams off the library stream first and joins them back at the end
+ * (tcmi_launch_dag), so one program's kernel ramp and tail overlap another
+ * program's kernels. Programs go to streams longest first, each to the stream
+ * with the fewest algorithmic bytes so far, so the streams end together. The
+ * programs must share no buffer that one of them writes (checked by address: each
+ * must own its buffers, as prepare() makes them) and must each be issued on one
+ * stream.
+ */
+class Concurrent {
+  constructor(runner, programs, streams) {
+    if (!(streams >= 1 && streams <= 4)) throw new Error(`streams must be 1..4, got ${streams}`);
+    this.a = runner.a;
+    const written = new Map();   // device address -> program index
+    programs.forEach((p, i) => {
+      if (p.dag) throw new Error('a program issued over several streams cannot join a concurrent group');
+      for (const l of p.launches) {
+        const w = p.bufs[l.node];
+        if (written.has(w) && written.get(w) !== i) throw new Error(`programs ${written.get(w)} and ${i} both write buffer ${w}`);
+        written.set(w, i);
+      }
+      if (written.has(p.ws) && written.get(p.ws) !== i) throw new Error(`programs ${written.get(p.ws)} and ${i} share a workspace`);
+      written.set(p.ws, i);
+    });
+    programs.forEach((p, i) => {
+      for (const l of p.launches) {
+        for (const id of l.inputs) {
+          const w = written.get(p.bufs[id]);
+          if (w !== undefined && w !== i) throw new Error(`program ${i} reads buffer ${p.bufs[id]} that program ${w} writes`);
+        }
+      }
+    });
+    const count = programs.reduce((c, p) => c + p.count, 0);
+    const bytes = programs.reduce((c, p) => c + p.args.length, 0);
+    this.fns = new Float64Array(count);
+    this.dims = new Uint32Array(count * 7);
+    this.args = new Uint8Array(bytes);
+    this.offsets = new Uint32Array(count + 1);
+    this.streamOf = new Uint8Array(count);
+    const work = programs.map((p) => p.launches.reduce((q, l) => q + l.bytes, 0));
+    const load = new Array(streams).fill(0), streamOfProgram = new Array(programs.length);
+    programs.map((_, i) => i).sort((x, y) => work[y] - work[x] || x - y).forEach((i) => {
+      let best = 0;
+      for (let t = 1; t < streams; t++) if (load[t] < load[best]) best = t;
+      streamOfProgram[i] = best;
+      load[best] += work[i];
+    });
+    this.load = load;
+    let k = 0, at = 0;
+    programs.forEach((p, i) => {
+      this.fns.set(p.fns, k);
+      this.dims.set(p.dims, k * 7);
+      this.args.set(p.args, at);
+      for (let j = 0; j < p.count; j++) this.offsets[k + j] = at + p.offsets[j];
+      this.streamOf.fill(streamOfProgram[i], k, k + p.count);
+      k += p.count;
+      at += p.args.length;
+    });
+    this.offsets[count] = at;
+    this.streams = streams;
+    this.recordEvent = new Int32Array(count).fill(-1);
+    this.waitBegin = new Uint32Array(count + 1);
+    this.waits = new Uint32Array(0);
+  }
+
+  /** Enqueue every program once (asynchronous). */
+  run() {
+    this.a.launchDag(this.fns, this.dims, this.args, this.offsets, this.streams, this.streamOf, this.recordEvent, this.waitBegin, this.waits);
+  }
+}
+
+module.exports = { HipRunner, Program, Concurrent, packArgs, packPtrs, translationUnit, precompile, CANARY_BITS, CANARY_PAD, ARG_BYTES, PTR_BYTES, PRELUDE };
