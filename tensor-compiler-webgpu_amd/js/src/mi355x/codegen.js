@@ -229,16 +229,21 @@ const indent = (lines, pad) => lines.map((l) => pad + l).join('\n');
  * scalar tail handles n % 4. Operands read at the output index are float4
  * loads; a span load is a float4 when its 4 lanes are contiguous in the source,
  * one scalar when they share an element, else 4 scalars.
- * `tuning`: { unroll (U, default 1), nt (default true), blocks (default 2048) }.
+ * `tuning`: { unroll (U), nt (default true), blocks }. Defaults by size, from
+ * whole-program sweeps on the MI355X: 2048 workgroups, U = 1 up to 2^25 elements
+ * (config 2's 32 MB tensors: fewer workgroups or U = 2 lost up to 7 %); 512
+ * workgroups, U = 2 from 2^25 up (config 3's 268 MB tensors: 6 % faster over its
+ * programs).
  */
 function elementwiseKernel(b, output, outShape, opts) {
   const o = opts || {};
   const tune = o.tuning || {};
-  const U = tune.unroll || 1;
-  const nt = tune.nt === undefined ? true : !!tune.nt;
-  const maxBlocks = tune.blocks || 2048;
-  checkOperands(b);
   const n = size(outShape);
+  const large = n >= 2 ** 25;
+  const U = tune.unroll || (large ? 2 : 1);
+  const nt = tune.nt === undefined ? true : !!tune.nt;
+  const maxBlocks = tune.blocks || (large ? 512 : 2048);
+  checkOperands(b);
   if (n >= 2 ** 31) throw new Error(`elementwise kernel over ${n} elements exceeds the 32-bit index space`);
   const params = [n];
 

@@ -119,7 +119,8 @@ function lowerNode(graph, node, opts, mmViews, folds) {
     if (inner === 1) {
       // A reduction over the last non-trivial axis: the rowwise kernel on [outer, n].
       const { body, output } = oneOpBody(graph, node, [[outer, n]], { axis: 1, keepDims: true });
-      return Object.assign({ kind: 'rowreduce' }, single(cg.rowwiseKernel(body, output, { tuning: (opts.tuning || {}).row })));
+      const t = opts.tuning || {};
+      return Object.assign({ kind: 'rowreduce' }, single(cg.rowwiseKernel(body, output, { tuning: t.rowreduce || t.row })));
     }
     const c = cg.colreduceKernels(node.op, outer, n, inner, (opts.tuning || {}).colreduce);
     return { kind: 'colreduce', kernels: c.launches, params: c.params, workspace: c.workspace, flops: 0 };
