@@ -154,6 +154,15 @@ int tcmi_capture_begin(void);
 int tcmi_capture_end(uint64_t* graph);
 /* Replay a captured graph on the library stream. */
 int tcmi_graph_launch(uint64_t graph);
+/* One training step in one call, as FusedTrainer.train does it with one queue
+ * submit (trainer-fused.js:59-81: write the batch, submit, read the loss back):
+ * `count` host->device copies of bytes[i] from src[i] to the allocation dst[i]
+ * (offset 0) on the library stream, small ones staged through pinned host
+ * memory, then the replay of `graph`, then `out_bytes` from the device address
+ * `out_src` into host `out`, then a wait for all of it. Everything is checked
+ * before anything is enqueued; the sources may be reused when it returns. */
+int tcmi_graph_step(uint32_t count, const uint64_t* dst, const void* const* src, const uint64_t* bytes, uint64_t graph,
+                    uint64_t out_src, void* out, uint64_t out_bytes);
 int tcmi_graph_destroy(uint64_t graph);
 
 /* --- built-in measurement kernels (workloads.js:312-345 ceilingPrograms) ----- */

@@ -84,16 +84,16 @@ struct Args {
     return true;
   }
   // Any TypedArray or Buffer: its bytes.
-  bool bytes(size_t i, void** data, size_t* length) {
+  bool bytes(size_t i, void** data, size_t* length) { return i < argc && typed_bytes(env, argv[i], data, length); }
+  static bool typed_bytes(napi_env env, napi_value v, void** data, size_t* length) {
     bool is = false;
-    if (i >= argc) return false;
-    napi_is_typedarray(env, argv[i], &is);
+    napi_is_typedarray(env, v, &is);
     if (is) {
       napi_typedarray_type type;
       size_t n;
       napi_value ab;
       size_t off;
-      if (napi_get_typedarray_info(env, argv[i], &type, &n, data, &ab, &off) != napi_ok) return false;
+      if (napi_get_typedarray_info(env, v, &type, &n, data, &ab, &off) != napi_ok) return false;
       size_t el = 1;
       switch (type) {
         case napi_int16_array: case napi_uint16_array: el = 2; break;
@@ -106,8 +106,8 @@ struct Args {
       *length = n * el;
       return true;
     }
-    napi_is_buffer(env, argv[i], &is);
-    if (is) return napi_get_buffer_info(env, argv[i], data, length) == napi_ok;
+    napi_is_buffer(env, v, &is);
+    if (is) return napi_get_buffer_info(env, v, data, length) == napi_ok;
     return false;
   }
   // An array of three unsigned 32-bit numbers.
@@ -360,6 +360,38 @@ napi_value LaunchDag(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+// graphStep(dsts: Float64Array, srcs: TypedArray[], graph, outSrc, out: TypedArray):
+// one training step in one native call (uploads, graph replay, result readback, wait).
+napi_value GraphStep(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  void *dsts, *out;
+  size_t nd, nout;
+  uint64_t graph, out_src;
+  bool is_array = false;
+  if (!a.bytes(0, &dsts, &nd) || a.argc < 2 || napi_is_array(env, a.argv[1], &is_array) != napi_ok || !is_array ||
+      !a.u64(2, &graph) || !a.u64(3, &out_src) || !a.bytes(4, &out, &nout))
+    return throw_type(env, "graphStep(dsts, srcs, graph, outSrc, out)");
+  uint32_t count = 0;
+  napi_get_array_length(env, a.argv[1], &count);
+  if (nd != count * 8) return throw_type(env, "graphStep: one destination per source");
+  std::vector<uint64_t> dst(count), bytes(count);
+  std::vector<const void*> src(count);
+  for (uint32_t i = 0; i < count; ++i) {
+    double h = static_cast<const double*>(dsts)[i];
+    if (!(h >= 0) || h > 9007199254740991.0 || std::floor(h) != h) return throw_type(env, "graphStep: bad destination handle");
+    dst[i] = static_cast<uint64_t>(h);
+    napi_value el;
+    void* data;
+    size_t n;
+    if (napi_get_element(env, a.argv[1], i, &el) != napi_ok || !Args::typed_bytes(env, el, &data, &n))
+      return throw_type(env, "graphStep: every source must be a TypedArray");
+    src[i] = data;
+    bytes[i] = n;
+  }
+  CHECK(tcmi_graph_step(count, dst.data(), src.data(), bytes.data(), graph, out_src, out, nout), "tcmi_graph_step");
+  return undef(env);
+}
+
 napi_value DagReserve(napi_env env, napi_callback_info info) {
   Args a(env, info);
   uint32_t n;
@@ -465,7 +497,7 @@ napi_value Register(napi_env env, napi_value exports) {
       {"launch", Launch}, {"launchMany", LaunchMany}, {"launchDag", LaunchDag}, {"dagReserve", DagReserve},
       {"sync", Sync}, {"eventCreate", EventCreate},
       {"eventRecord", EventRecord}, {"eventElapsed", EventElapsed}, {"eventDestroy", EventDestroy},
-      {"captureBegin", CaptureBegin}, {"captureEnd", CaptureEnd}, {"graphLaunch", GraphLaunch},
+      {"captureBegin", CaptureBegin}, {"captureEnd", CaptureEnd}, {"graphLaunch", GraphLaunch}, {"graphStep", GraphStep},
       {"graphDestroy", GraphDestroy}, {"ceilingCopy", CeilingCopy}, {"ceilingRead", CeilingRead},
   };
   for (auto& f : fns) {

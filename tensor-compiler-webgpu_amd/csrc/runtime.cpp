@@ -50,6 +50,10 @@ hipStream_t g_side[kSideStreams] = {};
 hipEvent_t g_fork = nullptr;
 hipEvent_t g_join[kSideStreams] = {};
 std::vector<hipEvent_t> g_dag_events;
+// Pinned host staging for tcmi_graph_step's small copies (hipHostMalloc'd at init):
+// a pageable copy costs a staging round trip of its own in the runtime.
+constexpr uint64_t kStageBytes = 1u << 20;
+char* g_stage = nullptr;
 hipDeviceProp_t g_props;
 std::string g_arch;        // "gfx950" (features stripped)
 std::string g_cache_dir;
@@ -306,6 +310,7 @@ int tcmi_init(void) {
     HIP_TRY(hipEventCreateWithFlags(&g_join[k], hipEventDisableTiming), "hipEventCreateWithFlags");
   }
   HIP_TRY(hipEventCreateWithFlags(&g_fork, hipEventDisableTiming), "hipEventCreateWithFlags");
+  HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&g_stage), kStageBytes, hipHostMallocDefault), "hipHostMalloc (staging)");
   g_init = true;
   return TCMI_OK;
 }
@@ -631,6 +636,43 @@ int tcmi_graph_launch(uint64_t graph) {
   auto it = g_graphs.find(graph);
   if (it == g_graphs.end()) return fail(TCMI_E_INVALID, "unknown graph");
   HIP_TRY(hipGraphLaunch(it->second.second, g_stream), "hipGraphLaunch");
+  return TCMI_OK;
+}
+
+int tcmi_graph_step(uint32_t count, const uint64_t* dst, const void* const* src, const uint64_t* bytes, uint64_t graph,
+                    uint64_t out_src, void* out, uint64_t out_bytes) {
+  if (int rc = ready()) return rc;
+  auto it = g_graphs.find(graph);
+  if (it == g_graphs.end()) return fail(TCMI_E_INVALID, "tcmi_graph_step: unknown graph");
+  if (count && (!dst || !src || !bytes)) return fail(TCMI_E_INVALID, "tcmi_graph_step: null copy arrays");
+  if (out_bytes && (!out || !range_ok(out_src, 0, out_bytes))) return fail(TCMI_E_INVALID, "tcmi_graph_step: bad output range");
+  // Check everything before enqueueing anything.
+  uint64_t staged = 0;
+  for (uint32_t i = 0; i < count; ++i) {
+    if (bytes[i] && (!src[i] || !range_ok(dst[i], 0, bytes[i]))) return fail(TCMI_E_INVALID, "tcmi_graph_step: copy outside its allocation");
+  }
+  // The uploads: small ones through the pinned staging buffer (one host memcpy, then a
+  // DMA the stream runs without a pageable round trip), large ones directly.
+  for (uint32_t i = 0; i < count; ++i) {
+    if (!bytes[i]) continue;
+    void* d = reinterpret_cast<void*>(dst[i]);
+    const uint64_t b = bytes[i];
+    if (b <= (kStageBytes >> 2) && staged + b <= kStageBytes - 4096) {
+      std::memcpy(g_stage + staged, src[i], b);
+      HIP_TRY(hipMemcpyAsync(d, g_stage + staged, b, hipMemcpyHostToDevice, g_stream), "hipMemcpyAsync H2D (staged)");
+      staged += (b + 255) & ~uint64_t(255);
+    } else {
+      HIP_TRY(hipMemcpyAsync(d, src[i], b, hipMemcpyHostToDevice, g_stream), "hipMemcpyAsync H2D");
+    }
+  }
+  HIP_TRY(hipGraphLaunch(it->second.second, g_stream), "hipGraphLaunch");
+  // The result: through the last page of the staging buffer when it fits.
+  char* back = out_bytes <= 4096 ? g_stage + kStageBytes - 4096 : static_cast<char*>(out);
+  if (out_bytes)
+    HIP_TRY(hipMemcpyAsync(back, reinterpret_cast<void*>(out_src), out_bytes, hipMemcpyDeviceToHost, g_stream),
+            "hipMemcpyAsync D2H");
+  HIP_TRY(hipStreamSynchronize(g_stream), "hipStreamSynchronize after the step");
+  if (out_bytes && back != out) std::memcpy(out, back, out_bytes);
   return TCMI_OK;
 }
 

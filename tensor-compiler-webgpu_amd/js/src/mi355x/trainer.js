@@ -104,10 +104,26 @@ class HipTrainer {
     this.advance();
   }
 
-  /** One training step; returns the loss computed from the parameters before the update. */
+  /**
+   * One training step; returns the loss computed from the parameters before the update.
+   * With graph replay the whole step (batch upload, replay, loss readback) is one
+   * native call (tcmi_graph_step).
+   */
   train(x, y) {
-    this.enqueue(x, y);
-    this.a.d2h(this.lossAt, 0, this.lossBuf);
+    if (!this.graph) {
+      this.enqueue(x, y);
+      this.a.d2h(this.lossAt, 0, this.lossBuf);
+      return this.lossBuf[0];
+    }
+    const p = this.programs[this.turn];
+    if (!p.graphHandle) p.capture();
+    const ix = this.step.inputs.x, iy = this.step.inputs.y;
+    const xs = x instanceof Float32Array ? x : Float32Array.from(x);
+    const ys = y instanceof Float32Array ? y : Float32Array.from(y);
+    if (xs.length !== p.n[ix] || ys.length !== p.n[iy]) throw new Error(`batch of ${xs.length} and ${ys.length} values, the step takes ${p.n[ix]} and ${p.n[iy]}`);
+    this.a.graphStep(Float64Array.from([p.bufs[ix], p.bufs[iy]]), [xs, ys], p.graphHandle, p.bufs[this.step.loss], this.lossBuf);
+    this.lossAt = p.bufs[this.step.loss];
+    this.turn ^= 1;
     return this.lossBuf[0];
   }
 
