@@ -1041,9 +1041,10 @@ function batchedKernel(k, count) {
   if (k.source.split(sig).length !== 2) throw new Error(`kernel ${k.name}: no single entry point to batch`);
   if (/gridDim\.z/.test(k.source)) throw new Error(`kernel ${k.name} reads gridDim.z`);
   const Z = k.grid[2];
+  const [head, tail] = k.source.split(sig);
+  const ownZ = (t) => t.split('blockIdx.z').join(`(blockIdx.z % ${Z}u)`);
   const entry = `__KERNEL__${suffix || ''}(const TcmiBatch<${count}> B) {\n  const TcmiPtrs& A = B.m[blockIdx.z / ${Z}u];`;
-  const text = k.source.split(sig).map((part) => part.split('blockIdx.z').join(`(blockIdx.z % ${Z}u)`)).join('\u0000')
-    .replace('\u0000', entry).split(base).join('__KERNEL__');
+  const text = (ownZ(head) + entry + ownZ(tail)).split(base).join('__KERNEL__');
   const b = kernelText(`b${k.name.split('_')[1]}`, text);
   return { name: b.name + (suffix || ''), source: b.source, grid: [k.grid[0], k.grid[1], Z * count], block: k.block.slice(), lds: k.lds,
     members: count };
