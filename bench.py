@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs c2,c3,c4] [--quick]
 
-The headline (`value`) is BASELINE config 2, the one BASELINE's metric is
+The headline (`value`) is config 2 of the benchmark, the one its metric is
 quoted on first: fused elementwise chains — 8 seeded programs of 8–16 ops over
 fp32 [8192, 1024] with a [1024] row-vector broadcast, each run forward and as
 its autodiff gradient graph — in algorithmic HBM GB/s (every unique operand of

@@ -1,6 +1,6 @@
 #!/usr/bin/env node
 'use strict';
-// Measurement of the MI355X backend on BASELINE's configs, printed as one JSON
+// Measurement of the MI355X backend on the benchmark's five configs, printed as one JSON
 // document (bench.py turns it into the driver's one-line record).
 //
 //   node bench.js [--configs ceiling,c2,c3,c4] [--steps K] [--warmup W] [--programs P]

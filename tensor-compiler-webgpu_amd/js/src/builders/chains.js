@@ -1,5 +1,5 @@
 'use strict';
-// BASELINE config 2: seeded random elementwise programs of 8–16 ops over
+// Benchmark config 2: seeded random elementwise programs of 8–16 ops over
 // [R, C] fp32 tensors (R 8192, C 1024 at full size), drawn from add, sub, mul,
 // div, neg, exp, log, relu, tanh, step and the broadcast of a [C] row vector.
 // Inputs are N(0, 1). log and div operands are made positive the way the

@@ -1,5 +1,5 @@
 'use strict';
-// Graphs and seeded inputs of BASELINE configs 3 and 4, shared by the bench and
+// Graphs and seeded inputs of benchmark configs 3 and 4, shared by the bench and
 // by the parity runs, so that both see the same values.
 //
 //   config 3  softmax / logSoftmax over x [R, C] (full size [16384, 4096]),

@@ -1,5 +1,5 @@
 'use strict';
-// BASELINE config 1: the MLP training step as one IR graph — X [128, 64] ->
+// Benchmark config 1: the MLP training step as one IR graph — X [128, 64] ->
 // dense 64->128 tanh -> dense 128->10, log-softmax cross-entropy against
 // one-hot labels, autodiff's gradient graph, plain SGD (p - 0.1·g) — built the
 // way the reference builds its MLP step (src/train/step.js:60-127 in

@@ -1,5 +1,5 @@
 'use strict';
-// The training steps of BASELINE's model configs, with their data:
+// The training steps of the benchmark's model configs (1 and 5), with their data:
 //   mlp            config 1: X [128, 64], 64 -> 128 tanh -> 10, log-softmax CE, SGD 0.1
 //   transformer    config 5: V 96, d 256, H 4, L 4, ff 1024 ReLU, T 128, batch B (64 at
 //                  full size), N(0, 0.02) weights from seed 0, plain SGD (lr 0.05)

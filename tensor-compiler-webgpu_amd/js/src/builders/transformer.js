@@ -11,7 +11,7 @@
 // reference fixes its sizes in a module constant (T 64, d 64, L 2, ff 256,
 // GELU); here they are a config, so that the same construction builds both the
 // reference's model (to pin the fusion pass against its recorded counts) and
-// BASELINE config 5 (V 96, d 256, H 4, L 4, ff 1024 ReLU, T 128).
+// benchmark config 5 (V 96, d 256, H 4, L 4, ff 1024 ReLU, T 128).
 
 const { Graph } = require('../ir/graph');
 const { grad } = require('../autodiff');

@@ -1,4 +1,4 @@
-"""GPU parity of BASELINE config 2 (fused elementwise chains, forward and gradient)
+"""GPU parity of benchmark config 2 (fused elementwise chains, forward and gradient)
 at its full size [8192, 1024], and of all eight programs at a small row count:
 every kept output of the fused and of the unfused launch list within the float32
 budget of the float64 oracle (streamed, node by node), canaries intact, and the

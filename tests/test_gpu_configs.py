@@ -1,4 +1,4 @@
-"""GPU parity of BASELINE configs 3 (softmax / logSoftmax forward and gradient
+"""GPU parity of benchmark configs 3 (softmax / logSoftmax forward and gradient
 over [16384, 4096], 1 % of rows shifted by +800) and 4 (matmul + bias -> relu |
 tanh at its three shapes, forward and gradient with the transposed-operand
 matmuls), at full size, fused and unfused, canary-padded.

@@ -1,4 +1,4 @@
-"""GPU parity of the training steps (BASELINE configs 1 and 5, and the reference's own
+"""GPU parity of the training steps (benchmark configs 1 and 5, and the reference's own
 transformer) through the fused trainer: node-local judging of every launch of the fused
 step on the float32-rounded reference operands (the reference's teacher-forced check,
 harness-m4.js:182-223 and :225-272), the first step's loss and new parameters against the
