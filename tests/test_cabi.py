@@ -38,13 +38,18 @@ def test_calls_before_init_fail_cleanly():
     assert rc == 10004
     assert b"tcmi_init" in t.lib.tcmi_last_error()
     assert b"packed-fp32-ops" in t.lib.tcmi_compile_options()
+    # So must a whole training step, the launch-list and the stream-graph entry points.
+    out = (ctypes.c_float * 1)()
+    assert t.lib.tcmi_graph_step(0, None, None, None, 1, 0, out, 4) == 10004
+    assert t.lib.tcmi_launch_dag(0, None, None, None, None, 1, None, None, None, None) == 10004
+    assert t.lib.tcmi_dag_reserve(1) == 10004
 
 
 def test_node_addon_loads_and_exports():
     js = ("const a=require(process.argv[1]);"
           "const want=['init','info','malloc','free','h2d','d2h','d2d','fill32','countNot32','compile','precompile',"
           "'function','launch','launchMany','sync','eventCreate','eventRecord','eventElapsed','captureBegin','captureEnd',"
-          "'graphLaunch','ceilingCopy','ceilingRead'];"
+          "'graphLaunch','graphStep','launchDag','dagReserve','ceilingCopy','ceilingRead'];"
           "const miss=want.filter((k)=>typeof a[k]!=='function'); if(miss.length){console.log(miss.join());process.exit(2);}"
           "try{a.malloc(16);process.exit(3);}catch(e){if(!/tcmi_init/.test(e.message))process.exit(4);}")
     p = subprocess.run(["node", "-e", js, str(PKG / "lib" / "tcmi.node")], capture_output=True, text=True)
