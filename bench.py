@@ -128,6 +128,15 @@ def main() -> None:
     full = json.loads(p.stdout)
     if a.out:
         pathlib.Path(a.out).write_text(json.dumps(full, indent=1))
+    line = compose(full)
+    if not a.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(8192 if not a.quick else 256, range(min(a.programs, 8)), 0.0 if a.quick else 10.0)
+    print(json.dumps(line))
+
+
+def compose(full: dict) -> dict:
+    """The driver's one-line record from bench.js's measurement document (everything but
+    the CPU baseline, which this process times itself)."""
     cfg = full["configs"]
     c2 = cfg.get("c2")
     extra = {}
@@ -204,9 +213,7 @@ def main() -> None:
                      "bytes_per_launch": dom["bytesPerLaunch"], "launches_per_step": dom["count"]},
         "extra": extra,
     }
-    if not a.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(8192 if not a.quick else 256, range(min(a.programs, 8)), 0.0 if a.quick else 10.0)
-    print(json.dumps(line))
+    return line
 
 
 if __name__ == "__main__":
