@@ -104,6 +104,8 @@ const ATTENTION_CASES = [
   { name: 'query-blocks', dims: [2, 2, 130, 256, 32, 32], scale: 0.18, fuses: true },
   { name: 'pre-transposed', dims: [2, 2, 64, 64, 32, 32], scale: 0.18, mask: true, kTransposed: true, vTransposed: true, fuses: true },
   { name: 'too-many-keys', dims: [1, 1, 8, 1024, 16, 16], scale: 0.25, fuses: false },
+  // Two independent attentions of one shape: the perf lowering batches their kernels.
+  { name: 'twin', dims: [2, 2, 48, 64, 32, 32], scale: 0.18, mask: true, twice: true, fuses: true },
 ];
 
 /**
@@ -116,21 +118,25 @@ function attentionGraphs(cases) {
   return cases.map((c) => {
     const g = new Graph();
     const [B, H, TQ, TK, DH, DV] = c.dims;
-    const q = g.input('q', [B, H, TQ, DH]);
-    const kt = c.kTransposed ? g.input('kt', [B, H, DH, TK]) : g.transpose(g.input('k', [B, H, TK, DH]), [0, 1, 3, 2]);
-    const v = c.vTransposed ? g.transpose(g.input('vt', [B, H, DV, TK]), [0, 1, 3, 2]) : g.input('v', [B, H, TK, DV]);
-    let s = g.matmul(q, kt);
-    if (c.scale) s = g.mul(s, g.const(c.scale));
-    if (c.mask) {
-      const m = [];
-      for (let i = 0; i < TQ; i++) for (let j = 0; j < TK; j++) m.push(j > i + (TK - TQ) ? -1e4 : 0);
-      s = g.add(s, g.const(m, [TQ, TK]));
-    }
-    const o = g.matmul(g.softmax(s, 3), v);
+    const one = (sfx) => {
+      const q = g.input(`q${sfx}`, [B, H, TQ, DH]);
+      const kt = c.kTransposed ? g.input(`kt${sfx}`, [B, H, DH, TK]) : g.transpose(g.input(`k${sfx}`, [B, H, TK, DH]), [0, 1, 3, 2]);
+      const v = c.vTransposed ? g.transpose(g.input(`vt${sfx}`, [B, H, DV, TK]), [0, 1, 3, 2]) : g.input(`v${sfx}`, [B, H, TK, DV]);
+      let s = g.matmul(q, kt);
+      if (c.scale) s = g.mul(s, g.const(c.scale));
+      if (c.mask) {
+        const m = [];
+        for (let i = 0; i < TQ; i++) for (let j = 0; j < TK; j++) m.push(j > i + (TK - TQ) ? -1e4 : 0);
+        s = g.add(s, g.const(m, [TQ, TK]));
+      }
+      return g.matmul(g.softmax(s, 3), v);
+    };
+    const keep = [one('')];
+    if (c.twice) keep.push(one('2'));
     const rng = new Rng(c.seed || 7);
     const inputs = {};
     for (const n of g.inputs()) inputs[n.attrs.name] = rng.array(size(n.shape), -2, 2);
-    return { name: c.name, fuses: c.fuses, graph: g.toJSON(), keep: [o], inputs };
+    return { name: c.name, fuses: c.fuses, graph: g.toJSON(), keep, inputs };
   });
 }
 
@@ -318,6 +324,7 @@ async function gpuGraphs(req, dir) {
       entry.perfFolded = lp.folded;
       entry.perfModes = lp.launches.filter((l) => l.flops && l.kind !== 'fused-attention').map(gemmModes);
       entry.perfViews = lp.launches.filter((l) => l.kind === 'fused-attention').map((l) => Object.keys(l.views || {}).sort());
+      entry.perfBatches = (lp.batches || []).map((x) => ({ count: x.count, kind: lp.launches[x.start].kind, kernels: x.kernels.map((k) => k.name) }));
       entry.canaryPerf = rp.canaryIntact.every(Boolean);
     }
     if (c.unfused) {

@@ -8,8 +8,9 @@ fused node is judged against the float64 oracle within the float32 budget (judge
 harness-m4.js:46-60), canaries must be intact, and the perf lowering's output must equal
 the plain one's bit for bit. Sizes cover the transformer's two head shapes, ragged
 query/key counts and head sizes (tile padding), head sizes that force per-element loads,
-more than one 64-row query block, keys and values given already transposed, and a key
-count past the kernel's limit that must stay three launches."""
+more than one 64-row query block, keys and values given already transposed, a key
+count past the kernel's limit that must stay three launches, and two independent
+attentions of one shape, which the perf lowering runs as one batched launch."""
 import sys
 
 import numpy as np
@@ -28,7 +29,8 @@ def _cases(tool, golden_cases):
         fw = tool("transformer-forward", {"config": config, "V": V, "B": B})
         reqs.append(({"name": f"transformer-{config}", "graph": fw["graph"], "inputs": fw["inputs"], "keep": fw["keep"]}, True))
     # The synthetic cases (tool.js ATTENTION_CASES): ragged sizes, per-element loads, several
-    # query blocks, pre-transposed keys and values, and one past the kernel's key limit.
+    # query blocks, pre-transposed keys and values, one past the kernel's key limit, and two
+    # independent attentions of one shape (a batched launch).
     for b in tool("attention-graphs"):
         fuses = b.pop("fuses")
         reqs.append((b, fuses))
@@ -67,6 +69,9 @@ def test_fused_attention_within_budget(tmp_path, tool, golden_cases):
         if req["name"] == "pre-transposed":
             # Kt is an input as it is; only V's transpose is read in place.
             assert c["perfViews"] == [["v"]], c["perfViews"]
+        if req["name"] == "twin":
+            # The two independent attentions run as one batched launch of the attention kernel.
+            assert [(x["count"], x["kind"]) for x in c["perfBatches"]] == [(2, "fused-attention")], c["perfBatches"]
         # The fused output against the contract's three launches: both within the budget of
         # the same reference; report how far apart they are.
         out_id = req["keep"][0]
