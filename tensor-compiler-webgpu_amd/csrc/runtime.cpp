@@ -651,26 +651,35 @@ int tcmi_graph_step(uint32_t count, const uint64_t* dst, const void* const* src,
   for (uint32_t i = 0; i < count; ++i) {
     if (bytes[i] && (!src[i] || !range_ok(dst[i], 0, bytes[i]))) return fail(TCMI_E_INVALID, "tcmi_graph_step: copy outside its allocation");
   }
+  // A failure after copies from the staging buffer were enqueued waits for the stream
+  // before returning, so that the next call cannot refill the buffer under them.
+  auto drained = [](hipError_t e, const char* what) {
+    const int rc = hip_fail(e, what);
+    (void)hipStreamSynchronize(g_stream);
+    return rc;
+  };
   // The uploads: small ones through the pinned staging buffer (one host memcpy, then a
   // DMA the stream runs without a pageable round trip), large ones directly.
+  hipError_t e;
   for (uint32_t i = 0; i < count; ++i) {
     if (!bytes[i]) continue;
     void* d = reinterpret_cast<void*>(dst[i]);
     const uint64_t b = bytes[i];
     if (b <= (kStageBytes >> 2) && staged + b <= kStageBytes - 4096) {
       std::memcpy(g_stage + staged, src[i], b);
-      HIP_TRY(hipMemcpyAsync(d, g_stage + staged, b, hipMemcpyHostToDevice, g_stream), "hipMemcpyAsync H2D (staged)");
+      if ((e = hipMemcpyAsync(d, g_stage + staged, b, hipMemcpyHostToDevice, g_stream)) != hipSuccess)
+        return drained(e, "hipMemcpyAsync H2D (staged)");
       staged += (b + 255) & ~uint64_t(255);
-    } else {
-      HIP_TRY(hipMemcpyAsync(d, src[i], b, hipMemcpyHostToDevice, g_stream), "hipMemcpyAsync H2D");
+    } else if ((e = hipMemcpyAsync(d, src[i], b, hipMemcpyHostToDevice, g_stream)) != hipSuccess) {
+      return drained(e, "hipMemcpyAsync H2D");
     }
   }
-  HIP_TRY(hipGraphLaunch(it->second.second, g_stream), "hipGraphLaunch");
+  if ((e = hipGraphLaunch(it->second.second, g_stream)) != hipSuccess) return drained(e, "hipGraphLaunch");
   // The result: through the last page of the staging buffer when it fits.
   char* back = out_bytes <= 4096 ? g_stage + kStageBytes - 4096 : static_cast<char*>(out);
-  if (out_bytes)
-    HIP_TRY(hipMemcpyAsync(back, reinterpret_cast<void*>(out_src), out_bytes, hipMemcpyDeviceToHost, g_stream),
-            "hipMemcpyAsync D2H");
+  if (out_bytes &&
+      (e = hipMemcpyAsync(back, reinterpret_cast<void*>(out_src), out_bytes, hipMemcpyDeviceToHost, g_stream)) != hipSuccess)
+    return drained(e, "hipMemcpyAsync D2H");
   HIP_TRY(hipStreamSynchronize(g_stream), "hipStreamSynchronize after the step");
   if (out_bytes && back != out) std::memcpy(out, back, out_bytes);
   return TCMI_OK;
