@@ -371,6 +371,13 @@ napi_value GraphStep(napi_env env, napi_callback_info info) {
   if (!a.bytes(0, &dsts, &nd) || a.argc < 2 || napi_is_array(env, a.argv[1], &is_array) != napi_ok || !is_array ||
       !a.u64(2, &graph) || !a.u64(3, &out_src) || !a.bytes(4, &out, &nout))
     return throw_type(env, "graphStep(dsts, srcs, graph, outSrc, out)");
+  // The destinations are device handles held as doubles: a Float64Array, nothing else.
+  napi_typedarray_type dtype;
+  size_t dlen, doff;
+  void* ddata;
+  napi_value dab;
+  if (napi_get_typedarray_info(env, a.argv[0], &dtype, &dlen, &ddata, &dab, &doff) != napi_ok || dtype != napi_float64_array)
+    return throw_type(env, "graphStep: destinations must be a Float64Array of handles");
   uint32_t count = 0;
   napi_get_array_length(env, a.argv[1], &count);
   if (nd != count * 8) return throw_type(env, "graphStep: one destination per source");

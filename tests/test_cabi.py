@@ -51,7 +51,11 @@ def test_node_addon_loads_and_exports():
           "'function','launch','launchMany','sync','eventCreate','eventRecord','eventElapsed','captureBegin','captureEnd',"
           "'graphLaunch','graphStep','launchDag','dagReserve','ceilingCopy','ceilingRead'];"
           "const miss=want.filter((k)=>typeof a[k]!=='function'); if(miss.length){console.log(miss.join());process.exit(2);}"
-          "try{a.malloc(16);process.exit(3);}catch(e){if(!/tcmi_init/.test(e.message))process.exit(4);}")
+          "try{a.malloc(16);process.exit(3);}catch(e){if(!/tcmi_init/.test(e.message))process.exit(4);}"
+          # graphStep reads its destinations as handles held in doubles: other arrays are refused
+          # before anything reaches the C ABI.
+          "try{a.graphStep(new Uint8Array(8),[new Float32Array(1)],1,0,new Float32Array(1));process.exit(5);}"
+          "catch(e){if(!/Float64Array/.test(e.message))process.exit(6);}")
     p = subprocess.run(["node", "-e", js, str(PKG / "lib" / "tcmi.node")], capture_output=True, text=True)
     assert p.returncode == 0, p.stdout + p.stderr
 
