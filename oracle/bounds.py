@@ -288,6 +288,11 @@ def local_reference_fused(graph, values):
     return expected, bound
 
 
+def _refused(node_id, node, reason, elements):
+    return {"pass": False, "unjudged": False, "worst": np.inf, "unjudgeable": 0, "elements": elements, "byKind": {},
+            "first": {"node": node_id, "op": node["op"], "pattern": node["attrs"].get("pattern"), "reason": reason}}
+
+
 def judge_local(graph, gpu, expected, bound):
     """Node-local judgement with the 1% unjudgeable rule (harness-m4.js:202-223)."""
     worst, first = 0.0, None
@@ -295,8 +300,15 @@ def judge_local(graph, gpu, expected, bound):
     by_kind: Dict[str, Dict[str, float]] = {}
     for node_id in sorted(expected):
         node = graph["nodes"][node_id]
-        g = np.asarray(gpu[node_id], dtype=np.float64)
         r, e = expected[node_id], bound[node_id]
+        # A launched node with no GPU value, or one of another length, fails outright
+        # (the reference indexes gpu[node.id][i] for every i; a missing or short array
+        # reads undefined, which never passes).
+        if node_id not in gpu:
+            return _refused(node_id, node, "missing", elements)
+        g = np.asarray(gpu[node_id], dtype=np.float64)
+        if g.size != r.size:
+            return _refused(node_id, node, "length", elements)
         kind = node["attrs"]["pattern"] if node["op"] == "fused" else "plain"
         k = by_kind.setdefault(kind, {"nodes": 0, "worst": 0.0})
         k["nodes"] += 1
@@ -321,8 +333,14 @@ def judge_outputs(values, bounds, gpu):
     """Outputs judged with the 1% unjudgeable rule (workloads.js:351-374)."""
     worst, first = 0.0, None
     unjudgeable = elements = 0
+    if len(gpu) != len(values) or len(bounds) != len(values):
+        return {"pass": False, "unjudged": False, "worst": np.inf, "unjudgeable": 0, "elements": 0,
+                "first": {"output": min(len(gpu), len(values)), "reason": "length"}}
     for k, (r, e, g) in enumerate(zip(values, bounds, gpu)):
         g = np.asarray(g, dtype=np.float64)
+        if g.size != r.size:
+            return {"pass": False, "unjudged": False, "worst": np.inf, "unjudgeable": unjudgeable,
+                    "elements": elements, "first": {"output": k, "reason": "length"}}
         elements += r.size
         bad = ~np.isfinite(r) | (np.abs(r) > F32_MAX) | ~np.isfinite(e)
         unjudgeable += int(np.count_nonzero(bad))

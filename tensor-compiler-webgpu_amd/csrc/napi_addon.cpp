@@ -110,6 +110,16 @@ struct Args {
     if (is) return napi_get_buffer_info(env, v, data, length) == napi_ok;
     return false;
   }
+  // A TypedArray of exactly `want`: its data and element count.
+  bool typed(size_t i, napi_typedarray_type want, void** data, size_t* count) {
+    bool is = false;
+    if (i >= argc || napi_is_typedarray(env, argv[i], &is) != napi_ok || !is) return false;
+    napi_typedarray_type type;
+    napi_value ab;
+    size_t off;
+    if (napi_get_typedarray_info(env, argv[i], &type, count, data, &ab, &off) != napi_ok) return false;
+    return type == want;
+  }
   // An array of three unsigned 32-bit numbers.
   bool dim3(size_t i, uint32_t out[3]) {
     bool is = false;
@@ -312,47 +322,62 @@ napi_value Launch(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+// A device or function handle held in a double: a whole number in [0, 2^53).
+bool handle_ok(double h) { return h >= 0 && h <= 9007199254740991.0 && std::floor(h) == h; }
+
+// Function handles of a Float64Array, each checked before the cast.
+bool handles(const double* F, size_t count, std::vector<uint64_t>& out) {
+  out.resize(count);
+  for (size_t i = 0; i < count; i++) {
+    if (!handle_ok(F[i])) return false;
+    out[i] = static_cast<uint64_t>(F[i]);
+  }
+  return true;
+}
+
 // launchMany(fns: Float64Array, dims: Uint32Array (7 per launch: grid xyz, block xyz, lds),
 //            args: Uint8Array, offsets: Uint32Array (n + 1)): one native call per launch sequence.
 napi_value LaunchMany(napi_env env, napi_callback_info info) {
   Args a(env, info);
   void *fns, *dims, *args, *offs;
-  size_t nf, nd, na, no;
-  if (!a.bytes(0, &fns, &nf) || !a.bytes(1, &dims, &nd) || !a.bytes(2, &args, &na) || !a.bytes(3, &offs, &no))
-    return throw_type(env, "launchMany(fns, dims, args, offsets)");
-  size_t count = nf / 8;
-  if (nd != count * 7 * 4 || no != (count + 1) * 4) return throw_type(env, "launchMany: array lengths disagree");
-  const double* F = static_cast<const double*>(fns);
+  size_t count, nd, na, no;
+  if (!a.typed(0, napi_float64_array, &fns, &count) || !a.typed(1, napi_uint32_array, &dims, &nd) ||
+      !a.bytes(2, &args, &na) || !a.typed(3, napi_uint32_array, &offs, &no))
+    return throw_type(env, "launchMany(fns: Float64Array, dims: Uint32Array, args, offsets: Uint32Array)");
+  if (nd != count * 7 || no != count + 1) return throw_type(env, "launchMany: array lengths disagree");
+  std::vector<uint64_t> F;
+  if (!handles(static_cast<const double*>(fns), count, F)) return throw_type(env, "launchMany: bad function handle");
   const uint32_t* D = static_cast<const uint32_t*>(dims);
   const uint32_t* O = static_cast<const uint32_t*>(offs);
   const uint8_t* A = static_cast<const uint8_t*>(args);
-  for (size_t i = 0; i < count; i++) {
+  for (size_t i = 0; i < count; i++)
     if (O[i] > O[i + 1] || O[i + 1] > na) return throw_type(env, "launchMany: bad argument offsets");
-    CHECK(tcmi_launch(static_cast<uint64_t>(F[i]), D + 7 * i, D + 7 * i + 3, D[7 * i + 6], A + O[i], O[i + 1] - O[i]),
-          "tcmi_launch");
-  }
+  for (size_t i = 0; i < count; i++)
+    CHECK(tcmi_launch(F[i], D + 7 * i, D + 7 * i + 3, D[7 * i + 6], A + O[i], O[i + 1] - O[i]), "tcmi_launch");
   return undef(env);
 }
 
-// launchDag(fns, dims, args, offsets, streams, streamOf: Uint8Array, recordEvent: Int32Array,
-//           waitBegin: Uint32Array (n + 1), waits: Uint32Array): a launch list over several streams.
+// launchDag(fns: Float64Array, dims: Uint32Array, args, offsets: Uint32Array, streams,
+//           streamOf: Uint8Array, recordEvent: Int32Array, waitBegin: Uint32Array (n + 1),
+//           waits: Uint32Array): a launch list over several streams.
 napi_value LaunchDag(napi_env env, napi_callback_info info) {
   Args a(env, info);
   void *fns, *dims, *args, *offs, *sof, *rec, *wb, *ws;
-  size_t nf, nd, na, no, ns, nr, nwb, nw;
+  size_t count, nd, na, no, ns, nr, nwb, nw;
   uint32_t streams;
-  if (!a.bytes(0, &fns, &nf) || !a.bytes(1, &dims, &nd) || !a.bytes(2, &args, &na) || !a.bytes(3, &offs, &no) ||
-      !a.u32(4, &streams) || !a.bytes(5, &sof, &ns) || !a.bytes(6, &rec, &nr) || !a.bytes(7, &wb, &nwb) ||
-      !a.bytes(8, &ws, &nw))
-    return throw_type(env, "launchDag(fns, dims, args, offsets, streams, streamOf, recordEvent, waitBegin, waits)");
-  size_t count = nf / 8;
-  if (nd != count * 7 * 4 || no != (count + 1) * 4 || ns != count || nr != count * 4 || nwb != (count + 1) * 4)
+  if (!a.typed(0, napi_float64_array, &fns, &count) || !a.typed(1, napi_uint32_array, &dims, &nd) ||
+      !a.bytes(2, &args, &na) || !a.typed(3, napi_uint32_array, &offs, &no) || !a.u32(4, &streams) ||
+      !a.typed(5, napi_uint8_array, &sof, &ns) || !a.typed(6, napi_int32_array, &rec, &nr) ||
+      !a.typed(7, napi_uint32_array, &wb, &nwb) || !a.typed(8, napi_uint32_array, &ws, &nw))
+    return throw_type(env, "launchDag(fns: Float64Array, dims: Uint32Array, args, offsets: Uint32Array, streams, "
+                           "streamOf: Uint8Array, recordEvent: Int32Array, waitBegin: Uint32Array, waits: Uint32Array)");
+  if (nd != count * 7 || no != count + 1 || ns != count || nr != count || nwb != count + 1)
     return throw_type(env, "launchDag: array lengths disagree");
   const uint32_t* O = static_cast<const uint32_t*>(offs);
   const uint32_t* WB = static_cast<const uint32_t*>(wb);
-  if (count && (O[count] > na || WB[count] > nw / 4)) return throw_type(env, "launchDag: offsets past the arrays");
-  std::vector<uint64_t> F(count);
-  for (size_t i = 0; i < count; i++) F[i] = static_cast<uint64_t>(static_cast<const double*>(fns)[i]);
+  if (O[count] > na || WB[count] > nw) return throw_type(env, "launchDag: offsets past the arrays");
+  std::vector<uint64_t> F;
+  if (!handles(static_cast<const double*>(fns), count, F)) return throw_type(env, "launchDag: bad function handle");
   CHECK(tcmi_launch_dag(static_cast<uint32_t>(count), F.data(), static_cast<const uint32_t*>(dims),
                         static_cast<const uint8_t*>(args), O, streams, static_cast<const uint8_t*>(sof),
                         static_cast<const int32_t*>(rec), WB, static_cast<const uint32_t*>(ws)),
@@ -385,7 +410,7 @@ napi_value GraphStep(napi_env env, napi_callback_info info) {
   std::vector<const void*> src(count);
   for (uint32_t i = 0; i < count; ++i) {
     double h = static_cast<const double*>(dsts)[i];
-    if (!(h >= 0) || h > 9007199254740991.0 || std::floor(h) != h) return throw_type(env, "graphStep: bad destination handle");
+    if (!handle_ok(h)) return throw_type(env, "graphStep: bad destination handle");
     dst[i] = static_cast<uint64_t>(h);
     napi_value el;
     void* data;

@@ -55,7 +55,20 @@ def test_node_addon_loads_and_exports():
           # graphStep reads its destinations as handles held in doubles: other arrays are refused
           # before anything reaches the C ABI.
           "try{a.graphStep(new Uint8Array(8),[new Float32Array(1)],1,0,new Float32Array(1));process.exit(5);}"
-          "catch(e){if(!/Float64Array/.test(e.message))process.exit(6);}")
+          "catch(e){if(!/Float64Array/.test(e.message))process.exit(6);}"
+          # launchMany and launchDag take function handles only as a Float64Array of whole
+          # numbers, dims/offsets only as Uint32Arrays: NaN, negative or fractional handles
+          # and reinterpretable arrays of the right byte length are refused the same way.
+          "const U=(n)=>new Uint32Array(n);"
+          "const many=[[new Float32Array(2),U(7),new Uint8Array(0),U(2)],[new Float64Array([NaN]),U(7),new Uint8Array(0),U(2)],"
+          "[new Float64Array([-1]),U(7),new Uint8Array(0),U(2)],[new Float64Array([1.5]),U(7),new Uint8Array(0),U(2)],"
+          "[new Float64Array(1),new Float32Array(7),new Uint8Array(0),U(2)],[new Float64Array(1),U(7),new Uint8Array(0),new Int32Array(2)]];"
+          "for(const [i,m] of many.entries()){try{a.launchMany(...m);console.log('many',i);process.exit(7);}"
+          "catch(e){if(!/launchMany/.test(e.message)||/tcmi_init/.test(e.message)){console.log('many',i,e.message);process.exit(8);}}}"
+          "const dag=(f,d)=>[f,d,new Uint8Array(0),U(2),1,new Uint8Array(1),new Int32Array(1),U(2),U(0)];"
+          "for(const [i,m] of [dag(new Float64Array([NaN]),U(7)),dag(new Float64Array([2**60]),U(7)),dag(new Float64Array(1),new Int32Array(7)),"
+          "dag(new BigUint64Array(1),U(7))].entries()){try{a.launchDag(...m);console.log('dag',i);process.exit(9);}"
+          "catch(e){if(!/launchDag/.test(e.message)||/tcmi_init/.test(e.message)){console.log('dag',i,e.message);process.exit(10);}}}")
     p = subprocess.run(["node", "-e", js, str(PKG / "lib" / "tcmi.node")], capture_output=True, text=True)
     assert p.returncode == 0, p.stdout + p.stderr
 
