@@ -26,6 +26,7 @@ transformer init logits/gradients of golden/torch-m3b.f64 within 1e-10.
 """
 from __future__ import annotations
 
+import contextlib
 import math
 from typing import Callable, Dict, List, Optional, Sequence
 
@@ -75,6 +76,28 @@ def k_max(x: np.ndarray, in_shape, axis) -> np.ndarray:
     return acc.reshape(-1)
 
 
+# Products with at least this many multiply-adds go to the BLAS (float64, its own
+# summation order) inside a `blas_matmul()` block; everything else, and every product
+# outside such a block, accumulates p = 0..K-1 as the reference does.
+_BLAS_FROM: Optional[int] = None
+
+
+@contextlib.contextmanager
+def blas_matmul(min_macs: int = 1 << 22):
+    """Within the block, large products are summed in the BLAS's order instead of p
+    ascending. Two orders of a float64 sum of K products differ by at most
+    2*gamma64(K) * sum|a||b| (gamma64(K) = K*2^-53 / (1 - K*2^-53)), about 1e-9 of the
+    float32 budget's gamma32(K) * sum|a||b| term; tests/test_oracle_golden.py pins
+    the difference to that bound and the golden cases to 1e-12 under it. For the
+    full-size training steps, whose products an ordered sum takes minutes to form."""
+    global _BLAS_FROM
+    prev, _BLAS_FROM = _BLAS_FROM, int(min_macs)
+    try:
+        yield
+    finally:
+        _BLAS_FROM = prev
+
+
 def k_matmul(a: np.ndarray, b: np.ndarray, a_shape, b_shape, rows: Optional[np.ndarray] = None) -> np.ndarray:
     """Batched matmul, p ascending from 0 per output; `rows` restricts to a subset of output rows."""
     m, k, n = int(a_shape[-2]), int(a_shape[-1]), int(b_shape[-1])
@@ -83,6 +106,8 @@ def k_matmul(a: np.ndarray, b: np.ndarray, a_shape, b_shape, rows: Optional[np.n
     B = b.reshape(batch, k, n)
     if rows is not None:
         A = A[:, rows, :]
+    if _BLAS_FROM is not None and batch * A.shape[1] * k * n >= _BLAS_FROM:
+        return np.matmul(A, B).reshape(-1)
     acc = np.zeros((batch, A.shape[1], n), dtype=np.float64)
     for p in range(k):
         acc = acc + A[:, :, p:p + 1] * B[:, p:p + 1, :]

@@ -19,8 +19,10 @@
 // GPU commands write a bundle (manifest.json + data.f32) under --out:
 //   gpu-direct       request {sabotage?}: every direct case, fused, canary-padded, on the GPU
 //   gpu-graphs       request {graphs: [{name, graph, inputs, keep, unfused?, perf?}]} fused (and unfused, and in the perf lowering) on the GPU
-//   gpu-fuzz         request {from, to}: the reference's corpus programs, fused / perf / unfused, on the GPU
+//   gpu-fuzz         request {from, to, recompute?}: the reference's corpus programs, fused / perf / unfused, on the GPU
 //   gpu-configs      request {c3: [...], c4: [...], unfused} configs 3 and 4, kept outputs as oracle-computable slices
+//   gpu-workloads    request {ids?, families?, allNodes?}: the workload sweep's variants run once, outputs for the gate
+//   gpu-step-slices  request {model, B, sequences}: a full-batch step's launches with their operands, as per-sequence blocks
 
 const fs = require('fs');
 const fs_ = fs;
@@ -234,6 +236,25 @@ function precompileGroup(group, arch, shard, shards) {
         lists.push(lowerMI355X(f.graph), lowerMI355X(f.graph, { perf: true, keep: keep.map((id) => f.index.get(id)) }));
       }
       lists.push(lowerMI355X(graph, { perf: true, keep }));
+    }
+    return precompile(lists, arch);
+  }
+  if (group === 'recompute') {
+    // The recompute GPU tests: corpus programs 1..100 fused with recomputation (plain and
+    // perf lowerings), and the fusion-loses workloads' fused and recompute variants in the
+    // plain lowering (their perf lowerings are the sweep group's).
+    const { corpusGraphs } = require('../src/testing/random_graph');
+    const { workloads } = require('../src/builders/workloads');
+    const lists = [];
+    for (let i = 1; i <= 100; i++) {
+      for (const c of corpusGraphs(i)) {
+        const f = fuse(c.graph, { keep: c.keep, recompute: true });
+        lists.push(lowerMI355X(f.graph), lowerMI355X(f.graph, { perf: true, keep: c.keep.map((id) => f.index.get(id)) }));
+      }
+    }
+    for (const w of workloads().filter((x) => x.variants.includes('recompute'))) {
+      const m = w.make();
+      for (const recompute of [false, true]) lists.push(lowerMI355X(fuse(m.graph, { keep: m.outputs, recompute }).graph));
     }
     return precompile(lists, arch);
   }
@@ -526,7 +547,7 @@ async function gpuFuzz(req, dir) {
     for (const c of corpusGraphs(i)) {
       const inputs = {}, ins = {};
       for (const name of Object.keys(c.inputs)) { inputs[name] = Float32Array.from(c.inputs[name]); ins[name] = bundle.put(inputs[name]); }
-      const f = fuse(c.graph, { keep: c.keep });
+      const f = fuse(c.graph, { keep: c.keep, recompute: !!req.recompute });
       const keepF = c.keep.map((id) => f.index.get(id));
       const rf = await runner.run(f.graph, lowerMI355X(f.graph), inputs, { canary: true });
       const rp = await runner.run(f.graph, lowerMI355X(f.graph, { perf: true, keep: keepF }), inputs, { canary: true });
@@ -541,7 +562,57 @@ async function gpuFuzz(req, dir) {
     }
     if (i % 100 === 0) process.stderr.write(`gpu-fuzz: program ${i}\n`);
   }
-  bundle.close({ device: runner.info(), from: req.from, to: req.to });
+  bundle.close({ device: runner.info(), from: req.from, to: req.to, recompute: !!req.recompute });
+}
+
+/**
+ * The reference's workload sweep (src/fusion/workloads.js:71-120) run once on the GPU
+ * in the lowerings the bench times, for the checker (workloads.js:351-374: every
+ * variant's outputs against the streamed float64 reference before it may be timed).
+ * Per workload: the graph, its inputs, and per variant (unfused, fused, recompute; the
+ * step's matmul-only variant is the fused variant's matmul launches and has no outputs
+ * of its own) the kept outputs and the canary verdict. With `allNodes`, the fused and
+ * recompute variants are also run in the plain lowering with every surviving node
+ * returned, with the fused graph and its origin map (judgeFused, harness-m4.js:46-60).
+ * Request: { ids?: [workload id...] (default all), families?: [...], allNodes? }.
+ */
+async function gpuWorkloads(req, dir) {
+  const { workloads } = require('../src/builders/workloads');
+  const { HipRunner } = require('../src/mi355x/runner');
+  const runner = HipRunner.create();
+  const bundle = new Bundle(dir);
+  const want = (w) => (!req.ids || req.ids.includes(w.id)) && (!req.families || req.families.includes(w.family));
+  for (const w of workloads().filter(want)) {
+    process.stderr.write(`gpu-workloads: ${w.id}\n`);
+    const m = w.make();
+    const ins = {};
+    for (const k of Object.keys(m.inputs)) ins[k] = bundle.put(m.inputs[k]);
+    const entry = { id: w.id, family: w.family, params: w.params, graph: m.graph.toJSON(), outputs: m.outputs, inputs: ins,
+      variants: {} };
+    for (const v of w.variants.filter((x) => x !== 'matmul-only')) {
+      let graph = m.graph, keep = m.outputs, f = null;
+      if (v !== 'unfused') {
+        f = fuse(m.graph, { keep: m.outputs, recompute: v === 'recompute' });
+        graph = f.graph;
+        keep = m.outputs.map((id) => f.index.get(id));
+      }
+      const lp = lowerMI355X(graph, { perf: true, keep });
+      const r = await runner.run(graph, lp, m.inputs, { canary: true });
+      const out = { outputs: keep.map((id) => bundle.put(r.values[id])), canary: r.canaryIntact.every(Boolean),
+        launches: lp.launches.length, kinds: lp.launches.map((l) => l.kind) };
+      if (req.allNodes && f) {
+        const lf = lowerMI355X(graph);
+        const rf = await runner.run(graph, lf, m.inputs, { canary: true });
+        out.fused = graph.toJSON();
+        out.origin = f.origin;
+        out.nodes = graph.nodes.map((n) => bundle.put(rf.values[n.id]));
+        out.canaryPlain = rf.canaryIntact.every(Boolean);
+      }
+      entry.variants[v] = out;
+    }
+    bundle.add(entry);
+  }
+  bundle.close({ device: runner.info() });
 }
 
 /**
@@ -574,6 +645,19 @@ async function gpuChains(req, dir) {
         entry.unfused = {};
         for (const id of v.keep) entry.unfused[id] = bundle.put(ru.values[id]);
         entry.canaryUnfused = ru.canaryIntact.every(Boolean);
+      }
+      if (req.perf) {
+        // The lowerings the bench times: broadcasts read in place by their consumers,
+        // dead launches dropped; the kernel names are the ones a profile of the bench shows.
+        const fk = v.keep.map((id) => f.index.get(id));
+        for (const [key, g, keep] of [['fusedPerf', f.graph, fk], ['unfusedPerf', v.graph, v.keep]]) {
+          const lp = lowerMI355X(g, { perf: true, keep });
+          const rp = await runner.run(g, lp, inputs, { canary: true });
+          entry[key] = {};
+          v.keep.forEach((id, k) => { entry[key][id] = bundle.put(rp.values[keep[k]]); });
+          entry[`${key}Canary`] = rp.canaryIntact.every(Boolean);
+          entry[`${key}Kernels`] = [].concat(...lp.launches.map((l) => l.kernels.map((x) => x.name)));
+        }
       }
       bundle.add(entry);
     }
@@ -698,6 +782,102 @@ async function gpuConcurrent(req) {
   }
   for (const p of programs) p.destroy();
   return out;
+}
+
+/**
+ * The batch axis of a node: the one dimension where its shape at the full batch differs
+ * from its shape in the one-sequence twin graph (the same builder at B = 1), or -1 for
+ * a node whose shape does not depend on the batch (parameters, their gradients and
+ * updates, the loss).
+ */
+function batchAxis(full, twin) {
+  const diff = [];
+  for (let d = 0; d < full.length; d++) if (full[d] !== twin[d]) diff.push(d);
+  if (full.length !== twin.length || diff.length > 1) throw new Error(`shapes ${full} / ${twin}: not one batch axis`);
+  return diff.length ? diff[0] : -1;
+}
+
+/** Block `b` (of size twin[p]) along axis p of a row-major array of shape `shape`. */
+function takeBlock(a, shape, p, q, b) {
+  let outer = 1, inner = 1;
+  for (let d = 0; d < p; d++) outer *= shape[d];
+  for (let d = p + 1; d < shape.length; d++) inner *= shape[d];
+  const span = q * inner, slab = shape[p] * inner;
+  const out = new Float32Array(outer * span);
+  for (let o = 0; o < outer; o++) out.set(a.subarray(o * slab + b * span, o * slab + (b + 1) * span), o * span);
+  return out;
+}
+
+/**
+ * A training step at its full batch, judged node-locally on the GPU's own operands
+ * (the check of harness-m4.js:182-223 with every launch's operands taken from one
+ * run of the checked lowering instead of the float64 reference, so that no full-size
+ * float64 evaluation of the step is needed). The checked lowering (one launch per
+ * node) runs once with canaries and every node is read back; the trainer's perf
+ * lowering (split-K weight gradients, batched dispatches, read-in-place transposes)
+ * then runs node-locally on those values. The bundle holds, for the checker:
+ *  - per launched node whose shape carries the batch: its block for each sampled
+ *    sequence, and the same blocks of its operands (a sequence's rows depend only on
+ *    that sequence's operand rows and on the parameters);
+ *  - per launched node whose shape does not (weight and bias gradients and their SGD
+ *    updates, the loss): its whole value and its operands' whole values;
+ *  - the fused graph at the full batch and its one-sequence twin (shapes of a block).
+ * Request: { model, B, sequences: [b...], batchIndex? }.
+ */
+async function gpuStepSlices(req, dir) {
+  const { modelStep } = require('../src/builders/models');
+  const { fusedStep } = require('../src/mi355x/trainer');
+  const { HipRunner } = require('../src/mi355x/runner');
+  const m = modelStep(req);
+  const fs = fusedStep(m.step);
+  const twin = fusedStep(modelStep(Object.assign({}, req, { B: 1 })).step);
+  if (!sameStructure(fs.graph, twin.graph)) throw new Error('the one-sequence twin differs in structure');
+  const nodes = fs.graph.nodes;
+  const axis = nodes.map((n, i) => batchAxis(n.shape, twin.graph.nodes[i].shape));
+  const B = req.B;
+  const seqs = req.sequences;
+  for (const b of seqs) if (!(b >= 0 && b < B)) throw new Error(`sequence ${b} outside the batch`);
+  const runner = HipRunner.create();
+  const batch = m.batch(req.batchIndex || 0);
+  const feed = Object.assign({}, m.params, m.state, { x: batch.x, y: batch.y });
+  feed[fs.cotangent] = [1];
+  process.stderr.write(`gpu-step-slices: checked lowering, ${fs.checked.launches.length} launches, every node read back\n`);
+  const r = await runner.run(fs.graph, fs.checked, feed, { canary: true });
+  process.stderr.write(`gpu-step-slices: perf lowering node-local, ${fs.lowered.launches.length} launches\n`);
+  const perf = await runner.runLocal(fs.graph, fs.lowered, r.values, { canary: true });
+  const bundle = new Bundle(dir);
+  // What each launched node needs: blocks (batch-carrying output) or whole values.
+  const wantBlocks = new Set(), wantWhole = new Set();
+  const launched = fs.checked.launches.map((l) => l.node);
+  for (const id of launched) {
+    if (axis[id] >= 0) {
+      wantBlocks.add(id);
+      for (const i of nodes[id].inputs) (axis[i] >= 0 ? wantBlocks : wantWhole).add(i);
+    } else {
+      wantWhole.add(id);
+      for (const i of nodes[id].inputs) wantWhole.add(i);
+    }
+  }
+  const put = (a, id) => {
+    const entry = {};
+    if (wantWhole.has(id)) entry.whole = bundle.put(a);
+    if (wantBlocks.has(id)) {
+      const q = twin.graph.nodes[id].shape[axis[id]];
+      entry.blocks = seqs.map((b) => bundle.put(takeBlock(a, nodes[id].shape, axis[id], q, b)));
+    }
+    return entry;
+  };
+  const values = {}, perfOut = {};
+  for (let id = 0; id < nodes.length; id++) if (wantBlocks.has(id) || wantWhole.has(id)) values[id] = put(r.values[id], id);
+  for (const l of fs.lowered.launches) perfOut[l.node] = put(perf[l.node], l.node);
+  bundle.add({ name: `${req.model}-B${B}`, graph: fs.graph.toJSON(), twin: twin.graph.toJSON(), axis, sequences: seqs,
+    launched, perfLaunched: fs.lowered.launches.map((l) => l.node), values, perf: perfOut,
+    canaryChecked: r.canaryIntact.every(Boolean),
+    canaryPerf: fs.lowered.launches.every((l) => perf.canaryIntact[l.node]),
+    loss: r.values[fs.loss][0], dispatchKinds: fs.lowered.launches.map((l) => l.kind),
+    splitK: fs.lowered.launches.filter((l) => { const k = gemmSplit(l); return k && k[0] > 1; }).length,
+    batches: (fs.lowered.batches || []).length, aliases: fs.lowered.aliases, folded: fs.lowered.folded, dead: fs.lowered.dead });
+  bundle.close({ device: runner.info() });
 }
 
 async function gpuTrain(req) {
@@ -1059,6 +1239,8 @@ async function main() {
     case 'gpu-direct': await gpuDirect(outDir(argv), req); out = { ok: true }; break;
     case 'step-graph': stepGraph(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-local': await gpuLocal(req, outDir(argv)); out = { ok: true }; break;
+    case 'gpu-workloads': await gpuWorkloads(req, outDir(argv)); out = { ok: true }; break;
+    case 'gpu-step-slices': await gpuStepSlices(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-train': out = await gpuTrain(req); break;
     case 'gpu-concurrent': out = await gpuConcurrent(req); break;
     case 'gpu-chains': await gpuChains(req, outDir(argv)); out = { ok: true }; break;

@@ -87,7 +87,10 @@ class Bundle:
     def __init__(self, directory):
         self.dir = pathlib.Path(directory)
         self.manifest = json.loads((self.dir / "manifest.json").read_text())
-        self.data = np.fromfile(self.dir / "data.f32", dtype=np.float32)
+        # Mapped, not read: a full-size training step's bundle holds gigabytes.
+        path = self.dir / "data.f32"
+        self.data = (np.memmap(path, dtype=np.float32, mode="r") if path.stat().st_size
+                     else np.zeros(0, dtype=np.float32))
 
     def arr(self, at) -> np.ndarray:
         return self.data[at["offset"]: at["offset"] + at["n"]]

@@ -71,9 +71,12 @@ def test_c5_structure_step_node_local(tool, tmp_path):
     node_local(tool, tmp_path, {"model": "transformer", "B": 1})
 
 
-def test_c1_first_step_against_composed_budget(tool):
+@pytest.mark.parametrize("graph,arena", [(False, False), (False, True), (True, True)])
+def test_c1_first_step_against_composed_budget(tool, graph, arena):
     """Step 0 of the fused trainer: loss and every new parameter within the composed budget
-    of the whole step graph (inputs float32-rounded, bounds propagated node by node)."""
+    of the whole step graph (inputs float32-rounded, bounds propagated node by node). With
+    `arena`, the step's intermediate buffers share one allocation by live range; with
+    `graph`, the step is the replay of a captured HIP graph."""
     import tcmi_bridge
     import tempfile
     with tempfile.TemporaryDirectory() as d:
@@ -81,7 +84,8 @@ def test_c1_first_step_against_composed_budget(tool):
         b = tcmi_bridge.Bundle(d)
         c = b.cases[0]
         inputs = {k: b.arr(v) for k, v in c["inputs"].items()}
-    r = tool("gpu-train", {"model": "mlp", "steps": 1, "returnParams": True})
+    r = tool("gpu-train", {"model": "mlp", "steps": 1, "returnParams": True, "graph": graph, "arena": arena})
+    assert (r["arena"] is not None) == arena
     ref = bounds.reference_with_bounds(c["graph"], inputs)
     ids = [c["loss"]] + [c["outputs"][k] for k in r["params"]]
     gpu = [np.array([r["losses"][0]])] + [np.asarray(r["params"][k]) for k in r["params"]]

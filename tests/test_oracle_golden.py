@@ -233,3 +233,34 @@ def test_transformer_init_matches_torch_m3b(tool):
     assert abs(vals[t["loss"]][0] - meta["loss"]) <= 1e-10 * abs(meta["loss"])
     for name, gid in zip(t["names"], t["grads"]):
         assert tensor_error(vals[gid], ten(f"grad/{name}")) <= 1e-10, name
+
+
+def test_blas_matmul_block_stays_within_the_order_bound(golden_cases):
+    """interp.blas_matmul(): the large products of the full-size training steps summed in
+    the BLAS's order. Against the ordered sum, each element differs by at most
+    2*gamma64(K)*sum|a||b| (two float64 orders of one sum, each within gamma64(K) of the
+    exact value), and every golden case still matches torch float64 at 1e-12 with
+    every product sent to the BLAS."""
+    rng = np.random.default_rng(17)
+    u64 = 2.0 ** -53
+    for (bt, m, k, n) in [(1, 3, 1, 5), (1, 17, 7, 9), (2, 64, 256, 96), (1, 128, 1024, 64), (4, 32, 4096, 8)]:
+        a = rng.normal(size=bt * m * k) * rng.choice([1e-3, 1, 1e3], size=bt * m * k)
+        b = rng.normal(size=bt * k * n)
+        sa, sb = ([bt, m, k] if bt > 1 else [m, k]), ([bt, k, n] if bt > 1 else [k, n])
+        ordered = interp.k_matmul(a, b, sa, sb)
+        with interp.blas_matmul(0):
+            fast = interp.k_matmul(a, b, sa, sb)
+        mass = interp.k_matmul(np.abs(a), np.abs(b), sa, sb)
+        g = k * u64 / (1 - k * u64)
+        assert np.all(np.abs(fast - ordered) <= 2 * g * mass), (bt, m, k, n)
+        # The ordered sum really is p ascending: equal to an explicit loop on one element.
+        A, B = a.reshape(bt, m, k), b.reshape(bt, k, n)
+        acc = 0.0
+        for p in range(k):
+            acc = acc + A[-1, -1, p] * B[-1, p, -1]
+        assert ordered[-1] == acc
+    with interp.blas_matmul(0):
+        for c in golden_cases:
+            vals = interp.evaluate(c["graph"], c["inputs"])
+            for j, out in enumerate(c["outputs"]):
+                assert tensor_error(vals[out], c["torchOutputs"][j]) <= TOL, (c["name"], j)
