@@ -376,6 +376,17 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
   }
 }
 
+// Output element j of a split-K matmul's product: its chunks' partial sums from the
+// workspace, added in chunk order — the value gemm_splitk_reduce forms for j itself.
+// An epilogue that reads the product at another element's index (a recomputed
+// broadcast or transpose of it) reads it here.
+template <class Args>
+__device__ __forceinline__ float gemm_product_at(const Args& A, uint32_t j, uint32_t total, uint32_t chunks) {
+  float acc = A.ws[j];
+  for (uint32_t c = 1; c < chunks; ++c) acc += A.ws[(size_t)c * total + j];
+  return acc;
+}
+
 // The second half of a split-K matmul: out[i] = Epi(A, i, Σ_chunk ws[chunk·total + i]),
 // the chunks summed in order; `total` = batch·M·N. Four outputs per thread when N % 4 == 0.
 template <bool VEC, class Epi, class Args>

@@ -9,7 +9,7 @@
 //   builder-cases    the hand-built graphs of the reference's exported cases
 //   grad             request {cases: [{name, graph, outputs}]} -> gradient graphs
 //   fuse             request {graphs: [{name, graph, keep, recompute?, sabotage?}]} -> fused graphs
-//   lower            request {graph, fuse?: {keep}} -> launch records (sources omitted)
+//   lower            request {graph, fuse?: {keep, recompute?}, sources?} -> launch records
 //   model-fusion     fusion summaries of the reference's transformer forward pass and Adam step
 //   direct-catalogue the direct adversarial cases: names, kinds, patterns, and what fuse() makes of each
 //   transformer-init the reference transformer (golden config) forward + gradient graph and its inputs
@@ -287,7 +287,8 @@ function gemmModes(l) {
 
 /** The K split (chunks, chunk length) of a matmul launch's kernel, or null. */
 function gemmSplit(l) {
-  const m = l.kernels[0].source.match(/(\d+)u, (\d+)u\);\s*}\s*$/);
+  // gemm_f32<...>(A, a, b, batch, M, K, N, chunks, chunkK, zid)
+  const m = l.kernels[0].source.match(/(\d+)u, (\d+)u, blockIdx\.z\);/);
   return l.flops && m ? [Number(m[1]), Number(m[2])] : null;
 }
 
@@ -875,7 +876,7 @@ async function gpuStepSlices(req, dir) {
     canaryChecked: r.canaryIntact.every(Boolean),
     canaryPerf: fs.lowered.launches.every((l) => perf.canaryIntact[l.node]),
     loss: r.values[fs.loss][0], dispatchKinds: fs.lowered.launches.map((l) => l.kind),
-    splitK: fs.lowered.launches.filter((l) => { const k = gemmSplit(l); return k && k[0] > 1; }).length,
+    splitK: fs.lowered.launches.filter((l) => l.kernels.some((k) => /_red$/.test(k.name))).length,
     batches: (fs.lowered.batches || []).length, aliases: fs.lowered.aliases, folded: fs.lowered.folded, dead: fs.lowered.dead });
   bundle.close({ device: runner.info() });
 }
@@ -957,7 +958,7 @@ async function main() {
       break;
     case 'lower': {
       const g = Graph.fromJSON(req.graph);
-      const target = req.fuse ? fuse(g, { keep: req.fuse.keep || [] }).graph : g;
+      const target = req.fuse ? fuse(g, { keep: req.fuse.keep || [], recompute: !!req.fuse.recompute }).graph : g;
       const l = lowerMI355X(target, { sabotage: req.sabotage });
       out = { workspace: l.workspace, launches: l.launches.map((x) => Object.assign({}, x, { params: Array.from(x.params),
         kernels: x.kernels.map((k) => ({ name: k.name, grid: k.grid, block: k.block, lds: k.lds, source: req.sources ? k.source : undefined })) })) };

@@ -755,8 +755,24 @@ function gemmKernel(b, output, opts) {
     const add = b.nodes.find((n) => n.op === 'add' && n.inputs.includes(root.id) && !n.inputs.every((i) => i === root.id));
     if (add && add.id !== output) biasAdd = add;
   }
+  const tl = gemmTiling(batch, M, N, K, o.tuning);
+  const total = batch * M * N;
+  // A group formed with recomputation may read its matmul through a broadcast or
+  // transpose, at another element's index than the one being stored. The product
+  // is then formed in the workspace first (the split-K path, with one chunk if the
+  // shape asks for none) and the second kernel reads element j's sum there, the
+  // chunks added in order: the bits the reduction forms for j itself.
+  let gathered = false;
   const em = new Emitter(b, params, {
-    special: (id) => (id === root.id || (biasAdd && id === biasAdd.id) ? 'acc' : undefined),
+    special: (id, ctx, lines) => {
+      if (biasAdd && id === biasAdd.id) return 'acc';
+      if (id !== root.id) return undefined;
+      if (ctx.root) return 'acc';
+      gathered = true;
+      const v = em.fresh('m');
+      lines.push(`const float ${v} = tcmi::gemm_product_at(A, ${ctx.idx}, ${total}u, ${tl.chunks}u);`);
+      return v;
+    },
     load(k, ctx, lines) {
       const v = `L${lines.length}_${k}`;
       lines.push(`const float ${v} = A.in[${k}][${ctx.idx}];`);
@@ -764,7 +780,7 @@ function gemmKernel(b, output, opts) {
     },
   });
   const lines = [];
-  const rootCtx = { key: 'i', idx: 'i', root: true, limit: batch * M * N };
+  const rootCtx = { key: 'i', idx: 'i', root: true, limit: total };
   let out = em.value(output, rootCtx, lines);
   if (biasAdd) {
     const other = biasAdd.inputs.find((i) => i !== root.id);
@@ -775,13 +791,11 @@ function gemmKernel(b, output, opts) {
   }
   const av = operandView('__KERNEL___av', views.a, batchDims, M, K);
   const bv = operandView('__KERNEL___bv', views.b, bs.slice(0, -2), K, N);
-  const tl = gemmTiling(batch, M, N, K, o.tuning);
   const T = tl.T;
-  const split = tl.chunks > 1;
+  const split = tl.chunks > 1 || gathered;
   const sizes = o.sizes || {};
   const need = { a: sizes.a !== undefined ? sizes.a : batch * M * K, b: sizes.b !== undefined ? sizes.b : batch * K * N };
   if (av.limit > need.a || bv.limit > need.b) throw new Error(`matmul operand view out of bounds (${av.limit}/${need.a}, ${bv.limit}/${need.b})`);
-  const total = batch * M * N;
   const epi = `struct __KERNEL___epi {
   template <class Args>
   __device__ __forceinline__ float operator()(const Args& A, uint32_t i, float acc) const {

@@ -245,6 +245,8 @@ def test_perf_lowering_views_address_the_operands(tool, req):
     if req["model"] != "mlp":
         assert checked > 10
     # Every matmul splits K exactly as in the plain lowering (the same order of the K sum).
+    splits = [l["split"] for l in d["launches"] if l["split"] is not None]
+    assert splits, "no matmul's K split was read from its kernel"
     for l in d["launches"]:
         assert l["split"] == l["plainSplit"], (l["node"], l["split"], l["plainSplit"])
 
@@ -258,6 +260,9 @@ def test_perf_lowering_keeps_the_split_of_config4_backward(tool):
         d = tool("perf-lower", {"graph": g["gradient"]["graph"], "keep": g["gradient"]["keep"]})
         nodes = d["graph"]["nodes"]
         assert sum(nodes[i]["op"] == "transpose" for i in d["folded"]) == 2   # transpose(W), transpose(X)
+        # Only the weight gradient over M = 8192 rows (a long K for few output tiles) splits.
+        chunks = sorted(l["split"][0] for l in d["launches"] if l["split"] is not None)
+        assert chunks == ([1, 1, 4] if g["M"] == 8192 else [1, 1, 1]), (g["M"], chunks)
         for l in d["launches"]:
             assert l["split"] == l["plainSplit"], (g["M"], g["K"], g["N"], l["node"])
 
@@ -297,3 +302,30 @@ def test_attention_fusion_leaves_training_steps_and_golden_cases_alone(golden_ca
     for c, f in zip(golden_cases, fused):
         assert "error" not in f, (c["name"], f.get("error"))
         assert _semantics(c["graph"], f["graph"], f["origin"], c["inputs"]), c["name"]
+
+
+def test_recomputed_epilogue_reads_its_product_through_the_workspace(tool):
+    """A group formed with recomputation can reach its matmul through a transpose
+    (x·w, scaled, transposed, added to a residual): the store of element i needs the
+    product at another index, which the epilogue's accumulator does not hold. The
+    lowering forms the product in the workspace first (the split-K form, one chunk) and
+    the second kernel reads element j's sum there; the plain matmul of the same shape
+    keeps its one-kernel form. (Corpus program 89's gradient has such a group; the GPU
+    test of recomputed corpus programs judges it.)"""
+    def inp(name, shape):
+        return {"op": "input", "inputs": [], "attrs": {"name": name, "shape": shape}, "shape": shape}
+    g = {"nodes": [inp("x", [2, 4, 4]), inp("w", [2, 4, 2]), inp("s", [2, 4, 2]), inp("r", [2, 4, 2]),
+                   {"op": "matmul", "inputs": [0, 1], "attrs": {}, "shape": [2, 4, 2]},
+                   {"op": "mul", "inputs": [4, 2], "attrs": {}, "shape": [2, 4, 2]},
+                   {"op": "transpose", "inputs": [5], "attrs": {"perm": [2, 1, 0]}, "shape": [2, 4, 2]},
+                   {"op": "add", "inputs": [3, 6], "attrs": {}, "shape": [2, 4, 2]}]}
+    plain = tool("lower", {"graph": g, "fuse": {"keep": [7]}, "sources": True})
+    rec = tool("lower", {"graph": g, "fuse": {"keep": [7], "recompute": True}, "sources": True})
+    # Without recomputation the transpose is a load of a stored product.
+    assert [l["kind"] for l in plain["launches"]] == ["fused-epilogue", "fused-elementwise"]
+    assert all("gemm_product_at" not in k["source"] for l in plain["launches"] for k in l["kernels"])
+    (epi,) = [l for l in rec["launches"] if l["kind"] == "fused-epilogue"]
+    assert len(rec["launches"]) == 1 and len(epi["kernels"]) == 2
+    part, red = epi["kernels"]
+    assert ", true, " in part["source"] and "gemm_product_at" in red["source"] and red["name"].endswith("_red")
+    assert rec["workspace"] >= 2 * 4 * 2 * 4
