@@ -84,6 +84,126 @@ def cpu_baseline(rows: int, seeds, min_seconds: float = 10.0) -> dict:
             "seconds": secs}
 
 
+def _timed(fn, min_seconds: float):
+    """Repeat fn() until at least `min_seconds` have passed (at least once): (runs, seconds)."""
+    runs = 0
+    t0 = time.perf_counter()
+    while runs == 0 or time.perf_counter() - t0 < min_seconds:
+        fn()
+        runs += 1
+    return runs, time.perf_counter() - t0
+
+
+def _where() -> str:
+    return f"{cpu_model()} ({os.cpu_count()} cores visible, 1 used)"
+
+
+def cpu_baselines(quick: bool) -> dict:
+    """The float64 oracle interpreter (numpy, vectorised over whole tensors, one thread;
+    matmuls sum p = 0..K-1 in order as src/interp.js:67-84 does) on each other config,
+    next to its GPU figure, in the GPU figure's unit. Bounded samples, labelled:
+    C1 the whole step; C3 every program at a row subset; C4 each shape's forward at a row
+    subset; C5 the step at a reduced batch; the rates are extrapolated linearly (work is
+    linear in rows and in batch)."""
+    import numpy as np
+    import tcmi_bridge
+    import tempfile
+    from oracle import interp
+    rng = np.random.default_rng(2024)
+    out = {}
+    budget = 0.2 if quick else 3.0
+    # C1: the MLP training step, whole.
+    with tempfile.TemporaryDirectory() as d:
+        tcmi_bridge.node_tool("step-graph", {"model": "mlp"}, out=d, echo_stderr=False)
+        b = tcmi_bridge.Bundle(d)
+        c = b.cases[0]
+        ins = {k: np.array(b.arr(v)) for k, v in c["inputs"].items()}
+    runs, secs = _timed(lambda: interp.evaluate(c["graph"], ins), budget)
+    out["c1"] = {"value": runs / secs, "unit": "steps/s", "cores": 1, "kind": "port",
+                 "sample": f"the whole step graph ({len(c['graph']['nodes'])} nodes), {runs} runs in {secs:.1f} s on {_where()}"}
+    # C3: softmax / logSoftmax forward and backward at R rows of 16384 (rows are independent).
+    R, C = (64 if quick else 1024), 4096
+    graphs = tcmi_bridge.node_tool("config-graphs", {"c3": [{"fn": f, "R": R, "C": C} for f in ("softmax", "logSoftmax")]})["c3"]
+    x = (rng.standard_normal(R * C) * 2).astype(np.float32)
+    x[: R * C // 100] += 800
+    dy = rng.standard_normal(R * C).astype(np.float32)
+    nbytes = 0
+    def c3():
+        nonlocal nbytes
+        for g in graphs:
+            interp.evaluate(g["forward"]["graph"], {"x": x})
+            interp.evaluate(g["gradient"]["graph"], {"x": x, "d0": dy})
+            # The fused programs' algorithmic bytes: forward reads x, writes y; backward
+            # reads x and dy, writes y and dx (as the GPU figure counts them).
+            nbytes += (2 + 4) * R * C * 4
+    runs, secs = _timed(c3, budget)
+    out["c3"] = {"value": nbytes / secs / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                 "sample": f"softmax and logSoftmax forward+backward at [{R},{C}] ({R}/16384 of the rows), {runs} pass(es), "
+                           f"{secs:.1f} s on {_where()}"}
+    # C4: each shape's forward (matmul + bias -> relu) at a row subset of M.
+    out["c4"] = {}
+    for (M, K, N) in ((512, 512, 512), (4096, 4096, 4096), (8192, 1024, 4096)):
+        rows = 4 if quick else max(8, 2 ** 20 // K // 8)
+        g = tcmi_bridge.node_tool("config-graphs", {"c4": [{"act": "relu", "M": rows, "K": K, "N": N}]})["c4"][0]
+        feed = {"X": (rng.standard_normal(rows * K) / np.sqrt(K)).astype(np.float32),
+                "W": (rng.standard_normal(K * N) / np.sqrt(K)).astype(np.float32),
+                "bias": (rng.standard_normal(N) * np.sqrt(0.1)).astype(np.float32)}
+        runs, secs = _timed(lambda: interp.evaluate(g["forward"]["graph"], feed), budget / 3)
+        out["c4"][f"{M}x{K}x{N}"] = {"value": 2 * rows * K * N * runs / secs / 1e12, "unit": "TFLOP/s", "cores": 1,
+                                     "kind": "port", "sample": f"forward at {rows} of {M} rows (extrapolated: work is linear "
+                                                               f"in rows), {runs} run(s), {secs:.1f} s on {_where()}"}
+    # C5: the transformer step at batch 1 of 64.
+    Bc = 1
+    with tempfile.TemporaryDirectory() as d:
+        tcmi_bridge.node_tool("step-graph", {"model": "transformer", "B": Bc}, out=d, echo_stderr=False)
+        b = tcmi_bridge.Bundle(d)
+        c = b.cases[0]
+        ins = {k: np.array(b.arr(v)) for k, v in c["inputs"].items()}
+    runs, secs = _timed(lambda: interp.evaluate(c["graph"], ins), 0.0 if quick else budget)
+    out["c5"] = {"value": runs / secs * Bc / 64, "unit": "steps/s", "cores": 1, "kind": "port",
+                 "sample": f"the step graph at batch {Bc} of 64 (extrapolated: work is linear in the batch), {runs} run(s) "
+                           f"in {secs:.1f} s on {_where()}"}
+    return out
+
+
+def sweep_gate(out_dir: pathlib.Path) -> dict:
+    """The sweep's correctness gate (src/fusion/workloads.js:351-374 there): every workload
+    of the reference's sweep, each variant run once on the GPU in the lowering the bench
+    times, its outputs judged against the streamed float64 oracle within the float32
+    budget, canaries intact. Returns {workload id: {pass, variants: {v: {pass, worst}}}};
+    the bench times only the workloads that pass."""
+    import numpy as np
+    import tcmi_bridge
+    from oracle import bounds, interp
+    tcmi_bridge.node_tool("gpu-workloads", {}, out=str(out_dir), timeout=900, echo_stderr=False)
+    b = tcmi_bridge.Bundle(out_dir)
+    gate = {}
+    for c in b.cases:
+        outs = {v: [np.asarray(b.arr(x)) for x in r["outputs"]] for v, r in c["variants"].items()}
+        variants = {}
+        if c["judge"] == "composed":
+            ins = {k: b.arr(v) for k, v in c["inputs"].items()}
+            with interp.blas_matmul():
+                ref = bounds.streaming_reference(c["graph"], ins, c["outputs"])
+            vals = [ref[i][0] for i in c["outputs"]]
+            bnds = [ref[i][1] for i in c["outputs"]]
+            for v, r in c["variants"].items():
+                j = bounds.judge_outputs(vals, bnds, outs[v])
+                variants[v] = {"pass": bool(j["pass"] and r["canary"]), "worst": j["worst"]}
+        else:
+            # The model workloads (the reference's revision R6): the composed bound is
+            # vacuous at the logits, so the fused outputs are compared with the unfused ones
+            # and every variant must be finite; the largest difference is recorded. (Their
+            # kernels are judged node by node against the oracle by the GPU tests.)
+            base = outs["unfused"]
+            for v, r in c["variants"].items():
+                finite = all(bool(np.all(np.isfinite(x))) for x in outs[v])
+                diff = max(float(np.max(np.abs(x.astype(np.float64) - y))) for x, y in zip(outs[v], base))
+                variants[v] = {"pass": bool(finite and r["canary"]), "max_abs_diff_vs_unfused": diff}
+        gate[c["id"]] = {"pass": all(x["pass"] for x in variants.values()), "judge": c["judge"], "variants": variants}
+    return gate
+
+
 def profiled_traffic(kernel: str):
     """HBM bytes per launch of `kernel` from a committed rocprofv3 --pmc summary
     (profiles/*.md, the json block profile_summary.py writes: {"traffic_bytes_per_launch":
@@ -112,105 +232,149 @@ def main() -> None:
     ap.add_argument("--programs", type=int, default=8)
     ap.add_argument("--quick", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-gate", action="store_true", help="time the sweep without its correctness gate")
     ap.add_argument("--out", default=None, help="also write the full measurement JSON here")
     a = ap.parse_args()
     if a.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported", file=sys.stderr)
+        print(f"bench.py: this build measures one GPU (every GPU box here has one); --gpus {a.gpus} is not supported",
+              file=sys.stderr)
         sys.exit(2)
+    import tempfile
+    work = pathlib.Path(tempfile.mkdtemp(prefix="tcmi-bench-"))
     cmd = ["node", str(PKG / "js" / "cli" / "bench.js"), "--configs", a.configs, "--steps", str(a.steps),
            "--warmup", str(a.warmup), "--programs", str(a.programs)]
     if a.quick:
         cmd.append("--quick")
+    gate = None
+    if "sweep" in a.configs.split(",") and not a.no_gate:
+        print("bench.py: sweep gate (every workload variant once, judged against the float64 oracle)", file=sys.stderr,
+              flush=True)
+        gate = sweep_gate(work / "gate")
+        (work / "gate.json").write_text(json.dumps(gate))
+        cmd += ["--gate", str(work / "gate.json")]
     p = subprocess.run(cmd, stdout=subprocess.PIPE)
     if p.returncode != 0:
         print(f"bench.py: node bench exited {p.returncode}", file=sys.stderr)
         sys.exit(p.returncode)
     full = json.loads(p.stdout)
-    if a.out:
-        pathlib.Path(a.out).write_text(json.dumps(full, indent=1))
+    if gate is not None:
+        full["gate"] = gate
     line = compose(full)
     if not a.no_cpu:
+        print("bench.py: CPU baselines", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(8192 if not a.quick else 256, range(min(a.programs, 8)), 0.0 if a.quick else 10.0)
-    print(json.dumps(line))
+        full["cpu_baselines"] = cpu_baselines(a.quick)
+        attach_cpu(line, full["cpu_baselines"])
+    if a.out:
+        pathlib.Path(a.out).write_text(json.dumps(full, indent=1))
+    import shutil
+    shutil.rmtree(work, ignore_errors=True)
+    print(json.dumps(line, separators=(",", ":")))
+
+
+def _r(x, n=3):
+    return None if x is None else float(f"{x:.{n}g}")
+
+
+def attach_cpu(line: dict, cpu: dict) -> None:
+    """Each config's CPU baseline beside its GPU figure in the line."""
+    e = line["extra"]
+    if "c1" in e:
+        e["c1"]["cpu_steps_s"] = _r(cpu["c1"]["value"])
+    if "c3" in e:
+        e["c3"]["cpu_GBs"] = _r(cpu["c3"]["value"])
+    if "c4" in e:
+        for shape, v in cpu["c4"].items():
+            if shape in e["c4"]:
+                e["c4"][shape]["cpu_TFLOPs"] = _r(v["value"])
+    if "c5" in e:
+        e["c5"]["cpu_steps_s"] = _r(cpu["c5"]["value"])
+    e["cpu"] = {"kind": "port", "cores": 1, "model": cpu_model(),
+                "samples": {k: (v["sample"] if "sample" in v else {s: x["sample"] for s, x in v.items()}) for k, v in cpu.items()}}
+
+
+def _groups(g: dict) -> dict:
+    """win / loss / noise counts over a config's fusion groups, and its worst group."""
+    if not g:
+        return None
+    w = g.get("worst") or {}
+    return {"n": g["groups"], "win": g["win"], "loss": g["loss"], "noise": g["noise"],
+            "worst": {"pattern": w.get("pattern"), "speedup": _r(w.get("speedup")), "verdict": w.get("verdict")} if w else None}
 
 
 def compose(full: dict) -> dict:
-    """The driver's one-line record from bench.js's measurement document (everything but
-    the CPU baseline, which this process times itself)."""
+    """The driver's one-line record from bench.js's measurement document: the contract's
+    fields, then a compact `extra` with every config's figures (the full document goes to
+    --out), small enough that the driver's output tail holds all of it."""
     cfg = full["configs"]
     c2 = cfg.get("c2")
-    extra = {}
-    if "c3" in cfg:
-        c3 = cfg["c3"]
-        extra["rowwise_c3"] = {"GBs": c3["gbs"], "frac_hbm": c3["gbs"] / HBM_PEAK,
-                               "dominant": {k: c3["dominant"][k] for k in ("code", "pattern", "avgUs", "gbs")},
-                               "programs": {r["name"]: {"fused_us": r["fused"]["median"], "unfused_us": r["unfused"]["median"],
-                                                        "speedup": r["verdict"]["speedup"], "verdict": r["verdict"]["verdict"],
-                                                        "GBs": r["gbs"]["fused"]} for r in c3["results"]}}
-    if "c4" in cfg:
-        c4 = cfg["c4"]
-        extra["matmul_c4"] = {r["name"]: {"fused_us": r["fused"]["median"], "TFLOPs": (r["tflops"] or {}).get("fused"),
-                                          "frac_mfma": ((r["tflops"] or {}).get("fused") or 0) / MFMA_FP32_PEAK,
-                                          "speedup_vs_unfused": r["verdict"]["speedup"]} for r in c4["results"]}
-    for key, label in (("c1", "mlp_step_c1"), ("c5", "transformer_step_c5")):
-        if key in cfg:
-            t = cfg[key]
-            extra[label] = {"steps_per_sec": t["stepsPerSec"], "ms_per_step": t["msPerStep"], "hip_graph_replay": t["graphReplay"],
-                            "resident_steps_per_sec": t["residentStepsPerSec"], "resident_ms_per_step": t["residentMsPerStep"],
-                            "launches": t["launches"], "fused_us": t["fused"]["median"], "unfused_us": t["unfused"]["median"],
-                            "speedup_vs_unfused": t["verdict"]["speedup"], "matmul_TFLOPs_resident": t["matmulTflopsResident"],
-                            "loss": t["lossLast"], "time_by_kind_us": {k: round(v["us"], 1) for k, v in t["byKind"].items()},
-                            "arena": {"bytes": t["arena"]["bytes"], "unshared_bytes": t["arena"]["unshared"],
-                                      "steps_per_sec": t["arena"]["stepsPerSec"],
-                                      "resident_steps_per_sec": t["arena"]["residentStepsPerSec"]},
-                            "dispatches": t["dispatches"], "batched_launches": t["batches"],
-                            "unbatched": {"dispatches": t["unbatched"]["dispatches"],
-                                          "steps_per_sec": t["unbatched"]["stepsPerSec"],
-                                          "resident_steps_per_sec": t["unbatched"]["residentStepsPerSec"]}}
-    if "attention" in cfg:
-        extra["attention_extension"] = {
-            r["name"]: {"contract_us": r["contract"]["median"], "attention_us": r["attention"]["median"],
-                        "speedup": r["verdict"]["speedup"], "verdict": r["verdict"]["verdict"], "launches": r["launches"],
-                        "max_abs_diff_logits": r["maxAbsDiffLogits"],
-                        "kernel_us": sum(g["kernelUs"] for g in r["groups"]) / len(r["groups"]),
-                        "replaced_launches_us": sum(g["replacedUs"] for g in r["groups"]) / len(r["groups"]),
-                        "kernel_TFLOPs": sum(g["tflops"] for g in r["groups"]) / len(r["groups"])}
-            for r in cfg["attention"]["results"]}
-    if "sweep" in cfg:
-        sw = cfg["sweep"]
-        extra["workload_sweep"] = {
-            "workloads": len(sw["workloads"]), "families": sw["families"],
-            "fusion_loses_by_design": {r["id"]: {"fused_vs_unfused": round(r["fused"]["speedup"], 3), "verdict": r["fused"]["verdict"],
-                                                 **({"recompute_vs_fused": round(r["recompute"]["speedup"], 3),
-                                                     "recompute_verdict": r["recompute"]["verdict"]} if "recompute" in r else {})}
-                                       for r in sw["workloads"] if r["family"] in ("broadcast-recompute", "lost-reuse")}}
     if c2 is None:
         raise SystemExit("bench.py: the headline needs config c2")
-    dom = c2["dominant"]
-    extra["c2_programs"] = {r["name"]: {"fused_us": r["fused"]["median"], "unfused_us": r["unfused"]["median"],
-                                        "speedup": r["verdict"]["speedup"], "verdict": r["verdict"]["verdict"],
-                                        "GBs": r["gbs"]["fused"], "bitwise_same_outputs": r["bitwiseSameOutputs"]}
-                            for r in c2["results"]}
+    extra = {}
+    ceiling = cfg.get("ceiling")
+    if ceiling:
+        extra["ceiling_1GiB_GBs"] = {"copy": _r(ceiling["copy"]["gbs"], 4), "read": _r(ceiling["read"]["gbs"], 4)}
     seq = c2["schedule"].get("sequential")
-    if seq:
-        extra["c2_step_sequential"] = {"GBs": seq["gbs"], "ms_per_step": seq["msPerStep"],
-                                       "note": "every program after the previous on one stream"}
-    extra["device"] = {k: full["device"].get(k) for k in ("name", "arch", "computeUnits", "clockKHz", "totalMemory")}
-    if "ceiling" in cfg:
-        extra["ceiling_1GiB"] = {"copy_GBs": cfg["ceiling"]["copy"]["gbs"], "read_GBs": cfg["ceiling"]["read"]["gbs"]}
+    dom = c2["dominant"]
+    extra["c2"] = {"GBs_2streams": _r(c2["gbs"], 4), "GBs_sequential": _r(seq["gbs"], 4) if seq else None,
+                   "frac_sequential": _r(seq["gbs"] / HBM_PEAK) if seq else None,
+                   "roofline_kernel_cold_GBs": _r(dom["gbs"], 4), "roofline_kernel_warm_GBs": _r(dom["warm"]["gbs"], 4),
+                   "groups": _groups(c2.get("groups")),
+                   "programs_win": sum(r["verdict"]["verdict"] == "win" for r in c2["results"]),
+                   "programs": len(c2["results"])}
+    if "c3" in cfg:
+        c3 = cfg["c3"]
+        extra["c3"] = {"GBs": _r(c3["gbs"], 4), "frac": _r(c3["gbs"] / HBM_PEAK),
+                       "dominant": {"kernel": c3["dominant"]["code"], "GBs": _r(c3["dominant"]["gbs"], 4)},
+                       "speedups": {r["name"].replace("c3-", ""): _r(r["verdict"]["speedup"]) for r in c3["results"]},
+                       "groups": _groups(c3.get("groups"))}
+    if "c4" in cfg:
+        c4 = cfg["c4"]
+        shapes = {}
+        for r in c4["results"]:
+            _, shape, act, kind = r["name"].split("-")
+            t = (r["tflops"] or {}).get("fused")
+            e = shapes.setdefault(shape, {})
+            e[f"{act}_{'fwd' if kind == 'forward' else 'bwd'}_TFLOPs"] = _r(t)
+        for shape, e in shapes.items():
+            e["frac_fwd"] = _r(max(e.get("relu_fwd_TFLOPs") or 0, e.get("tanh_fwd_TFLOPs") or 0) / MFMA_FP32_PEAK)
+        extra["c4"] = shapes
+        extra["c4_groups"] = _groups(c4.get("groups"))
+    for key in ("c1", "c5"):
+        if key in cfg:
+            t = cfg[key]
+            extra[key] = {"steps_s": _r(t["stepsPerSec"], 4), "resident_steps_s": _r(t["residentStepsPerSec"], 4),
+                          "launches": t["launches"]["fused"], "dispatches": t["dispatches"],
+                          "speedup_vs_unfused": _r(t["verdict"]["speedup"]), "groups": _groups(t.get("groups")),
+                          "matmul_TFLOPs": _r(t["matmulTflopsResident"]), "arena_resident_steps_s": _r(t["arena"]["residentStepsPerSec"], 4)}
+    if "attention" in cfg:
+        extra["attention"] = {r["name"]: {"speedup": _r(r["verdict"]["speedup"]), "kernel_TFLOPs":
+                                          _r(sum(g["tflops"] for g in r["groups"]) / len(r["groups"]))}
+                              for r in cfg["attention"]["results"]}
+    if "sweep" in cfg:
+        sw = cfg["sweep"]
+        gate = full.get("gate")
+        extra["sweep"] = {"workloads": len(sw["workloads"]), "timed": sw["timedWorkloads"],
+                          "gate_pass": sum(bool(g["pass"]) for g in gate.values()) if gate else None,
+                          "families": {k: {"win": v.get("win", 0), "loss": v.get("loss", 0), "noise": v.get("noise", 0),
+                                           "median_speedup": _r(v["speedup"]["median"])} for k, v in sw["families"].items()},
+                          "fusion_loses": {r["id"]: _r(r["fused"]["speedup"]) for r in sw["workloads"]
+                                           if r.get("timed") and r["family"] in ("broadcast-recompute", "lost-reuse")}}
+    extra["timed_regions_checked"] = full.get("timedRegionsChecked")
+    extra["device"] = full["device"].get("name") or full["device"].get("arch")
     traffic, traffic_src = profiled_traffic(dom["code"])
+    read_ceiling = ceiling["read"]["gbs"] if ceiling else None
     line = {
         "metric": METRIC, "value": c2["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": c2["steps"], "warmup": c2["warmup"],
         "ms_per_step": c2["msPerStep"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
-        "config": {"workload": "C2: fused elementwise chains, seeded programs of 8-16 ops (forward + autodiff gradient) "
-                               "over fp32 [8192,1024] with a [1024] row broadcast",
+        "config": {"workload": "C2 fused elementwise chains fwd+grad, fp32 [8192,1024]",
                    "programs": c2["programs"], "shape": c2["shape"], "step_bytes": c2["stepBytes"],
-                   "schedule": f"the {2 * c2['programs']} independent programs issued over {c2['schedule']['streams']} "
-                               "streams, balanced by bytes"},
+                   "streams": c2["schedule"]["streams"]},
         "roofline": {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK, "unit": "GB/s", "frac": dom["gbs"] / HBM_PEAK,
                      "traffic": traffic, "traffic_source": traffic_src, "kernel": dom["code"], "kernel_avg_us": dom["avgUs"],
-                     "bytes_per_launch": dom["bytesPerLaunch"], "launches_per_step": dom["count"]},
+                     "bytes_per_launch": dom["bytesPerLaunch"], "timing": "cold: operands read from HBM",
+                     "warm_achieved": dom["warm"]["gbs"], "read_ceiling": read_ceiling},
         "extra": extra,
     }
     return line

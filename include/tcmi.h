@@ -165,6 +165,24 @@ int tcmi_graph_step(uint32_t count, const uint64_t* dst, const void* const* src,
                     uint64_t out_src, void* out, uint64_t out_bytes);
 int tcmi_graph_destroy(uint64_t graph);
 
+/* --- counters (src/fusion/bench.js:41-47: every object-creating call and every write
+ * is counted, and the timed region must create none; DESIGN.md:1153-1162 there) ------ */
+
+/* Indices into the array tcmi_counters fills. Each counts successful calls since the
+ * library loaded: device allocations, frees, module loads (compiled or from the cache),
+ * host->device copies (tcmi_h2d and each upload of tcmi_graph_step), device->host
+ * copies, event creations, graph instantiations. */
+#define TCMI_COUNT_MALLOC 0
+#define TCMI_COUNT_FREE 1
+#define TCMI_COUNT_MODULE 2
+#define TCMI_COUNT_H2D 3
+#define TCMI_COUNT_D2H 4
+#define TCMI_COUNT_EVENT 5
+#define TCMI_COUNT_GRAPH 6
+#define TCMI_COUNTERS 7
+/* Copy min(n, TCMI_COUNTERS) counters into out; works before tcmi_init. */
+int tcmi_counters(uint64_t* out, uint32_t n);
+
 /* --- built-in measurement kernels (workloads.js:312-345 ceilingPrograms) ----- */
 
 /* dst[i] = src[i] over `bytes` (a multiple of 16), grid-strided, `blocks` x 256 threads. */

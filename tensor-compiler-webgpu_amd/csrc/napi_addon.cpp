@@ -517,6 +517,17 @@ napi_value CeilingRead(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+// counters(): { malloc, free, module, h2d, d2h, event, graph } since the library loaded.
+napi_value Counters(napi_env env, napi_callback_info) {
+  uint64_t c[TCMI_COUNTERS];
+  CHECK(tcmi_counters(c, TCMI_COUNTERS), "tcmi_counters");
+  static const char* names[TCMI_COUNTERS] = {"malloc", "free", "module", "h2d", "d2h", "event", "graph"};
+  napi_value o;
+  napi_create_object(env, &o);
+  for (int k = 0; k < TCMI_COUNTERS; ++k) napi_set_named_property(env, o, names[k], num(env, static_cast<double>(c[k])));
+  return o;
+}
+
 napi_value Register(napi_env env, napi_value exports) {
   struct {
     const char* name;
@@ -531,6 +542,7 @@ napi_value Register(napi_env env, napi_value exports) {
       {"eventRecord", EventRecord}, {"eventElapsed", EventElapsed}, {"eventDestroy", EventDestroy},
       {"captureBegin", CaptureBegin}, {"captureEnd", CaptureEnd}, {"graphLaunch", GraphLaunch}, {"graphStep", GraphStep},
       {"graphDestroy", GraphDestroy}, {"ceilingCopy", CeilingCopy}, {"ceilingRead", CeilingRead},
+      {"counters", Counters},
   };
   for (auto& f : fns) {
     napi_value fn;

@@ -67,6 +67,9 @@ std::unordered_map<uint64_t, hipFunction_t> g_functions;
 std::unordered_map<uint64_t, hipEvent_t> g_events;
 std::unordered_map<uint64_t, std::pair<hipGraph_t, hipGraphExec_t>> g_graphs;
 uint64_t g_next_handle = 1;
+// Calls that create objects or move data between host and device (tcmi_counters).
+std::atomic<uint64_t> g_count[TCMI_COUNTERS];
+inline void count(int k, uint64_t n = 1) { g_count[k].fetch_add(n, std::memory_order_relaxed); }
 
 // Options every kernel is compiled with. Packed fp32 instructions are turned
 // off (some of their forms have produced silent wrong results on MI355X), and floating
@@ -345,6 +348,7 @@ int tcmi_malloc(uint64_t bytes, uint64_t* handle) {
   HIP_TRY(hipMalloc(&p, bytes ? bytes : 4), "hipMalloc");
   g_allocs[reinterpret_cast<uint64_t>(p)] = bytes ? bytes : 4;
   *handle = reinterpret_cast<uint64_t>(p);
+  count(TCMI_COUNT_MALLOC);
   return TCMI_OK;
 }
 
@@ -357,6 +361,7 @@ int tcmi_free(uint64_t handle) {
   hipError_t e = hipStreamSynchronize(g_stream);
   if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize before free");
   HIP_TRY(hipFree(reinterpret_cast<void*>(handle)), "hipFree");
+  count(TCMI_COUNT_FREE);
   return TCMI_OK;
 }
 
@@ -374,6 +379,7 @@ int tcmi_h2d(uint64_t dst, uint64_t dst_offset, const void* src, uint64_t bytes)
   HIP_TRY(hipMemcpyAsync(reinterpret_cast<char*>(dst) + dst_offset, src, bytes, hipMemcpyHostToDevice, g_stream),
           "hipMemcpyAsync H2D");
   HIP_TRY(hipStreamSynchronize(g_stream), "hipStreamSynchronize after H2D");
+  count(TCMI_COUNT_H2D);
   return TCMI_OK;
 }
 
@@ -384,6 +390,7 @@ int tcmi_d2h(void* dst, uint64_t src, uint64_t src_offset, uint64_t bytes) {
   HIP_TRY(hipMemcpyAsync(dst, reinterpret_cast<char*>(src) + src_offset, bytes, hipMemcpyDeviceToHost, g_stream),
           "hipMemcpyAsync D2H");
   HIP_TRY(hipStreamSynchronize(g_stream), "hipStreamSynchronize after D2H");
+  count(TCMI_COUNT_D2H);
   return TCMI_OK;
 }
 
@@ -443,6 +450,7 @@ int tcmi_module_compile(const char* source, const char* extra_options, uint64_t*
   if (int rc = compile_code(source, extra_options ? extra_options : "", g_arch, code)) return rc;
   hipModule_t m;
   HIP_TRY(hipModuleLoadData(&m, code.data()), "hipModuleLoadData");
+  count(TCMI_COUNT_MODULE);
   uint64_t h = g_next_handle++;
   g_modules[h] = m;
   *module = h;
@@ -578,6 +586,7 @@ int tcmi_event_create(uint64_t* event) {
   if (int rc = ready()) return rc;
   hipEvent_t e;
   HIP_TRY(hipEventCreate(&e), "hipEventCreate");
+  count(TCMI_COUNT_EVENT);
   uint64_t h = g_next_handle++;
   g_events[h] = e;
   *event = h;
@@ -625,6 +634,7 @@ int tcmi_capture_end(uint64_t* graph) {
     (void)hipGraphDestroy(g);
     return hip_fail(e, "hipGraphInstantiate");
   }
+  count(TCMI_COUNT_GRAPH);
   uint64_t h = g_next_handle++;
   g_graphs[h] = {g, x};
   *graph = h;
@@ -682,6 +692,10 @@ int tcmi_graph_step(uint32_t count, const uint64_t* dst, const void* const* src,
     return drained(e, "hipMemcpyAsync D2H");
   HIP_TRY(hipStreamSynchronize(g_stream), "hipStreamSynchronize after the step");
   if (out_bytes && back != out) std::memcpy(out, back, out_bytes);
+  uint64_t uploads = 0;
+  for (uint32_t i = 0; i < count; ++i) uploads += bytes[i] != 0;
+  ::count(TCMI_COUNT_H2D, uploads);
+  if (out_bytes) ::count(TCMI_COUNT_D2H);
   return TCMI_OK;
 }
 
@@ -692,6 +706,12 @@ int tcmi_graph_destroy(uint64_t graph) {
   (void)hipGraphExecDestroy(it->second.second);
   (void)hipGraphDestroy(it->second.first);
   g_graphs.erase(it);
+  return TCMI_OK;
+}
+
+int tcmi_counters(uint64_t* out, uint32_t n) {
+  if (!out && n) return fail(TCMI_E_INVALID, "tcmi_counters: null output");
+  for (uint32_t k = 0; k < n && k < TCMI_COUNTERS; ++k) out[k] = g_count[k].load(std::memory_order_relaxed);
   return TCMI_OK;
 }
 

@@ -5,6 +5,7 @@
 //
 //   node bench.js [--configs ceiling,c2,c3,c4] [--steps K] [--warmup W] [--programs P]
 //                 [--reps N] [--c4-shapes all|small] [--quick] [--graphs] [--no-trainer-graphs] [--step-only]
+//                 [--roofline-only] [--gate FILE]
 //
 // --graphs: the c2 step's programs replayed as captured HIP graphs. The trainers
 // of c1 and c5 replay each step as a captured HIP graph by default (a step is
@@ -50,15 +51,55 @@ function prepared(runner, graph, lowered, inputs, opts) {
   return p;
 }
 
-/** Time every launch of `program` alone: ms per launch (median of a few repetitions). */
+/** Time every launch of `program` alone: µs per launch (median, min and max of a few repetitions). */
 function timeLaunches(runner, bench, program, reps) {
   const out = [];
   for (const l of program.lowered.launches) {
     const one = runner.prepare(program.graph, { launches: [l], workspace: program.lowered.workspace }, { buffers: program.bufs });
     const r = bench.time({ one }, { reps: reps || 5, warmup: 1, targetMs: 0.5, direct: true });
     out.push({ node: l.node, kind: l.kind, pattern: l.pattern || null, code: l.code, bytes: l.bytes, flops: l.flops,
-      us: r.stats.one.median });
+      us: r.stats.one.median, minUs: r.stats.one.min, maxUs: r.stats.one.max });
     one.destroy();
+  }
+  return out;
+}
+
+/**
+ * Fused against unfused for every fusion group of `f` (fuse.js:228 groups), including
+ * groups where fusion is neutral or slower: the group's fused launch timed alone against
+ * the summed times of its members' unfused launches, each timed alone. A group wins or
+ * loses only when the ranges do not overlap (the fused launch's min-max against the
+ * members' summed mins and maxes).
+ */
+function groupVerdicts(f, launchF, launchU) {
+  const fusedAt = new Map(launchF.map((l) => [l.node, l]));
+  const unfusedAt = new Map(launchU.map((l) => [l.node, l]));
+  const groups = [];
+  for (const g of f.groups) {
+    if (!f.index.has(g.sink)) continue;
+    const fl = fusedAt.get(f.index.get(g.sink));
+    if (!fl) continue;
+    const sum = { median: 0, min: 0, max: 0 };
+    let launches = 0;
+    for (const m of g.members) {
+      const u = unfusedAt.get(m);
+      if (!u) continue;
+      sum.median += u.us; sum.min += u.minUs; sum.max += u.maxUs; launches++;
+    }
+    if (!launches) continue;
+    const v = verdict(sum, { median: fl.us, min: fl.minUs, max: fl.maxUs });
+    groups.push({ sink: g.sink, kind: g.kind, pattern: g.pattern, members: g.members.size, unfusedLaunches: launches,
+      fusedUs: fl.us, unfusedUs: sum.median, speedup: v.speedup, verdict: v.verdict });
+  }
+  return groups;
+}
+
+/** Win / loss / noise counts of a list of group verdicts, with the worst (lowest speedup) group. */
+function groupSummary(groups) {
+  const out = { groups: groups.length, win: 0, loss: 0, noise: 0, worst: null };
+  for (const g of groups) {
+    out[g.verdict]++;
+    if (!out.worst || g.speedup < out.worst.speedup) out.worst = g;
   }
   return out;
 }
@@ -92,16 +133,7 @@ function measureGraph(runner, bench, name, graph, keep, inputs, opts) {
   const bytesF = lf.launches.reduce((s, l) => s + l.bytes, 0);
   const bytesU = lu.launches.reduce((s, l) => s + l.bytes, 0);
   const flops = lf.launches.reduce((s, l) => s + (l.flops || 0), 0);
-  const unfusedUs = new Map();
-  if (launchU) for (const l of launchU) unfusedUs.set(l.node, l.us);
-  const groups = f.groups.filter((g) => f.index.has(g.sink)).map((g) => {
-    const fusedLaunch = launchF.find((l) => l.node === f.index.get(g.sink));
-    let unfused = 0, count = 0;
-    for (const m of g.members) if (unfusedUs.has(m)) { unfused += unfusedUs.get(m); count++; }
-    return { sink: g.sink, kind: g.kind, pattern: g.pattern, members: g.members.size, unfusedLaunches: count,
-      fusedUs: fusedLaunch ? fusedLaunch.us : null, unfusedUs: launchU ? unfused : null,
-      speedup: launchU && fusedLaunch ? unfused / fusedLaunch.us : null };
-  });
+  const groups = launchU ? groupVerdicts(f, launchF, launchU) : [];
   const res = {
     name, launches: { fused: lf.launches.length, unfused: lu.launches.length }, k: t.k,
     fused: t.stats.fused, unfused: t.stats.unfused, verdict: verdict(t.stats.unfused, t.stats.fused),
@@ -137,6 +169,72 @@ function dominant(launches) {
     tflops: best.flops ? best.flops / best.count / (avgUs * 1e6) : null });
 }
 
+/** The fused kernel moving the most algorithmic bytes per step, from the lowerings alone (no timing). */
+function dominantByBytes(programs) {
+  const launches = [];
+  for (const p of programs) for (const l of p.launches) if (l.kind.startsWith('fused-')) launches.push(Object.assign({ us: 0 }, l));
+  const d = dominant(launches);
+  return d ? { code: d.code, kind: d.kind, pattern: d.pattern, count: d.count, bytes: d.bytes, bytesPerLaunch: d.bytes / d.count } : null;
+}
+
+const COLD_SETS = 8;
+
+/**
+ * Launch `l` of program `p` timed cold: COLD_SETS copies of every buffer it reads and
+ * writes, the launch issued on set i mod COLD_SETS, k launches back to back between two
+ * events, k chosen for >= 4 ms (or `runs` launches untimed, for a profiler). Returns the
+ * average µs per launch and the bytes the sets span.
+ */
+function coldLaunch(runner, bench, p, l, runs) {
+  const a = runner.a;
+  const ids = Array.from(new Set(l.inputs.concat([l.node])));
+  const sets = [];
+  let span = 0;
+  for (let s = 0; s < COLD_SETS; s++) {
+    const bufs = p.bufs.slice();
+    const owned = [];
+    for (const id of ids) {
+      const bytes = p.n[id] * 4;
+      const h = a.malloc(bytes);
+      a.d2d(h, 0, p.bufs[id], 0, bytes);
+      bufs[id] = h;
+      owned.push(h);
+      span += bytes;
+    }
+    const prog = runner.prepare(p.graph, { launches: [l], workspace: p.lowered.workspace }, { buffers: bufs });
+    sets.push({ prog, owned });
+  }
+  a.sync();
+  const issue = (k) => { for (let i = 0; i < k; i++) sets[i % COLD_SETS].prog.run(); };
+  let out;
+  if (runs) {
+    issue(runs);
+    a.sync();
+    out = { runs, sets: COLD_SETS, spanBytes: span };
+  } else {
+    issue(2 * COLD_SETS);
+    a.sync();
+    a.eventRecord(bench.start);
+    issue(COLD_SETS);
+    a.eventRecord(bench.end);
+    const one = a.eventElapsed(bench.start, bench.end) / COLD_SETS;
+    const k = Math.max(COLD_SETS, Math.ceil(4 / one / COLD_SETS) * COLD_SETS);
+    const reps = [];
+    bench.region(() => {
+      for (let r = 0; r < 9; r++) {
+        a.eventRecord(bench.start);
+        issue(k);
+        a.eventRecord(bench.end);
+        reps.push(a.eventElapsed(bench.start, bench.end) / k);
+      }
+    });
+    const st = summarize(reps);
+    out = { avgUs: st.median, minUs: st.min, maxUs: st.max, k, reps: reps.length, sets: COLD_SETS, spanBytes: span };
+  }
+  for (const s of sets) { s.prog.destroy(); for (const h of s.owned) a.free(h); }
+  return out;
+}
+
 // ---- configs -----------------------------------------------------------------------
 
 function c2(runner, bench, opts) {
@@ -145,7 +243,10 @@ function c2(runner, bench, opts) {
   const K = Number(arg('steps', 20)), W = Number(arg('warmup', 3));
   const programs = [];
   const results = [];
-  const stepOnly = flag('step-only');
+  // --roofline-only (for the profile behind `roofline`): the programs are built and only
+  // the roofline kernel's cold rotation runs, --warmup + --steps launches of it.
+  const rooflineOnly = flag('roofline-only');
+  const stepOnly = flag('step-only') || rooflineOnly;
   const arena = flag('arena');
   for (let s = 0; s < P; s++) {
     const w = chainWorkload(s, R, C);
@@ -171,6 +272,13 @@ function c2(runner, bench, opts) {
       results.push(r);
     }
   }
+  if (rooflineOnly) {
+    const dom = dominantByBytes(programs);
+    const p = programs.find((q) => q.launches.some((x) => x.code === dom.code));
+    dom.cold = coldLaunch(runner, bench, p, p.launches.find((x) => x.code === dom.code), W + K);
+    for (const q of programs) q.destroy();
+    return { config: 'c2', rooflineOnly: true, shape: [R, C], programs: P, dominant: dom, results };
+  }
   // The headline step: every fused program once; W warm-up steps, then K timed steps
   // bracketed by hipEvents. The 16 programs are independent (each its own buffers), so
   // the step issues them as one concurrent group over --c2-streams streams (default 2:
@@ -188,38 +296,47 @@ function c2(runner, bench, opts) {
     runner.a.sync();
     return { msPerStep: ms / K, wallMsPerStep: Number(process.hrtime.bigint() - t0) / 1e6 / K };
   };
+  const timeStepsChecked = (issue) => bench.region(() => timeSteps(issue));
   const go = bench.graphs ? (p) => p.replay() : (p) => p.run();
   for (const p of programs) if (bench.graphs) p.capture();
-  const sequential = timeSteps(() => { for (const p of programs) go(p); });
+  const sequential = timeStepsChecked(() => { for (const p of programs) go(p); });
   // Profiling mode runs the sequential step only, so each kernel's traced duration is its own.
   const S = Number(arg('c2-streams', 2));
   const group = stepOnly ? null : new Concurrent(runner, programs, S);
-  const headline = stepOnly ? sequential : timeSteps(() => group.run());
+  const headline = stepOnly ? sequential : timeStepsChecked(() => group.run());
   const ms = headline.msPerStep * K, wallMs = headline.wallMsPerStep * K;
   const stepBytes = results.reduce((s, r) => s + r.bytes.fused, 0);
   // The roofline kernel: the fused kernel moving the most algorithmic bytes per step,
   // chosen without timing so a profile of the same step names the same kernel (each
   // fused body is its own kernel, at one size, so its average is well defined). Its
   // duration: the launch alone in its own program's buffers, 21 repetitions' median.
-  const all = [].concat.apply([], results.map((r) => r.launchF)).filter((l) => l.kind.startsWith('fused-'));
+  const all = stepOnly ? [] : [].concat.apply([], results.map((r) => r.launchF)).filter((l) => l.kind.startsWith('fused-'));
   const dom = stepOnly ? null : dominant(all);
   if (dom) {
-    for (const p of programs) {
-      const l = p.launches.find((x) => x.code === dom.code);
-      if (!l) continue;
+    const p = programs.find((q) => q.launches.some((x) => x.code === dom.code));
+    const l = p.launches.find((x) => x.code === dom.code);
+    // Warm: the launch alone in its own program's buffers, repeated back to back (its
+    // 235 MB fit the 256 MB last-level cache, so repeats find operands cached).
+    {
       const one = runner.prepare(p.graph, { launches: [l], workspace: p.lowered.workspace }, { buffers: p.bufs });
       const t = bench.time({ one }, { reps: 21, warmup: 3, targetMs: 1, direct: true });
       one.destroy();
-      Object.assign(dom, { avgUs: t.stats.one.median, reps: 21 });
-      dom.gbs = dom.bytesPerLaunch / (dom.avgUs * 1e3);
-      break;
+      dom.warm = { avgUs: t.stats.one.median, gbs: dom.bytesPerLaunch / (t.stats.one.median * 1e3), reps: 21 };
     }
+    // Cold: the figure `roofline` reports. The launch rotates over COLD_SETS copies of its
+    // operands and output, so between two launches on one set the other sets' bytes
+    // (several times the last-level cache) have passed through it: every launch reads its
+    // operands from HBM.
+    dom.cold = coldLaunch(runner, bench, p, l, 0);
+    dom.avgUs = dom.cold.avgUs;
+    dom.gbs = dom.bytesPerLaunch / (dom.avgUs * 1e3);
   }
   for (const p of programs) p.destroy();
   sequential.gbs = stepBytes / (sequential.msPerStep * 1e6);
   const schedule = stepOnly ? { streams: 1 } : { streams: S, bytesPerStream: group.load, sequential };
+  const groups = groupSummary([].concat.apply([], results.map((r) => r.groups || [])));
   return { config: 'c2', shape: [R, C], programs: P, steps: K, warmup: W, arena, schedule, msPerStep: ms / K, wallMsPerStep: wallMs / K,
-    stepBytes, gbs: stepBytes / ((ms / K) * 1e6), dominant: dom, results };
+    stepBytes, gbs: stepBytes / ((ms / K) * 1e6), dominant: dom, groups, results };
 }
 
 /**
@@ -334,7 +451,8 @@ function c3(runner, bench, opts) {
   const all = [].concat.apply([], results.map((r) => r.launchF));
   const bytes = results.reduce((s, r) => s + r.bytes.fused, 0);
   const us = results.reduce((s, r) => s + r.fused.median, 0);
-  return { config: 'c3', shape: [R, C], shiftedRows: shifted.length, gbs: bytes / (us * 1e3), dominant: dominant(all), results };
+  return { config: 'c3', shape: [R, C], shiftedRows: shifted.length, gbs: bytes / (us * 1e3), dominant: dominant(all),
+    groups: groupSummary([].concat.apply([], results.map((r) => r.groups))), results };
 }
 
 function c4(runner, bench, opts) {
@@ -359,7 +477,7 @@ function c4(runner, bench, opts) {
   }
   if (flag('step-only')) return { config: 'c4', shapes, results };
   const mm = [].concat.apply([], results.map((r) => r.launchF)).filter((l) => l.flops);
-  return { config: 'c4', shapes, dominant: dominant(mm), results };
+  return { config: 'c4', shapes, dominant: dominant(mm), groups: groupSummary([].concat.apply([], results.map((r) => r.groups))), results };
 }
 
 /**
@@ -391,25 +509,33 @@ function trainStep(runner, bench, name, req, opts) {
       results: [{ name: `${name}-step`, launches: launchRecords(fs.lowered) }] };
   }
   for (let i = 0; i < W; i++) trainer.train(batch.x, batch.y);
+  // A step through train() uploads the batch and reads the loss back (trainer-fused.js:
+  // 59-81); it creates nothing. The batch-resident steps move no data at all.
+  const STEP_IO = ['h2d', 'd2h'];
   const t0 = process.hrtime.bigint();
   let loss = 0;
-  for (let i = 0; i < K; i++) loss = trainer.train(batch.x, batch.y);
+  bench.region(() => { for (let i = 0; i < K; i++) loss = trainer.train(batch.x, batch.y); }, STEP_IO);
   const wallMs = Number(process.hrtime.bigint() - t0) / 1e6 / K;
   // Batch resident: the steps' launches only, K steps between two events.
   runner.a.sync();
-  runner.a.eventRecord(bench.start);
-  for (let i = 0; i < K; i++) trainer.advance();
-  runner.a.eventRecord(bench.end);
+  const residentMs = bench.region(() => {
+    runner.a.eventRecord(bench.start);
+    for (let i = 0; i < K; i++) trainer.advance();
+    runner.a.eventRecord(bench.end);
+    return runner.a.eventElapsed(bench.start, bench.end) / K;
+  });
   const p = trainer.program;
-  const residentMs = runner.a.eventElapsed(bench.start, bench.end) / K;
   // Unfused step (same graph, no fusion), batch resident.
   const pu = runner.prepare(m.step.graph, lu);
   const all = Object.assign({}, m.params, m.state, { x: batch.x, y: batch.y });
   all[m.step.cotangent] = [1];
   for (const node of m.step.graph.nodes) if (node.op === 'input') pu.write(node.id, all[node.attrs.name]);
   const t = bench.time({ fused: p, unfused: pu }, { reps: opts.quick ? 3 : 8, warmup: 2 });
-  // Time by kind (each launch alone).
+  // Time by kind (each launch alone), and every fusion group against its members'
+  // unfused launches, each timed alone.
   const launches = timeLaunches(runner, bench, p, 3);
+  const launchesU = timeLaunches(runner, bench, pu, 3);
+  const groupList = groupVerdicts(fs.fusion, launches, launchesU);
   const byKind = {};
   for (const l of launches) {
     const e = byKind[l.kind] || (byKind[l.kind] = { launches: 0, us: 0, bytes: 0, flops: 0 });
@@ -426,13 +552,15 @@ function trainStep(runner, bench, name, req, opts) {
   const ta = new HipTrainer(runner, fs, m.params, m.state, { graph, arena: true });
   for (let i = 0; i < W; i++) ta.train(batch.x, batch.y);
   const ta0 = process.hrtime.bigint();
-  for (let i = 0; i < K; i++) ta.train(batch.x, batch.y);
+  bench.region(() => { for (let i = 0; i < K; i++) ta.train(batch.x, batch.y); }, STEP_IO);
   const arenaWallMs = Number(process.hrtime.bigint() - ta0) / 1e6 / K;
   runner.a.sync();
-  runner.a.eventRecord(bench.start);
-  for (let i = 0; i < K; i++) ta.advance();
-  runner.a.eventRecord(bench.end);
-  const arenaResidentMs = runner.a.eventElapsed(bench.start, bench.end) / K;
+  const arenaResidentMs = bench.region(() => {
+    runner.a.eventRecord(bench.start);
+    for (let i = 0; i < K; i++) ta.advance();
+    runner.a.eventRecord(bench.end);
+    return runner.a.eventElapsed(bench.start, bench.end) / K;
+  });
   const plan = ta.program.arena;
   const arena = { bytes: plan.size, unshared: plan.unshared, msPerStep: arenaWallMs, residentMsPerStep: arenaResidentMs,
     stepsPerSec: 1e3 / arenaWallMs, residentStepsPerSec: 1e3 / arenaResidentMs };
@@ -462,13 +590,15 @@ function trainStep(runner, bench, name, req, opts) {
   const tp = new HipTrainer(runner, fsPlain, m.params, m.state, { graph });
   for (let i = 0; i < W; i++) tp.train(batch.x, batch.y);
   const tp0 = process.hrtime.bigint();
-  for (let i = 0; i < K; i++) tp.train(batch.x, batch.y);
+  bench.region(() => { for (let i = 0; i < K; i++) tp.train(batch.x, batch.y); }, STEP_IO);
   const plainWall = Number(process.hrtime.bigint() - tp0) / 1e6 / K;
   runner.a.sync();
-  runner.a.eventRecord(bench.start);
-  for (let i = 0; i < K; i++) tp.advance();
-  runner.a.eventRecord(bench.end);
-  const plainResident = runner.a.eventElapsed(bench.start, bench.end) / K;
+  const plainResident = bench.region(() => {
+    runner.a.eventRecord(bench.start);
+    for (let i = 0; i < K; i++) tp.advance();
+    runner.a.eventRecord(bench.end);
+    return runner.a.eventElapsed(bench.start, bench.end) / K;
+  });
   const unbatched = { dispatches: tp.program.dispatches, msPerStep: plainWall, residentMsPerStep: plainResident,
     stepsPerSec: 1e3 / plainWall, residentStepsPerSec: 1e3 / plainResident };
   tp.destroy();
@@ -478,7 +608,8 @@ function trainStep(runner, bench, name, req, opts) {
     launches: { fused: fs.lowered.launches.length, unfused: lu.launches.length },
     dispatches: p.dispatches, batches: (fs.lowered.batches || []).length, unbatched,
     fused: t.stats.fused, unfused: t.stats.unfused, verdict: verdict(t.stats.unfused, t.stats.fused),
-    matmulFlopsPerStep: flops, matmulTflopsResident: flops / (residentMs * 1e9), byKind };
+    matmulFlopsPerStep: flops, matmulTflopsResident: flops / (residentMs * 1e9), byKind,
+    groups: groupSummary(groupList), groupList };
 }
 
 function c1(runner, bench, opts) { return trainStep(runner, bench, 'c1', { model: 'mlp' }, opts); }
@@ -494,8 +625,21 @@ function c5(runner, bench, opts) { return trainStep(runner, bench, 'c5', { model
  */
 function sweep(runner, bench, opts) {
   const { workloads } = require('../src/builders/workloads');
+  // The correctness gate (workloads.js:351-374, web/m4-bench.html:120-150 there): every
+  // variant was run once and judged against the float64 oracle before timing (bench.py
+  // writes the verdicts to --gate); a workload any of whose variants failed is not timed.
+  const gateFile = arg('gate', null);
+  const gate = gateFile ? JSON.parse(require('fs').readFileSync(gateFile, 'utf8')) : null;
   const rows = [];
+  let timed = 0;
   for (const w of workloads()) {
+    const g = gate ? gate[w.id] : null;
+    if (gate && !(g && g.pass)) {
+      rows.push({ id: w.id, family: w.family, params: w.params, gate: g || { pass: false, reason: 'not judged' }, timed: false });
+      log(`sweep ${w.id}: failed its gate, not timed`);
+      continue;
+    }
+    timed++;
     const m = w.make();
     const variants = {}, info = {};
     for (const v of w.variants) {
@@ -515,7 +659,7 @@ function sweep(runner, bench, opts) {
       info[v] = { launches: launches.length, bytes: launches.reduce((q, l) => q + l.bytes, 0), flops: launches.reduce((q, l) => q + (l.flops || 0), 0) };
     }
     const t = bench.time(variants, { reps: opts.reps || 16 });
-    const row = { id: w.id, family: w.family, params: w.params, k: t.k, variants: {} };
+    const row = { id: w.id, family: w.family, params: w.params, gate: g, timed: true, k: t.k, variants: {} };
     for (const v of w.variants) {
       const st = t.stats[v];
       row.variants[v] = Object.assign({ medianUs: st.median * 1e3, minUs: st.min * 1e3, maxUs: st.max * 1e3, gbs: info[v].bytes / (st.median * 1e6) }, info[v]);
@@ -524,7 +668,7 @@ function sweep(runner, bench, opts) {
     if (t.stats.recompute) row.recompute = verdict(t.stats.fused, t.stats.recompute);
     rows.push(row);
     for (const v of w.variants) variants[v].destroy();
-    log(`sweep ${w.id}: ${row.fused ? `fused ${row.fused.speedup.toFixed(2)}x ${row.fused.verdict}` : ''}`);
+    if (timed % 20 === 0) log(`sweep: ${timed} workloads timed`);
   }
   // Per family: workloads, fused wins / losses / noise, median and range of the speedup.
   const families = {};
@@ -540,7 +684,7 @@ function sweep(runner, bench, opts) {
     f.speedup = { median: median(f.speedups), min: f.speedups[0], max: f.speedups[f.speedups.length - 1] };
     delete f.speedups;
   }
-  return { config: 'sweep', workloads: rows, families };
+  return { config: 'sweep', gated: !!gate, timedWorkloads: timed, workloads: rows, families };
 }
 
 /** The bandwidth ceiling (workloads.js:312-345): copy and pure read of 1 GiB, grid-strided, 1024 x 256 threads. */
@@ -581,6 +725,7 @@ async function main() {
     out.configs[c].seconds = (Date.now() - t0) / 1e3;
     log(`${c} done in ${out.configs[c].seconds.toFixed(1)} s`);
   }
+  out.timedRegionsChecked = bench.checked;
   bench.destroy();
   process.stdout.write(JSON.stringify(out));
 }

@@ -22,6 +22,7 @@
 //   gpu-fuzz         request {from, to, recompute?}: the reference's corpus programs, fused / perf / unfused, on the GPU
 //   gpu-configs      request {c3: [...], c4: [...], unfused} configs 3 and 4, kept outputs as oracle-computable slices
 //   gpu-workloads    request {ids?, families?, allNodes?}: the workload sweep's variants run once, outputs for the gate
+//   gpu-bench-selftest  the timing protocol's counters: a clean timed region, a planted leak that must trip
 //   gpu-step-slices  request {model, B, sequences}: a full-batch step's launches with their operands, as per-sequence blocks
 
 const fs = require('fs');
@@ -588,8 +589,8 @@ async function gpuWorkloads(req, dir) {
     const m = w.make();
     const ins = {};
     for (const k of Object.keys(m.inputs)) ins[k] = bundle.put(m.inputs[k]);
-    const entry = { id: w.id, family: w.family, params: w.params, graph: m.graph.toJSON(), outputs: m.outputs, inputs: ins,
-      variants: {} };
+    const entry = { id: w.id, family: w.family, params: w.params, judge: w.judge, graph: m.graph.toJSON(), outputs: m.outputs,
+      inputs: ins, variants: {} };
     for (const v of w.variants.filter((x) => x !== 'matmul-only')) {
       let graph = m.graph, keep = m.outputs, f = null;
       if (v !== 'unfused') {
@@ -879,6 +880,44 @@ async function gpuStepSlices(req, dir) {
     splitK: fs.lowered.launches.filter((l) => l.kernels.some((k) => /_red$/.test(k.name))).length,
     batches: (fs.lowered.batches || []).length, aliases: fs.lowered.aliases, folded: fs.lowered.folded, dead: fs.lowered.dead });
   bundle.close({ device: runner.info() });
+}
+
+/**
+ * The timing protocol's counters and their self-test (src/fusion/bench.js:122-132,
+ * 175-192 there: a deliberate leak inside the timed region must be caught): a small fused
+ * program timed once as the bench times it (nothing may be created or copied inside the
+ * repetitions), then again with `leak` (an allocation and a free inside every
+ * repetition), which must throw; and a timed region around an upload, which must throw
+ * unless uploads are allowed (a training step's batch).
+ */
+async function gpuBenchSelftest() {
+  const { HipRunner } = require('../src/mi355x/runner');
+  const { HipBench, TimedRegionError } = require('../src/mi355x/bench');
+  const { chainWorkload, chainInputs } = require('../src/builders/chains');
+  const runner = HipRunner.create();
+  const bench = new HipBench(runner);
+  const w = chainWorkload(0, 64, 1024), inputs = chainInputs(0, 64, 1024);
+  const f = fuse(w.forward.graph, { keep: w.forward.keep });
+  const lf = lowerMI355X(f.graph, { perf: true, keep: w.forward.keep.map((id) => f.index.get(id)) });
+  const p = runner.prepare(f.graph, lf);
+  for (const n of f.graph.nodes) if (n.op === 'input') p.write(n.id, inputs[n.attrs.name]);
+  const out = { clean: null, leak: null, upload: null, uploadAllowed: null };
+  const t = bench.time({ fused: p }, { reps: 4, warmup: 1 });
+  out.clean = { k: t.k, checked: bench.checked };
+  const trips = (fn) => {
+    try { fn(); return { threw: false }; } catch (e) {
+      return { threw: e instanceof TimedRegionError, created: e.created || null, message: e.message };
+    }
+  };
+  out.leak = trips(() => bench.time({ fused: p }, { reps: 2, warmup: 0, leak: true }));
+  const h = runner.a.malloc(16);
+  out.upload = trips(() => bench.region(() => runner.a.h2d(h, 0, new Float32Array(4))));
+  out.uploadAllowed = trips(() => bench.region(() => runner.a.h2d(h, 0, new Float32Array(4)), ['h2d']));
+  runner.a.free(h);
+  out.checked = bench.checked;
+  p.destroy();
+  bench.destroy();
+  return out;
 }
 
 async function gpuTrain(req) {
@@ -1243,6 +1282,7 @@ async function main() {
     case 'gpu-workloads': await gpuWorkloads(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-step-slices': await gpuStepSlices(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-train': out = await gpuTrain(req); break;
+    case 'gpu-bench-selftest': out = await gpuBenchSelftest(); break;
     case 'gpu-concurrent': out = await gpuConcurrent(req); break;
     case 'gpu-chains': await gpuChains(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-graphs': await gpuGraphs(req, outDir(argv)); out = { ok: true }; break;

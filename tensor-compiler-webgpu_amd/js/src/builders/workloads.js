@@ -41,7 +41,8 @@ function drawInputs(graph, seed, ranges) {
 function graphWorkload(id, family, params, build, options) {
   const o = options || {};
   return {
-    id, family, params, variants: o.variants || ['unfused', 'fused'],
+    // Outputs judged against the composed float32 budget of the whole graph.
+    id, family, params, judge: 'composed', variants: o.variants || ['unfused', 'fused'],
     make() {
       const g = new Graph();
       const outputs = [].concat(build(g));
@@ -60,7 +61,10 @@ function binaryChain(g, n, L) {
 /** The reference transformer's forward pass or Adam step at (V, B), its seeding and a random batch. */
 function modelWorkload(what, V, B) {
   return {
-    id: `${what}-V${V}-B${B}`, family: what === 'step' ? 'training-step' : 'forward', params: { V, B },
+    // The model's composed budget is infinite at its logits (layer norm divides by a
+    // deviation whose bound exceeds it), so its variants are compared with each other
+    // and must be finite (the reference's revision R6).
+    id: `${what}-V${V}-B${B}`, family: what === 'step' ? 'training-step' : 'forward', params: { V, B }, judge: 'compare',
     variants: what === 'step' ? ['unfused', 'fused', 'matmul-only'] : ['unfused', 'fused'],
     make() {
       const cfg = tf.REFERENCE_CONFIG;

@@ -10,7 +10,12 @@
 //   * 5 warm-up repetitions per variant, then 32 repetitions in ABBA order;
 //   * summaries are median/min/max microseconds per program run, and two
 //     variants win or lose against each other only when their min-max ranges
-//     do not overlap (verdict), speedup being the ratio of medians.
+//     do not overlap (verdict), speedup being the ratio of medians;
+//   * the library's counters of object-creating calls and host<->device copies
+//     (tcmi_counters) are read on both sides of the repetitions, and a timed
+//     region that created anything or moved data throws (bench.js:41-47,175-192
+//     there). `leak` (the counters' self-test) allocates inside every repetition,
+//     which must make time() throw.
 
 const WARMUP = 5;
 const REPS = 32;
@@ -34,12 +39,43 @@ function verdict(base, other) {
   return { speedup, verdict: v };
 }
 
+/** The counters that moved between two readings of tcmi_counters, by name. */
+function created(before, after) {
+  const out = {};
+  for (const k of Object.keys(after)) if (after[k] !== before[k]) out[k] = after[k] - before[k];
+  return out;
+}
+
+class TimedRegionError extends Error {
+  constructor(what) {
+    super(`objects created or data moved inside a timed region: ${JSON.stringify(what)}`);
+    this.name = 'TimedRegionError';
+    this.created = what;
+  }
+}
+
 class HipBench {
   constructor(runner, options) {
     this.a = runner.a;
     this.graphs = !!(options && options.graphs);
     this.start = this.a.eventCreate();
     this.end = this.a.eventCreate();
+    this.checked = 0;     // timed regions whose counters were checked
+  }
+
+  /**
+   * Run `body` as a timed region: the counters must not move across it, except the
+   * kinds listed in `allow` (a training step's batch upload and loss readback).
+   * Returns body's result; throws TimedRegionError otherwise.
+   */
+  region(body, allow) {
+    const before = this.a.counters();
+    const r = body();
+    const moved = created(before, this.a.counters());
+    for (const k of allow || []) delete moved[k];
+    if (Object.keys(moved).length) throw new TimedRegionError(moved);
+    this.checked++;
+    return r;
   }
 
   /**
@@ -48,11 +84,12 @@ class HipBench {
    * so the GPU runs them back to back; with `graphs` the program is captured
    * once as a HIP graph and replayed k times.
    */
-  rep(program, k, direct) {
+  rep(program, k, direct, leak) {
     const a = this.a;
     a.eventRecord(this.start);
     if (direct) program.runTimes(k);
     else for (let i = 0; i < k; i++) program.replay();
+    if (leak) a.free(a.malloc(256));
     a.eventRecord(this.end);
     return a.eventElapsed(this.start, this.end) / k;
   }
@@ -84,10 +121,12 @@ class HipBench {
     const msPerRun = {};
     for (const n of names) msPerRun[n] = [];
     const reps = o.reps || REPS;
-    for (let b = 0; b < reps; b++) {
-      const order = b % 2 === 0 ? names : names.slice().reverse();
-      for (const n of order) msPerRun[n].push(this.rep(variants[n], k, direct));
-    }
+    this.region(() => {
+      for (let b = 0; b < reps; b++) {
+        const order = b % 2 === 0 ? names : names.slice().reverse();
+        for (const n of order) msPerRun[n].push(this.rep(variants[n], k, direct, !!o.leak));
+      }
+    });
     const stats = {};
     for (const n of names) stats[n] = summarize(msPerRun[n]);
     return { k, stats, msPerRun };
@@ -99,4 +138,4 @@ class HipBench {
   }
 }
 
-module.exports = { HipBench, summarize, verdict, median, WARMUP, REPS, TARGET_MS };
+module.exports = { HipBench, TimedRegionError, created, summarize, verdict, median, WARMUP, REPS, TARGET_MS };

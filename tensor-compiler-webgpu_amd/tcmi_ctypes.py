@@ -62,6 +62,7 @@ PROTOTYPES = {
     "tcmi_graph_launch": ([u64], ctypes.c_int),
     "tcmi_graph_step": ([u32, P(u64), P(ctypes.c_void_p), P(u64), u64, u64, ctypes.c_void_p, u64], ctypes.c_int),
     "tcmi_graph_destroy": ([u64], ctypes.c_int),
+    "tcmi_counters": ([P(u64), u32], ctypes.c_int),
     "tcmi_ceiling_copy": ([u64, u64, u64, u32], ctypes.c_int),
     "tcmi_ceiling_read": ([u64, u64, u64, u32], ctypes.c_int),
 }

@@ -19,12 +19,15 @@ def trim(doc: dict) -> dict:
     for key in ("c1", "c5"):
         if key in cfg:
             cfg[key]["byKind"] = {k: {"us": v["us"]} for k, v in cfg[key].get("byKind", {}).items()}
+            cfg[key].pop("groupList", None)
     if "attention" in cfg:
         for r in cfg["attention"]["results"]:
             r["groups"] = [{k: g[k] for k in ("kernelUs", "replacedUs", "tflops")} for g in r.get("groups", [])]
     if "sweep" in cfg:
         sw = cfg["sweep"]
-        sw["workloads"] = [{k: w[k] for k in ("id", "family", "fused", "recompute") if k in w} for w in sw["workloads"]]
+        sw["workloads"] = [{k: w[k] for k in ("id", "family", "fused", "recompute", "timed") if k in w} for w in sw["workloads"]]
+    if "gate" in doc:
+        doc["gate"] = {k: {"pass": v["pass"]} for k, v in doc["gate"].items()}
     return doc
 
 

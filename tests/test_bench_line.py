@@ -2,9 +2,10 @@
 bench.js wrote on the MI355X (tests/golden/bench_document.json, a `--quick` run trimmed by
 tests/golden/trim_bench_document.py): every field of the driver's contract is there with
 its type, `value` is config 2's step rate, the roofline figure is the named kernel's
-algorithmic bytes over its measured duration against the 8 TB/s peak, its HBM traffic comes
-from the committed profile that names the same kernel, and the side figures of the other
-configs are carried along."""
+algorithmic bytes over its cold (HBM-read) duration against the 8 TB/s peak and does not
+exceed the measured read ceiling, its HBM traffic comes from the committed profile that
+names the same kernel, every config's figures and fusion-group verdicts are carried in a
+compact `extra`, and the whole line stays small enough for the driver's output tail."""
 import json
 
 import pytest
@@ -33,29 +34,37 @@ def test_contract_fields(line):
     assert r["value"] == pytest.approx(c2["stepBytes"] / (c2["msPerStep"] * 1e6))
 
 
-def test_roofline_of_the_named_kernel(line):
+def test_roofline_is_the_cold_figure_of_the_named_kernel(line):
     import bench
     doc, r = line
     rf = r["roofline"]
     dom = doc["configs"]["c2"]["dominant"]
     assert rf["bound"] == "hbm" and rf["unit"] == "GB/s" and rf["peak"] == 8000.0
     assert rf["kernel"] == dom["code"]
+    assert rf["kernel_avg_us"] == dom["cold"]["avgUs"]
     assert rf["achieved"] == pytest.approx(rf["bytes_per_launch"] / (rf["kernel_avg_us"] * 1e3))
     assert rf["frac"] == pytest.approx(rf["achieved"] / rf["peak"])
+    # Cold: below the pure-read ceiling measured in the same run, and below the warm figure.
+    assert rf["achieved"] <= rf["read_ceiling"] and rf["achieved"] < rf["warm_achieved"]
+    # The rotation spans several times the 256 MB last-level cache.
+    assert dom["cold"]["spanBytes"] >= 4 * 256 * 2 ** 20
     traffic, src = bench.profiled_traffic(rf["kernel"])
     assert rf["traffic"] == traffic and rf["traffic_source"] == src and traffic is not None
-    # The kernel moves its algorithmic bytes: traffic within a percent of them.
     assert abs(rf["traffic"] / rf["bytes_per_launch"] - 1) < 0.01
 
 
-def test_side_figures_are_carried(line):
+def test_every_config_is_carried_compactly(line):
     _, r = line
     ex = r["extra"]
-    for k in ("rowwise_c3", "matmul_c4", "mlp_step_c1", "transformer_step_c5", "attention_extension", "workload_sweep",
-              "c2_programs", "c2_step_sequential", "device", "ceiling_1GiB"):
+    for k in ("c1", "c2", "c3", "c4", "c5", "attention", "sweep", "ceiling_1GiB_GBs", "timed_regions_checked"):
         assert k in ex, k
-    t = ex["transformer_step_c5"]
-    assert t["steps_per_sec"] > 0 and t["resident_steps_per_sec"] >= t["steps_per_sec"] * 0.9
-    assert t["dispatches"] < t["unbatched"]["dispatches"]
-    assert 0 < ex["rowwise_c3"]["frac_hbm"] < 1
-    assert all(0 < v["frac_mfma"] < 1 for v in ex["matmul_c4"].values())
+    assert ex["timed_regions_checked"] > 0
+    for k in ("c1", "c2", "c3", "c5"):
+        g = ex[k]["groups"]
+        assert g["n"] == g["win"] + g["loss"] + g["noise"] > 0 and g["worst"]["verdict"] in ("win", "loss", "noise"), k
+    assert ex["c4_groups"]["n"] > 0
+    assert ex["c5"]["resident_steps_s"] >= ex["c5"]["steps_s"] * 0.9
+    assert 0 < ex["c3"]["frac"] < 1
+    assert all(0 < v["frac_fwd"] < 1 for v in ex["c4"].values())
+    assert ex["sweep"]["timed"] == ex["sweep"]["gate_pass"] <= ex["sweep"]["workloads"]
+    assert len(json.dumps(r, separators=(",", ":"))) < 6000

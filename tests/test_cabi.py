@@ -43,13 +43,17 @@ def test_calls_before_init_fail_cleanly():
     assert t.lib.tcmi_graph_step(0, None, None, None, 1, 0, out, 4) == 10004
     assert t.lib.tcmi_launch_dag(0, None, None, None, None, 1, None, None, None, None) == 10004
     assert t.lib.tcmi_dag_reserve(1) == 10004
+    # The counters read without a device, and nothing has been counted in this process.
+    c = (tcmi_ctypes.u64 * 7)()
+    assert t.lib.tcmi_counters(c, 7) == 0 and list(c) == [0] * 7
+    assert t.lib.tcmi_counters(None, 1) == 10001
 
 
 def test_node_addon_loads_and_exports():
     js = ("const a=require(process.argv[1]);"
           "const want=['init','info','malloc','free','h2d','d2h','d2d','fill32','countNot32','compile','precompile',"
           "'function','launch','launchMany','sync','eventCreate','eventRecord','eventElapsed','captureBegin','captureEnd',"
-          "'graphLaunch','graphStep','launchDag','dagReserve','ceilingCopy','ceilingRead'];"
+          "'graphLaunch','graphStep','launchDag','dagReserve','ceilingCopy','ceilingRead','counters'];"
           "const miss=want.filter((k)=>typeof a[k]!=='function'); if(miss.length){console.log(miss.join());process.exit(2);}"
           "try{a.malloc(16);process.exit(3);}catch(e){if(!/tcmi_init/.test(e.message))process.exit(4);}"
           # graphStep reads its destinations as handles held in doubles: other arrays are refused
