@@ -244,7 +244,7 @@ function c2(runner, bench, opts) {
   const programs = [];
   const results = [];
   // --roofline-only (for the profile behind `roofline`): the programs are built and only
-  // the roofline kernel's cold rotation runs, --warmup + --steps launches of it.
+  // the roofline kernel's cold measurement runs.
   const rooflineOnly = flag('roofline-only');
   const stepOnly = flag('step-only') || rooflineOnly;
   const arena = flag('arena');
@@ -273,9 +273,13 @@ function c2(runner, bench, opts) {
     }
   }
   if (rooflineOnly) {
+    // The cold measurement exactly as the bench makes it, and nothing else of the step:
+    // a tracer's average over this command's launches of the kernel is the same figure.
     const dom = dominantByBytes(programs);
     const p = programs.find((q) => q.launches.some((x) => x.code === dom.code));
-    dom.cold = coldLaunch(runner, bench, p, p.launches.find((x) => x.code === dom.code), W + K);
+    dom.cold = coldLaunch(runner, bench, p, p.launches.find((x) => x.code === dom.code), 0);
+    dom.avgUs = dom.cold.avgUs;
+    dom.gbs = dom.bytesPerLaunch / (dom.avgUs * 1e3);
     for (const q of programs) q.destroy();
     return { config: 'c2', rooflineOnly: true, shape: [R, C], programs: P, dominant: dom, results };
   }
