@@ -74,13 +74,15 @@ struct DenseView {
 // operand's extents), and both need every other stride a multiple of 4, so a
 // 128-bit load is aligned and either wholly inside the operand or wholly out.
 template <int TM, int TN, int BK, int PF, int AMODE, int BMODE, bool SPLIT, class AV, class BV, class Epi, int WN = 2,
-          bool PRIO = false, class Args = TcmiArgs>
+          bool PRIO = false, int KW = 1, class Args = TcmiArgs>
 __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict__ a_ptr,
                                          const float* __restrict__ b_ptr, const uint32_t batch, const uint32_t M,
                                          const uint32_t K, const uint32_t N, const uint32_t chunks,
                                          const uint32_t chunkK, const uint32_t zid) {
-  // 2 x WN wavefronts; each owns (TM·16) x (TN·16) of the BM x BN tile.
-  constexpr int THREADS = 64 * 2 * WN;
+  // KW groups of 2 x WN wavefronts; in each group a wavefront owns (TM·16) x (TN·16)
+  // of the BM x BN tile, and group g sums its own part of K (see below).
+  static_assert(KW == 1 || KW == 2 || KW == 4, "K groups");
+  constexpr int THREADS = 64 * 2 * WN;   // threads of one K group
   constexpr int BM = 2 * TM * 16;
   constexpr int BN = WN * TN * 16;
   static_assert(BK == 16 || BK == 32 || BK == 64, "slice depth");
@@ -89,20 +91,31 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
   constexpr bool B_NMAJOR = BMODE == MODE_R;   // Bs[col][k] instead of Bs[k][col]
   constexpr int AS = A_KMAJOR ? BM + 4 : BK + 4;   // padded row stride of the A tile
   constexpr int BS = B_NMAJOR ? BK + 4 : BN + 4;   // padded row stride of the B tile
-  __shared__ __attribute__((aligned(16))) float As[2][(A_KMAJOR ? BK : BM) * AS];
-  __shared__ __attribute__((aligned(16))) float Bs[2][(B_NMAJOR ? BN : BK) * BS];
+  __shared__ __attribute__((aligned(16))) float As_[KW][2][(A_KMAJOR ? BK : BM) * AS];
+  __shared__ __attribute__((aligned(16))) float Bs_[KW][2][(B_NMAJOR ? BN : BK) * BS];
 
   // zid: the workgroup's z index within this launch (blockIdx.z, or its part
   // below the member index in a batched launch).
   const uint32_t kz = SPLIT ? zid % chunks : 0u;
   const uint32_t bz = SPLIT ? zid / chunks : zid;
-  const uint32_t kbeg = SPLIT ? kz * chunkK : 0u;
-  const uint32_t kend = SPLIT ? min(K, kbeg + chunkK) : K;
+  const uint32_t kbeg0 = SPLIT ? kz * chunkK : 0u;
+  const uint32_t kend0 = SPLIT ? min(K, kbeg0 + chunkK) : K;
+  // K groups (KW > 1, for few-tile products: more wavefronts in flight per CU): group g
+  // sums K range [kbeg0 + g·sub, kbeg0 + (g+1)·sub) of this workgroup's range, every
+  // group the same number of slices (a short last range is zero-filled, so every
+  // barrier is reached by all), and the groups' sums are added in order g = 0, 1, ...
+  // after the loop. The split depends on (M, N, K, KW) alone, as everything else here.
+  const int kg = KW == 1 ? 0 : static_cast<int>(threadIdx.x) / THREADS;
+  const uint32_t sub = KW == 1 ? kend0 - kbeg0 : ((kend0 - kbeg0 + KW * BK - 1) / (KW * BK)) * BK;
+  const uint32_t kbeg = kbeg0 + kg * sub;
+  const uint32_t kend = min(kend0, kbeg + sub);
+  float (*As)[(A_KMAJOR ? BK : BM) * AS] = As_[kg];
+  float (*Bs)[(B_NMAJOR ? BN : BK) * BS] = Bs_[kg];
   const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const float* __restrict__ Ab = a_ptr + AV::batch(bz);
   const float* __restrict__ Bb = b_ptr + BV::batch(bz);
 
-  const int tid = threadIdx.x;
+  const int tid = KW == 1 ? static_cast<int>(threadIdx.x) : static_cast<int>(threadIdx.x) % THREADS;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -300,7 +313,7 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
     if (PRIO) __builtin_amdgcn_s_setprio(0);
   };
 
-  const uint32_t slices = (kend - kbeg + BK - 1) / BK;
+  const uint32_t slices = KW == 1 ? (kend - kbeg + BK - 1) / BK : sub / BK;
   load_slice(st0, kbeg);
   store_slice(st0, 0);
   if (PF == 2 && slices > 1) load_slice(st1, kbeg + BK);
@@ -327,6 +340,26 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
       if (ks + 2 < slices) store_slice(st0, 0);
       __syncthreads();
     }
+  }
+
+  if constexpr (KW > 1) {
+    // Groups 1 .. KW-1 hand their sums to group 0 through LDS, which adds them in
+    // group order; group 0 alone stores (no barrier follows).
+    __shared__ f4 red[KW - 1][THREADS][TM * TN];
+    if (kg > 0) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) red[kg - 1][tid][i * TN + j] = acc[i][j];
+    }
+    __syncthreads();
+    if (kg > 0) return;
+#pragma unroll
+    for (int g = 1; g < KW; ++g)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] += red[g - 1][tid][i * TN + j];
   }
 
   // Store: lane (t16, q) of tile (i, j) holds row t16, columns 4q .. 4q+3.

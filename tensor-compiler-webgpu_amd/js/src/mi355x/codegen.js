@@ -685,11 +685,16 @@ function gemmTiling(batch, M, N, K, tuning) {
   // An on-device sweep of every config-4 and config-5 product: 5-15 % faster than 2
   // wavefronts wherever N >= 64T, slower where N is narrower.
   const wn = t.waves || (T >= 2 && N >= 64 * T ? 4 : 2);
-  const bk = t.bk || (wn === 4 ? 32 : T === 1 ? 64 : T === 2 ? 32 : 16);
+  // K groups inside a workgroup: where 32 x 32 tiles leave at most two workgroups per CU
+  // and K is not split across workgroups, 2 or 4 groups of four wavefronts each sum a
+  // part of K (their sums added in order in LDS), so more wavefronts keep loads in
+  // flight and the matrix cores fed on each CU.
+  const kw = t.kw || (T === 1 && chunks === 1 && blocks(1) <= 512 && K >= 256 ? (K >= 512 ? 4 : 2) : 1);
+  const bk = t.bk || (kw > 1 ? 32 : wn === 4 ? 32 : T === 1 ? 64 : T === 2 ? 32 : 16);
   const pf = t.pf || 2;
   const prio = t.prio !== undefined ? !!t.prio : true;
   const wide = batch * Math.ceil(M / (32 * T)) * Math.ceil(N / (16 * wn * T));
-  return { T, chunks, chunkK, bk, pf, wn, prio, blocks: wide * chunks };
+  return { T, chunks, chunkK, bk, pf, wn, prio, kw, blocks: wide * chunks };
 }
 
 /**
@@ -804,8 +809,8 @@ ${indent(lines, '    ')}
   }
 };
 `;
-  const threads = 128 * tl.wn;
-  const variant = tl.wn === 2 && !tl.prio ? '' : `, ${tl.wn}, ${tl.prio}`;
+  const threads = 128 * tl.wn * tl.kw;
+  const variant = tl.kw > 1 ? `, ${tl.wn}, ${tl.prio}, ${tl.kw}` : tl.wn === 2 && !tl.prio ? '' : `, ${tl.wn}, ${tl.prio}`;
   const main = `extern "C" __global__ void __launch_bounds__(${threads}) __KERNEL__(const TcmiArgs A) {
   tcmi::gemm_f32<${T}, ${T}, ${tl.bk}, ${tl.pf}, ${av.mode}, ${bv.mode}, ${split}, __KERNEL___av, __KERNEL___bv, __KERNEL___epi${variant}>(A, A.in[${ia}], A.in[${ib}],
       ${batch}u, ${M}u, ${K}u, ${N}u, ${tl.chunks}u, ${tl.chunkK}u, blockIdx.z);
