@@ -722,6 +722,7 @@ async function gpuLocal(req, dir) {
     entry[`${key}Launches`] = lowered.launches.length;
   }
   entry.canaryIntact = entry.gpuCanary && entry.gpuPerfCanary;
+  entry.rowFolds = rowFoldsOf(fs.lowered);
   entry.aliases = fs.lowered.aliases;
   entry.folded = fs.lowered.folded;
   entry.dead = fs.lowered.dead;
@@ -878,8 +879,16 @@ async function gpuStepSlices(req, dir) {
     canaryPerf: fs.lowered.launches.every((l) => perf.canaryIntact[l.node]),
     loss: r.values[fs.loss][0], dispatchKinds: fs.lowered.launches.map((l) => l.kind),
     splitK: fs.lowered.launches.filter((l) => l.kernels.some((k) => /_red$/.test(k.name))).length,
-    batches: (fs.lowered.batches || []).length, aliases: fs.lowered.aliases, folded: fs.lowered.folded, dead: fs.lowered.dead });
+    batches: (fs.lowered.batches || []).length, aliases: fs.lowered.aliases, folded: fs.lowered.folded, dead: fs.lowered.dead,
+    rowFolds: rowFoldsOf(fs.lowered) });
   bundle.close({ device: runner.info() });
+}
+
+/** {chain node: [{ reduction, pos }]}: the row reductions a perf lowering folded into their chains. */
+function rowFoldsOf(lowered) {
+  const out = {};
+  for (const l of lowered.launches) if (l.rowFolds) out[l.node] = l.rowFolds;
+  return out;
 }
 
 /**
@@ -1270,7 +1279,7 @@ async function main() {
       }
       const l = lowerMI355X(g, { perf: true, keep });
       const plain = new Map(lowerMI355X(g).launches.map((x) => [x.node, x]));
-      out = { graph: g.toJSON(), keep, aliases: l.aliases, folded: l.folded, dead: l.dead,
+      out = { graph: g.toJSON(), keep, aliases: l.aliases, folded: l.folded, dead: l.dead, rowFolds: rowFoldsOf(l),
         launches: l.launches.map((x) => ({ node: x.node, kind: x.kind, inputs: x.inputs, views: x.views || null, modes: gemmModes(x),
           split: gemmSplit(x), plainSplit: gemmSplit(plain.get(x.node)) })) };
       break;

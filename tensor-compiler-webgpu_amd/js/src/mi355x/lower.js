@@ -90,7 +90,16 @@ function widenInputs(body, output, folds) {
 }
 
 /** Kernels for one node. */
-function lowerNode(graph, node, opts, mmViews, folds) {
+function lowerNode(graph, node, opts, mmViews, folds, rowFold) {
+  if (rowFold) {
+    // A row-statistics chain with its reductions folded in: the rowwise kernel of the
+    // reductions, with their own tuning so the rows are reduced in their order.
+    const folds = rowFold.map((f) => ({ pos: f.pos, op: graph.nodes[f.red].op, attrs: graph.nodes[f.red].attrs,
+      shape: graph.nodes[f.red].shape, inShape: graph.nodes[graph.nodes[f.red].inputs[0]].shape }));
+    const f = foldReductions(bodyOf(node), node.attrs.output, folds);
+    const t = opts.tuning || {};
+    return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(f.body, f.output, { tuning: t.rowreduce || t.row })));
+  }
   if (node.op === 'fused') {
     const w = widenInputs(bodyOf(node), node.attrs.output, folds);
     const b = w.body;
@@ -236,6 +245,38 @@ function perfPlan(graph, keep) {
       });
     }
   }
+  // Row statistics folded into their reduction: a plain sum or max over the last
+  // non-trivial axis whose consumers (one or two) are all fused elementwise chains of its
+  // own size (LayerNorm's mean and deviation scale, softmax's row scale, and the backward
+  // pass's chains over the same statistics), every operand of each chain a value of that
+  // size (read at the row index), launches nothing: each chain runs as a rowwise kernel
+  // that forms the reduction itself from the reduction's operand, its body on the row's
+  // reduced value in registers — the same reduction order and the same ops in the same
+  // order, so the same bits as the separate launches. The reductions a chain takes in
+  // must share one operand shape (one rowwise kernel walks one row length).
+  const rowFolds = new Map();   // chain id -> [{ red: reduction id, pos: its operand positions }]
+  const isChain = (c, rows) => c.op === 'fused' && c.attrs.kind === 'elementwise' && size(c.shape) === rows
+    && c.inputs.every((i) => size(graph.nodes[i].shape) === rows && !folded.has(i));
+  const cand = new Set();
+  for (const n of graph.nodes) {
+    if ((n.op !== 'sum' && n.op !== 'max') || keep.has(n.id) || dead.has(n.id) || cons[n.id].length === 0) continue;
+    const inShape = graph.nodes[n.inputs[0]].shape;
+    if (size(inShape.slice(n.attrs.axis + 1)) !== 1 || inShape[n.attrs.axis] === 1) continue;
+    const users = Array.from(new Set(cons[n.id]));
+    if (users.length <= 2 && users.every((u) => isChain(graph.nodes[u], size(n.shape)))) cand.add(n.id);
+  }
+  const inShapeOf = (r) => graph.nodes[graph.nodes[r].inputs[0]].shape.join('x');
+  for (const c of graph.nodes) {
+    const reds = Array.from(new Set(c.inputs.filter((i) => cand.has(i))));
+    for (const r of reds) if (inShapeOf(r) !== inShapeOf(reds[0])) cand.delete(r);
+  }
+  for (const r of cand) {
+    folded.add(r);
+    for (const u of new Set(cons[r])) {
+      if (!rowFolds.has(u)) rowFolds.set(u, []);
+      rowFolds.get(u).push({ red: r, pos: graph.nodes[u].inputs.map((i, k) => (i === r ? k : -1)).filter((k) => k >= 0) });
+    }
+  }
   const views = new Map();
   for (const n of graph.nodes) {
     for (const [slot, pos] of matmulSlots(n)) {
@@ -256,7 +297,38 @@ function perfPlan(graph, keep) {
       views.get(n.id)[slot] = { pos, source: cur, view, size: size(graph.nodes[cur].shape) };
     }
   }
-  return { aliases, folded, views, broadcasts, dead };
+  return { aliases, folded, views, broadcasts, dead, rowFolds };
+}
+
+/**
+ * `body` with each input at the positions of a fold (a row reduction's value) replaced by
+ * that reduction of a new input, in the first of those positions: the reduction's operand
+ * read as [outer, n] rows (its reduced axis is the last non-trivial one) and reduced along
+ * them, as the plain lowering reduces it, then reshaped to the reduction's own shape — the
+ * body of a chain with its reductions folded in.
+ */
+function foldReductions(body, output, folds) {
+  const g = new Graph();
+  const map = new Map();
+  const at = new Map();
+  for (const f of folds) for (const p of f.pos) at.set(p, f);
+  const reduced = new Map();
+  for (const n of body.nodes) {
+    const f = n.op === 'input' ? at.get(Number(n.attrs.name.slice(1))) : undefined;
+    if (f) {
+      if (!reduced.has(f)) {
+        const outer = size(f.inShape.slice(0, f.attrs.axis)), len = f.inShape[f.attrs.axis];
+        const r = g.emit(f.op, [g.input(`a${f.pos[0]}`, [outer, len])], { axis: 1, keepDims: true });
+        reduced.set(f, g.reshape(r, f.shape));
+      }
+      map.set(n.id, reduced.get(f));
+    } else if (n.op === 'input') {
+      map.set(n.id, g.input(n.attrs.name, n.shape));
+    } else {
+      map.set(n.id, g.emit(n.op, n.inputs.map((i) => map.get(i)), n.attrs));
+    }
+  }
+  return { body: g, output: map.get(output) };
 }
 
 /**
@@ -275,7 +347,7 @@ function lowerMI355X(graph, options) {
   const opts = options || {};
   if (opts.perf && !opts.keep) throw new Error('the perf lowering needs `keep`: the nodes whose values are read');
   const plan = opts.perf ? perfPlan(graph, new Set(opts.keep))
-    : { aliases: new Map(), folded: new Set(), views: new Map(), broadcasts: new Map(), dead: new Set() };
+    : { aliases: new Map(), folded: new Set(), views: new Map(), broadcasts: new Map(), dead: new Set(), rowFolds: new Map() };
   const cache = new Map();
   const launches = [];
   let workspace = 0;
@@ -290,21 +362,29 @@ function lowerMI355X(graph, options) {
     }
     const folds = plan.broadcasts.get(node.id) || null;
     const foldKey = folds ? Array.from(folds.entries()).map(([pos, f]) => [pos, f.from, f.to]) : null;
+    const rowFold = plan.rowFolds.get(node.id) || null;
+    const rowKey = rowFold ? rowFold.map((f) => [f.pos, graph.nodes[f.red].op, graph.nodes[f.red].attrs,
+      graph.nodes[graph.nodes[f.red].inputs[0]].shape]) : null;
     // Kernels depend on structure, shapes, operand views and folded broadcasts only: reuse across identical nodes.
     const key = JSON.stringify([node.op, node.inputs.map((id) => graph.nodes[id].shape), node.attrs, node.shape,
-      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey]);
+      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey, rowKey]);
     let k = cache.get(key);
-    if (!k) { k = lowerNode(graph, node, opts, mmViews, folds); cache.set(key, k); }
+    if (!k) { k = lowerNode(graph, node, opts, mmViews, folds, rowFold); cache.set(key, k); }
     workspace = Math.max(workspace, k.workspace);
     const resolve = (id) => (plan.aliases.has(id) ? plan.aliases.get(id) : id);
     const inputs = node.inputs.map(resolve);
     if (v) for (const s of Object.values(v)) inputs[s.pos] = resolve(s.source);
     if (folds) for (const [pos, f] of folds) inputs[pos] = resolve(f.source);
+    if (rowFold) for (const f of rowFold) for (const pos of f.pos) inputs[pos] = resolve(graph.nodes[f.red].inputs[0]);
     launches.push({
       node: node.id, op: node.op, kind: k.kind, pattern: node.op === 'fused' ? node.attrs.pattern : undefined,
       inputs, params: k.params, grid: k.kernels[0].grid, code: k.kernels[0].name,
       kernels: k.kernels, workspace: k.workspace, bytes: algorithmicBytes(graph, node, inputs), flops: k.flops,
     });
+    if (rowFold) {
+      // The reduction folded into this launch, and the launch's own body (for node-local checks).
+      launches[launches.length - 1].rowFolds = rowFold.map((f) => ({ reduction: f.red, pos: f.pos }));
+    }
     if (v) {
       // Operands read in place: for each folded slot, the node it stands for and the view of its source.
       launches[launches.length - 1].views = {};

@@ -28,10 +28,53 @@ def take_block(a: np.ndarray, shape: Sequence[int], p: int, q: int, b: int) -> n
     return np.ascontiguousarray(nd[tuple(idx)]).reshape(-1)
 
 
-def twin_node(full, twin, node_id):
-    """The full graph's node with the twin's shapes and the full graph's constants: body
-    nodes keep their op, inputs, axes, permutations and constant values, and take the
-    twin's shapes and shape attributes."""
+def fold_reductions(graph, node_id, folds):
+    """A launch of the perf lowering that took row reductions into a chain (its record's
+    rowFolds: [{reduction, pos}]): the chain's node with each body input at `pos` (the
+    reduction's value) replaced by the reduction itself, applied to a new input a{pos[0]},
+    and the launch's operand node ids (the reduction's operand in those positions).
+    Restated here from the lowering's rule, so a wrong fold there fails the judge."""
+    node = graph["nodes"][node_id]
+    if not folds:
+        return node, list(node["inputs"])
+    at = {p: f for f in folds for p in f["pos"]}
+    body = node["attrs"]["body"]["nodes"]
+    out, where, reduced = [], {}, {}
+    for bid, b in enumerate(body):
+        f = at.get(int(b["attrs"]["name"][1:])) if b["op"] == "input" else None
+        if f is not None:
+            red = graph["nodes"][f["reduction"]]
+            if f["reduction"] not in reduced:
+                # The operand as [outer, n] rows reduced along them (the reduced axis is the
+                # last non-trivial one), then the reduction's own shape.
+                src = graph["nodes"][red["inputs"][0]]["shape"]
+                axis = red["attrs"]["axis"]
+                rows = [int(np.prod(src[:axis])), src[axis]]
+                out.append({"op": "input", "inputs": [], "attrs": {"name": f"a{f['pos'][0]}", "shape": rows}, "shape": rows})
+                out.append({"op": red["op"], "inputs": [len(out) - 1], "attrs": {"axis": 1, "keepDims": True},
+                            "shape": [rows[0], 1]})
+                if red["shape"] != [rows[0], 1]:
+                    out.append({"op": "reshape", "inputs": [len(out) - 1], "attrs": {"shape": red["shape"]},
+                                "shape": red["shape"]})
+                reduced[f["reduction"]] = len(out) - 1
+            where[bid] = reduced[f["reduction"]]
+        else:
+            out.append(dict(b, inputs=[where[i] for i in b["inputs"]]))
+            where[bid] = len(out) - 1
+    inputs = list(node["inputs"])
+    for f in folds:
+        for p in f["pos"]:
+            assert inputs[p] == f["reduction"]
+            inputs[p] = graph["nodes"][f["reduction"]]["inputs"][0]
+    attrs = dict(node["attrs"], body={"nodes": out}, output=where[node["attrs"]["output"]])
+    return dict(node, attrs=attrs, inputs=inputs), inputs
+
+
+def merge_twin(n, t):
+    """Node `n` of the full graph with the shapes of its twin `t` (the same node of the
+    one-sequence graph) and the full graph's constants: body nodes keep their op, inputs,
+    axes, permutations and constant values, and take the twin's shapes and shape
+    attributes."""
     def merge(a, b):
         assert a["op"] == b["op"] and a["inputs"] == b["inputs"]
         attrs = dict(a["attrs"])
@@ -39,12 +82,16 @@ def twin_node(full, twin, node_id):
             attrs["shape"] = b["attrs"]["shape"]
         return dict(a, attrs=attrs, shape=b["shape"])
 
-    n, t = full["nodes"][node_id], twin["nodes"][node_id]
     node = merge(n, t)
     if n["op"] == "fused":
         body = {"nodes": [merge(x, y) for x, y in zip(n["attrs"]["body"]["nodes"], t["attrs"]["body"]["nodes"])]}
         node["attrs"] = dict(node["attrs"], body=body)
     return node
+
+
+def twin_node(full, twin, node_id):
+    """The full graph's node with the twin's shapes and the full graph's constants."""
+    return merge_twin(full["nodes"][node_id], twin["nodes"][node_id])
 
 
 def local(graph, node, operands: List[np.ndarray]):
@@ -58,19 +105,23 @@ def local(graph, node, operands: List[np.ndarray]):
     return r["values"][out], r["bounds"][out]
 
 
-def expectations(full, twin, launched, operand, sequences):
+def expectations(full, twin, launched, operand, sequences, row_folds=None):
     """Yield (node id, sequence index or None, value, bound) for every launched node:
     per sequence where its output carries the batch axis, whole otherwise.
-    `operand(i, s)` is node i's value: its block for sequence index s, or whole for None."""
+    `operand(i, s)` is node i's value: its block for sequence index s, or whole for None.
+    `row_folds` ({node id: [{reduction, pos}]}, a perf lowering's): those launches are the
+    chain with its row reductions taken in, on the reductions' operands."""
     axis = [batch_axis(n["shape"], t["shape"]) for n, t in zip(full["nodes"], twin["nodes"])]
+    row_folds = row_folds or {}
     for nid in launched:
-        node = full["nodes"][nid]
+        folds = row_folds.get(nid) or row_folds.get(str(nid))
+        node, ins = fold_reductions(full, nid, folds)
         if axis[nid] >= 0:
-            tn = twin_node(full, twin, nid)
+            tn = merge_twin(node, fold_reductions(twin, nid, folds)[0])
             for s in range(len(sequences)):
-                ops = [operand(i, s if axis[i] >= 0 else None) for i in node["inputs"]]
+                ops = [operand(i, s if axis[i] >= 0 else None) for i in ins]
                 v, e = local(twin, tn, ops)
                 yield nid, s, v, e
         else:
-            v, e = local(full, node, [operand(i, None) for i in node["inputs"]])
+            v, e = local(full, node, [operand(i, None) for i in ins])
             yield nid, None, v, e

@@ -1,7 +1,7 @@
 """GPU parity of config 5's training step at its benchmark batch (B 64): every launch of
 the checked lowering and of the trainer's perf lowering (split-K weight gradients over
 8192 rows, batched dispatches, transposes read in place, the [8192, ...] elementwise and
-rowwise kernels) judged node-locally against the float64 oracle within the float32
+rowwise kernels, row statistics folded into their reductions) judged node-locally against the float64 oracle within the float32
 budget (src/gpu/harness-m4.js:182-223), on the GPU's own operands from one run of the
 checked lowering.
 
@@ -53,7 +53,8 @@ def test_c5_full_batch_step_node_local(tmp_path, tool):
         ref_v, ref_e, gpu = [], [], []
         blocks = wholes = 0
         with interp.blas_matmul():
-            for nid, s, v, e in expectations(full, twin, launched, operand, SEQUENCES):
+            folds = c["rowFolds"] if variant == "perf" else None
+            for nid, s, v, e in expectations(full, twin, launched, operand, SEQUENCES, folds):
                 ref_v.append(v)
                 ref_e.append(e)
                 gpu.append(b.arr(outs[nid]["whole"] if s is None else outs[nid]["blocks"][s]))
@@ -66,6 +67,8 @@ def test_c5_full_batch_step_node_local(tmp_path, tool):
         print(f"C5 B64 {variant}: {len(launched)} launches ({blocks} sequence blocks, {wholes} whole), worst "
               f"{j['worst']:.3g} over {j['elements']} elements, unjudgeable {j['unjudgeable']}", file=sys.stderr)
         assert j["pass"], (variant, j["first"], j["unjudged"])
-    print(f"C5 B64: split-K launches {c['splitK']}, batched dispatches {c['batches']}", file=sys.stderr)
+    print(f"C5 B64: split-K launches {c['splitK']}, batched dispatches {c['batches']}, row reductions folded into "
+          f"{len(c['rowFolds'])} chains", file=sys.stderr)
+    assert len(c["rowFolds"]) > 0
     assert counts["checked"][0] >= 4 * 300 and counts["checked"][1] >= 40, counts
     assert counts["perf"][0] > 0 and counts["perf"][1] > 0, counts

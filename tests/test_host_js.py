@@ -196,13 +196,25 @@ def test_perf_lowering_views_address_the_operands(tool, req):
     nodes = g["nodes"]
     for a, src in d["aliases"]:
         assert nodes[a]["op"] == "reshape" and nodes[src]["op"] != "reshape"
-    assert all(nodes[i]["op"] in ("transpose", "broadcast") for i in d["folded"])
+    # Folded: transposes read in place by matmuls, broadcasts read through their index map,
+    # and row reductions taken into the row-statistics chains that read them.
+    reductions = {f["reduction"] for fs in d["rowFolds"].values() for f in fs}
+    assert all(nodes[i]["op"] in ("transpose", "broadcast") for i in set(d["folded"]) - reductions)
     # A folded broadcast is read by elementwise, rowwise or epilogue bodies only (never
     # by a reduction, a gather or as a matmul operand), through the broadcast's source.
     consumers = {}
     for n_id, n in enumerate(nodes):
         for i in n["inputs"]:
             consumers.setdefault(i, set()).add(n_id)
+    for chain, fs in d["rowFolds"].items():
+        c = nodes[int(chain)]
+        assert c["op"] == "fused" and c["attrs"]["kind"] == "elementwise"
+        for f in fs:
+            r = nodes[f["reduction"]]
+            assert r["op"] in ("sum", "max") and r["shape"] != nodes[r["inputs"][0]]["shape"]
+            assert f["reduction"] not in d["keep"] and all(c["inputs"][p] == f["reduction"] for p in f["pos"])
+            # Every launched consumer of a folded reduction takes it in.
+            assert all(str(u) in d["rowFolds"] for u in consumers[f["reduction"]] if u not in d["dead"])
     for i in d["folded"]:
         if nodes[i]["op"] == "broadcast":
             for c in consumers[i]:

@@ -9,7 +9,7 @@ sequence would break the equality."""
 import numpy as np
 
 from oracle import bounds, interp
-from step_slices import batch_axis, expectations, local, take_block
+from step_slices import batch_axis, expectations, fold_reductions, local, take_block
 
 
 def test_sequence_blocks_equal_the_whole_launch(tmp_path, tool):
@@ -59,3 +59,37 @@ def test_sequence_blocks_equal_the_whole_launch(tmp_path, tool):
     # The launches judged whole do not carry the batch, and some read operands that do.
     wholes = [i for i in launched if axis[i] < 0]
     assert wholes and any(axis[j] >= 0 for i in wholes for j in nodes[i]["inputs"])
+
+
+def test_folded_row_reductions_are_the_chain_on_the_reduction(tool):
+    """The perf lowering takes config 5's row reductions (LayerNorm's sums, softmax's row
+    sums) into the row-statistics chains that read them. The checkers' restatement of such
+    a launch (fold_reductions) evaluated in float64 on a chain's operands equals the
+    reduction evaluated first and the chain's own body applied to its value, bit for bit,
+    value and bound: the fold changes where the reduction runs, not what is computed."""
+    d = tool("perf-lower", {"model": "transformer", "B": 1})
+    graph, folds = d["graph"], {int(k): v for k, v in d["rowFolds"].items()}
+    assert len(folds) >= 20
+    reds = {f["reduction"] for fs in folds.values() for f in fs}
+    assert reds <= set(d["folded"]) and all(graph["nodes"][r]["op"] in ("sum", "max") for r in reds)
+    rng = np.random.default_rng(3)
+    for k, fs in list(folds.items())[:12]:
+        node, ins = fold_reductions(graph, k, fs)
+        # Positive operands keep the deviation chains' square roots real.
+        ops = [rng.uniform(0.5, 2.0, size=interp.size(graph["nodes"][i]["shape"])).astype(np.float32) for i in ins]
+        v, e = local(graph, node, ops)
+        # The same launch the unfolded way: each reduction by itself, then the chain.
+        chain_ops = []
+        for pos, i in enumerate(graph["nodes"][k]["inputs"]):
+            if i in reds and i in [f["reduction"] for f in fs]:
+                red = graph["nodes"][i]
+                rv, re_ = local(graph, red, [ops[pos]])
+                chain_ops.append((rv, re_))
+            else:
+                chain_ops.append((ops[pos].astype(np.float64), np.zeros(ops[pos].size)))
+        body = graph["nodes"][k]["attrs"]["body"]
+        carried = {f"a{p}": ce for p, ce in enumerate(chain_ops)}
+        r = bounds.reference_with_bounds(body, {}, carried=carried)
+        out = graph["nodes"][k]["attrs"]["output"]
+        assert np.array_equal(v, r["values"][out]) and np.all(np.isfinite(v)), k
+        assert np.array_equal(e, r["bounds"][out]), k
