@@ -31,7 +31,7 @@ class Graph {
     attrs = attrs || {};
     for (const id of inputs) {
       if (!Number.isInteger(id) || id < 0 || id >= this.nodes.length) {
-        throw new ShapeError(`${op}: input ${id} is not a value of this graph`);
+        throw new ShapeError(`${op}: operand ${id} does not name a node of this graph`);
       }
     }
     const shape = inferShape(op, inputs.map((id) => this.nodes[id].shape), attrs);
@@ -65,7 +65,7 @@ class Graph {
     for (const n of json.nodes) {
       const id = g.emit(n.op, n.inputs, n.attrs);
       if (!sameShape(g.shape(id), n.shape)) {
-        throw new ShapeError(`node ${id}: stored shape ${fmt(n.shape)} but inferred ${fmt(g.shape(id))}`);
+        throw new ShapeError(`node ${id} (${n.op}): recorded as ${fmt(n.shape)}, its rule gives ${fmt(g.shape(id))}`);
       }
     }
     return g;
@@ -74,7 +74,7 @@ class Graph {
   // ---- builder ---------------------------------------------------------------
 
   input(name, shape) {
-    if (this.inputId(name) !== undefined) throw new Error(`input '${name}' already exists`);
+    if (this.inputId(name) !== undefined) throw new Error(`the graph has an input named '${name}' already`);
     return this.emit('input', [], { name, shape });
   }
 
@@ -86,7 +86,7 @@ class Graph {
 
   binary(op, a, b) {
     const shape = broadcastShapes(this.shape(a), this.shape(b));
-    if (!shape) throw new ShapeError(`${op}: ${fmt(this.shape(a))} and ${fmt(this.shape(b))} do not broadcast`);
+    if (!shape) throw new ShapeError(`${op}: no common broadcast shape for ${fmt(this.shape(a))} and ${fmt(this.shape(b))}`);
     const ba = this.broadcast(a, shape);
     const bb = this.broadcast(b, shape);
     return this.emit(op, [ba, bb]);

@@ -2,8 +2,9 @@
 // Static shapes of the IR: every op's result shape, computed once when the node
 // is created, so a graph that exists is shape-consistent.
 //
-// Same rules and op set as src/ir/shapes.js of abho7/tensor-compiler-webgpu
-// (OPS :51, inferShape :55-116, broadcastShapes :29-39); the reference's own
+// The op set and shape rules are the reference's (src/ir/shapes.js of
+// abho7/tensor-compiler-webgpu: OPS :51, inferShape :55-116, broadcastShapes
+// :29-39), since graphs must be interchangeable with its builder's; the reference's
 // module needs Node >= 24, so the host side of this backend carries its own.
 
 class ShapeError extends Error {
@@ -26,13 +27,13 @@ const fmt = (shape) => `[${shape.join(',')}]`;
 
 function checkShape(shape, what) {
   const ok = Array.isArray(shape) && shape.every((d) => Number.isInteger(d) && d >= 1);
-  if (!ok) throw new ShapeError(`${what}: shape must be a list of positive integers, got ${JSON.stringify(shape)}`);
+  if (!ok) throw new ShapeError(`${what}: a shape is a list of positive integers, not ${JSON.stringify(shape)}`);
 }
 
 /** A possibly negative axis resolved against `rank` (shapes.js:20-27). */
 function normAxis(axis, rank, op) {
   const a = axis < 0 ? axis + rank : axis;
-  if (!Number.isInteger(a) || a < 0 || a >= rank) throw new ShapeError(`${op}: axis ${axis} out of range for rank ${rank}`);
+  if (!Number.isInteger(a) || a < 0 || a >= rank) throw new ShapeError(`${op}: no axis ${axis} in a rank-${rank} value`);
   return a;
 }
 
@@ -63,75 +64,109 @@ const BINARY = new Set(['add', 'sub', 'mul', 'div']);
 const REDUCE = new Set(['sum', 'max']);
 const OPS = ['input', 'const', 'add', 'sub', 'mul', 'div', 'neg', 'exp', 'log', 'relu', 'tanh', 'step',
   'stopGradient', 'sqrt', 'matmul', 'sum', 'max', 'broadcast', 'reshape', 'transpose'];
-const OP_SET = new Set(OPS);
 
-function arityOf(op) {
-  if (op === 'input' || op === 'const') return 0;
-  if (op === 'matmul' || BINARY.has(op)) return 2;
-  return 1;
+/** Is `p` a permutation of 0 .. rank-1? */
+function isPermutation(p, rank) {
+  if (!Array.isArray(p) || p.length !== rank) return false;
+  const seen = new Array(rank).fill(false);
+  for (const v of p) {
+    if (!Number.isInteger(v) || v < 0 || v >= rank || seen[v]) return false;
+    seen[v] = true;
+  }
+  return true;
 }
 
-/** The result shape of `op` on inputs of `shapes`, or a thrown ShapeError (shapes.js:55-116). */
+/** A leaf's declared shape (and a constant's value, one number or one per element). */
+function leafShape(op, attrs) {
+  checkShape(attrs.shape, op);
+  if (op === 'const') {
+    const v = attrs.value;
+    if (!(typeof v === 'number' || (Array.isArray(v) && v.length === size(attrs.shape)))) {
+      throw new ShapeError(`const of shape ${fmt(attrs.shape)}: expected one number or ${size(attrs.shape)} of them`);
+    }
+  }
+  return attrs.shape.slice();
+}
+
+/**
+ * Shape rules: op -> { arity, rule(shapes, attrs, op) } (the result shape, or a thrown
+ * ShapeError). Binary ops take equal shapes only: the builder inserts broadcasts.
+ */
+const SHAPE_RULES = {
+  input: { arity: 0, rule: (s, attrs, op) => leafShape(op, attrs) },
+  const: { arity: 0, rule: (s, attrs, op) => leafShape(op, attrs) },
+  matmul: {
+    arity: 2,
+    rule([a, b]) {
+      if (a.length < 2 || b.length < 2) throw new ShapeError(`matmul of ${fmt(a)} by ${fmt(b)}: both operands need two or more axes`);
+      if (a.length !== b.length || !sameShape(a.slice(0, -2), b.slice(0, -2))) {
+        throw new ShapeError(`matmul of ${fmt(a)} by ${fmt(b)}: the leading (batch) axes must agree`);
+      }
+      const k = a[a.length - 1];
+      if (k !== b[b.length - 2]) throw new ShapeError(`matmul of ${fmt(a)} by ${fmt(b)}: contracted lengths ${k} and ${b[b.length - 2]}`);
+      return a.slice(0, -1).concat([b[b.length - 1]]);
+    },
+  },
+  broadcast: {
+    arity: 1,
+    rule([x], attrs, op) {
+      checkShape(attrs.shape, op);
+      if (!broadcastsTo(x, attrs.shape)) throw new ShapeError(`broadcast: cannot stretch ${fmt(x)} to ${fmt(attrs.shape)}`);
+      return attrs.shape.slice();
+    },
+  },
+  reshape: {
+    arity: 1,
+    rule([x], attrs, op) {
+      checkShape(attrs.shape, op);
+      if (size(attrs.shape) !== size(x)) {
+        throw new ShapeError(`reshape: ${fmt(x)} (${size(x)} elements) cannot become ${fmt(attrs.shape)} (${size(attrs.shape)})`);
+      }
+      return attrs.shape.slice();
+    },
+  },
+  transpose: {
+    arity: 1,
+    rule([x], attrs) {
+      if (!isPermutation(attrs.perm, x.length)) {
+        throw new ShapeError(`transpose of ${fmt(x)}: ${JSON.stringify(attrs.perm)} is not a permutation of its ${x.length} axes`);
+      }
+      return attrs.perm.map((i) => x[i]);
+    },
+  },
+};
+for (const op of BINARY) {
+  SHAPE_RULES[op] = {
+    arity: 2,
+    rule([a, b]) {
+      if (!sameShape(a, b)) throw new ShapeError(`${op} of ${fmt(a)} and ${fmt(b)}: operands must have one shape (insert a broadcast)`);
+      return a.slice();
+    },
+  };
+}
+for (const op of UNARY) SHAPE_RULES[op] = { arity: 1, rule: ([x]) => x.slice() };
+for (const op of REDUCE) {
+  SHAPE_RULES[op] = {
+    arity: 1,
+    rule([x], attrs) {
+      const axis = normAxis(attrs.axis, x.length, op);
+      if (attrs.axis !== axis) throw new ShapeError(`${op}: store the axis as ${axis}, not ${attrs.axis}`);
+      const out = [];
+      for (let i = 0; i < x.length; i++) {
+        if (i !== axis) out.push(x[i]);
+        else if (attrs.keepDims) out.push(1);
+      }
+      return out;
+    },
+  };
+}
+
+/** The result shape of `op` on inputs of `shapes`, or a thrown ShapeError (the rules of shapes.js:55-116). */
 function inferShape(op, shapes, attrs) {
-  if (!OP_SET.has(op)) throw new ShapeError(`unknown op '${op}'`);
-  const want = arityOf(op);
-  if (shapes.length !== want) throw new ShapeError(`${op}: takes ${want} inputs, got ${shapes.length}`);
-  if (op === 'input' || op === 'const') {
-    checkShape(attrs.shape, op);
-    if (op === 'const') {
-      const v = attrs.value;
-      const ok = typeof v === 'number' || (Array.isArray(v) && v.length === size(attrs.shape));
-      if (!ok) throw new ShapeError(`const: value must be a number or ${size(attrs.shape)} numbers`);
-    }
-    return attrs.shape.slice();
-  }
-  if (BINARY.has(op)) {
-    if (!sameShape(shapes[0], shapes[1])) {
-      throw new ShapeError(`${op}: shapes ${fmt(shapes[0])} and ${fmt(shapes[1])} differ; broadcast explicitly`);
-    }
-    return shapes[0].slice();
-  }
-  if (UNARY.has(op)) return shapes[0].slice();
-  if (op === 'matmul') {
-    const a = shapes[0], b = shapes[1];
-    if (a.length < 2 || b.length < 2) throw new ShapeError(`matmul: needs rank >= 2, got ${fmt(a)} and ${fmt(b)}`);
-    if (a.length !== b.length || !sameShape(a.slice(0, -2), b.slice(0, -2))) {
-      throw new ShapeError(`matmul: batch dims of ${fmt(a)} and ${fmt(b)} differ`);
-    }
-    if (a[a.length - 1] !== b[b.length - 2]) throw new ShapeError(`matmul: inner dims of ${fmt(a)} and ${fmt(b)} differ`);
-    return a.slice(0, -1).concat([b[b.length - 1]]);
-  }
-  if (REDUCE.has(op)) {
-    const x = shapes[0];
-    const axis = normAxis(attrs.axis, x.length, op);
-    if (attrs.axis !== axis) throw new ShapeError(`${op}: axis must be stored normalised`);
-    return attrs.keepDims ? x.map((d, i) => (i === axis ? 1 : d)) : x.filter((_, i) => i !== axis);
-  }
-  if (op === 'broadcast') {
-    checkShape(attrs.shape, op);
-    if (!broadcastsTo(shapes[0], attrs.shape)) {
-      throw new ShapeError(`broadcast: ${fmt(shapes[0])} does not broadcast to ${fmt(attrs.shape)}`);
-    }
-    return attrs.shape.slice();
-  }
-  if (op === 'reshape') {
-    checkShape(attrs.shape, op);
-    if (size(attrs.shape) !== size(shapes[0])) {
-      throw new ShapeError(`reshape: ${fmt(shapes[0])} has ${size(shapes[0])} elements, ${fmt(attrs.shape)} has ${size(attrs.shape)}`);
-    }
-    return attrs.shape.slice();
-  }
-  if (op === 'transpose') {
-    const x = shapes[0], p = attrs.perm;
-    let isPerm = Array.isArray(p) && p.length === x.length;
-    if (isPerm) {
-      const sorted = p.slice().sort((u, v) => u - v);
-      isPerm = sorted.every((v, i) => v === i);
-    }
-    if (!isPerm) throw new ShapeError(`transpose: ${JSON.stringify(p)} is not a permutation of rank ${x.length}`);
-    return p.map((i) => x[i]);
-  }
-  throw new ShapeError(`no shape rule for '${op}'`);
+  const r = SHAPE_RULES[op];
+  if (!r) throw new ShapeError(`'${op}' is not an op of this IR`);
+  if (shapes.length !== r.arity) throw new ShapeError(`${op} takes ${r.arity} operand(s), was given ${shapes.length}`);
+  return r.rule(shapes, attrs || {}, op);
 }
 
 /** Row-major strides of `shape` (interp.js:10-15). */

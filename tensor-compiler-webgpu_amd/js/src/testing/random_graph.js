@@ -1,19 +1,24 @@
 'use strict';
 // Seeded random well-typed programs: the fuzzing corpus of the reference
-// (src/testing/random-graph.js, "version 2", in abho7/tensor-compiler-webgpu).
+// (src/testing/random-graph.js, its "version 2", in abho7/tensor-compiler-webgpu).
 //
-// The corpus has to be the reference's program for program, because its
-// recorded counts — golden/cases.json's 40 v2 graphs, and the fusion pass's
-// results over corpus programs 1..2000 in golden/measurements.json m4 — pin this
-// backend's builder, autodiff and fusion pass. So the construction follows the
-// reference's steps and draws from the same generator (mulberry32, ../rng) in
-// the same order: every value carries an interval sound for inputs in [-2, 2];
-// log, div and exp are emitted only where the interval proves them safe (the
-// operand wrapped as x*x + c, exp of something bounded, or tanh otherwise); an
-// op whose result could exceed BOUND in magnitude is discarded with every node
-// it emitted; programs are either general (weighted op choices over a pool that
-// favours recent values) or targeted at one op (matmul, transpose, reshape,
-// broadcast, sum); every computed value nothing consumes is an output.
+// The corpus must be the reference's program for program: its recorded counts —
+// golden/cases.json's 40 v2 graphs, and the fusion pass's results over corpus
+// programs 1..2000 in golden/measurements.json m4 — pin this backend's builder,
+// autodiff and fusion pass. So every random decision below is drawn from the same
+// generator (mulberry32, ./rng) at the same point of the construction as there; the
+// construction itself is this file's own. Its rules:
+//   - every value carries an interval that is sound for inputs in [-2, 2]; an op
+//     whose result could exceed BOUND in magnitude is undone with every node it
+//     emitted (the input counter is not rewound);
+//   - log, div, sqrt and exp only see operands their interval proves safe: the
+//     operand is replaced by x·x + c, -(x·x + c), exp(x) or tanh(x) where needed;
+//   - tensors hold at most MAX_SIZE elements;
+//   - a general program draws weighted ops over a pool of values that favours the
+//     recent ones; a targeted program is built around one op (matmul, transpose,
+//     reshape, broadcast, sum), with no size-1 dims and fresh inputs, then takes a
+//     few more ops;
+//   - every computed value nothing consumes is an output.
 
 const { Graph } = require('../ir/graph');
 const { broadcastShapes, size } = require('../ir/shapes');
@@ -21,398 +26,436 @@ const { Rng } = require('./rng');
 
 const MAX_SIZE = 96;
 const BOUND = 1e3;
-const INPUT_RANGE = [-2, 2];
+const INPUT_LO = -2, INPUT_HI = 2;
 
-/** Relative weights of the general generator's ops (random-graph.js:38-41). */
+/** Relative weights of the general programs' ops (in this key order). */
 const GENERATED = {
   add: 3, sub: 3, mul: 3, div: 3, neg: 1, exp: 2, log: 2, relu: 3, tanh: 2,
   matmul: 4, sum: 3, broadcast: 2, reshape: 3, transpose: 3, softmax: 2, logSoftmax: 2,
 };
 
-/** Ops with a targeted generator (random-graph.js:44). */
+/** Ops with a program built around them, in this order. */
 const TARGETS = ['matmul', 'transpose', 'reshape', 'broadcast', 'sum'];
 
-const last = (a) => a[a.length - 1];
+/** The ops a targeted program may take after its target. */
+const FOLLOW_UPS = ['add', 'mul', 'tanh', 'exp', 'log', 'div', 'relu', 'sum', 'softmax'];
 
-function mulIv(x, y) {
-  const p = [x[0] * y[0], x[0] * y[1], x[1] * y[0], x[1] * y[1]];
-  return [Math.min(p[0], p[1], p[2], p[3]), Math.max(p[0], p[1], p[2], p[3])];
+const lastOf = (a) => a[a.length - 1];
+const absMax = ([lo, hi]) => Math.max(Math.abs(lo), Math.abs(hi));
+const sameDims = (a, b) => a.length === b.length && a.every((d, i) => d === b[i]);
+const snap = (v) => Math.round(v * 1024) / 1024;   // to a multiple of 2^-10
+
+/** The interval of a product of two intervals. */
+function product([a0, a1], [b0, b1]) {
+  const c = [a0 * b0, a0 * b1, a1 * b0, a1 * b1];
+  return [Math.min.apply(null, c), Math.max.apply(null, c)];
 }
 
-const magnitude = (iv) => Math.max(Math.abs(iv[0]), Math.abs(iv[1]));
+const WHOLE_LINE = [-Infinity, Infinity];
 
-/** The interval of node `id` from its inputs' intervals (sound, not tight). */
-function interval(g, id, iv, squareAware) {
+/**
+ * Interval rules, op -> (a, b, node, graph, squares) with a, b the operands' intervals.
+ * `squares`: x·x is known non-negative (the generator's square-aware mode).
+ */
+const RANGE = {
+  input: () => [INPUT_LO, INPUT_HI],
+  const: (a, b, n) => {
+    const v = n.attrs.value;
+    if (typeof v === 'number') return [v, v];
+    return [Math.min.apply(null, v), Math.max.apply(null, v)];
+  },
+  add: (a, b) => [a[0] + b[0], a[1] + b[1]],
+  sub: (a, b) => [a[0] - b[1], a[1] - b[0]],
+  mul: (a, b, n, g, squares) => {
+    if (!(squares && n.inputs[0] === n.inputs[1])) return product(a, b);
+    const m = absMax(a);
+    return [a[0] <= 0 && a[1] >= 0 ? 0 : Math.min(a[0] * a[0], a[1] * a[1]), m * m];
+  },
+  div: (a, b) => (b[0] <= 0 && b[1] >= 0 ? WHOLE_LINE.slice() : product(a, [1 / b[1], 1 / b[0]])),
+  neg: (a) => [-a[1], -a[0]],
+  exp: (a) => [Math.exp(a[0]), Math.exp(a[1])],
+  log: (a) => (a[0] > 0 ? [Math.log(a[0]), Math.log(a[1])] : WHOLE_LINE.slice()),
+  relu: (a) => [Math.max(0, a[0]), Math.max(0, a[1])],
+  step: () => [0, 1],
+  tanh: (a) => [Math.tanh(a[0]), Math.tanh(a[1])],
+  sqrt: (a) => (a[0] >= 0 ? [Math.sqrt(a[0]), Math.sqrt(a[1])] : WHOLE_LINE.slice()),
+  // A sum of K products, K the contracted length.
+  matmul: (a, b, n, g) => product(a, b).map((x) => x * lastOf(g.shape(n.inputs[0]))),
+  // A sum of `len` values.
+  sum: (a, b, n, g) => a.map((x) => x * g.shape(n.inputs[0])[n.attrs.axis]),
+  max: (a) => a.slice(),
+  stopGradient: (a) => a.slice(),
+  broadcast: (a) => a.slice(),
+  reshape: (a) => a.slice(),
+  transpose: (a) => a.slice(),
+};
+
+/** The interval of node `id` from its operands' intervals in `known` (sound, not tight). */
+function interval(g, id, known, squares) {
   const n = g.nodes[id];
-  const a = n.inputs.length > 0 ? iv.get(n.inputs[0]) : undefined;
-  const b = n.inputs.length > 1 ? iv.get(n.inputs[1]) : undefined;
-  switch (n.op) {
-    case 'input': return INPUT_RANGE.slice();
-    case 'const': {
-      const v = n.attrs.value;
-      if (typeof v === 'number') return [v, v];
-      let lo = Infinity, hi = -Infinity;
-      for (const x of v) { if (x < lo) lo = x; if (x > hi) hi = x; }
-      return [lo, hi];
-    }
-    case 'add': return [a[0] + b[0], a[1] + b[1]];
-    case 'sub': return [a[0] - b[1], a[1] - b[0]];
-    case 'mul':
-      if (squareAware && n.inputs[0] === n.inputs[1]) {
-        const m = magnitude(a);
-        const lo = a[0] <= 0 && a[1] >= 0 ? 0 : Math.min(a[0] * a[0], a[1] * a[1]);
-        return [lo, m * m];
-      }
-      return mulIv(a, b);
-    case 'div':
-      if (b[0] <= 0 && b[1] >= 0) return [-Infinity, Infinity];
-      return mulIv(a, [1 / b[1], 1 / b[0]]);
-    case 'neg': return [-a[1], -a[0]];
-    case 'exp': return [Math.exp(a[0]), Math.exp(a[1])];
-    case 'log': return a[0] > 0 ? [Math.log(a[0]), Math.log(a[1])] : [-Infinity, Infinity];
-    case 'relu': return [Math.max(0, a[0]), Math.max(0, a[1])];
-    case 'step': return [0, 1];
-    case 'tanh': return [Math.tanh(a[0]), Math.tanh(a[1])];
-    case 'sqrt': return a[0] >= 0 ? [Math.sqrt(a[0]), Math.sqrt(a[1])] : [-Infinity, Infinity];
-    case 'matmul': {
-      const k = last(g.shape(n.inputs[0]));
-      const p = mulIv(a, b);
-      return [k * p[0], k * p[1]];
-    }
-    case 'sum': {
-      const len = g.shape(n.inputs[0])[n.attrs.axis];
-      return [len * a[0], len * a[1]];
-    }
-    case 'max': case 'stopGradient': case 'broadcast': case 'reshape': case 'transpose':
-      return a.slice();
-    default: throw new Error(`no interval rule for ${n.op}`);
-  }
+  const rule = RANGE[n.op];
+  if (!rule) throw new Error(`no interval rule for ${n.op}`);
+  const ranges = n.inputs.map((i) => known.get(i));
+  return rule(ranges[0], ranges[1], n, g, squares);
 }
 
-const round1024 = (v) => Math.round(v * 1024) / 1024;
-
-/** Every ordered factorisation of n into `rank` factors, smallest first factor first. */
+/** Every ordered factorisation of n into `rank` factors, by increasing first factor. */
 function factorizations(n, rank) {
   if (rank === 1) return [[n]];
   const out = [];
   for (let d = 1; d <= n; d++) {
-    if (n % d) continue;
-    for (const rest of factorizations(n / d, rank - 1)) out.push([d].concat(rest));
+    if (n % d !== 0) continue;
+    for (const tail of factorizations(n / d, rank - 1)) out.push([d].concat(tail));
   }
   return out;
 }
 
-const isInvolution = (perm) => perm.every((p, i) => perm[p] === i);
-const sameShape = (a, b) => a.length === b.length && a.every((d, i) => d === b[i]);
+const identity = (perm) => perm.every((p, i) => p === i);
+const selfInverse = (perm) => perm.every((p, i) => perm[p] === i);
 
-class ProgramBuilder {
-  constructor(rng) {
+/** The state of one program under construction, and the draws that shape it. */
+class Generator {
+  constructor(rng, o) {
     this.rng = rng;
     this.g = new Graph();
-    this.iv = new Map();
-    this.pool = [];
-    this.leaves = 0;
-    this.strict = false;        // targeted programs: no size-1 dims, matmul's B always an input
-    this.f32 = false;           // float32 guards (exp arguments kept above -40)
-    this.squareAware = false;
-    this.operand = undefined;
+    this.known = new Map();      // node id -> interval
+    this.pool = [];              // values later ops may take, oldest first
+    this.inputs = 0;             // inputs made so far (names x0, x1, ...)
+    this.strict = false;         // targeted construction: no size-1 dims, matmul's B a fresh input
+    this.f32 = !!o.f32;          // float32 guard: exp arguments kept above -40
+    this.squares = !!o.squareAware;
+    this.forced = undefined;     // the operand an op must take, if any
   }
 
-  /** Give every node up to `id` its interval (helpers may have emitted nodes in between). */
-  track(id) {
-    if (!this.iv.has(id)) {
-      for (let i = 0; i <= id; i++) if (!this.iv.has(i)) this.iv.set(i, interval(this.g, i, this.iv, this.squareAware));
-    }
+  // ---- intervals -------------------------------------------------------------------
+
+  /** Give every node up to `id` its interval (guards may have emitted nodes in between). */
+  settle(id) {
+    if (this.known.has(id)) return id;
+    for (let i = 0; i <= id; i++) if (!this.known.has(i)) this.known.set(i, interval(this.g, i, this.known, this.squares));
     return id;
   }
 
-  ok(id) { return magnitude(this.iv.get(this.track(id))) <= BOUND; }
+  bounded(id) { return absMax(this.known.get(this.settle(id))) <= BOUND; }
 
-  dim() {
+  /** A mark to rewind to: nodes, intervals and pool entries after it are dropped. */
+  mark() { return this.g.nodes.length; }
+
+  rewind(at) {
+    this.g.nodes.length = at;
+    for (const k of Array.from(this.known.keys())) if (k >= at) this.known.delete(k);
+    this.pool = this.pool.filter((id) => id < at);
+  }
+
+  // ---- shapes ----------------------------------------------------------------------
+
+  dimension() {
     if (this.strict) return this.rng.int(2, 5);
     return this.rng.chance(0.2) ? 1 : this.rng.int(2, 6);
   }
 
-  shape(minRank, maxRank) {
-    const lo = minRank === undefined ? 0 : minRank, hi = maxRank === undefined ? 4 : maxRank;
+  /** A shape of rank in [lo, hi] (default [0, 4]) holding at most MAX_SIZE elements. */
+  randomShape(lo, hi) {
+    const minRank = lo === undefined ? 0 : lo, maxRank = hi === undefined ? 4 : hi;
     for (;;) {
-      const rank = this.rng.int(lo, hi);
-      const s = [];
-      for (let i = 0; i < rank; i++) s.push(this.dim());
-      if (size(s) <= MAX_SIZE) return s;
+      const rank = this.rng.int(minRank, maxRank);
+      const dims = [];
+      for (let i = 0; i < rank; i++) dims.push(this.dimension());
+      if (size(dims) <= MAX_SIZE) return dims;
     }
   }
 
-  input(shape) { return this.push(this.g.input(`x${this.leaves++}`, shape)); }
+  // ---- values ----------------------------------------------------------------------
 
-  leaf(shape) {
-    if (this.rng.chance(0.7)) return this.input(shape);
-    return this.push(this.g.const(this.rng.array(size(shape), -2, 2).map(round1024), shape));
+  /** A value later ops may take. */
+  offer(id) { this.settle(id); this.pool.push(id); return id; }
+
+  freshInput(shape) { return this.offer(this.g.input(`x${this.inputs++}`, shape)); }
+
+  /** A new input (70 %) or constant tensor of `shape`. */
+  freshLeaf(shape) {
+    if (this.rng.chance(0.7)) return this.freshInput(shape);
+    const values = this.rng.array(size(shape), -2, 2).map(snap);
+    return this.offer(this.g.const(values, shape));
   }
 
-  push(id) { this.track(id); this.pool.push(id); return id; }
-
-  /** A pool value passing `filter`, favouring recent ones (r² skews toward the end). */
-  choose(filter) {
-    const f = filter || (() => true);
-    const c = this.pool.filter((id) => f(this.g.shape(id), id));
-    if (c.length === 0) return undefined;
+  /** A pool value passing `keep(shape, id)`, recent ones favoured (index skewed by r²). */
+  pickValue(keep) {
+    const fits = this.pool.filter((id) => !keep || keep(this.g.shape(id), id));
+    if (fits.length === 0) return undefined;
     const r = this.rng.next();
-    return c[c.length - 1 - Math.floor(r * r * c.length)];
+    return fits[fits.length - 1 - Math.floor(r * r * fits.length)];
   }
 
-  /** The op's first operand: the forced one when given (if it passes `filter`), else chosen. */
-  first(filter) {
-    const f = filter || (() => true);
-    if (this.operand === undefined) return this.choose(f);
-    return f(this.g.shape(this.operand), this.operand) ? this.operand : undefined;
+  /** An op's first operand: the forced one if there is one (and it passes), else picked. */
+  firstOperand(keep) {
+    if (this.forced === undefined) return this.pickValue(keep);
+    return !keep || keep(this.g.shape(this.forced), this.forced) ? this.forced : undefined;
   }
 
-  scalarConst(lo, hi) { return this.track(this.g.const(round1024(this.rng.uniform(lo, hi)))); }
+  /** A second operand for a binary op with x: a broadcast-compatible pool value, or a new leaf. */
+  secondOperand(x) {
+    const xs = this.g.shape(x);
+    const compatible = (s) => { const out = broadcastShapes(xs, s); return !!out && size(out) <= MAX_SIZE; };
+    const found = this.rng.chance(0.5) ? this.pickValue(compatible) : undefined;
+    if (found !== undefined) return found;
+    const drop = this.rng.chance(0.3) ? this.rng.int(0, xs.length) : 0;
+    return this.freshLeaf(xs.slice(drop).map((d) => (this.rng.chance(0.3) ? 1 : d)));
+  }
 
-  safeDenominator(x) {
-    const [lo, hi] = this.iv.get(x);
+  literal(lo, hi) { return this.settle(this.g.const(snap(this.rng.uniform(lo, hi)))); }
+
+  // ---- guards: operands an op can take safely ----------------------------------------
+
+  /** x·x + c, c in [0.2, 1]: positive. */
+  squarePlus(x) { const sq = this.g.mul(x, x); return this.g.add(sq, this.literal(0.2, 1)); }
+
+  /** x if exp(x) stays bounded (and, with the float32 guard, normal), else tanh(x). */
+  expSafe(x) {
+    const [lo, hi] = this.known.get(x);
+    return hi <= 4 && (!this.f32 || lo >= -40) ? x : this.settle(this.g.tanh(x));
+  }
+
+  /** x if it is at least 0.1 away from zero, else a value that is. */
+  awayFromZero(x) {
+    const [lo, hi] = this.known.get(x);
     if (lo >= 0.1 || hi <= -0.1) return x;
     const r = this.rng.next();
-    const g = this.g;
-    if (r < 0.4) return this.track(g.add(g.mul(x, x), this.scalarConst(0.2, 1)));
-    if (r < 0.6) return this.track(g.neg(g.add(g.mul(x, x), this.scalarConst(0.2, 1))));
-    return this.track(g.exp(this.boundedForExp(x)));
+    if (r < 0.4) return this.settle(this.squarePlus(x));
+    if (r < 0.6) return this.settle(this.g.neg(this.squarePlus(x)));
+    return this.settle(this.g.exp(this.expSafe(x)));
   }
 
-  boundedForExp(x) {
-    const [lo, hi] = this.iv.get(x);
-    return hi <= 4 && (!this.f32 || lo >= -40) ? x : this.track(this.g.tanh(x));
+  /** x if it is at least 0.1, else exp(x) + c. */
+  sqrtSafe(x) {
+    if (this.known.get(x)[0] >= 0.1) return x;
+    const e = this.g.exp(this.expSafe(x));
+    return this.settle(this.g.add(e, this.literal(0.2, 1)));
   }
 
-  safeSqrtArgument(x) {
-    if (this.iv.get(x)[0] >= 0.1) return x;
-    return this.track(this.g.add(this.g.exp(this.boundedForExp(x)), this.scalarConst(0.2, 1)));
+  /** x if it is at least 0.1, else x·x + c (60 %) or exp(x). */
+  logSafe(x) {
+    if (this.known.get(x)[0] >= 0.1) return x;
+    return this.rng.chance(0.6) ? this.settle(this.squarePlus(x)) : this.settle(this.g.exp(this.expSafe(x)));
   }
 
-  safeLogArgument(x) {
-    if (this.iv.get(x)[0] >= 0.1) return x;
-    const g = this.g;
-    return this.rng.chance(0.6)
-      ? this.track(g.add(g.mul(x, x), this.scalarConst(0.2, 1)))
-      : this.track(g.exp(this.boundedForExp(x)));
-  }
+  // ---- structural ops ----------------------------------------------------------------
 
-  /** A partner for a binary op with x: an existing broadcast-compatible value, or a new leaf. */
-  partner(x) {
-    const xs = this.g.shape(x);
-    const b = this.rng.chance(0.5)
-      ? this.choose((s) => { const o = broadcastShapes(xs, s); return !!o && size(o) <= MAX_SIZE; })
-      : undefined;
-    if (b !== undefined) return b;
-    const drop = this.rng.chance(0.3) ? this.rng.int(0, xs.length) : 0;
-    return this.leaf(xs.slice(drop).map((d) => (this.rng.chance(0.3) ? 1 : d)));
-  }
-
-  apply(op, operand) {
+  matmulWith(first) {
     const { g, rng } = this;
-    this.operand = operand;
-    switch (op) {
-      case 'add': case 'sub': case 'mul': {
-        const a = this.first();
-        return g[op](a, this.partner(a));
-      }
-      case 'div': {
-        const a = this.first();
-        return g.div(a, this.safeDenominator(this.partner(a)));
-      }
-      case 'log': return g.log(this.safeLogArgument(this.first()));
-      case 'exp': return g.exp(this.boundedForExp(this.first()));
-      case 'sqrt': return g.sqrt(this.safeSqrtArgument(this.first()));
-      case 'neg': case 'relu': case 'tanh': return g[op](this.first());
-      case 'matmul': return this.matmul(this.first());
-      case 'sum': {
-        const x = this.first((s) => s.length >= 1);
-        return x === undefined ? undefined : g.sum(x, rng.int(0, g.shape(x).length - 1), rng.chance(0.4));
-      }
-      case 'softmax': case 'logSoftmax': {
-        const x = this.first((s) => s.length >= 1);
-        return x === undefined ? undefined : g[op](x, rng.int(0, g.shape(x).length - 1));
-      }
-      case 'broadcast': return this.broadcast(this.first());
-      case 'reshape': return this.reshape(this.first());
-      case 'transpose': {
-        const x = this.first((s) => s.length >= 2);
-        return x === undefined ? undefined : this.transpose(x);
-      }
-      default: throw new Error(`generator has no case for '${op}'`);
-    }
-  }
-
-  matmul(a0) {
-    const { g, rng } = this;
-    let a = a0;
+    let a = first;
     let as = g.shape(a);
     if (as.length < 2) {
-      const options = factorizations(size(as), 2);
-      const square = options.filter(([m, k]) => m > 1 && k > 1);
-      a = this.track(g.reshape(a, rng.pick(square.length && rng.chance(0.8) ? square : options)));
+      // A vector or scalar is first reshaped into a matrix, square-ish (80 %) where possible.
+      const all = factorizations(size(as), 2);
+      const square = all.filter(([m, k]) => m > 1 && k > 1);
+      const choice = square.length && rng.chance(0.8) ? square : all;
+      a = this.settle(g.reshape(a, rng.pick(choice)));
       as = g.shape(a);
     }
-    const batch = as.slice(0, -2);
-    const k = last(as), m = as[as.length - 2];
-    const n = this.dim();
+    const batch = as.slice(0, -2), m = as[as.length - 2], k = lastOf(as);
+    const n = this.dimension();
     if (size(batch.concat([m, n])) > MAX_SIZE || size(batch.concat([k, n])) > MAX_SIZE) return undefined;
-    const fits = (s) => s.length === as.length && s[s.length - 2] === k && batch.every((d, i) => d === s[i]) &&
-      size(batch.concat([m, last(s)])) <= MAX_SIZE;
+    const fitsB = (s) => s.length === as.length && s[s.length - 2] === k && batch.every((d, i) => d === s[i])
+      && size(batch.concat([m, lastOf(s)])) <= MAX_SIZE;
     let b;
-    if (this.strict) b = this.input(batch.concat([k, n]));
-    else {
-      b = rng.chance(0.3) ? this.choose(fits) : undefined;
-      if (b === undefined) b = this.leaf(batch.concat([k, n]));
+    if (this.strict) {
+      b = this.freshInput(batch.concat([k, n]));
+    } else {
+      if (rng.chance(0.3)) b = this.pickValue(fitsB);
+      if (b === undefined) b = this.freshLeaf(batch.concat([k, n]));
     }
     return g.matmul(a, b);
   }
 
-  broadcast(x) {
+  broadcastOf(x) {
     const { g, rng } = this;
     const xs = g.shape(x);
     const lead = [];
-    if (rng.chance(0.5)) for (let i = rng.int(1, 2); i > 0; i--) lead.push(rng.int(2, 4));
-    const to = lead.concat(xs.map((d) => (d === 1 && rng.chance(0.7) ? rng.int(2, 5) : d)));
-    if (to.length > 4 || size(to) > MAX_SIZE || sameShape(to, xs)) return undefined;
+    if (rng.chance(0.5)) for (let count = rng.int(1, 2); count > 0; count--) lead.push(rng.int(2, 4));
+    const stretched = xs.map((d) => (d === 1 && rng.chance(0.7) ? rng.int(2, 5) : d));
+    const to = lead.concat(stretched);
+    if (to.length > 4 || size(to) > MAX_SIZE || sameDims(to, xs)) return undefined;
     return g.broadcast(x, to);
   }
 
-  reshape(x) {
+  reshapeOf(x) {
     const { g, rng } = this;
-    const n = size(g.shape(x));
-    const all = factorizations(n, rng.int(1, 4)).filter((s) => s.length <= 4);
-    const wide = all.filter((s) => s.length >= 2 && last(s) > 1 && s[s.length - 2] > 1);
-    const shape = rng.pick(wide.length && rng.chance(this.strict ? 0.9 : 0.7) ? wide : all);
-    const id = g.reshape(x, shape);
+    const rank = rng.int(1, 4);
+    const all = factorizations(size(g.shape(x)), rank).filter((s) => s.length <= 4);
+    const wide = all.filter((s) => s.length >= 2 && lastOf(s) > 1 && s[s.length - 2] > 1);
+    const choice = wide.length && rng.chance(this.strict ? 0.9 : 0.7) ? wide : all;
+    const id = g.reshape(x, rng.pick(choice));
     return id === x ? undefined : id;
   }
 
-  transpose(x) {
+  transposeOf(x) {
     const { g, rng } = this;
-    const rank = g.shape(x).length;
-    let perm;
-    for (let t = 0; t < 10; t++) {
-      perm = rng.shuffle(Array.from({ length: rank }, (_, i) => i));
-      if (!perm.every((p, i) => p === i) && (!isInvolution(perm) || rng.chance(this.strict ? 0.1 : 0.3))) break;
+    const axes = Array.from({ length: g.shape(x).length }, (_, i) => i);
+    // Up to ten shuffles for a permutation that moves something; one that is its own
+    // inverse is taken only sometimes.
+    let perm = axes;
+    for (let tries = 0; tries < 10; tries++) {
+      perm = rng.shuffle(axes);
+      if (identity(perm)) continue;
+      if (!selfInverse(perm) || rng.chance(this.strict ? 0.1 : 0.3)) break;
     }
     const id = g.transpose(x, perm);
     return id === x ? undefined : id;
   }
 
-  /** x weighted elementwise by a new input of its shape, so its cotangent is not uniform. */
-  weigh(x) { return this.g.mul(x, this.input(this.g.shape(x))); }
+  /** x times a new input of its shape, so the cotangent reaching x is not uniform. */
+  weighted(x) { return this.g.mul(x, this.freshInput(this.g.shape(x))); }
 }
 
-/** Programs built around one op, placed on a path to the output and weighted after it. */
-const TARGETED = {
-  matmul(b) {
-    const rank = b.rng.chance(0.6) ? 2 : 3;
-    const batch = rank === 3 ? [b.rng.int(2, 3)] : [];
-    const m = b.rng.int(2, 5), k = b.rng.int(2, 5);
-    let x = b.input(batch.concat([m, k]));
-    for (let i = b.rng.int(1, 2); i > 0; i--) {
-      if (b.rng.chance(0.5)) x = b.push(b.g.tanh(x));
-      const y = b.matmul(x);
-      if (y === undefined || !b.ok(y)) break;
-      x = b.push(y);
+/** How each op is emitted, given the generator (its first operand forced or picked). */
+const EMIT = {
+  add: (s) => { const a = s.firstOperand(); return s.g.add(a, s.secondOperand(a)); },
+  sub: (s) => { const a = s.firstOperand(); return s.g.sub(a, s.secondOperand(a)); },
+  mul: (s) => { const a = s.firstOperand(); return s.g.mul(a, s.secondOperand(a)); },
+  div: (s) => { const a = s.firstOperand(); return s.g.div(a, s.awayFromZero(s.secondOperand(a))); },
+  log: (s) => s.g.log(s.logSafe(s.firstOperand())),
+  exp: (s) => s.g.exp(s.expSafe(s.firstOperand())),
+  sqrt: (s) => s.g.sqrt(s.sqrtSafe(s.firstOperand())),
+  neg: (s) => s.g.neg(s.firstOperand()),
+  relu: (s) => s.g.relu(s.firstOperand()),
+  tanh: (s) => s.g.tanh(s.firstOperand()),
+  matmul: (s) => s.matmulWith(s.firstOperand()),
+  sum: (s) => {
+    const x = s.firstOperand((sh) => sh.length >= 1);
+    if (x === undefined) return undefined;
+    const axis = s.rng.int(0, s.g.shape(x).length - 1);
+    return s.g.sum(x, axis, s.rng.chance(0.4));
+  },
+  softmax: (s) => {
+    const x = s.firstOperand((sh) => sh.length >= 1);
+    return x === undefined ? undefined : s.g.softmax(x, s.rng.int(0, s.g.shape(x).length - 1));
+  },
+  logSoftmax: (s) => {
+    const x = s.firstOperand((sh) => sh.length >= 1);
+    return x === undefined ? undefined : s.g.logSoftmax(x, s.rng.int(0, s.g.shape(x).length - 1));
+  },
+  broadcast: (s) => s.broadcastOf(s.firstOperand()),
+  reshape: (s) => s.reshapeOf(s.firstOperand()),
+  transpose: (s) => {
+    const x = s.firstOperand((sh) => sh.length >= 2);
+    return x === undefined ? undefined : s.transposeOf(x);
+  },
+};
+
+/**
+ * Emit `op` (its first operand `forced` when given) and keep it only if its result is
+ * provably within BOUND; otherwise undo everything it emitted. Returns the new value or
+ * undefined.
+ */
+function attempt(s, op, forced) {
+  const at = s.mark();
+  s.forced = forced;
+  const emit = EMIT[op];
+  if (!emit) throw new Error(`no emitter for '${op}'`);
+  const id = emit(s);
+  if (id === undefined) return undefined;
+  if (!s.bounded(id)) { s.rewind(at); return undefined; }
+  return s.offer(id);
+}
+
+/** Programs built around one op: the op on a path to the result, weighted after it. */
+const AROUND = {
+  matmul(s) {
+    const rank = s.rng.chance(0.6) ? 2 : 3;
+    const batch = rank === 3 ? [s.rng.int(2, 3)] : [];
+    const m = s.rng.int(2, 5), k = s.rng.int(2, 5);
+    let x = s.freshInput(batch.concat([m, k]));
+    for (let times = s.rng.int(1, 2); times > 0; times--) {
+      if (s.rng.chance(0.5)) x = s.offer(s.g.tanh(x));
+      const y = s.matmulWith(x);
+      if (y === undefined || !s.bounded(y)) break;
+      x = s.offer(y);
     }
     return x;
   },
-  transpose(b) {
-    const x0 = b.input(b.shape(3, 4));
-    const t0 = b.transpose(x0);
-    let x = b.push(t0 === undefined ? x0 : t0);
-    x = b.push(b.weigh(b.g.tanh(x)));
-    if (b.rng.chance(0.5)) { const t1 = b.transpose(x); x = b.push(t1 === undefined ? x : t1); }
+  transpose(s) {
+    const x0 = s.freshInput(s.randomShape(3, 4));
+    const t0 = s.transposeOf(x0);
+    let x = s.offer(t0 === undefined ? x0 : t0);
+    x = s.offer(s.weighted(s.g.tanh(x)));
+    if (s.rng.chance(0.5)) {
+      const t1 = s.transposeOf(x);
+      x = s.offer(t1 === undefined ? x : t1);
+    }
     return x;
   },
-  reshape(b) {
-    for (let t = 0; t < 10; t++) {
-      const x0 = b.input(b.shape(2, 4));
-      let x = b.push(b.g.tanh(x0));
-      const r = b.reshape(x);
+  reshape(s) {
+    for (let tries = 0; tries < 10; tries++) {
+      const x0 = s.freshInput(s.randomShape(2, 4));
+      let x = s.offer(s.g.tanh(x0));
+      const r = s.reshapeOf(x);
       if (r === undefined) continue;
-      x = b.push(r);
-      x = b.push(b.weigh(x));
-      if (b.rng.chance(0.4)) { const r2 = b.reshape(x); if (r2 !== undefined) x = b.push(r2); }
+      x = s.offer(s.weighted(s.offer(r)));
+      if (s.rng.chance(0.4)) {
+        const r2 = s.reshapeOf(x);
+        if (r2 !== undefined) x = s.offer(r2);
+      }
       return x;
     }
     throw new Error('no reshape in 10 tries');
   },
-  broadcast(b) {
-    for (let t = 0; t < 10; t++) {
-      const x0 = b.input(b.shape(1, 3).map((d) => (b.rng.chance(0.5) ? 1 : d)));
-      const y = b.broadcast(b.push(b.g.tanh(x0)));
+  broadcast(s) {
+    for (let tries = 0; tries < 10; tries++) {
+      const dims = s.randomShape(1, 3).map((d) => (s.rng.chance(0.5) ? 1 : d));
+      const y = s.broadcastOf(s.offer(s.g.tanh(s.freshInput(dims))));
       if (y === undefined) continue;
-      return b.push(b.weigh(b.push(y)));
+      return s.offer(s.weighted(s.offer(y)));
     }
     throw new Error('no broadcast in 10 tries');
   },
-  sum(b) {
-    const x0 = b.input(b.shape(2, 4));
-    const x = b.push(b.g.tanh(x0));
-    const axis = b.rng.int(0, b.g.shape(x).length - 1);
-    return b.push(b.weigh(b.push(b.g.sum(x, axis, b.rng.chance(0.4)))));
+  sum(s) {
+    const x = s.offer(s.g.tanh(s.freshInput(s.randomShape(2, 4))));
+    const axis = s.rng.int(0, s.g.shape(x).length - 1);
+    return s.offer(s.weighted(s.offer(s.g.sum(x, axis, s.rng.chance(0.4)))));
   },
 };
 
-/** Apply an op, keeping it only if its result is provably within BOUND (else unwind it). */
-function tryOp(b, op, operand) {
-  const before = b.g.nodes.length;
-  const id = b.apply(op, operand);
-  if (id === undefined) return undefined;
-  if (!b.ok(id)) {
-    b.g.nodes.length = before;
-    for (const k of Array.from(b.iv.keys())) if (k >= before) b.iv.delete(k);
-    b.pool = b.pool.filter((p) => p < before);
-    return undefined;
-  }
-  return b.push(id);
-}
-
 /**
- * A random program { seed, focus, graph, outputs, inputs, bounds }: general, or
- * built around `focus` (one of TARGETS); `f32` turns on the float32 guards.
+ * A random program { seed, focus, graph, outputs, inputs, bounds }: general, or built
+ * around `focus` (one of TARGETS). Options: f32 (the float32 guard), squareAware,
+ * withSqrt (sqrt among the general ops).
  */
 function randomProgram(seed, options) {
   const o = options || {};
   const focus = o.focus;
   const rng = new Rng(focus ? (seed * 31 + TARGETS.indexOf(focus) + 1) >>> 0 : seed);
-  const b = new ProgramBuilder(rng);
-  b.f32 = !!o.f32;
-  b.squareAware = !!o.squareAware;
+  const s = new Generator(rng, o);
   if (focus) {
-    b.strict = true;
-    let lastId = TARGETED[focus](b);
-    b.strict = false;
-    for (let i = rng.int(0, 2); i > 0; i--) {
-      const id = tryOp(b, rng.pick(['add', 'mul', 'tanh', 'exp', 'log', 'div', 'relu', 'sum', 'softmax']), lastId);
-      if (id !== undefined) lastId = id;
+    s.strict = true;
+    let result = AROUND[focus](s);
+    s.strict = false;
+    for (let more = rng.int(0, 2); more > 0; more--) {
+      const id = attempt(s, rng.pick(FOLLOW_UPS), result);
+      if (id !== undefined) result = id;
     }
   } else {
-    for (let i = rng.int(1, 3); i > 0; i--) b.input(b.shape());
+    for (let count = rng.int(1, 3); count > 0; count--) s.freshInput(s.randomShape());
     const weights = o.withSqrt ? Object.assign({}, GENERATED, { sqrt: 3 }) : GENERATED;
-    const ops = [];
-    for (const op of Object.keys(weights)) for (let w = 0; w < weights[op]; w++) ops.push(op);
-    const steps = rng.int(2, 10);
+    const bag = [];
+    for (const op of Object.keys(weights)) for (let w = 0; w < weights[op]; w++) bag.push(op);
+    const want = rng.int(2, 10);
     let made = 0;
-    for (let attempt = 0; made < steps && attempt < steps * 20; attempt++) {
-      if (tryOp(b, rng.pick(ops)) !== undefined) made++;
+    for (let tries = 0; made < want && tries < want * 20; tries++) {
+      if (attempt(s, rng.pick(bag)) !== undefined) made++;
     }
   }
-  const consumed = new Set();
-  for (const n of b.g.nodes) for (const i of n.inputs) consumed.add(i);
-  let outputs = b.g.nodes.filter((n) => n.op !== 'input' && n.op !== 'const' && !consumed.has(n.id)).map((n) => n.id);
-  if (outputs.length === 0) outputs = [last(b.pool)];
+  const read = new Set();
+  for (const n of s.g.nodes) for (const i of n.inputs) read.add(i);
+  let outputs = s.g.nodes.filter((n) => n.op !== 'input' && n.op !== 'const' && !read.has(n.id)).map((n) => n.id);
+  if (outputs.length === 0) outputs = [lastOf(s.pool)];
   return {
-    seed, focus: focus || null, graph: b.g, outputs, inputs: b.g.inputs().map((n) => n.attrs.name),
-    bounds: b.g.nodes.map((n) => (b.iv.has(n.id) ? b.iv.get(n.id) : interval(b.g, n.id, b.iv, b.squareAware))),
+    seed, focus: focus || null, graph: s.g, outputs, inputs: s.g.inputs().map((n) => n.attrs.name),
+    bounds: s.g.nodes.map((n) => (s.known.has(n.id) ? s.known.get(n.id) : interval(s.g, n.id, s.known, s.squares))),
   };
 }
 
-/** Corpus program i: general for odd i, targeted (cycling through TARGETS) for even i. */
+/** Corpus program i: general for odd i, targeted (TARGETS in turn) for even i. */
 function corpusProgram(i, options) {
   const o = options || {};
   if (i % 2 === 1) return randomProgram(i, o);
@@ -420,11 +463,11 @@ function corpusProgram(i, options) {
 }
 
 /**
- * The two graphs of corpus program i as the reference's fusion checks and GPU
- * fuzzer run them (src/fusion/measure-m4.js:27-40, src/gpu/harness-m4.js:126-142):
- * the program (float32 guards on) and its gradient graph, with inputs uniform in
- * [-2, 2] and cotangents uniform in [-1, 1] drawn from Rng(i * 7919 + 17), and
- * the ids each keeps (the outputs; the outputs and every gradient).
+ * The two graphs of corpus program i as the reference's fusion checks and GPU fuzzer
+ * run them (src/fusion/measure-m4.js:27-40, src/gpu/harness-m4.js:126-142): the program
+ * (float32 guard on) and its gradient graph, inputs uniform in [-2, 2] and cotangents
+ * uniform in [-1, 1] drawn from Rng(i·7919 + 17), with the ids each keeps (the outputs;
+ * the outputs and every gradient).
  */
 function corpusGraphs(i) {
   const { grad } = require('../autodiff');
