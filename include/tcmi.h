@@ -113,6 +113,23 @@ int tcmi_launch(uint64_t function, const uint32_t grid[3], const uint32_t block[
 /* Wait for all work on the library stream; reports (and latches) asynchronous faults. */
 int tcmi_sync(void);
 
+/* --- a launch that allocates nothing ---------------------------------------------
+ * No counterpart in the reference. For callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid it):
+ * tcmi_launch with the kernel's workspace (split-K partial sums, column-sum partials)
+ * taken from a fixed device array the library holds on each GPU from tcmi_init until
+ * the process ends, instead of a tcmi_malloc'd buffer. The 8 bytes at `scratch_offset`
+ * of the argument block (the workspace pointer, at byte 72 of the TcmiArgs layout) are
+ * replaced by that array's address before the launch; `scratch_bytes` is the workspace
+ * the launch's kernels use, at most TCMI_SCRATCH_BYTES (else TCMI_E_INVALID, nothing
+ * enqueued). Nothing is cleared: the kernels this library generates write every
+ * workspace element before they read it. Every call on one GPU shares the array and
+ * it keeps the last call's contents, so launches that use it must not overlap: they
+ * do not when issued on the library stream (in order), as these are. */
+#define TCMI_SCRATCH_BYTES (64ull << 20)
+int tcmi_launch_scratch(uint64_t function, const uint32_t grid[3], const uint32_t block[3], uint32_t lds_bytes,
+                        const void* args, uint64_t args_bytes, uint64_t scratch_offset, uint64_t scratch_bytes);
+
 /* --- launch graphs over several streams ----------------------------------------
  * No counterpart in the reference, whose launches go to one in-order WebGPU queue
  * (runtime.js:86-101); here independent launches of a launch list may overlap.

@@ -35,6 +35,11 @@
 
 #include "../../include/tcmi.h"
 
+// Device memory for tcmi_launch_scratch: a launch's workspace without an allocation.
+// Each GPU the library runs on holds its own copy from module load until the process
+// ends; its address is taken per device at tcmi_init (hipGetSymbolAddress).
+static __device__ __align__(256) unsigned char scratch[TCMI_SCRATCH_BYTES];
+
 namespace {
 
 thread_local std::string g_error;
@@ -50,6 +55,10 @@ hipStream_t g_side[kSideStreams] = {};
 hipEvent_t g_fork = nullptr;
 hipEvent_t g_join[kSideStreams] = {};
 std::vector<hipEvent_t> g_dag_events;
+// The device address of `scratch` (below) on each device, found once at tcmi_init with
+// the device current; host code uses these addresses, never the array's name.
+constexpr int kMaxDevices = 16;
+void* g_scratch[kMaxDevices] = {};
 // Pinned host staging for tcmi_graph_step's small copies (hipHostMalloc'd at init):
 // a pageable copy costs a staging round trip of its own in the runtime.
 constexpr uint64_t kStageBytes = 1u << 20;
@@ -314,6 +323,12 @@ int tcmi_init(void) {
   }
   HIP_TRY(hipEventCreateWithFlags(&g_fork, hipEventDisableTiming), "hipEventCreateWithFlags");
   HIP_TRY(hipHostMalloc(reinterpret_cast<void**>(&g_stage), kStageBytes, hipHostMallocDefault), "hipHostMalloc (staging)");
+  // This device's copy of the scratch array (tcmi_launch_scratch), with the device current.
+  if (g_device >= kMaxDevices) return fail(TCMI_E_INVALID, "tcmi_init: device index beyond the scratch table");
+  void* sp = nullptr;
+  HIP_TRY(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)), "hipGetSymbolAddress (scratch)");
+  if (!sp) return fail(TCMI_E_INVALID, "hipGetSymbolAddress (scratch) gave no address");
+  g_scratch[g_device] = sp;
   g_init = true;
   return TCMI_OK;
 }
@@ -514,6 +529,39 @@ int tcmi_launch(uint64_t function, const uint32_t grid[3], const uint32_t block[
   HIP_TRY(hipModuleLaunchKernel(it->second, grid[0], grid[1], grid[2], block[0], block[1], block[2], lds_bytes,
                                 g_stream, nullptr, args_bytes ? config : nullptr),
           "hipModuleLaunchKernel");
+  return TCMI_OK;
+}
+
+int tcmi_launch_scratch(uint64_t function, const uint32_t grid[3], const uint32_t block[3], uint32_t lds_bytes,
+                        const void* args, uint64_t args_bytes, uint64_t scratch_offset, uint64_t scratch_bytes) {
+  if (int rc = ready()) return rc;
+  auto it = g_functions.find(function);
+  if (it == g_functions.end()) return fail(TCMI_E_INVALID, "tcmi_launch_scratch: unknown function");
+  if (!grid || !block) return fail(TCMI_E_INVALID, "tcmi_launch_scratch: null grid or block");
+  if (int rc = check_launch_shape(grid, block, lds_bytes)) return rc;
+  constexpr uint64_t kMaxArgs = 4096;
+  if (args_bytes > kMaxArgs || !args) return fail(TCMI_E_INVALID, "tcmi_launch_scratch: bad argument block");
+  if (scratch_bytes > TCMI_SCRATCH_BYTES) {
+    std::ostringstream m;
+    m << "tcmi_launch_scratch: the launch needs " << scratch_bytes << " bytes of scratch, the library holds "
+      << TCMI_SCRATCH_BYTES << " per GPU";
+    return fail(TCMI_E_INVALID, m.str());
+  }
+  if (scratch_offset % 8 || scratch_offset > args_bytes || args_bytes - scratch_offset < 8)
+    return fail(TCMI_E_INVALID, "tcmi_launch_scratch: the scratch pointer's slot is outside the argument block");
+  void* base = g_scratch[g_device];
+  if (!base) return fail(TCMI_E_INVALID, "tcmi_launch_scratch: no scratch address for this device");
+  // The caller's block with the workspace slot pointing at this device's scratch; HIP
+  // copies the block into the launch when it is enqueued.
+  alignas(16) unsigned char block_copy[kMaxArgs];
+  std::memcpy(block_copy, args, args_bytes);
+  const uint64_t addr = reinterpret_cast<uint64_t>(base);
+  std::memcpy(block_copy + scratch_offset, &addr, sizeof addr);
+  size_t size = static_cast<size_t>(args_bytes);
+  void* config[] = {HIP_LAUNCH_PARAM_BUFFER_POINTER, block_copy, HIP_LAUNCH_PARAM_BUFFER_SIZE, &size, HIP_LAUNCH_PARAM_END};
+  HIP_TRY(hipModuleLaunchKernel(it->second, grid[0], grid[1], grid[2], block[0], block[1], block[2], lds_bytes, g_stream,
+                                nullptr, config),
+          "hipModuleLaunchKernel (scratch)");
   return TCMI_OK;
 }
 

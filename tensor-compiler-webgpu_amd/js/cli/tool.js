@@ -240,6 +240,10 @@ function precompileGroup(group, arch, shard, shards) {
     }
     return precompile(lists, arch);
   }
+  if (group === 'scratch') {
+    // The no-allocation entry point's GPU test: split-K matmuls, one translation unit.
+    return precompile(scratchLowerings(SCRATCH_SHAPES), arch);
+  }
   if (group === 'recompute') {
     // The recompute GPU tests: corpus programs 1..100 fused with recomputation (plain and
     // perf lowerings), and the fusion-loses workloads' fused and recompute variants in the
@@ -275,6 +279,18 @@ function precompileGroup(group, arch, shard, shards) {
     return precompile(lists, arch, (name) => parseInt(fnv(name), 16) % k === me);
   }
   throw new Error(`unknown precompile group '${group}'`);
+}
+
+/** Products whose K is split across workgroups (a workspace of partial sums): the scratch test's. */
+const SCRATCH_SHAPES = [[256, 4096, 256], [128, 2048, 128]];
+
+/** The plain lowering of matmul(x[M,K], w[K,N]) for each shape. */
+function scratchLowerings(shapes) {
+  return shapes.map(([M, K, N]) => {
+    const g = new Graph();
+    g.matmul(g.input('x', [M, K]), g.input('w', [K, N]));
+    return lowerMI355X(g);
+  });
 }
 
 /** The load modes (A, B) of a matmul launch's kernel, or null. */
@@ -1083,6 +1099,21 @@ async function main() {
         c3: (req.c3 || []).map((c) => { const g = cfg.c3Graphs(c.fn, c.R, c.C); return { fn: c.fn, R: c.R, C: c.C, forward: one(g.forward), gradient: one(g.gradient) }; }),
         c4: (req.c4 || []).map((c) => { const g = cfg.c4Graphs(c.act, c.M, c.K, c.N); return { act: c.act, M: c.M, K: c.K, N: c.N, forward: one(g.forward), gradient: one(g.gradient) }; }),
       };
+      break;
+    }
+    case 'scratch-kernels': {
+      // The split-K matmuls of the no-allocation entry point's test: one translation unit
+      // (as the build precompiles it), and per shape its kernels in launch order with their
+      // launch shapes, parameters and workspace bytes.
+      const { translationUnit } = require('../src/mi355x/runner');
+      const lists = scratchLowerings(SCRATCH_SHAPES);
+      const m = new Map();
+      for (const l of lists) for (const [name, src] of kernelSources(l)) m.set(name, src);
+      out = { unit: translationUnit(m), shapes: SCRATCH_SHAPES, launches: lists.map((l) => {
+        const x = l.launches[0];
+        return { workspace: l.workspace, params: Array.from(x.params),
+          kernels: x.kernels.map((k) => ({ name: k.name, grid: k.grid, block: k.block, lds: k.lds })) };
+      }) };
       break;
     }
     case 'kernel-unit': {

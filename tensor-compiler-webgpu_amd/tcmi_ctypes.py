@@ -50,6 +50,7 @@ PROTOTYPES = {
     "tcmi_function_attrs": ([u64, P(i32), P(i32), P(i32), P(i32)], ctypes.c_int),
     "tcmi_launch": ([u64, P(u32), P(u32), u32, ctypes.c_void_p, u64], ctypes.c_int),
     "tcmi_sync": ([], ctypes.c_int),
+    "tcmi_launch_scratch": ([u64, P(u32), P(u32), u32, ctypes.c_void_p, u64, u64, u64], ctypes.c_int),
     "tcmi_dag_reserve": ([u32], ctypes.c_int),
     "tcmi_launch_dag": ([u32, P(u64), P(u32), P(ctypes.c_uint8), P(u32), u32, P(ctypes.c_uint8), P(i32), P(u32), P(u32)],
                         ctypes.c_int),
