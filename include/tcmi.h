@@ -71,8 +71,11 @@ const char* tcmi_compile_options(void);
 
 /* --- memory (runtime.js:68-83,103-125; trainer-fused.js:72) ----------------- */
 
-/* Device allocation of `bytes`; the handle is the device address. Every copy
- * below is checked against the allocation's size before it is issued. */
+/* Device allocation of `bytes`; the handle is the device address, 256-byte
+ * aligned. Allocations of 1 MiB or more start at one of 16 staggered offsets
+ * (multiples of 4352 bytes) past their hipMalloc base, so that the operands of a
+ * streaming kernel do not meet the memory channels in step. Every copy below is
+ * checked against the allocation's size before it is issued. */
 int tcmi_malloc(uint64_t bytes, uint64_t* handle);
 int tcmi_free(uint64_t handle);
 /* Size in bytes of a live allocation (TCMI_E_INVALID if unknown). */
@@ -147,9 +150,10 @@ int tcmi_dag_reserve(uint32_t events);
  * slots waits[wait_begin[i] .. wait_begin[i + 1]), and records slot record_event[i]
  * after it (-1: none). The side streams first wait for all work already on the
  * library stream, and the library stream waits for every side stream at the end,
- * so the whole sequence is ordered against other work like one launch list (and is
- * captured into a HIP graph like one). Everything is checked before anything is
- * enqueued. */
+ * so the whole sequence is ordered against other work like one launch list.
+ * Everything is checked before anything is enqueued. With streams > 1 it is refused
+ * (TCMI_E_INVALID) while the library stream is being captured: capture over several
+ * streams is switched off; with one stream it is captured like any launch list. */
 int tcmi_launch_dag(uint32_t count, const uint64_t* functions, const uint32_t* dims, const uint8_t* args,
                     const uint32_t* offsets, uint32_t streams, const uint8_t* stream_of, const int32_t* record_event,
                     const uint32_t* wait_begin, const uint32_t* waits);

@@ -221,17 +221,19 @@ const indent = (lines, pad) => lines.map((l) => pad + l).join('\n');
 
 /**
  * A fused (or one-op) elementwise body over n output elements, output node
- * `output` of body graph `b`. A grid-stride loop over float4 groups with a
- * fixed, modest number of long-lived workgroups (`blocks`, default 2048 = 8
- * per CU): each trip a thread loads U groups spaced one grid apart (every
+ * `output` of body graph `b`. A grid-stride loop over float4 groups with at
+ * most `blocks` workgroups (below): each trip a thread loads U groups spaced one grid apart (every
  * operand load of all U issued before any arithmetic), computes, and stores
  * (non-temporally by default: the output is not re-read by this kernel). A
  * scalar tail handles n % 4. Operands read at the output index are float4
  * loads; a span load is a float4 when its 4 lanes are contiguous in the source,
  * one scalar when they share an element, else 4 scalars.
  * `tuning`: { unroll (U), nt (default true), blocks }. Defaults by size, from
- * whole-program sweeps on the MI355X: 2048 workgroups, U = 1 up to 2^25 elements
- * (config 2's 32 MB tensors: fewer workgroups or U = 2 lost up to 7 %); 512
+ * whole-program sweeps on the MI355X: up to 8192 workgroups, U = 1 below 2^25
+ * elements, so up to 2^23 elements every thread handles one group and the loop runs
+ * once (config 2's 32 MB tensors, with the runtime's staggered allocations: its
+ * step 5.79 -> 5.97-5.99 TB/s and its largest kernel read cold 5.18 -> 5.45 TB/s
+ * against 2048 workgroups; 1024 workgroups or U = 2 were slower on the step); 512
  * workgroups, U = 2 from 2^25 up (config 3's 268 MB tensors: 6 % faster over its
  * programs).
  */
@@ -242,7 +244,7 @@ function elementwiseKernel(b, output, outShape, opts) {
   const large = n >= 2 ** 25;
   const U = tune.unroll || (large ? 2 : 1);
   const nt = tune.nt === undefined ? true : !!tune.nt;
-  const maxBlocks = tune.blocks || (large ? 512 : 2048);
+  const maxBlocks = tune.blocks || (large ? 512 : 8192);
   checkOperands(b);
   if (n >= 2 ** 31) throw new Error(`elementwise kernel over ${n} elements exceeds the 32-bit index space`);
   const params = [n];

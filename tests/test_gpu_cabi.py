@@ -55,3 +55,36 @@ def test_graph_step_uploads_replays_and_reads_back():
     finally:
         for h in bufs.values():
             t.free(h)
+
+
+@pytest.mark.gpu
+def test_launch_dag_over_several_streams_is_refused_inside_a_capture():
+    """Capture over several streams is switched off in the C ABI itself: an empty
+    two-stream launch group is accepted eagerly and refused, with nothing enqueued,
+    while the library stream is capturing; the capture then ends normally."""
+    import tcmi_ctypes
+    t = tcmi_ctypes.load()
+    t.init()
+    lib = t.lib
+    assert lib.tcmi_launch_dag(0, None, None, None, None, 2, None, None, None, None) == 0, lib.tcmi_last_error()
+    t.sync()
+    h = tcmi_ctypes.u64()
+    t.malloc(1 << 12, ctypes.byref(h))
+    try:
+        t.capture_begin()
+        refused = lib.tcmi_launch_dag(0, None, None, None, None, 2, None, None, None, None)
+        message = lib.tcmi_last_error()
+        one_stream = lib.tcmi_launch_dag(0, None, None, None, None, 1, None, None, None, None)
+        t.fill32(h.value, 0, 7, 1 << 10)
+        g = tcmi_ctypes.u64()
+        t.capture_end(ctypes.byref(g))
+        assert refused == 10001 and b"stream capture" in message
+        assert one_stream == 0
+        t.graph_launch(g.value)
+        t.sync()
+        back = np.zeros(1 << 10, dtype=np.uint32)
+        t.d2h(back.ctypes.data, h.value, 0, 1 << 12)
+        assert np.all(back == 7)
+        t.graph_destroy(g.value)
+    finally:
+        t.free(h.value)
