@@ -58,7 +58,7 @@ function timeLaunches(runner, bench, program, reps) {
     const one = runner.prepare(program.graph, { launches: [l], workspace: program.lowered.workspace }, { buffers: program.bufs });
     const r = bench.time({ one }, { reps: reps || 5, warmup: 1, targetMs: 0.5, direct: true });
     out.push({ node: l.node, kind: l.kind, pattern: l.pattern || null, code: l.code, bytes: l.bytes, flops: l.flops,
-      us: r.stats.one.median, minUs: r.stats.one.min, maxUs: r.stats.one.max });
+      us: r.stats.one.median, minUs: r.stats.one.min, maxUs: r.stats.one.max, rowFolds: l.rowFolds || null });
     one.destroy();
   }
   return out;
@@ -69,27 +69,45 @@ function timeLaunches(runner, bench, program, reps) {
  * groups where fusion is neutral or slower: the group's fused launch timed alone against
  * the summed times of its members' unfused launches, each timed alone. A group wins or
  * loses only when the ranges do not overlap (the fused launch's min-max against the
- * members' summed mins and maxes).
+ * members' summed mins and maxes). A launch that also forms the reductions folded into
+ * it (the perf lowering's row folds) does their work as well: the unfused launches of
+ * those reductions (of their groups' members, where a reduction is a group's sink)
+ * count on its side too (`folded`: the reductions' node ids in the unfused graph).
  */
 function groupVerdicts(f, launchF, launchU) {
   const fusedAt = new Map(launchF.map((l) => [l.node, l]));
   const unfusedAt = new Map(launchU.map((l) => [l.node, l]));
+  const groupAt = new Map();
+  for (const g of f.groups) if (f.index.has(g.sink)) groupAt.set(f.index.get(g.sink), g);
+  const original = new Map();
+  for (const [id, fid] of f.index) if (!original.has(fid)) original.set(fid, id);
   const groups = [];
   for (const g of f.groups) {
     if (!f.index.has(g.sink)) continue;
     const fl = fusedAt.get(f.index.get(g.sink));
     if (!fl) continue;
+    const members = new Set(g.members);
+    const folded = [];
+    for (const rf of fl.rowFolds || []) {
+      const g2 = groupAt.get(rf.reduction);
+      if (g2 === g) continue;
+      const id = g2 ? g2.sink : original.get(rf.reduction);
+      if (id === undefined) continue;
+      folded.push(id);
+      if (g2) for (const m of g2.members) members.add(m);
+      else members.add(id);
+    }
     const sum = { median: 0, min: 0, max: 0 };
     let launches = 0;
-    for (const m of g.members) {
+    for (const m of members) {
       const u = unfusedAt.get(m);
       if (!u) continue;
       sum.median += u.us; sum.min += u.minUs; sum.max += u.maxUs; launches++;
     }
     if (!launches) continue;
     const v = verdict(sum, { median: fl.us, min: fl.minUs, max: fl.maxUs });
-    groups.push({ sink: g.sink, kind: g.kind, pattern: g.pattern, members: g.members.size, unfusedLaunches: launches,
-      fusedUs: fl.us, unfusedUs: sum.median, speedup: v.speedup, verdict: v.verdict });
+    groups.push({ sink: g.sink, kind: g.kind, pattern: g.pattern, members: members.size, unfusedLaunches: launches,
+      fusedUs: fl.us, unfusedUs: sum.median, speedup: v.speedup, verdict: v.verdict, folded: folded.length ? folded : undefined });
   }
   return groups;
 }

@@ -228,7 +228,8 @@ const indent = (lines, pad) => lines.map((l) => pad + l).join('\n');
  * scalar tail handles n % 4. Operands read at the output index are float4
  * loads; a span load is a float4 when its 4 lanes are contiguous in the source,
  * one scalar when they share an element, else 4 scalars.
- * `tuning`: { unroll (U), nt (default true), blocks }. Defaults by size, from
+ * `tuning`: { unroll (U), nt (default true), ntl (non-temporal loads of the full-size
+ * operands, default false), blocks }. Defaults by size, from
  * whole-program sweeps on the MI355X: up to 8192 workgroups, U = 1 below 2^25
  * elements, so up to 2^23 elements every thread handles one group and the loop runs
  * once (config 2's 32 MB tensors, with the runtime's staggered allocations: its
@@ -244,6 +245,10 @@ function elementwiseKernel(b, output, outShape, opts) {
   const large = n >= 2 ** 25;
   const U = tune.unroll || (large ? 2 : 1);
   const nt = tune.nt === undefined ? true : !!tune.nt;
+  // Non-temporal loads: every full-size operand (tuning ntl), or those at the positions
+  // `o.lastReads` lists (the lowering's last reads of their buffers).
+  const ntlAt = new Set(tune.ntl ? [] : (o.lastReads || []));
+  const ntl = (k) => !!tune.ntl || ntlAt.has(k);
   const maxBlocks = tune.blocks || (large ? 512 : 8192);
   checkOperands(b);
   if (n >= 2 ** 31) throw new Error(`elementwise kernel over ${n} elements exceeds the 32-bit index space`);
@@ -264,7 +269,11 @@ function elementwiseKernel(b, output, outShape, opts) {
   };
   const vecEmitter = new Emitter(b, params, {
     load(k, ctx, lines) {
-      if (ctx.root) return `${hoistAs(`full${k}`, 'tcmi::f4', `reinterpret_cast<const tcmi::f4*>(A.in[${k}])[v]`)}[j][l]`;
+      if (ctx.root) {
+        const load = ntl(k) ? `__builtin_nontemporal_load(reinterpret_cast<const tcmi::f4*>(A.in[${k}]) + v)`
+          : `reinterpret_cast<const tcmi::f4*>(A.in[${k}])[v]`;
+        return `${hoistAs(`full${k}`, 'tcmi::f4', load)}[j][l]`;
+      }
       const g = ctx.gather;
       if (ctx.parent && ctx.parent.root && g) {
         if (g.g.mode === 'zero') return `${hoistAs(`zero${k}`, 'float', `A.in[${k}][0]`)}[j]`;

@@ -90,7 +90,7 @@ function widenInputs(body, output, folds) {
 }
 
 /** Kernels for one node. */
-function lowerNode(graph, node, opts, mmViews, folds, rowFold) {
+function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads) {
   if (rowFold) {
     // A row-statistics chain with its reductions folded in: the rowwise kernel of the
     // reductions, with their own tuning so the rows are reduced in their order.
@@ -108,7 +108,8 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold) {
     const tuning = opts.tuning || {};
     const sab = { sabotage: opts.sabotage, pattern: node.attrs.pattern };
     if (kind === 'elementwise') {
-      return Object.assign({ kind: 'fused-elementwise' }, single(cg.elementwiseKernel(b, out, node.shape, Object.assign({ tuning: tuning.ew }, sab))));
+      return Object.assign({ kind: 'fused-elementwise' },
+        single(cg.elementwiseKernel(b, out, node.shape, Object.assign({ tuning: tuning.ew, lastReads }, sab))));
     }
     if (kind === 'rowwise') return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(b, out, Object.assign({ tuning: tuning.row }, sab))));
     if (kind === 'epilogue') return Object.assign({ kind: 'fused-epilogue' }, single(cg.gemmKernel(b, out, Object.assign({ tuning: tuning.gemm }, sab, mmViews))));
@@ -119,7 +120,7 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold) {
     const one = oneOpBody(graph, node);
     const { body, output } = widenInputs(one.body, one.output, folds);
     const kind = GATHERS.has(node.op) ? 'gather' : 'elementwise';
-    return Object.assign({ kind }, single(cg.elementwiseKernel(body, output, node.shape, { tuning: (opts.tuning || {}).ew })));
+    return Object.assign({ kind }, single(cg.elementwiseKernel(body, output, node.shape, { tuning: (opts.tuning || {}).ew, lastReads })));
   }
   if (node.op === 'sum' || node.op === 'max') {
     const inShape = graph.nodes[node.inputs[0]].shape;
@@ -343,6 +344,9 @@ function foldReductions(body, output, folds) {
  * scratch the largest launch needs; aliases: [[node, source]]; folded and dead: node
  * ids with neither a launch nor a buffer; batches, perf only: [{ start, count, kernels, wsStride }]).
  */
+/** Bytes from which a last read is streamed (non-temporal loads): 1 MiB. */
+const STREAM_FROM = 1 << 20;
+
 function lowerMI355X(graph, options) {
   const opts = options || {};
   if (opts.perf && !opts.keep) throw new Error('the perf lowering needs `keep`: the nodes whose values are read');
@@ -351,9 +355,32 @@ function lowerMI355X(graph, options) {
   const cache = new Map();
   const launches = [];
   let workspace = 0;
+  const launched = (node) => node.op !== 'input' && node.op !== 'const' && !plan.aliases.has(node.id)
+    && !plan.folded.has(node.id) && !plan.dead.has(node.id);
+  const resolve = (id) => (plan.aliases.has(id) ? plan.aliases.get(id) : id);
+  // The buffers a launch reads, operand by operand: a reshape's buffer is its source's,
+  // and an operand read through a view, a folded broadcast or a folded reduction is
+  // read from the node it stands for.
+  const inputsOf = (node) => {
+    const inputs = node.inputs.map(resolve);
+    const v = plan.views.get(node.id);
+    if (v) for (const s of Object.values(v)) inputs[s.pos] = resolve(s.source);
+    const folds = plan.broadcasts.get(node.id);
+    if (folds) for (const [pos, f] of folds) inputs[pos] = resolve(f.source);
+    const rowFold = plan.rowFolds.get(node.id);
+    if (rowFold) for (const f of rowFold) for (const pos of f.pos) inputs[pos] = resolve(graph.nodes[f.red].inputs[0]);
+    return inputs;
+  };
+  // Last reads (perf lowering): an elementwise kernel loads a full-size operand of
+  // STREAM_FROM bytes or more non-temporally where no later launch of the list reads
+  // that buffer, so data read for the last time streams past the caches instead of
+  // displacing data still to be read. A hint only: the values loaded are the same.
+  // Smaller buffers stay cached: streaming them saves nothing, and a repeated launch
+  // of a small kernel would miss where it hits.
+  const lastRead = new Map();
+  if (opts.perf) for (const node of graph.nodes) if (launched(node)) for (const id of inputsOf(node)) lastRead.set(id, node.id);
   for (const node of graph.nodes) {
-    if (node.op === 'input' || node.op === 'const') continue;
-    if (plan.aliases.has(node.id) || plan.folded.has(node.id) || plan.dead.has(node.id)) continue;
+    if (!launched(node)) continue;
     const v = plan.views.get(node.id);
     let mmViews = null;
     if (v) {
@@ -365,17 +392,18 @@ function lowerMI355X(graph, options) {
     const rowFold = plan.rowFolds.get(node.id) || null;
     const rowKey = rowFold ? rowFold.map((f) => [f.pos, graph.nodes[f.red].op, graph.nodes[f.red].attrs,
       graph.nodes[graph.nodes[f.red].inputs[0]].shape]) : null;
-    // Kernels depend on structure, shapes, operand views and folded broadcasts only: reuse across identical nodes.
+    const inputs = inputsOf(node);
+    const lastReads = [];
+    inputs.forEach((id, pos) => {
+      if (lastRead.get(id) === node.id && size(graph.nodes[id].shape) * 4 >= STREAM_FROM) lastReads.push(pos);
+    });
+    // Kernels depend on structure, shapes, operand views, folded broadcasts and last
+    // reads only: reuse across identical nodes.
     const key = JSON.stringify([node.op, node.inputs.map((id) => graph.nodes[id].shape), node.attrs, node.shape,
-      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey, rowKey]);
+      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey, rowKey, lastReads]);
     let k = cache.get(key);
-    if (!k) { k = lowerNode(graph, node, opts, mmViews, folds, rowFold); cache.set(key, k); }
+    if (!k) { k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads); cache.set(key, k); }
     workspace = Math.max(workspace, k.workspace);
-    const resolve = (id) => (plan.aliases.has(id) ? plan.aliases.get(id) : id);
-    const inputs = node.inputs.map(resolve);
-    if (v) for (const s of Object.values(v)) inputs[s.pos] = resolve(s.source);
-    if (folds) for (const [pos, f] of folds) inputs[pos] = resolve(f.source);
-    if (rowFold) for (const f of rowFold) for (const pos of f.pos) inputs[pos] = resolve(graph.nodes[f.red].inputs[0]);
     launches.push({
       node: node.id, op: node.op, kind: k.kind, pattern: node.op === 'fused' ? node.attrs.pattern : undefined,
       inputs, params: k.params, grid: k.kernels[0].grid, code: k.kernels[0].name,
