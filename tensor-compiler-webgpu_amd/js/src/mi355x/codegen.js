@@ -376,6 +376,9 @@ const isReduce = (n) => n.op === 'sum' || n.op === 'max';
  */
 function rowwiseKernel(b, output, opts) {
   const o = opts || {};
+  // Operand positions whose full-size loads are the lowering's last reads of their
+  // buffers: loaded non-temporally (row length a multiple of 4 only).
+  const streamed = new Set(o.lastReads || []);
   checkOperands(b);
   const reductions = b.nodes.filter(isReduce);
   if (!reductions.length) throw new Error('rowwise kernel without a reduction');
@@ -430,7 +433,15 @@ function rowwiseKernel(b, output, opts) {
         if (!caches.has(ck)) {
           const c = `X${caches.size}`;
           caches.set(ck, c);
-          if (vec) {
+          if (vec && streamed.has(k)) {
+            // The lowering's last read of this buffer: streamed past the caches.
+            cacheDecl.push(`float4 ${c}[${E}];`,
+              `#pragma unroll`,
+              `for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = (ln + s * ${T}u) * 4u;`,
+              `  tcmi::f4 t = {0.f, 0.f, 0.f, 0.f};`,
+              `  if (c0 < C) t = __builtin_nontemporal_load(reinterpret_cast<const tcmi::f4*>(A.in[${k}] + rowBase) + (c0 >> 2));`,
+              `  ${c}[s] = make_float4(t[0], t[1], t[2], t[3]); }`);
+          } else if (vec) {
             cacheDecl.push(`float4 ${c}[${E}];`,
               `#pragma unroll`,
               `for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = (ln + s * ${T}u) * 4u;`,

@@ -98,7 +98,7 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads) {
       shape: graph.nodes[f.red].shape, inShape: graph.nodes[graph.nodes[f.red].inputs[0]].shape }));
     const f = foldReductions(bodyOf(node), node.attrs.output, folds);
     const t = opts.tuning || {};
-    return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(f.body, f.output, { tuning: t.rowreduce || t.row })));
+    return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(f.body, f.output, { tuning: t.rowreduce || t.row, lastReads })));
   }
   if (node.op === 'fused') {
     const w = widenInputs(bodyOf(node), node.attrs.output, folds);
@@ -111,7 +111,9 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads) {
       return Object.assign({ kind: 'fused-elementwise' },
         single(cg.elementwiseKernel(b, out, node.shape, Object.assign({ tuning: tuning.ew, lastReads }, sab))));
     }
-    if (kind === 'rowwise') return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(b, out, Object.assign({ tuning: tuning.row }, sab))));
+    if (kind === 'rowwise') {
+      return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(b, out, Object.assign({ tuning: tuning.row, lastReads }, sab))));
+    }
     if (kind === 'epilogue') return Object.assign({ kind: 'fused-epilogue' }, single(cg.gemmKernel(b, out, Object.assign({ tuning: tuning.gemm }, sab, mmViews))));
     if (kind === 'attention') return Object.assign({ kind: 'fused-attention' }, single(cg.attentionKernel(b, out, Object.assign({}, mmViews))));
     throw new Error(`no MI355X kernel for fused kind '${kind}'`);
@@ -130,7 +132,7 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads) {
       // A reduction over the last non-trivial axis: the rowwise kernel on [outer, n].
       const { body, output } = oneOpBody(graph, node, [[outer, n]], { axis: 1, keepDims: true });
       const t = opts.tuning || {};
-      return Object.assign({ kind: 'rowreduce' }, single(cg.rowwiseKernel(body, output, { tuning: t.rowreduce || t.row })));
+      return Object.assign({ kind: 'rowreduce' }, single(cg.rowwiseKernel(body, output, { tuning: t.rowreduce || t.row, lastReads })));
     }
     const c = cg.colreduceKernels(node.op, outer, n, inner, (opts.tuning || {}).colreduce);
     return { kind: 'colreduce', kernels: c.launches, params: c.params, workspace: c.workspace, flops: 0 };
@@ -371,7 +373,7 @@ function lowerMI355X(graph, options) {
     if (rowFold) for (const f of rowFold) for (const pos of f.pos) inputs[pos] = resolve(graph.nodes[f.red].inputs[0]);
     return inputs;
   };
-  // Last reads (perf lowering): an elementwise kernel loads a full-size operand of
+  // Last reads (perf lowering): an elementwise or rowwise kernel loads a full-size operand of
   // STREAM_FROM bytes or more non-temporally where no later launch of the list reads
   // that buffer, so data read for the last time streams past the caches instead of
   // displacing data still to be read. A hint only: the values loaded are the same.
