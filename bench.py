@@ -364,6 +364,10 @@ def compose(full: dict) -> dict:
     extra["device"] = full["device"].get("name") or full["device"].get("arch")
     traffic, traffic_src = profiled_traffic(dom["code"])
     read_ceiling = ceiling["read"]["gbs"] if ceiling else None
+    # A cold figure above the pure-read ceiling measured in the same run (2 % for run
+    # to run spread) cannot be HBM alone: it is marked, not reported as an HBM figure.
+    above = bool(read_ceiling) and dom["gbs"] > 1.02 * read_ceiling
+    timing = "cold: operands read from HBM" if not above else "cold, but above the measured read ceiling: cache-assisted"
     line = {
         "metric": METRIC, "value": c2["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": c2["steps"], "warmup": c2["warmup"],
         "ms_per_step": c2["msPerStep"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -373,8 +377,8 @@ def compose(full: dict) -> dict:
                    "streams": c2["schedule"]["streams"]},
         "roofline": {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK, "unit": "GB/s", "frac": dom["gbs"] / HBM_PEAK,
                      "traffic": traffic, "traffic_source": traffic_src, "kernel": dom["code"], "kernel_avg_us": dom["avgUs"],
-                     "bytes_per_launch": dom["bytesPerLaunch"], "timing": "cold: operands read from HBM",
-                     "warm_achieved": dom["warm"]["gbs"], "read_ceiling": read_ceiling},
+                     "bytes_per_launch": dom["bytesPerLaunch"], "timing": timing,
+                     "warm_achieved": dom["warm"]["gbs"], "read_ceiling": read_ceiling, "above_read_ceiling": above},
         "extra": extra,
     }
     return line

@@ -46,6 +46,7 @@ def test_roofline_is_the_cold_figure_of_the_named_kernel(line):
     assert rf["frac"] == pytest.approx(rf["achieved"] / rf["peak"])
     # Cold: below the pure-read ceiling measured in the same run, and below the warm figure.
     assert rf["achieved"] <= rf["read_ceiling"] and rf["achieved"] < rf["warm_achieved"]
+    assert rf["above_read_ceiling"] is False and rf["timing"].startswith("cold: operands read from HBM")
     # The rotation spans several times the 256 MB last-level cache.
     assert dom["cold"]["spanBytes"] >= 4 * 256 * 2 ** 20
     traffic, src = bench.profiled_traffic(rf["kernel"])
@@ -68,3 +69,15 @@ def test_every_config_is_carried_compactly(line):
     assert all(0 < v["frac_fwd"] < 1 for v in ex["c4"].values())
     assert ex["sweep"]["timed"] == ex["sweep"]["gate_pass"] <= ex["sweep"]["workloads"]
     assert len(json.dumps(r, separators=(",", ":"))) < 6000
+
+
+def test_a_cold_figure_above_the_read_ceiling_is_marked():
+    """compose() marks a roofline figure above the pure-read ceiling of the same run as
+    cache-assisted instead of reporting it as an HBM figure (planted: the document's cold
+    figure raised to 1.1 times the ceiling)."""
+    import bench
+    doc = json.loads((ROOT / "tests" / "golden" / "bench_document.json").read_text())
+    ceiling = doc["configs"]["ceiling"]["read"]["gbs"]
+    doc["configs"]["c2"]["dominant"]["gbs"] = 1.1 * ceiling
+    rf = bench.compose(doc)["roofline"]
+    assert rf["above_read_ceiling"] is True and "cache-assisted" in rf["timing"]
