@@ -73,12 +73,34 @@ struct DenseView {
 // epilogue. MODE_C needs C % 4 == 0 and MODE_R needs R % 4 == 0 (R, C: the
 // operand's extents), and both need every other stride a multiple of 4, so a
 // 128-bit load is aligned and either wholly inside the operand or wholly out.
+// A workgroup's (x, y, z) place in its launch's grid.
+struct Wg {
+  uint32_t x, y, z;
+};
+
+// Workgroups grouped by XCD for split-K launches. The G = gridDim.x * gridDim.y tiles
+// of one z index (one K chunk of one product) read the same A and B panels; the
+// hardware hands a launch's workgroups to the 8 XCDs in turn by linear id L, so L
+// runs on XCD L % 8, and consecutive tiles would land on 8 different L2 caches.
+// Here z index q = L % 8 + 8 * (L / (8 * G)) and tile t = (L / 8) % G: every tile of
+// one z index runs on one XCD. A bijection of [0, G * gridDim.z) when gridDim.z is a
+// multiple of 8 (launch order kept otherwise), so every (tile, z) is computed once,
+// by the same code: only which workgroup computes it changes, not the result.
+__device__ __forceinline__ Wg xcd_grouped() {
+  const uint32_t gx = gridDim.x, gy = gridDim.y, nz = gridDim.z, G = gx * gy;
+  if (nz % 8u != 0u) return {blockIdx.x, blockIdx.y, blockIdx.z};
+  const uint32_t L = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const uint32_t rest = L / 8u, t = rest % G;
+  return {t % gx, t / gx, L % 8u + 8u * (rest / G)};
+}
+
 template <int TM, int TN, int BK, int PF, int AMODE, int BMODE, bool SPLIT, class AV, class BV, class Epi, int WN = 2,
           bool PRIO = false, int KW = 1, class Args = TcmiArgs>
 __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict__ a_ptr,
                                          const float* __restrict__ b_ptr, const uint32_t batch, const uint32_t M,
                                          const uint32_t K, const uint32_t N, const uint32_t chunks,
-                                         const uint32_t chunkK, const uint32_t zid) {
+                                         const uint32_t chunkK, const uint32_t zid, const uint32_t tx,
+                                         const uint32_t ty) {
   // KW groups of 2 x WN wavefronts; in each group a wavefront owns (TM·16) x (TN·16)
   // of the BM x BN tile, and group g sums its own part of K (see below).
   static_assert(KW == 1 || KW == 2 || KW == 4, "K groups");
@@ -95,7 +117,8 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
   __shared__ __attribute__((aligned(16))) float Bs_[KW][2][(B_NMAJOR ? BN : BK) * BS];
 
   // zid: the workgroup's z index within this launch (blockIdx.z, or its part
-  // below the member index in a batched launch).
+  // below the member index in a batched launch); (tx, ty): its output tile's column
+  // and row (blockIdx.x and .y, or their XCD-grouped places).
   const uint32_t kz = SPLIT ? zid % chunks : 0u;
   const uint32_t bz = SPLIT ? zid / chunks : zid;
   const uint32_t kbeg0 = SPLIT ? kz * chunkK : 0u;
@@ -111,7 +134,7 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
   const uint32_t kend = min(kend0, kbeg + sub);
   float (*As)[(A_KMAJOR ? BK : BM) * AS] = As_[kg];
   float (*Bs)[(B_NMAJOR ? BN : BK) * BS] = Bs_[kg];
-  const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const uint32_t m0 = ty * BM, n0 = tx * BN;
   const float* __restrict__ Ab = a_ptr + AV::batch(bz);
   const float* __restrict__ Bb = b_ptr + BV::batch(bz);
 
@@ -413,6 +436,17 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
 // workspace, added in chunk order — the value gemm_splitk_reduce forms for j itself.
 // An epilogue that reads the product at another element's index (a recomputed
 // broadcast or transpose of it) reads it here.
+// The tile of each workgroup at its launch place (blockIdx.x, blockIdx.y).
+template <int TM, int TN, int BK, int PF, int AMODE, int BMODE, bool SPLIT, class AV, class BV, class Epi, int WN = 2,
+          bool PRIO = false, int KW = 1, class Args = TcmiArgs>
+__device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict__ a_ptr,
+                                         const float* __restrict__ b_ptr, const uint32_t batch, const uint32_t M,
+                                         const uint32_t K, const uint32_t N, const uint32_t chunks,
+                                         const uint32_t chunkK, const uint32_t zid) {
+  gemm_f32<TM, TN, BK, PF, AMODE, BMODE, SPLIT, AV, BV, Epi, WN, PRIO, KW, Args>(A, a_ptr, b_ptr, batch, M, K, N, chunks,
+                                                                               chunkK, zid, blockIdx.x, blockIdx.y);
+}
+
 template <class Args>
 __device__ __forceinline__ float gemm_product_at(const Args& A, uint32_t j, uint32_t total, uint32_t chunks) {
   float acc = A.ws[j];

@@ -24,6 +24,7 @@
 //   gpu-workloads    request {ids?, families?, allNodes?}: the workload sweep's variants run once, outputs for the gate
 //   gpu-bench-selftest  the timing protocol's counters: a clean timed region, a planted leak that must trip
 //   gpu-step-slices  request {model, B, sequences}: a full-batch step's launches with their operands, as per-sequence blocks
+//   grouped-batches  request {model, B}: the batched kernels of a step's split-K products, with their text
 
 const fs = require('fs');
 const fs_ = fs;
@@ -304,8 +305,9 @@ function gemmModes(l) {
 
 /** The K split (chunks, chunk length) of a matmul launch's kernel, or null. */
 function gemmSplit(l) {
-  // gemm_f32<...>(A, a, b, batch, M, K, N, chunks, chunkK, zid)
-  const m = l.kernels[0].source.match(/(\d+)u, (\d+)u, blockIdx\.z\);/);
+  // gemm_f32<...>(A, a, b, batch, M, K, N, chunks, chunkK, zid[, tx, ty]): zid is
+  // blockIdx.z, or wg.z (with wg.x, wg.y) where the tiles take XCD-grouped places.
+  const m = l.kernels[0].source.match(/(\d+)u, (\d+)u, (?:blockIdx\.z|wg\.z, wg\.x, wg\.y)\);/);
   return l.flops && m ? [Number(m[1]), Number(m[2])] : null;
 }
 
@@ -1237,6 +1239,26 @@ async function main() {
           }
         }
       }
+      break;
+    }
+    case 'grouped-batches': {
+      // The batched forms of a model step's split-K products (their workgroups take
+      // XCD-grouped places): each batched kernel's text and its members' z extent.
+      const { modelStep } = require('../src/builders/models');
+      const { fusedStep } = require('../src/mi355x/trainer');
+      const { kernelSources } = require('../src/mi355x/lower');
+      const fs = fusedStep(modelStep(req).step);
+      const src = kernelSources(fs.lowered);
+      const kernels = [];
+      let batches = 0;
+      for (const b of fs.lowered.batches || []) {
+        const l = fs.lowered.launches[b.start];
+        if (!(l.kernels.length === 2 && /_red$/.test(l.kernels[1].name))) continue;
+        batches++;
+        const k = b.kernels[0];
+        kernels.push({ name: k.name, z: l.kernels[0].grid[2], source: src.get(k.name) });
+      }
+      out = { batches, kernels };
       break;
     }
     case 'batch-check': {

@@ -833,9 +833,14 @@ ${indent(lines, '    ')}
 `;
   const threads = 128 * tl.wn * tl.kw;
   const variant = tl.kw > 1 ? `, ${tl.wn}, ${tl.prio}, ${tl.kw}` : tl.wn === 2 && !tl.prio ? '' : `, ${tl.wn}, ${tl.prio}`;
+  // A launch split along K places the tiles of each chunk on one XCD (tcmi::xcd_grouped),
+  // so they share its L2 for the A and B panels they all read.
+  const grouped = tl.chunks > 1;
+  const place = grouped ? ', wg.z, wg.x, wg.y' : ', blockIdx.z';
   const main = `extern "C" __global__ void __launch_bounds__(${threads}) __KERNEL__(const TcmiArgs A) {
-  tcmi::gemm_f32<${T}, ${T}, ${tl.bk}, ${tl.pf}, ${av.mode}, ${bv.mode}, ${split}, __KERNEL___av, __KERNEL___bv, __KERNEL___epi${variant}>(A, A.in[${ia}], A.in[${ib}],
-      ${batch}u, ${M}u, ${K}u, ${N}u, ${tl.chunks}u, ${tl.chunkK}u, blockIdx.z);
+${grouped ? `  ${XCD_GROUPED}
+` : ''}  tcmi::gemm_f32<${T}, ${T}, ${tl.bk}, ${tl.pf}, ${av.mode}, ${bv.mode}, ${split}, __KERNEL___av, __KERNEL___bv, __KERNEL___epi${variant}>(A, A.in[${ia}], A.in[${ib}],
+      ${batch}u, ${M}u, ${K}u, ${N}u, ${tl.chunks}u, ${tl.chunkK}u${place});
 }
 `;
   const text = `#include "tcmi_gemm.h"\n${av.text}${bv.text}${epi}${main}`;
@@ -1074,6 +1079,9 @@ function batchable(k, count) {
  * of an attention layer and their weight gradients) fills the chip with one
  * launch's workgroups instead of paying a launch's ramp and drain each.
  */
+/** The statement that opens a kernel whose workgroups take XCD-grouped places. */
+const XCD_GROUPED = 'const tcmi::Wg wg = tcmi::xcd_grouped();';
+
 function batchedKernel(k, count) {
   if (!batchable(k, count)) throw new Error(`kernel ${k.name} cannot be batched ${count} times`);
   if (!(Number.isInteger(count) && count >= 2 && count <= MAX_BATCH)) throw new Error(`batch of ${count} launches (2..${MAX_BATCH})`);
@@ -1082,9 +1090,14 @@ function batchedKernel(k, count) {
   if (k.source.split(sig).length !== 2) throw new Error(`kernel ${k.name}: no single entry point to batch`);
   if (/gridDim\.z/.test(k.source)) throw new Error(`kernel ${k.name} reads gridDim.z`);
   const Z = k.grid[2];
-  const [head, tail] = k.source.split(sig);
-  const ownZ = (t) => t.split('blockIdx.z').join(`(blockIdx.z % ${Z}u)`);
-  const entry = `__KERNEL__${suffix || ''}(const TcmiBatch<${count}> B) {\n  const TcmiPtrs& A = B.m[blockIdx.z / ${Z}u];`;
+  const [head, body] = k.source.split(sig);
+  // A member taking an XCD-grouped place: the place is taken over the whole batched
+  // grid, and its z index chooses the member as blockIdx.z does otherwise.
+  const grouped = body.includes(`  ${XCD_GROUPED}\n`);
+  const tail = grouped ? body.replace(`  ${XCD_GROUPED}\n`, '') : body;
+  const z = grouped ? 'wg.z' : 'blockIdx.z';
+  const ownZ = (t) => t.split(z).join(`(${z} % ${Z}u)`);
+  const entry = `__KERNEL__${suffix || ''}(const TcmiBatch<${count}> B) {\n${grouped ? `  ${XCD_GROUPED}\n` : ''}  const TcmiPtrs& A = B.m[${z} / ${Z}u];`;
   const text = (ownZ(head) + entry + ownZ(tail)).split(base).join('__KERNEL__');
   const b = kernelText(`b${k.name.split('_')[1]}`, text);
   return { name: b.name + (suffix || ''), source: b.source, grid: [k.grid[0], k.grid[1], Z * count], block: k.block.slice(), lds: k.lds,

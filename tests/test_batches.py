@@ -52,10 +52,31 @@ def test_same_text_over_another_grid_is_not_batched(tool):
 def test_headers_never_read_the_z_index():
     """A batched kernel is the member kernel's text with its z index rewritten to
     blockIdx.z % Z: that is complete only if no device header reads blockIdx.z or
-    gridDim.z itself (the matmul takes its z index as an argument)."""
+    gridDim.z itself (the matmul takes its z index as an argument). The one exception
+    is tcmi::xcd_grouped, which places a workgroup over the whole launch's grid on
+    purpose; a batched kernel that calls it chooses its member from that place's z
+    index (test_xcd_grouped_batches_choose_members_by_place)."""
     import pathlib
     import re
     kernels = pathlib.Path(__file__).resolve().parents[1] / "tensor-compiler-webgpu_amd" / "csrc" / "kernels"
+    grouped = 0
     for h in sorted(kernels.glob("*.h")):
         code = "\n".join(line.split("//")[0] for line in h.read_text().splitlines())
+        code, n = re.subn(r"__device__ __forceinline__ Wg xcd_grouped\(\) \{.*?\n\}", "", code, flags=re.S)
+        grouped += n
         assert not re.search(r"\b(blockIdx|gridDim)\.z\b", code), h.name
+    assert grouped == 1
+
+
+def test_xcd_grouped_batches_choose_members_by_place(tool):
+    """Config 5's weight gradients are split-K products batched 16 and 4 at a time:
+    each member kernel takes its place from tcmi::xcd_grouped, and its batched form
+    takes that place once, over the whole batched grid, chooses the member by the
+    place's z index and hands the member the rest of it, never blockIdx.z."""
+    r = tool("grouped-batches", {"model": "transformer", "B": 64})
+    assert r["batches"] >= 3, r
+    for k in r["kernels"]:
+        src = k["source"]
+        assert src.count("const tcmi::Wg wg = tcmi::xcd_grouped();") == 1, k["name"]
+        assert f"B.m[wg.z / {k['z']}u]" in src and f"(wg.z % {k['z']}u), wg.x, wg.y)" in src, k["name"]
+        assert "blockIdx" not in src, k["name"]
