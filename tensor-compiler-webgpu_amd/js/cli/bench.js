@@ -51,15 +51,31 @@ function prepared(runner, graph, lowered, inputs, opts) {
   return p;
 }
 
-/** Time every launch of `program` alone: µs per launch (median, min and max of a few repetitions). */
+/**
+ * Time every dispatch of `program` alone, as the program issues it: µs per launch
+ * (median, min and max of a few repetitions). A batched dispatch is timed whole and
+ * its time shared evenly among its member launches (`batched`: the member count), so
+ * a member costs what it costs inside its batch, not what it would cost by itself.
+ */
 function timeLaunches(runner, bench, program, reps) {
   const out = [];
-  for (const l of program.lowered.launches) {
-    const one = runner.prepare(program.graph, { launches: [l], workspace: program.lowered.workspace }, { buffers: program.bufs });
+  const L = program.lowered;
+  const batchAt = new Map((L.batches || []).map((b) => [b.start, b]));
+  for (let i = 0; i < L.launches.length;) {
+    const b = batchAt.get(i);
+    const members = L.launches.slice(i, i + (b ? b.count : 1));
+    const lowered = { launches: members, workspace: L.workspace };
+    if (b) lowered.batches = [Object.assign({}, b, { start: 0 })];
+    const one = runner.prepare(program.graph, lowered, { buffers: program.bufs });
     const r = bench.time({ one }, { reps: reps || 5, warmup: 1, targetMs: 0.5, direct: true });
-    out.push({ node: l.node, kind: l.kind, pattern: l.pattern || null, code: l.code, bytes: l.bytes, flops: l.flops,
-      us: r.stats.one.median, minUs: r.stats.one.min, maxUs: r.stats.one.max, rowFolds: l.rowFolds || null });
+    const n = members.length;
+    for (const l of members) {
+      out.push({ node: l.node, kind: l.kind, pattern: l.pattern || null, code: l.code, bytes: l.bytes, flops: l.flops,
+        us: r.stats.one.median / n, minUs: r.stats.one.min / n, maxUs: r.stats.one.max / n, rowFolds: l.rowFolds || null,
+        batched: n > 1 ? n : undefined });
+    }
     one.destroy();
+    i += n;
   }
   return out;
 }

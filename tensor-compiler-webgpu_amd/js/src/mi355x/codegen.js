@@ -687,8 +687,11 @@ function colreduceKernels(op, outer, n, inner, tuning) {
  * so a matmul gives the same bits (the split fixes the order of the K sum)
  * whether its operands are materialised or read through views.
  */
-function gemmTiling(batch, M, N, K, tuning) {
+function gemmTiling(batch, M, N, K, tuning, peers) {
   const t = tuning || {};
+  // Products of this shape in the same graph (1 if unknown): they share the chip, so
+  // the K split aims at its workgroup count over all of them.
+  const P = peers || 1;
   // Tile counts of 32T x 32T: the T and split rules are stated on them.
   const blocks = (T) => batch * Math.ceil(M / (32 * T)) * Math.ceil(N / (32 * T));
   const longK = K >= 2048;
@@ -699,7 +702,7 @@ function gemmTiling(batch, M, N, K, tuning) {
   else T = 1;
   let chunks = 1;
   if (t.splitk !== undefined) chunks = t.splitk;
-  else if (longK && blocks(T) < 512) chunks = Math.max(1, Math.min(Math.ceil(1024 / blocks(T)), Math.floor(K / 256), 32));
+  else if (longK && blocks(T) < 512) chunks = Math.max(1, Math.min(Math.ceil(1024 / (blocks(T) * P)), Math.floor(K / 256), 32));
   let chunkK = Math.ceil(Math.ceil(K / chunks) / 16) * 16;
   chunks = Math.ceil(K / chunkK);
   // Wavefronts along N: 4 (a 32T x 64T tile, 512 threads) wherever N fills the wider
@@ -782,7 +785,7 @@ function gemmKernel(b, output, opts) {
     const add = b.nodes.find((n) => n.op === 'add' && n.inputs.includes(root.id) && !n.inputs.every((i) => i === root.id));
     if (add && add.id !== output) biasAdd = add;
   }
-  const tl = gemmTiling(batch, M, N, K, o.tuning);
+  const tl = gemmTiling(batch, M, N, K, o.tuning, o.peers);
   const total = batch * M * N;
   // A group formed with recomputation may read its matmul through a broadcast or
   // transpose, at another element's index than the one being stored. The product

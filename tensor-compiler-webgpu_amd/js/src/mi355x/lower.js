@@ -90,7 +90,7 @@ function widenInputs(body, output, folds) {
 }
 
 /** Kernels for one node. */
-function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads) {
+function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers) {
   if (rowFold) {
     // A row-statistics chain with its reductions folded in: the rowwise kernel of the
     // reductions, with their own tuning so the rows are reduced in their order.
@@ -114,7 +114,9 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads) {
     if (kind === 'rowwise') {
       return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(b, out, Object.assign({ tuning: tuning.row, lastReads }, sab))));
     }
-    if (kind === 'epilogue') return Object.assign({ kind: 'fused-epilogue' }, single(cg.gemmKernel(b, out, Object.assign({ tuning: tuning.gemm }, sab, mmViews))));
+    if (kind === 'epilogue') {
+      return Object.assign({ kind: 'fused-epilogue' }, single(cg.gemmKernel(b, out, Object.assign({ tuning: tuning.gemm, peers }, sab, mmViews))));
+    }
     if (kind === 'attention') return Object.assign({ kind: 'fused-attention' }, single(cg.attentionKernel(b, out, Object.assign({}, mmViews))));
     throw new Error(`no MI355X kernel for fused kind '${kind}'`);
   }
@@ -139,7 +141,7 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads) {
   }
   if (node.op === 'matmul') {
     const { body, output } = oneOpBody(graph, node);
-    return Object.assign({ kind: 'matmul' }, single(cg.gemmKernel(body, output, Object.assign({ tuning: (opts.tuning || {}).gemm }, mmViews))));
+    return Object.assign({ kind: 'matmul' }, single(cg.gemmKernel(body, output, Object.assign({ tuning: (opts.tuning || {}).gemm, peers }, mmViews))));
   }
   throw new Error(`no MI355X lowering for '${node.op}'`);
 }
@@ -346,6 +348,18 @@ function foldReductions(body, output, folds) {
  * scratch the largest launch needs; aliases: [[node, source]]; folded and dead: node
  * ids with neither a launch nor a buffer; batches, perf only: [{ start, count, kernels, wsStride }]).
  */
+/** A matmul's shape (batch, M, K, N) as a key — of a plain matmul node or of an epilogue group's matmul — or null. */
+function productKey(graph, node) {
+  let a, b;
+  if (node.op === 'matmul') [a, b] = node.inputs.map((i) => graph.nodes[i].shape);
+  else if (node.op === 'fused' && node.attrs.kind === 'epilogue') {
+    const body = node.attrs.body;
+    const mm = body.nodes.find((n) => n.op === 'matmul');
+    [a, b] = mm.inputs.map((i) => body.nodes[i].shape);
+  } else return null;
+  return `${size(a.slice(0, -2))}x${a[a.length - 2]}x${a[a.length - 1]}x${b[b.length - 1]}`;
+}
+
 /** Bytes from which a last read is streamed (non-temporal loads): 1 MiB. */
 const STREAM_FROM = 1 << 20;
 
@@ -379,6 +393,14 @@ function lowerMI355X(graph, options) {
   // displacing data still to be read. A hint only: the values loaded are the same.
   // Smaller buffers stay cached: streaming them saves nothing, and a repeated launch
   // of a small kernel would miss where it hits.
+  // Products of each shape in the graph (every matmul, plain or with an epilogue,
+  // launched or not): the K split of a product depends on its shape and on this count
+  // alone, so the plain and the perf lowering of a graph split every product alike.
+  const productPeers = new Map();
+  for (const node of graph.nodes) {
+    const pk = productKey(graph, node);
+    if (pk !== null) productPeers.set(pk, (productPeers.get(pk) || 0) + 1);
+  }
   const lastRead = new Map();
   if (opts.perf) for (const node of graph.nodes) if (launched(node)) for (const id of inputsOf(node)) lastRead.set(id, node.id);
   for (const node of graph.nodes) {
@@ -404,7 +426,7 @@ function lowerMI355X(graph, options) {
     const key = JSON.stringify([node.op, node.inputs.map((id) => graph.nodes[id].shape), node.attrs, node.shape,
       node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey, rowKey, lastReads]);
     let k = cache.get(key);
-    if (!k) { k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads); cache.set(key, k); }
+    if (!k) { k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, productPeers.get(productKey(graph, node)) || 1); cache.set(key, k); }
     workspace = Math.max(workspace, k.workspace);
     launches.push({
       node: node.id, op: node.op, kind: k.kind, pattern: node.op === 'fused' ? node.attrs.pattern : undefined,
