@@ -88,3 +88,37 @@ def test_launch_dag_over_several_streams_is_refused_inside_a_capture():
         t.graph_destroy(g.value)
     finally:
         t.free(h.value)
+
+
+@pytest.mark.gpu
+def test_staggered_allocations_keep_their_size_alignment_and_contents():
+    """Allocations of 1 MiB or more start at staggered offsets past their hipMalloc
+    base: every handle is still 256-byte aligned, copies are checked against the size
+    asked for (a copy of exactly that size works, one element more is refused), the
+    last bytes hold what was written, and every allocation frees."""
+    import tcmi_ctypes
+    t = tcmi_ctypes.load()
+    t.init()
+    u64 = tcmi_ctypes.u64
+    sizes = [(1 << 20) + 4 * k for k in range(18)] + [4096, 1 << 22]
+    handles = []
+    try:
+        for n in sizes:
+            h = u64()
+            t.malloc(n, ctypes.byref(h))
+            handles.append((h.value, n))
+            assert h.value % 256 == 0, (n, h.value)
+            got = u64()
+            t.size(h.value, ctypes.byref(got))
+            assert got.value == n
+        assert len({h for h, _ in handles}) == len(handles)
+        for i, (h, n) in enumerate(handles):
+            data = (np.arange(n // 4, dtype=np.uint32) * 2654435761 + i).astype(np.uint32)
+            t.h2d(h, 0, data.ctypes.data, n)
+            assert t.lib.tcmi_h2d(h, 4, data.ctypes.data, n) == 10001      # one element past the end
+            back = np.zeros(n // 4, dtype=np.uint32)
+            t.d2h(back.ctypes.data, h, 0, n)
+            assert np.array_equal(back, data), n
+    finally:
+        for h, _ in handles:
+            t.free(h)
