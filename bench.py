@@ -325,7 +325,8 @@ def compose(full: dict) -> dict:
     if "c3" in cfg:
         c3 = cfg["c3"]
         extra["c3"] = {"GBs": _r(c3["gbs"], 4), "frac": _r(c3["gbs"] / HBM_PEAK),
-                       "dominant": {"kernel": c3["dominant"]["code"], "GBs": _r(c3["dominant"]["gbs"], 4)},
+                       "dominant": {"kernel": c3["dominant"]["code"], "GBs": _r(c3["dominant"]["gbs"], 4),
+                                    "cold_GBs": _r((c3["dominant"].get("cold") or {}).get("gbs"), 4)},
                        "speedups": {r["name"].replace("c3-", ""): _r(r["verdict"]["speedup"]) for r in c3["results"]},
                        "groups": _groups(c3.get("groups"))}
     if "c4" in cfg:

@@ -473,6 +473,7 @@ function c3(runner, bench, opts) {
   const R = opts.quick ? 2048 : cfg.C3_SHAPE[0], C = cfg.C3_SHAPE[1];
   const { x, dy, shifted } = cfg.c3Inputs(R, C);
   const results = [];
+  const programs = [];
   for (const fn of ['softmax', 'logSoftmax']) {
     const g = cfg.c3Graphs(fn, R, C);
     if (flag('step-only')) {
@@ -480,16 +481,30 @@ function c3(runner, bench, opts) {
       results.push(runOnly(runner, `c3-${fn}-backward`, g.gradient.graph, g.gradient.keep, { x, d0: dy }));
       continue;
     }
+    const keep = (r) => { programs.push(r.programs.pf); r.programs.pu.destroy(); delete r.programs; return r; };
     log(`c3 ${fn} forward`);
-    results.push(measureGraph(runner, bench, `c3-${fn}-forward`, g.forward.graph, g.forward.keep, { x }, { reps: opts.reps }));
+    results.push(keep(measureGraph(runner, bench, `c3-${fn}-forward`, g.forward.graph, g.forward.keep, { x },
+      { reps: opts.reps, keepPrograms: true })));
     log(`c3 ${fn} backward`);
-    results.push(measureGraph(runner, bench, `c3-${fn}-backward`, g.gradient.graph, g.gradient.keep, { x, d0: dy }, { reps: opts.reps }));
+    results.push(keep(measureGraph(runner, bench, `c3-${fn}-backward`, g.gradient.graph, g.gradient.keep, { x, d0: dy },
+      { reps: opts.reps, keepPrograms: true })));
   }
   if (flag('step-only')) return { config: 'c3', shape: [R, C], results };
   const all = [].concat.apply([], results.map((r) => r.launchF));
   const bytes = results.reduce((s, r) => s + r.bytes.fused, 0);
   const us = results.reduce((s, r) => s + r.fused.median, 0);
-  return { config: 'c3', shape: [R, C], shiftedRows: shifted.length, gbs: bytes / (us * 1e3), dominant: dominant(all),
+  // The programs are timed repeated on their own buffers, where a program's re-reads of
+  // its 268 MB tensors partly hit the 256 MB last-level cache; the dominant kernel is
+  // also timed cold, as config 2's roofline kernel is (operands rotated over sets that
+  // span several times that cache), for an HBM figure beside the warm one.
+  const dom = dominant(all);
+  if (dom) {
+    const p = programs.find((q) => q.launches.some((x) => x.code === dom.code));
+    dom.cold = coldLaunch(runner, bench, p, p.launches.find((x) => x.code === dom.code), 0);
+    dom.cold.gbs = dom.bytesPerLaunch / (dom.cold.avgUs * 1e3);
+  }
+  for (const p of programs) p.destroy();
+  return { config: 'c3', shape: [R, C], shiftedRows: shifted.length, gbs: bytes / (us * 1e3), dominant: dom,
     groups: groupSummary([].concat.apply([], results.map((r) => r.groups))), results };
 }
 
