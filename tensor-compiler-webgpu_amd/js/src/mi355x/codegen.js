@@ -689,8 +689,8 @@ function colreduceKernels(op, outer, n, inner, tuning) {
  */
 function gemmTiling(batch, M, N, K, tuning, peers) {
   const t = tuning || {};
-  // Products of this shape in the same graph (1 if unknown): they share the chip, so
-  // the K split aims at its workgroup count over all of them.
+  // Products of this shape that may share one dispatch (1 if unknown): they share the
+  // chip, so the K split aims at its workgroup count over all of them.
   const P = peers || 1;
   // Tile counts of 32T x 32T: the T and split rules are stated on them.
   const blocks = (T) => batch * Math.ceil(M / (32 * T)) * Math.ceil(N / (32 * T));

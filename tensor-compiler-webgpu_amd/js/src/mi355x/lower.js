@@ -393,14 +393,20 @@ function lowerMI355X(graph, options) {
   // displacing data still to be read. A hint only: the values loaded are the same.
   // Smaller buffers stay cached: streaming them saves nothing, and a repeated launch
   // of a small kernel would miss where it hits.
-  // Products of each shape in the graph (every matmul, plain or with an epilogue,
-  // launched or not): the K split of a product depends on its shape and on this count
-  // alone, so the plain and the perf lowering of a graph split every product alike.
+  // Products that may share one dispatch: those whose value no node reads (a trainer's
+  // weight gradients with their update epilogues), counted per shape, launched or not.
+  // Nothing waits on them, so the perf lowering can issue all of them together; a
+  // product that another node reads runs where its readers need it, alone as far as
+  // this count can tell (1). The K split of a product depends on its shape and on this
+  // count alone, so the plain and the perf lowering of a graph split every product alike.
+  const readers = new Set();
+  for (const node of graph.nodes) for (const id of node.inputs) readers.add(id);
   const productPeers = new Map();
   for (const node of graph.nodes) {
-    const pk = productKey(graph, node);
+    const pk = readers.has(node.id) ? null : productKey(graph, node);
     if (pk !== null) productPeers.set(pk, (productPeers.get(pk) || 0) + 1);
   }
+  const peersOf = (node) => (readers.has(node.id) ? 1 : productPeers.get(productKey(graph, node)) || 1);
   const lastRead = new Map();
   if (opts.perf) for (const node of graph.nodes) if (launched(node)) for (const id of inputsOf(node)) lastRead.set(id, node.id);
   for (const node of graph.nodes) {
@@ -423,10 +429,11 @@ function lowerMI355X(graph, options) {
     });
     // Kernels depend on structure, shapes, operand views, folded broadcasts and last
     // reads only: reuse across identical nodes.
+    const peers = peersOf(node);
     const key = JSON.stringify([node.op, node.inputs.map((id) => graph.nodes[id].shape), node.attrs, node.shape,
-      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey, rowKey, lastReads]);
+      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey, rowKey, lastReads, peers]);
     let k = cache.get(key);
-    if (!k) { k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, productPeers.get(productKey(graph, node)) || 1); cache.set(key, k); }
+    if (!k) { k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers); cache.set(key, k); }
     workspace = Math.max(workspace, k.workspace);
     launches.push({
       node: node.id, op: node.op, kind: k.kind, pattern: node.op === 'fused' ? node.attrs.pattern : undefined,
