@@ -1320,7 +1320,13 @@ async function main() {
     case 'perf-lower': {
       // The perf lowering of a model step or of a graph: launches, aliases, folded nodes, operand views.
       let g, keep;
-      if (req.model) {
+      if (req.model && req.unfused) {
+        // The model's step graph without fusion (the bench's unfused step).
+        const { modelStep } = require('../src/builders/models');
+        const st = modelStep(req).step;
+        g = st.graph;
+        keep = [st.loss, st.logits].concat(Object.values(st.outputs));
+      } else if (req.model) {
         const { modelStep } = require('../src/builders/models');
         const { fusedStep } = require('../src/mi355x/trainer');
         const fs = fusedStep(modelStep(req).step);

@@ -283,6 +283,52 @@ def test_perf_lowering_keeps_the_split_of_config4_backward(tool):
             assert l["split"] == l["plainSplit"], (g["M"], g["K"], g["N"], l["node"])
 
 
+def _product_shape(nodes, n):
+    """(batch dims, M, K, N) of a plain matmul node or of an epilogue group's matmul, or None."""
+    if n["op"] == "matmul":
+        a, b = (nodes[i]["shape"] for i in n["inputs"])
+    elif n["op"] == "fused" and n["attrs"]["kind"] == "epilogue":
+        body = n["attrs"]["body"]["nodes"]
+        mm = next(x for x in body if x["op"] == "matmul")
+        a, b = (body[i]["shape"] for i in mm["inputs"])
+    else:
+        return None
+    return (tuple(a[:-2]), a[-2], a[-1], b[-1])
+
+
+def _splits_by_product(d):
+    """{(shape, read by a node): [chunks of each launch]} of a perf-lower result."""
+    nodes = d["graph"]["nodes"]
+    read = {i for n in nodes for i in n["inputs"]}
+    out = {}
+    for l in d["launches"]:
+        shape = _product_shape(nodes, nodes[l["node"]])
+        if shape is not None and l["split"] is not None:
+            out.setdefault((shape, l["node"] in read), []).append(l["split"][0])
+    return out
+
+
+def test_k_split_shares_the_chip_only_among_products_no_node_reads(tool):
+    """A product whose value no node reads (a weight gradient with its update epilogue) may
+    share one dispatch with the others of its shape, so its K split aims at the chip over all
+    of them; a product that a node reads splits as it would alone. Config 5's step at batch
+    64: the 16 fused attention-projection weight gradients (256 x 8192 x 256, nothing reads
+    them) split alike, into fewer chunks than the same products of the unfused step, which
+    the separate updates read; those split as the product does alone in a graph of its own."""
+    fused = _splits_by_product(tool("perf-lower", {"model": "transformer", "B": 64}))
+    unfused = _splits_by_product(tool("perf-lower", {"model": "transformer", "B": 64, "unfused": True}))
+    wgrad = ((), 256, 8192, 256)
+    assert len(fused[(wgrad, False)]) == 16 and len(set(fused[(wgrad, False)])) == 1
+    assert (wgrad, True) not in fused
+    assert len(unfused[(wgrad, True)]) == 16 and (wgrad, False) not in unfused
+    nodes = [{"op": "input", "inputs": [], "attrs": {"name": "a", "shape": [256, 8192]}, "shape": [256, 8192]},
+             {"op": "input", "inputs": [], "attrs": {"name": "b", "shape": [8192, 256]}, "shape": [8192, 256]},
+             {"op": "matmul", "inputs": [0, 1], "attrs": {}, "shape": [256, 256]}]
+    alone = _splits_by_product(tool("perf-lower", {"graph": {"nodes": nodes}, "keep": [2]}))[(wgrad, False)]
+    assert set(unfused[(wgrad, True)]) == set(alone)
+    assert fused[(wgrad, False)][0] < alone[0]
+
+
 @pytest.mark.parametrize("config,V,B,layers", [("reference", 16, 2, 2), ("c5", 96, 1, 4)])
 def test_attention_fusion_preserves_semantics(tool, config, V, B, layers):
     """The attention extension (fuse(..., {attention: true}), off by default): every
