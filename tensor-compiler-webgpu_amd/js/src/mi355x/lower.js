@@ -94,8 +94,17 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers)
   if (rowFold) {
     // A row-statistics chain with its reductions folded in: the rowwise kernel of the
     // reductions, with their own tuning so the rows are reduced in their order.
-    const folds = rowFold.map((f) => ({ pos: f.pos, op: graph.nodes[f.red].op, attrs: graph.nodes[f.red].attrs,
-      shape: graph.nodes[f.red].shape, inShape: graph.nodes[graph.nodes[f.red].inputs[0]].shape }));
+    const folds = rowFold.map((f) => {
+      const fold = { pos: f.pos, op: graph.nodes[f.red].op, attrs: graph.nodes[f.red].attrs,
+        shape: graph.nodes[f.red].shape, inShape: graph.nodes[graph.nodes[f.red].inputs[0]].shape };
+      if (f.prod !== undefined) {
+        // The producer's body, its inputs at the launch positions `ppos`.
+        const p = graph.nodes[f.prod];
+        const one = p.op === 'fused' ? { body: bodyOf(p), output: p.attrs.output } : oneOpBody(graph, p);
+        fold.producer = Object.assign(widenInputs(one.body, one.output, f.prodFolds), { ppos: f.ppos });
+      }
+      return fold;
+    });
     const f = foldReductions(bodyOf(node), node.attrs.output, folds);
     const t = opts.tuning || {};
     return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(f.body, f.output, { tuning: t.rowreduce || t.row, lastReads })));
@@ -282,6 +291,56 @@ function perfPlan(graph, keep) {
       rowFolds.get(u).push({ red: r, pos: graph.nodes[u].inputs.map((i, k) => (i === r ? k : -1)).filter((k) => k >= 0) });
     }
   }
+  // A folded reduction's producer folded in with it: an elementwise node (one op or a
+  // fused chain) of the reduction's [rows, n] operand shape that only the reduction reads
+  // and nothing keeps launches nothing either. The rowwise kernel forms the producer's
+  // value per element from the producer's own operands, in registers, with the same ops
+  // in the same order, then reduces it: the same bits, without writing the operand and
+  // reading it back. Its operands join the chain's (the first in the reduction's slot,
+  // the rest after the chain's own), all within one argument block. A fused producer's
+  // body must hold full-size values only, besides its operands and constants and their
+  // broadcasts: the rowwise kernel tells a row's value from an element's by size, so a
+  // computed vector of the row length would be read at the row index where the rows are
+  // as many as their length.
+  const fullBody = (p) => {
+    if (p.op !== 'fused') return true;
+    const b = p.attrs.body.nodes;
+    const n = size(p.shape);
+    return b.every((x) => x.op === 'input' || x.op === 'const' || (ELEMENTWISE_OPS.has(x.op) && size(x.shape) === n)
+      || (x.op === 'broadcast' && (b[x.inputs[0]].op === 'input' || b[x.inputs[0]].op === 'const')));
+  };
+  const producer = (r) => {
+    const red = graph.nodes[r];
+    const p = graph.nodes[red.inputs[0]];
+    if (keep.has(p.id) || folded.has(p.id) || aliases.has(p.id) || p.shape.length !== 2 || red.attrs.axis !== 1) return null;
+    if (!ELEMENTWISE_OPS.has(p.op) && !(p.op === 'fused' && p.attrs.kind === 'elementwise' && fullBody(p))) return null;
+    if (new Set(cons[p.id]).size !== 1) return null;
+    const own = broadcasts.get(p.id);
+    if (!p.inputs.every((i, pos) => !folded.has(i) || (own && own.has(pos)))) return null;
+    return p;
+  };
+  const producers = new Map();   // reduction id -> producer node
+  for (const r of cand) { const p = producer(r); if (p) producers.set(r, p); }
+  const operandsWith = (u) => rowFolds.get(u).reduce((n, f) => n + (producers.has(f.red) ? producers.get(f.red).inputs.length - 1 : 0),
+    graph.nodes[u].inputs.length);
+  for (let again = true; again;) {
+    again = false;
+    for (const u of rowFolds.keys()) {
+      if (operandsWith(u) <= cg.MAX_IN) continue;
+      for (const f of rowFolds.get(u)) again = producers.delete(f.red) || again;
+    }
+  }
+  for (const [u, fs] of rowFolds) {
+    let next = graph.nodes[u].inputs.length;
+    for (const f of fs) {
+      const p = producers.get(f.red);
+      if (!p) continue;
+      folded.add(p.id);
+      f.prod = p.id;
+      f.prodFolds = broadcasts.get(p.id) || null;
+      f.ppos = p.inputs.map((_, j) => (j === 0 ? f.pos[0] : next++));
+    }
+  }
   const views = new Map();
   for (const n of graph.nodes) {
     for (const [slot, pos] of matmulSlots(n)) {
@@ -323,7 +382,19 @@ function foldReductions(body, output, folds) {
     if (f) {
       if (!reduced.has(f)) {
         const outer = size(f.inShape.slice(0, f.attrs.axis)), len = f.inShape[f.attrs.axis];
-        const r = g.emit(f.op, [g.input(`a${f.pos[0]}`, [outer, len])], { axis: 1, keepDims: true });
+        let src;
+        if (f.producer) {
+          // The reduction's operand formed in place by its producer's body ([outer, len]).
+          const pm = new Map();
+          for (const pn of f.producer.body.nodes) {
+            pm.set(pn.id, pn.op === 'input' ? g.input(`a${f.producer.ppos[Number(pn.attrs.name.slice(1))]}`, pn.shape)
+              : g.emit(pn.op, pn.inputs.map((i) => pm.get(i)), pn.attrs));
+          }
+          src = pm.get(f.producer.output);
+        } else {
+          src = g.input(`a${f.pos[0]}`, [outer, len]);
+        }
+        const r = g.emit(f.op, [src], { axis: 1, keepDims: true });
         reduced.set(f, g.reshape(r, f.shape));
       }
       map.set(n.id, reduced.get(f));
@@ -384,7 +455,19 @@ function lowerMI355X(graph, options) {
     const folds = plan.broadcasts.get(node.id);
     if (folds) for (const [pos, f] of folds) inputs[pos] = resolve(f.source);
     const rowFold = plan.rowFolds.get(node.id);
-    if (rowFold) for (const f of rowFold) for (const pos of f.pos) inputs[pos] = resolve(graph.nodes[f.red].inputs[0]);
+    if (rowFold) {
+      for (const f of rowFold) {
+        if (f.prod === undefined) {
+          for (const pos of f.pos) inputs[pos] = resolve(graph.nodes[f.red].inputs[0]);
+          continue;
+        }
+        // The producer's operands (a broadcast it reads in place: the broadcast's source).
+        const p = graph.nodes[f.prod];
+        const pins = p.inputs.map((i, j) => resolve(f.prodFolds && f.prodFolds.has(j) ? f.prodFolds.get(j).source : i));
+        for (const pos of f.pos) inputs[pos] = pins[0];
+        f.ppos.forEach((pos, j) => { inputs[pos] = pins[j]; });
+      }
+    }
     return inputs;
   };
   // Last reads (perf lowering): an elementwise or rowwise kernel loads a full-size operand of
@@ -420,8 +503,14 @@ function lowerMI355X(graph, options) {
     const folds = plan.broadcasts.get(node.id) || null;
     const foldKey = folds ? Array.from(folds.entries()).map(([pos, f]) => [pos, f.from, f.to]) : null;
     const rowFold = plan.rowFolds.get(node.id) || null;
+    const prodKey = (f) => {
+      if (f.prod === undefined) return null;
+      const p = graph.nodes[f.prod];
+      return [f.ppos, p.op, p.attrs, p.inputs.map((i) => graph.nodes[i].shape),
+        f.prodFolds ? Array.from(f.prodFolds.entries()).map(([pos, b]) => [pos, b.from, b.to]) : null];
+    };
     const rowKey = rowFold ? rowFold.map((f) => [f.pos, graph.nodes[f.red].op, graph.nodes[f.red].attrs,
-      graph.nodes[graph.nodes[f.red].inputs[0]].shape]) : null;
+      graph.nodes[graph.nodes[f.red].inputs[0]].shape, prodKey(f)]) : null;
     const inputs = inputsOf(node);
     const lastReads = [];
     inputs.forEach((id, pos) => {
@@ -442,7 +531,8 @@ function lowerMI355X(graph, options) {
     });
     if (rowFold) {
       // The reduction folded into this launch, and the launch's own body (for node-local checks).
-      launches[launches.length - 1].rowFolds = rowFold.map((f) => ({ reduction: f.red, pos: f.pos }));
+      launches[launches.length - 1].rowFolds = rowFold.map((f) => (f.prod === undefined ? { reduction: f.red, pos: f.pos }
+        : { reduction: f.red, pos: f.pos, producer: f.prod, producerPos: f.ppos }));
     }
     if (v) {
       // Operands read in place: for each folded slot, the node it stands for and the view of its source.

@@ -28,12 +28,25 @@ def take_block(a: np.ndarray, shape: Sequence[int], p: int, q: int, b: int) -> n
     return np.ascontiguousarray(nd[tuple(idx)]).reshape(-1)
 
 
+def _producer_body(graph, p):
+    """The body nodes and output index of producer node `p`: a fused node's own body, or
+    its one op on inputs a0.. (the node's operands in order)."""
+    if p["op"] == "fused":
+        return p["attrs"]["body"]["nodes"], p["attrs"]["output"]
+    ins = [{"op": "input", "inputs": [], "attrs": {"name": f"a{k}", "shape": graph["nodes"][i]["shape"]},
+            "shape": graph["nodes"][i]["shape"]} for k, i in enumerate(p["inputs"])]
+    return ins + [{"op": p["op"], "inputs": list(range(len(ins))), "attrs": p["attrs"], "shape": p["shape"]}], len(ins)
+
+
 def fold_reductions(graph, node_id, folds):
     """A launch of the perf lowering that took row reductions into a chain (its record's
-    rowFolds: [{reduction, pos}]): the chain's node with each body input at `pos` (the
-    reduction's value) replaced by the reduction itself, applied to a new input a{pos[0]},
-    and the launch's operand node ids (the reduction's operand in those positions).
-    Restated here from the lowering's rule, so a wrong fold there fails the judge."""
+    rowFolds: [{reduction, pos}], with producer and producerPos where the reduction's
+    operand is formed in the launch too): the chain's node with each body input at `pos`
+    (the reduction's value) replaced by the reduction itself, applied to a new input
+    a{pos[0]} — or to the producer's body on inputs a{producerPos[j]} — and the launch's
+    operand node ids (the reduction's operand in those positions, or the producer's
+    operands). Restated here from the lowering's rule, so a wrong fold there fails the
+    judge."""
     node = graph["nodes"][node_id]
     if not folds:
         return node, list(node["inputs"])
@@ -50,8 +63,24 @@ def fold_reductions(graph, node_id, folds):
                 src = graph["nodes"][red["inputs"][0]]["shape"]
                 axis = red["attrs"]["axis"]
                 rows = [int(np.prod(src[:axis])), src[axis]]
-                out.append({"op": "input", "inputs": [], "attrs": {"name": f"a{f['pos'][0]}", "shape": rows}, "shape": rows})
-                out.append({"op": red["op"], "inputs": [len(out) - 1], "attrs": {"axis": 1, "keepDims": True},
+                if "producer" in f:
+                    p = graph["nodes"][f["producer"]]
+                    assert red["inputs"][0] == f["producer"] and p["shape"] == rows
+                    pnodes, pout = _producer_body(graph, p)
+                    pmap = {}
+                    for pid, pn in enumerate(pnodes):
+                        if pn["op"] == "input":
+                            name = f"a{f['producerPos'][int(pn['attrs']['name'][1:])]}"
+                            out.append(dict(pn, attrs=dict(pn["attrs"], name=name)))
+                        else:
+                            out.append(dict(pn, inputs=[pmap[i] for i in pn["inputs"]]))
+                        pmap[pid] = len(out) - 1
+                    operand = pmap[pout]
+                else:
+                    out.append({"op": "input", "inputs": [], "attrs": {"name": f"a{f['pos'][0]}", "shape": rows},
+                                "shape": rows})
+                    operand = len(out) - 1
+                out.append({"op": red["op"], "inputs": [operand], "attrs": {"axis": 1, "keepDims": True},
                             "shape": [rows[0], 1]})
                 if red["shape"] != [rows[0], 1]:
                     out.append({"op": "reshape", "inputs": [len(out) - 1], "attrs": {"shape": red["shape"]},
@@ -66,6 +95,14 @@ def fold_reductions(graph, node_id, folds):
         for p in f["pos"]:
             assert inputs[p] == f["reduction"]
             inputs[p] = graph["nodes"][f["reduction"]]["inputs"][0]
+        if "producer" in f:
+            pins = graph["nodes"][f["producer"]]["inputs"]
+            for p in f["pos"]:
+                inputs[p] = pins[0]
+            for j, p in enumerate(f["producerPos"]):
+                inputs.extend([None] * (p + 1 - len(inputs)))
+                inputs[p] = pins[j]
+    assert None not in inputs
     attrs = dict(node["attrs"], body={"nodes": out}, output=where[node["attrs"]["output"]])
     return dict(node, attrs=attrs, inputs=inputs), inputs
 

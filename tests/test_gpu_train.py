@@ -48,11 +48,15 @@ def node_local(tool, tmp_path, req):
     perf = {int(k): g.arr(v) for k, v in gc["gpuPerf"].items()}
     skipped = set(expected) - set(perf)
     assert skipped == {a for a, _ in gc["aliases"]} | set(gc["folded"]) | set(gc["dead"])
-    # Reductions folded into their row-statistics chains are the other launches it skips.
+    # Reductions folded into their row-statistics chains, and the producers of their
+    # operands formed in the same launches, are the other launches it skips.
     folds = {int(k): v for k, v in gc["rowFolds"].items()}
     reductions = {f["reduction"] for fs in folds.values() for f in fs}
-    assert all(c["fused"]["nodes"][i]["op"] in ("reshape", "transpose", "broadcast") for i in skipped - set(gc["dead"]) - reductions)
+    producers = {f["producer"] for fs in folds.values() for f in fs if "producer" in f}
+    assert all(c["fused"]["nodes"][i]["op"] in ("reshape", "transpose", "broadcast")
+               for i in skipped - set(gc["dead"]) - reductions - producers)
     assert all(c["fused"]["nodes"][i]["op"] in ("sum", "max") for i in reductions)
+    assert all(c["fused"]["nodes"][i]["op"] not in ("sum", "max", "matmul") for i in producers)
     # A chain with its reductions folded in is judged as the launch it is: the reductions and
     # the chain on the reductions' operands.
     pexp, pbound = {}, {}

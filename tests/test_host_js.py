@@ -10,6 +10,8 @@ import pytest
 
 from oracle import interp
 
+ELEMENTWISE = ("add", "sub", "mul", "div", "neg", "exp", "log", "relu", "tanh", "sqrt", "step", "stopGradient")
+
 
 def test_builder_graphs_equal_reference_cases(golden_cases, tool):
     ref = {c["name"]: c for c in golden_cases}
@@ -203,7 +205,8 @@ def test_perf_lowering_views_address_the_operands(tool, req):
     # Folded: transposes read in place by matmuls, broadcasts read through their index map,
     # and row reductions taken into the row-statistics chains that read them.
     reductions = {f["reduction"] for fs in d["rowFolds"].values() for f in fs}
-    assert all(nodes[i]["op"] in ("transpose", "broadcast") for i in set(d["folded"]) - reductions)
+    producers = {f["producer"] for fs in d["rowFolds"].values() for f in fs if "producer" in f}
+    assert all(nodes[i]["op"] in ("transpose", "broadcast") for i in set(d["folded"]) - reductions - producers)
     # A folded broadcast is read by elementwise, rowwise or epilogue bodies only (never
     # by a reduction, a gather or as a matmul operand), through the broadcast's source.
     consumers = {}
@@ -219,11 +222,20 @@ def test_perf_lowering_views_address_the_operands(tool, req):
             assert f["reduction"] not in d["keep"] and all(c["inputs"][p] == f["reduction"] for p in f["pos"])
             # Every launched consumer of a folded reduction takes it in.
             assert all(str(u) in d["rowFolds"] for u in consumers[f["reduction"]] if u not in d["dead"])
+            if "producer" in f:
+                # A producer formed in the launch: an elementwise node of the reduction's
+                # 2-D operand shape, read by the reduction alone, kept by nobody.
+                p = nodes[f["producer"]]
+                assert r["inputs"][0] == f["producer"] and consumers[f["producer"]] == {f["reduction"]}
+                assert f["producer"] not in d["keep"] and len(p["shape"]) == 2
+                assert p["op"] in ELEMENTWISE or (p["op"] == "fused" and p["attrs"]["kind"] == "elementwise")
+                assert f["producerPos"][0] == f["pos"][0] and len(f["producerPos"]) == len(p["inputs"])
+    if req["model"] != "mlp":
+        assert producers
     for i in d["folded"]:
         if nodes[i]["op"] == "broadcast":
             for c in consumers[i]:
-                assert nodes[c]["op"] == "fused" or nodes[c]["op"] in ("add", "sub", "mul", "div", "neg", "exp", "log",
-                                                                      "relu", "tanh", "sqrt", "step", "stopGradient"), nodes[c]["op"]
+                assert nodes[c]["op"] == "fused" or nodes[c]["op"] in ELEMENTWISE, nodes[c]["op"]
     # Dead nodes: exactly those no kept node depends on (liveness recomputed here).
     live = set()
     for n_id in range(len(nodes) - 1, -1, -1):

@@ -66,24 +66,36 @@ def test_folded_row_reductions_are_the_chain_on_the_reduction(tool):
     sums) into the row-statistics chains that read them. The checkers' restatement of such
     a launch (fold_reductions) evaluated in float64 on a chain's operands equals the
     reduction evaluated first and the chain's own body applied to its value, bit for bit,
-    value and bound: the fold changes where the reduction runs, not what is computed."""
+    value and bound: the fold changes where the reduction runs, not what is computed. The
+    same holds where the launch also forms the reduction's operand from its producer's
+    operands (the producer evaluated first on the unfolded side)."""
     d = tool("perf-lower", {"model": "transformer", "B": 1})
     graph, folds = d["graph"], {int(k): v for k, v in d["rowFolds"].items()}
     assert len(folds) >= 20
     reds = {f["reduction"] for fs in folds.values() for f in fs}
     assert reds <= set(d["folded"]) and all(graph["nodes"][r]["op"] in ("sum", "max") for r in reds)
     rng = np.random.default_rng(3)
-    for k, fs in list(folds.items())[:12]:
+    producers = [k for k, fs in folds.items() if any("producer" in f for f in fs)]
+    assert len(producers) >= 6
+    for k, fs in list(folds.items())[:12] + [(k, folds[k]) for k in producers[:12]]:
         node, ins = fold_reductions(graph, k, fs)
         # Positive operands keep the deviation chains' square roots real.
         ops = [rng.uniform(0.5, 2.0, size=interp.size(graph["nodes"][i]["shape"])).astype(np.float32) for i in ins]
         v, e = local(graph, node, ops)
-        # The same launch the unfolded way: each reduction by itself, then the chain.
+        # The same launch the unfolded way: each reduction's producer by itself (where the
+        # launch forms the reduction's operand too), each reduction, then the chain.
         chain_ops = []
+        by_red = {f["reduction"]: f for f in fs}
         for pos, i in enumerate(graph["nodes"][k]["inputs"]):
-            if i in reds and i in [f["reduction"] for f in fs]:
-                red = graph["nodes"][i]
-                rv, re_ = local(graph, red, [ops[pos]])
+            if i in by_red:
+                red, f = graph["nodes"][i], by_red[i]
+                if "producer" in f:
+                    pv, pe = local(graph, graph["nodes"][f["producer"]], [ops[q] for q in f["producerPos"]])
+                    rg, rout = bounds.one_op_graph(graph, red)
+                    r = bounds.reference_with_bounds(rg, {}, carried={"a0": (pv, pe)})
+                    rv, re_ = r["values"][rout], r["bounds"][rout]
+                else:
+                    rv, re_ = local(graph, red, [ops[pos]])
                 chain_ops.append((rv, re_))
             else:
                 chain_ops.append((ops[pos].astype(np.float64), np.zeros(ops[pos].size)))
