@@ -1335,6 +1335,12 @@ async function main() {
       } else {
         g = Graph.fromJSON(req.graph);
         keep = req.keep || [];
+        if (req.fuse) {
+          // The graph fused first (with the recompute option as asked); ids are the fused graph's.
+          const f = fuse(g, { keep, recompute: !!req.fuse.recompute });
+          g = f.graph;
+          keep = keep.map((id) => f.index.get(id));
+        }
       }
       const l = lowerMI355X(g, { perf: true, keep });
       const plain = new Map(lowerMI355X(g).launches.map((x) => [x.node, x]));

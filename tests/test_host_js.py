@@ -295,6 +295,34 @@ def test_perf_lowering_keeps_the_split_of_config4_backward(tool):
             assert l["split"] == l["plainSplit"], (g["M"], g["K"], g["N"], l["node"])
 
 
+def test_row_fold_takes_in_a_producer_only_with_a_full_size_body(tool):
+    """A row reduction's elementwise producer joins the reduction's rowwise launch only when
+    every value of its body is full size (besides its operands, constants and their
+    broadcasts): the rowwise kernel tells a row's value from an element's by size, so with as
+    many rows as their length a computed vector of the row length would be read at the row
+    index. The GPU corpus run with recompute found it (program 25's gradient: exp and log of
+    a [1, 3] vector broadcast over [3, 3], read at the row index). Here the same graph fused
+    plainly leaves the vector's exp and log a launch of their own and the producer folds;
+    with recompute they move into the producer, which then stays a launch."""
+    def node(op, inputs, out_shape, **attrs):
+        return {"op": op, "inputs": inputs, "attrs": attrs, "shape": out_shape}
+    nodes = [node("input", [], [1, 3], name="v", shape=[1, 3]), node("input", [], [3, 3], name="m", shape=[3, 3]),
+             node("exp", [0], [1, 3]), node("log", [2], [1, 3]), node("broadcast", [3], [3, 3], shape=[3, 3]),
+             node("mul", [1, 4], [3, 3]), node("neg", [5], [3, 3]),
+             node("sum", [6], [3, 1], axis=1, keepDims=True), node("neg", [7], [3, 1]), node("exp", [8], [3, 1])]
+    for recompute in (False, True):
+        d = tool("perf-lower", {"graph": {"nodes": nodes}, "keep": [9], "fuse": {"recompute": recompute}})
+        g = d["graph"]["nodes"]
+        (chain, folds), = d["rowFolds"].items()
+        (f,) = folds
+        assert g[f["reduction"]]["op"] == "sum"
+        producer = g[f["reduction"]]["inputs"][0]
+        body = g[producer]["attrs"]["body"]["nodes"]
+        assert [b["op"] for b in body if b["op"] in ("exp", "log")] == (["exp", "log"] if recompute else [])
+        assert ("producer" in f) != recompute and (producer in d["folded"]) != recompute
+        assert (producer in [l["node"] for l in d["launches"]]) == recompute
+
+
 def _product_shape(nodes, n):
     """(batch dims, M, K, N) of a plain matmul node or of an epilogue group's matmul, or None."""
     if n["op"] == "matmul":
