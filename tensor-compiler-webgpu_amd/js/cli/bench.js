@@ -151,7 +151,7 @@ function measureGraph(runner, bench, name, graph, keep, inputs, opts) {
   // place by their matmuls): what the trainer runs; outputs equal the plain lowering's.
   const f = fuse(graph, { keep });
   const lf = lowerMI355X(f.graph, { perf: true, keep: keep.map((id) => f.index.get(id)) });
-  const lu = lowerMI355X(graph, { perf: true, keep });
+  const lu = lowerMI355X(graph, { perf: true, keep, rowFolds: false });
   runner.functions([lf, lu]);
   // With o.arena, each program's node buffers share one allocation by live range.
   const pf = prepared(runner, f.graph, lf, inputs, o.arena ? { arena: { keep: keep.map((id) => f.index.get(id)) } } : undefined);
@@ -550,7 +550,7 @@ function trainStep(runner, bench, name, req, opts) {
   const m = modelStep(req);
   const fs = fusedStep(m.step);
   // The unfused step in the same perf lowering the fused trainer runs.
-  const lu = lowerMI355X(m.step.graph, { perf: true, keep: [m.step.loss, m.step.logits].concat(Object.values(m.step.outputs)) });
+  const lu = lowerMI355X(m.step.graph, { perf: true, keep: [m.step.loss, m.step.logits].concat(Object.values(m.step.outputs)), rowFolds: false });
   runner.functions([fs.lowered, lu]);
   const K = Number(arg('train-steps', opts.quick ? 3 : 10)), W = 2;
   const batch = m.batch(0);
@@ -702,7 +702,7 @@ function sweep(runner, bench, opts) {
       let graph, lowered, only;
       if (v === 'unfused') {
         graph = m.graph;
-        lowered = lowerMI355X(m.graph, { perf: true, keep: m.outputs });
+        lowered = lowerMI355X(m.graph, { perf: true, keep: m.outputs, rowFolds: false });
       } else {
         const f = fuse(m.graph, { keep: m.outputs, recompute: v === 'recompute' });
         graph = f.graph;

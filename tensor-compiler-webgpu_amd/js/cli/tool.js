@@ -183,7 +183,7 @@ function precompileGroup(group, arch, shard, shards) {
       const m = modelStep(r);
       const fs = fusedStep(m.step);
       // The bench's unfused step runs in the perf lowering as well.
-      const unfused = lowerMI355X(m.step.graph, { perf: true, keep: [m.step.loss, m.step.logits].concat(Object.values(m.step.outputs)) });
+      const unfused = lowerMI355X(m.step.graph, { perf: true, keep: [m.step.loss, m.step.logits].concat(Object.values(m.step.outputs)), rowFolds: false });
       n += precompile([fs.lowered], arch) + precompile([fs.checked], arch) + precompile([unfused], arch);
     }
     return n;
@@ -196,7 +196,7 @@ function precompileGroup(group, arch, shard, shards) {
     const both = (v) => {
       const f = fuse(v.graph, { keep: v.keep });
       const fk = v.keep.map((id) => f.index.get(id));
-      lists.push(lowerMI355X(f.graph), lowerMI355X(v.graph), lowerMI355X(f.graph, { perf: true, keep: fk }), lowerMI355X(v.graph, { perf: true, keep: v.keep }));
+      lists.push(lowerMI355X(f.graph), lowerMI355X(v.graph), lowerMI355X(f.graph, { perf: true, keep: fk }), lowerMI355X(v.graph, { perf: true, keep: v.keep, rowFolds: false }));
     };
     for (const R of [8192, 64]) {
       for (let seed = 0; seed < 8; seed++) { const w = chainWorkload(seed, R, 1024); both(w.forward); both(w.gradient); }
@@ -214,7 +214,7 @@ function precompileGroup(group, arch, shard, shards) {
     for (const w of workloads()) {
       const m = w.make();
       for (const v of w.variants) {
-        if (v === 'unfused') { lists.push(lowerMI355X(m.graph, { perf: true, keep: m.outputs })); continue; }
+        if (v === 'unfused') { lists.push(lowerMI355X(m.graph, { perf: true, keep: m.outputs, rowFolds: false })); continue; }
         const f = fuse(m.graph, { keep: m.outputs, recompute: v === 'recompute' });
         lists.push(lowerMI355X(f.graph, { perf: true, keep: m.outputs.map((id) => f.index.get(id)) }));
       }
@@ -237,7 +237,7 @@ function precompileGroup(group, arch, shard, shards) {
         const f = fuse(graph, { keep, attention });
         lists.push(lowerMI355X(f.graph), lowerMI355X(f.graph, { perf: true, keep: keep.map((id) => f.index.get(id)) }));
       }
-      lists.push(lowerMI355X(graph, { perf: true, keep }));
+      lists.push(lowerMI355X(graph, { perf: true, keep, rowFolds: false }));
     }
     return precompile(lists, arch);
   }

@@ -105,7 +105,8 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers)
       }
       return fold;
     });
-    const f = foldReductions(bodyOf(node), node.attrs.output, folds);
+    const chain = node.op === 'fused' ? { body: bodyOf(node), output: node.attrs.output } : oneOpBody(graph, node);
+    const f = foldReductions(chain.body, chain.output, folds);
     const t = opts.tuning || {};
     return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(f.body, f.output, { tuning: t.rowreduce || t.row, lastReads })));
   }
@@ -211,7 +212,7 @@ function matmulSlots(n) {
  * such sinks, e.g. the gradient flowing into the max shift's stopGradient, or the dX of a
  * one-hot input): no launch, no buffer. Inputs and constants are never dead.
  */
-function perfPlan(graph, keep) {
+function perfPlan(graph, keep, rowFolding) {
   const cons = consumersOf(graph);
   const live = new Set();
   for (let id = graph.nodes.length - 1; id >= 0; id--) {
@@ -260,19 +261,20 @@ function perfPlan(graph, keep) {
     }
   }
   // Row statistics folded into their reduction: a plain sum or max over the last
-  // non-trivial axis whose consumers (one or two) are all fused elementwise chains of its
-  // own size (LayerNorm's mean and deviation scale, softmax's row scale, and the backward
-  // pass's chains over the same statistics), every operand of each chain a value of that
+  // non-trivial axis whose consumers (one or two) are all elementwise chains of its own
+  // size, fused or a single op (LayerNorm's mean and deviation scale, softmax's row
+  // scale, the backward pass's chains over the same statistics, the loss's log-sum and
+  // mean), every operand of each chain a value of that
   // size (read at the row index), launches nothing: each chain runs as a rowwise kernel
   // that forms the reduction itself from the reduction's operand, its body on the row's
   // reduced value in registers — the same reduction order and the same ops in the same
   // order, so the same bits as the separate launches. The reductions a chain takes in
   // must share one operand shape (one rowwise kernel walks one row length).
   const rowFolds = new Map();   // chain id -> [{ red: reduction id, pos: its operand positions }]
-  const isChain = (c, rows) => c.op === 'fused' && c.attrs.kind === 'elementwise' && size(c.shape) === rows
-    && c.inputs.every((i) => size(graph.nodes[i].shape) === rows && !folded.has(i));
+  const isChain = (c, rows) => ((c.op === 'fused' && c.attrs.kind === 'elementwise') || ELEMENTWISE_OPS.has(c.op))
+    && size(c.shape) === rows && c.inputs.every((i) => size(graph.nodes[i].shape) === rows && !folded.has(i));
   const cand = new Set();
-  for (const n of graph.nodes) {
+  for (const n of rowFolding ? graph.nodes : []) {
     if ((n.op !== 'sum' && n.op !== 'max') || keep.has(n.id) || dead.has(n.id) || cons[n.id].length === 0) continue;
     const inShape = graph.nodes[n.inputs[0]].shape;
     if (size(inShape.slice(n.attrs.axis + 1)) !== 1 || inShape[n.attrs.axis] === 1) continue;
@@ -414,7 +416,9 @@ function foldReductions(body, output, folds) {
  * applied to fused kernels only; tuning ({ ew: { unroll, nt, blocks }, colreduce: { blocks } })
  * overrides the kernels' launch-shape defaults (used by sweeps); perf and
  * keep (node ids) as described at the top of this file; batch: false keeps the
- * perf lowering's launches one dispatch each, in graph order.
+ * perf lowering's launches one dispatch each, in graph order; rowFolds: false keeps
+ * every reduction and its producer a launch of their own (an unfused graph measured
+ * against its fused form, where a fold would be fusion by another name).
  * Returns { launches, workspace, aliases, folded, dead, batches } (workspace: bytes of
  * scratch the largest launch needs; aliases: [[node, source]]; folded and dead: node
  * ids with neither a launch nor a buffer; batches, perf only: [{ start, count, kernels, wsStride }]).
@@ -437,7 +441,7 @@ const STREAM_FROM = 1 << 20;
 function lowerMI355X(graph, options) {
   const opts = options || {};
   if (opts.perf && !opts.keep) throw new Error('the perf lowering needs `keep`: the nodes whose values are read');
-  const plan = opts.perf ? perfPlan(graph, new Set(opts.keep))
+  const plan = opts.perf ? perfPlan(graph, new Set(opts.keep), opts.rowFolds !== false)
     : { aliases: new Map(), folded: new Set(), views: new Map(), broadcasts: new Map(), dead: new Set(), rowFolds: new Map() };
   const cache = new Map();
   const launches = [];

@@ -29,8 +29,8 @@ def take_block(a: np.ndarray, shape: Sequence[int], p: int, q: int, b: int) -> n
 
 
 def _producer_body(graph, p):
-    """The body nodes and output index of producer node `p`: a fused node's own body, or
-    its one op on inputs a0.. (the node's operands in order)."""
+    """The body nodes and output index of node `p` (a producer or a chain): a fused node's
+    own body, or its one op on inputs a0.. (the node's operands in order)."""
     if p["op"] == "fused":
         return p["attrs"]["body"]["nodes"], p["attrs"]["output"]
     ins = [{"op": "input", "inputs": [], "attrs": {"name": f"a{k}", "shape": graph["nodes"][i]["shape"]},
@@ -39,19 +39,24 @@ def _producer_body(graph, p):
 
 
 def fold_reductions(graph, node_id, folds):
-    """A launch of the perf lowering that took row reductions into a chain (its record's
-    rowFolds: [{reduction, pos}], with producer and producerPos where the reduction's
-    operand is formed in the launch too): the chain's node with each body input at `pos`
-    (the reduction's value) replaced by the reduction itself, applied to a new input
-    a{pos[0]} — or to the producer's body on inputs a{producerPos[j]} — and the launch's
-    operand node ids (the reduction's operand in those positions, or the producer's
-    operands). Restated here from the lowering's rule, so a wrong fold there fails the
-    judge."""
+    """A launch of the perf lowering that took row reductions into a chain, fused or a
+    single op (its record's rowFolds: [{reduction, pos}], with producer and producerPos
+    where the reduction's operand is formed in the launch too): the chain as a fused node,
+    each body input at `pos` (the reduction's value) replaced by the reduction itself,
+    applied to a new input a{pos[0]} — or to the producer's body on inputs
+    a{producerPos[j]} — and the launch's operand node ids (the reduction's operand in
+    those positions, or the producer's operands). Restated here from the lowering's rule,
+    so a wrong fold there fails the judge."""
     node = graph["nodes"][node_id]
     if not folds:
         return node, list(node["inputs"])
     at = {p: f for f in folds for p in f["pos"]}
-    body = node["attrs"]["body"]["nodes"]
+    if node["op"] == "fused":
+        body, chain_out, attrs = node["attrs"]["body"]["nodes"], node["attrs"]["output"], node["attrs"]
+    else:
+        # A single-op chain: its op on inputs a0.. (the node's operands in order).
+        body, chain_out = _producer_body(graph, node)
+        attrs = {"kind": "elementwise", "pattern": "elementwise"}
     out, where, reduced = [], {}, {}
     for bid, b in enumerate(body):
         f = at.get(int(b["attrs"]["name"][1:])) if b["op"] == "input" else None
@@ -103,8 +108,8 @@ def fold_reductions(graph, node_id, folds):
                 inputs.extend([None] * (p + 1 - len(inputs)))
                 inputs[p] = pins[j]
     assert None not in inputs
-    attrs = dict(node["attrs"], body={"nodes": out}, output=where[node["attrs"]["output"]])
-    return dict(node, attrs=attrs, inputs=inputs), inputs
+    attrs = dict(attrs, body={"nodes": out}, output=where[chain_out])
+    return dict(node, op="fused", attrs=attrs, inputs=inputs), inputs
 
 
 def merge_twin(n, t):

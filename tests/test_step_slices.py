@@ -99,9 +99,12 @@ def test_folded_row_reductions_are_the_chain_on_the_reduction(tool):
                 chain_ops.append((rv, re_))
             else:
                 chain_ops.append((ops[pos].astype(np.float64), np.zeros(ops[pos].size)))
-        body = graph["nodes"][k]["attrs"]["body"]
+        chain = graph["nodes"][k]
+        if chain["op"] == "fused":
+            body, out = chain["attrs"]["body"], chain["attrs"]["output"]
+        else:
+            body, out = bounds.one_op_graph(graph, chain)
         carried = {f"a{p}": ce for p, ce in enumerate(chain_ops)}
         r = bounds.reference_with_bounds(body, {}, carried=carried)
-        out = graph["nodes"][k]["attrs"]["output"]
         assert np.array_equal(v, r["values"][out]) and np.all(np.isfinite(v)), k
         assert np.array_equal(e, r["bounds"][out]), k
