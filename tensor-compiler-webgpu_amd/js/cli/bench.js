@@ -71,7 +71,7 @@ function timeLaunches(runner, bench, program, reps) {
     const n = members.length;
     for (const l of members) {
       out.push({ node: l.node, kind: l.kind, pattern: l.pattern || null, code: l.code, bytes: l.bytes, flops: l.flops,
-        us: r.stats.one.median / n, minUs: r.stats.one.min / n, maxUs: r.stats.one.max / n, rowFolds: l.rowFolds || null,
+        us: r.stats.one.median / n, minUs: r.stats.one.min / n, maxUs: r.stats.one.max / n, rowFolds: l.rowFolds || null, absorbed: l.absorbed || null,
         batched: n > 1 ? n : undefined });
     }
     one.destroy();
@@ -86,10 +86,10 @@ function timeLaunches(runner, bench, program, reps) {
  * the summed times of its members' unfused launches, each timed alone. A group wins or
  * loses only when the ranges do not overlap (the fused launch's min-max against the
  * members' summed mins and maxes). A launch that also forms the reductions folded into
- * it (the perf lowering's row folds), and the producers of their operands formed in the
- * same launch, does their work as well: the unfused launches of those reductions and
- * producers (of their groups' members, where one is a group's sink) count on its side
- * too (`folded`: their node ids in the unfused graph).
+ * it (the perf lowering's row folds), the producers of their operands formed in the
+ * same launch, and the producers an elementwise launch absorbed, does their work as well:
+ * the unfused launches of those nodes (of their groups' members, where one is a group's
+ * sink) count on its side too (`folded`: their node ids in the unfused graph).
  */
 function groupVerdicts(f, launchF, launchU) {
   const fusedAt = new Map(launchF.map((l) => [l.node, l]));
@@ -105,16 +105,18 @@ function groupVerdicts(f, launchF, launchU) {
     if (!fl) continue;
     const members = new Set(g.members);
     const folded = [];
-    for (const rf of fl.rowFolds || []) {
-      for (const fid of rf.producer === undefined ? [rf.reduction] : [rf.reduction, rf.producer]) {
-        const g2 = groupAt.get(fid);
-        if (g2 === g) continue;
-        const id = g2 ? g2.sink : original.get(fid);
-        if (id === undefined) continue;
-        folded.push(id);
-        if (g2) for (const m of g2.members) members.add(m);
-        else members.add(id);
-      }
+    const formed = [];
+    const walk = (records) => { for (const a of records || []) { formed.push(a.producer); walk(a.absorbed); } };
+    walk(fl.absorbed);
+    for (const rf of fl.rowFolds || []) formed.push(...(rf.producer === undefined ? [rf.reduction] : [rf.reduction, rf.producer]));
+    for (const fid of formed) {
+      const g2 = groupAt.get(fid);
+      if (g2 === g) continue;
+      const id = g2 ? g2.sink : original.get(fid);
+      if (id === undefined) continue;
+      folded.push(id);
+      if (g2) for (const m of g2.members) members.add(m);
+      else members.add(id);
     }
     const sum = { median: 0, min: 0, max: 0 };
     let launches = 0;

@@ -741,6 +741,7 @@ async function gpuLocal(req, dir) {
   }
   entry.canaryIntact = entry.gpuCanary && entry.gpuPerfCanary;
   entry.rowFolds = rowFoldsOf(fs.lowered);
+  entry.absorbed = absorbedOf(fs.lowered);
   entry.aliases = fs.lowered.aliases;
   entry.folded = fs.lowered.folded;
   entry.dead = fs.lowered.dead;
@@ -898,7 +899,7 @@ async function gpuStepSlices(req, dir) {
     loss: r.values[fs.loss][0], dispatchKinds: fs.lowered.launches.map((l) => l.kind),
     splitK: fs.lowered.launches.filter((l) => l.kernels.some((k) => /_red$/.test(k.name))).length,
     batches: (fs.lowered.batches || []).length, aliases: fs.lowered.aliases, folded: fs.lowered.folded, dead: fs.lowered.dead,
-    rowFolds: rowFoldsOf(fs.lowered) });
+    rowFolds: rowFoldsOf(fs.lowered), absorbed: absorbedOf(fs.lowered) });
   bundle.close({ device: runner.info() });
 }
 
@@ -906,6 +907,13 @@ async function gpuStepSlices(req, dir) {
 function rowFoldsOf(lowered) {
   const out = {};
   for (const l of lowered.launches) if (l.rowFolds) out[l.node] = l.rowFolds;
+  return out;
+}
+
+/** {reader node: [{ producer, pos, producerPos, absorbed? }]}: the producers a perf lowering's launches form. */
+function absorbedOf(lowered) {
+  const out = {};
+  for (const l of lowered.launches) if (l.absorbed) out[l.node] = l.absorbed;
   return out;
 }
 
@@ -1319,7 +1327,9 @@ async function main() {
     case 'transformer-forward': out = transformerForward(req); break;
     case 'perf-lower': {
       // The perf lowering of a model step or of a graph: launches, aliases, folded nodes, operand views.
-      let g, keep;
+      // A model's fused step as the trainer lowers it (producers absorbed); a graph with
+      // absorb: true likewise.
+      let g, keep, absorb = !!req.absorb;
       if (req.model && req.unfused) {
         // The model's step graph without fusion (the bench's unfused step).
         const { modelStep } = require('../src/builders/models');
@@ -1332,6 +1342,7 @@ async function main() {
         const fs = fusedStep(modelStep(req).step);
         g = fs.graph;
         keep = [fs.loss, fs.logits].concat(Object.values(fs.outputs));
+        absorb = true;
       } else {
         g = Graph.fromJSON(req.graph);
         keep = req.keep || [];
@@ -1342,9 +1353,9 @@ async function main() {
           keep = keep.map((id) => f.index.get(id));
         }
       }
-      const l = lowerMI355X(g, { perf: true, keep });
+      const l = lowerMI355X(g, { perf: true, keep, absorb });
       const plain = new Map(lowerMI355X(g).launches.map((x) => [x.node, x]));
-      out = { graph: g.toJSON(), keep, aliases: l.aliases, folded: l.folded, dead: l.dead, rowFolds: rowFoldsOf(l),
+      out = { graph: g.toJSON(), keep, aliases: l.aliases, folded: l.folded, dead: l.dead, rowFolds: rowFoldsOf(l), absorbed: absorbedOf(l),
         launches: l.launches.map((x) => ({ node: x.node, kind: x.kind, inputs: x.inputs, views: x.views || null, modes: gemmModes(x),
           split: gemmSplit(x), plainSplit: gemmSplit(plain.get(x.node)) })) };
       break;

@@ -90,7 +90,7 @@ function widenInputs(body, output, folds) {
 }
 
 /** Kernels for one node. */
-function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers) {
+function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs) {
   if (rowFold) {
     // A row-statistics chain with its reductions folded in: the rowwise kernel of the
     // reductions, with their own tuning so the rows are reduced in their order.
@@ -111,7 +111,7 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers)
     return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(f.body, f.output, { tuning: t.rowreduce || t.row, lastReads })));
   }
   if (node.op === 'fused') {
-    const w = widenInputs(bodyOf(node), node.attrs.output, folds);
+    const w = absorbProducers(graph, widenInputs(bodyOf(node), node.attrs.output, folds), absorbs);
     const b = w.body;
     const out = w.output;
     const kind = node.attrs.kind;
@@ -132,7 +132,7 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers)
   }
   if (ELEMENTWISE_OPS.has(node.op) || GATHERS.has(node.op)) {
     const one = oneOpBody(graph, node);
-    const { body, output } = widenInputs(one.body, one.output, folds);
+    const { body, output } = absorbProducers(graph, widenInputs(one.body, one.output, folds), absorbs);
     const kind = GATHERS.has(node.op) ? 'gather' : 'elementwise';
     return Object.assign({ kind }, single(cg.elementwiseKernel(body, output, node.shape, { tuning: (opts.tuning || {}).ew, lastReads })));
   }
@@ -212,7 +212,7 @@ function matmulSlots(n) {
  * such sinks, e.g. the gradient flowing into the max shift's stopGradient, or the dX of a
  * one-hot input): no launch, no buffer. Inputs and constants are never dead.
  */
-function perfPlan(graph, keep, rowFolding) {
+function perfPlan(graph, keep, rowFolding, absorbing) {
   const cons = consumersOf(graph);
   const live = new Set();
   for (let id = graph.nodes.length - 1; id >= 0; id--) {
@@ -343,6 +343,45 @@ function perfPlan(graph, keep, rowFolding) {
       f.ppos = p.inputs.map((_, j) => (j === 0 ? f.pos[0] : next++));
     }
   }
+  // Producers absorbed into their one reader (with `absorb`: the trainer's lowering). An
+  // elementwise node (one op or a fused chain) that nothing keeps and whose only live
+  // reader is another elementwise node runs inside that reader's kernel: the reader's body
+  // forms the producer's value from the producer's own operands, with the producer's ops
+  // in their order, where it would have loaded it — the same bits, without writing the
+  // value and reading it back. Autodiff leaves such pairs where the producer's other
+  // consumer is dead (a stopGradient branch) and the fusion contract, which keeps every
+  // node, could not join them. A producer read through a broadcast inside the reader's
+  // body is formed at the broadcast's source index. A producer may have absorbed its own
+  // producers (taken along), row-statistics chains take no part, and every operand fits
+  // one argument block.
+  const absorbed = new Map();   // reader id -> [{ prod, pos: [reader positions], ppos, prodFolds, nested }]
+  const operands = new Map();   // reader id -> its kernel's operand count with what it absorbed
+  const isElementwise = (n) => ELEMENTWISE_OPS.has(n.op) || (n.op === 'fused' && n.attrs.kind === 'elementwise');
+  for (const e of absorbing ? graph.nodes : []) {
+    if (!isElementwise(e) || folded.has(e.id) || dead.has(e.id) || aliases.has(e.id) || rowFolds.has(e.id)) continue;
+    const own = broadcasts.get(e.id);
+    let next = e.inputs.length;
+    const list = [];
+    for (const pid of new Set(e.inputs)) {
+      const p = graph.nodes[pid];
+      const at = e.inputs.map((i, pos) => (i === pid ? pos : -1)).filter((pos) => pos >= 0);
+      if (!isElementwise(p) || keep.has(pid) || folded.has(pid) || dead.has(pid) || aliases.has(pid) || rowFolds.has(pid)) continue;
+      if (at.some((pos) => own && own.has(pos))) continue;
+      if (new Set(cons[pid].filter((c) => !dead.has(c))).size !== 1) continue;
+      const pf = broadcasts.get(pid);
+      if (!p.inputs.every((i, j) => !folded.has(i) || (pf && pf.has(j)) || (absorbed.get(pid) || []).some((a) => a.prod === i))) continue;
+      const m = operands.get(pid) || p.inputs.length;
+      if (next + m - 1 > cg.MAX_IN) continue;
+      const ppos = [];
+      for (let j = 0; j < m; j++) ppos.push(j === 0 ? at[0] : next + j - 1);
+      list.push({ prod: pid, pos: at, ppos, prodFolds: pf || null, nested: absorbed.get(pid) || null });
+      next += m - 1;
+    }
+    if (!list.length) continue;
+    absorbed.set(e.id, list);
+    operands.set(e.id, next);
+    for (const a of list) folded.add(a.prod);
+  }
   const views = new Map();
   for (const n of graph.nodes) {
     for (const [slot, pos] of matmulSlots(n)) {
@@ -363,7 +402,45 @@ function perfPlan(graph, keep, rowFolding) {
       views.get(n.id)[slot] = { pos, source: cur, view, size: size(graph.nodes[cur].shape) };
     }
   }
-  return { aliases, folded, views, broadcasts, dead, rowFolds };
+  return { aliases, folded, views, broadcasts, dead, rowFolds, absorbed };
+}
+
+/**
+ * `w.body` with the input at the positions of each absorbed producer replaced by that
+ * producer's body on the producer's own operands (inputs a{ppos[j]}, broadcasts it reads
+ * in place widened as for any body, and what it absorbed formed the same way): the
+ * reader's kernel forms the producer's value where it would have loaded it. Returns
+ * { body, output }.
+ */
+function absorbProducers(graph, w, absorbs) {
+  if (!absorbs) return w;
+  const g = new Graph();
+  const map = new Map();
+  const at = new Map();
+  for (const a of absorbs) for (const pos of a.pos) at.set(pos, a);
+  const formed = new Map();
+  for (const n of w.body.nodes) {
+    const a = n.op === 'input' ? at.get(Number(n.attrs.name.slice(1))) : undefined;
+    if (a) {
+      if (!formed.has(a)) {
+        const p = graph.nodes[a.prod];
+        const one = p.op === 'fused' ? { body: bodyOf(p), output: p.attrs.output } : oneOpBody(graph, p);
+        const pw = absorbProducers(graph, widenInputs(one.body, one.output, a.prodFolds), a.nested);
+        const pm = new Map();
+        for (const pn of pw.body.nodes) {
+          pm.set(pn.id, pn.op === 'input' ? g.input(`a${a.ppos[Number(pn.attrs.name.slice(1))]}`, pn.shape)
+            : g.emit(pn.op, pn.inputs.map((i) => pm.get(i)), pn.attrs));
+        }
+        formed.set(a, pm.get(pw.output));
+      }
+      map.set(n.id, formed.get(a));
+    } else if (n.op === 'input') {
+      map.set(n.id, g.input(n.attrs.name, n.shape));
+    } else {
+      map.set(n.id, g.emit(n.op, n.inputs.map((i) => map.get(i)), n.attrs));
+    }
+  }
+  return { body: g, output: map.get(w.output) };
 }
 
 /**
@@ -441,8 +518,8 @@ const STREAM_FROM = 1 << 20;
 function lowerMI355X(graph, options) {
   const opts = options || {};
   if (opts.perf && !opts.keep) throw new Error('the perf lowering needs `keep`: the nodes whose values are read');
-  const plan = opts.perf ? perfPlan(graph, new Set(opts.keep), opts.rowFolds !== false)
-    : { aliases: new Map(), folded: new Set(), views: new Map(), broadcasts: new Map(), dead: new Set(), rowFolds: new Map() };
+  const plan = opts.perf ? perfPlan(graph, new Set(opts.keep), opts.rowFolds !== false, opts.absorb === true && opts.rowFolds !== false)
+    : { aliases: new Map(), folded: new Set(), views: new Map(), broadcasts: new Map(), dead: new Set(), rowFolds: new Map(), absorbed: new Map() };
   const cache = new Map();
   const launches = [];
   let workspace = 0;
@@ -471,6 +548,12 @@ function lowerMI355X(graph, options) {
         for (const pos of f.pos) inputs[pos] = pins[0];
         f.ppos.forEach((pos, j) => { inputs[pos] = pins[j]; });
       }
+    }
+    for (const a of plan.absorbed.get(node.id) || []) {
+      // An absorbed producer's operands (its own, with what it absorbed), in its positions.
+      const pins = inputsOf(graph.nodes[a.prod]);
+      for (const pos of a.pos) inputs[pos] = pins[0];
+      a.ppos.forEach((pos, j) => { inputs[pos] = pins[j]; });
     }
     return inputs;
   };
@@ -515,6 +598,10 @@ function lowerMI355X(graph, options) {
     };
     const rowKey = rowFold ? rowFold.map((f) => [f.pos, graph.nodes[f.red].op, graph.nodes[f.red].attrs,
       graph.nodes[graph.nodes[f.red].inputs[0]].shape, prodKey(f)]) : null;
+    const absorbs = plan.absorbed.get(node.id) || null;
+    const absorbSig = (a) => [a.pos, prodKey({ prod: a.prod, ppos: a.ppos, prodFolds: a.prodFolds }),
+      a.nested ? a.nested.map(absorbSig) : null];
+    const absorbKey = absorbs ? absorbs.map(absorbSig) : null;
     const inputs = inputsOf(node);
     const lastReads = [];
     inputs.forEach((id, pos) => {
@@ -524,9 +611,9 @@ function lowerMI355X(graph, options) {
     // reads only: reuse across identical nodes.
     const peers = peersOf(node);
     const key = JSON.stringify([node.op, node.inputs.map((id) => graph.nodes[id].shape), node.attrs, node.shape,
-      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey, rowKey, lastReads, peers]);
+      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey, rowKey, lastReads, peers, absorbKey]);
     let k = cache.get(key);
-    if (!k) { k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers); cache.set(key, k); }
+    if (!k) { k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs); cache.set(key, k); }
     workspace = Math.max(workspace, k.workspace);
     launches.push({
       node: node.id, op: node.op, kind: k.kind, pattern: node.op === 'fused' ? node.attrs.pattern : undefined,
@@ -537,6 +624,12 @@ function lowerMI355X(graph, options) {
       // The reduction folded into this launch, and the launch's own body (for node-local checks).
       launches[launches.length - 1].rowFolds = rowFold.map((f) => (f.prod === undefined ? { reduction: f.red, pos: f.pos }
         : { reduction: f.red, pos: f.pos, producer: f.prod, producerPos: f.ppos }));
+    }
+    if (absorbs) {
+      // The producers this launch forms in place of loading them (for node-local checks).
+      const record = (a) => Object.assign({ producer: a.prod, pos: a.pos, producerPos: a.ppos },
+        a.nested ? { absorbed: a.nested.map(record) } : {});
+      launches[launches.length - 1].absorbed = absorbs.map(record);
     }
     if (v) {
       // Operands read in place: for each folded slot, the node it stands for and the view of its source.

@@ -112,6 +112,85 @@ def fold_reductions(graph, node_id, folds):
     return dict(node, op="fused", attrs=attrs, inputs=inputs), inputs
 
 
+def _absorbed_body(graph, node_id, absorbed):
+    """(body nodes, output index, operand node ids) of node `node_id` with the producers in
+    `absorbed` formed inside its body: each input at `pos` replaced by the producer's own
+    body (with what that producer absorbed, restated the same way) on inputs
+    a{producerPos[j]}, the producer's operands taking those positions."""
+    node = graph["nodes"][node_id]
+    body, out = _producer_body(graph, node)
+    inputs = list(node["inputs"])
+    if not absorbed:
+        return body, out, inputs
+    at = {p: a for a in absorbed for p in a["pos"]}
+    nodes, where, formed = [], {}, {}
+    for bid, b in enumerate(body):
+        a = at.get(int(b["attrs"]["name"][1:])) if b["op"] == "input" else None
+        if a is not None:
+            key = a["producer"]
+            if key not in formed:
+                assert node["inputs"][a["pos"][0]] == a["producer"]
+                pbody, pout, _ = _absorbed_body(graph, a["producer"], a.get("absorbed"))
+                pmap = {}
+                for pid, pn in enumerate(pbody):
+                    if pn["op"] == "input":
+                        name = f"a{a['producerPos'][int(pn['attrs']['name'][1:])]}"
+                        nodes.append(dict(pn, attrs=dict(pn["attrs"], name=name)))
+                    else:
+                        nodes.append(dict(pn, inputs=[pmap[i] for i in pn["inputs"]]))
+                    pmap[pid] = len(nodes) - 1
+                formed[key] = pmap[pout]
+            where[bid] = formed[key]
+        else:
+            nodes.append(dict(b, inputs=[where[i] for i in b["inputs"]]))
+            where[bid] = len(nodes) - 1
+    for a in absorbed:
+        _, _, pins = _absorbed_body(graph, a["producer"], a.get("absorbed"))
+        assert len(pins) == len(a["producerPos"])
+        for p in a["pos"]:
+            inputs[p] = pins[0]
+        for j, p in enumerate(a["producerPos"]):
+            inputs.extend([None] * (p + 1 - len(inputs)))
+            inputs[p] = pins[j]
+    assert None not in inputs
+    return nodes, where[out], inputs
+
+
+def absorbed_producers(absorbed):
+    """Every producer node id in a {reader: [absorbed records]} map, nested ones included."""
+    out = set()
+
+    def walk(records):
+        for a in records or []:
+            out.add(a["producer"])
+            walk(a.get("absorbed"))
+    for records in absorbed.values():
+        walk(records)
+    return out
+
+
+def absorb_producers(graph, node_id, absorbed):
+    """A launch of the perf lowering that absorbed elementwise producers (its record's
+    absorbed: [{producer, pos, producerPos, absorbed?}]): the reader as a fused node whose
+    body forms each producer's value where it would have loaded it, and the launch's
+    operand node ids. Restated here from the lowering's rule, so a wrong absorption there
+    fails the judge."""
+    node = graph["nodes"][node_id]
+    nodes, out, inputs = _absorbed_body(graph, node_id, absorbed)
+    attrs = {"kind": "elementwise", "pattern": node["attrs"].get("pattern", "elementwise"), "body": {"nodes": nodes},
+             "output": out}
+    return dict(node, op="fused", attrs=attrs, inputs=inputs), inputs
+
+
+def restate(graph, node_id, folds=None, absorbed=None):
+    """The launch of node `node_id` as the perf lowering runs it: its row folds or its
+    absorbed producers restated (a launch has one or the other), or the node itself."""
+    if absorbed:
+        assert not folds
+        return absorb_producers(graph, node_id, absorbed)
+    return fold_reductions(graph, node_id, folds)
+
+
 def merge_twin(n, t):
     """Node `n` of the full graph with the shapes of its twin `t` (the same node of the
     one-sequence graph) and the full graph's constants: body nodes keep their op, inputs,
@@ -147,19 +226,22 @@ def local(graph, node, operands: List[np.ndarray]):
     return r["values"][out], r["bounds"][out]
 
 
-def expectations(full, twin, launched, operand, sequences, row_folds=None):
+def expectations(full, twin, launched, operand, sequences, row_folds=None, absorbed=None):
     """Yield (node id, sequence index or None, value, bound) for every launched node:
     per sequence where its output carries the batch axis, whole otherwise.
     `operand(i, s)` is node i's value: its block for sequence index s, or whole for None.
     `row_folds` ({node id: [{reduction, pos}]}, a perf lowering's): those launches are the
-    chain with its row reductions taken in, on the reductions' operands."""
+    chain with its row reductions taken in, on the reductions' operands; `absorbed`
+    ({node id: [{producer, pos, producerPos}]}): those launches form their producers."""
     axis = [batch_axis(n["shape"], t["shape"]) for n, t in zip(full["nodes"], twin["nodes"])]
     row_folds = row_folds or {}
+    absorbed = absorbed or {}
     for nid in launched:
         folds = row_folds.get(nid) or row_folds.get(str(nid))
-        node, ins = fold_reductions(full, nid, folds)
+        took = absorbed.get(nid) or absorbed.get(str(nid))
+        node, ins = restate(full, nid, folds, took)
         if axis[nid] >= 0:
-            tn = merge_twin(node, fold_reductions(twin, nid, folds)[0])
+            tn = merge_twin(node, restate(twin, nid, folds, took)[0])
             for s in range(len(sequences)):
                 ops = [operand(i, s if axis[i] >= 0 else None) for i in ins]
                 v, e = local(twin, tn, ops)

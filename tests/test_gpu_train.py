@@ -13,7 +13,7 @@ import pytest
 
 from conftest import GOLDEN
 from oracle import bounds
-from step_slices import fold_reductions, local
+from step_slices import absorbed_producers, local, restate
 
 pytestmark = pytest.mark.gpu
 
@@ -51,8 +51,10 @@ def node_local(tool, tmp_path, req):
     # Reductions folded into their row-statistics chains, and the producers of their
     # operands formed in the same launches, are the other launches it skips.
     folds = {int(k): v for k, v in gc["rowFolds"].items()}
+    took = {int(k): v for k, v in gc["absorbed"].items()}
     reductions = {f["reduction"] for fs in folds.values() for f in fs}
     producers = {f["producer"] for fs in folds.values() for f in fs if "producer" in f}
+    producers |= absorbed_producers(took)
     assert all(c["fused"]["nodes"][i]["op"] in ("reshape", "transpose", "broadcast")
                for i in skipped - set(gc["dead"]) - reductions - producers)
     assert all(c["fused"]["nodes"][i]["op"] in ("sum", "max") for i in reductions)
@@ -61,8 +63,8 @@ def node_local(tool, tmp_path, req):
     # the chain on the reductions' operands.
     pexp, pbound = {}, {}
     for k in perf:
-        if k in folds:
-            node, ins = fold_reductions(c["fused"], k, folds[k])
+        if k in folds or k in took:
+            node, ins = restate(c["fused"], k, folds.get(k), took.get(k))
             pexp[k], pbound[k] = local(c["fused"], node, [fused_vals[i] for i in ins])
         else:
             pexp[k], pbound[k] = expected[k], bound[k]

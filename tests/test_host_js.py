@@ -206,13 +206,30 @@ def test_perf_lowering_views_address_the_operands(tool, req):
     # and row reductions taken into the row-statistics chains that read them.
     reductions = {f["reduction"] for fs in d["rowFolds"].values() for f in fs}
     producers = {f["producer"] for fs in d["rowFolds"].values() for f in fs if "producer" in f}
-    assert all(nodes[i]["op"] in ("transpose", "broadcast") for i in set(d["folded"]) - reductions - producers)
-    # A folded broadcast is read by elementwise, rowwise or epilogue bodies only (never
-    # by a reduction, a gather or as a matmul operand), through the broadcast's source.
+    absorbed = set()
+
+    def walk(records, reader):
+        for a in records:
+            # An absorbed producer: an elementwise node its reader reads at `pos`, kept by
+            # nobody, read by no other launched node.
+            p = nodes[a["producer"]]
+            assert all(nodes[reader]["inputs"][q] == a["producer"] for q in a["pos"])
+            assert p["op"] in ELEMENTWISE or (p["op"] == "fused" and p["attrs"]["kind"] == "elementwise")
+            assert a["producer"] not in d["keep"] and a["producerPos"][0] == a["pos"][0]
+            assert consumers[a["producer"]] - set(d["dead"]) == {reader}
+            absorbed.add(a["producer"])
+            walk(a.get("absorbed", []), a["producer"])
     consumers = {}
     for n_id, n in enumerate(nodes):
         for i in n["inputs"]:
             consumers.setdefault(i, set()).add(n_id)
+    for reader, records in d["absorbed"].items():
+        walk(records, int(reader))
+    if req["model"] != "mlp":
+        assert absorbed
+    assert all(nodes[i]["op"] in ("transpose", "broadcast") for i in set(d["folded"]) - reductions - producers - absorbed)
+    # A folded broadcast is read by elementwise, rowwise or epilogue bodies only (never
+    # by a reduction, a gather or as a matmul operand), through the broadcast's source.
     for chain, fs in d["rowFolds"].items():
         c = nodes[int(chain)]
         assert (c["op"] == "fused" and c["attrs"]["kind"] == "elementwise") or c["op"] in ELEMENTWISE

@@ -9,7 +9,8 @@ sequence would break the equality."""
 import numpy as np
 
 from oracle import bounds, interp
-from step_slices import batch_axis, expectations, fold_reductions, local, take_block
+from step_slices import (absorb_producers, absorbed_producers, batch_axis, expectations, fold_reductions, local,
+                         take_block)
 
 
 def test_sequence_blocks_equal_the_whole_launch(tmp_path, tool):
@@ -108,3 +109,42 @@ def test_folded_row_reductions_are_the_chain_on_the_reduction(tool):
         r = bounds.reference_with_bounds(body, {}, carried=carried)
         assert np.array_equal(v, r["values"][out]) and np.all(np.isfinite(v)), k
         assert np.array_equal(e, r["bounds"][out]), k
+
+
+def _unabsorbed(graph, nid, records, ops):
+    """(value, bound) of node `nid` evaluated the unabsorbed way: each absorbed producer
+    evaluated first, on its own operands (its producerPos of the launch's operands), then
+    the node's own body on those values and its other operands."""
+    node = graph["nodes"][nid]
+    at = {p: a for a in records or [] for p in a["pos"]}
+    carried = {}
+    for p in range(len(node["inputs"])):
+        a = at.get(p)
+        carried[f"a{p}"] = ops[p] if a is None else _unabsorbed(graph, a["producer"], a.get("absorbed"),
+                                                                 [ops[q] for q in a["producerPos"]])
+    if node["op"] == "fused":
+        body, out = node["attrs"]["body"], node["attrs"]["output"]
+    else:
+        body, out = bounds.one_op_graph(graph, node)
+    r = bounds.reference_with_bounds(body, {}, carried=carried)
+    return r["values"][out], r["bounds"][out]
+
+
+def test_absorbed_producers_are_formed_as_computed(tool):
+    """The trainer's lowering lets an elementwise launch form an elementwise producer that
+    only it reads (the producer's other consumer dead), where it would have loaded it. The
+    checkers' restatement of such a launch (absorb_producers), evaluated in float64 on the
+    launch's operands, equals each producer evaluated first and the reader's own body
+    applied to its value, bit for bit, value and bound."""
+    d = tool("perf-lower", {"model": "transformer", "B": 1})
+    graph, took = d["graph"], {int(k): v for k, v in d["absorbed"].items()}
+    assert len(took) >= 6
+    assert absorbed_producers(took) <= set(d["folded"])
+    rng = np.random.default_rng(4)
+    for k, records in took.items():
+        node, ins = absorb_producers(graph, k, records)
+        ops = [rng.uniform(0.5, 2.0, size=interp.size(graph["nodes"][i]["shape"])).astype(np.float32) for i in ins]
+        v, e = local(graph, node, ops)
+        rv, re_ = _unabsorbed(graph, k, records, [(o.astype(np.float64), np.zeros(o.size)) for o in ops])
+        assert np.array_equal(v, rv) and np.all(np.isfinite(v)), k
+        assert np.array_equal(e, re_), k
