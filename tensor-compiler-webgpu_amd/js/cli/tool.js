@@ -255,7 +255,7 @@ function precompileGroup(group, arch, shard, shards) {
     for (let i = 1; i <= 100; i++) {
       for (const c of corpusGraphs(i)) {
         const f = fuse(c.graph, { keep: c.keep, recompute: true });
-        lists.push(lowerMI355X(f.graph), lowerMI355X(f.graph, { perf: true, keep: c.keep.map((id) => f.index.get(id)) }));
+        lists.push(lowerMI355X(f.graph), lowerMI355X(f.graph, { perf: true, keep: c.keep.map((id) => f.index.get(id)), absorb: true }));
       }
     }
     for (const w of workloads().filter((x) => x.variants.includes('recompute'))) {
@@ -273,7 +273,7 @@ function precompileGroup(group, arch, shard, shards) {
     for (let i = 1; i <= 2000; i++) {
       for (const c of corpusGraphs(i)) {
         const f = fuse(c.graph, { keep: c.keep });
-        lists.push(lowerMI355X(f.graph), lowerMI355X(f.graph, { perf: true, keep: c.keep.map((id) => f.index.get(id)) }), lowerMI355X(c.graph));
+        lists.push(lowerMI355X(f.graph), lowerMI355X(f.graph, { perf: true, keep: c.keep.map((id) => f.index.get(id)), absorb: true }), lowerMI355X(c.graph));
       }
     }
     const k = shards || 1, me = shard || 0;
@@ -570,7 +570,7 @@ async function gpuFuzz(req, dir) {
       const f = fuse(c.graph, { keep: c.keep, recompute: !!req.recompute });
       const keepF = c.keep.map((id) => f.index.get(id));
       const rf = await runner.run(f.graph, lowerMI355X(f.graph), inputs, { canary: true });
-      const rp = await runner.run(f.graph, lowerMI355X(f.graph, { perf: true, keep: keepF }), inputs, { canary: true });
+      const rp = await runner.run(f.graph, lowerMI355X(f.graph, { perf: true, keep: keepF, absorb: true }), inputs, { canary: true });
       const ru = await runner.run(c.graph, lowerMI355X(c.graph), inputs, { canary: true });
       const entry = { program: i, label: c.label, graph: c.graph.toJSON(), fused: f.graph.toJSON(), origin: f.origin, keep: c.keep,
         inputs: ins, gpuFused: {}, gpuUnfused: {}, gpuPerf: {},
@@ -1159,7 +1159,7 @@ async function main() {
       const { checkSchedule } = require('../src/testing/schedule_check');
       out = [];
       const one = (name, graph, keep) => {
-        const lw = lowerMI355X(graph, { perf: true, keep });
+        const lw = lowerMI355X(graph, { perf: true, keep, absorb: true });
         const alias = new Map(lw.aliases);
         const owner = (id) => (alias.has(id) ? alias.get(id) : id);
         for (const streams of [2, 3, 4]) {
@@ -1201,7 +1201,7 @@ async function main() {
       const { planArena } = require('../src/mi355x/arena');
       const { simulateArena, peakLive } = require('../src/testing/arena_check');
       const one = (name, graph, keep) => {
-        const lowered = lowerMI355X(graph, { perf: true, keep });
+        const lowered = lowerMI355X(graph, { perf: true, keep, absorb: true });
         const plan = planArena(graph, lowered, { keep });
         const res = { name, launches: lowered.launches.length, buffers: plan.buffers.length, bytes: plan.size,
           unshared: plan.unshared, peak: peakLive(lowered, plan), check: simulateArena(graph, lowered, plan) };
@@ -1274,8 +1274,8 @@ async function main() {
       // the plain order; with `plant`, the two planted mistakes of batch_check.js as well.
       const { checkBatches, plantBatchMistake } = require('../src/testing/batch_check');
       const one = (name, graph, keep) => {
-        const plain = lowerMI355X(graph, { perf: true, keep, batch: false });
-        const batched = lowerMI355X(graph, { perf: true, keep });
+        const plain = lowerMI355X(graph, { perf: true, keep, batch: false, absorb: true });
+        const batched = lowerMI355X(graph, { perf: true, keep, absorb: true });
         const res = { name, launches: batched.launches.length, check: checkBatches(plain, batched) };
         if (req.plant) {
           for (const kind of ['dependent', 'early', 'grid']) {

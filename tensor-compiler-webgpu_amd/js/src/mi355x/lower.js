@@ -371,7 +371,8 @@ function perfPlan(graph, keep, rowFolding, absorbing) {
       const pf = broadcasts.get(pid);
       if (!p.inputs.every((i, j) => !folded.has(i) || (pf && pf.has(j)) || (absorbed.get(pid) || []).some((a) => a.prod === i))) continue;
       const m = operands.get(pid) || p.inputs.length;
-      if (next + m - 1 > cg.MAX_IN) continue;
+      // A producer of constants alone has no operand to take the reader's slot.
+      if (m === 0 || next + m - 1 > cg.MAX_IN) continue;
       const ppos = [];
       for (let j = 0; j < m; j++) ppos.push(j === 0 ? at[0] : next + j - 1);
       list.push({ prod: pid, pos: at, ppos, prodFolds: pf || null, nested: absorbed.get(pid) || null });

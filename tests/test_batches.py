@@ -30,7 +30,7 @@ def test_planted_batch_mistakes_are_caught(tool):
     batching two such launches by name alone once ran one member over the other's grid,
     which the GPU fuzz test caught as a canary overwrite and as perf-lowering
     differences in 3 of 4000 corpus graphs)."""
-    res = tool("batch-check", {"models": MODELS[:1], "corpus": {"from": 1, "to": 100}, "plant": True})
+    res = tool("batch-check", {"models": MODELS[:1], "corpus": {"from": 1, "to": 200}, "plant": True})
     dep = [r for r in res if "dependent" in r]
     early = [r for r in res if "early" in r]
     grid = [r for r in res if "grid" in r]
@@ -80,3 +80,12 @@ def test_xcd_grouped_batches_choose_members_by_place(tool):
         assert src.count("const tcmi::Wg wg = tcmi::xcd_grouped();") == 1, k["name"]
         assert f"B.m[wg.z / {k['z']}u]" in src and f"(wg.z % {k['z']}u), wg.x, wg.y)" in src, k["name"]
         assert "blockIdx" not in src, k["name"]
+
+
+def test_a_producer_of_constants_is_not_absorbed(tool):
+    """Corpus program 1285 (forward) holds a fused chain of constants alone ([1, 1], no
+    operands) read by one elementwise node: absorbing it would leave its reader's slot
+    with no operand, so it stays a launch, and the lowering (producers absorbed, as the
+    trainer lowers) goes through."""
+    res = tool("batch-check", {"corpus": {"from": 1285, "to": 1285}})
+    assert len(res) == 2 and all(r["check"]["ok"] for r in res), res
