@@ -141,8 +141,9 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers,
     const axis = node.attrs.axis;
     const outer = size(inShape.slice(0, axis)), n = inShape[axis], inner = size(inShape.slice(axis + 1));
     if (inner === 1) {
-      // A reduction over the last non-trivial axis: the rowwise kernel on [outer, n].
-      const { body, output } = oneOpBody(graph, node, [[outer, n]], { axis: 1, keepDims: true });
+      // A reduction over the last non-trivial axis: the rowwise kernel on [outer, n] (its
+      // operand formed in place where the lowering absorbed the operand's producer).
+      const { body, output } = absorbProducers(graph, oneOpBody(graph, node, [[outer, n]], { axis: 1, keepDims: true }), absorbs);
       const t = opts.tuning || {};
       return Object.assign({ kind: 'rowreduce' }, single(cg.rowwiseKernel(body, output, { tuning: t.rowreduce || t.row, lastReads })));
     }
@@ -354,11 +355,19 @@ function perfPlan(graph, keep, rowFolding, absorbing) {
   // body is formed at the broadcast's source index. A producer may have absorbed its own
   // producers (taken along), row-statistics chains take no part, and every operand fits
   // one argument block.
+  // A row reduction over the last axis of a 2-D operand (a rowwise kernel) absorbs its
+  // operand's producer too, where the producer's body, and those of the producers it
+  // brings along, hold full-size values only (the rule of producer folds).
   const absorbed = new Map();   // reader id -> [{ prod, pos: [reader positions], ppos, prodFolds, nested }]
   const operands = new Map();   // reader id -> its kernel's operand count with what it absorbed
   const isElementwise = (n) => ELEMENTWISE_OPS.has(n.op) || (n.op === 'fused' && n.attrs.kind === 'elementwise');
+  const isRowReduction = (n) => (n.op === 'sum' || n.op === 'max') && n.attrs.axis === 1
+    && graph.nodes[n.inputs[0]].shape.length === 2;
+  const fullTree = (id, n) => size(graph.nodes[id].shape) === n && fullBody(graph.nodes[id])
+    && (absorbed.get(id) || []).every((a) => fullTree(a.prod, n));
   for (const e of absorbing ? graph.nodes : []) {
-    if (!isElementwise(e) || folded.has(e.id) || dead.has(e.id) || aliases.has(e.id) || rowFolds.has(e.id)) continue;
+    const reduction = isRowReduction(e);
+    if (!(isElementwise(e) || reduction) || folded.has(e.id) || dead.has(e.id) || aliases.has(e.id) || rowFolds.has(e.id)) continue;
     const own = broadcasts.get(e.id);
     let next = e.inputs.length;
     const list = [];
@@ -368,6 +377,7 @@ function perfPlan(graph, keep, rowFolding, absorbing) {
       if (!isElementwise(p) || keep.has(pid) || folded.has(pid) || dead.has(pid) || aliases.has(pid) || rowFolds.has(pid)) continue;
       if (at.some((pos) => own && own.has(pos))) continue;
       if (new Set(cons[pid].filter((c) => !dead.has(c))).size !== 1) continue;
+      if (reduction && !fullTree(pid, size(p.shape))) continue;
       const pf = broadcasts.get(pid);
       if (!p.inputs.every((i, j) => !folded.has(i) || (pf && pf.has(j)) || (absorbed.get(pid) || []).some((a) => a.prod === i))) continue;
       const m = operands.get(pid) || p.inputs.length;
