@@ -8,7 +8,10 @@
 // Operands are strided views: element (b, r, c) of an operand is at
 // V::batch(b) + r·V::SR + c·V::SC of its buffer, so a transposed operand
 // (autodiff's transpose(W) and transpose(X), attention's transposed keys, a
-// head split) is read in place instead of being materialised first. The load
+// head split) is read in place instead of being materialised first. A mapped view
+// (V::MAPPED) places the element at V::batch(b) + V::row(r) + V::col(c) instead: a
+// chain of transposes and reshapes (attention's heads merged back into rows) makes
+// the row or column index step over several strides. The load
 // path per operand (MODE) follows its layout:
 //   MODE_C  c contiguous (SC = 1): 128-bit loads along c (the row-major case)
 //   MODE_R  r contiguous (SR = 1): 128-bit loads along r (the transposed case)
@@ -64,6 +67,32 @@ struct DenseView {
   static __device__ __forceinline__ size_t batch(uint32_t b) { return (size_t)b * R * C; }
 };
 
+// One LDS array of FLOATS floats per size: every caller asking for the same size gets the
+// same array.
+template <int FLOATS>
+__device__ __forceinline__ float* lds_pool() {
+  __shared__ __attribute__((aligned(16))) float pool[FLOATS];
+  return pool;
+}
+
+// A view's row and column offsets: r·SR and c·SC, or, for a mapped view (MAPPED: an
+// operand read through a chain of transposes and reshapes, whose row or column index
+// steps over several strides), its own row(r) and col(c).
+template <class V>
+__device__ constexpr auto mapped_view(int) -> decltype(V::MAPPED, bool()) { return true; }
+template <class V>
+__device__ constexpr bool mapped_view(long) { return false; }
+template <class V>
+__device__ __forceinline__ size_t vrow(uint32_t r) {
+  if constexpr (mapped_view<V>(0)) return V::row(r);
+  else return (size_t)r * V::SR;
+}
+template <class V>
+__device__ __forceinline__ size_t vcol(uint32_t c) {
+  if constexpr (mapped_view<V>(0)) return V::col(c);
+  else return (size_t)c * V::SC;
+}
+
 // Sizes are compile-time constants of the generated kernel (batch, M, K, N, and
 // for SPLIT the number of K chunks and their length, a multiple of 16). The
 // workgroup's z index `zid` enumerates batches, or for SPLIT (batch, chunk)
@@ -113,8 +142,14 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
   constexpr bool B_NMAJOR = BMODE == MODE_R;   // Bs[col][k] instead of Bs[k][col]
   constexpr int AS = A_KMAJOR ? BM + 4 : BK + 4;   // padded row stride of the A tile
   constexpr int BS = B_NMAJOR ? BK + 4 : BN + 4;   // padded row stride of the B tile
-  __shared__ __attribute__((aligned(16))) float As_[KW][2][(A_KMAJOR ? BK : BM) * AS];
-  __shared__ __attribute__((aligned(16))) float Bs_[KW][2][(B_NMAJOR ? BN : BK) * BS];
+  // The tiles (and the K groups' hand-over area) live in one LDS pool of this size: two
+  // instantiations of the same size in one kernel (members of one batched launch whose
+  // operand views differ) share it instead of adding up.
+  constexpr int A_TILE = (A_KMAJOR ? BK : BM) * AS, B_TILE = (B_NMAJOR ? BN : BK) * BS;
+  constexpr int TILES = KW * 2 * (A_TILE + B_TILE);
+  float* const pool = lds_pool<TILES + (KW > 1 ? (KW - 1) * THREADS * TM * TN * 4 : 0)>();
+  float (*As_)[2][A_TILE] = reinterpret_cast<float (*)[2][A_TILE]>(pool);
+  float (*Bs_)[2][B_TILE] = reinterpret_cast<float (*)[2][B_TILE]>(pool + KW * 2 * A_TILE);
 
   // zid: the workgroup's z index within this launch (blockIdx.z, or its part
   // below the member index in a batched launch); (tx, ty): its output tile's column
@@ -132,8 +167,8 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
   const uint32_t sub = KW == 1 ? kend0 - kbeg0 : ((kend0 - kbeg0 + KW * BK - 1) / (KW * BK)) * BK;
   const uint32_t kbeg = kbeg0 + kg * sub;
   const uint32_t kend = min(kend0, kbeg + sub);
-  float (*As)[(A_KMAJOR ? BK : BM) * AS] = As_[kg];
-  float (*Bs)[(B_NMAJOR ? BN : BK) * BS] = Bs_[kg];
+  float (*As)[A_TILE] = As_[kg];
+  float (*Bs)[B_TILE] = Bs_[kg];
   const uint32_t m0 = ty * BM, n0 = tx * BN;
   const float* __restrict__ Ab = a_ptr + AV::batch(bz);
   const float* __restrict__ Bb = b_ptr + BV::batch(bz);
@@ -173,7 +208,7 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
         const uint32_t row = t / (BK / 4), kk = (t % (BK / 4)) * 4;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t < BM * BK / 4 && m0 + row < M && k0 + kk < kend)
-          x = *reinterpret_cast<const float4*>(Ab + (size_t)(m0 + row) * AV::SR + k0 + kk);
+          x = *reinterpret_cast<const float4*>(Ab + vrow<AV>(m0 + row) + vcol<AV>(k0 + kk));
         ra[v] = x;
       }
     } else if (AMODE == MODE_R) {
@@ -183,7 +218,7 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
         const uint32_t kk = t / (BM / 4), row = (t % (BM / 4)) * 4;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t < BM * BK / 4 && m0 + row < M && k0 + kk < kend)
-          x = *reinterpret_cast<const float4*>(Ab + (size_t)(k0 + kk) * AV::SC + m0 + row);
+          x = *reinterpret_cast<const float4*>(Ab + vcol<AV>(k0 + kk) + vrow<AV>(m0 + row));
         ra[v] = x;
       }
     } else {
@@ -192,7 +227,7 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
         const int t = tid + v * THREADS;
         const uint32_t row = t / BK, kk = t % BK;
         float x = 0.f;
-        if (t < BM * BK && m0 + row < M && k0 + kk < kend) x = Ab[(size_t)(m0 + row) * AV::SR + (size_t)(k0 + kk) * AV::SC];
+        if (t < BM * BK && m0 + row < M && k0 + kk < kend) x = Ab[vrow<AV>(m0 + row) + vcol<AV>(k0 + kk)];
         sa[v] = x;
       }
     }
@@ -203,7 +238,7 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
         const uint32_t kk = t / (BN / 4), c = (t % (BN / 4)) * 4;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t < BK * BN / 4 && k0 + kk < kend && n0 + c < N)
-          x = *reinterpret_cast<const float4*>(Bb + (size_t)(k0 + kk) * BV::SR + n0 + c);
+          x = *reinterpret_cast<const float4*>(Bb + vrow<BV>(k0 + kk) + vcol<BV>(n0 + c));
         rb[v] = x;
       }
     } else if (BMODE == MODE_R) {
@@ -213,7 +248,7 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
         const uint32_t c = t / (BK / 4), kk = (t % (BK / 4)) * 4;
         float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t < BK * BN / 4 && k0 + kk < kend && n0 + c < N)
-          x = *reinterpret_cast<const float4*>(Bb + (size_t)(n0 + c) * BV::SC + k0 + kk);
+          x = *reinterpret_cast<const float4*>(Bb + vcol<BV>(n0 + c) + vrow<BV>(k0 + kk));
         rb[v] = x;
       }
     } else {
@@ -222,7 +257,7 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
         const int t = tid + v * THREADS;
         const uint32_t kk = t / BN, c = t % BN;
         float x = 0.f;
-        if (t < BK * BN && k0 + kk < kend && n0 + c < N) x = Bb[(size_t)(k0 + kk) * BV::SR + (size_t)(n0 + c) * BV::SC];
+        if (t < BK * BN && k0 + kk < kend && n0 + c < N) x = Bb[vrow<BV>(k0 + kk) + vcol<BV>(n0 + c)];
         sb[v] = x;
       }
     }
@@ -368,7 +403,7 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
   if constexpr (KW > 1) {
     // Groups 1 .. KW-1 hand their sums to group 0 through LDS, which adds them in
     // group order; group 0 alone stores (no barrier follows).
-    __shared__ f4 red[KW - 1][THREADS][TM * TN];
+    f4 (*red)[THREADS][TM * TN] = reinterpret_cast<f4 (*)[THREADS][TM * TN]>(pool + TILES);
     if (kg > 0) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)

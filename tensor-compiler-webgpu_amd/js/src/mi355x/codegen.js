@@ -723,35 +723,70 @@ function gemmTiling(batch, M, N, K, tuning, peers) {
 }
 
 /**
- * The view struct of a matmul operand (tcmi_gemm.h): element (b, r, c) at
- * batch(b) + r·SR + c·SC of its buffer, and the load mode its layout allows.
- * `view` = { batch: [[extent, stride], ...], sr, sc } (null: dense row-major
- * [batch, R, C]); R, C the operand's extents.
+ * Index `x` over mixed-radix factors [[extent, stride], ...] (outer to inner): the
+ * expression Σ_f ((x / inner_f) % extent_f) · stride_f, the outermost factor without the
+ * modulo (the kernels form offsets of in-range indices only); extent-1 and stride-0
+ * factors add nothing.
  */
-function operandView(name, view, batchDims, R, C) {
-  const v = view || { batch: batchDims.map((e, d) => [e, R * C * size(batchDims.slice(d + 1))]), sr: C, sc: 1 };
-  const strides = v.batch.map((x) => x[1]);
-  const others4 = (x) => strides.every((s) => s % 4 === 0) && x % 4 === 0;
-  let mode = 2;
-  if (v.sc === 1 && C % 4 === 0 && others4(v.sr)) mode = 0;
-  else if (v.sr === 1 && R % 4 === 0 && others4(v.sc)) mode = 1;
+function factorTerms(x, fs) {
   const terms = [];
   let inner = 1;
-  for (let d = v.batch.length - 1; d >= 0; d--) {
-    const [e, st] = v.batch[d];
+  for (let d = fs.length - 1; d >= 0; d--) {
+    const [e, st] = fs[d];
     if (e > 1 && st !== 0) {
-      const idx = inner === 1 ? 'b' : `(b / ${inner}u)`;
+      const idx = inner === 1 ? x : `(${x} / ${inner}u)`;
       terms.push(`(size_t)(${d === 0 ? idx : `${idx} % ${e}u`}) * ${st}u`);
     }
     inner *= e;
   }
+  return terms.length ? terms.join(' + ') : '0';
+}
+
+/**
+ * The view struct of a matmul operand (tcmi_gemm.h): element (b, r, c) at
+ * batch(b) + r·SR + c·SC of its buffer, and the load mode its layout allows.
+ * `view` = { batch: [[extent, stride], ...], sr, sc } (null: dense row-major
+ * [batch, R, C]); R, C the operand's extents. A mapped view ({ batch, r, c }: the row
+ * and column indices over mixed-radix factors [[extent, stride], ...], as a chain of
+ * transposes and reshapes lays them out) places the element at batch(b) + row(r) +
+ * col(c) instead, and takes 128-bit loads along c (or r) where c's (r's) innermost
+ * factor is contiguous, holds whole groups of 4, and every other stride is a multiple
+ * of 4 (so each load is aligned and inside one group).
+ */
+function operandView(name, view, batchDims, R, C) {
+  const v = view || { batch: batchDims.map((e, d) => [e, R * C * size(batchDims.slice(d + 1))]), sr: C, sc: 1 };
+  const strides = v.batch.map((x) => x[1]);
+  const batchTerms = factorTerms('b', v.batch);
+  const batchLimit = v.batch.reduce((t, [e, st]) => t + (e - 1) * st, 0);
+  if (v.r || v.c) {
+    const rf = v.r || [[R, v.sr]], cf = v.c || [[C, v.sc]];
+    const all4 = (fs) => fs.every(([e, st]) => e === 1 || st % 4 === 0) && strides.every((st) => st % 4 === 0);
+    const along = (fs, other, ext) => {
+      const [e, st] = fs[fs.length - 1];
+      return st === 1 && e % 4 === 0 && ext % 4 === 0 && all4(fs.slice(0, -1)) && all4(other);
+    };
+    const mode = along(cf, rf, C) ? 0 : along(rf, cf, R) ? 1 : 2;
+    const text = `struct ${name} {
+  static constexpr bool MAPPED = true;
+  static __device__ __forceinline__ size_t batch(uint32_t b) { return ${batchTerms}; }
+  static __device__ __forceinline__ size_t row(uint32_t r) { return ${factorTerms('r', rf)}; }
+  static __device__ __forceinline__ size_t col(uint32_t c) { return ${factorTerms('c', cf)}; }
+};
+`;
+    const span = (fs) => fs.reduce((t, [e, st]) => t + (e - 1) * st, 0);
+    return { text, mode, limit: 1 + batchLimit + span(rf) + span(cf), mapped: true };
+  }
+  const others4 = (x) => strides.every((s) => s % 4 === 0) && x % 4 === 0;
+  let mode = 2;
+  if (v.sc === 1 && C % 4 === 0 && others4(v.sr)) mode = 0;
+  else if (v.sr === 1 && R % 4 === 0 && others4(v.sc)) mode = 1;
   const text = `struct ${name} {
   static constexpr size_t SR = ${v.sr}, SC = ${v.sc};
-  static __device__ __forceinline__ size_t batch(uint32_t b) { return ${terms.length ? terms.join(' + ') : '0'}; }
+  static __device__ __forceinline__ size_t batch(uint32_t b) { return ${batchTerms}; }
 };
 `;
   // One past the largest element offset the kernel can address.
-  const limit = 1 + v.batch.reduce((t, [e, st]) => t + (e - 1) * st, 0) + (R - 1) * v.sr + (C - 1) * v.sc;
+  const limit = 1 + batchLimit + (R - 1) * v.sr + (C - 1) * v.sc;
   return { text, mode, limit };
 }
 
@@ -1006,6 +1041,8 @@ ${indent(inner, '      ')}
   const qv = operandView('__KERNEL___qv', views.q, batchDims, TQ, DH);
   const kv = operandView('__KERNEL___kv', views.k, batchDims, DH, TK);
   const vv = operandView('__KERNEL___vv', views.v, batchDims, TK, DV);
+  // The attention kernel addresses its operands by SR and SC: a mapped view never reaches it.
+  if (qv.mapped || kv.mapped || vv.mapped) throw new Error('attention operand read through a mapped view');
   const need = (slot, dense) => (sizes[slot] !== undefined ? sizes[slot] : dense);
   if (qv.limit > need('q', batch * TQ * DH) || kv.limit > need('k', batch * DH * TK) || vv.limit > need('v', batch * TK * DV)) {
     throw new Error('attention operand view out of bounds');
@@ -1085,27 +1122,81 @@ function batchable(k, count) {
 /** The statement that opens a kernel whose workgroups take XCD-grouped places. */
 const XCD_GROUPED = 'const tcmi::Wg wg = tcmi::xcd_grouped();';
 
-function batchedKernel(k, count) {
+/**
+ * The family of kernel `k` for batching: its text with its operand view structs taken out
+ * and its own name blanked. Launches of one family differ at most in how their matmul
+ * operands are addressed (a mapped view here, a plain one there); their sizes, tiling,
+ * epilogue and code are the same, so they can share one dispatch.
+ */
+function batchFamily(k) {
+  // Matmul tiles take their LDS from a pool shared by instantiations of one size
+  // (tcmi::lds_pool); other kernels' views would each add their own LDS: one text a family.
+  if (!/^tcmi_mm_[0-9a-f]+$/.test(k.name)) return `${k.name}@${k.grid.join(',')}/${k.block.join(',')}/${k.lds}`;
+  const views = new RegExp(`struct ${k.name}_(?:av|bv|qv|kv|vv) \\{[\\s\\S]*?\\n\\};\\n`, 'g');
+  return `${k.source.replace(views, '').split(k.name).join('@')}@${k.grid.join(',')}/${k.block.join(',')}/${k.lds}`;
+}
+
+/**
+ * The batched kernel of `members` (the member launches' kernels at one position, or one
+ * kernel repeated `count` times): one dispatch of `count` member grids along z, member
+ * blockIdx.z / Z taking its argument block and blockIdx.z % Z as its own z index. Members
+ * of one family whose texts differ (their operand views) each run their own body: a
+ * switch on the member index picks it, uniformly per workgroup.
+ */
+function batchedKernel(members, count) {
+  const ks = Array.isArray(members) ? members : new Array(count).fill(members);
+  const k = ks[0];
+  count = ks.length;
   if (!batchable(k, count)) throw new Error(`kernel ${k.name} cannot be batched ${count} times`);
   if (!(Number.isInteger(count) && count >= 2 && count <= MAX_BATCH)) throw new Error(`batch of ${count} launches (2..${MAX_BATCH})`);
+  const family = batchFamily(k);
   const [, base, , suffix] = k.name.match(BATCHABLE);
-  const sig = `${k.name}(const TcmiArgs A) {`;
-  if (k.source.split(sig).length !== 2) throw new Error(`kernel ${k.name}: no single entry point to batch`);
-  if (/gridDim\.z/.test(k.source)) throw new Error(`kernel ${k.name} reads gridDim.z`);
+  const variants = [];
+  const variantOf = ks.map((m) => {
+    if (m.name !== k.name && batchFamily(m) !== family) throw new Error(`kernels ${k.name} and ${m.name} are not of one family`);
+    let v = variants.findIndex((x) => x.name === m.name);
+    if (v < 0) { v = variants.length; variants.push(m); }
+    return v;
+  });
   const Z = k.grid[2];
-  const [head, body] = k.source.split(sig);
+  const parts = variants.map((m) => {
+    const sig = `${m.name}(const TcmiArgs A) {`;
+    if (m.source.split(sig).length !== 2) throw new Error(`kernel ${m.name}: no single entry point to batch`);
+    if (/gridDim\.z/.test(m.source)) throw new Error(`kernel ${m.name} reads gridDim.z`);
+    const [head, body] = m.source.split(sig);
+    return { m, head, body };
+  });
   // A member taking an XCD-grouped place: the place is taken over the whole batched
   // grid, and its z index chooses the member as blockIdx.z does otherwise.
-  const grouped = body.includes(`  ${XCD_GROUPED}\n`);
-  const tail = grouped ? body.replace(`  ${XCD_GROUPED}\n`, '') : body;
+  const grouped = parts[0].body.includes(`  ${XCD_GROUPED}\n`);
   const z = grouped ? 'wg.z' : 'blockIdx.z';
   const ownZ = (t) => t.split(z).join(`(${z} % ${Z}u)`);
+  const strip = (body) => (grouped ? body.replace(`  ${XCD_GROUPED}\n`, '') : body);
   const entry = `__KERNEL__${suffix || ''}(const TcmiBatch<${count}> B) {\n${grouped ? `  ${XCD_GROUPED}\n` : ''}  const TcmiPtrs& A = B.m[${z} / ${Z}u];`;
-  const text = (ownZ(head) + entry + ownZ(tail)).split(base).join('__KERNEL__');
+  let text;
+  if (variants.length === 1) {
+    text = (ownZ(parts[0].head) + entry + ownZ(strip(parts[0].body))).split(base).join('__KERNEL__');
+  } else {
+    // Every variant's structs (named for its own kernel), then one entry point whose
+    // switch runs the member's own body.
+    const decl = parts[0].head.slice(parts[0].head.lastIndexOf('extern "C"'));
+    const lines = (p) => p.head.slice(0, p.head.lastIndexOf('extern "C"')).split('\n');
+    const includes = lines(parts[0]).filter((l) => l.startsWith('#include')).join('\n');
+    // Each variant's structs renamed for the batched kernel (v0_, v1_, ...): the members'
+    // own kernels may share its module.
+    const own = (t, v) => t.split(`${parts[v].m.name}_`).join(`__KERNEL___v${v}_`);
+    const structs = parts.map((p, v) => own(lines(p).filter((l) => !l.startsWith('#include')).join('\n'), v));
+    const cases = parts.map((p, v) => {
+      const labels = variantOf.map((x, i) => (x === v ? `    case ${i}u:` : null)).filter(Boolean).join('\n');
+      const stmts = own(ownZ(strip(p.body)), v).replace(/\}\s*$/, '').split('\n').map((l) => (l ? `  ${l}` : l)).join('\n');
+      return `${labels} {\n${stmts.replace(/\s+$/, '')}\n      break;\n    }`;
+    });
+    text = `${includes}\n${structs.join('')}${decl}${entry}\n  switch (${z} / ${Z}u) {\n${cases.join('\n')}\n  }\n}\n`;
+  }
   const b = kernelText(`b${k.name.split('_')[1]}`, text);
   return { name: b.name + (suffix || ''), source: b.source, grid: [k.grid[0], k.grid[1], Z * count], block: k.block.slice(), lds: k.lds,
-    members: count };
+    members: count, variants: variants.length > 1 ? variantOf.map((v) => variants[v].name) : undefined };
 }
 
 module.exports = { elementwiseKernel, rowwiseKernel, colreduceKernels, gemmKernel, gemmTiling, attentionKernel, classifyGather, gatherStrides,
-  literal, fnv, Emitter, WG, MAX_P, MAX_IN, MAX_BATCH, batchable, batchedKernel };
+  literal, fnv, Emitter, WG, MAX_P, MAX_IN, MAX_BATCH, batchable, batchedKernel, batchFamily };

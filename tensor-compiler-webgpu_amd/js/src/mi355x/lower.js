@@ -231,13 +231,7 @@ function perfPlan(graph, keep, rowFolding, absorbing) {
   // Which (consumer, operand position) pairs are matmul-only operand slots.
   const slotOf = new Map();
   for (const n of graph.nodes) for (const [slot, pos] of matmulSlots(n)) slotOf.set(`${n.id}:${pos}`, slot);
-  const folded = new Set();
-  for (let id = graph.nodes.length - 1; id >= 0; id--) {
-    const n = graph.nodes[id];
-    if (n.op !== 'transpose' || keep.has(id) || cons[id].length === 0) continue;
-    const ok = cons[id].every((c) => folded.has(c) || graph.nodes[c].inputs.every((i, pos) => i !== id || slotOf.has(`${c}:${pos}`)));
-    if (ok) folded.add(id);
-  }
+  const { folded, views } = inPlaceTransposes(graph, keep, cons, slotOf, dead);
   // Broadcasts read in place by every consumer's body (never through a matmul
   // operand slot, a plain reduction or another gather).
   const bodyReader = (c, pos) => {
@@ -393,27 +387,126 @@ function perfPlan(graph, keep, rowFolding, absorbing) {
     operands.set(e.id, next);
     for (const a of list) folded.add(a.prod);
   }
-  const views = new Map();
-  for (const n of graph.nodes) {
-    for (const [slot, pos] of matmulSlots(n)) {
-      let cur = n.inputs[pos];
-      if (!folded.has(cur)) continue;
-      const shape = graph.nodes[cur].shape;
-      let perm = shape.map((_, d) => d);
-      while (folded.has(cur)) {
-        const t = graph.nodes[cur];
-        perm = perm.map((d) => t.attrs.perm[d]);
-        cur = t.inputs[0];
-      }
-      const st = stridesOf(graph.nodes[cur].shape);
-      const s = perm.map((d) => st[d]);
-      const r = shape.length;
-      const view = { batch: shape.slice(0, r - 2).map((e, d) => [e, s[d]]), sr: s[r - 2], sc: s[r - 1] };
-      if (!views.has(n.id)) views.set(n.id, {});
-      views.get(n.id)[slot] = { pos, source: cur, view, size: size(graph.nodes[cur].shape) };
-    }
-  }
   return { aliases, folded, views, broadcasts, dead, rowFolds, absorbed };
+}
+
+/**
+ * The index map of a value read from a source buffer through a chain of transposes and
+ * reshapes (`chain`: node ids from the source's reader to the value): per dimension of the
+ * value, its factors [[extent, stride], ...] outer to inner, so that index x of the
+ * dimension addresses Σ_f ((x / inner_f) % extent_f) · stride_f (inner_f: the product of
+ * the extents inside f). A transpose permutes the dimensions; a reshape regroups the
+ * factors of the row-major order, splitting one where a new dimension ends inside it.
+ * null where a reshape cuts a factor at a point that divides neither way (no such map).
+ */
+function chainMap(graph, source, chain) {
+  const shape = graph.nodes[source].shape;
+  const st = stridesOf(shape);
+  let dims = shape.map((e, d) => [[e, st[d]]]);
+  for (const id of chain) {
+    const n = graph.nodes[id];
+    if (n.op === 'transpose') {
+      dims = n.attrs.perm.map((p) => dims[p]);
+      continue;
+    }
+    const flat = [].concat(...dims).filter(([e]) => e > 1);
+    const out = new Array(n.shape.length);
+    for (let d = n.shape.length - 1; d >= 0; d--) {
+      let E = n.shape[d];
+      const fs = [];
+      while (E > 1) {
+        if (!flat.length) return null;
+        const [e, s] = flat.pop();
+        if (E % e === 0) { fs.unshift([e, s]); E /= e; } else if (e % E === 0) { fs.unshift([E, s]); flat.push([e / E, s * E]); E = 1; } else return null;
+      }
+      out[d] = fs;
+    }
+    if (flat.length) return null;
+    dims = out;
+  }
+  // Adjacent factors that step as one (outer stride = inner extent · inner stride) merge.
+  return dims.map((fs) => {
+    const m = [];
+    for (const [e, s] of fs) {
+      const last = m[m.length - 1];
+      if (last && last[1] === e * s) m[m.length - 1] = [last[0] * e, s];
+      else m.push([e, s]);
+    }
+    return m.length ? m : [[1, 0]];
+  });
+}
+
+/**
+ * Transposes read in place by matmuls, and the operand views through which they are read.
+ * A transpose launches nothing when every consumer reads it as a matmul operand (or is such
+ * a transpose itself): the matmul reads the transpose's source through a strided view. A
+ * reshape between them (the heads of an attention merged back into rows, transpose(o)
+ * reshaped to [B·T, d], and the gradients of q, k and v on their way back) is passed
+ * through as well where the readers are plain or epilogue products (operand slots a and
+ * b); their view then maps a row or column index over several strides (chainMap). A chain
+ * whose reshape no such map expresses keeps its transposes launched. Dead readers (nodes no
+ * kept value depends on) launch nothing and do not count.
+ * Returns { folded: Set of transposes, views: consumer id -> { slot: { pos, source, view, size } } }.
+ */
+function inPlaceTransposes(graph, keep, cons, slotOf, dead) {
+  const refused = new Set();
+  const bySlot = (c, id, ab) => graph.nodes[c].inputs.every((i, pos) => {
+    if (i !== id) return true;
+    const s = slotOf.get(`${c}:${pos}`);
+    return s !== undefined && (!ab || s === 'a' || s === 'b');
+  });
+  // Whether transpose or reshape `id` is read only through matmul operand slots, directly or
+  // through further transposes and reshapes (`via`: a reshape lies on the way).
+  const inPlace = (id, via) => {
+    const users = cons[id].filter((c) => !dead.has(c));
+    if (keep.has(id) || users.length === 0) return false;
+    return users.every((c) => {
+      const n = graph.nodes[c];
+      if (n.op === 'transpose') return !refused.has(c) && inPlace(c, via);
+      if (n.op === 'reshape') return inPlace(c, true);
+      return bySlot(c, id, via);
+    });
+  };
+  for (;;) {
+    const folded = new Set();
+    for (const n of graph.nodes) if (n.op === 'transpose' && !refused.has(n.id) && inPlace(n.id, false)) folded.add(n.id);
+    const views = new Map();
+    let bad = null;
+    for (const n of graph.nodes) {
+      for (const [slot, pos] of matmulSlots(n)) {
+        let cur = n.inputs[pos];
+        const chain = [];
+        while (folded.has(cur) || (graph.nodes[cur].op === 'reshape' && !keep.has(cur))) {
+          chain.push(cur);
+          cur = graph.nodes[cur].inputs[0];
+        }
+        // Reshapes at the source's end read the source's layout as it is: the view starts there.
+        while (chain.length && !folded.has(chain[chain.length - 1])) cur = chain.pop();
+        if (!chain.length) continue;
+        const shape = graph.nodes[n.inputs[pos]].shape;
+        const r = shape.length;
+        let view;
+        if (chain.every((id) => graph.nodes[id].op === 'transpose')) {
+          let perm = shape.map((_, d) => d);
+          for (const id of chain) perm = perm.map((d) => graph.nodes[id].attrs.perm[d]);
+          const st = stridesOf(graph.nodes[cur].shape);
+          const s = perm.map((d) => st[d]);
+          view = { batch: shape.slice(0, r - 2).map((e, d) => [e, s[d]]), sr: s[r - 2], sc: s[r - 1] };
+        } else {
+          const dims = chainMap(graph, cur, chain.slice().reverse());
+          if (!dims) { bad = chain.filter((id) => folded.has(id)); break; }
+          const batch = [].concat(...dims.slice(0, r - 2)).filter(([e]) => e > 1);
+          const [rf, cf] = [dims[r - 2], dims[r - 1]];
+          view = rf.length === 1 && cf.length === 1 ? { batch, sr: rf[0][1], sc: cf[0][1] } : { batch, sr: null, sc: null, r: rf, c: cf };
+        }
+        if (!views.has(n.id)) views.set(n.id, {});
+        views.get(n.id)[slot] = { pos, source: cur, view, size: size(graph.nodes[cur].shape) };
+      }
+      if (bad) break;
+    }
+    if (!bad) return { folded, views };
+    for (const id of bad) refused.add(id);
+  }
 }
 
 /**
@@ -688,8 +781,9 @@ function batchPlan(launches, aliases) {
   launches.forEach((l, i) => writer.set(owner(l.node), i));
   // A launch's kernels as run: a kernel's text does not always fix its grid (a
   // column sum's outer extent is its grid's z extent only).
-  const one = (l) => (l.kernels.every((k) => cg.batchable(k))
-    ? l.kernels.map((k) => `${k.name}@${k.grid.join(',')}/${k.block.join(',')}/${k.lds}`).join(' ') : null);
+  // Launches of one kernel family at each position (the same text up to its operand views)
+  // may share a dispatch.
+  const one = (l) => (l.kernels.every((k) => cg.batchable(k)) ? l.kernels.map((k) => cg.batchFamily(k)).join(' ') : null);
   const fits = (l, count) => l.kernels.every((k) => cg.batchable(k, count));
   // Pass 1: units (arrays of launches; two or more: a batch), in order.
   const placed = new Uint8Array(n);
@@ -769,7 +863,7 @@ function batchPlan(launches, aliases) {
   for (const u of units) {
     if (u.length > 1) {
       const l = u[0];
-      batches.push({ start: order.length, count: u.length, kernels: l.kernels.map((k) => cg.batchedKernel(k, u.length)),
+      batches.push({ start: order.length, count: u.length, kernels: l.kernels.map((k, j) => cg.batchedKernel(u.map((m) => m.kernels[j]), u.length)),
         wsStride: l.workspace ? Math.ceil(l.workspace / 256) * 256 : 0 });
     }
     order.push(...u);

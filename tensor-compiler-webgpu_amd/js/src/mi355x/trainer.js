@@ -23,15 +23,54 @@ const { fuse } = require('../fusion/fuse');
 const { lowerMI355X } = require('./lower');
 
 /**
+ * Products transposed by their one reader, formed transposed instead (in place, on the
+ * fused graph, ids unchanged): transpose(matmul(A, B)) over the last two axes, where A is
+ * itself transpose(A0) over them and only that transpose reads the product, becomes
+ * matmul(transpose(B), A0) — the product's node now holds transpose(B) and the
+ * transpose's node the product. Every output element sums the same terms in the same
+ * order of k (only which operand is which changes), and the result comes out in the
+ * layout its readers take. Autodiff's gradient of the transposed keys of an attention,
+ * transpose(matmul(transpose(q), dS)), is one: the key gradient then has the query
+ * gradient's layout, so the same kernels (and batches) read both. `origin` (the fusion's
+ * map of each node to the original node holding its value) marks the new transpose -1:
+ * no original node holds transpose(B). Returns the count.
+ */
+function formTransposedProducts(graph, keep, origin) {
+  const readers = graph.nodes.map(() => 0);
+  for (const n of graph.nodes) for (const i of n.inputs) readers[i]++;
+  const swapsLast = (n) => n.op === 'transpose' && n.attrs.perm.every((p, d) => {
+    const r = n.attrs.perm.length;
+    return d < r - 2 ? p === d : p === (d === r - 2 ? r - 1 : r - 2);
+  });
+  let count = 0;
+  for (const t of graph.nodes) {
+    if (!swapsLast(t) || t.shape.length < 2) continue;
+    const x = graph.nodes[t.inputs[0]];
+    if (x.op !== 'matmul' || keep.has(x.id) || readers[x.id] !== 1) continue;
+    const a = graph.nodes[x.inputs[0]], b = graph.nodes[x.inputs[1]];
+    if (!swapsLast(a) || a.shape.length !== b.shape.length || a.shape.slice(0, -2).join() !== b.shape.slice(0, -2).join()) continue;
+    const bt = b.shape.slice(0, -2).concat([b.shape[b.shape.length - 1], b.shape[b.shape.length - 2]]);
+    graph.nodes[x.id] = { id: x.id, op: 'transpose', inputs: [b.id], attrs: { perm: t.attrs.perm.slice() }, shape: bt };
+    graph.nodes[t.id] = { id: t.id, op: 'matmul', inputs: [x.id, a.inputs[0]], attrs: {}, shape: t.shape.slice() };
+    readers[b.id]++;
+    if (origin) origin[x.id] = -1;
+    count++;
+  }
+  return count;
+}
+
+/**
  * Fuse and lower a step from the builders ({ graph, loss, logits, inputs, outputs, cotangent, ... }).
  * `lowered` is the perf lowering the trainer runs (reshapes share buffers,
  * transposes read in place by their matmuls; `perf: false` turns it off);
- * `checked` is the plain lowering, one launch per node, for node-by-node checks.
+ * `checked` is the plain lowering, one launch per node, for node-by-node checks. Both
+ * lower the fused graph with its transposed products formed transposed (above).
  */
 function fusedStep(step, options) {
   const o = options || {};
   const keep = [step.loss, step.logits].concat(Object.values(step.outputs));
   const f = fuse(step.graph, { keep, sabotage: o.passSabotage });
+  formTransposedProducts(f.graph, new Set(keep.map((id) => f.index.get(id))), f.origin);
   const at = (id) => f.index.get(id);
   const remap = (m) => { const r = {}; for (const k of Object.keys(m)) r[k] = at(m[k]); return r; };
   const checked = lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning });
@@ -139,4 +178,4 @@ class HipTrainer {
   }
 }
 
-module.exports = { fusedStep, HipTrainer };
+module.exports = { fusedStep, HipTrainer, formTransposedProducts };

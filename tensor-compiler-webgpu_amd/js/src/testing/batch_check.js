@@ -3,11 +3,35 @@
 // batchPlan): the batched launch list must hold the same launches as the plain
 // order, every launch must read only buffers already written (or written by no
 // launch), the members of a batch must be launches of the same kernel texts
-// over the same grids (a column sum's text leaves its outer extent to the
-// grid) with no data path between them, each batched kernel's grid must repeat the
+// (or of texts that differ in their operand views alone, each member then run
+// by its own case of the batched kernel) over the same grids (a column sum's
+// text leaves its outer extent to the grid) with no data path between them, each batched kernel's grid must repeat the
 // member kernel's grid once per member along z, and the members' workspace
 // slices must be disjoint and inside the workspace. Checked from the launch
 // records alone, not from the planner's own bookkeeping.
+
+// A kernel's text with its matmul operand view structs (named for the kernel) taken out
+// and its name blanked: members of a batch may differ in how they address their operands
+// only.
+function family(k) {
+  const views = new RegExp(`struct ${k.name}_(?:av|bv|qv|kv|vv) \\{[\\s\\S]*?\\n\\};\\n`, 'g');
+  return k.source.replace(views, '').split(k.name).join('@');
+}
+
+// Whether batched kernel `bk` runs, for member k, the body of kernel `x`: the switch case
+// of k reaches, before its break, a call over a set of structs that the batched text
+// declares exactly as x declares its own (under the batched kernel's name).
+function runsOwnBody(bk, k, x) {
+  const at = bk.source.indexOf(`case ${k}u:`);
+  if (at < 0) return false;
+  const end = bk.source.indexOf('break;', at);
+  const m = end > at ? bk.source.slice(at, end).match(new RegExp(`(${bk.name}_v\\d+)_av`)) : null;
+  if (!m) return false;
+  const structs = (src, prefix) => (src.match(new RegExp(`struct ${prefix}_(?:av|bv|epi) \\{[\\s\\S]*?\\n\\};\\n`, 'g')) || [])
+    .map((t) => t.split(prefix).join('@')).join('');
+  const mine = structs(x.source, x.name);
+  return mine.length > 0 && structs(bk.source, m[1]) === mine;
+}
 
 function checkBatches(plain, batched) {
   const alias = new Map(batched.aliases || []);
@@ -35,7 +59,10 @@ function checkBatches(plain, batched) {
       const l = L[b.start + k];
       const same = l.kernels.length === first.kernels.length && l.kernels.every((x, j) => {
         const y = first.kernels[j];
-        return x.name === y.name && x.grid.join() === y.grid.join() && x.block.join() === y.block.join() && x.lds === y.lds;
+        if (x.grid.join() !== y.grid.join() || x.block.join() !== y.block.join() || x.lds !== y.lds) return false;
+        if (x.name === y.name) return true;
+        // Another text of the same family: the batched kernel must run this member's own body.
+        return family(x) === family(y) && runsOwnBody(b.kernels[j], k, x);
       });
       if (!same || l.workspace !== first.workspace) return { ok: false, why: `batch at ${b.start}: member ${k} is not a launch of the same kernels` };
       unitOf[b.start + k] = b.start;

@@ -9,7 +9,22 @@ from typing import List, Sequence
 
 import numpy as np
 
-from oracle import bounds
+from oracle import bounds, interp
+
+
+def fused_values(fused, origin, values):
+    """The value of every node of a fused step graph: its original node's value, or, for a
+    node no original node holds (origin -1: the transposed operand the trainer's lowering
+    forms for a product it forms transposed), its own op on the values before it."""
+    out = []
+    for i, o in enumerate(origin):
+        if o >= 0:
+            out.append(values[o])
+            continue
+        node = fused["nodes"][i]
+        assert node["op"] == "transpose", node["op"]
+        out.append(interp.kernel(node, [out[j] for j in node["inputs"]], fused))
+    return out
 
 
 def batch_axis(full_shape: Sequence[int], twin_shape: Sequence[int]) -> int:

@@ -86,3 +86,83 @@ def test_matmul_operand_views(tmp_path, tool):
         want_b = (1 if K % 4 == 0 else 2) if tb else (0 if N % 4 == 0 else 2)
         assert modes == [want_a, want_b], (c["name"], modes, [want_a, want_b])
         print(f"{c['name']}: modes {modes} worst {j['worst']:.3g}", file=sys.stderr)
+
+
+def _mapped_case(name, src_shape, chain, role, other, act):
+    """matmul over an operand formed from input `S` by `chain` ([("transpose", perm) or
+    ("reshape", shape)], in order) in operand slot `role` ("a": X·W, "b": Y·X), the other
+    operand an input of shape `other`, plus bias and `act`."""
+    nodes = []
+
+    def add(op, inputs, attrs, shape):
+        nodes.append({"op": op, "inputs": inputs, "attrs": attrs, "shape": shape})
+        return len(nodes) - 1
+
+    x = add("input", [], {"name": "S", "shape": src_shape}, src_shape)
+    shape = list(src_shape)
+    for op, arg in chain:
+        if op == "transpose":
+            shape = [shape[p] for p in arg]
+            x = add("transpose", [x], {"perm": arg}, shape)
+        else:
+            shape = list(arg)
+            x = add("reshape", [x], {"shape": shape}, shape)
+    o = add("input", [], {"name": "O", "shape": other}, other)
+    a, b = (x, o) if role == "a" else (o, x)
+    M, N = nodes[a]["shape"][-2], nodes[b]["shape"][-1]
+    mm = add("matmul", [a, b], {}, [M, N])
+    bias = add("input", [], {"name": "bias", "shape": [N]}, [N])
+    bb = add("broadcast", [bias], {"shape": [M, N]}, [M, N])
+    y = add(act, [add("add", [mm, bb], {}, [M, N])], {}, [M, N])
+    shapes = {"S": src_shape, "O": other, "bias": [N]}
+    return {"name": name, "graph": {"nodes": nodes}, "keep": [y], "perf": True}, shapes, y
+
+
+# (name, source shape, chain, slot, other operand's shape, transposes read in place, modes):
+# the heads of an attention merged back into rows ([B, H, T, dh] -> [B, T, H, dh] ->
+# [B·T, H·dh]) read as A, as B and transposed (the weight gradient's form), the key
+# gradient's double transpose, a head size that is not a multiple of 4 (per-element
+# loads), and a reshape that cuts the transposed layout where no mixed-radix map exists
+# (its transpose stays a launch).
+MAPPED = [
+    ("heads-a", [2, 3, 20, 8], [("transpose", [0, 2, 1, 3]), ("reshape", [40, 24])], "a", [24, 36], 1, [0, 0]),
+    ("heads-b", [2, 3, 20, 8], [("transpose", [0, 2, 1, 3]), ("reshape", [40, 24])], "b", [36, 40], 1, [0, 0]),
+    ("heads-ta", [2, 3, 20, 8], [("transpose", [0, 2, 1, 3]), ("reshape", [40, 24]), ("transpose", [1, 0])], "a",
+     [40, 16], 2, [1, 0]),
+    ("key-double", [2, 3, 8, 20], [("transpose", [0, 1, 3, 2]), ("transpose", [0, 2, 1, 3]), ("reshape", [40, 24])],
+     "a", [24, 12], 2, [1, 0]),
+    ("odd-heads", [2, 3, 20, 5], [("transpose", [0, 2, 1, 3]), ("reshape", [40, 15])], "a", [15, 9], 1, [2, 2]),
+    ("unmappable", [6, 4], [("transpose", [1, 0]), ("reshape", [3, 8])], "a", [8, 5], 0, [0, 2]),
+]
+
+
+def test_matmul_mapped_views(tmp_path, tool):
+    """Operands read through a chain of transposes and reshapes (a mapped view: the row or
+    column index steps over several strides): plain and perf lowerings within the budget,
+    equal bit for bit, the transposes read in place where a map exists, and the load modes
+    the map allows."""
+    import tcmi_bridge
+    rng = np.random.default_rng(11)
+    reqs, meta = [], []
+    for name, src, chain, role, other, folded, modes in MAPPED:
+        req, shapes, y = _mapped_case(name, src, chain, role, other, "relu" if role == "a" else "tanh")
+        req["inputs"] = {k: (rng.standard_normal(int(np.prod(s))) / 4).astype(np.float32).tolist() for k, s in shapes.items()}
+        reqs.append(req)
+        meta.append((y, folded, modes))
+    print(f"gpu step: gpu-graphs, {len(reqs)} mapped view cases", flush=True)
+    tool("gpu-graphs", {"graphs": reqs}, out=str(tmp_path), timeout=300)
+    b = tcmi_bridge.Bundle(tmp_path)
+    for c, req, (y, folded, modes) in zip(b.cases, reqs, meta):
+        ref = bounds.reference_with_bounds(req["graph"], {k: np.asarray(v) for k, v in req["inputs"].items()})
+        gpu = [b.arr(c["gpuFused"][str(i)]) for i in range(len(c["fused"]["nodes"]))]
+        j = bounds.judge_fused(c["fused"], c["origin"], gpu, ref)
+        assert j["pass"], (c["name"], j["first"])
+        assert all(c["canaryFused"]) and c["canaryPerf"], c["name"]
+        (yf,) = [int(k) for k in c["gpuPerf"]]
+        perf = b.arr(c["gpuPerf"][str(yf)])
+        jp = bounds.judge_outputs([ref["values"][y]], [ref["bounds"][y]], [perf])
+        assert jp["pass"], (c["name"], "perf", jp["first"])
+        assert np.array_equal(perf.view(np.uint32), b.arr(c["gpuFused"][str(yf)]).view(np.uint32)), c["name"]
+        assert len(c["perfFolded"]) == folded, (c["name"], c["perfFolded"])
+        assert c["perfModes"] == [modes], (c["name"], c["perfModes"])
+        print(f"{c['name']}: modes {c['perfModes']} worst {j['worst']:.3g}", file=sys.stderr)

@@ -13,7 +13,7 @@ import pytest
 
 from conftest import GOLDEN
 from oracle import bounds
-from step_slices import absorbed_producers, local, restate
+from step_slices import absorbed_producers, fused_values, local, restate
 
 pytestmark = pytest.mark.gpu
 
@@ -26,7 +26,7 @@ def node_local(tool, tmp_path, req):
     c = b.cases[0]
     inputs = {k: b.arr(v) for k, v in c["inputs"].items()}
     ref = bounds.reference_with_bounds(c["graph"], inputs)
-    fused_vals = [ref["values"][o] for o in c["origin"]]
+    fused_vals = fused_values(c["fused"], c["origin"], ref["values"])
     np.concatenate([v.astype(np.float32) for v in fused_vals]).tofile(tmp_path / "values.f32")
     out = tmp_path / "local"
     print(f"gpu step: gpu-local {req}", flush=True)

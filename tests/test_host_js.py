@@ -174,6 +174,18 @@ def test_generated_kernels_read_no_parameter_block(golden_cases, tool):
                 assert not re.search(r"\.P\[", k["source"]), k["name"]
 
 
+def _mixed_radix(n, factors):
+    """Offsets of indices 0..n-1 over factors [[extent, stride], ...] (outer to inner)."""
+    x = np.arange(n, dtype=np.int64)
+    off = np.zeros(n, dtype=np.int64)
+    inner = 1
+    for e, st in reversed(factors):
+        off += ((x // inner) % e) * st
+        inner *= e
+    assert inner == n or n == 1, (n, factors)
+    return off
+
+
 def _chain_value(graph, operand, source, src_value):
     """The operand's value from its source through the transpose/reshape chain between them (oracle kernels)."""
     from oracle import interp
@@ -263,7 +275,7 @@ def test_perf_lowering_views_address_the_operands(tool, req):
     skipped = {a for a, _ in d["aliases"]} | set(d["folded"]) | set(d["dead"])
     assert launched.isdisjoint(skipped)
     assert launched | skipped == {n_id for n_id, n in enumerate(nodes) if n["op"] not in ("input", "const")}
-    checked = 0
+    checked = mapped = 0
     for l in d["launches"]:
         for i in l["inputs"]:
             assert i not in skipped, (l["node"], i)
@@ -273,22 +285,31 @@ def test_perf_lowering_views_address_the_operands(tool, req):
             src = np.arange(int(np.prod(src_shape)), dtype=np.float64)
             want = _chain_value(g, v["operand"], v["source"], src).reshape(shape)
             view = v["view"]
-            idx = np.zeros(shape, dtype=np.int64)
-            strides = [s for _, s in view["batch"]] + [view["sr"], view["sc"]]
-            for axis, st in enumerate(strides):
-                sh = [1] * len(shape)
-                sh[axis] = shape[axis]
-                idx = idx + np.arange(shape[axis]).reshape(sh) * st
+            R, C = shape[-2], shape[-1]
+            nb = int(np.prod(shape[:-2]))
+            # Every index decoded over the view's mixed-radix factors: the flattened batch
+            # index over view["batch"], the row and column over their own factors (or the
+            # single strides sr and sc), outer to inner.
+            rf = view.get("r") or [[R, view["sr"]]]
+            cf = view.get("c") or [[C, view["sc"]]]
+            idx = (_mixed_radix(nb, view["batch"])[:, None, None] + _mixed_radix(R, rf)[None, :, None]
+                   + _mixed_radix(C, cf)[None, None, :]).reshape(shape)
             assert np.array_equal(src[idx], want), (l["node"], slot)
             mode = l["modes"][0 if slot == "a" else 1]
-            R, C = shape[-2], shape[-1]
-            if view["sc"] == 1 and C % 4 == 0:
+            strides4 = all(st % 4 == 0 for e, st in view["batch"] + rf[:-1] + cf[:-1] if e > 1)
+            if cf[-1][1] == 1 and cf[-1][0] % 4 == 0 and C % 4 == 0 and strides4 and all(st % 4 == 0 for e, st in rf if e > 1):
                 assert mode == 0
-            elif view["sr"] == 1 and R % 4 == 0 and view["sc"] % 4 == 0:
+            elif rf[-1][1] == 1 and rf[-1][0] % 4 == 0 and R % 4 == 0 and strides4 and all(st % 4 == 0 for e, st in cf if e > 1):
                 assert mode == 1
+            if "r" in view:
+                mapped += 1
             checked += 1
     if req["model"] != "mlp":
         assert checked > 10
+    if req["model"] == "transformer":
+        # The heads merged back into rows (and the head gradients on their way back) are read
+        # through mapped views, not materialised.
+        assert mapped >= 8
     # Every matmul splits K exactly as in the plain lowering (the same order of the K sum).
     splits = [l["split"] for l in d["launches"] if l["split"] is not None]
     assert splits, "no matmul's K split was read from its kernel"

@@ -9,8 +9,8 @@ sequence would break the equality."""
 import numpy as np
 
 from oracle import bounds, interp
-from step_slices import (absorb_producers, absorbed_producers, batch_axis, expectations, fold_reductions, local,
-                         take_block)
+from step_slices import (absorb_producers, absorbed_producers, batch_axis, expectations, fold_reductions, fused_values,
+                         local, take_block)
 
 
 def test_sequence_blocks_equal_the_whole_launch(tmp_path, tool):
@@ -25,7 +25,7 @@ def test_sequence_blocks_equal_the_whole_launch(tmp_path, tool):
     with interp.blas_matmul():
         ref = bounds.reference_with_bounds(c["graph"], inputs)
     # The operands: float32 values of every fused node, as a GPU run would give them.
-    vals = [ref["values"][o].astype(np.float32) for o in c["origin"]]
+    vals = [v.astype(np.float32) for v in fused_values(full, c["origin"], ref["values"])]
     del ref
     nodes, tnodes = full["nodes"], twin["nodes"]
     axis = [batch_axis(n["shape"], t["shape"]) for n, t in zip(nodes, tnodes)]
