@@ -93,6 +93,26 @@ __device__ __forceinline__ size_t vcol(uint32_t c) {
   else return (size_t)c * V::SC;
 }
 
+// The op a view applies to each element it loads: V::OP 1 is relu (tcmi::op_relu, the
+// op a relu kernel runs, so the same bits as reading that kernel's output); a view
+// without OP loads elements as they are. Applied as a staged slice is stored to LDS,
+// not as it is loaded: the slice's global loads stay in flight while the previous
+// slice is computed (an op right after the load would wait for it).
+template <class V>
+__device__ constexpr auto view_op(int) -> decltype(V::OP, int()) { return V::OP; }
+template <class V>
+__device__ constexpr int view_op(long) { return 0; }
+template <class V>
+__device__ __forceinline__ float vop(float x) {
+  if constexpr (view_op<V>(0) == 1) return op_relu(x);
+  else return x;
+}
+template <class V>
+__device__ __forceinline__ float4 vop(float4 x) {
+  if constexpr (view_op<V>(0) == 1) return make_float4(op_relu(x.x), op_relu(x.y), op_relu(x.z), op_relu(x.w));
+  else return x;
+}
+
 // Sizes are compile-time constants of the generated kernel (batch, M, K, N, and
 // for SPLIT the number of K chunks and their length, a multiple of 16). The
 // workgroup's z index `zid` enumerates batches, or for SPLIT (batch, chunk)
@@ -274,7 +294,7 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
         const int t = tid + v * THREADS;
         if (t < BM * BK / 4) {
           const int row = t / (BK / 4), kk = (t % (BK / 4)) * 4;
-          *reinterpret_cast<float4*>(&As[buf][row * AS + kk]) = ra[v];
+          *reinterpret_cast<float4*>(&As[buf][row * AS + kk]) = vop<AV>(ra[v]);
         }
       }
     } else if (AMODE == MODE_R) {
@@ -283,14 +303,14 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
         const int t = tid + v * THREADS;
         if (t < BM * BK / 4) {
           const int kk = t / (BM / 4), row = (t % (BM / 4)) * 4;
-          *reinterpret_cast<float4*>(&As[buf][kk * AS + row]) = ra[v];
+          *reinterpret_cast<float4*>(&As[buf][kk * AS + row]) = vop<AV>(ra[v]);
         }
       }
     } else {
 #pragma unroll
       for (int v = 0; v < A_SC; ++v) {
         const int t = tid + v * THREADS;
-        if (t < BM * BK) As[buf][(t / BK) * AS + (t % BK)] = sa[v];
+        if (t < BM * BK) As[buf][(t / BK) * AS + (t % BK)] = vop<AV>(sa[v]);
       }
     }
     if (BMODE == MODE_C) {
@@ -299,7 +319,7 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
         const int t = tid + v * THREADS;
         if (t < BK * BN / 4) {
           const int kk = t / (BN / 4), c = (t % (BN / 4)) * 4;
-          *reinterpret_cast<float4*>(&Bs[buf][kk * BS + c]) = rb[v];
+          *reinterpret_cast<float4*>(&Bs[buf][kk * BS + c]) = vop<BV>(rb[v]);
         }
       }
     } else if (BMODE == MODE_R) {
@@ -308,14 +328,14 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
         const int t = tid + v * THREADS;
         if (t < BK * BN / 4) {
           const int c = t / (BK / 4), kk = (t % (BK / 4)) * 4;
-          *reinterpret_cast<float4*>(&Bs[buf][c * BS + kk]) = rb[v];
+          *reinterpret_cast<float4*>(&Bs[buf][c * BS + kk]) = vop<BV>(rb[v]);
         }
       }
     } else {
 #pragma unroll
       for (int v = 0; v < B_SC; ++v) {
         const int t = tid + v * THREADS;
-        if (t < BK * BN) Bs[buf][(t / BN) * BS + (t % BN)] = sb[v];
+        if (t < BK * BN) Bs[buf][(t / BN) * BS + (t % BN)] = vop<BV>(sb[v]);
       }
     }
   };

@@ -742,6 +742,7 @@ async function gpuLocal(req, dir) {
   entry.canaryIntact = entry.gpuCanary && entry.gpuPerfCanary;
   entry.rowFolds = rowFoldsOf(fs.lowered);
   entry.absorbed = absorbedOf(fs.lowered);
+  entry.loadOps = loadOpsOf(fs.lowered);
   entry.aliases = fs.lowered.aliases;
   entry.folded = fs.lowered.folded;
   entry.dead = fs.lowered.dead;
@@ -907,6 +908,19 @@ async function gpuStepSlices(req, dir) {
 function rowFoldsOf(lowered) {
   const out = {};
   for (const l of lowered.launches) if (l.rowFolds) out[l.node] = l.rowFolds;
+  return out;
+}
+
+/** {reader node: [{ slot, op, node, source }]}: the ops a perf lowering's matmuls apply to operands as they load them. */
+function loadOpsOf(lowered) {
+  const out = {};
+  for (const l of lowered.launches) {
+    for (const [slot, v] of Object.entries(l.views || {})) {
+      if (!v.view.op) continue;
+      if (!out[l.node]) out[l.node] = [];
+      out[l.node].push({ slot, op: v.view.op, node: v.opNode, source: v.source });
+    }
+  }
   return out;
 }
 
@@ -1355,7 +1369,7 @@ async function main() {
       }
       const l = lowerMI355X(g, { perf: true, keep, absorb });
       const plain = new Map(lowerMI355X(g).launches.map((x) => [x.node, x]));
-      out = { graph: g.toJSON(), keep, aliases: l.aliases, folded: l.folded, dead: l.dead, rowFolds: rowFoldsOf(l), absorbed: absorbedOf(l),
+      out = { graph: g.toJSON(), keep, aliases: l.aliases, folded: l.folded, dead: l.dead, rowFolds: rowFoldsOf(l), absorbed: absorbedOf(l), loadOps: loadOpsOf(l),
         launches: l.launches.map((x) => ({ node: x.node, kind: x.kind, inputs: x.inputs, views: x.views || null, modes: gemmModes(x),
           split: gemmSplit(x), plainSplit: gemmSplit(plain.get(x.node)) })) };
       break;

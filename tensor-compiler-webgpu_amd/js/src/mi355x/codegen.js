@@ -722,6 +722,15 @@ function gemmTiling(batch, M, N, K, tuning, peers) {
   return { T, chunks, chunkK, bk, pf, wn, prio, kw, blocks: wide * chunks };
 }
 
+// The op a view applies to every element it loads (view.op: 'relu'), as the view struct's
+// OP member (tcmi_gemm.h vop); nothing for a plain view, whose text stays as it was.
+const LOAD_OPS = { relu: 1 };
+function loadOp(v) {
+  if (!v.op) return '';
+  if (!LOAD_OPS[v.op]) throw new Error(`no operand load op '${v.op}'`);
+  return `\n  static constexpr int OP = ${LOAD_OPS[v.op]};   // ${v.op} on load`;
+}
+
 /**
  * Index `x` over mixed-radix factors [[extent, stride], ...] (outer to inner): the
  * expression Σ_f ((x / inner_f) % extent_f) · stride_f, the outermost factor without the
@@ -767,7 +776,7 @@ function operandView(name, view, batchDims, R, C) {
     };
     const mode = along(cf, rf, C) ? 0 : along(rf, cf, R) ? 1 : 2;
     const text = `struct ${name} {
-  static constexpr bool MAPPED = true;
+  static constexpr bool MAPPED = true;${loadOp(v)}
   static __device__ __forceinline__ size_t batch(uint32_t b) { return ${batchTerms}; }
   static __device__ __forceinline__ size_t row(uint32_t r) { return ${factorTerms('r', rf)}; }
   static __device__ __forceinline__ size_t col(uint32_t c) { return ${factorTerms('c', cf)}; }
@@ -781,7 +790,7 @@ function operandView(name, view, batchDims, R, C) {
   if (v.sc === 1 && C % 4 === 0 && others4(v.sr)) mode = 0;
   else if (v.sr === 1 && R % 4 === 0 && others4(v.sc)) mode = 1;
   const text = `struct ${name} {
-  static constexpr size_t SR = ${v.sr}, SC = ${v.sc};
+  static constexpr size_t SR = ${v.sr}, SC = ${v.sc};${loadOp(v)}
   static __device__ __forceinline__ size_t batch(uint32_t b) { return ${batchTerms}; }
 };
 `;
@@ -1041,8 +1050,11 @@ ${indent(inner, '      ')}
   const qv = operandView('__KERNEL___qv', views.q, batchDims, TQ, DH);
   const kv = operandView('__KERNEL___kv', views.k, batchDims, DH, TK);
   const vv = operandView('__KERNEL___vv', views.v, batchDims, TK, DV);
-  // The attention kernel addresses its operands by SR and SC: a mapped view never reaches it.
-  if (qv.mapped || kv.mapped || vv.mapped) throw new Error('attention operand read through a mapped view');
+  // The attention kernel addresses its operands by SR and SC and loads them as they are:
+  // a mapped view or a load op never reaches it.
+  if (qv.mapped || kv.mapped || vv.mapped || [views.q, views.k, views.v].some((v) => v && v.op)) {
+    throw new Error('attention operand read through a mapped view or a load op');
+  }
   const need = (slot, dense) => (sizes[slot] !== undefined ? sizes[slot] : dense);
   if (qv.limit > need('q', batch * TQ * DH) || kv.limit > need('k', batch * DH * TK) || vv.limit > need('v', batch * TK * DV)) {
     throw new Error('attention operand view out of bounds');

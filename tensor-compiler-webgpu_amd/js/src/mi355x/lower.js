@@ -26,7 +26,13 @@
 //     further such transposes, or as an epilogue group's operand that only its
 //     matmul reads) launches nothing either (`folded`): the matmuls read its
 //     source in place through a strided view (tcmi_gemm.h). The records of
-//     those matmuls name the source as their input.
+//     those matmuls name the source as their input. Reshapes on the way are
+//     passed through where the readers are plain or epilogue products: their
+//     view then maps a row or column index over several strides (a mapped view,
+//     chainMap below; attention's heads merged back into rows).
+//   - a relu whose every reader takes it as such a matmul operand launches
+//     nothing: the matmuls apply relu to the relu's operand as they load it
+//     (operandLoadOps below).
 //   - a broadcast whose every consumer reads it in an elementwise, rowwise or
 //     epilogue body (not as a matmul operand, not through a reduction or another
 //     gather) launches nothing: each consumer's kernel reads the broadcast's
@@ -213,7 +219,7 @@ function matmulSlots(n) {
  * such sinks, e.g. the gradient flowing into the max shift's stopGradient, or the dX of a
  * one-hot input): no launch, no buffer. Inputs and constants are never dead.
  */
-function perfPlan(graph, keep, rowFolding, absorbing) {
+function perfPlan(graph, keep, rowFolding, absorbing, loadOps) {
   const cons = consumersOf(graph);
   const live = new Set();
   for (let id = graph.nodes.length - 1; id >= 0; id--) {
@@ -387,7 +393,56 @@ function perfPlan(graph, keep, rowFolding, absorbing) {
     operands.set(e.id, next);
     for (const a of list) folded.add(a.prod);
   }
+  if (loadOps) operandLoadOps(graph, keep, cons, slotOf, dead, folded, views);
   return { aliases, folded, views, broadcasts, dead, rowFolds, absorbed };
+}
+
+/** The dense row-major view of an operand of `shape` ([..batch, R, C]). */
+function denseView(shape) {
+  const st = stridesOf(shape);
+  const r = shape.length;
+  return { batch: shape.slice(0, r - 2).map((e, d) => [e, st[d]]), sr: st[r - 2], sc: st[r - 1] };
+}
+
+/**
+ * Relu applied as matmul operands load (perf lowering): a relu whose every live reader
+ * takes it as a matmul operand (slot a or b), directly or through transposes and reshapes
+ * read in place, launches nothing. Each such matmul reads the relu's own operand through
+ * the same view, with `op: 'relu'` on it, and applies relu to every element it loads
+ * (tcmi::op_relu, the op the relu kernel would run, so the same bits; a zero-filled tile
+ * edge stays 0). Config 5's relu(h·W1 + b1) is one: read by h·W2 and, transposed, by the
+ * weight gradient of W2, while the backward pass reads the pre-activation. Updates
+ * `folded` and `views` (consumer id -> { slot: { pos, source, view, size } }).
+ */
+function operandLoadOps(graph, keep, cons, slotOf, dead, folded, views) {
+  for (const n of graph.nodes) {
+    if (n.op !== 'relu' || keep.has(n.id) || dead.has(n.id) || folded.has(n.id) || n.shape.length < 2) continue;
+    const src = n.inputs[0];
+    if (folded.has(src) || dead.has(src)) continue;
+    const users = cons[n.id].filter((c) => !dead.has(c));
+    const direct = [];
+    const ok = users.length > 0 && users.every((c) => {
+      if (folded.has(c) && graph.nodes[c].op === 'transpose') return true;
+      return graph.nodes[c].inputs.every((i, pos) => {
+        if (i !== n.id) return true;
+        const slot = slotOf.get(`${c}:${pos}`);
+        if (slot !== 'a' && slot !== 'b') return false;
+        direct.push([c, slot, pos]);
+        return true;
+      });
+    });
+    if (!ok) continue;
+    const viewed = [];
+    for (const slots of views.values()) for (const [slot, v] of Object.entries(slots)) if (v.source === n.id) viewed.push([slot, v]);
+    if (viewed.some(([slot]) => slot !== 'a' && slot !== 'b')) continue;
+    folded.add(n.id);
+    const size_ = size(graph.nodes[src].shape);
+    for (const [, v] of viewed) Object.assign(v, { source: src, view: Object.assign({}, v.view, { op: 'relu' }), size: size_, opNode: n.id });
+    for (const [c, slot, pos] of direct) {
+      if (!views.has(c)) views.set(c, {});
+      views.get(c)[slot] = { pos, source: src, view: Object.assign(denseView(n.shape), { op: 'relu' }), size: size_, opNode: n.id };
+    }
+  }
 }
 
 /**
@@ -622,7 +677,8 @@ const STREAM_FROM = 1 << 20;
 function lowerMI355X(graph, options) {
   const opts = options || {};
   if (opts.perf && !opts.keep) throw new Error('the perf lowering needs `keep`: the nodes whose values are read');
-  const plan = opts.perf ? perfPlan(graph, new Set(opts.keep), opts.rowFolds !== false, opts.absorb === true && opts.rowFolds !== false)
+  const plan = opts.perf ? perfPlan(graph, new Set(opts.keep), opts.rowFolds !== false, opts.absorb === true && opts.rowFolds !== false,
+    opts.loadOps !== false)
     : { aliases: new Map(), folded: new Set(), views: new Map(), broadcasts: new Map(), dead: new Set(), rowFolds: new Map(), absorbed: new Map() };
   const cache = new Map();
   const launches = [];
@@ -738,7 +794,11 @@ function lowerMI355X(graph, options) {
     if (v) {
       // Operands read in place: for each folded slot, the node it stands for and the view of its source.
       launches[launches.length - 1].views = {};
-      for (const slot of Object.keys(v)) launches[launches.length - 1].views[slot] = { pos: v[slot].pos, operand: node.inputs[v[slot].pos], source: v[slot].source, view: v[slot].view };
+      // A view applying an op on load (view.op) names the node of that op (opNode).
+      for (const slot of Object.keys(v)) {
+        launches[launches.length - 1].views[slot] = Object.assign({ pos: v[slot].pos, operand: node.inputs[v[slot].pos], source: v[slot].source,
+          view: v[slot].view }, v[slot].opNode !== undefined ? { opNode: v[slot].opNode } : {});
+      }
     }
   }
   const out = { launches, workspace, aliases: Array.from(plan.aliases.entries()), folded: Array.from(plan.folded), dead: Array.from(plan.dead) };

@@ -75,7 +75,8 @@ function fusedStep(step, options) {
   const remap = (m) => { const r = {}; for (const k of Object.keys(m)) r[k] = at(m[k]); return r; };
   const checked = lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning });
   const lowered = o.perf === false ? checked
-    : lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning, perf: true, keep: keep.map(at), batch: o.batch, absorb: true });
+    : lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning, perf: true, keep: keep.map(at), batch: o.batch, absorb: true,
+      loadOps: o.loadOps });
   return Object.assign({}, step, {
     graph: f.graph, fusion: f, original: step.graph,
     loss: at(step.loss), logits: at(step.logits),

@@ -104,6 +104,8 @@ def _mapped_case(name, src_shape, chain, role, other, act):
         if op == "transpose":
             shape = [shape[p] for p in arg]
             x = add("transpose", [x], {"perm": arg}, shape)
+        elif op == "relu":
+            x = add("relu", [x], {}, shape)
         else:
             shape = list(arg)
             x = add("reshape", [x], {"shape": shape}, shape)
@@ -122,8 +124,9 @@ def _mapped_case(name, src_shape, chain, role, other, act):
 # the heads of an attention merged back into rows ([B, H, T, dh] -> [B, T, H, dh] ->
 # [B·T, H·dh]) read as A, as B and transposed (the weight gradient's form), the key
 # gradient's double transpose, a head size that is not a multiple of 4 (per-element
-# loads), and a reshape that cuts the transposed layout where no mixed-radix map exists
-# (its transpose stays a launch).
+# loads), a reshape that cuts the transposed layout where no mixed-radix map exists
+# (its transpose stays a launch), and relus applied on load; "transposes read in place"
+# counts every node the perf lowering folds (the relus too).
 MAPPED = [
     ("heads-a", [2, 3, 20, 8], [("transpose", [0, 2, 1, 3]), ("reshape", [40, 24])], "a", [24, 36], 1, [0, 0]),
     ("heads-b", [2, 3, 20, 8], [("transpose", [0, 2, 1, 3]), ("reshape", [40, 24])], "b", [36, 40], 1, [0, 0]),
@@ -133,6 +136,14 @@ MAPPED = [
      "a", [24, 12], 2, [1, 0]),
     ("odd-heads", [2, 3, 20, 5], [("transpose", [0, 2, 1, 3]), ("reshape", [40, 15])], "a", [15, 9], 1, [2, 2]),
     ("unmappable", [6, 4], [("transpose", [1, 0]), ("reshape", [3, 8])], "a", [8, 5], 0, [0, 2]),
+    # A relu read only as a matmul operand: applied as the matmul loads it (the relu and
+    # the transposes after it launch nothing), directly, transposed through mapped views,
+    # and with per-element loads.
+    ("relu-a", [40, 24], [("relu", None)], "a", [24, 12], 1, [0, 0]),
+    ("relu-b", [40, 24], [("relu", None)], "b", [20, 40], 1, [0, 0]),
+    ("relu-heads-ta", [2, 3, 20, 8], [("relu", None), ("transpose", [0, 2, 1, 3]), ("reshape", [40, 24]),
+                                      ("transpose", [1, 0])], "a", [40, 16], 3, [1, 0]),
+    ("relu-odd", [9, 7], [("relu", None), ("transpose", [1, 0])], "b", [5, 7], 2, [2, 2]),
 ]
 
 

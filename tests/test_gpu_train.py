@@ -55,8 +55,11 @@ def node_local(tool, tmp_path, req):
     reductions = {f["reduction"] for fs in folds.values() for f in fs}
     producers = {f["producer"] for fs in folds.values() for f in fs if "producer" in f}
     producers |= absorbed_producers(took)
+    # Relus the matmuls reading them apply as they load their operand.
+    on_load = {o["node"] for ops in gc["loadOps"].values() for o in ops}
+    assert all(c["fused"]["nodes"][i]["op"] == "relu" for i in on_load)
     assert all(c["fused"]["nodes"][i]["op"] in ("reshape", "transpose", "broadcast")
-               for i in skipped - set(gc["dead"]) - reductions - producers)
+               for i in skipped - set(gc["dead"]) - reductions - producers - on_load)
     assert all(c["fused"]["nodes"][i]["op"] in ("sum", "max") for i in reductions)
     assert all(c["fused"]["nodes"][i]["op"] not in ("sum", "max", "matmul") for i in producers)
     # A chain with its reductions folded in is judged as the launch it is: the reductions and

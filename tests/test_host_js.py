@@ -187,13 +187,14 @@ def _mixed_radix(n, factors):
 
 
 def _chain_value(graph, operand, source, src_value):
-    """The operand's value from its source through the transpose/reshape chain between them (oracle kernels)."""
+    """The operand's value from its source through the transpose/reshape chain between them
+    (and the relu a view applies on load), by the oracle's kernels."""
     from oracle import interp
     chain = []
     cur = operand
     while cur != source:
         node = graph["nodes"][cur]
-        assert node["op"] in ("transpose", "reshape"), node["op"]
+        assert node["op"] in ("transpose", "reshape", "relu"), node["op"]
         chain.append(node)
         cur = node["inputs"][0]
     v = src_value
@@ -239,7 +240,21 @@ def test_perf_lowering_views_address_the_operands(tool, req):
         walk(records, int(reader))
     if req["model"] != "mlp":
         assert absorbed
-    assert all(nodes[i]["op"] in ("transpose", "broadcast") for i in set(d["folded"]) - reductions - producers - absorbed)
+    # Relus applied by the matmuls that read them, as they load them: every launched reader
+    # of such a relu reads it as a matmul operand through a view that names it.
+    on_load = {}
+    for reader, ops in d["loadOps"].items():
+        for o in ops:
+            assert nodes[o["node"]]["op"] == "relu" and o["op"] == "relu" and o["source"] == nodes[o["node"]]["inputs"][0]
+            on_load.setdefault(o["node"], set()).add(int(reader))
+    if req["model"] == "transformer":
+        assert len(on_load) == 4
+    for relu, readers in on_load.items():
+        assert relu not in d["keep"]
+        for l in d["launches"]:
+            named = any(v.get("opNode") == relu for v in (l["views"] or {}).values())
+            assert named == (l["node"] in readers), (relu, l["node"])
+    assert all(nodes[i]["op"] in ("transpose", "broadcast") for i in set(d["folded"]) - reductions - producers - absorbed - set(on_load))
     # A folded broadcast is read by elementwise, rowwise or epilogue bodies only (never
     # by a reduction, a gather or as a matmul operand), through the broadcast's source.
     for chain, fs in d["rowFolds"].items():
