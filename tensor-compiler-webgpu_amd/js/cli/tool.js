@@ -872,14 +872,33 @@ async function gpuStepSlices(req, dir) {
   // What each launched node needs: blocks (batch-carrying output) or whole values.
   const wantBlocks = new Set(), wantWhole = new Set();
   const launched = fs.checked.launches.map((l) => l.node);
-  for (const id of launched) {
+  const need = (id, ins) => {
     if (axis[id] >= 0) {
       wantBlocks.add(id);
-      for (const i of nodes[id].inputs) (axis[i] >= 0 ? wantBlocks : wantWhole).add(i);
+      for (const i of ins) (axis[i] >= 0 ? wantBlocks : wantWhole).add(i);
     } else {
       wantWhole.add(id);
-      for (const i of nodes[id].inputs) wantWhole.add(i);
+      for (const i of ins) wantWhole.add(i);
     }
+  };
+  for (const id of launched) need(id, nodes[id].inputs);
+  // A perf launch that forms values in place (absorbed producers, row folds) is judged on
+  // the operands of what it forms: a column sum that forms its operand is judged whole on
+  // that producer's operands whole, though the producer's own launch takes their blocks.
+  for (const l of fs.lowered.launches) {
+    const ins = new Set(nodes[l.node].inputs);
+    const walk = (records) => {
+      for (const a of records || []) {
+        for (const i of nodes[a.producer].inputs) ins.add(i);
+        walk(a.absorbed);
+      }
+    };
+    walk(l.absorbed);
+    for (const f of l.rowFolds || []) {
+      for (const i of nodes[f.reduction].inputs) ins.add(i);
+      if (f.producer !== undefined) for (const i of nodes[f.producer].inputs) ins.add(i);
+    }
+    need(l.node, ins);
   }
   const put = (a, id) => {
     const entry = {};

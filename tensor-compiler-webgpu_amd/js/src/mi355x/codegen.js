@@ -582,8 +582,15 @@ ${indent(store, '    ')}
  * Every output sums its terms in a fixed order (deterministic). Scalar form
  * (inner % 4 != 0): the same with one column per lane.
  */
-function colreduceKernels(op, outer, n, inner, tuning) {
+function colreduceKernels(op, outer, n, inner, tuning, producer) {
   const tune = tuning || {};
+  // A producer formed in place (`producer`: one elementwise op over full-size operands
+  // A.in[0..]): each element of the reduced operand is that op on the operands' elements
+  // at its index, through the op's own helper, so the same bits as reading the
+  // producer's output.
+  const pfn = producer ? (BINARY[producer.op] || UNARY[producer.op]) : null;
+  if (producer && !pfn) throw new Error(`no column-reduction producer '${producer.op}'`);
+  const arity = producer ? (BINARY[producer.op] ? 2 : 1) : 1;
   const isMax = op === 'max';
   const init = isMax ? '(-TCMI_INF)' : '0.f';
   const comb = isMax ? 'tcmi::red_max' : 'tcmi::red_sum';
@@ -602,6 +609,12 @@ function colreduceKernels(op, outer, n, inner, tuning) {
     : (a, b) => `${comb}(${a}, ${b})`;
   const ld = (ptr, idx) => (vec ? `reinterpret_cast<const tcmi::f4*>(${ptr})[(${idx}) >> 2]` : `(${ptr})[${idx}]`);
   const st = (ptr, idx, v) => (vec ? `reinterpret_cast<tcmi::f4*>(${ptr})[(${idx}) >> 2] = ${v};` : `(${ptr})[${idx}] = ${v};`);
+  const args = (l) => Array.from({ length: arity }, (_, q) => (vec ? `a${q}[${l}]` : `a${q}`)).join(', ');
+  const formed = producer ? [
+    ...Array.from({ length: arity }, (_, q) => `      const ${T} a${q} = ${ld(`x${q}`, '(size_t)k * inner + j')};`),
+    vec ? `      const ${T} v = tcmi::f4{${[0, 1, 2, 3].map((l) => `tcmi::${pfn}(${args(l)})`).join(', ')}};`
+      : `      const ${T} v = tcmi::${pfn}(${args(null)});`,
+  ].join('\n') : '';
   const first = `extern "C" __global__ void __launch_bounds__(256) __KERNEL__(const TcmiArgs A) {
   __shared__ ${T} part[4][64];
   const uint32_t n = ${n}u, inner = ${inner}u, splits = ${splits}u, chunk = ${chunk}u;
@@ -612,10 +625,10 @@ function colreduceKernels(op, outer, n, inner, tuning) {
   const uint32_t k1 = min(n, k0 + chunk);
   ${T} acc = ${zero};
   if (j < inner) {
-    const float* __restrict__ x = A.in[0] + (size_t)o * n * inner;
+${Array.from({ length: arity }, (_, q) => `    const float* __restrict__ x${q} = A.in[${q}] + (size_t)o * n * inner;`).join('\n')}
 #pragma unroll 8
     for (uint32_t k = k0 + g; k < k1; k += 4u) {
-      const ${T} v = ${ld('x', '(size_t)k * inner + j')};
+${producer ? formed : `      const ${T} v = ${ld('x0', '(size_t)k * inner + j')};`}
       acc = ${combV('acc', 'v')};
     }
   }

@@ -153,7 +153,10 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers,
       const t = opts.tuning || {};
       return Object.assign({ kind: 'rowreduce' }, single(cg.rowwiseKernel(body, output, { tuning: t.rowreduce || t.row, lastReads })));
     }
-    const c = cg.colreduceKernels(node.op, outer, n, inner, (opts.tuning || {}).colreduce);
+    // A column reduction whose operand's producer (one elementwise op) the lowering absorbed
+    // forms that op on the producer's operands as it reads them.
+    const prod = absorbs ? { op: graph.nodes[absorbs[0].prod].op } : null;
+    const c = cg.colreduceKernels(node.op, outer, n, inner, (opts.tuning || {}).colreduce, prod);
     return { kind: 'colreduce', kernels: c.launches, params: c.params, workspace: c.workspace, flops: 0 };
   }
   if (node.op === 'matmul') {
@@ -357,7 +360,8 @@ function perfPlan(graph, keep, rowFolding, absorbing, loadOps) {
   // one argument block.
   // A row reduction over the last axis of a 2-D operand (a rowwise kernel) absorbs its
   // operand's producer too, where the producer's body, and those of the producers it
-  // brings along, hold full-size values only (the rule of producer folds).
+  // brings along, hold full-size values only (the rule of producer folds); a column
+  // reduction absorbs a producer of one op (below).
   const absorbed = new Map();   // reader id -> [{ prod, pos: [reader positions], ppos, prodFolds, nested }]
   const operands = new Map();   // reader id -> its kernel's operand count with what it absorbed
   const isElementwise = (n) => ELEMENTWISE_OPS.has(n.op) || (n.op === 'fused' && n.attrs.kind === 'elementwise');
@@ -365,9 +369,17 @@ function perfPlan(graph, keep, rowFolding, absorbing, loadOps) {
     && graph.nodes[n.inputs[0]].shape.length === 2;
   const fullTree = (id, n) => size(graph.nodes[id].shape) === n && fullBody(graph.nodes[id])
     && (absorbed.get(id) || []).every((a) => fullTree(a.prod, n));
+  // A column reduction (a sum or max over an axis other than the last non-trivial one: the
+  // column-reduction kernels) absorbs a producer of one elementwise op over operands of the
+  // producer's own size, read at the same index (LayerNorm's dγ = Σ dy·x̂ over rows).
+  const isColReduction = (n) => (n.op === 'sum' || n.op === 'max') && !dead.has(n.id)
+    && size(graph.nodes[n.inputs[0]].shape.slice(n.attrs.axis + 1)) > 1;
+  const oneOpFull = (p) => ELEMENTWISE_OPS.has(p.op) && !broadcasts.has(p.id) && !absorbed.has(p.id)
+    && p.inputs.every((i) => size(graph.nodes[i].shape) === size(p.shape) && !folded.has(i));
   for (const e of absorbing ? graph.nodes : []) {
     const reduction = isRowReduction(e);
-    if (!(isElementwise(e) || reduction) || folded.has(e.id) || dead.has(e.id) || aliases.has(e.id) || rowFolds.has(e.id)) continue;
+    const columns = isColReduction(e);
+    if (!(isElementwise(e) || reduction || columns) || folded.has(e.id) || dead.has(e.id) || aliases.has(e.id) || rowFolds.has(e.id)) continue;
     const own = broadcasts.get(e.id);
     let next = e.inputs.length;
     const list = [];
@@ -378,6 +390,7 @@ function perfPlan(graph, keep, rowFolding, absorbing, loadOps) {
       if (at.some((pos) => own && own.has(pos))) continue;
       if (new Set(cons[pid].filter((c) => !dead.has(c))).size !== 1) continue;
       if (reduction && !fullTree(pid, size(p.shape))) continue;
+      if (columns && !oneOpFull(p)) continue;
       const pf = broadcasts.get(pid);
       if (!p.inputs.every((i, j) => !folded.has(i) || (pf && pf.has(j)) || (absorbed.get(pid) || []).some((a) => a.prod === i))) continue;
       const m = operands.get(pid) || p.inputs.length;
