@@ -362,8 +362,8 @@ function perfPlan(graph, keep, rowFolding, absorbing, loadOps) {
   // operand's producer too, where the producer's body, and those of the producers it
   // brings along, hold full-size values only (the rule of producer folds); a column
   // reduction absorbs a producer of one op (below).
-  const absorbed = new Map();   // reader id -> [{ prod, pos: [reader positions], ppos, prodFolds, nested }]
-  const operands = new Map();   // reader id -> its kernel's operand count with what it absorbed
+  let absorbed = new Map();   // reader id -> [{ prod, pos: [reader positions], ppos, prodFolds, nested }]
+  let operands = new Map();   // reader id -> its kernel's operand count with what it absorbed
   const isElementwise = (n) => ELEMENTWISE_OPS.has(n.op) || (n.op === 'fused' && n.attrs.kind === 'elementwise');
   const isRowReduction = (n) => (n.op === 'sum' || n.op === 'max') && n.attrs.axis === 1
     && graph.nodes[n.inputs[0]].shape.length === 2;
@@ -376,35 +376,75 @@ function perfPlan(graph, keep, rowFolding, absorbing, loadOps) {
     && size(graph.nodes[n.inputs[0]].shape.slice(n.attrs.axis + 1)) > 1;
   const oneOpFull = (p) => ELEMENTWISE_OPS.has(p.op) && !broadcasts.has(p.id) && !absorbed.has(p.id)
     && p.inputs.every((i) => size(graph.nodes[i].shape) === size(p.shape) && !folded.has(i));
-  for (const e of absorbing ? graph.nodes : []) {
-    const reduction = isRowReduction(e);
-    const columns = isColReduction(e);
-    if (!(isElementwise(e) || reduction || columns) || folded.has(e.id) || dead.has(e.id) || aliases.has(e.id) || rowFolds.has(e.id)) continue;
-    const own = broadcasts.get(e.id);
-    let next = e.inputs.length;
-    const list = [];
-    for (const pid of new Set(e.inputs)) {
-      const p = graph.nodes[pid];
-      const at = e.inputs.map((i, pos) => (i === pid ? pos : -1)).filter((pos) => pos >= 0);
-      if (!isElementwise(p) || keep.has(pid) || folded.has(pid) || dead.has(pid) || aliases.has(pid) || rowFolds.has(pid)) continue;
-      if (at.some((pos) => own && own.has(pos))) continue;
-      if (new Set(cons[pid].filter((c) => !dead.has(c))).size !== 1) continue;
-      if (reduction && !fullTree(pid, size(p.shape))) continue;
-      if (columns && !oneOpFull(p)) continue;
-      const pf = broadcasts.get(pid);
-      if (!p.inputs.every((i, j) => !folded.has(i) || (pf && pf.has(j)) || (absorbed.get(pid) || []).some((a) => a.prod === i))) continue;
-      const m = operands.get(pid) || p.inputs.length;
-      // A producer of constants alone has no operand to take the reader's slot.
-      if (m === 0 || next + m - 1 > cg.MAX_IN) continue;
-      const ppos = [];
-      for (let j = 0; j < m; j++) ppos.push(j === 0 ? at[0] : next + j - 1);
-      list.push({ prod: pid, pos: at, ppos, prodFolds: pf || null, nested: absorbed.get(pid) || null });
-      next += m - 1;
+  const readersOf = (pid) => Array.from(new Set(cons[pid].filter((c) => !dead.has(c))));
+  // The full-size operands a producer's kernel reads (its folded broadcasts' sources and
+  // its operands of other sizes aside; those of the producers it absorbed included).
+  const fullReads = (pid) => {
+    const p = graph.nodes[pid];
+    const pf = broadcasts.get(pid);
+    const took = new Map((absorbed.get(pid) || []).map((a) => [a.prod, a]));
+    const out = new Set();
+    p.inputs.forEach((i, j) => {
+      if (pf && pf.has(j)) return;
+      if (took.has(i)) for (const x of fullReads(i)) out.add(x);
+      else if (size(graph.nodes[i].shape) === size(p.shape)) out.add(i);
+    });
+    return out;
+  };
+  // A producer with several live readers is formed by each of them where all of them can
+  // take it in and that moves no more bytes than its own launch would: r readers reading its
+  // f full-size operands instead of its value (r·f) against the launch reading them and
+  // writing its value (f + 1) and the readers reading that (r). LayerNorm's centred rows,
+  // normalised rows and scaled gradient (read by two to five chains each) are such. Passes
+  // repeat with the producers some reader could not take in left out, until every producer
+  // allowed is taken in by all its readers (those launch nothing).
+  let allowed = null;
+  const before = new Set(folded);
+  for (;;) {
+    absorbed = new Map();
+    operands = new Map();
+    for (const id of Array.from(folded)) if (!before.has(id)) folded.delete(id);
+    const shared = new Map();   // producer with several readers -> readers that took it in
+    for (const e of absorbing ? graph.nodes : []) {
+      const reduction = isRowReduction(e);
+      const columns = isColReduction(e);
+      if (!(isElementwise(e) || reduction || columns) || folded.has(e.id) || dead.has(e.id) || aliases.has(e.id) || rowFolds.has(e.id)) continue;
+      const own = broadcasts.get(e.id);
+      let next = e.inputs.length;
+      const list = [];
+      for (const pid of new Set(e.inputs)) {
+        const p = graph.nodes[pid];
+        const at = e.inputs.map((i, pos) => (i === pid ? pos : -1)).filter((pos) => pos >= 0);
+        if (!isElementwise(p) || keep.has(pid) || folded.has(pid) || dead.has(pid) || aliases.has(pid) || rowFolds.has(pid)) continue;
+        if (at.some((pos) => own && own.has(pos))) continue;
+        const r = readersOf(pid).length;
+        if (r !== 1) {
+          if (allowed ? !allowed.has(pid) : r * fullReads(pid).size > fullReads(pid).size + 1 + r) continue;
+        }
+        if (reduction && !fullTree(pid, size(p.shape))) continue;
+        if (columns && !oneOpFull(p)) continue;
+        const pf = broadcasts.get(pid);
+        if (!p.inputs.every((i, j) => !folded.has(i) || (pf && pf.has(j)) || (absorbed.get(pid) || []).some((a) => a.prod === i))) continue;
+        const m = operands.get(pid) || p.inputs.length;
+        // A producer of constants alone has no operand to take the reader's slot.
+        if (m === 0 || next + m - 1 > cg.MAX_IN) continue;
+        const ppos = [];
+        for (let j = 0; j < m; j++) ppos.push(j === 0 ? at[0] : next + j - 1);
+        list.push({ prod: pid, pos: at, ppos, prodFolds: pf || null, nested: absorbed.get(pid) || null });
+        next += m - 1;
+        if (r !== 1) { if (!shared.has(pid)) shared.set(pid, new Set()); shared.get(pid).add(e.id); }
+      }
+      if (!list.length) continue;
+      absorbed.set(e.id, list);
+      operands.set(e.id, next);
+      for (const a of list) if (!shared.has(a.prod)) folded.add(a.prod);
     }
-    if (!list.length) continue;
-    absorbed.set(e.id, list);
-    operands.set(e.id, next);
-    for (const a of list) folded.add(a.prod);
+    const whole = new Set(Array.from(shared).filter(([pid, by]) => by.size === readersOf(pid).length).map(([pid]) => pid));
+    if (allowed && whole.size === allowed.size) {
+      for (const pid of whole) folded.add(pid);
+      break;
+    }
+    allowed = whole;
   }
   if (loadOps) operandLoadOps(graph, keep, cons, slotOf, dead, folded, views);
   return { aliases, folded, views, broadcasts, dead, rowFolds, absorbed };

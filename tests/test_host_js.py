@@ -221,15 +221,17 @@ def test_perf_lowering_views_address_the_operands(tool, req):
     producers = {f["producer"] for fs in d["rowFolds"].values() for f in fs if "producer" in f}
     absorbed = set()
 
+    takers = {}
+
     def walk(records, reader):
         for a in records:
             # An absorbed producer: an elementwise node its reader reads at `pos`, kept by
-            # nobody, read by no other launched node.
+            # nobody; every live reader of it forms it (checked below).
             p = nodes[a["producer"]]
             assert all(nodes[reader]["inputs"][q] == a["producer"] for q in a["pos"])
             assert p["op"] in ELEMENTWISE or (p["op"] == "fused" and p["attrs"]["kind"] == "elementwise")
             assert a["producer"] not in d["keep"] and a["producerPos"][0] == a["pos"][0]
-            assert consumers[a["producer"]] - set(d["dead"]) == {reader}
+            takers.setdefault(a["producer"], set()).add(reader)
             absorbed.add(a["producer"])
             walk(a.get("absorbed", []), a["producer"])
     consumers = {}
@@ -238,6 +240,10 @@ def test_perf_lowering_views_address_the_operands(tool, req):
             consumers.setdefault(i, set()).add(n_id)
     for reader, records in d["absorbed"].items():
         walk(records, int(reader))
+    # A producer formed in place is formed by every live reader of it (a launch, or a
+    # producer formed in place in turn): nothing reads a buffer it would have written.
+    for prod, by in takers.items():
+        assert consumers[prod] - set(d["dead"]) == by, (prod, by)
     if req["model"] != "mlp":
         assert absorbed
     # Relus applied by the matmuls that read them, as they load them: every launched reader
