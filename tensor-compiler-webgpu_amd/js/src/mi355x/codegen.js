@@ -584,13 +584,6 @@ ${indent(store, '    ')}
  */
 function colreduceKernels(op, outer, n, inner, tuning, producer) {
   const tune = tuning || {};
-  // A producer formed in place (`producer`: one elementwise op over full-size operands
-  // A.in[0..]): each element of the reduced operand is that op on the operands' elements
-  // at its index, through the op's own helper, so the same bits as reading the
-  // producer's output.
-  const pfn = producer ? (BINARY[producer.op] || UNARY[producer.op]) : null;
-  if (producer && !pfn) throw new Error(`no column-reduction producer '${producer.op}'`);
-  const arity = producer ? (BINARY[producer.op] ? 2 : 1) : 1;
   const isMax = op === 'max';
   const init = isMax ? '(-TCMI_INF)' : '0.f';
   const comb = isMax ? 'tcmi::red_max' : 'tcmi::red_sum';
@@ -609,12 +602,36 @@ function colreduceKernels(op, outer, n, inner, tuning, producer) {
     : (a, b) => `${comb}(${a}, ${b})`;
   const ld = (ptr, idx) => (vec ? `reinterpret_cast<const tcmi::f4*>(${ptr})[(${idx}) >> 2]` : `(${ptr})[${idx}]`);
   const st = (ptr, idx, v) => (vec ? `reinterpret_cast<tcmi::f4*>(${ptr})[(${idx}) >> 2] = ${v};` : `(${ptr})[${idx}] = ${v};`);
-  const args = (l) => Array.from({ length: arity }, (_, q) => (vec ? `a${q}[${l}]` : `a${q}`)).join(', ');
-  const formed = producer ? [
-    ...Array.from({ length: arity }, (_, q) => `      const ${T} a${q} = ${ld(`x${q}`, '(size_t)k * inner + j')};`),
-    vec ? `      const ${T} v = tcmi::f4{${[0, 1, 2, 3].map((l) => `tcmi::${pfn}(${args(l)})`).join(', ')}};`
-      : `      const ${T} v = tcmi::${pfn}(${args(null)});`,
-  ].join('\n') : '';
+  // A producer formed in place (`producer`: { body, output }, an elementwise body over the
+  // launch's operands A.in[0..], its value of the reduced operand's shape): each element
+  // the reduction reads is the body at that element's flat index g0 (+ its lane in a
+  // 4-column group), through the same emitter and op helpers as an elementwise kernel, so
+  // the same bits as reading the producer's output. Operands of the full size load a
+  // 4-column group at once; others (broadcast rows or columns) load at their index map.
+  const pparams = [];
+  let formed = '';
+  if (producer) {
+    if (outer * n * inner >= 2 ** 32) throw new Error('column reduction with a producer: operand past 2^32 elements');
+    const lines = [];
+    const full = new Set();
+    const em = new Emitter(producer.body, pparams, {
+      load(k, ctx, ls) {
+        if (ctx.root && vec) {
+          if (!full.has(k)) { ls.push(`const tcmi::f4 F${k} = reinterpret_cast<const tcmi::f4*>(A.in[${k}])[g0 >> 2];`); full.add(k); }
+          return `F${k}[${ctx.lane}]`;
+        }
+        const v = `L${ls.length}_${k}`;
+        ls.push(`const float ${v} = A.in[${k}][${ctx.idx}];`);
+        return v;
+      },
+    });
+    const outs = [];
+    for (let l = 0; l < W; l++) {
+      outs.push(em.value(producer.output, { key: `e${l}`, idx: l ? `(g0 + ${l}u)` : 'g0', root: true, lane: l, limit: outer * n * inner }, lines));
+    }
+    formed = [`      const uint32_t g0 = (o * n + k) * inner + j;`, ...lines.map((x) => `      ${x}`),
+      `      const ${T} v = ${vec ? `tcmi::f4{${outs.join(', ')}}` : outs[0]};`].join('\n');
+  }
   const first = `extern "C" __global__ void __launch_bounds__(256) __KERNEL__(const TcmiArgs A) {
   __shared__ ${T} part[4][64];
   const uint32_t n = ${n}u, inner = ${inner}u, splits = ${splits}u, chunk = ${chunk}u;
@@ -625,10 +642,9 @@ function colreduceKernels(op, outer, n, inner, tuning, producer) {
   const uint32_t k1 = min(n, k0 + chunk);
   ${T} acc = ${zero};
   if (j < inner) {
-${Array.from({ length: arity }, (_, q) => `    const float* __restrict__ x${q} = A.in[${q}] + (size_t)o * n * inner;`).join('\n')}
-#pragma unroll 8
+${producer ? '' : '    const float* __restrict__ x = A.in[0] + (size_t)o * n * inner;\n'}#pragma unroll 8
     for (uint32_t k = k0 + g; k < k1; k += 4u) {
-${producer ? formed : `      const ${T} v = ${ld('x0', '(size_t)k * inner + j')};`}
+${producer ? formed : `      const ${T} v = ${ld('x', '(size_t)k * inner + j')};`}
       acc = ${combV('acc', 'v')};
     }
   }
@@ -678,7 +694,7 @@ ${producer ? formed : `      const ${T} v = ${ld('x0', '(size_t)k * inner + j')}
     const k2 = kernelText('colfin', second);
     launches.push({ name: k2.name, source: k2.source, grid: [Math.ceil(inner / (W * groupsPerBlock)), outer, 1], block: [256, 1, 1], lds: 0 });
   }
-  return { launches, params: Uint32Array.from([outer, n, inner, splits, chunk]), workspace: splits > 1 ? outer * splits * inner * 4 : 0 };
+  return { launches, params: Uint32Array.from([outer, n, inner, splits, chunk, ...pparams]), workspace: splits > 1 ? outer * splits * inner * 4 : 0 };
 }
 
 // ---- matmul with epilogue ----------------------------------------------------------------

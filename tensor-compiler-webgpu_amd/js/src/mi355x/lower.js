@@ -153,9 +153,14 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers,
       const t = opts.tuning || {};
       return Object.assign({ kind: 'rowreduce' }, single(cg.rowwiseKernel(body, output, { tuning: t.rowreduce || t.row, lastReads })));
     }
-    // A column reduction whose operand's producer (one elementwise op) the lowering absorbed
-    // forms that op on the producer's operands as it reads them.
-    const prod = absorbs ? { op: graph.nodes[absorbs[0].prod].op } : null;
+    // A column reduction whose operand's producer the lowering absorbed forms it (with what
+    // it took in) on the producer's operands as it reads them.
+    let prod = null;
+    if (absorbs) {
+      const g = new Graph();
+      const a0 = g.input('a0', inShape);
+      prod = absorbProducers(graph, { body: g, output: a0 }, absorbs);
+    }
     const c = cg.colreduceKernels(node.op, outer, n, inner, (opts.tuning || {}).colreduce, prod);
     return { kind: 'colreduce', kernels: c.launches, params: c.params, workspace: c.workspace, flops: 0 };
   }
@@ -360,8 +365,8 @@ function perfPlan(graph, keep, rowFolding, absorbing, loadOps) {
   // one argument block.
   // A row reduction over the last axis of a 2-D operand (a rowwise kernel) absorbs its
   // operand's producer too, where the producer's body, and those of the producers it
-  // brings along, hold full-size values only (the rule of producer folds); a column
-  // reduction absorbs a producer of one op (below).
+  // brings along, hold full-size values only (the rule of producer folds); so does a
+  // column reduction (below).
   let absorbed = new Map();   // reader id -> [{ prod, pos: [reader positions], ppos, prodFolds, nested }]
   let operands = new Map();   // reader id -> its kernel's operand count with what it absorbed
   const isElementwise = (n) => ELEMENTWISE_OPS.has(n.op) || (n.op === 'fused' && n.attrs.kind === 'elementwise');
@@ -370,12 +375,12 @@ function perfPlan(graph, keep, rowFolding, absorbing, loadOps) {
   const fullTree = (id, n) => size(graph.nodes[id].shape) === n && fullBody(graph.nodes[id])
     && (absorbed.get(id) || []).every((a) => fullTree(a.prod, n));
   // A column reduction (a sum or max over an axis other than the last non-trivial one: the
-  // column-reduction kernels) absorbs a producer of one elementwise op over operands of the
-  // producer's own size, read at the same index (LayerNorm's dγ = Σ dy·x̂ over rows).
+  // column-reduction kernels) absorbs its operand's producer too: the kernel forms it at
+  // each element's flat index, broadcast operands through their index maps (LayerNorm's
+  // dγ = Σ dy·x̂ over rows, x̂ formed from the centred rows and the row deviation).
   const isColReduction = (n) => (n.op === 'sum' || n.op === 'max') && !dead.has(n.id)
-    && size(graph.nodes[n.inputs[0]].shape.slice(n.attrs.axis + 1)) > 1;
-  const oneOpFull = (p) => ELEMENTWISE_OPS.has(p.op) && !broadcasts.has(p.id) && !absorbed.has(p.id)
-    && p.inputs.every((i) => size(graph.nodes[i].shape) === size(p.shape) && !folded.has(i));
+    && size(graph.nodes[n.inputs[0]].shape.slice(n.attrs.axis + 1)) > 1
+    && size(graph.nodes[n.inputs[0]].shape) < 2 ** 32;
   const readersOf = (pid) => Array.from(new Set(cons[pid].filter((c) => !dead.has(c))));
   // The full-size operands a producer's kernel reads (its folded broadcasts' sources and
   // its operands of other sizes aside; those of the producers it absorbed included).
@@ -422,8 +427,7 @@ function perfPlan(graph, keep, rowFolding, absorbing, loadOps) {
           if (allowed ? !allowed.has(pid) : r * fullReads(pid).size > fullReads(pid).size + 1 + r) continue;
         }
         if (reduction && !fullTree(pid, size(p.shape))) continue;
-        if (columns && !oneOpFull(p)) continue;
-        const pf = broadcasts.get(pid);
+          const pf = broadcasts.get(pid);
         if (!p.inputs.every((i, j) => !folded.has(i) || (pf && pf.has(j)) || (absorbed.get(pid) || []).some((a) => a.prod === i))) continue;
         const m = operands.get(pid) || p.inputs.length;
         // A producer of constants alone has no operand to take the reader's slot.

@@ -169,4 +169,4 @@ def test_c5_full_size_trainer(tool, graph, arena, streams):
     assert r["batches"] >= 12, r["batches"]
     assert r["dispatches"] == (r["kernels"] - r["batchSaves"] if streams == 1 else r["kernels"]), r
     if arena:
-        assert r["arena"]["bytes"] < 0.5 * r["arena"]["unshared"], r["arena"]
+        assert r["arena"]["bytes"] < 0.55 * r["arena"]["unshared"] and r["arena"]["bytes"] < 0.85e9, r["arena"]
