@@ -554,7 +554,9 @@ function trainStep(runner, bench, name, req, opts) {
   // The unfused step in the same perf lowering the fused trainer runs.
   const lu = lowerMI355X(m.step.graph, { perf: true, keep: [m.step.loss, m.step.logits].concat(Object.values(m.step.outputs)), rowFolds: false });
   runner.functions([fs.lowered, lu]);
-  const K = Number(arg('train-steps', opts.quick ? 3 : 10)), W = 2;
+  // 40 timed steps after 5 warm-ups: config 1's step is about 50 µs, so fewer steps would
+  // time a few hundred µs of work.
+  const K = Number(arg('train-steps', opts.quick ? 3 : 40)), W = opts.quick ? 2 : 5;
   const batch = m.batch(0);
   const graph = !flag('no-trainer-graphs');
   const trainer = new HipTrainer(runner, fs, m.params, m.state, { graph });
