@@ -1358,6 +1358,25 @@ async function main() {
     }
     case 'attention-graphs': out = attentionGraphs(req.cases || ATTENTION_CASES); break;
     case 'transformer-forward': out = transformerForward(req); break;
+    case 'chain-map': {
+      // The index maps of values read through chains of transposes and reshapes (lower.js
+      // chainMap): for each { shape, chain: [["transpose", perm] | ["reshape", shape]] }, the
+      // factor lists per dimension of the chain's value, or null where no such map exists.
+      const { chainMap } = require('../src/mi355x/lower');
+      out = req.cases.map((c) => {
+        const g = new Graph();
+        let x = g.input('s', c.shape);
+        const ids = [];
+        for (const [op, arg] of c.chain) {
+          // The builder returns its operand for an identity transpose or reshape.
+          const y = op === 'transpose' ? g.transpose(x, arg) : g.reshape(x, arg);
+          if (y !== x) ids.push(y);
+          x = y;
+        }
+        return { map: chainMap(g, 0, ids), shape: g.nodes[x].shape };
+      });
+      break;
+    }
     case 'perf-lower': {
       // The perf lowering of a model step or of a graph: launches, aliases, folded nodes, operand views.
       // A model's fused step as the trainer lowers it (producers absorbed); a graph with

@@ -996,4 +996,4 @@ function kernelSources(lowered) {
   return seen;
 }
 
-module.exports = { lowerMI355X, kernelSources, batchPlan, lowerNode, oneOpBody, algorithmicBytes };
+module.exports = { lowerMI355X, kernelSources, batchPlan, lowerNode, oneOpBody, algorithmicBytes, chainMap };

@@ -490,3 +490,50 @@ def test_recomputed_epilogue_reads_its_product_through_the_workspace(tool):
     part, red = epi["kernels"]
     assert ", true, " in part["source"] and "gemm_product_at" in red["source"] and red["name"].endswith("_red")
     assert rec["workspace"] >= 2 * 4 * 2 * 4
+
+
+def test_chain_maps_address_random_transpose_reshape_chains(tool):
+    """The mixed-radix index maps of the perf lowering's mapped views (lower.js chainMap),
+    against numpy on distinct values: random chains of transposes and reshapes over random
+    shapes: where a map is given (about two thirds of them; the others hold a reshape that
+    cuts a factor where neither extent divides the other), every element of the chain's
+    value is found at the offset the map gives."""
+    rng = np.random.default_rng(5)
+    cases = []
+    for _ in range(300):
+        rank = int(rng.integers(2, 5))
+        shape = [int(rng.choice([1, 2, 3, 4, 5, 6, 8])) for _ in range(rank)]
+        chain, cur = [], list(shape)
+        for _ in range(int(rng.integers(1, 5))):
+            if rng.random() < 0.5:
+                perm = [int(p) for p in rng.permutation(len(cur))]
+                chain.append(["transpose", perm])
+                cur = [cur[p] for p in perm]
+            else:
+                n = int(np.prod(cur))
+                dims = []
+                while n > 1:
+                    d = int(rng.choice([f for f in range(2, n + 1) if n % f == 0]))
+                    dims.append(d)
+                    n //= d
+                cur = dims or [1]
+                chain.append(["reshape", cur])
+        cases.append({"shape": shape, "chain": chain})
+    res = tool("chain-map", {"cases": cases})
+    mapped = 0
+    for c, r in zip(cases, res):
+        src = np.arange(int(np.prod(c["shape"]))).reshape(c["shape"])
+        v = src
+        for op, arg in c["chain"]:
+            v = np.transpose(v, arg) if op == "transpose" else v.reshape(arg)
+        assert list(v.shape) == r["shape"]
+        if r["map"] is None:
+            continue
+        mapped += 1
+        idx = np.zeros(v.shape, dtype=np.int64)
+        for axis, factors in enumerate(r["map"]):
+            sh = [1] * v.ndim
+            sh[axis] = v.shape[axis]
+            idx = idx + _mixed_radix(v.shape[axis], factors).reshape(sh)
+        assert np.array_equal(src.reshape(-1)[idx], v), c
+    assert mapped >= 150
