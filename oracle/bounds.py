@@ -247,6 +247,12 @@ def judge_fused(fused_graph, origin, gpu, ref):
     worst, first = 0.0, None
     for node_id, node in enumerate(fused_graph["nodes"]):
         o = origin[node_id]
+        # A node no original node holds (origin -1: a transposed operand formed for a
+        # product formed transposed) has no reference value here; refuse it rather than
+        # read ref[-1], which Python would take as the last node.
+        if o is None or o < 0:
+            return {"pass": False, "worst": np.inf, "first": {"node": node_id, "origin": o, "op": node["op"],
+                                                              "reason": "origin"}}
         g, r, e = np.asarray(gpu[node_id]), ref["values"][o], ref["bounds"][o]
         if g.size != r.size:
             return {"pass": False, "worst": np.inf, "first": {"node": node_id, "origin": o, "op": node["op"], "reason": "length"}}

@@ -72,8 +72,8 @@ def check_node_loads() -> None:
 
 
 # (group, shard, shards): the fuzz corpus's ~7500 kernels are compiled in 6 parts.
-PRECOMPILE_JOBS = ([("direct", 0, 1), ("models", 0, 1), ("configs", 0, 1), ("sweep", 0, 1), ("attention", 0, 1),
-                    ("recompute", 0, 1), ("scratch", 0, 1)]
+PRECOMPILE_JOBS = ([("direct", 0, 1), ("models", 0, 1), ("golden", 0, 1), ("configs", 0, 1), ("sweep", 0, 1),
+                    ("attention", 0, 1), ("recompute", 0, 1), ("scratch", 0, 1)]
                    + [("fuzz", k, 6) for k in range(6)])
 KCACHE = PKG / "_build" / "kcache"
 

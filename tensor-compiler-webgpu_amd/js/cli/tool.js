@@ -16,6 +16,8 @@
 //   random-programs  request {programs: [{seed, focus?, f32?}]} -> the reference's v2 random programs
 //   corpus-fusion    request {from, to, sabotageTo?} -> fusion counts over corpus programs
 //   config-graphs    request {c3: [{fn, R, C}], c4: [{act, M, K, N}]} -> forward and gradient graphs of configs 3 and 4
+//   step-graph       (bundle) request {model, V?, B?, seed?, firstBatch?, params64?}: a model's step graph, fused, with its inputs
+//   forward-graph    (bundle) request {model, V?, B?, seed?, firstBatch?, params64?}: a model's forward pass, fused, with its inputs
 // GPU commands write a bundle (manifest.json + data.f32) under --out:
 //   gpu-direct       request {sabotage?}: every direct case, fused, canary-padded, on the GPU
 //   gpu-graphs       request {graphs: [{name, graph, inputs, keep, unfused?, perf?}]} fused (and unfused, and in the perf lowering) on the GPU
@@ -24,6 +26,8 @@
 //   gpu-workloads    request {ids?, families?, allNodes?}: the workload sweep's variants run once, outputs for the gate
 //   gpu-bench-selftest  the timing protocol's counters: a clean timed region, a planted leak that must trip
 //   gpu-step-slices  request {model, B, sequences}: a full-batch step's launches with their operands, as per-sequence blocks
+//   gpu-local        request {model, forward?, valuesFile, sets?, sabotage?, perf?}: a fused step or forward pass run
+//                    node-locally on the checker's reference operands, one case per value set
 //   grouped-batches  request {model, B}: the batched kernels of a step's split-K products, with their text
 
 const fs = require('fs');
@@ -185,6 +189,23 @@ function precompileGroup(group, arch, shard, shards) {
       // The bench's unfused step runs in the perf lowering as well.
       const unfused = lowerMI355X(m.step.graph, { perf: true, keep: [m.step.loss, m.step.logits].concat(Object.values(m.step.outputs)), rowFolds: false });
       n += precompile([fs.lowered], arch) + precompile([fs.checked], arch) + precompile([unfused], arch);
+    }
+    return n;
+  }
+  if (group === 'golden') {
+    // The reference transformer's model-level checks at its golden size (V 16, batch 4):
+    // the forward pass fused (plain and perf lowerings), and the step and the forward pass
+    // under each kernel sabotage (plain lowering). The honest step is the models group's.
+    const { modelForward } = require('../src/builders/models');
+    const { fusedForward } = require('../src/mi355x/trainer');
+    const { modelStep } = require('../src/builders/models');
+    const { fusedStep } = require('../src/mi355x/trainer');
+    const req = { model: 'transformer-ref' };
+    const ff = fusedForward(modelForward(req).fwd);
+    let n = precompile([ff.checked], arch) + precompile([ff.lowered], arch);
+    for (const sabotage of KERNEL_SABOTAGES) {
+      n += precompile([fusedForward(modelForward(req).fwd, { sabotage, perf: false }).checked], arch);
+      n += precompile([fusedStep(modelStep(req).step, { sabotage, perf: false }).checked], arch);
     }
     return n;
   }
@@ -685,10 +706,15 @@ async function gpuChains(req, dir) {
   bundle.close({ device: runner.info() });
 }
 
+/** Plain arrays of a name -> values map, at full (float64) precision, for a JSON manifest. */
+const plainArrays = (m) => { const r = {}; for (const k of Object.keys(m)) r[k] = Array.from(m[k]); return r; };
+
 /**
  * The step graph of a model request as a bundle: the original and fused graphs,
  * the origin map, the ids that matter, and the step's inputs (parameters, state,
- * batch k, cotangent 1) as float32 arrays. No GPU.
+ * batch k, cotangent 1) as float32 arrays. With `params64`, the initial parameters
+ * and state also as float64 numbers in the manifest (a float64 trajectory starts
+ * from them, as the reference's trainCpu3b does). No GPU.
  */
 function stepGraph(req, dir) {
   const { modelStep } = require('../src/builders/models');
@@ -701,52 +727,90 @@ function stepGraph(req, dir) {
   values[m.step.cotangent] = [1];
   const inputs = {};
   for (const k of Object.keys(values)) inputs[k] = bundle.put(values[k]);
-  bundle.add({ name: req.model, graph: m.step.graph.toJSON(), fused: fs.graph.toJSON(), origin: fs.fusion.origin, inputs,
+  const entry = { name: req.model, graph: m.step.graph.toJSON(), fused: fs.graph.toJSON(), origin: fs.fusion.origin, inputs,
     loss: m.step.loss, logits: m.step.logits, outputs: m.step.outputs, stepInputs: m.step.inputs, names: m.step.names,
-    launchesFused: fs.lowered.launches.length, info: m.info });
+    stateNames: m.step.stateNames || [], cotangent: m.step.cotangent,
+    launchesFused: fs.lowered.launches.length, launchesChecked: fs.checked.launches.length,
+    launchesUnfused: lowerMI355X(m.step.graph).launches.length, info: m.info };
+  if (req.params64) Object.assign(entry, { params64: plainArrays(m.params), state64: plainArrays(m.state) });
+  bundle.add(entry);
   bundle.close();
 }
 
 /**
- * Node-local run of a model's fused step: every launch reads the float32
- * reference operands given in `values.f32` (all fused-graph nodes, in node
- * order, as the checker computed them) and writes its own output (with canaries).
+ * The forward pass of a model request (the transformer's logits and loss) as a bundle,
+ * like step-graph: original and fused graphs (fused keeping the logits and the loss, as
+ * src/gpu/harness-m4.js:281 does), the origin map, and the inputs (parameters, batch k) as
+ * float32 arrays; with `params64`, the parameters as float64 numbers too. No GPU.
+ */
+function forwardGraph(req, dir) {
+  const { modelForward } = require('../src/builders/models');
+  const { fusedForward } = require('../src/mi355x/trainer');
+  const m = modelForward(req);
+  const ff = fusedForward(m.fwd);
+  const bundle = new Bundle(dir);
+  const b = m.batch(req.batchIndex || 0);
+  const values = Object.assign({}, m.params, { x: b.x, y: b.y });
+  const inputs = {};
+  for (const k of Object.keys(values)) inputs[k] = bundle.put(values[k]);
+  const entry = { name: req.model, graph: m.fwd.graph.toJSON(), fused: ff.graph.toJSON(), origin: ff.fusion.origin, inputs,
+    loss: m.fwd.loss, logits: m.fwd.logits, launchesFused: ff.lowered.launches.length, launchesChecked: ff.checked.launches.length,
+    launchesUnfused: lowerMI355X(m.fwd.graph).launches.length, info: m.info };
+  if (req.params64) entry.params64 = plainArrays(m.params);
+  bundle.add(entry);
+  bundle.close();
+}
+
+/**
+ * Node-local run of a model's fused step (or, with `forward`, of its fused forward pass):
+ * every launch reads the float32 reference operands given in `valuesFile` (all fused-graph
+ * nodes, in node order, as the checker computed them) and writes its own output (with
+ * canaries). The file may hold `sets` such value sets back to back (the teacher-forced
+ * check's steps, src/gpu/harness-m4.js:225-272): each is run as its own case, in order.
+ * `sabotage` plants one of the reference's kernel sabotages in both lowerings;
+ * `perf: false` runs the checked lowering alone.
  */
 async function gpuLocal(req, dir) {
-  const { modelStep } = require('../src/builders/models');
-  const { fusedStep } = require('../src/mi355x/trainer');
+  const { modelStep, modelForward } = require('../src/builders/models');
+  const { fusedStep, fusedForward } = require('../src/mi355x/trainer');
   const { HipRunner } = require('../src/mi355x/runner');
-  const m = modelStep(req);
-  const fs = fusedStep(m.step, { sabotage: req.sabotage });
+  const fs = req.forward ? fusedForward(modelForward(req).fwd, { sabotage: req.sabotage })
+    : fusedStep(modelStep(req).step, { sabotage: req.sabotage });
   const raw = fs_.readFileSync(req.valuesFile);
   const data = new Float32Array(raw.buffer, raw.byteOffset, raw.byteLength / 4);
-  const values = [];
-  let off = 0;
-  for (const node of fs.graph.nodes) {
-    const n = node.shape.reduce((a, c) => a * c, 1);
-    values.push(data.subarray(off, off + n));
-    off += n;
-  }
-  if (off !== data.length) throw new Error(`values file holds ${data.length} floats, the fused graph needs ${off}`);
+  const sets = req.sets || 1;
+  const per = fs.graph.nodes.reduce((c, node) => c + node.shape.reduce((a, d) => a * d, 1), 0);
+  if (per * sets !== data.length) throw new Error(`values file holds ${data.length} floats, ${sets} value sets of the fused graph need ${per * sets}`);
   const runner = HipRunner.create();
   const bundle = new Bundle(dir);
-  // The checked lowering (every node launched) and the trainer's perf lowering.
-  const entry = { name: req.model };
-  for (const [key, lowered] of [['gpu', fs.checked], ['gpuPerf', fs.lowered]]) {
-    const out = await runner.runLocal(fs.graph, lowered, values, { canary: true });
-    entry[key] = {};
-    for (const l of lowered.launches) entry[key][l.node] = bundle.put(out[l.node]);
-    entry[`${key}Canary`] = lowered.launches.every((l) => out.canaryIntact[l.node]);
-    entry[`${key}Launches`] = lowered.launches.length;
+  const lowerings = req.perf === false ? [['gpu', fs.checked]] : [['gpu', fs.checked], ['gpuPerf', fs.lowered]];
+  for (let s = 0; s < sets; s++) {
+    const values = [];
+    let off = s * per;
+    for (const node of fs.graph.nodes) {
+      const n = node.shape.reduce((a, c) => a * c, 1);
+      values.push(data.subarray(off, off + n));
+      off += n;
+    }
+    // The checked lowering (every node launched) and the trainer's perf lowering.
+    const entry = { name: req.model, set: s };
+    for (const [key, lowered] of lowerings) {
+      const out = await runner.runLocal(fs.graph, lowered, values, { canary: true });
+      entry[key] = {};
+      for (const l of lowered.launches) entry[key][l.node] = bundle.put(out[l.node]);
+      entry[`${key}Canary`] = lowered.launches.every((l) => out.canaryIntact[l.node]);
+      entry[`${key}Launches`] = lowered.launches.length;
+    }
+    entry.canaryIntact = lowerings.every(([key]) => entry[`${key}Canary`]);
+    entry.rowFolds = rowFoldsOf(fs.lowered);
+    entry.absorbed = absorbedOf(fs.lowered);
+    entry.loadOps = loadOpsOf(fs.lowered);
+    entry.aliases = fs.lowered.aliases;
+    entry.folded = fs.lowered.folded;
+    entry.dead = fs.lowered.dead;
+    bundle.add(entry);
+    if (sets > 1) process.stderr.write(`gpu-local: ${req.model}${req.forward ? ' forward' : ''} set ${s + 1}/${sets}\n`);
   }
-  entry.canaryIntact = entry.gpuCanary && entry.gpuPerfCanary;
-  entry.rowFolds = rowFoldsOf(fs.lowered);
-  entry.absorbed = absorbedOf(fs.lowered);
-  entry.loadOps = loadOpsOf(fs.lowered);
-  entry.aliases = fs.lowered.aliases;
-  entry.folded = fs.lowered.folded;
-  entry.dead = fs.lowered.dead;
-  bundle.add(entry);
   bundle.close({ device: runner.info() });
 }
 
@@ -1415,6 +1479,7 @@ async function main() {
     case 'precompile': out = { kernels: precompileGroup(req.group || 'direct', req.arch, req.shard, req.shards) }; break;
     case 'gpu-direct': await gpuDirect(outDir(argv), req); out = { ok: true }; break;
     case 'step-graph': stepGraph(req, outDir(argv)); out = { ok: true }; break;
+    case 'forward-graph': forwardGraph(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-local': await gpuLocal(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-workloads': await gpuWorkloads(req, outDir(argv)); out = { ok: true }; break;
     case 'gpu-step-slices': await gpuStepSlices(req, outDir(argv)); out = { ok: true }; break;

@@ -27,7 +27,7 @@ function randomTokens(B, T, V, seed) {
 
 /**
  * { step, params, state, batch(k) -> {x, y}, info } for a model request
- * { model, B?, V?, seed?, cfg? (overrides of the transformer config) }.
+ * { model, B?, V?, seed?, cfg? (overrides of the transformer config), firstBatch?, batches? }.
  */
 function modelStep(req) {
   const model = req.model || 'mlp';
@@ -55,11 +55,32 @@ function modelStep(req) {
     const shapes = {};
     for (const [n, s] of spec) shapes[n] = s;
     const state = tf.adamInitialState(step.names, shapes);
-    const batch = (k) => (req.firstBatch && !k ? tf.encodeBatch(req.firstBatch, V, cfg.T)
-      : tf.encodeBatch(randomTokens(B, cfg.T, V, seed * 1000 + (k || 0)), V, cfg.T));
+    // `batches`: every step's sequences given (a golden run's schedule); else `firstBatch`
+    // for step 0 and seeded random tokens after.
+    const batch = (k) => (req.batches ? tf.encodeBatch(req.batches[(k || 0) % req.batches.length], V, cfg.T)
+      : req.firstBatch && !k ? tf.encodeBatch(req.firstBatch, V, cfg.T)
+        : tf.encodeBatch(randomTokens(B, cfg.T, V, seed * 1000 + (k || 0)), V, cfg.T));
     return { step, params, state, batch, info: { config: 'reference transformer', V, B, cfg } };
   }
   throw new Error(`unknown model '${model}'`);
 }
 
-module.exports = { modelStep, randomTokens, C5_LR };
+/**
+ * { fwd, params, batch(k) -> {x, y}, info } for a forward-pass request { model, B?, V?, seed?,
+ * firstBatch? }: the transformer's forward graph (logits and loss from the parameters) with
+ * the same parameters and batches as modelStep's.
+ */
+function modelForward(req) {
+  const model = req.model || 'transformer-ref';
+  if (model !== 'transformer' && model !== 'transformer-ref') throw new Error(`no forward pass for model '${model}'`);
+  const ref = model === 'transformer-ref';
+  const cfg = Object.assign({}, ref ? tf.REFERENCE_CONFIG : tf.C5_CONFIG, req.cfg || {});
+  const V = req.V || (ref ? 16 : 96), B = req.B || (ref ? 4 : 64), seed = req.seed || (ref ? 1 : 0);
+  const fwd = tf.buildForward(V, B, cfg);
+  const params = ref ? tf.initParams(V, seed, cfg) : tf.initNormal(V, seed, 0.02, cfg);
+  const batch = (k) => (req.firstBatch && !k ? tf.encodeBatch(req.firstBatch, V, cfg.T)
+    : tf.encodeBatch(randomTokens(B, cfg.T, V, seed * 1000 + (k || 0)), V, cfg.T));
+  return { fwd, params, batch, info: { config: ref ? 'reference transformer' : 'C5', V, B, cfg } };
+}
+
+module.exports = { modelStep, modelForward, randomTokens, C5_LR };

@@ -7,6 +7,7 @@
 //   HipRunner.create(); runner.run(...)         for GpuRunner.create / run
 //   runner.runLocal(graph, lowered, values)     for harness-m3b.js runLocal
 //   fusedStep(step); new HipTrainer(...)        for fusedStep / FusedTrainer
+//   fusedForward(fwd)                           for harness-m4.js's fuse + lowerFused of a forward pass
 //   new HipBench(runner); bench.time(...)       for Bench.time; verdict, summarize
 // and this backend's own additions: fuseAttention(fused, { keep }) (attention
 // as one fused node, after the reference's fuse) and planArena (the liveness
@@ -16,10 +17,10 @@
 
 const { lowerMI355X, kernelSources } = require('./lower');
 const { HipRunner, Program, precompile } = require('./runner');
-const { fusedStep, HipTrainer } = require('./trainer');
+const { fusedStep, fusedForward, HipTrainer } = require('./trainer');
 const { HipBench, summarize, verdict } = require('./bench');
 const { fuseAttention } = require('../fusion/attention');
 const { planArena } = require('./arena');
 
-module.exports = { lowerMI355X, kernelSources, HipRunner, Program, precompile, fusedStep, HipTrainer, HipBench, summarize, verdict,
+module.exports = { lowerMI355X, kernelSources, HipRunner, Program, precompile, fusedStep, fusedForward, HipTrainer, HipBench, summarize, verdict,
   fuseAttention, planArena };

@@ -33,9 +33,10 @@ const { lowerMI355X } = require('./lower');
  * transpose(matmul(transpose(q), dS)), is one: the key gradient then has the query
  * gradient's layout, so the same kernels (and batches) read both. `origin` (the fusion's
  * map of each node to the original node holding its value) marks the new transpose -1:
- * no original node holds transpose(B). Returns the count.
+ * no original node holds transpose(B), and `index` (original id -> fused id) drops the
+ * product's entry, since no node holds the product itself any more. Returns the count.
  */
-function formTransposedProducts(graph, keep, origin) {
+function formTransposedProducts(graph, keep, origin, index) {
   const readers = graph.nodes.map(() => 0);
   for (const n of graph.nodes) for (const i of n.inputs) readers[i]++;
   const swapsLast = (n) => n.op === 'transpose' && n.attrs.perm.every((p, d) => {
@@ -53,6 +54,7 @@ function formTransposedProducts(graph, keep, origin) {
     graph.nodes[x.id] = { id: x.id, op: 'transpose', inputs: [b.id], attrs: { perm: t.attrs.perm.slice() }, shape: bt };
     graph.nodes[t.id] = { id: t.id, op: 'matmul', inputs: [x.id, a.inputs[0]], attrs: {}, shape: t.shape.slice() };
     readers[b.id]++;
+    if (index && origin && origin[x.id] >= 0 && index.get(origin[x.id]) === x.id) index.delete(origin[x.id]);
     if (origin) origin[x.id] = -1;
     count++;
   }
@@ -70,7 +72,7 @@ function fusedStep(step, options) {
   const o = options || {};
   const keep = [step.loss, step.logits].concat(Object.values(step.outputs));
   const f = fuse(step.graph, { keep, sabotage: o.passSabotage });
-  formTransposedProducts(f.graph, new Set(keep.map((id) => f.index.get(id))), f.origin);
+  formTransposedProducts(f.graph, new Set(keep.map((id) => f.index.get(id))), f.origin, f.index);
   const at = (id) => f.index.get(id);
   const remap = (m) => { const r = {}; for (const k of Object.keys(m)) r[k] = at(m[k]); return r; };
   const checked = lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning });
@@ -83,6 +85,23 @@ function fusedStep(step, options) {
     inputs: remap(step.inputs), outputs: remap(step.outputs),
     lowered, checked,
   });
+}
+
+/**
+ * Fuse and lower a forward pass ({ graph, logits, loss } from a builder) keeping the logits
+ * and the loss, as the reference's fused forward check does (src/gpu/harness-m4.js:281-289:
+ * fuse(f.graph, { keep: [f.logits, f.loss] }) then lowerFused). `checked` is the plain
+ * lowering (one launch per node), `lowered` the perf lowering with those two kept.
+ */
+function fusedForward(fwd, options) {
+  const o = options || {};
+  const keep = [fwd.logits, fwd.loss];
+  const f = fuse(fwd.graph, { keep, sabotage: o.passSabotage });
+  const at = (id) => f.index.get(id);
+  const checked = lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning });
+  const lowered = o.perf === false ? checked
+    : lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning, perf: true, keep: keep.map(at), absorb: true });
+  return { graph: f.graph, fusion: f, original: fwd.graph, logits: at(fwd.logits), loss: at(fwd.loss), lowered, checked };
 }
 
 class HipTrainer {
@@ -179,4 +198,4 @@ class HipTrainer {
   }
 }
 
-module.exports = { fusedStep, HipTrainer, formTransposedProducts };
+module.exports = { fusedStep, fusedForward, HipTrainer, formTransposedProducts };

@@ -19,6 +19,15 @@ test reads the reference at run time.
                       golden/spec-m3b.json golden-seed1 (V, batch, seed, initSha,
                       the four token sequences of its first batch) and
                       golden/torch-m3b.f64's init logits, loss and gradients
+  transformer_golden.json + transformer_golden.f64
+                      the four golden training runs of golden/spec-m3b.json
+                      (seed, V, batch, steps, initSha, the 20-step batch
+                      schedule, the optimizer, the projection count and its
+                      sha256, and the 512 synthetic training sequences the
+                      schedules index) with golden/torch-m3b.json's per-step
+                      training losses and parameter projections, its initial
+                      loss per run, and from golden/torch-m3b.f64 each run's
+                      initial logits and golden-seed1's final parameters
 """
 import json
 import pathlib
@@ -86,6 +95,40 @@ def main(ref_root: str) -> None:
             "loss": init["loss"], "tensors": tensors}
     (HERE / "transformer_init.json").write_text(json.dumps(meta))
     (HERE / "transformer_init.f64").write_bytes(bytes(data))
+
+    golden_runs(spec, tm, blob, index)
+
+
+def golden_runs(spec, tm, blob, index) -> None:
+    """The four golden training runs: what the teacher-forced, forward and trajectory
+    checks need, as data (golden/spec-m3b.json, golden/torch-m3b.json and .f64)."""
+    tensors, data = {}, bytearray()
+
+    def take(key, name):
+        off, n = index[key]
+        tensors[name] = [len(data) // 8, n]
+        data.extend(blob[off * 8: (off + n) * 8])
+
+    runs = []
+    inits = {i["name"]: i["loss"] for i in tm["init"]}
+    training = {t["name"]: t for t in tm["training"]}
+    for g in spec["golden"]:
+        t = training[g["name"]]
+        take(f"init/{g['name']}/logits", f"init/{g['name']}/logits")
+        runs.append({k: g[k] for k in ("name", "seed", "V", "batch", "steps", "initSha", "schedule")}
+                    | {"initLoss": inits[g["name"]], "losses": t["losses"], "projections": t["projections"]})
+    first = spec["golden"][0]["name"]
+    for p in spec["paramOrder"]:
+        take(f"train/{first}/final/{p['name']}", f"final/{first}/{p['name']}")
+    syn = spec["synthetic"]
+    meta = {"source": "golden/spec-m3b.json golden[0..3] + synthetic.train, golden/torch-m3b.json init/training, "
+                      "golden/torch-m3b.f64 init logits and golden-seed1's final parameters",
+            "config": spec["config"], "optimizer": spec["optimizer"], "paramOrder": spec["paramOrder"],
+            "projections": spec["projections"],
+            "synthetic": {k: syn[k] for k in ("seed", "vocab", "period")} | {"train": syn["train"]},
+            "golden": runs, "tensors": tensors}
+    (HERE / "transformer_golden.json").write_text(json.dumps(meta))
+    (HERE / "transformer_golden.f64").write_bytes(bytes(data))
 
 
 if __name__ == "__main__":

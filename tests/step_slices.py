@@ -264,3 +264,49 @@ def expectations(full, twin, launched, operand, sequences, row_folds=None, absor
         else:
             v, e = local(full, node, [operand(i, None) for i in ins])
             yield nid, None, v, e
+
+
+def judge_case(fused, fused_vals, gc, arr):
+    """Node-local judgement of one gpu-local case (tool.js gpuLocal): every launch of the
+    checked lowering against its float64 expectation on the reference operands
+    `fused_vals` (localReferenceFused + judgeLocal, harness-m4.js:182-223), and, where the
+    case holds it, every launch of the perf lowering — whose skipped nodes must be exactly
+    its shared reshapes, in-place transposes and broadcasts, folded reductions and
+    producers, relus applied on load and dead nodes, and whose folded launches are judged
+    as the launches they are. `arr` reads a bundle array. Returns (checked, perf or None)."""
+    expected, bound = bounds.local_reference_fused(fused, fused_vals)
+    gpu = {int(k): arr(v) for k, v in gc["gpu"].items()}
+    assert set(gpu) == set(expected)
+    j = bounds.judge_local(fused, gpu, expected, bound)
+    if "gpuPerf" not in gc:
+        return j, None
+    perf = {int(k): arr(v) for k, v in gc["gpuPerf"].items()}
+    skipped = set(expected) - set(perf)
+    assert skipped == {a for a, _ in gc["aliases"]} | set(gc["folded"]) | set(gc["dead"])
+    # Reductions folded into their row-statistics chains, and the producers of their
+    # operands formed in the same launches, are the other launches it skips.
+    folds = {int(k): v for k, v in gc["rowFolds"].items()}
+    took = {int(k): v for k, v in gc["absorbed"].items()}
+    reductions = {f["reduction"] for fs in folds.values() for f in fs}
+    producers = {f["producer"] for fs in folds.values() for f in fs if "producer" in f}
+    producers |= absorbed_producers(took)
+    # Relus the matmuls reading them apply as they load their operand.
+    on_load = {o["node"] for ops in gc["loadOps"].values() for o in ops}
+    nodes = fused["nodes"]
+    assert all(nodes[i]["op"] == "relu" for i in on_load)
+    assert all(nodes[i]["op"] in ("reshape", "transpose", "broadcast")
+               for i in skipped - set(gc["dead"]) - reductions - producers - on_load)
+    assert all(nodes[i]["op"] in ("sum", "max") for i in reductions)
+    assert all(nodes[i]["op"] not in ("sum", "max", "matmul") for i in producers)
+    # A chain with its reductions folded in is judged as the launch it is: the reductions and
+    # the chain on the reductions' operands.
+    pexp, pbound = {}, {}
+    for k in perf:
+        if k in folds or k in took:
+            node, ins = restate(fused, k, folds.get(k), took.get(k))
+            pexp[k], pbound[k] = local(fused, node, [fused_vals[i] for i in ins])
+        else:
+            pexp[k], pbound[k] = expected[k], bound[k]
+    jp = bounds.judge_local(fused, perf, pexp, pbound)
+    jp["skipped"], jp["chains"] = len(skipped), len(folds)
+    return j, jp

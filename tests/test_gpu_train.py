@@ -13,7 +13,7 @@ import pytest
 
 from conftest import GOLDEN
 from oracle import bounds
-from step_slices import absorbed_producers, fused_values, local, restate
+from step_slices import fused_values, judge_case
 
 pytestmark = pytest.mark.gpu
 
@@ -33,47 +33,17 @@ def node_local(tool, tmp_path, req):
     tool("gpu-local", dict(req, valuesFile=str(tmp_path / "values.f32")), out=str(out), timeout=600)
     g = tcmi_bridge.Bundle(out)
     gc = g.cases[0]
-    expected, bound = bounds.local_reference_fused(c["fused"], fused_vals)
-    gpu = {int(k): g.arr(v) for k, v in gc["gpu"].items()}
-    assert set(gpu) == set(expected)
-    j = bounds.judge_local(c["fused"], gpu, expected, bound)
+    assert gc["canaryIntact"]
+    j, jp = judge_case(c["fused"], fused_vals, gc, g.arr)
     print(f"{req['model']}: node-local worst {j['worst']:.3g} over {j['elements']} elements, "
           f"unjudgeable {j['unjudgeable']}, by kind {j['byKind']}", file=sys.stderr)
-    assert gc["canaryIntact"]
     assert j["pass"], (j["first"], j["unjudged"])
     # The perf lowering: every node it launches (all but the shared reshapes, the
     # transposes its matmuls read in place, the broadcasts its consumers read through
     # their index maps, and the dead nodes no kept value depends on), on the same
     # reference operands.
-    perf = {int(k): g.arr(v) for k, v in gc["gpuPerf"].items()}
-    skipped = set(expected) - set(perf)
-    assert skipped == {a for a, _ in gc["aliases"]} | set(gc["folded"]) | set(gc["dead"])
-    # Reductions folded into their row-statistics chains, and the producers of their
-    # operands formed in the same launches, are the other launches it skips.
-    folds = {int(k): v for k, v in gc["rowFolds"].items()}
-    took = {int(k): v for k, v in gc["absorbed"].items()}
-    reductions = {f["reduction"] for fs in folds.values() for f in fs}
-    producers = {f["producer"] for fs in folds.values() for f in fs if "producer" in f}
-    producers |= absorbed_producers(took)
-    # Relus the matmuls reading them apply as they load their operand.
-    on_load = {o["node"] for ops in gc["loadOps"].values() for o in ops}
-    assert all(c["fused"]["nodes"][i]["op"] == "relu" for i in on_load)
-    assert all(c["fused"]["nodes"][i]["op"] in ("reshape", "transpose", "broadcast")
-               for i in skipped - set(gc["dead"]) - reductions - producers - on_load)
-    assert all(c["fused"]["nodes"][i]["op"] in ("sum", "max") for i in reductions)
-    assert all(c["fused"]["nodes"][i]["op"] not in ("sum", "max", "matmul") for i in producers)
-    # A chain with its reductions folded in is judged as the launch it is: the reductions and
-    # the chain on the reductions' operands.
-    pexp, pbound = {}, {}
-    for k in perf:
-        if k in folds or k in took:
-            node, ins = restate(c["fused"], k, folds.get(k), took.get(k))
-            pexp[k], pbound[k] = local(c["fused"], node, [fused_vals[i] for i in ins])
-        else:
-            pexp[k], pbound[k] = expected[k], bound[k]
-    jp = bounds.judge_local(c["fused"], perf, pexp, pbound)
     print(f"{req['model']}: perf lowering node-local worst {jp['worst']:.3g} over {jp['elements']} elements, "
-          f"{len(skipped)} nodes shared or folded, {len(folds)} chains with their reductions", file=sys.stderr)
+          f"{jp['skipped']} nodes shared or folded, {jp['chains']} chains with their reductions", file=sys.stderr)
     assert jp["pass"], (jp["first"], jp["unjudged"])
     return j
 

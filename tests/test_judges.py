@@ -208,3 +208,24 @@ def test_local_reference_fused_equals_the_whole_graph_on_exact_operands(tool):
     chain = max(expected)
     assert np.all(bound[chain] > 0)
     assert f["graph"]["nodes"][chain]["attrs"]["pattern"] == "elementwise"
+
+
+def test_judge_fused_refuses_a_node_no_original_holds(tool):
+    """A fused node whose origin is -1 (the transposed operand the trainer's lowering forms
+    for a product formed transposed) has no reference value: judge_fused refuses it with
+    reason 'origin' instead of reading the last node's reference. The trainer's fused step
+    marks such nodes -1 and no longer maps the product's original id to them."""
+    import tcmi_bridge
+    import tempfile
+    with tempfile.TemporaryDirectory() as d:
+        tool("step-graph", {"model": "transformer-ref"}, out=d)
+        c = tcmi_bridge.Bundle(d).cases[0]
+    formed = [i for i, o in enumerate(c["origin"]) if o < 0]
+    assert formed and all(c["fused"]["nodes"][i]["op"] == "transpose" for i in formed)
+    g = {"nodes": [{"op": "input", "inputs": [], "attrs": {"name": "a"}, "shape": [2]},
+                   {"op": "neg", "inputs": [0], "attrs": {}, "shape": [2]}]}
+    ref = bounds.reference_with_bounds(g, {"a": [1.0, 2.0]})
+    gpu = [np.array([1.0, 2.0]), np.array([-1.0, -2.0])]
+    assert bounds.judge_fused(g, [0, 1], gpu, ref)["pass"]
+    j = bounds.judge_fused(g, [0, -1], gpu, ref)
+    assert not j["pass"] and j["first"]["reason"] == "origin" and j["first"]["node"] == 1
