@@ -125,7 +125,10 @@ int tcmi_sync(void);
  * of the argument block (the workspace pointer, at byte 72 of the TcmiArgs layout) are
  * replaced by that array's address before the launch; `scratch_bytes` is the workspace
  * the launch's kernels use, at most TCMI_SCRATCH_BYTES (else TCMI_E_INVALID, nothing
- * enqueued). Nothing is cleared: the kernels this library generates write every
+ * enqueued). The library cannot see what the kernels write: a `scratch_bytes` below the
+ * launch's real workspace is undefined behaviour (the kernels write past the array), so
+ * callers take it from the lowering's launch record (`workspace`), as the Python binding's
+ * launch_list_with_scratch does. Nothing is cleared: the kernels this library generates write every
  * workspace element before they read it. Every call on one GPU shares the array and
  * it keeps the last call's contents, so launches that use it must not overlap: they
  * do not when issued on the library stream (in order), as these are. */

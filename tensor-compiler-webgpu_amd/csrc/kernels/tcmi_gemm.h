@@ -113,15 +113,6 @@ __device__ __forceinline__ float4 vop(float4 x) {
   else return x;
 }
 
-// Sizes are compile-time constants of the generated kernel (batch, M, K, N, and
-// for SPLIT the number of K chunks and their length, a multiple of 16). The
-// workgroup's z index `zid` enumerates batches, or for SPLIT (batch, chunk)
-// pairs, and each SPLIT workgroup stores its raw
-// partial tile to the workspace at ((chunk·batch + b)·M + row)·N + col; a
-// second kernel (gemm_splitk_reduce) sums the chunks in order and applies the
-// epilogue. MODE_C needs C % 4 == 0 and MODE_R needs R % 4 == 0 (R, C: the
-// operand's extents), and both need every other stride a multiple of 4, so a
-// 128-bit load is aligned and either wholly inside the operand or wholly out.
 // A workgroup's (x, y, z) place in its launch's grid.
 struct Wg {
   uint32_t x, y, z;
@@ -143,6 +134,15 @@ __device__ __forceinline__ Wg xcd_grouped() {
   return {t % gx, t / gx, L % 8u + 8u * (rest / G)};
 }
 
+// Sizes are compile-time constants of the generated kernel (batch, M, K, N, and
+// for SPLIT the number of K chunks and their length, a multiple of 16). The
+// workgroup's z index `zid` enumerates batches, or for SPLIT (batch, chunk)
+// pairs, and each SPLIT workgroup stores its raw
+// partial tile to the workspace at ((chunk·batch + b)·M + row)·N + col; a
+// second kernel (gemm_splitk_reduce) sums the chunks in order and applies the
+// epilogue. MODE_C needs C % 4 == 0 and MODE_R needs R % 4 == 0 (R, C: the
+// operand's extents), and both need every other stride a multiple of 4, so a
+// 128-bit load is aligned and either wholly inside the operand or wholly out.
 template <int TM, int TN, int BK, int PF, int AMODE, int BMODE, bool SPLIT, class AV, class BV, class Epi, int WN = 2,
           bool PRIO = false, int KW = 1, class Args = TcmiArgs>
 __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict__ a_ptr,
@@ -487,10 +487,6 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
   }
 }
 
-// Output element j of a split-K matmul's product: its chunks' partial sums from the
-// workspace, added in chunk order — the value gemm_splitk_reduce forms for j itself.
-// An epilogue that reads the product at another element's index (a recomputed
-// broadcast or transpose of it) reads it here.
 // The tile of each workgroup at its launch place (blockIdx.x, blockIdx.y).
 template <int TM, int TN, int BK, int PF, int AMODE, int BMODE, bool SPLIT, class AV, class BV, class Epi, int WN = 2,
           bool PRIO = false, int KW = 1, class Args = TcmiArgs>
@@ -502,6 +498,10 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
                                                                                chunkK, zid, blockIdx.x, blockIdx.y);
 }
 
+// Output element j of a split-K matmul's product: its chunks' partial sums from the
+// workspace, added in chunk order — the value gemm_splitk_reduce forms for j itself.
+// An epilogue that reads the product at another element's index (a recomputed
+// broadcast or transpose of it) reads it here.
 template <class Args>
 __device__ __forceinline__ float gemm_product_at(const Args& A, uint32_t j, uint32_t total, uint32_t chunks) {
   float acc = A.ws[j];

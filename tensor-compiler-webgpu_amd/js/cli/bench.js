@@ -551,9 +551,13 @@ function trainStep(runner, bench, name, req, opts) {
   const { fusedStep, HipTrainer } = require('../src/mi355x/trainer');
   const m = modelStep(req);
   const fs = fusedStep(m.step);
-  // The unfused step in the same perf lowering the fused trainer runs.
-  const lu = lowerMI355X(m.step.graph, { perf: true, keep: [m.step.loss, m.step.logits].concat(Object.values(m.step.outputs)), rowFolds: false });
-  runner.functions([fs.lowered, lu]);
+  // The unfused step in the perf lowering (views, batching) without anything that forms
+  // one node's value inside another's launch (no folds, absorption or relus on load).
+  const lu = lowerMI355X(m.step.graph, { perf: true, keep: [m.step.loss, m.step.logits].concat(Object.values(m.step.outputs)),
+    rowFolds: false, loadOps: false });
+  // The fused step under the fusion contract alone: the same lowering of the fused graph.
+  const fsContract = fusedStep(m.step, { contract: true });
+  runner.functions([fs.lowered, lu, fsContract.lowered]);
   // 40 timed steps after 5 warm-ups: config 1's step is about 50 µs, so fewer steps would
   // time a few hundred µs of work.
   const K = Number(arg('train-steps', opts.quick ? 3 : 40)), W = opts.quick ? 2 : 5;
@@ -590,7 +594,13 @@ function trainStep(runner, bench, name, req, opts) {
   const all = Object.assign({}, m.params, m.state, { x: batch.x, y: batch.y });
   all[m.step.cotangent] = [1];
   for (const node of m.step.graph.nodes) if (node.op === 'input') pu.write(node.id, all[node.attrs.name]);
-  const t = bench.time({ fused: p, unfused: pu }, { reps: opts.quick ? 3 : 8, warmup: 2 });
+  const tc = new HipTrainer(runner, fsContract, m.params, m.state, { graph });
+  tc.train(batch.x, batch.y);
+  const t = bench.time({ fused: p, unfused: pu, contract: tc.program }, { reps: opts.quick ? 3 : 8, warmup: 2 });
+  const contract = { launches: fsContract.lowered.launches.length, dispatches: tc.program.dispatches,
+    residentMsPerStep: t.stats.contract.median / 1e3, residentStepsPerSec: 1e6 / t.stats.contract.median,
+    verdict: verdict(t.stats.unfused, t.stats.contract), fullOverContract: verdict(t.stats.contract, t.stats.fused) };
+  tc.destroy();
   // Time by kind (each launch alone), and every fusion group against its members'
   // unfused launches, each timed alone.
   const launches = timeLaunches(runner, bench, p, 3);
@@ -666,7 +676,7 @@ function trainStep(runner, bench, name, req, opts) {
   return { config: name, info: m.info, steps: K, warmup: W, lossLast: loss, arena, streams: streamRuns, graphReplay: graph,
     stepsPerSec: 1e3 / wallMs, msPerStep: wallMs, residentMsPerStep: residentMs, residentStepsPerSec: 1e3 / residentMs,
     launches: { fused: fs.lowered.launches.length, unfused: lu.launches.length },
-    dispatches: p.dispatches, batches: (fs.lowered.batches || []).length, unbatched,
+    dispatches: p.dispatches, batches: (fs.lowered.batches || []).length, unbatched, contract,
     fused: t.stats.fused, unfused: t.stats.unfused, verdict: verdict(t.stats.unfused, t.stats.fused),
     matmulFlopsPerStep: flops, matmulTflopsResident: flops / (residentMs * 1e9), byKind,
     groups: groupSummary(groupList), groupList };

@@ -1472,7 +1472,7 @@ async function main() {
       const l = lowerMI355X(g, { perf: true, keep, absorb });
       const plain = new Map(lowerMI355X(g).launches.map((x) => [x.node, x]));
       out = { graph: g.toJSON(), keep, aliases: l.aliases, folded: l.folded, dead: l.dead, rowFolds: rowFoldsOf(l), absorbed: absorbedOf(l), loadOps: loadOpsOf(l),
-        launches: l.launches.map((x) => ({ node: x.node, kind: x.kind, inputs: x.inputs, views: x.views || null, modes: gemmModes(x),
+        launches: l.launches.map((x) => ({ node: x.node, kind: x.kind, inputs: x.inputs, params: x.params.length, views: x.views || null, modes: gemmModes(x),
           split: gemmSplit(x), plainSplit: gemmSplit(plain.get(x.node)) })) };
       break;
     }

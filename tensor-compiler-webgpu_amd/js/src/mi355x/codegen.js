@@ -94,6 +94,11 @@ function gatherStrides(node, inShape) {
  * loads of operands and the values of nodes it treats specially (the matmul
  * root of an epilogue, the reductions of a rowwise body).
  */
+/** A kernel whose parameter words (its sizes and index maps) would not fit one argument block. */
+class ParamOverflow extends Error {
+  constructor(message) { super(message); this.name = 'ParamOverflow'; }
+}
+
 class Emitter {
   constructor(body, params, hooks, slack) {
     this.b = body;
@@ -136,7 +141,7 @@ class Emitter {
         this.params.push(rank);
         for (let d = rank - 1; d >= 0; d--) this.params.push(g.extents[d], g.strides[d]);
       }
-      if (this.params.length > MAX_P) throw new Error(`kernel parameters exceed ${MAX_P} words`);
+      if (this.params.length > MAX_P) throw new ParamOverflow(`kernel parameters exceed ${MAX_P} words`);
       this.gatherBase.set(key, base);
     }
     // The index maps are baked into the kernel text as constants (the lowering
@@ -608,7 +613,9 @@ function colreduceKernels(op, outer, n, inner, tuning, producer) {
   // 4-column group), through the same emitter and op helpers as an elementwise kernel, so
   // the same bits as reading the producer's output. Operands of the full size load a
   // 4-column group at once; others (broadcast rows or columns) load at their index map.
-  const pparams = [];
+  // The launch's parameter words are these five, then the producer's gather maps: the
+  // emitter starts on them, so its word limit and the offsets it records count them.
+  const pparams = [outer, n, inner, splits, chunk];
   let formed = '';
   if (producer) {
     if (outer * n * inner >= 2 ** 32) throw new Error('column reduction with a producer: operand past 2^32 elements');
@@ -694,7 +701,7 @@ ${producer ? formed : `      const ${T} v = ${ld('x', '(size_t)k * inner + j')};
     const k2 = kernelText('colfin', second);
     launches.push({ name: k2.name, source: k2.source, grid: [Math.ceil(inner / (W * groupsPerBlock)), outer, 1], block: [256, 1, 1], lds: 0 });
   }
-  return { launches, params: Uint32Array.from([outer, n, inner, splits, chunk, ...pparams]), workspace: splits > 1 ? outer * splits * inner * 4 : 0 };
+  return { launches, params: Uint32Array.from(pparams), workspace: splits > 1 ? outer * splits * inner * 4 : 0 };
 }
 
 // ---- matmul with epilogue ----------------------------------------------------------------
@@ -1240,4 +1247,4 @@ function batchedKernel(members, count) {
 }
 
 module.exports = { elementwiseKernel, rowwiseKernel, colreduceKernels, gemmKernel, gemmTiling, attentionKernel, classifyGather, gatherStrides,
-  literal, fnv, Emitter, WG, MAX_P, MAX_IN, MAX_BATCH, batchable, batchedKernel, batchFamily };
+  literal, fnv, Emitter, ParamOverflow, WG, MAX_P, MAX_IN, MAX_BATCH, batchable, batchedKernel, batchFamily };

@@ -227,7 +227,7 @@ function matmulSlots(n) {
  * such sinks, e.g. the gradient flowing into the max shift's stopGradient, or the dX of a
  * one-hot input): no launch, no buffer. Inputs and constants are never dead.
  */
-function perfPlan(graph, keep, rowFolding, absorbing, loadOps) {
+function perfPlan(graph, keep, rowFolding, absorbing, loadOps, noAbsorb) {
   const cons = consumersOf(graph);
   const live = new Set();
   for (let id = graph.nodes.length - 1; id >= 0; id--) {
@@ -414,6 +414,7 @@ function perfPlan(graph, keep, rowFolding, absorbing, loadOps) {
       const reduction = isRowReduction(e);
       const columns = isColReduction(e);
       if (!(isElementwise(e) || reduction || columns) || folded.has(e.id) || dead.has(e.id) || aliases.has(e.id) || rowFolds.has(e.id)) continue;
+      if (noAbsorb && noAbsorb.has(e.id)) continue;
       const own = broadcasts.get(e.id);
       let next = e.inputs.length;
       const list = [];
@@ -734,8 +735,22 @@ const STREAM_FROM = 1 << 20;
 function lowerMI355X(graph, options) {
   const opts = options || {};
   if (opts.perf && !opts.keep) throw new Error('the perf lowering needs `keep`: the nodes whose values are read');
+  // A launch that takes producers in, with their index maps, may need more parameter words
+  // than its argument block holds: its reader then takes none in, and the plan is made again.
+  const noAbsorb = new Set();
+  for (;;) {
+    try {
+      return lowerOnce(graph, opts, noAbsorb);
+    } catch (e) {
+      if (!(e instanceof cg.ParamOverflow) || e.reader === undefined || noAbsorb.has(e.reader)) throw e;
+      noAbsorb.add(e.reader);
+    }
+  }
+}
+
+function lowerOnce(graph, opts, noAbsorb) {
   const plan = opts.perf ? perfPlan(graph, new Set(opts.keep), opts.rowFolds !== false, opts.absorb === true && opts.rowFolds !== false,
-    opts.loadOps !== false)
+    opts.loadOps !== false, noAbsorb)
     : { aliases: new Map(), folded: new Set(), views: new Map(), broadcasts: new Map(), dead: new Set(), rowFolds: new Map(), absorbed: new Map() };
   const cache = new Map();
   const launches = [];
@@ -830,7 +845,15 @@ function lowerMI355X(graph, options) {
     const key = JSON.stringify([node.op, node.inputs.map((id) => graph.nodes[id].shape), node.attrs, node.shape,
       node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey, rowKey, lastReads, peers, absorbKey]);
     let k = cache.get(key);
-    if (!k) { k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs); cache.set(key, k); }
+    if (!k) {
+      try {
+        k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs);
+      } catch (e) {
+        if (e instanceof cg.ParamOverflow && absorbs) e.reader = node.id;
+        throw e;
+      }
+      cache.set(key, k);
+    }
     workspace = Math.max(workspace, k.workspace);
     launches.push({
       node: node.id, op: node.op, kind: k.kind, pattern: node.op === 'fused' ? node.attrs.pattern : undefined,

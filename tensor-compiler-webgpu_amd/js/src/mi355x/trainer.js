@@ -66,7 +66,9 @@ function formTransposedProducts(graph, keep, origin, index) {
  * `lowered` is the perf lowering the trainer runs (reshapes share buffers,
  * transposes read in place by their matmuls; `perf: false` turns it off);
  * `checked` is the plain lowering, one launch per node, for node-by-node checks. Both
- * lower the fused graph with its transposed products formed transposed (above).
+ * lower the fused graph with its transposed products formed transposed (above). With
+ * `contract`, the perf lowering adds nothing to the fusion contract's partition beyond
+ * views and batching: no row folds, no absorbed producers, no relus applied on load.
  */
 function fusedStep(step, options) {
   const o = options || {};
@@ -77,8 +79,10 @@ function fusedStep(step, options) {
   const remap = (m) => { const r = {}; for (const k of Object.keys(m)) r[k] = at(m[k]); return r; };
   const checked = lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning });
   const lowered = o.perf === false ? checked
-    : lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning, perf: true, keep: keep.map(at), batch: o.batch, absorb: true,
-      loadOps: o.loadOps });
+    : o.contract ? lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning, perf: true, keep: keep.map(at), batch: o.batch,
+      rowFolds: false, absorb: false, loadOps: false })
+      : lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning, perf: true, keep: keep.map(at), batch: o.batch, absorb: true,
+        loadOps: o.loadOps });
   return Object.assign({}, step, {
     graph: f.graph, fusion: f, original: step.graph,
     loss: at(step.loss), logits: at(step.logits),

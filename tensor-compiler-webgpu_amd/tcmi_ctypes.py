@@ -105,3 +105,28 @@ class Tcmi:
 
 def load(path: pathlib.Path = LIB_PATH) -> Tcmi:
     return Tcmi(path)
+
+
+TCMI_SCRATCH_BYTES = 64 << 20             # include/tcmi.h
+WORKSPACE_SLOT = 8 * 8 + 8                # byte offset of the workspace pointer in a TcmiArgs block
+
+
+def launch_list_with_scratch(t: Tcmi, items) -> None:
+    """Issue lowered launches with the library's device scratch as their workspace
+    (tcmi_launch_scratch). `items` is [(functions, launch, args, args_bytes)]: a launch
+    record from the lowering (its `kernels`, each with grid, block and lds, and its
+    `workspace` in bytes), the module function of each of its kernels, and its packed
+    argument block. The scratch size given to the library is each record's own workspace,
+    never a caller's figure (an under-stated size would let the kernels write past the
+    array); a list any launch of which needs more than TCMI_SCRATCH_BYTES is refused before
+    any kernel is enqueued."""
+    items = list(items)
+    for _, launch, _, _ in items:
+        need = int(launch["workspace"])
+        if need > TCMI_SCRATCH_BYTES:
+            raise TcmiError(f"launch of {launch['kernels'][0]['name']} needs {need} bytes of workspace, "
+                            f"the library's scratch holds {TCMI_SCRATCH_BYTES}: nothing launched")
+    for functions, launch, args, args_bytes in items:
+        for f, k in zip(functions, launch["kernels"]):
+            t.launch_scratch(f, (u32 * 3)(*k["grid"]), (u32 * 3)(*k["block"]), k["lds"], args, args_bytes,
+                             WORKSPACE_SLOT, int(launch["workspace"]))

@@ -81,3 +81,29 @@ def test_kernel_headers_compile_for_gfx950_offline(tool):
     """The skeletons compile with hiprtc for gfx950 (no GPU): every direct case's kernels as one module."""
     out = tool("precompile", {"group": "direct", "arch": "gfx950"})
     assert out["kernels"] > 30
+
+
+def test_scratch_launches_take_their_size_from_the_lowering(tool):
+    """launch_list_with_scratch (the Python binding of tcmi_launch_scratch) gives the library
+    each launch record's own workspace as the scratch size, and refuses a launch list any
+    launch of which needs more than the library's 64 MiB before any kernel is enqueued
+    (a stand-in library records the calls; nothing reaches a GPU)."""
+    import tcmi_ctypes
+    calls = []
+
+    class Stub:
+        def launch_scratch(self, *args):
+            calls.append(args)
+
+    d = tool("scratch-kernels")
+    launches = d["launches"]
+    assert all(0 < launch["workspace"] <= tcmi_ctypes.TCMI_SCRATCH_BYTES for launch in launches)
+    items = [([11, 12], launch, 0, 272) for launch in launches]
+    tcmi_ctypes.launch_list_with_scratch(Stub(), items)
+    assert [c[-1] for c in calls] == [launch["workspace"] for launch in launches for _ in launch["kernels"]]
+    assert all(c[-2] == tcmi_ctypes.WORKSPACE_SLOT for c in calls)
+    calls.clear()
+    big = dict(launches[1], workspace=tcmi_ctypes.TCMI_SCRATCH_BYTES + 4)
+    with pytest.raises(tcmi_ctypes.TcmiError, match="nothing launched"):
+        tcmi_ctypes.launch_list_with_scratch(Stub(), items[:1] + [([11, 12], big, 0, 272)])
+    assert calls == []

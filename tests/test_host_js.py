@@ -382,6 +382,34 @@ def test_row_fold_takes_in_a_producer_only_with_a_full_size_body(tool):
         assert (producer in [l["node"] for l in d["launches"]]) == recompute
 
 
+def test_column_reduction_takes_in_a_producer_only_where_its_maps_fit(tool):
+    """A column reduction forms its operand's producer in place (the trainer's lowering),
+    the producer's index maps appended to the launch's five size words. With four
+    transposed rank-4 operands the maps fit one argument block (41 of 48 words) and the
+    producer is taken in; with five (50 words) it is not: the producer stays a launch of
+    its own and the reduction reads its value. Counting only the producer's words would
+    pass the second at lowering and fail it at launch."""
+    def graph(k):
+        nodes, acc = [], None
+        for j in range(k):
+            nodes.append({"op": "input", "inputs": [], "attrs": {"name": f"x{j}", "shape": [2, 3, 4, 8]}, "shape": [2, 3, 4, 8]})
+            nodes.append({"op": "transpose", "inputs": [len(nodes) - 1], "attrs": {"perm": [3, 2, 1, 0]}, "shape": [8, 4, 3, 2]})
+            t = len(nodes) - 1
+            if acc is not None:
+                nodes.append({"op": "add", "inputs": [acc, t], "attrs": {}, "shape": [8, 4, 3, 2]})
+                t = len(nodes) - 1
+            acc = t
+        nodes.append({"op": "sum", "inputs": [acc], "attrs": {"axis": 0}, "shape": [4, 3, 2]})
+        return {"nodes": nodes}, len(nodes) - 1
+    for k, taken in ((4, True), (5, False)):
+        g, s = graph(k)
+        d = tool("perf-lower", {"graph": g, "keep": [s], "fuse": {}, "absorb": True})
+        kinds = [x["kind"] for x in d["launches"]]
+        assert ("fused-elementwise" not in kinds) == taken, kinds
+        assert bool(d["absorbed"]) == taken
+        assert all(x["params"] <= 48 for x in d["launches"])
+
+
 def _product_shape(nodes, n):
     """(batch dims, M, K, N) of a plain matmul node or of an epilogue group's matmul, or None."""
     if n["op"] == "matmul":

@@ -75,10 +75,8 @@ def test_scratch_launch_gives_the_workspace_launch_bits(tool):
             # The same kernels with the library's scratch as the workspace: no allocation.
             t.counters(counters, 7)
             before = counters[MALLOC]
-            for f, k in zip(fns, launch["kernels"]):
-                a = pack([hx, hw], y_scr, 0, launch["params"])
-                t.launch_scratch(f, (u32 * 3)(*k["grid"]), (u32 * 3)(*k["block"]), k["lds"], a.ctypes.data, ARG_BYTES,
-                                 WS_SLOT, launch["workspace"])
+            a = pack([hx, hw], y_scr, 0, launch["params"])
+            tcmi_ctypes.launch_list_with_scratch(t, [(fns, launch, a.ctypes.data, ARG_BYTES)])
             t.sync()
             t.counters(counters, 7)
             assert counters[MALLOC] == before
