@@ -406,14 +406,23 @@ function rowwiseKernel(b, output, opts) {
   const rowTier = (id) => size(b.nodes[id].shape) === R && size(b.nodes[id].shape) !== R * C;
   const outRow = rowTier(output) || (R === size(b.nodes[output].shape) && C !== 1 && size(b.nodes[output].shape) !== R * C);
 
-  // Loads at the element index: cached per load site in registers.
-  const cacheDecl = [];   // declarations + fill loops before the phases
+  // Loads at the element index: cached per load site in registers. `fills` keeps
+  // each cache's kind in first-use order; the kernel text declares and fills them.
+  const fills = [];
   const caches = new Map();
   const reduced = new Map();
   const rowLines = [];    // row-tier statements, emitted as they are first needed
   let em;
   const ROW = { key: 'r', idx: 'r', root: false, row: true, limit: R };
   const elemCtx = () => ({ key: 'e', idx: 'e', root: true, limit: R * C });
+  const cache = (ck, k, mode) => {
+    if (!caches.has(ck)) {
+      const c = `X${caches.size}`;
+      caches.set(ck, c);
+      fills.push({ c, k, mode });
+    }
+    return caches.get(ck);
+  };
 
   const hooks = {
     special(id, ctx, lines) {
@@ -434,51 +443,38 @@ function rowwiseKernel(b, output, opts) {
         return v;
       }
       if (ctx.root) {
-        const ck = `full${k}`;
-        if (!caches.has(ck)) {
-          const c = `X${caches.size}`;
-          caches.set(ck, c);
-          if (vec && streamed.has(k)) {
-            // The lowering's last read of this buffer: streamed past the caches.
-            cacheDecl.push(`float4 ${c}[${E}];`,
-              `#pragma unroll`,
-              `for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = (ln + s * ${T}u) * 4u;`,
-              `  tcmi::f4 t = {0.f, 0.f, 0.f, 0.f};`,
-              `  if (c0 < C) t = __builtin_nontemporal_load(reinterpret_cast<const tcmi::f4*>(A.in[${k}] + rowBase) + (c0 >> 2));`,
-              `  ${c}[s] = make_float4(t[0], t[1], t[2], t[3]); }`);
-          } else if (vec) {
-            cacheDecl.push(`float4 ${c}[${E}];`,
-              `#pragma unroll`,
-              `for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = (ln + s * ${T}u) * 4u;`,
-              `  ${c}[s] = c0 < C ? reinterpret_cast<const float4*>(A.in[${k}] + rowBase)[c0 >> 2] : make_float4(0.f, 0.f, 0.f, 0.f); }`);
-          } else {
-            cacheDecl.push(`float ${c}[${E}];`,
-              `#pragma unroll`,
-              `for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = ln + s * ${T}u;`,
-              `  ${c}[s] = c0 < C ? A.in[${k}][rowBase + c0] : 0.f; }`);
-          }
-        }
-        return vec ? `tcmi::lane4(${caches.get(ck)}[s], l)` : `${caches.get(ck)}[s]`;
+        // The lowering's last read of a buffer is streamed past the caches.
+        const c = cache(`full${k}`, k, !vec ? 'scalar' : streamed.has(k) ? 'nt' : 'vec');
+        return vec ? `tcmi::lane4(${c}[s], l)` : `${c}[s]`;
       }
       const g = ctx.gather;
       if (vec && ctx.parent && ctx.parent.root && g && g.g.mode === 'span' && g.g.inner === 1 && g.g.extent === C) {
         // A per-column vector (LayerNorm gain/bias): cached like a full operand.
-        const ck = `col${k}`;
-        if (!caches.has(ck)) {
-          const c = `X${caches.size}`;
-          caches.set(ck, c);
-          cacheDecl.push(`float4 ${c}[${E}];`,
-            `#pragma unroll`,
-            `for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = (ln + s * ${T}u) * 4u;`,
-            `  ${c}[s] = c0 < C ? reinterpret_cast<const float4*>(A.in[${k}])[c0 >> 2] : make_float4(0.f, 0.f, 0.f, 0.f); }`);
-        }
-        return `tcmi::lane4(${caches.get(ck)}[s], l)`;
+        return `tcmi::lane4(${cache(`col${k}`, k, 'col')}[s], l)`;
       }
       const v = `L${lines.length}_${k}`;
       lines.push(`const float ${v} = A.in[${k}][${ctx.idx}];`);
       return v;
     },
   };
+  // The lines filling cache `f` into array `dst` from the row at `rowBase`.
+  const fillLines = (f, dst) => {
+    const head = [`#pragma unroll`];
+    if (f.mode === 'nt') {
+      return head.concat([`for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = (ln + s * ${T}u) * 4u;`,
+        `  tcmi::f4 t = {0.f, 0.f, 0.f, 0.f};`,
+        `  if (c0 < C) t = __builtin_nontemporal_load(reinterpret_cast<const tcmi::f4*>(A.in[${f.k}] + rowBase) + (c0 >> 2));`,
+        `  ${dst}[s] = make_float4(t[0], t[1], t[2], t[3]); }`]);
+    }
+    if (f.mode === 'vec' || f.mode === 'col') {
+      const src = f.mode === 'col' ? `A.in[${f.k}]` : `A.in[${f.k}] + rowBase`;
+      return head.concat([`for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = (ln + s * ${T}u) * 4u;`,
+        `  ${dst}[s] = c0 < C ? reinterpret_cast<const float4*>(${src})[c0 >> 2] : make_float4(0.f, 0.f, 0.f, 0.f); }`]);
+    }
+    return head.concat([`for (int s = 0; s < ${E}; ++s) { const uint32_t c0 = ln + s * ${T}u;`,
+      `  ${dst}[s] = c0 < C ? A.in[${f.k}][rowBase + c0] : 0.f; }`]);
+  };
+  const cacheType = (f) => (f.mode === 'scalar' ? 'float' : 'float4');
   em = new Emitter(b, params, hooks);
 
   // One element loop: `body` runs for every valid element with `e` its flat index.
@@ -556,6 +552,8 @@ ${indent(inner, '      ')}
       store = [...pre, loop(inner.concat([`A.out[e] = ${v};`]))];
     }
   }
+  const cacheDecl = [];
+  for (const f of fills) cacheDecl.push(`${cacheType(f)} ${f.c}[${E}];`, ...fillLines(f, f.c));
   const text = `extern "C" __global__ void __launch_bounds__(${BLOCK}) __KERNEL__(const TcmiArgs A) {
 ${T === 256 ? '  __shared__ float red[4];\n' : ''}  const uint32_t R = ${R}u;
   const uint32_t C = ${C}u;
@@ -736,6 +734,17 @@ function gemmTiling(batch, M, N, K, tuning, peers) {
   else if (M >= 128 && N >= 128 && blocks(4) >= 256) T = 4;
   else if (M >= 64 && N >= 64 && (blocks(2) >= 256 || longK)) T = 2;
   else T = 1;
+  // A tile that would pad the product by more than an eighth drops to 32 x 32, which
+  // divides any multiple of 32 (config 5's vocabulary of 96: 64-wide tiles did a third
+  // more MFMA work). An on-device sweep of its three such products (the logits, the
+  // output and embedding weight gradients): 32 x 32 tiles 18-31 % faster than 64-wide
+  // tiles or 48- and 96-wide ones, the products' bits unchanged.
+  const padded = (T2) => {
+    const bn = 16 * (T2 >= 2 && N >= 64 * T2 ? 4 : 2) * T2;
+    return Math.ceil(M / (32 * T2)) * 32 * T2 * Math.ceil(N / bn) * bn;
+  };
+  const unpad = !t.tile && !t.waves && t.pad !== false && T > 1 && padded(T) * 8 > 9 * M * N;
+  if (unpad) T = 1;
   let chunks = 1;
   if (t.splitk !== undefined) chunks = t.splitk;
   else if (longK && blocks(T) < 512) chunks = Math.max(1, Math.min(Math.ceil(1024 / (blocks(T) * P)), Math.floor(K / 256), 32));
@@ -750,12 +759,30 @@ function gemmTiling(batch, M, N, K, tuning, peers) {
   // and K is not split across workgroups, 2 or 4 groups of four wavefronts each sum a
   // part of K (their sums added in order in LDS), so more wavefronts keep loads in
   // flight and the matrix cores fed on each CU.
-  const kw = t.kw || (T === 1 && chunks === 1 && blocks(1) <= 512 && K >= 256 ? (K >= 512 ? 4 : 2) : 1);
+  // Unpadded products (above) take two groups up to 1024 tiles (the logits: 7.2 -> 6.7 us).
+  const kw = t.kw || (T === 1 && chunks === 1 && blocks(1) <= 512 && K >= 256 ? (K >= 512 ? 4 : 2)
+    : unpad && chunks === 1 && blocks(1) <= 1024 && K >= 256 ? 2 : 1);
   const bk = t.bk || (kw > 1 ? 32 : wn === 4 ? 32 : T === 1 ? 64 : T === 2 ? 32 : 16);
   const pf = t.pf || 2;
   const prio = t.prio !== undefined ? !!t.prio : true;
-  const wide = batch * Math.ceil(M / (32 * T)) * Math.ceil(N / (16 * wn * T));
-  return { T, chunks, chunkK, bk, pf, wn, prio, kw, blocks: wide * chunks };
+  // Per-wavefront accumulator tiles along M (tm) and N (tn): T x T unless tuned.
+  const tm = t.tm || T, tn = t.tn || T;
+  const wide = batch * Math.ceil(M / (32 * tm)) * Math.ceil(N / (16 * wn * tn));
+  return { T, tm, tn, chunks, chunkK, bk, pf, wn, prio, kw, blocks: wide * chunks };
+}
+
+/**
+ * Floats of the LDS pool (tcmi::lds_pool) tcmi_gemm.h's gemm_f32 takes for tiling `tl`
+ * and operand load modes (0 row-major, 1 transposed, 2 strided): both staged slices of
+ * each K group's A and B tiles, rows padded by 4, and the K groups' hand-over area.
+ */
+function gemmPoolFloats(tl, amode, bmode) {
+  const BM = 32 * tl.tm, BN = 16 * tl.wn * tl.tn, BK = tl.bk;
+  const aK = amode === 1, bN = bmode === 1;
+  const aTile = (aK ? BK : BM) * (aK ? BM + 4 : BK + 4);
+  const bTile = (bN ? BN : BK) * (bN ? BK + 4 : BN + 4);
+  const threads = 128 * tl.wn;
+  return tl.kw * 2 * (aTile + bTile) + (tl.kw > 1 ? (tl.kw - 1) * threads * tl.tm * tl.tn * 4 : 0);
 }
 
 // The op a view applies to every element it loads (view.op: 'relu'), as the view struct's
@@ -901,7 +928,6 @@ function gemmKernel(b, output, opts) {
   }
   const av = operandView('__KERNEL___av', views.a, batchDims, M, K);
   const bv = operandView('__KERNEL___bv', views.b, bs.slice(0, -2), K, N);
-  const T = tl.T;
   const split = tl.chunks > 1 || gathered;
   const sizes = o.sizes || {};
   const need = { a: sizes.a !== undefined ? sizes.a : batch * M * K, b: sizes.b !== undefined ? sizes.b : batch * K * N };
@@ -922,14 +948,14 @@ ${indent(lines, '    ')}
   const place = grouped ? ', wg.z, wg.x, wg.y' : ', blockIdx.z';
   const main = `extern "C" __global__ void __launch_bounds__(${threads}) __KERNEL__(const TcmiArgs A) {
 ${grouped ? `  ${XCD_GROUPED}
-` : ''}  tcmi::gemm_f32<${T}, ${T}, ${tl.bk}, ${tl.pf}, ${av.mode}, ${bv.mode}, ${split}, __KERNEL___av, __KERNEL___bv, __KERNEL___epi${variant}>(A, A.in[${ia}], A.in[${ib}],
+` : ''}  tcmi::gemm_f32<${tl.tm}, ${tl.tn}, ${tl.bk}, ${tl.pf}, ${av.mode}, ${bv.mode}, ${split}, __KERNEL___av, __KERNEL___bv, __KERNEL___epi${variant}>(A, A.in[${ia}], A.in[${ib}],
       ${batch}u, ${M}u, ${K}u, ${N}u, ${tl.chunks}u, ${tl.chunkK}u${place});
 }
 `;
   const text = `#include "tcmi_gemm.h"\n${av.text}${bv.text}${epi}${main}`;
   const k = kernelText('mm', text);
-  const kernels = [{ name: k.name, source: k.source, grid: [Math.ceil(N / (16 * tl.wn * T)), Math.ceil(M / (32 * T)), batch * tl.chunks],
-    block: [threads, 1, 1], lds: 0 }];
+  const kernels = [{ name: k.name, source: k.source, grid: [Math.ceil(N / (16 * tl.wn * tl.tn)), Math.ceil(M / (32 * tl.tm)), batch * tl.chunks],
+    block: [threads, 1, 1], lds: 0, pool: gemmPoolFloats(tl, av.mode, bv.mode) }];
   let workspace = 0;
   if (split) {
     // The reduction kernel shares the epilogue struct of the partial kernel's text.
@@ -1180,6 +1206,13 @@ function batchFamily(k) {
   // Matmul tiles take their LDS from a pool shared by instantiations of one size
   // (tcmi::lds_pool); other kernels' views would each add their own LDS: one text a family.
   if (!/^tcmi_mm_[0-9a-f]+$/.test(k.name)) return `${k.name}@${k.grid.join(',')}/${k.block.join(',')}/${k.lds}`;
+  if (k.pool !== undefined) {
+    // Products whose kernels differ in anything else (operand load modes, tiling,
+    // epilogue) run their own bodies too: one grid and workgroup size, one LDS pool
+    // size (so the batch takes no more LDS than a member), and the same workgroup
+    // places (XCD-grouped or not, which decides how a member's z index is read).
+    return `mm@${k.pool}@${k.source.includes(XCD_GROUPED) ? 'xcd' : ''}@${k.grid.join(',')}/${k.block.join(',')}/${k.lds}`;
+  }
   const views = new RegExp(`struct ${k.name}_(?:av|bv|qv|kv|vv) \\{[\\s\\S]*?\\n\\};\\n`, 'g');
   return `${k.source.replace(views, '').split(k.name).join('@')}@${k.grid.join(',')}/${k.block.join(',')}/${k.lds}`;
 }
