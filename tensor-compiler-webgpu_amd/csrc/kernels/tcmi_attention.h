@@ -191,4 +191,94 @@ __device__ __forceinline__ void attn_store(float* __restrict__ out, const f4 (&o
   }
 }
 
+// ---- the gradient (fusion/attention.js, fuseAttentionTraining) --------------------------
+//
+// dQ = dS·K, dK = dSᵀ·Q and dV = Pᵀ·dO of one attention, with the scores S = Q·Kᵀ, P and
+// dP = dO·Vᵀ recomputed: one workgroup per batch index holds all TQ query rows (16 per
+// wavefront, W wavefronts) and all TK keys. K and V are staged in LDS; each wavefront
+// forms its rows' S and dP in registers (attn_scores), the generated body turns them into
+// dS and P there, and dQ takes dS as the A operand of its product with K straight from
+// the registers (attn_pv). dK and dV sum over the queries, which the wavefronts hold one
+// row per lane: dS (then P) is written to LDS as a [query][key] tile beside Q (then dO),
+// and each wavefront forms the rows of 16 keys at a time, reading the tile down its
+// columns. Every product walks its k index in the order of tcmi_gemm.h (16 at a time, 4
+// per MFMA step), so each output is computed the same way whichever others a kernel forms.
+
+template <int TQ, int TK, int DH, int DV>
+struct AttnGradTiles {
+  static constexpr int W = (TQ + 15) / 16;        // wavefronts: one per 16 query rows
+  static constexpr int NT = (TK + 15) / 16;       // key tiles of 16
+  static constexpr int DH16 = (DH + 15) / 16;
+  static constexpr int DV16 = (DV + 15) / 16;
+  static constexpr int ROWS = NT * 16;            // keys staged (zero past TK)
+  static constexpr int QROWS = W * 16;            // query rows staged (zero past TQ)
+  static constexpr int KS = DH16 * 16 + 4;        // Ks[key][d]
+  static constexpr int VS = DV16 * 16 + 4;        // Vs[key][d]
+  static constexpr int TS = ROWS + 4;             // Ts[query][key]: dS, then P
+  static constexpr int QS = DH16 * 16 + 4;        // Qs[query][d]
+  static constexpr int OS = DV16 * 16 + 4;        // Os[query][d] (dO)
+  static constexpr int PHASE1 = ROWS * KS + ROWS * VS;
+  static constexpr int PHASE2 = QROWS * TS + QROWS * QS;
+  static constexpr int PHASE3 = QROWS * TS + QROWS * OS;
+  static constexpr int POOL = PHASE1 > PHASE2 ? (PHASE1 > PHASE3 ? PHASE1 : PHASE3) : (PHASE2 > PHASE3 ? PHASE2 : PHASE3);
+  static_assert(W >= 1 && W <= 8, "the gradient kernel holds at most 128 query rows");
+};
+
+// Registers in the scores' layout (lane (t, q): row 16·wave + t, keys 16jt + 4q .. +3)
+// written to a [row][key] tile of row stride TS.
+template <int NT, int TS>
+__device__ __forceinline__ void attn_rows_to_lds(float* tile, const f4 (&v)[NT], int wave, int t16, int q) {
+  float* row = tile + (16 * wave + t16) * TS + 4 * q;
+#pragma unroll
+  for (int jt = 0; jt < NT; ++jt) *reinterpret_cast<f4*>(row + 16 * jt) = v[jt];
+}
+
+// A lane's operand fragments (row 16·wave + t, columns 16g + 4q .. +3) written to a
+// [row][column] tile of row stride S.
+template <int D16, int S>
+__device__ __forceinline__ void attn_frags_to_lds(float* tile, const f4 (&v)[D16], int wave, int t16, int q) {
+  float* row = tile + (16 * wave + t16) * S + 4 * q;
+#pragma unroll
+  for (int g = 0; g < D16; ++g) *reinterpret_cast<f4*>(row + 16 * g) = v[g];
+}
+
+// out[b][key][d] = Σ_query T[query][key] · X[query][d] for the key tiles of this wavefront
+// (kt = wave, wave + W, ...): the A operand read down T's columns (lane (t, q) at step s:
+// T[16g + 4q + s][16kt + t]), the B operand along X's rows, the queries 16 at a time.
+template <int NT, int W, int D16, int TS, int XS, int TK, int D>
+__device__ __forceinline__ void attn_grad_keys(float* __restrict__ out, const float* T, const float* X, uint32_t b,
+                                               int wave, int t16, int q) {
+  for (int kt = wave; kt < NT; kt += W) {
+    f4 acc[D16];
+#pragma unroll
+    for (int jn = 0; jn < D16; ++jn) acc[jn] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int g = 0; g < W; ++g) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int qr = 16 * g + 4 * q + s;
+        const float a = T[qr * TS + 16 * kt + t16];
+#pragma unroll
+        for (int jn = 0; jn < D16; ++jn)
+          acc[jn] = __builtin_amdgcn_mfma_f32_16x16x4f32(X[qr * XS + 16 * jn + t16], a, acc[jn], 0, 0, 0);
+      }
+    }
+    const int key = 16 * kt + t16;
+    if (key < TK) {
+      float* __restrict__ o = out + ((size_t)b * TK + key) * D;
+#pragma unroll
+      for (int jn = 0; jn < D16; ++jn) {
+        const int c0 = 16 * jn + 4 * q;
+        if (D % 4 == 0) {
+          if (c0 < D) *reinterpret_cast<f4*>(o + c0) = acc[jn];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (c0 + r < D) o[c0 + r] = acc[jn][r];
+        }
+      }
+    }
+  }
+}
+
 }  // namespace tcmi

@@ -5,7 +5,11 @@
 //
 //   node bench.js [--configs ceiling,c2,c3,c4] [--steps K] [--warmup W] [--programs P]
 //                 [--reps N] [--c4-shapes all|small] [--quick] [--graphs] [--no-trainer-graphs] [--step-only]
+//                 [--no-attention]
 //                 [--roofline-only] [--gate FILE]
+//
+// --no-attention: c5's perf path without each attention and its gradient fused
+// (fusion/attention.js fuseAttentionTraining), which it uses by default.
 //
 // --graphs: the c2 step's programs replayed as captured HIP graphs. The trainers
 // of c1 and c5 replay each step as a captured HIP graph by default (a step is
@@ -550,7 +554,10 @@ function trainStep(runner, bench, name, req, opts) {
   const { modelStep } = require('../src/builders/models');
   const { fusedStep, HipTrainer } = require('../src/mi355x/trainer');
   const m = modelStep(req);
-  const fs = fusedStep(m.step);
+  // The perf path fuses each attention and its gradient (fusion/attention.js) unless
+  // --no-attention; the contract-only lowering beside it never does.
+  const attention = !!req.attention && !flag('no-attention');
+  const fs = fusedStep(m.step, { attention });
   // The unfused step in the perf lowering (views, batching) without anything that forms
   // one node's value inside another's launch (no folds, absorption or relus on load).
   const lu = lowerMI355X(m.step.graph, { perf: true, keep: [m.step.loss, m.step.logits].concat(Object.values(m.step.outputs)),
@@ -569,7 +576,7 @@ function trainStep(runner, bench, name, req, opts) {
     const n = Number(arg('warmup', 3)) + Number(arg('steps', 20));
     for (let i = 0; i < n; i++) trainer.train(batch.x, batch.y);
     trainer.destroy();
-    return { config: name, info: m.info, stepOnly: true, runs: n, graphReplay: graph,
+    return { config: name, info: m.info, stepOnly: true, runs: n, graphReplay: graph, attention,
       results: [{ name: `${name}-step`, launches: launchRecords(fs.lowered) }] };
   }
   for (let i = 0; i < W; i++) trainer.train(batch.x, batch.y);
@@ -656,7 +663,7 @@ function trainStep(runner, bench, name, req, opts) {
     ts.destroy();
   }
   // The same step with every launch dispatched by itself (no batched launches).
-  const fsPlain = fusedStep(m.step, { batch: false });
+  const fsPlain = fusedStep(m.step, { batch: false, attention });
   const tp = new HipTrainer(runner, fsPlain, m.params, m.state, { graph });
   for (let i = 0; i < W; i++) tp.train(batch.x, batch.y);
   const tp0 = process.hrtime.bigint();
@@ -673,7 +680,7 @@ function trainStep(runner, bench, name, req, opts) {
     stepsPerSec: 1e3 / plainWall, residentStepsPerSec: 1e3 / plainResident };
   tp.destroy();
   const flops = fs.lowered.launches.reduce((q, l) => q + (l.flops || 0), 0);
-  return { config: name, info: m.info, steps: K, warmup: W, lossLast: loss, arena, streams: streamRuns, graphReplay: graph,
+  return { config: name, info: m.info, steps: K, warmup: W, lossLast: loss, arena, streams: streamRuns, graphReplay: graph, attention,
     stepsPerSec: 1e3 / wallMs, msPerStep: wallMs, residentMsPerStep: residentMs, residentStepsPerSec: 1e3 / residentMs,
     launches: { fused: fs.lowered.launches.length, unfused: lu.launches.length },
     dispatches: p.dispatches, batches: (fs.lowered.batches || []).length, unbatched, contract,
@@ -683,7 +690,7 @@ function trainStep(runner, bench, name, req, opts) {
 }
 
 function c1(runner, bench, opts) { return trainStep(runner, bench, 'c1', { model: 'mlp' }, opts); }
-function c5(runner, bench, opts) { return trainStep(runner, bench, 'c5', { model: 'transformer', B: opts.quick ? 8 : 64 }, opts); }
+function c5(runner, bench, opts) { return trainStep(runner, bench, 'c5', { model: 'transformer', B: opts.quick ? 8 : 64, attention: true }, opts); }
 
 /**
  * The reference's workload sweep (src/fusion/workloads.js:71-120): every graph

@@ -181,11 +181,12 @@ function precompileGroup(group, arch, shard, shards) {
     // The trainer compiles a step's kernels as one module: the same text here.
     const { modelStep } = require('../src/builders/models');
     const { fusedStep } = require('../src/mi355x/trainer');
-    const reqs = [{ model: 'mlp' }, { model: 'transformer', B: 1 }, { model: 'transformer', B: 64 }, { model: 'transformer-ref' }];
+    const reqs = [{ model: 'mlp' }, { model: 'transformer', B: 1 }, { model: 'transformer', B: 64 }, { model: 'transformer-ref' },
+      { model: 'transformer', B: 1, attention: true }, { model: 'transformer', B: 64, attention: true }];
     let n = 0;
     for (const r of reqs) {
       const m = modelStep(r);
-      const fs = fusedStep(m.step);
+      const fs = fusedStep(m.step, { attention: !!r.attention });
       // The bench's unfused step runs in the perf lowering as well.
       const unfused = lowerMI355X(m.step.graph, { perf: true, keep: [m.step.loss, m.step.logits].concat(Object.values(m.step.outputs)), rowFolds: false });
       n += precompile([fs.lowered], arch) + precompile([fs.checked], arch) + precompile([unfused], arch);
@@ -720,7 +721,7 @@ function stepGraph(req, dir) {
   const { modelStep } = require('../src/builders/models');
   const { fusedStep } = require('../src/mi355x/trainer');
   const m = modelStep(req);
-  const fs = fusedStep(m.step);
+  const fs = fusedStep(m.step, { attention: !!req.attention });
   const bundle = new Bundle(dir);
   const b = m.batch(req.batchIndex || 0);
   const values = Object.assign({}, m.params, m.state, { x: b.x, y: b.y });
@@ -775,7 +776,7 @@ async function gpuLocal(req, dir) {
   const { fusedStep, fusedForward } = require('../src/mi355x/trainer');
   const { HipRunner } = require('../src/mi355x/runner');
   const fs = req.forward ? fusedForward(modelForward(req).fwd, { sabotage: req.sabotage })
-    : fusedStep(modelStep(req).step, { sabotage: req.sabotage });
+    : fusedStep(modelStep(req).step, { sabotage: req.sabotage, attention: !!req.attention });
   const raw = fs_.readFileSync(req.valuesFile);
   const data = new Float32Array(raw.buffer, raw.byteOffset, raw.byteLength / 4);
   const sets = req.sets || 1;
@@ -916,8 +917,8 @@ async function gpuStepSlices(req, dir) {
   const { fusedStep } = require('../src/mi355x/trainer');
   const { HipRunner } = require('../src/mi355x/runner');
   const m = modelStep(req);
-  const fs = fusedStep(m.step);
-  const twin = fusedStep(modelStep(Object.assign({}, req, { B: 1 })).step);
+  const fs = fusedStep(m.step, { attention: !!req.attention });
+  const twin = fusedStep(modelStep(Object.assign({}, req, { B: 1 })).step, { attention: !!req.attention });
   if (!sameStructure(fs.graph, twin.graph)) throw new Error('the one-sequence twin differs in structure');
   const nodes = fs.graph.nodes;
   const axis = nodes.map((n, i) => batchAxis(n.shape, twin.graph.nodes[i].shape));
@@ -1057,7 +1058,7 @@ async function gpuTrain(req) {
   const { fusedStep, HipTrainer } = require('../src/mi355x/trainer');
   const { HipRunner } = require('../src/mi355x/runner');
   const m = modelStep(req);
-  const fs = fusedStep(m.step);
+  const fs = fusedStep(m.step, { attention: !!req.attention });
   const runner = HipRunner.create();
   const trainer = new HipTrainer(runner, fs, m.params, m.state, { graph: !!req.graph, arena: !!req.arena, streams: req.streams || 1 });
   const plan = trainer.program.arena;
@@ -1241,6 +1242,10 @@ async function main() {
       const fs = fusedStep(modelStep({ model: 'transformer', B: 64 }).step);
       add(fs.lowered);
       add(fs.checked);
+      // The step with attention and its gradient fused (its joint gradient kernel included).
+      const fa = fusedStep(modelStep({ model: 'transformer', B: 64 }).step, { attention: true });
+      add(fa.lowered);
+      add(fa.checked);
       for (let s2 = 0; s2 < 8; s2++) { const w = chainWorkload(s2, 8192, 1024); perf(w.forward); perf(w.gradient); }
       for (const fn of ['softmax', 'logSoftmax']) { const g = cfg.c3Graphs(fn, cfg.C3_SHAPE[0], cfg.C3_SHAPE[1]); perf(g.forward); perf(g.gradient); }
       for (const [M, K, N] of cfg.C4_SHAPES) for (const act of ['relu', 'tanh']) { const g = cfg.c4Graphs(act, M, K, N); perf(g.forward); perf(g.gradient); }
@@ -1278,8 +1283,8 @@ async function main() {
       const { fusedStep } = require('../src/mi355x/trainer');
       for (const r of req.models || []) {
         const m = modelStep(r);
-        const f = fusedStep(m.step);
-        one(`${r.model}-${r.B || ''}`, f.graph, [f.loss, f.logits].concat(Object.values(f.outputs)));
+        const f = fusedStep(m.step, { attention: !!r.attention });
+        one(`${r.model}-${r.B || ''}${r.attention ? '-attention' : ''}`, f.graph, [f.loss, f.logits].concat(Object.values(f.outputs)));
       }
       if (req.corpus) {
         const { corpusGraphs } = require('../src/testing/random_graph');
@@ -1332,8 +1337,8 @@ async function main() {
       const { fusedStep } = require('../src/mi355x/trainer');
       for (const r of req.models || []) {
         const m = modelStep(r);
-        const f = fusedStep(m.step);
-        out.push(one(`${r.model}-${r.B || ''}`, f.graph, [f.loss, f.logits].concat(Object.values(f.outputs))));
+        const f = fusedStep(m.step, { attention: !!r.attention });
+        out.push(one(`${r.model}-${r.B || ''}${r.attention ? '-attention' : ''}`, f.graph, [f.loss, f.logits].concat(Object.values(f.outputs))));
       }
       if (req.corpus) {
         const { corpusGraphs } = require('../src/testing/random_graph');
@@ -1352,7 +1357,7 @@ async function main() {
       const { modelStep } = require('../src/builders/models');
       const { fusedStep } = require('../src/mi355x/trainer');
       const { kernelSources } = require('../src/mi355x/lower');
-      const fs = fusedStep(modelStep(req).step);
+      const fs = fusedStep(modelStep(req).step, { attention: !!req.attention });
       const src = kernelSources(fs.lowered);
       const kernels = [];
       let batches = 0;
@@ -1386,8 +1391,8 @@ async function main() {
       const { modelStep } = require('../src/builders/models');
       const { fusedStep } = require('../src/mi355x/trainer');
       for (const r of req.models || []) {
-        const f = fusedStep(modelStep(r).step);
-        out.push(one(`${r.model}-${r.B || ''}`, f.graph, [f.loss, f.logits].concat(Object.values(f.outputs))));
+        const f = fusedStep(modelStep(r).step, { attention: !!r.attention });
+        out.push(one(`${r.model}-${r.B || ''}${r.attention ? '-attention' : ''}`, f.graph, [f.loss, f.logits].concat(Object.values(f.outputs))));
       }
       if (req.corpus) {
         const { corpusGraphs } = require('../src/testing/random_graph');
@@ -1455,7 +1460,7 @@ async function main() {
       } else if (req.model) {
         const { modelStep } = require('../src/builders/models');
         const { fusedStep } = require('../src/mi355x/trainer');
-        const fs = fusedStep(modelStep(req).step);
+        const fs = fusedStep(modelStep(req).step, { attention: !!req.attention });
         g = fs.graph;
         keep = [fs.loss, fs.logits].concat(Object.values(fs.outputs));
         absorb = true;
@@ -1473,7 +1478,8 @@ async function main() {
       const plain = new Map(lowerMI355X(g).launches.map((x) => [x.node, x]));
       out = { graph: g.toJSON(), keep, aliases: l.aliases, folded: l.folded, dead: l.dead, rowFolds: rowFoldsOf(l), absorbed: absorbedOf(l), loadOps: loadOpsOf(l),
         launches: l.launches.map((x) => ({ node: x.node, kind: x.kind, inputs: x.inputs, params: x.params.length, views: x.views || null, modes: gemmModes(x),
-          split: gemmSplit(x), plainSplit: gemmSplit(plain.get(x.node)) })) };
+          split: gemmSplit(x), plainSplit: gemmSplit(plain.get(x.node)) })),
+        batches: (l.batches || []).map((b) => ({ start: b.start, count: b.count, joint: !!b.joint, kernels: b.kernels.map((k) => k.name) })) };
       break;
     }
     case 'precompile': out = { kernels: precompileGroup(req.group || 'direct', req.arch, req.shard, req.shards) }; break;

@@ -1122,7 +1122,7 @@ ${indent(inner, '      ')}
     throw new Error('attention operand view out of bounds');
   }
   // Wavefronts per workgroup: one per 16 query rows, up to 8 (128 rows share one K and V tile).
-  const WAVES = Math.min(8, Math.ceil(TQ / 16));
+  const WAVES = (o.tuning && o.tuning.waves) || Math.min(8, Math.ceil(TQ / 16));
   const THREADS = 64 * WAVES;
   const text = `#include "tcmi_attention.h"
 ${qv.text}${kv.text}${vv.text}extern "C" __global__ void __launch_bounds__(${THREADS}) __KERNEL__(const TcmiArgs A) {
@@ -1165,6 +1165,282 @@ ${indent(pre.concat([pLoop]), '  ')}
   return { name: k.name, source: k.source, params: Uint32Array.from(params), grid: [Math.ceil(TQ / (16 * WAVES)), batch, 1],
     block: [THREADS, 1, 1], lds: 0, ldsStatic: lds, workspace: 0, flops: 2 * batch * TQ * TK * (DH + DV),
     modes: [qv.mode, kv.mode, vv.mode] };
+}
+
+// ---- the attention gradient (fusion/attention.js, fuseAttentionTraining) -------------
+
+const GRAD_PARTS = ['dq', 'dk', 'dv'];
+
+/**
+ * The parts of an attention-grad body (its inputs a0 Q, a1 K, a2 V, a3 dO, then score
+ * operands): the scores S = matmul(a0, transpose(a1)), dP = matmul(a3, transpose(a2)),
+ * and the three products dQ = matmul(dS, a1), dK = matmul(transpose(dS), a0) and
+ * dV = matmul(transpose(P), a3), as fuseAttentionTraining builds it.
+ */
+function gradBodyParts(b) {
+  const N = b.nodes;
+  const inputAt = (id, k) => N[id].op === 'input' && N[id].attrs.name === `a${k}`;
+  const tOf = (id, k) => N[id].op === 'transpose' && inputAt(N[id].inputs[0], k);
+  const mm = N.filter((n) => n.op === 'matmul');
+  const one = (pred, what) => {
+    const f = mm.filter(pred);
+    if (f.length !== 1) throw new Error(`attention-grad body: expected one ${what}`);
+    return f[0];
+  };
+  const S = one((n) => inputAt(n.inputs[0], 0) && tOf(n.inputs[1], 1), 'score product');
+  const dP = one((n) => inputAt(n.inputs[0], 3) && tOf(n.inputs[1], 2), 'dP product');
+  const dQ = one((n) => inputAt(n.inputs[1], 1) && !inputAt(n.inputs[0], 0), 'dQ product');
+  const dK = one((n) => inputAt(n.inputs[1], 0) && N[n.inputs[0]].op === 'transpose', 'dK product');
+  const dV = one((n) => inputAt(n.inputs[1], 3) && N[n.inputs[0]].op === 'transpose', 'dV product');
+  const ds = dQ.inputs[0];
+  if (N[dK.inputs[0]].inputs[0] !== ds) throw new Error('attention-grad body: dK must read the dQ product\'s dS');
+  return { S, dP, dQ, dK, dV, ds, p: N[dV.inputs[0]].inputs[0] };
+}
+
+/** The part ('dq' | 'dk' | 'dv') node `output` of an attention-grad body is. */
+function gradPart(b, output) {
+  const x = gradBodyParts(b);
+  const part = output === x.dQ.id ? 'dq' : output === x.dK.id ? 'dk' : output === x.dV.id ? 'dv' : null;
+  if (!part) throw new Error('attention-grad body: the output must be one of its three products');
+  return part;
+}
+
+/**
+ * The text of a kernel forming `parts` of an attention-grad body (tcmi_attention.h's
+ * gradient): one workgroup per batch index, W = ceil(TQ / 16) wavefronts. With `joint`,
+ * one launch writes all three, member 0 (dQ), 1 (dK) and 2 (dV) of a batched launch's
+ * argument block; otherwise the one part goes to A.out. Every part is formed by the same
+ * code in either form (the body's values below, then the part's product), so a part's
+ * bits do not depend on which others the kernel forms.
+ */
+function attnGradText(b, parts, opts) {
+  const o = opts || {};
+  checkOperands(b);
+  const x = gradBodyParts(b);
+  const N = b.nodes;
+  const shapeOf = (k) => N.find((n) => n.op === 'input' && n.attrs.name === `a${k}`).shape;
+  const qs = shapeOf(0), ks = shapeOf(1), vs = shapeOf(2), os = shapeOf(3);
+  const r = qs.length;
+  const batchDims = qs.slice(0, r - 2);
+  const batch = size(batchDims), TQ = qs[r - 2], DH = qs[r - 1], TK = ks[r - 2], DV = vs[r - 1];
+  if (ks[r - 1] !== DH || vs[r - 2] !== TK || os[r - 2] !== TQ || os[r - 1] !== DV) throw new Error('attention-grad body: operand shapes');
+  if (TQ > 128) throw new Error(`attention-grad: ${TQ} queries (at most 128 in one workgroup)`);
+  if (batch * TQ * TK >= 2 ** 31) throw new Error('attention-grad exceeds the 32-bit index space');
+  if (batch > 65535) throw new Error(`attention-grad batch ${batch} exceeds the grid`);
+  const want = new Set(parts);
+  const needDs = want.has('dq') || want.has('dk');
+  const needP = want.has('dv');
+  const R = batch * TQ, C = TK;
+  const params = [batch, TQ, DH, TK, DV];
+  const rowTier = (id) => size(N[id].shape) === R && size(N[id].shape) !== R * C;
+  // The body's values the kernel forms: dS and/or P, and the reductions they depend on.
+  const goals = [].concat(needDs ? [x.ds] : [], needP ? [x.p] : []);
+  const deps = new Set();
+  const walk = (id) => {
+    if (deps.has(id)) return;
+    deps.add(id);
+    if (id === x.S.id || id === x.dP.id) return;
+    for (const i of N[id].inputs) walk(i);
+  };
+  for (const gl of goals) walk(gl);
+  const needDp = deps.has(x.dP.id);
+  const reductions = N.filter((n) => isReduce(n) && deps.has(n.id));
+  for (const rd of reductions) {
+    const src = N[rd.inputs[0]].shape;
+    if (rd.attrs.axis !== src.length - 1 || size(src) !== R * C) throw new Error('attention-grad body: reductions must be over the keys');
+  }
+  const NT = Math.ceil(TK / 16);
+  const reduced = new Map();
+  const rowLines = [];
+  const caches = new Map();
+  const cacheFill = [];
+  let em;
+  const ROW = { key: 'r', idx: 'r', root: false, row: true, limit: R };
+  const elemCtx = () => ({ key: 'e', idx: 'e', root: true, limit: R * C });
+  em = new Emitter(b, params, {
+    special(id, ctx) {
+      if (id === x.S.id || id === x.dP.id) {
+        if (ctx.row || !ctx.root) throw new Error('attention-grad body: the scores are read at their own index only');
+        return id === x.S.id ? 'sacc[jt][l]' : 'dpacc[jt][l]';
+      }
+      if (reduced.has(id)) return reduced.get(id);
+      const n = N[id];
+      if (!ctx.row && rowTier(id) && n.op !== 'input' && n.op !== 'const') return em.value(id, ROW, rowLines);
+      if (n.op === 'broadcast' && !ctx.row && rowTier(n.inputs[0])) {
+        const src = N[n.inputs[0]];
+        if (src.op !== 'input' && src.op !== 'const') return em.value(src.id, ROW, rowLines);
+      }
+      return undefined;
+    },
+    load(k, ctx, lines) {
+      if (k < 4) throw new Error('attention-grad body: Q, K, V and dO are read by the products only');
+      if (ctx.key.startsWith('e')) {
+        const ck = `${k}|${ctx.idx}`;
+        if (!caches.has(ck)) {
+          const c = `C${caches.size}`;
+          caches.set(ck, c);
+          cacheFill.push(`float ${c}[${NT}][4];`, `#pragma unroll
+for (int jt = 0; jt < ${NT}; ++jt) {
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    const uint32_t c = 16u * jt + 4u * q + l;
+    const uint32_t e = rowBase + c;
+    ${c}[jt][l] = rowOk && c < ${TK}u ? A.in[${k}][${ctx.idx}] : 0.f;
+  }
+}`);
+        }
+        return `${caches.get(ck)}[jt][l]`;
+      }
+      const v = `L${lines.length}_${k}`;
+      lines.push(`const float ${v} = A.in[${k}][${ctx.idx}];`);
+      return v;
+    },
+  });
+  const loop = (bodyLines) => `#pragma unroll
+for (int jt = 0; jt < ${NT}; ++jt) {
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    const uint32_t c = 16u * jt + 4u * q + l;
+    if (rowOk && c < ${TK}u) {
+      const uint32_t e = rowBase + c;
+${indent(bodyLines, '      ')}
+    }
+  }
+}`;
+  const phases = [];
+  reductions.forEach((rd, k) => {
+    for (const key of Array.from(em.memo.keys())) if (key.startsWith('e')) em.memo.delete(key);
+    const rowBefore = rowLines.length;
+    const inner = [];
+    const v = em.value(rd.inputs[0], elemCtx(), inner);
+    const isMax = rd.op === 'max';
+    const pre = rowLines.splice(rowBefore);
+    phases.push(...pre,
+      `float acc${k} = ${isMax ? '(-TCMI_INF)' : '0.f'};`,
+      loop(inner.concat([`acc${k} = tcmi::red_${isMax ? 'max' : 'sum'}(acc${k}, ${v});`])),
+      `const float red${k} = tcmi::quad16_reduce<${isMax}>(acc${k});`);
+    reduced.set(rd.id, `red${k}`);
+  });
+  // dS and P per score, in the scores' register layout (0 past TK and for rows past TQ).
+  for (const key of Array.from(em.memo.keys())) if (key.startsWith('e')) em.memo.delete(key);
+  const rowBefore = rowLines.length;
+  const inner = [];
+  const dsv = needDs ? em.value(x.ds, elemCtx(), inner) : null;
+  const pv = needP ? em.value(x.p, elemCtx(), inner) : null;
+  const pre = rowLines.splice(rowBefore);
+  const valLoop = `#pragma unroll
+for (int jt = 0; jt < ${NT}; ++jt) {
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    const uint32_t c = 16u * jt + 4u * q + l;
+${needDs ? '    float dse = 0.f;\n' : ''}${needP ? '    float pe = 0.f;\n' : ''}    if (rowOk && c < ${TK}u) {
+      const uint32_t e = rowBase + c;
+${indent(inner, '      ')}
+${needDs ? `      dse = ${dsv};\n` : ''}${needP ? `      pe = ${pv};\n` : ''}    }
+${needDs ? '    dsr[jt][l] = dse;\n' : ''}${needP ? '    pr[jt][l] = pe;\n' : ''}  }
+}`;
+  const views = o.views || {};
+  const sizes = o.sizes || {};
+  const qv = operandView('__KERNEL___qv', views.q, batchDims, TQ, DH);
+  const kv = operandView('__KERNEL___kv', views.k, batchDims, TK, DH);
+  const vv = operandView('__KERNEL___vv', views.v, batchDims, TK, DV);
+  const ov = operandView('__KERNEL___ov', views.o, batchDims, TQ, DV);
+  if ([qv, kv, vv, ov].some((v) => v.mapped) || [views.q, views.k, views.v, views.o].some((v) => v && v.op)) {
+    throw new Error('attention-grad operand read through a mapped view or a load op');
+  }
+  const need = (slot, dense) => (sizes[slot] !== undefined ? sizes[slot] : dense);
+  if (qv.limit > need('q', batch * TQ * DH) || kv.limit > need('k', batch * TK * DH) || vv.limit > need('v', batch * TK * DV)
+    || ov.limit > need('o', batch * TQ * DV)) {
+    throw new Error('attention-grad operand view out of bounds');
+  }
+  const W = Math.ceil(TQ / 16);
+  const THREADS = 64 * W;
+  const joint = !!o.joint;
+  const outOf = (part) => (joint ? `B.m[${GRAD_PARTS.indexOf(part)}].out` : 'A.out');
+  const steps = [];
+  if (want.has('dq')) {
+    steps.push(`{ // dQ = dS · K: dS from the registers, K from LDS
+  tcmi::f4 oacc[G::DH16];
+  tcmi::attn_pv<G::NT, G::DH16, G::KS>(oacc, dsr, Ks, t16, q);
+  tcmi::attn_store<${TQ}, ${DH}, G::DH16>(${outOf('dq')}, oacc, b, row, q);
+}`);
+  }
+  if (want.has('dk')) {
+    steps.push(`__syncthreads();   // K and V read: the pool takes dS and Q
+tcmi::attn_rows_to_lds<G::NT, G::TS>(pool, dsr, wave, t16, q);
+tcmi::attn_frags_to_lds<G::DH16, G::QS>(pool + G::QROWS * G::TS, qf, wave, t16, q);
+__syncthreads();
+tcmi::attn_grad_keys<G::NT, G::W, G::DH16, G::TS, G::QS, ${TK}, ${DH}>(${outOf('dk')}, pool, pool + G::QROWS * G::TS, b, wave, t16, q);`);
+  }
+  if (want.has('dv')) {
+    steps.push(`__syncthreads();   // the pool takes P and dO
+tcmi::attn_rows_to_lds<G::NT, G::TS>(pool, pr, wave, t16, q);
+tcmi::attn_frags_to_lds<G::DV16, G::OS>(pool + G::QROWS * G::TS, dof, wave, t16, q);
+__syncthreads();
+tcmi::attn_grad_keys<G::NT, G::W, G::DV16, G::TS, G::OS, ${TK}, ${DV}>(${outOf('dv')}, pool, pool + G::QROWS * G::TS, b, wave, t16, q);`);
+  }
+  const needDo = needDp || want.has('dv');
+  const needV = needDp;
+  const sig = joint ? 'const TcmiBatch<3> B' : 'const TcmiArgs A';
+  const text = `#include "tcmi_attention.h"
+${qv.text}${kv.text}${vv.text}${ov.text}extern "C" __global__ void __launch_bounds__(${THREADS}) __KERNEL__(${sig}) {
+${joint ? '  const TcmiPtrs& A = B.m[0];   // the three members read the same operands\n' : ''}  using G = tcmi::AttnGradTiles<${TQ}, ${TK}, ${DH}, ${DV}>;
+  __shared__ __attribute__((aligned(16))) float pool[G::POOL];
+  float* const Ks = pool;
+  float* const Vs = pool + G::ROWS * G::KS;
+  const uint32_t b = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t16 = lane & 15, q = lane >> 4;
+  const uint32_t row = wave * 16u + t16;   // this lane's query row
+  tcmi::attn_zero_padding<${TK}, ${DH}, ${DV}, ${THREADS}>(Ks, Vs);
+  using Kst = tcmi::AttnStage<${TK}, ${DH}, G::KS, ${kv.mode}, false, __KERNEL___kv, ${THREADS}>;
+  tcmi::f4 kr[Kst::PER];
+  Kst::load(kr, A.in[1], b);
+${needV ? `  using Vst = tcmi::AttnStage<${TK}, ${DV}, G::VS, ${vv.mode}, false, __KERNEL___vv, ${THREADS}>;
+  tcmi::f4 vr[Vst::PER];
+  Vst::load(vr, A.in[2], b);
+` : ''}  tcmi::f4 qf[G::DH16];
+  tcmi::attn_q<${TQ}, ${DH}, G::DH16, ${qv.mode}, __KERNEL___qv>(qf, A.in[0], b, row, q);
+${needDo ? `  tcmi::f4 dof[G::DV16];
+  tcmi::attn_q<${TQ}, ${DV}, G::DV16, ${ov.mode}, __KERNEL___ov>(dof, A.in[3], b, row, q);
+` : ''}  const bool rowOk = row < ${TQ}u;
+  const uint32_t r = b * ${TQ}u + (rowOk ? row : 0u);   // the score row (rows past TQ compute nothing)
+  const uint32_t rowBase = r * ${TK}u;
+${indent(cacheFill, '  ')}
+  Kst::store(kr, Ks);
+${needV ? '  Vst::store(vr, Vs);\n' : ''}  __syncthreads();
+  tcmi::f4 sacc[G::NT];
+  tcmi::attn_scores<G::NT, G::DH16, G::KS>(sacc, qf, Ks, t16, q);
+${needDp ? '  tcmi::f4 dpacc[G::NT];\n  tcmi::attn_scores<G::NT, G::DV16, G::VS>(dpacc, dof, Vs, t16, q);\n' : ''}${indent(phases, '  ')}
+${needDs ? '  tcmi::f4 dsr[G::NT];\n' : ''}${needP ? '  tcmi::f4 pr[G::NT];\n' : ''}${indent(pre.concat([valLoop]), '  ')}
+${indent(steps.join('\n').split('\n'), '  ')}
+}
+`;
+  const flops = 2 * batch * TQ * TK * DH
+    + (needDp ? 2 * batch * TQ * TK * DV : 0)
+    + (want.has('dq') ? 2 * batch * TQ * TK * DH : 0) + (want.has('dk') ? 2 * batch * TQ * TK * DH : 0)
+    + (want.has('dv') ? 2 * batch * TQ * TK * DV : 0);
+  return { text, grid: [1, batch, 1], block: [THREADS, 1, 1], params, flops, modes: [qv.mode, kv.mode, vv.mode, ov.mode] };
+}
+
+/**
+ * One part of an attention-grad node (the part its output is), and, in `joint`, the
+ * kernel forming all three of its body's parts in one launch: the perf lowering runs the
+ * three nodes sharing a body as one batched launch of it (lower.js batchPlan).
+ */
+function attentionGradKernel(b, output, opts) {
+  const part = gradPart(b, output);
+  const one = attnGradText(b, [part], opts);
+  const k = kernelText('attng', one.text);
+  const all = attnGradText(b, GRAD_PARTS, Object.assign({}, opts, { joint: true }));
+  const j = kernelText('attnj', all.text);
+  const joint = { name: j.name, source: j.source, grid: all.grid, block: all.block, lds: 0, flops: all.flops, parts: GRAD_PARTS };
+  // Work per part: its product, and dP (which only dQ and dK read) counted with dQ; the
+  // recomputed scores are not the graph's work.
+  const [batch, TQ, DH, TK, DV] = one.params;
+  const flops = 2 * batch * TQ * TK * (part === 'dq' ? DH + DV : part === 'dk' ? DH : DV);
+  return { name: k.name, source: k.source, params: Uint32Array.from(one.params), grid: one.grid, block: one.block, lds: 0,
+    workspace: 0, flops, part, joint, modes: one.modes };
 }
 
 // ---- batched launches ----------------------------------------------------------------
@@ -1279,5 +1555,6 @@ function batchedKernel(members, count) {
     members: count, variants: variants.length > 1 ? variantOf.map((v) => variants[v].name) : undefined };
 }
 
-module.exports = { elementwiseKernel, rowwiseKernel, colreduceKernels, gemmKernel, gemmTiling, attentionKernel, classifyGather, gatherStrides,
+module.exports = { elementwiseKernel, rowwiseKernel, colreduceKernels, gemmKernel, gemmTiling, attentionKernel, attentionGradKernel,
+  gradPart, GRAD_PARTS, classifyGather, gatherStrides,
   literal, fnv, Emitter, ParamOverflow, WG, MAX_P, MAX_IN, MAX_BATCH, batchable, batchedKernel, batchFamily };

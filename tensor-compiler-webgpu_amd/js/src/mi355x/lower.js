@@ -133,7 +133,18 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers,
     if (kind === 'epilogue') {
       return Object.assign({ kind: 'fused-epilogue' }, single(cg.gemmKernel(b, out, Object.assign({ tuning: tuning.gemm, peers }, sab, mmViews))));
     }
-    if (kind === 'attention') return Object.assign({ kind: 'fused-attention' }, single(cg.attentionKernel(b, out, Object.assign({}, mmViews))));
+    if (kind === 'attention') {
+      return Object.assign({ kind: 'fused-attention' }, single(cg.attentionKernel(b, out, Object.assign({ tuning: tuning.attn }, mmViews))));
+    }
+    if (kind === 'attention-grad') {
+      // One part of the three sharing this body; the kernel forming all three rides along
+      // (batchPlan runs the three as one launch of it).
+      const k = cg.attentionGradKernel(b, out, Object.assign({}, mmViews));
+      const r = single(k);
+      r.kernels[0].joint = k.joint;
+      r.kernels[0].part = k.part;
+      return Object.assign({ kind: 'fused-attention-grad' }, r);
+    }
     throw new Error(`no MI355X kernel for fused kind '${kind}'`);
   }
   if (ELEMENTWISE_OPS.has(node.op) || GATHERS.has(node.op)) {
@@ -194,6 +205,8 @@ function consumersOf(graph) {
  */
 function matmulSlots(n) {
   if (n.op === 'matmul') return [['a', 0], ['b', 1]];
+  // An attention gradient reads Q, K, V and dO (a0..a3) in its products alone.
+  if (n.op === 'fused' && n.attrs.kind === 'attention-grad') return [['q', 0], ['k', 1], ['v', 2], ['o', 3]];
   if (n.op === 'fused' && n.attrs.kind === 'attention') {
     const b = n.attrs.body;
     const m2 = b.nodes[n.attrs.output];
@@ -929,8 +942,31 @@ function batchPlan(launches, aliases) {
   const placed = new Uint8Array(n);
   const ready = (l) => l.inputs.every((id) => { const w = writer.get(owner(id)); return w === undefined || placed[w] === 1; });
   let units = [];
+  // An attention gradient's three parts (the same operands, none reading another) run as
+  // one launch of their joint kernel, members in the order dQ, dK, dV, where the first
+  // of them stood.
+  const jointOf = (l) => l.kernels.length === 1 && l.kernels[0].joint ? l.kernels[0].joint.name : null;
   for (let i = 0; i < n; i++) {
     if (placed[i]) continue;
+    const jn = jointOf(launches[i]);
+    if (jn) {
+      const parts = new Map();
+      for (let j = i; j < n; j++) {
+        const l = launches[j];
+        if (!placed[j] && jointOf(l) === jn && l.inputs.join() === launches[i].inputs.join() && !parts.has(l.kernels[0].part)) {
+          parts.set(l.kernels[0].part, j);
+        }
+      }
+      const order = launches[i].kernels[0].joint.parts;
+      if (order.every((p) => parts.has(p))) {
+        const group = order.map((p) => parts.get(p));
+        const unit = group.map((j) => launches[j]);
+        unit.joint = launches[i].kernels[0].joint;
+        for (const j of group) placed[j] = 1;
+        units.push(unit);
+        continue;
+      }
+    }
     const group = [i];
     const name = one(launches[i]);
     if (name) {
@@ -1001,6 +1037,13 @@ function batchPlan(launches, aliases) {
   }
   const order = [], batches = [];
   for (const u of units) {
+    if (u.joint) {
+      const j = u.joint;
+      batches.push({ start: order.length, count: u.length, kernels: [{ name: j.name, source: j.source, grid: j.grid, block: j.block, lds: j.lds }],
+        wsStride: 0, joint: true });
+      order.push(...u);
+      continue;
+    }
     if (u.length > 1) {
       const l = u[0];
       batches.push({ start: order.length, count: u.length, kernels: l.kernels.map((k, j) => cg.batchedKernel(u.map((m) => m.kernels[j]), u.length)),

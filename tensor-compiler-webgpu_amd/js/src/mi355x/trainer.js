@@ -20,6 +20,7 @@
 // allocation (arena.js), shared by both programs.
 
 const { fuse } = require('../fusion/fuse');
+const { fuseAttentionTraining } = require('../fusion/attention');
 const { lowerMI355X } = require('./lower');
 
 /**
@@ -73,8 +74,11 @@ function formTransposedProducts(graph, keep, origin, index) {
 function fusedStep(step, options) {
   const o = options || {};
   const keep = [step.loss, step.logits].concat(Object.values(step.outputs));
-  const f = fuse(step.graph, { keep, sabotage: o.passSabotage });
+  let f = fuse(step.graph, { keep, sabotage: o.passSabotage });
   formTransposedProducts(f.graph, new Set(keep.map((id) => f.index.get(id))), f.origin, f.index);
+  // With `attention`, each attention and its gradient take the attention extension's
+  // nodes (fusion/attention.js fuseAttentionTraining); off, the contract's partition.
+  if (o.attention) f = fuseAttentionTraining(f, { keep });
   const at = (id) => f.index.get(id);
   const remap = (m) => { const r = {}; for (const k of Object.keys(m)) r[k] = at(m[k]); return r; };
   const checked = lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning });

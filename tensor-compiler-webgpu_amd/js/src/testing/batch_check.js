@@ -3,34 +3,39 @@
 // batchPlan): the batched launch list must hold the same launches as the plain
 // order, every launch must read only buffers already written (or written by no
 // launch), the members of a batch must be launches of the same kernel texts
-// (or of texts that differ in their operand views alone, each member then run
-// by its own case of the batched kernel) over the same grids (a column sum's
-// text leaves its outer extent to the grid) with no data path between them, each batched kernel's grid must repeat the
+// (or of matmul texts that differ, each member then run by its own case of the
+// batched kernel, which holds exactly its own body) over the same grids (a column
+// sum's text leaves its outer extent to the grid) with no data path between them, or
+// the three parts of one attention gradient in one launch of their joint kernel; each
+// batched kernel's grid must repeat the
 // member kernel's grid once per member along z, and the members' workspace
 // slices must be disjoint and inside the workspace. Checked from the launch
 // records alone, not from the planner's own bookkeeping.
 
-// A kernel's text with its matmul operand view structs (named for the kernel) taken out
-// and its name blanked: members of a batch may differ in how they address their operands
-// only.
-function family(k) {
-  const views = new RegExp(`struct ${k.name}_(?:av|bv|qv|kv|vv) \\{[\\s\\S]*?\\n\\};\\n`, 'g');
-  return k.source.replace(views, '').split(k.name).join('@');
-}
-
 // Whether batched kernel `bk` runs, for member k, the body of kernel `x`: the switch case
-// of k reaches, before its break, a call over a set of structs that the batched text
-// declares exactly as x declares its own (under the batched kernel's name).
+// of k holds, before its break, exactly x's own entry-point body (its statements, with the
+// member's z index read as the batched kernel reads it), over a set of structs that the
+// batched text declares exactly as x declares its own (under the batched kernel's name).
 function runsOwnBody(bk, k, x) {
   const at = bk.source.indexOf(`case ${k}u:`);
   if (at < 0) return false;
   const end = bk.source.indexOf('break;', at);
-  const m = end > at ? bk.source.slice(at, end).match(new RegExp(`(${bk.name}_v\\d+)_av`)) : null;
+  if (end < at) return false;
+  const kase = bk.source.slice(bk.source.indexOf('{', at) + 1, end);
+  const m = kase.match(new RegExp(`(${bk.name}_v\\d+)_(?:av|bv|epi)`));
   if (!m) return false;
   const structs = (src, prefix) => (src.match(new RegExp(`struct ${prefix}_(?:av|bv|epi) \\{[\\s\\S]*?\\n\\};\\n`, 'g')) || [])
     .map((t) => t.split(prefix).join('@')).join('');
   const mine = structs(x.source, x.name);
-  return mine.length > 0 && structs(bk.source, m[1]) === mine;
+  if (!(mine.length > 0 && structs(bk.source, m[1]) === mine)) return false;
+  // The member's own statements: its entry point's body, names and z index normalised.
+  const sig = `${x.name}(const TcmiArgs A) {`;
+  const own = x.source.slice(x.source.indexOf(sig) + sig.length).replace(/\}\s*$/, '');
+  const norm = (t, prefix) => t.split(`${prefix}_`).join('@_')
+    .replace(/\((blockIdx\.z|wg\.z) % \d+u\)/g, '$1')
+    .replace('const tcmi::Wg wg = tcmi::xcd_grouped();', '')
+    .replace(/\s+/g, '');
+  return norm(kase, m[1]) === norm(own, x.name);
 }
 
 function checkBatches(plain, batched) {
@@ -47,6 +52,19 @@ function checkBatches(plain, batched) {
     if (b.start < next || b.count < 2 || b.start + b.count > L.length) return { ok: false, why: `batch at ${b.start} overlaps or is out of range` };
     next = b.start + b.count;
     const first = L[b.start];
+    if (first.kernels.length === 1 && first.kernels[0].joint) {
+      // An attention gradient's three parts in one launch of their joint kernel: members
+      // dQ, dK, dV in that order, of one joint kernel, reading the same operands.
+      const j = first.kernels[0].joint;
+      const ms = L.slice(b.start, b.start + b.count);
+      const ok = b.count === j.parts.length && b.kernels.length === 1 && b.kernels[0].name === j.name
+        && b.kernels[0].source === j.source && b.kernels[0].grid.join() === j.grid.join()
+        && ms.every((l, k) => l.kernels.length === 1 && l.kernels[0].joint && l.kernels[0].joint.name === j.name
+          && l.kernels[0].part === j.parts[k] && l.inputs.join() === first.inputs.join() && !l.workspace);
+      if (!ok) return { ok: false, why: `batch at ${b.start}: not the three parts of one attention gradient` };
+      for (let k = 0; k < b.count; k++) unitOf[b.start + k] = b.start;
+      continue;
+    }
     if (b.kernels.length !== first.kernels.length) return { ok: false, why: `batch at ${b.start}: ${b.kernels.length} batched kernels for ${first.kernels.length}` };
     for (let j = 0; j < b.kernels.length; j++) {
       const g = b.kernels[j].grid, m = first.kernels[j].grid;
@@ -61,8 +79,9 @@ function checkBatches(plain, batched) {
         const y = first.kernels[j];
         if (x.grid.join() !== y.grid.join() || x.block.join() !== y.block.join() || x.lds !== y.lds) return false;
         if (x.name === y.name) return true;
-        // Another text of the same family: the batched kernel must run this member's own body.
-        return family(x) === family(y) && runsOwnBody(b.kernels[j], k, x);
+        // Another matmul text (operand views, load modes, tiling or epilogue differ) over the
+        // same grid and workgroup: the batched kernel must run this member's own body.
+        return /^tcmi_mm_/.test(x.name) && /^tcmi_mm_/.test(y.name) && runsOwnBody(b.kernels[j], k, x);
       });
       if (!same || l.workspace !== first.workspace) return { ok: false, why: `batch at ${b.start}: member ${k} is not a launch of the same kernels` };
       unitOf[b.start + k] = b.start;

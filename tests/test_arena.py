@@ -8,7 +8,8 @@ launch list, which no placement can go under. The GPU side (the trainer with an 
 bit for bit the checked path) is in test_gpu_train.py."""
 
 MODELS = [{"model": "transformer", "B": 64}, {"model": "transformer", "B": 1}, {"model": "mlp"},
-          {"model": "transformer-ref"}]
+          {"model": "transformer-ref"}, {"model": "transformer", "B": 64, "attention": True},
+          {"model": "transformer-ref", "attention": True}]
 
 
 def test_arena_plans_keep_every_value_until_its_last_use(tool):

@@ -8,7 +8,8 @@ front of its operand's writer) must be refused. The GPU side — batched runs bi
 plain ones — is in test_gpu_train.py (config 5's step) and test_gpu_fuzz.py (corpus programs)."""
 
 MODELS = [{"model": "transformer", "B": 64}, {"model": "transformer", "B": 1}, {"model": "mlp"},
-          {"model": "transformer-ref"}]
+          {"model": "transformer-ref"}, {"model": "transformer", "B": 64, "attention": True},
+          {"model": "transformer-ref", "attention": True}]
 
 
 def test_batched_launch_lists_are_valid_orders(tool):

@@ -10,8 +10,10 @@ single-stream results) is in test_gpu_train.py."""
 
 def test_schedules_order_every_dependency(tool):
     res = tool("schedule-check", {"models": [{"model": "transformer", "B": 64}, {"model": "mlp"},
-                                             {"model": "transformer-ref"}], "corpus": {"from": 1, "to": 200}})
-    assert len(res) == 3 * (3 + 400)
+                                             {"model": "transformer-ref"},
+                                             {"model": "transformer", "B": 64, "attention": True}],
+                                  "corpus": {"from": 1, "to": 200}})
+    assert len(res) == 3 * (4 + 400)
     bad = [r for r in res if not r["check"]["ok"]]
     assert not bad, bad[:3]
     c5 = [r for r in res if r["name"] == "transformer-64"]
@@ -21,6 +23,9 @@ def test_schedules_order_every_dependency(tool):
     # mapped views, the MLP's relu applied by the matmuls reading it) on a dependency chain
     # of 200; every stream gets work.
     assert all(r["launches"] == 277 and r["criticalPath"] < 210 and r["used"] == r["streams"] for r in c5), c5
+    # With attention and its gradient fused (fusion/attention.js): 249 launches.
+    c5a = [r for r in res if r["name"] == "transformer-64-attention"]
+    assert all(r["launches"] == 249 and r["used"] == r["streams"] for r in c5a), c5a
 
 
 def test_a_dropped_wait_is_caught(tool):

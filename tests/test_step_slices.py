@@ -7,17 +7,21 @@ the whole launch, bit for bit. A block taken along the wrong axis, a constant ta
 from the twin (the loss scale 1/(B*T)), or a launch whose rows depended on another
 sequence would break the equality."""
 import numpy as np
+import pytest
 
 from oracle import bounds, interp
 from step_slices import (absorb_producers, absorbed_producers, batch_axis, expectations, fold_reductions, fused_values,
                          local, take_block)
 
 
-def test_sequence_blocks_equal_the_whole_launch(tmp_path, tool):
+@pytest.mark.parametrize("attention", [False, True])
+def test_sequence_blocks_equal_the_whole_launch(tmp_path, tool, attention):
+    """With `attention`, the step with attention and its gradient fused
+    (fusion/attention.js): its attention and attention-grad nodes are blocked the same way."""
     import tcmi_bridge
     B = 2
-    tool("step-graph", {"model": "transformer", "B": B}, out=str(tmp_path / "full"))
-    tool("step-graph", {"model": "transformer", "B": 1}, out=str(tmp_path / "twin"))
+    tool("step-graph", {"model": "transformer", "B": B, "attention": attention}, out=str(tmp_path / "full"))
+    tool("step-graph", {"model": "transformer", "B": 1, "attention": attention}, out=str(tmp_path / "twin"))
     fb, tb = tcmi_bridge.Bundle(tmp_path / "full"), tcmi_bridge.Bundle(tmp_path / "twin")
     c = fb.cases[0]
     full, twin = c["fused"], tb.cases[0]["fused"]
@@ -54,7 +58,10 @@ def test_sequence_blocks_equal_the_whole_launch(tmp_path, tool):
             for x in nodes[nid]["attrs"]["body"]["nodes"]:
                 if x["op"] == "const" and isinstance(x["attrs"].get("value"), (int, float)):
                     scales.add(x["attrs"]["value"])
-    assert blocked >= 2 * 300, blocked
+    assert blocked >= 2 * (250 if attention else 300), blocked
+    if attention:
+        kinds = {nodes[n]["attrs"]["kind"] for n in whole if nodes[n]["op"] == "fused"}
+        assert {"attention", "attention-grad"} <= kinds, kinds
     # The step's mean over B*T positions reaches some per-sequence launch as a constant.
     assert any(abs(v * B * 128 - 1) < 1e-12 or abs(v - B * 128) < 1e-9 for v in scales), sorted(scales)[:20]
     # The launches judged whole do not carry the batch, and some read operands that do.
