@@ -76,7 +76,7 @@ function timeLaunches(runner, bench, program, reps) {
     for (const l of members) {
       out.push({ node: l.node, kind: l.kind, pattern: l.pattern || null, code: l.code, bytes: l.bytes, flops: l.flops,
         us: r.stats.one.median / n, minUs: r.stats.one.min / n, maxUs: r.stats.one.max / n, rowFolds: l.rowFolds || null, absorbed: l.absorbed || null,
-        batched: n > 1 ? n : undefined });
+        batched: n > 1 ? n : undefined, joint: b && b.joint ? true : undefined });
     }
     one.destroy();
     i += n;
@@ -130,9 +130,12 @@ function groupVerdicts(f, launchF, launchU) {
       sum.median += u.us; sum.min += u.minUs; sum.max += u.maxUs; launches++;
     }
     if (!launches) continue;
-    const v = verdict(sum, { median: fl.us, min: fl.minUs, max: fl.maxUs });
+    // A group whose launch is one part of a joint launch (an attention gradient's dQ, dK
+    // and dV in one kernel) takes the whole launch's time: the group holds all three.
+    const whole = fl.joint ? fl.batched : 1;
+    const v = verdict(sum, { median: fl.us * whole, min: fl.minUs * whole, max: fl.maxUs * whole });
     groups.push({ sink: g.sink, kind: g.kind, pattern: g.pattern, members: members.size, unfusedLaunches: launches,
-      fusedUs: fl.us, unfusedUs: sum.median, speedup: v.speedup, verdict: v.verdict, folded: folded.length ? folded : undefined });
+      fusedUs: fl.us * whole, unfusedUs: sum.median, speedup: v.speedup, verdict: v.verdict, folded: folded.length ? folded : undefined });
   }
   return groups;
 }

@@ -261,9 +261,12 @@ function fuseAttentionTraining(fused, options) {
       if (kind === 'attention-grad') attrs.part = rep.role;
       out.nodes.push({ id, op: 'fused', inputs: body.operands.map((i) => index.get(i)), attrs, shape: n.shape.slice() });
       const sink = fused.origin[n.id];
-      const members = membersOf(p.groupNodes[rep.role]);
-      newGroups.push({ sink, members, kind, root: sink, pattern: kind });
-      if (rep.role === 'o') attention.push({ sink, members });
+      // The gradient is one group (its three parts run as one launch): dQ's node is its sink.
+      if (rep.role !== 'dk' && rep.role !== 'dv') {
+        const members = membersOf(rep.role === 'o' ? p.groupNodes.o : p.groupNodes.dq.concat(p.groupNodes.dk, p.groupNodes.dv));
+        newGroups.push({ sink, members, kind, root: sink, pattern: kind });
+      }
+      if (rep.role === 'o') attention.push({ sink, members: membersOf(p.groupNodes.o) });
       else {
         let rec = attentionGrad.find((r) => r.plan === p);
         if (!rec) { rec = { plan: p }; attentionGrad.push(rec); }
@@ -368,7 +371,7 @@ function matchTraining(g, m2, liveReaders, last, keepFused) {
   return {
     internal: uniq, replaced, outputs: { o: m2.id, dq: dq.id, dk: dk.id, dv: dv.id },
     forwardBody, gradBody,
-    groupNodes: { o: [m1.id, r1.id, sm.id, pd.id, m2.id], dq: [dp.id, z.id, ds.id, dq.id], dk: [dk.id], dv: [dv.id] },
+    groupNodes: { o: [m1.id, r1.id, sm.id, pd.id, m2.id], dq: [dp.id, z.id, ds.id, dq.id], dk: [dk.id], dv: [dv.id] },   // fused-graph ids
   };
 }
 

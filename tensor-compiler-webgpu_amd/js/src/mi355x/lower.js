@@ -49,6 +49,7 @@ const { size } = require('../ir/shapes');
 const { bodyOf } = require('../fusion/fuse');
 const cg = require('./codegen');
 
+const isReduce = (n) => n.op === 'sum' || n.op === 'max';
 const ELEMENTWISE_OPS = new Set(['add', 'sub', 'mul', 'div', 'neg', 'exp', 'log', 'relu', 'tanh', 'sqrt', 'step', 'stopGradient']);
 const GATHERS = new Set(['broadcast', 'transpose', 'reshape']);
 
@@ -95,24 +96,103 @@ function widenInputs(body, output, folds) {
   return { body: g, output: map.get(output) };
 }
 
+/**
+ * The body of a row-statistics chain `node` with its reductions folded in (`rowFold`, the
+ * plan's records): inputs a{k} at the chain's launch positions, the reductions formed from
+ * their operands (or their producers' bodies), then the chain. Returns { body, output }.
+ */
+function rowFoldBody(graph, node, rowFold) {
+  const folds = rowFold.map((f) => {
+    const fold = { pos: f.pos, op: graph.nodes[f.red].op, attrs: graph.nodes[f.red].attrs,
+      shape: graph.nodes[f.red].shape, inShape: graph.nodes[graph.nodes[f.red].inputs[0]].shape };
+    if (f.prod !== undefined) {
+      // The producer's body, its inputs at the launch positions `ppos`.
+      const p = graph.nodes[f.prod];
+      const one = p.op === 'fused' ? { body: bodyOf(p), output: p.attrs.output } : oneOpBody(graph, p);
+      fold.producer = Object.assign(widenInputs(one.body, one.output, f.prodFolds), { ppos: f.ppos });
+    }
+    return fold;
+  });
+  const chain = node.op === 'fused' ? { body: bodyOf(node), output: node.attrs.output } : oneOpBody(graph, node);
+  return foldReductions(chain.body, chain.output, folds);
+}
+
+/**
+ * The body of row value `u` — a last-axis reduction (its operand as [rows, n], input a0),
+ * or a row-statistics chain with its reductions folded in (`rowFold`) — on its launch's
+ * inputs, as its own launch forms it. Returns { body, output } (output of u's shape).
+ */
+function rowValueBody(graph, u, rowFold) {
+  if (rowFold) return rowFoldBody(graph, u, rowFold);
+  const inShape = graph.nodes[u.inputs[0]].shape;
+  const outer = size(inShape.slice(0, u.attrs.axis)), n = inShape[u.attrs.axis];
+  const g = new Graph();
+  const r = g.emit(u.op, [g.input('a0', [outer, n])], { axis: 1, keepDims: true });
+  return { body: g, output: g.reshape(r, u.shape) };
+}
+
+/**
+ * A reader's body (`w`, its broadcast operands widened) with the row values it forms
+ * (`forms`: [{ value, pos, map, rowFold }]) computed inside it: each value's body inlined
+ * on the reader's own inputs (value input j read from reader input map[j], reshaped to the
+ * rows the value reduces), standing for the reader's inputs at `pos`. Returns { body, output }.
+ */
+function formRowValues(graph, w, forms) {
+  const g = new Graph();
+  const map = new Map();
+  const at = new Map();
+  for (const f of forms) for (const p of f.pos) at.set(p, f);
+  const inputAt = new Map();
+  for (const n of w.body.nodes) {
+    if (n.op !== 'input') continue;
+    const pos = Number(n.attrs.name.slice(1));
+    if (at.has(pos)) continue;
+    const id = g.input(n.attrs.name, n.shape);
+    map.set(n.id, id);
+    inputAt.set(pos, id);
+  }
+  const made = new Map();
+  for (const f of forms) {
+    const vb = rowValueBody(graph, graph.nodes[f.value], f.rowFold);
+    const vm = new Map();
+    for (const n of vb.body.nodes) {
+      if (n.op === 'input') {
+        const src = inputAt.get(f.map[Number(n.attrs.name.slice(1))]);
+        if (src === undefined) throw new Error(`row value ${f.value}: operand ${n.attrs.name} is not among its reader's inputs`);
+        if (size(g.nodes[src].shape) !== size(n.shape)) throw new Error(`row value ${f.value}: operand size differs from its reader's`);
+        vm.set(n.id, g.reshape(src, n.shape));
+      } else {
+        vm.set(n.id, g.emit(n.op, n.inputs.map((i) => vm.get(i)), n.attrs));
+      }
+    }
+    made.set(f, vm.get(vb.output));
+  }
+  for (const n of w.body.nodes) {
+    if (n.op === 'input') {
+      const f = at.get(Number(n.attrs.name.slice(1)));
+      if (f) map.set(n.id, g.reshape(made.get(f), n.shape));
+      continue;
+    }
+    map.set(n.id, g.emit(n.op, n.inputs.map((i) => map.get(i)), n.attrs));
+  }
+  return { body: g, output: map.get(w.output) };
+}
+
 /** Kernels for one node. */
-function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs) {
+function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs, forms) {
+  if (forms) {
+    // A full-size launch that forms the row values it reads (a rowwise kernel: the values'
+    // reductions over the rows it reads anyway, then its own body), with the reductions'
+    // own tuning so the rows are reduced in their order.
+    const base = node.op === 'fused' ? { body: bodyOf(node), output: node.attrs.output } : oneOpBody(graph, node);
+    const f = formRowValues(graph, widenInputs(base.body, base.output, folds), forms);
+    const t = opts.tuning || {};
+    return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(f.body, f.output, { tuning: t.rowreduce || t.row, lastReads })));
+  }
   if (rowFold) {
     // A row-statistics chain with its reductions folded in: the rowwise kernel of the
     // reductions, with their own tuning so the rows are reduced in their order.
-    const folds = rowFold.map((f) => {
-      const fold = { pos: f.pos, op: graph.nodes[f.red].op, attrs: graph.nodes[f.red].attrs,
-        shape: graph.nodes[f.red].shape, inShape: graph.nodes[graph.nodes[f.red].inputs[0]].shape };
-      if (f.prod !== undefined) {
-        // The producer's body, its inputs at the launch positions `ppos`.
-        const p = graph.nodes[f.prod];
-        const one = p.op === 'fused' ? { body: bodyOf(p), output: p.attrs.output } : oneOpBody(graph, p);
-        fold.producer = Object.assign(widenInputs(one.body, one.output, f.prodFolds), { ppos: f.ppos });
-      }
-      return fold;
-    });
-    const chain = node.op === 'fused' ? { body: bodyOf(node), output: node.attrs.output } : oneOpBody(graph, node);
-    const f = foldReductions(chain.body, chain.output, folds);
+    const f = rowFoldBody(graph, node, rowFold);
     const t = opts.tuning || {};
     return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(f.body, f.output, { tuning: t.rowreduce || t.row, lastReads })));
   }
@@ -800,8 +880,84 @@ function lowerOnce(graph, opts, noAbsorb) {
       for (const pos of a.pos) inputs[pos] = pins[0];
       a.ppos.forEach((pos, j) => { inputs[pos] = pins[j]; });
     }
+    // A row value formed by this launch is not read: its slots name one of the buffers it
+    // is formed from (which the launch reads anyway).
+    for (const f of formed.get(node.id) || []) for (const pos of f.pos) inputs[pos] = f.ins[0];
     return inputs;
   };
+  // Row values formed by their readers (perf lowering, with row folds): a row value — a
+  // last-axis reduction, or a row-statistics chain with its reductions folded in — whose
+  // launch reads full-size buffers only, and whose every live reader is a full-size
+  // elementwise or rowwise launch over the same rows (reading the value directly, a
+  // fused body broadcasting it inside, or through a broadcast it reads in place) that
+  // reads every one of those buffers itself, launches nothing. Each reader becomes a
+  // rowwise kernel that forms the value from the buffers it loads anyway — the value's
+  // own launch body, the same reductions over rows of the same length with the same
+  // lanes, so the same bits — and then runs its own body: the value is never written or
+  // read back, and one launch goes (LayerNorm's means, the softmax backward's row sums).
+  // Readers forming values take no producers in (absorbed ones), and a value read at row
+  // size by anything else (a chain, a product) stays a launch.
+  const formed = new Map();   // reader id -> [{ value, pos, ins, map, rowFold }]
+  if (opts.perf && opts.rowFolds !== false && opts.formRows !== false) {
+    const keepSet = new Set(opts.keep);
+    const cons = consumersOf(graph);
+    const lastDim = (shape) => shape[shape.length - 1];
+    for (const u of graph.nodes) {
+      if (!launched(u) || keepSet.has(u.id) || plan.absorbed.has(u.id)) continue;
+      const rowFold = plan.rowFolds.get(u.id) || null;
+      let inShape;
+      if (rowFold) inShape = graph.nodes[graph.nodes[rowFold[0].red].inputs[0]].shape;
+      else if ((u.op === 'sum' || u.op === 'max') && u.attrs.keepDims) {
+        inShape = graph.nodes[u.inputs[0]].shape;
+        if (size(inShape.slice(u.attrs.axis + 1)) !== 1 || inShape[u.attrs.axis] === 1) continue;
+      } else continue;
+      const n = lastDim(inShape), full = size(inShape);
+      if (size(u.shape) * n !== full) continue;
+      const ins = inputsOf(u);
+      if (!ins.length || !ins.every((id) => size(graph.nodes[id].shape) === full)) continue;
+      // Its readers and the positions at which each reads it.
+      const readers = new Map();
+      let ok = true;
+      for (const c of new Set(cons[u.id])) {
+        const cn = graph.nodes[c];
+        if (plan.dead.has(c)) continue;
+        if (cn.op === 'broadcast' && plan.folded.has(c)) {
+          for (const r of new Set(cons[c])) {
+            if (plan.dead.has(r)) continue;
+            const bf = plan.broadcasts.get(r);
+            const pos = bf ? Array.from(bf.entries()).filter(([, f]) => f.source === u.id).map(([q]) => q) : [];
+            if (!pos.length) { ok = false; break; }
+            readers.set(r, (readers.get(r) || []).concat(pos));
+          }
+        } else if (cn.op === 'fused' && (cn.attrs.kind === 'elementwise' || cn.attrs.kind === 'rowwise')) {
+          const pos = cn.inputs.map((i, q) => (i === u.id ? q : -1)).filter((q) => q >= 0);
+          readers.set(c, (readers.get(c) || []).concat(pos));
+        } else ok = false;
+        if (!ok) break;
+      }
+      if (!ok || !readers.size) continue;
+      const plans = [];
+      for (const [r, pos] of readers) {
+        const rn = graph.nodes[r];
+        const kind = rn.op === 'fused' ? rn.attrs.kind : ELEMENTWISE_OPS.has(rn.op) ? 'elementwise' : null;
+        if (!(kind === 'elementwise' || kind === 'rowwise') || !launched(rn) || plan.rowFolds.has(r) || plan.absorbed.has(r)
+          || plan.views.has(r) || size(rn.shape) !== full || lastDim(rn.shape) !== n) { ok = false; break; }
+        if (kind === 'rowwise' && bodyOf(rn).nodes.some((x) => isReduce(x) && lastDim(bodyOf(rn).nodes[x.inputs[0]].shape) !== n)) { ok = false; break; }
+        const rIns = inputsOf(rn);
+        const bf = plan.broadcasts.get(r);
+        const taken = new Set(pos.concat((formed.get(r) || []).flatMap((f) => f.pos)));
+        const map = ins.map((id) => rIns.findIndex((x, q) => x === id && !taken.has(q) && !(bf && bf.has(q))));
+        if (map.some((q) => q < 0)) { ok = false; break; }
+        plans.push({ r, pos: Array.from(new Set(pos)).sort((a, b) => a - b), map });
+      }
+      if (!ok) continue;
+      plan.folded.add(u.id);
+      for (const q of plans) {
+        if (!formed.has(q.r)) formed.set(q.r, []);
+        formed.get(q.r).push({ value: u.id, pos: q.pos, ins, map: q.map, rowFold });
+      }
+    }
+  }
   // Last reads (perf lowering): an elementwise or rowwise kernel loads a full-size operand of
   // STREAM_FROM bytes or more non-temporally where no later launch of the list reads
   // that buffer, so data read for the last time streams past the caches instead of
@@ -847,6 +1003,13 @@ function lowerOnce(graph, opts, noAbsorb) {
     const absorbSig = (a) => [a.pos, prodKey({ prod: a.prod, ppos: a.ppos, prodFolds: a.prodFolds }),
       a.nested ? a.nested.map(absorbSig) : null];
     const absorbKey = absorbs ? absorbs.map(absorbSig) : null;
+    const forms = formed.get(node.id) || null;
+    const rowSig = (rf) => rf.map((f) => [f.pos, graph.nodes[f.red].op, graph.nodes[f.red].attrs,
+      graph.nodes[graph.nodes[f.red].inputs[0]].shape, prodKey(f)]);
+    const formKey = forms ? forms.map((f) => {
+      const u = graph.nodes[f.value];
+      return [f.pos, f.map, u.op, u.attrs, u.shape, u.inputs.map((i) => graph.nodes[i].shape), f.rowFold ? rowSig(f.rowFold) : null];
+    }) : null;
     const inputs = inputsOf(node);
     const lastReads = [];
     inputs.forEach((id, pos) => {
@@ -856,11 +1019,11 @@ function lowerOnce(graph, opts, noAbsorb) {
     // reads only: reuse across identical nodes.
     const peers = peersOf(node);
     const key = JSON.stringify([node.op, node.inputs.map((id) => graph.nodes[id].shape), node.attrs, node.shape,
-      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey, rowKey, lastReads, peers, absorbKey]);
+      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey, rowKey, lastReads, peers, absorbKey, formKey]);
     let k = cache.get(key);
     if (!k) {
       try {
-        k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs);
+        k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs, forms);
       } catch (e) {
         if (e instanceof cg.ParamOverflow && absorbs) e.reader = node.id;
         throw e;
@@ -877,6 +1040,13 @@ function lowerOnce(graph, opts, noAbsorb) {
       // The reduction folded into this launch, and the launch's own body (for node-local checks).
       launches[launches.length - 1].rowFolds = rowFold.map((f) => (f.prod === undefined ? { reduction: f.red, pos: f.pos }
         : { reduction: f.red, pos: f.pos, producer: f.prod, producerPos: f.ppos }));
+    }
+    if (forms) {
+      // The row values this launch forms (for node-local checks): each value, the positions
+      // it stands for, and the reader positions of its operands; a chain's folded reductions.
+      launches[launches.length - 1].formedRows = forms.map((f) => Object.assign({ value: f.value, pos: f.pos, map: f.map },
+        f.rowFold ? { rowFolds: f.rowFold.map((x) => (x.prod === undefined ? { reduction: x.red, pos: x.pos }
+          : { reduction: x.red, pos: x.pos, producer: x.prod, producerPos: x.ppos })) } : {}));
     }
     if (absorbs) {
       // The producers this launch forms in place of loading them (for node-local checks).

@@ -86,7 +86,7 @@ function fusedStep(step, options) {
     : o.contract ? lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning, perf: true, keep: keep.map(at), batch: o.batch,
       rowFolds: false, absorb: false, loadOps: false })
       : lowerMI355X(f.graph, { sabotage: o.sabotage, tuning: o.tuning, perf: true, keep: keep.map(at), batch: o.batch, absorb: true,
-        loadOps: o.loadOps });
+        loadOps: o.loadOps, formRows: o.formRows });
   return Object.assign({}, step, {
     graph: f.graph, fusion: f, original: step.graph,
     loss: at(step.loss), logits: at(step.logits),

@@ -197,9 +197,83 @@ def absorb_producers(graph, node_id, absorbed):
     return dict(node, op="fused", attrs=attrs, inputs=inputs), inputs
 
 
-def restate(graph, node_id, folds=None, absorbed=None):
-    """The launch of node `node_id` as the perf lowering runs it: its row folds or its
-    absorbed producers restated (a launch has one or the other), or the node itself."""
+def form_rows(graph, node_id, formed):
+    """A launch of the perf lowering that forms the row values it reads (its record's
+    formedRows: [{value, pos, map, rowFolds?}]): the reader as a fused node whose body
+    computes each value — the value node itself (a last-axis reduction) or, for a
+    row-statistics chain, the chain with its reductions taken in (fold_reductions) — on the
+    reader's own inputs (value operand j read from reader input map[j], reshaped to the
+    value's operand shape), standing for the reader's inputs at `pos` (broadcast to their
+    shape where the reader read the value through a broadcast). The reader's operands at
+    `pos` become the value's first operand (the launch reads no value buffer). Restated
+    here from the lowering's rule."""
+    node = graph["nodes"][node_id]
+    body, out = _producer_body(graph, node)
+    at = {p: f for f in formed for p in f["pos"]}
+    inputs = list(node["inputs"])
+    new, where, input_at = [], {}, {}
+    for bid, b in enumerate(body):
+        if b["op"] == "input" and int(b["attrs"]["name"][1:]) not in at:
+            new.append(dict(b))
+            where[bid] = input_at[int(b["attrs"]["name"][1:])] = len(new) - 1
+    made = {}
+    for f in formed:
+        vnode, vins = fold_reductions(graph, f["value"], f.get("rowFolds"))
+        vbody, vout = _producer_body(graph, vnode)
+        vwhere = {}
+        for vbid, vb in enumerate(vbody):
+            if vb["op"] == "input":
+                j = int(vb["attrs"]["name"][1:])
+                src = input_at[f["map"][j]]
+                if new[src]["shape"] != vb["shape"]:
+                    new.append({"op": "reshape", "inputs": [src], "attrs": {"shape": vb["shape"]}, "shape": vb["shape"]})
+                    src = len(new) - 1
+                vwhere[vbid] = src
+            else:
+                new.append(dict(vb, inputs=[vwhere[i] for i in vb["inputs"]]))
+                vwhere[vbid] = len(new) - 1
+        made[f["value"]] = (vwhere[vout], vins)
+    for bid, b in enumerate(body):
+        if b["op"] == "input" and int(b["attrs"]["name"][1:]) in at:
+            v, _ = made[at[int(b["attrs"]["name"][1:])]["value"]]
+            if new[v]["shape"] != b["shape"]:
+                value_shape = graph["nodes"][at[int(b["attrs"]["name"][1:])]["value"]]["shape"]
+                assert new[v]["shape"] == value_shape
+                new.append({"op": "broadcast", "inputs": [v], "attrs": {"shape": b["shape"]}, "shape": b["shape"]})
+                v = len(new) - 1
+            where[bid] = v
+    for bid, b in enumerate(body):
+        if b["op"] != "input":
+            new.append(dict(b, inputs=[where[i] for i in b["inputs"]]))
+            where[bid] = len(new) - 1
+    for p, f in at.items():
+        inputs[p] = made[f["value"]][1][0]
+    attrs = dict(node["attrs"]) if node["op"] == "fused" else {"kind": "rowwise", "pattern": "rowwise"}
+    attrs = dict(attrs, body={"nodes": new}, output=where[out])
+    return dict(node, op="fused", attrs=attrs, inputs=inputs), inputs
+
+
+def formed_values(formed):
+    """The row values, and the reductions and producers folded into them, that the launches
+    of {reader: [formedRows records]} form."""
+    values, reductions, producers = set(), set(), set()
+    for records in formed.values():
+        for f in records:
+            values.add(f["value"])
+            for x in f.get("rowFolds") or []:
+                reductions.add(x["reduction"])
+                if "producer" in x:
+                    producers.add(x["producer"])
+    return values, reductions, producers
+
+
+def restate(graph, node_id, folds=None, absorbed=None, formed=None):
+    """The launch of node `node_id` as the perf lowering runs it: its row folds, its
+    absorbed producers or the row values it forms restated (a launch has one of them), or
+    the node itself."""
+    if formed:
+        assert not folds and not absorbed
+        return form_rows(graph, node_id, formed)
     if absorbed:
         assert not folds
         return absorb_producers(graph, node_id, absorbed)
@@ -241,22 +315,25 @@ def local(graph, node, operands: List[np.ndarray]):
     return r["values"][out], r["bounds"][out]
 
 
-def expectations(full, twin, launched, operand, sequences, row_folds=None, absorbed=None):
+def expectations(full, twin, launched, operand, sequences, row_folds=None, absorbed=None, formed=None):
     """Yield (node id, sequence index or None, value, bound) for every launched node:
     per sequence where its output carries the batch axis, whole otherwise.
     `operand(i, s)` is node i's value: its block for sequence index s, or whole for None.
     `row_folds` ({node id: [{reduction, pos}]}, a perf lowering's): those launches are the
     chain with its row reductions taken in, on the reductions' operands; `absorbed`
-    ({node id: [{producer, pos, producerPos}]}): those launches form their producers."""
+    ({node id: [{producer, pos, producerPos}]}): those launches form their producers;
+    `formed` ({node id: [formedRows records]}): those launches form the row values they read."""
     axis = [batch_axis(n["shape"], t["shape"]) for n, t in zip(full["nodes"], twin["nodes"])]
     row_folds = row_folds or {}
     absorbed = absorbed or {}
+    formed = formed or {}
     for nid in launched:
         folds = row_folds.get(nid) or row_folds.get(str(nid))
         took = absorbed.get(nid) or absorbed.get(str(nid))
-        node, ins = restate(full, nid, folds, took)
+        rows = formed.get(nid) or formed.get(str(nid))
+        node, ins = restate(full, nid, folds, took, rows)
         if axis[nid] >= 0:
-            tn = merge_twin(node, restate(twin, nid, folds, took)[0])
+            tn = merge_twin(node, restate(twin, nid, folds, took, rows)[0])
             for s in range(len(sequences)):
                 ops = [operand(i, s if axis[i] >= 0 else None) for i in ins]
                 v, e = local(twin, tn, ops)
@@ -287,26 +364,32 @@ def judge_case(fused, fused_vals, gc, arr):
     # operands formed in the same launches, are the other launches it skips.
     folds = {int(k): v for k, v in gc["rowFolds"].items()}
     took = {int(k): v for k, v in gc["absorbed"].items()}
+    rows = {int(k): v for k, v in gc.get("formedRows", {}).items()}
     reductions = {f["reduction"] for fs in folds.values() for f in fs}
     producers = {f["producer"] for fs in folds.values() for f in fs if "producer" in f}
     producers |= absorbed_producers(took)
+    # Row values formed by their readers, with what their own launches would fold.
+    values, value_reductions, value_producers = formed_values(rows)
+    assert all(fused["nodes"][i]["op"] not in ("matmul", "input", "const") for i in values)
+    reductions |= {i for i in values if fused["nodes"][i]["op"] in ("sum", "max")} | value_reductions
+    producers |= value_producers
     # Relus the matmuls reading them apply as they load their operand.
     on_load = {o["node"] for ops in gc["loadOps"].values() for o in ops}
     nodes = fused["nodes"]
     assert all(nodes[i]["op"] == "relu" for i in on_load)
     assert all(nodes[i]["op"] in ("reshape", "transpose", "broadcast")
-               for i in skipped - set(gc["dead"]) - reductions - producers - on_load)
+               for i in skipped - set(gc["dead"]) - reductions - producers - on_load - values)
     assert all(nodes[i]["op"] in ("sum", "max") for i in reductions)
     assert all(nodes[i]["op"] not in ("sum", "max", "matmul") for i in producers)
     # A chain with its reductions folded in is judged as the launch it is: the reductions and
     # the chain on the reductions' operands.
     pexp, pbound = {}, {}
     for k in perf:
-        if k in folds or k in took:
-            node, ins = restate(fused, k, folds.get(k), took.get(k))
+        if k in folds or k in took or k in rows:
+            node, ins = restate(fused, k, folds.get(k), took.get(k), rows.get(k))
             pexp[k], pbound[k] = local(fused, node, [fused_vals[i] for i in ins])
         else:
             pexp[k], pbound[k] = expected[k], bound[k]
     jp = bounds.judge_local(fused, perf, pexp, pbound)
-    jp["skipped"], jp["chains"] = len(skipped), len(folds)
+    jp["skipped"], jp["chains"], jp["formed"] = len(skipped), len(folds), len(values)
     return j, jp

@@ -220,6 +220,17 @@ def test_perf_lowering_views_address_the_operands(tool, req):
     reductions = {f["reduction"] for fs in d["rowFolds"].values() for f in fs}
     producers = {f["producer"] for fs in d["rowFolds"].values() for f in fs if "producer" in f}
     absorbed = set()
+    # Row values formed by their readers: a last-axis reduction, or a row-statistics chain
+    # with its reductions (and their producers) folded in, that every live reader forms.
+    formed, formers = set(), {}
+    for reader, records in d["formedRows"].items():
+        for f in records:
+            formed.add(f["value"])
+            formers.setdefault(f["value"], set()).add(int(reader))
+            for x in f.get("rowFolds") or []:
+                reductions.add(x["reduction"])
+                if "producer" in x:
+                    producers.add(x["producer"])
 
     takers = {}
 
@@ -260,7 +271,21 @@ def test_perf_lowering_views_address_the_operands(tool, req):
         for l in d["launches"]:
             named = any(v.get("opNode") == relu for v in (l["views"] or {}).values())
             assert named == (l["node"] in readers), (relu, l["node"])
-    assert all(nodes[i]["op"] in ("transpose", "broadcast") for i in set(d["folded"]) - reductions - producers - absorbed - set(on_load))
+    assert all(nodes[i]["op"] in ("transpose", "broadcast")
+               for i in set(d["folded"]) - reductions - producers - absorbed - set(on_load) - formed)
+    # A formed value is kept by nobody, and every live reader of it (directly, or through a
+    # broadcast read in place) forms it.
+    for v, by in formers.items():
+        assert v not in d["keep"] and (nodes[v]["op"] in ("sum", "max", "fused") or nodes[v]["op"] in ELEMENTWISE)
+        readers = set()
+        for c in consumers[v] - set(d["dead"]):
+            if nodes[c]["op"] == "broadcast" and c in d["folded"]:
+                readers |= consumers[c] - set(d["dead"])
+            else:
+                readers.add(c)
+        assert readers == by, (v, readers, by)
+    if req["model"] == "transformer":
+        assert len(formed) >= 18, len(formed)
     # A folded broadcast is read by elementwise, rowwise or epilogue bodies only (never
     # by a reduction, a gather or as a matmul operand), through the broadcast's source.
     for chain, fs in d["rowFolds"].items():
@@ -271,7 +296,7 @@ def test_perf_lowering_views_address_the_operands(tool, req):
             assert r["op"] in ("sum", "max") and r["shape"] != nodes[r["inputs"][0]]["shape"]
             assert f["reduction"] not in d["keep"] and all(c["inputs"][p] == f["reduction"] for p in f["pos"])
             # Every launched consumer of a folded reduction takes it in.
-            assert all(str(u) in d["rowFolds"] for u in consumers[f["reduction"]] if u not in d["dead"])
+            assert all(str(u) in d["rowFolds"] or u in formed for u in consumers[f["reduction"]] if u not in d["dead"])
             if "producer" in f:
                 # A producer formed in the launch: an elementwise node of the reduction's
                 # 2-D operand shape, read by the reduction alone, kept by nobody.

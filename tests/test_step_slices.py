@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from oracle import bounds, interp
-from step_slices import (absorb_producers, absorbed_producers, batch_axis, expectations, fold_reductions, fused_values,
+from step_slices import (absorb_producers, absorbed_producers, batch_axis, expectations, fold_reductions, form_rows, fused_values,
                          local, take_block)
 
 
@@ -155,3 +155,45 @@ def test_absorbed_producers_are_formed_as_computed(tool):
         rv, re_ = _unabsorbed(graph, k, records, [(o.astype(np.float64), np.zeros(o.size)) for o in ops])
         assert np.array_equal(v, rv) and np.all(np.isfinite(v)), k
         assert np.array_equal(e, re_), k
+
+
+@pytest.mark.parametrize("req", [{"model": "transformer", "B": 1}, {"model": "transformer", "B": 1, "attention": True}])
+def test_formed_row_values_are_the_value_then_the_reader(tool, req):
+    """The perf lowering lets a full-size launch form the row values it reads (LayerNorm's
+    means and its backward's row statistics: a last-axis reduction, or a row-statistics
+    chain with its reductions folded in), from the rows it loads anyway. The checkers'
+    restatement of such a launch (form_rows), evaluated in float64 on the launch's
+    operands, equals the value's own launch evaluated first (fold_reductions) and the
+    reader's body applied to it, bit for bit, value and bound."""
+    d = tool("perf-lower", req)
+    graph, rows = d["graph"], {int(k): v for k, v in d["formedRows"].items()}
+    assert len(rows) >= 18, len(rows)
+    formed = {f["value"] for fs in rows.values() for f in fs}
+    assert formed <= set(d["folded"])
+    rng = np.random.default_rng(5)
+    for k, records in rows.items():
+        node, ins = form_rows(graph, k, records)
+        ops = [rng.uniform(0.5, 2.0, size=interp.size(graph["nodes"][i]["shape"])).astype(np.float32) for i in ins]
+        v, e = local(graph, node, ops)
+        # The unformed way: each value's own launch on its operands (the reader's, at map),
+        # then the reader's body with the value in its place (broadcast where it read one).
+        reader = graph["nodes"][k]
+        carried = {f"a{p}": (o.astype(np.float64), np.zeros(o.size)) for p, o in enumerate(ops)}
+        for f in records:
+            vnode, vins = fold_reductions(graph, f["value"], f.get("rowFolds"))
+            vv, ve = local(graph, vnode, [ops[q] for q in f["map"]])
+            for p in f["pos"]:
+                src = graph["nodes"][reader["inputs"][p]]
+                if src["op"] == "broadcast":
+                    vv_, ve_ = interp.k_broadcast(vv, graph["nodes"][f["value"]]["shape"], src["shape"]), \
+                        interp.k_broadcast(ve, graph["nodes"][f["value"]]["shape"], src["shape"])
+                    carried[f"a{p}"] = (vv_, ve_)
+                else:
+                    carried[f"a{p}"] = (vv, ve)
+        if reader["op"] == "fused":
+            body, out = reader["attrs"]["body"], reader["attrs"]["output"]
+        else:
+            body, out = bounds.one_op_graph(graph, reader)
+        r = bounds.reference_with_bounds(body, {}, carried=carried)
+        assert np.array_equal(v, r["values"][out]) and np.all(np.isfinite(v)), k
+        assert np.array_equal(e, r["bounds"][out]), k
