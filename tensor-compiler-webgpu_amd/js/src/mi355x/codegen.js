@@ -249,7 +249,9 @@ function elementwiseKernel(b, output, outShape, opts) {
   const n = size(outShape);
   const large = n >= 2 ** 25;
   const U = tune.unroll || (large ? 2 : 1);
-  const nt = tune.nt === undefined ? true : !!tune.nt;
+  // Non-temporal stores unless the lowering says the next launch reads the output
+  // (streamOut false), which then finds it in the caches; tuning nt forces either way.
+  const nt = tune.nt === undefined ? o.streamOut !== false : !!tune.nt;
   // Non-temporal loads: every full-size operand (tuning ntl), or those at the positions
   // `o.lastReads` lists (the lowering's last reads of their buffers).
   const ntlAt = new Set(tune.ntl ? [] : (o.lastReads || []));
@@ -384,6 +386,10 @@ function rowwiseKernel(b, output, opts) {
   // Operand positions whose full-size loads are the lowering's last reads of their
   // buffers: loaded non-temporally (row length a multiple of 4 only).
   const streamed = new Set(o.lastReads || []);
+  // Full-size output that the next launch does not read: stored non-temporally, so it
+  // does not displace data that launch reads from the caches (tuning nto forces either way).
+  const tuneRow = o.tuning || {};
+  const ntOut = tuneRow.nto === undefined ? o.streamOut === true : !!tuneRow.nto;
   checkOperands(b);
   const reductions = b.nodes.filter(isReduce);
   if (!reductions.length) throw new Error('rowwise kernel without a reduction');
@@ -545,7 +551,8 @@ for (int s = 0; s < ${E}; ++s) {
 ${indent(inner, '      ')}
       o4[l] = ${v};
     }
-    reinterpret_cast<float4*>(A.out + rowBase)[c0 >> 2] = make_float4(o4[0], o4[1], o4[2], o4[3]);
+    ${ntOut ? '__builtin_nontemporal_store(tcmi::f4{o4[0], o4[1], o4[2], o4[3]}, reinterpret_cast<tcmi::f4*>(A.out + rowBase) + (c0 >> 2));'
+    : 'reinterpret_cast<float4*>(A.out + rowBase)[c0 >> 2] = make_float4(o4[0], o4[1], o4[2], o4[3]);'}
   }
 }`];
     } else {

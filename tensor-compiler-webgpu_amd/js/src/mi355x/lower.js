@@ -179,7 +179,7 @@ function formRowValues(graph, w, forms) {
 }
 
 /** Kernels for one node. */
-function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs, forms) {
+function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs, forms, streamOut) {
   if (forms) {
     // A full-size launch that forms the row values it reads (a rowwise kernel: the values'
     // reductions over the rows it reads anyway, then its own body), with the reductions'
@@ -187,14 +187,14 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers,
     const base = node.op === 'fused' ? { body: bodyOf(node), output: node.attrs.output } : oneOpBody(graph, node);
     const f = formRowValues(graph, widenInputs(base.body, base.output, folds), forms);
     const t = opts.tuning || {};
-    return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(f.body, f.output, { tuning: t.rowreduce || t.row, lastReads })));
+    return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(f.body, f.output, { tuning: t.rowreduce || t.row, lastReads, streamOut })));
   }
   if (rowFold) {
     // A row-statistics chain with its reductions folded in: the rowwise kernel of the
     // reductions, with their own tuning so the rows are reduced in their order.
     const f = rowFoldBody(graph, node, rowFold);
     const t = opts.tuning || {};
-    return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(f.body, f.output, { tuning: t.rowreduce || t.row, lastReads })));
+    return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(f.body, f.output, { tuning: t.rowreduce || t.row, lastReads, streamOut })));
   }
   if (node.op === 'fused') {
     const w = absorbProducers(graph, widenInputs(bodyOf(node), node.attrs.output, folds), absorbs);
@@ -205,10 +205,10 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers,
     const sab = { sabotage: opts.sabotage, pattern: node.attrs.pattern };
     if (kind === 'elementwise') {
       return Object.assign({ kind: 'fused-elementwise' },
-        single(cg.elementwiseKernel(b, out, node.shape, Object.assign({ tuning: tuning.ew, lastReads }, sab))));
+        single(cg.elementwiseKernel(b, out, node.shape, Object.assign({ tuning: tuning.ew, lastReads, streamOut }, sab))));
     }
     if (kind === 'rowwise') {
-      return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(b, out, Object.assign({ tuning: tuning.row, lastReads }, sab))));
+      return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(b, out, Object.assign({ tuning: tuning.row, lastReads, streamOut }, sab))));
     }
     if (kind === 'epilogue') {
       return Object.assign({ kind: 'fused-epilogue' }, single(cg.gemmKernel(b, out, Object.assign({ tuning: tuning.gemm, peers }, sab, mmViews))));
@@ -231,7 +231,7 @@ function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers,
     const one = oneOpBody(graph, node);
     const { body, output } = absorbProducers(graph, widenInputs(one.body, one.output, folds), absorbs);
     const kind = GATHERS.has(node.op) ? 'gather' : 'elementwise';
-    return Object.assign({ kind }, single(cg.elementwiseKernel(body, output, node.shape, { tuning: (opts.tuning || {}).ew, lastReads })));
+    return Object.assign({ kind }, single(cg.elementwiseKernel(body, output, node.shape, { tuning: (opts.tuning || {}).ew, lastReads, streamOut })));
   }
   if (node.op === 'sum' || node.op === 'max') {
     const inShape = graph.nodes[node.inputs[0]].shape;
@@ -980,6 +980,20 @@ function lowerOnce(graph, opts, noAbsorb) {
   const peersOf = (node) => (readers.has(node.id) ? 1 : productPeers.get(productKey(graph, node)) || 1);
   const lastRead = new Map();
   if (opts.perf) for (const node of graph.nodes) if (launched(node)) for (const id of inputsOf(node)) lastRead.set(id, node.id);
+  // Output stores (perf lowering), a hint like the last reads: an output the next launch of
+  // the list reads is stored through the caches, where that launch finds it (false); one of
+  // STREAM_FROM bytes or more that it does not read is stored non-temporally, so it does not
+  // displace what that launch reads (true). Elementwise kernels store non-temporally unless
+  // false, rowwise kernels only if true.
+  const streamOut = new Map();
+  if (opts.perf) {
+    const order = graph.nodes.filter(launched);
+    order.forEach((node, i) => {
+      const next = order[i + 1];
+      if (next && inputsOf(next).includes(node.id)) streamOut.set(node.id, false);
+      else if (size(node.shape) * 4 >= STREAM_FROM) streamOut.set(node.id, true);
+    });
+  }
   for (const node of graph.nodes) {
     if (!launched(node)) continue;
     const v = plan.views.get(node.id);
@@ -1019,11 +1033,12 @@ function lowerOnce(graph, opts, noAbsorb) {
     // reads only: reuse across identical nodes.
     const peers = peersOf(node);
     const key = JSON.stringify([node.op, node.inputs.map((id) => graph.nodes[id].shape), node.attrs, node.shape,
-      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey, rowKey, lastReads, peers, absorbKey, formKey]);
+      node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey, rowKey, lastReads, peers, absorbKey, formKey,
+      streamOut.get(node.id)]);
     let k = cache.get(key);
     if (!k) {
       try {
-        k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs, forms);
+        k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs, forms, streamOut.get(node.id));
       } catch (e) {
         if (e instanceof cg.ParamOverflow && absorbs) e.reader = node.id;
         throw e;

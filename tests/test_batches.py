@@ -31,7 +31,7 @@ def test_planted_batch_mistakes_are_caught(tool):
     batching two such launches by name alone once ran one member over the other's grid,
     which the GPU fuzz test caught as a canary overwrite and as perf-lowering
     differences in 3 of 4000 corpus graphs)."""
-    res = tool("batch-check", {"models": MODELS[:1], "corpus": {"from": 1, "to": 500}, "plant": True})
+    res = tool("batch-check", {"models": MODELS[:1], "corpus": {"from": 1, "to": 900}, "plant": True})
     dep = [r for r in res if "dependent" in r]
     early = [r for r in res if "early" in r]
     grid = [r for r in res if "grid" in r]
