@@ -649,6 +649,7 @@ async function gpuWorkloads(req, dir) {
         out.origin = f.origin;
         out.nodes = graph.nodes.map((n) => bundle.put(rf.values[n.id]));
         out.canaryPlain = rf.canaryIntact.every(Boolean);
+        out.plainLaunches = lf.launches.length;
       }
       entry.variants[v] = out;
     }
@@ -804,7 +805,7 @@ async function gpuLocal(req, dir) {
     }
     entry.canaryIntact = lowerings.every(([key]) => entry[`${key}Canary`]);
     entry.rowFolds = rowFoldsOf(fs.lowered);
-    entry.formedRows = formedRowsOf(fs.lowered);
+    entry.formed = formedOf(fs.lowered);
     entry.absorbed = absorbedOf(fs.lowered);
     entry.loadOps = loadOpsOf(fs.lowered);
     entry.aliases = fs.lowered.aliases;
@@ -985,7 +986,7 @@ async function gpuStepSlices(req, dir) {
     loss: r.values[fs.loss][0], dispatchKinds: fs.lowered.launches.map((l) => l.kind),
     splitK: fs.lowered.launches.filter((l) => l.kernels.some((k) => /_red$/.test(k.name))).length,
     batches: (fs.lowered.batches || []).length, aliases: fs.lowered.aliases, folded: fs.lowered.folded, dead: fs.lowered.dead,
-    rowFolds: rowFoldsOf(fs.lowered), absorbed: absorbedOf(fs.lowered), formedRows: formedRowsOf(fs.lowered) });
+    rowFolds: rowFoldsOf(fs.lowered), absorbed: absorbedOf(fs.lowered), formed: formedOf(fs.lowered) });
   bundle.close({ device: runner.info() });
 }
 
@@ -1016,10 +1017,10 @@ function absorbedOf(lowered) {
   return out;
 }
 
-/** {reader node: [{ value, pos, map, rowFolds? }]}: the row values a perf lowering's launches form. */
-function formedRowsOf(lowered) {
+/** {reader node: [{ value, rowFolds?, absorbed? }]}: the values a perf lowering's launches form. */
+function formedOf(lowered) {
   const out = {};
-  for (const l of lowered.launches) if (l.formedRows) out[l.node] = l.formedRows;
+  for (const l of lowered.launches) if (l.formed) out[l.node] = l.formed;
   return out;
 }
 
@@ -1484,7 +1485,7 @@ async function main() {
       }
       const l = lowerMI355X(g, { perf: true, keep, absorb });
       const plain = new Map(lowerMI355X(g).launches.map((x) => [x.node, x]));
-      out = { graph: g.toJSON(), keep, aliases: l.aliases, folded: l.folded, dead: l.dead, rowFolds: rowFoldsOf(l), absorbed: absorbedOf(l), formedRows: formedRowsOf(l), loadOps: loadOpsOf(l),
+      out = { graph: g.toJSON(), keep, aliases: l.aliases, folded: l.folded, dead: l.dead, rowFolds: rowFoldsOf(l), absorbed: absorbedOf(l), formed: formedOf(l), loadOps: loadOpsOf(l),
         launches: l.launches.map((x) => ({ node: x.node, kind: x.kind, inputs: x.inputs, params: x.params.length, views: x.views || null, modes: gemmModes(x),
           split: gemmSplit(x), plainSplit: gemmSplit(plain.get(x.node)) })),
         batches: (l.batches || []).map((b) => ({ start: b.start, count: b.count, joint: !!b.joint, kernels: b.kernels.map((k) => k.name) })) };

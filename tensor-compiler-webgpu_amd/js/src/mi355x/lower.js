@@ -118,76 +118,105 @@ function rowFoldBody(graph, node, rowFold) {
 }
 
 /**
- * The body of row value `u` — a last-axis reduction (its operand as [rows, n], input a0),
- * or a row-statistics chain with its reductions folded in (`rowFold`) — on its launch's
- * inputs, as its own launch forms it. Returns { body, output } (output of u's shape).
+ * The body a launch of `node` runs in the perf lowering before it forms any value it reads
+ * (lowerNode's elementwise, rowwise, row-statistics-chain and row-reduction kernels), on
+ * inputs a{k} at its operand positions: a row-statistics chain with its reductions folded
+ * in; a fused elementwise or rowwise body, or one elementwise op, with its broadcast
+ * operands widened and its absorbed producers formed; a reduction over the last
+ * non-trivial axis on its operand as [rows, n] rows (its producers formed), reshaped to
+ * its own shape. Returns { body, output }, or null for other launches.
  */
-function rowValueBody(graph, u, rowFold) {
-  if (rowFold) return rowFoldBody(graph, u, rowFold);
-  const inShape = graph.nodes[u.inputs[0]].shape;
-  const outer = size(inShape.slice(0, u.attrs.axis)), n = inShape[u.attrs.axis];
-  const g = new Graph();
-  const r = g.emit(u.op, [g.input('a0', [outer, n])], { axis: 1, keepDims: true });
-  return { body: g, output: g.reshape(r, u.shape) };
+function launchBase(graph, node, folds, rowFold, absorbs) {
+  if (rowFold) return rowFoldBody(graph, node, rowFold);
+  if (node.op === 'fused') {
+    if (node.attrs.kind !== 'elementwise' && node.attrs.kind !== 'rowwise') return null;
+    return absorbProducers(graph, widenInputs(bodyOf(node), node.attrs.output, folds), absorbs);
+  }
+  if (ELEMENTWISE_OPS.has(node.op)) {
+    const one = oneOpBody(graph, node);
+    return absorbProducers(graph, widenInputs(one.body, one.output, folds), absorbs);
+  }
+  if (node.op === 'sum' || node.op === 'max') {
+    const inShape = graph.nodes[node.inputs[0]].shape;
+    const axis = node.attrs.axis;
+    const outer = size(inShape.slice(0, axis)), n = inShape[axis];
+    if (size(inShape.slice(axis + 1)) !== 1 || n < 2) return null;
+    const { body, output } = absorbProducers(graph, oneOpBody(graph, node, [[outer, n]], { axis: 1, keepDims: true }), absorbs);
+    return { body, output: body.reshape(output, node.shape) };
+  }
+  return null;
 }
 
 /**
- * A reader's body (`w`, its broadcast operands widened) with the row values it forms
- * (`forms`: [{ value, pos, map, rowFold }]) computed inside it: each value's body inlined
- * on the reader's own inputs (value input j read from reader input map[j], reshaped to the
- * rows the value reduces), standing for the reader's inputs at `pos`. Returns { body, output }.
+ * Whether a broadcast from `from` to `to` spreads a value of one element per row along the
+ * rows' last C elements: the dims of `to` up to some point are the source's own, the rest
+ * (C elements) are broadcast. The source's element for flat index e is then e / C.
  */
-function formRowValues(graph, w, forms) {
-  const g = new Graph();
-  const map = new Map();
-  const at = new Map();
-  for (const f of forms) for (const p of f.pos) at.set(p, f);
-  const inputAt = new Map();
-  for (const n of w.body.nodes) {
-    if (n.op !== 'input') continue;
-    const pos = Number(n.attrs.name.slice(1));
-    if (at.has(pos)) continue;
-    const id = g.input(n.attrs.name, n.shape);
-    map.set(n.id, id);
-    inputAt.set(pos, id);
+function rowBroadcast(from, to, C) {
+  const lead = to.length - from.length;
+  const src = (d) => (d < lead ? 1 : from[d - lead]);
+  for (let p = 0; p <= to.length; p++) {
+    if (size(to.slice(p)) !== C) continue;
+    let ok = true;
+    for (let d = 0; d < to.length && ok; d++) ok = d < p ? src(d) === to[d] : (src(d) === 1 || to[d] === 1);
+    if (ok) return true;
   }
-  const made = new Map();
-  for (const f of forms) {
-    const vb = rowValueBody(graph, graph.nodes[f.value], f.rowFold);
-    const vm = new Map();
-    for (const n of vb.body.nodes) {
-      if (n.op === 'input') {
-        const src = inputAt.get(f.map[Number(n.attrs.name.slice(1))]);
-        if (src === undefined) throw new Error(`row value ${f.value}: operand ${n.attrs.name} is not among its reader's inputs`);
-        if (size(g.nodes[src].shape) !== size(n.shape)) throw new Error(`row value ${f.value}: operand size differs from its reader's`);
-        vm.set(n.id, g.reshape(src, n.shape));
-      } else {
-        vm.set(n.id, g.emit(n.op, n.inputs.map((i) => vm.get(i)), n.attrs));
-      }
+  return false;
+}
+
+/**
+ * The rows a body reduces: { R, C } where every reduction reduces the last axis (C > 1
+ * elements) of an operand of R·C elements and the output has R·C or R elements; { R: 0 }
+ * for a body without reductions; null where they disagree, or where a value it computes
+ * with R elements would pass for a row value without being one (no rowwise kernel runs
+ * it). The rowwise kernel computes a value of R elements once per row, at the row index:
+ * every reader of such a value must then be another value of R elements or a broadcast
+ * spreading it along the rows (rowBroadcast) — with as many rows as their length, a
+ * column vector broadcast down the rows has R elements too. And it reduces the row it is
+ * on: a value depending on a reduction may reach an element only through ops at that
+ * element's own index and such broadcasts, never through a transpose or another
+ * broadcast, which would read it at another row's element.
+ */
+function rowLayout(body, output) {
+  let R = 0, C = 0;
+  for (const n of body.nodes) {
+    if (!isReduce(n)) continue;
+    const s = body.nodes[n.inputs[0]].shape;
+    const c = s[s.length - 1];
+    if (n.attrs.axis !== s.length - 1 || c < 2) return null;
+    if (C === 0) { C = c; R = size(s) / c; } else if (c !== C || size(s) !== R * C) return null;
+  }
+  if (C === 0) return { R: 0 };
+  const o = size(body.nodes[output].shape);
+  if (o !== R * C && o !== R) return null;
+  const rowDep = new Set();
+  for (const n of body.nodes) {
+    if (n.op === 'input' || n.op === 'const') continue;
+    if (isReduce(n) || n.inputs.some((i) => rowDep.has(i))) rowDep.add(n.id);
+    for (const i of n.inputs) {
+      const src = body.nodes[i];
+      const gather = n.op === 'broadcast' || n.op === 'transpose';
+      if (gather && rowDep.has(i) && !(n.op === 'broadcast' && size(src.shape) === R && rowBroadcast(src.shape, n.shape, C))) return null;
+      if (src.op === 'input' || src.op === 'const' || size(src.shape) !== R) continue;
+      if (n.op === 'broadcast' ? !rowBroadcast(src.shape, n.shape, C) : (n.op === 'transpose' || size(n.shape) !== R)) return null;
     }
-    made.set(f, vm.get(vb.output));
   }
-  for (const n of w.body.nodes) {
-    if (n.op === 'input') {
-      const f = at.get(Number(n.attrs.name.slice(1)));
-      if (f) map.set(n.id, g.reshape(made.get(f), n.shape));
-      continue;
-    }
-    map.set(n.id, g.emit(n.op, n.inputs.map((i) => map.get(i)), n.attrs));
-  }
-  return { body: g, output: map.get(w.output) };
+  return { R, C };
 }
 
 /** Kernels for one node. */
-function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs, forms, streamOut) {
-  if (forms) {
-    // A full-size launch that forms the row values it reads (a rowwise kernel: the values'
-    // reductions over the rows it reads anyway, then its own body), with the reductions'
-    // own tuning so the rows are reduced in their order.
-    const base = node.op === 'fused' ? { body: bodyOf(node), output: node.attrs.output } : oneOpBody(graph, node);
-    const f = formRowValues(graph, widenInputs(base.body, base.output, folds), forms);
+function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs, composed, streamOut) {
+  if (composed) {
+    // A launch forming values it reads (`composed`: its body with theirs inside, on the
+    // buffers left to read): a rowwise kernel where the body reduces rows, with the
+    // reductions' own tuning so the rows are reduced in their order; else elementwise.
     const t = opts.tuning || {};
-    return Object.assign({ kind: 'fused-rowwise' }, single(cg.rowwiseKernel(f.body, f.output, { tuning: t.rowreduce || t.row, lastReads, streamOut })));
+    if (composed.body.nodes.some(isReduce)) {
+      return Object.assign({ kind: 'fused-rowwise' },
+        single(cg.rowwiseKernel(composed.body, composed.output, { tuning: t.rowreduce || t.row, lastReads, streamOut })));
+    }
+    return Object.assign({ kind: 'fused-elementwise' },
+      single(cg.elementwiseKernel(composed.body, composed.output, node.shape, { tuning: t.ew, lastReads, streamOut })));
   }
   if (rowFold) {
     // A row-statistics chain with its reductions folded in: the rowwise kernel of the
@@ -822,26 +851,71 @@ function productKey(graph, node) {
   return `${size(a.slice(0, -2))}x${a[a.length - 2]}x${a[a.length - 1]}x${b[b.length - 1]}`;
 }
 
+/** Launch records of folded reductions and absorbed producers (for node-local checks). */
+const foldRecords = (rowFold) => rowFold.map((f) => (f.prod === undefined ? { reduction: f.red, pos: f.pos }
+  : { reduction: f.red, pos: f.pos, producer: f.prod, producerPos: f.ppos }));
+const absorbRecord = (a) => Object.assign({ producer: a.prod, pos: a.pos, producerPos: a.ppos },
+  a.nested ? { absorbed: a.nested.map(absorbRecord) } : {});
+
 /** Bytes from which a last read is streamed (non-temporal loads): 1 MiB. */
 const STREAM_FROM = 1 << 20;
+/** Full rows a launch forming values may hold in registers (its cached operands). */
+const FORM_CACHED = 6;
+/**
+ * Element ops a value's readers may repeat between them to form it: (readers - 1) times
+ * the ops it computes per element (elementOps). Forming trades the value's write and
+ * read-back for that arithmetic; beyond a few ops per element it costs more than the
+ * bytes save (the reference's lost-reuse workload: a 16-op chain shared by four readers).
+ */
+const FORM_OPS = 16;
+
+/** Ops a body computes per element of its widest values (reductions included; shape-only ops not). */
+function elementOps(body) {
+  const widest = Math.max(...body.nodes.map((n) => size(n.shape)));
+  const free = new Set(['input', 'const', 'reshape', 'broadcast', 'transpose', 'stopGradient']);
+  return body.nodes.filter((n) => isReduce(n) || (!free.has(n.op) && size(n.shape) === widest)).length;
+}
+
+/**
+ * Whether the value at node `v` of a reader's body is spread by a broadcast onto more
+ * elements than it has (the reader would compute it once per element it is spread to: the
+ * reference's broadcast-recompute workload), other than a row value spread along the rows
+ * of a rowwise body, which that kernel computes once per row. Reshapes are followed.
+ */
+function expanded(body, v, lay) {
+  const consumers = body.nodes.map(() => []);
+  for (const n of body.nodes) for (const i of n.inputs) consumers[i].push(n);
+  const walk = (id) => consumers[id].some((n) => {
+    if (n.op === 'reshape') return walk(n.id);
+    if (n.op !== 'broadcast' || size(n.shape) === size(body.nodes[id].shape)) return false;
+    return !(lay.R && size(body.nodes[id].shape) === lay.R && rowBroadcast(body.nodes[id].shape, n.shape, lay.C));
+  });
+  return walk(v);
+}
 
 function lowerMI355X(graph, options) {
   const opts = options || {};
   if (opts.perf && !opts.keep) throw new Error('the perf lowering needs `keep`: the nodes whose values are read');
   // A launch that takes producers in, with their index maps, may need more parameter words
   // than its argument block holds: its reader then takes none in, and the plan is made again.
+  // So may a launch forming values: those values are then launched, and the plan is made again.
   const noAbsorb = new Set();
+  const noForm = new Set();
   for (;;) {
     try {
-      return lowerOnce(graph, opts, noAbsorb);
+      return lowerOnce(graph, opts, noAbsorb, noForm);
     } catch (e) {
+      if (e instanceof cg.ParamOverflow && e.formed && e.formed.some((v) => !noForm.has(v))) {
+        for (const v of e.formed) noForm.add(v);
+        continue;
+      }
       if (!(e instanceof cg.ParamOverflow) || e.reader === undefined || noAbsorb.has(e.reader)) throw e;
       noAbsorb.add(e.reader);
     }
   }
 }
 
-function lowerOnce(graph, opts, noAbsorb) {
+function lowerOnce(graph, opts, noAbsorb, noForm) {
   const plan = opts.perf ? perfPlan(graph, new Set(opts.keep), opts.rowFolds !== false, opts.absorb === true && opts.rowFolds !== false,
     opts.loadOps !== false, noAbsorb)
     : { aliases: new Map(), folded: new Set(), views: new Map(), broadcasts: new Map(), dead: new Set(), rowFolds: new Map(), absorbed: new Map() };
@@ -851,10 +925,10 @@ function lowerOnce(graph, opts, noAbsorb) {
   const launched = (node) => node.op !== 'input' && node.op !== 'const' && !plan.aliases.has(node.id)
     && !plan.folded.has(node.id) && !plan.dead.has(node.id);
   const resolve = (id) => (plan.aliases.has(id) ? plan.aliases.get(id) : id);
-  // The buffers a launch reads, operand by operand: a reshape's buffer is its source's,
-  // and an operand read through a view, a folded broadcast or a folded reduction is
-  // read from the node it stands for.
-  const inputsOf = (node) => {
+  // The buffers a launch reads before it forms any value, operand by operand: a reshape's
+  // buffer is its source's, and an operand read through a view, a folded broadcast or a
+  // folded reduction is read from the node it stands for.
+  const baseInputsOf = (node) => {
     const inputs = node.inputs.map(resolve);
     const v = plan.views.get(node.id);
     if (v) for (const s of Object.values(v)) inputs[s.pos] = resolve(s.source);
@@ -876,88 +950,116 @@ function lowerOnce(graph, opts, noAbsorb) {
     }
     for (const a of plan.absorbed.get(node.id) || []) {
       // An absorbed producer's operands (its own, with what it absorbed), in its positions.
-      const pins = inputsOf(graph.nodes[a.prod]);
+      const pins = baseInputsOf(graph.nodes[a.prod]);
       for (const pos of a.pos) inputs[pos] = pins[0];
       a.ppos.forEach((pos, j) => { inputs[pos] = pins[j]; });
     }
-    // A row value formed by this launch is not read: its slots name one of the buffers it
-    // is formed from (which the launch reads anyway).
-    for (const f of formed.get(node.id) || []) for (const pos of f.pos) inputs[pos] = f.ins[0];
     return inputs;
   };
-  // Row values formed by their readers (perf lowering, with row folds): a row value — a
-  // last-axis reduction, or a row-statistics chain with its reductions folded in — whose
-  // launch reads full-size buffers only, and whose every live reader is a full-size
-  // elementwise or rowwise launch over the same rows (reading the value directly, a
-  // fused body broadcasting it inside, or through a broadcast it reads in place) that
-  // reads every one of those buffers itself, launches nothing. Each reader becomes a
-  // rowwise kernel that forms the value from the buffers it loads anyway — the value's
-  // own launch body, the same reductions over rows of the same length with the same
-  // lanes, so the same bits — and then runs its own body: the value is never written or
-  // read back, and one launch goes (LayerNorm's means, the softmax backward's row sums).
-  // Readers forming values take no producers in (absorbed ones), and a value read at row
-  // size by anything else (a chain, a product) stays a launch.
-  const formed = new Map();   // reader id -> [{ value, pos, ins, map, rowFold }]
-  if (opts.perf && opts.rowFolds !== false && opts.formRows !== false) {
-    const keepSet = new Set(opts.keep);
-    const cons = consumersOf(graph);
-    const lastDim = (shape) => shape[shape.length - 1];
-    for (const u of graph.nodes) {
-      if (!launched(u) || keepSet.has(u.id) || plan.absorbed.has(u.id)) continue;
-      const rowFold = plan.rowFolds.get(u.id) || null;
-      let inShape;
-      if (rowFold) inShape = graph.nodes[graph.nodes[rowFold[0].red].inputs[0]].shape;
-      else if ((u.op === 'sum' || u.op === 'max') && u.attrs.keepDims) {
-        inShape = graph.nodes[u.inputs[0]].shape;
-        if (size(inShape.slice(u.attrs.axis + 1)) !== 1 || inShape[u.attrs.axis] === 1) continue;
-      } else continue;
-      const n = lastDim(inShape), full = size(inShape);
-      if (size(u.shape) * n !== full) continue;
-      const ins = inputsOf(u);
-      if (!ins.length || !ins.every((id) => size(graph.nodes[id].shape) === full)) continue;
-      // Its readers and the positions at which each reads it.
-      const readers = new Map();
-      let ok = true;
-      for (const c of new Set(cons[u.id])) {
-        const cn = graph.nodes[c];
-        if (plan.dead.has(c)) continue;
-        if (cn.op === 'broadcast' && plan.folded.has(c)) {
-          for (const r of new Set(cons[c])) {
-            if (plan.dead.has(r)) continue;
-            const bf = plan.broadcasts.get(r);
-            const pos = bf ? Array.from(bf.entries()).filter(([, f]) => f.source === u.id).map(([q]) => q) : [];
-            if (!pos.length) { ok = false; break; }
-            readers.set(r, (readers.get(r) || []).concat(pos));
-          }
-        } else if (cn.op === 'fused' && (cn.attrs.kind === 'elementwise' || cn.attrs.kind === 'rowwise')) {
-          const pos = cn.inputs.map((i, q) => (i === u.id ? q : -1)).filter((q) => q >= 0);
-          readers.set(c, (readers.get(c) || []).concat(pos));
-        } else ok = false;
-        if (!ok) break;
+  // Values formed by their readers (perf lowering, with row folds). A value — full-size or
+  // a row value — computed by an elementwise, rowwise or row-statistics launch or a
+  // last-axis reduction, kept by nobody, launches nothing where every launch reading it can
+  // compute it instead: each such reader forms it inside its own kernel from what the value's
+  // launch would have read (its body inlined there, the values that body reads formed in
+  // turn), so the value is never written or read back. A reader so formed runs a rowwise
+  // kernel where its body then reduces rows (all over rows of one length, its output of
+  // full or row size: rowLayout), else an elementwise one; the reductions run with the
+  // same lanes and order as in the value's own launch (the rowwise kernel's layout depends
+  // on the row length and tuning alone), so every bit is the plain lowering's. A value is
+  // formed where that moves no more bytes: the readers reading the value's operands that
+  // they do not read already, against the value's launch reading them and writing it and
+  // each reader reading it back (LayerNorm's centred rows and statistics, softmax's
+  // exponentials and row sums: the backward of a row function then reads x and dy alone).
+  // Values are taken in graph order, so a value's own operands are settled before it.
+  // Not under a sabotage (the planted kernel runs alone) or with rowwise and row-reduction
+  // tunings that differ (the reductions' lanes would).
+  const formedSet = new Set();
+  const baseOf = new Map();
+  const baseBody = (id) => {
+    if (!baseOf.has(id)) {
+      const node = graph.nodes[id];
+      baseOf.set(id, plan.views.has(id) ? null : launchBase(graph, node, plan.broadcasts.get(id) || null,
+        plan.rowFolds.get(id) || null, plan.absorbed.get(id) || null));
+    }
+    return baseOf.get(id);
+  };
+  // Launch `id`'s body with every value of `set` it reads formed inside it (each once: its
+  // base body on what it reads), on the buffers left to read: { body, output, ins, values }.
+  const compose = (id, set) => {
+    const g = new Graph();
+    const ins = [];
+    const leafAt = new Map();
+    const made = new Map();
+    let inline;
+    const valueOf = (buf) => {
+      if (set.has(buf)) {
+        if (!made.has(buf)) made.set(buf, inline(buf));
+        return made.get(buf);
       }
-      if (!ok || !readers.size) continue;
-      const plans = [];
-      for (const [r, pos] of readers) {
-        const rn = graph.nodes[r];
-        const kind = rn.op === 'fused' ? rn.attrs.kind : ELEMENTWISE_OPS.has(rn.op) ? 'elementwise' : null;
-        if (!(kind === 'elementwise' || kind === 'rowwise') || !launched(rn) || plan.rowFolds.has(r) || plan.absorbed.has(r)
-          || plan.views.has(r) || size(rn.shape) !== full || lastDim(rn.shape) !== n) { ok = false; break; }
-        if (kind === 'rowwise' && bodyOf(rn).nodes.some((x) => isReduce(x) && lastDim(bodyOf(rn).nodes[x.inputs[0]].shape) !== n)) { ok = false; break; }
-        const rIns = inputsOf(rn);
-        const bf = plan.broadcasts.get(r);
-        const taken = new Set(pos.concat((formed.get(r) || []).flatMap((f) => f.pos)));
-        const map = ins.map((id) => rIns.findIndex((x, q) => x === id && !taken.has(q) && !(bf && bf.has(q))));
-        if (map.some((q) => q < 0)) { ok = false; break; }
-        plans.push({ r, pos: Array.from(new Set(pos)).sort((a, b) => a - b), map });
+      if (!leafAt.has(buf)) {
+        leafAt.set(buf, g.input(`a${ins.length}`, graph.nodes[buf].shape));
+        ins.push(buf);
       }
-      if (!ok) continue;
-      plan.folded.add(u.id);
-      for (const q of plans) {
-        if (!formed.has(q.r)) formed.set(q.r, []);
-        formed.get(q.r).push({ value: u.id, pos: q.pos, ins, map: q.map, rowFold });
+      return leafAt.get(buf);
+    };
+    inline = (nid) => {
+      const base = baseBody(nid);
+      const bins = baseInputsOf(graph.nodes[nid]);
+      const map = new Map();
+      for (const n of base.body.nodes) {
+        map.set(n.id, n.op === 'input' ? g.reshape(valueOf(bins[Number(n.attrs.name.slice(1))]), n.shape)
+          : g.emit(n.op, n.inputs.map((i) => map.get(i)), n.attrs));
+      }
+      return map.get(base.output);
+    };
+    const output = inline(id);
+    return { body: g, output, ins, values: Array.from(made.keys()), made };
+  };
+  const tune = opts.tuning || {};
+  const rowTuningsAlike = !tune.rowreduce || JSON.stringify(tune.rowreduce) === JSON.stringify(tune.row);
+  if (opts.perf && opts.rowFolds !== false && opts.formRows !== false && !opts.sabotage && rowTuningsAlike) {
+    const keepBufs = new Set(opts.keep.map(resolve));
+    const sz = (id) => size(graph.nodes[id].shape);
+    const order = graph.nodes.filter(launched);
+    // What each launch reads, kept up to date as values are formed.
+    const reads = new Map(order.map((n) => [n.id, new Set(baseInputsOf(n))]));
+    for (const u of order) {
+      if (keepBufs.has(u.id) || noForm.has(u.id) || !baseBody(u.id)) continue;
+      const readers = order.filter((r) => r !== u && !formedSet.has(r.id) && reads.get(r.id).has(u.id));
+      if (!readers.length || !readers.every((r) => baseBody(r.id))) continue;
+      const own = compose(u.id, formedSet);
+      if (!rowLayout(own.body, own.output) || (readers.length - 1) * elementOps(own.body) > FORM_OPS) continue;
+      const trial = new Set(formedSet).add(u.id);
+      let ok = true, after = 0;
+      for (const r of readers) {
+        const c = compose(r.id, trial);
+        const lay = rowLayout(c.body, c.output);
+        // Within the argument block, at most FORM_CACHED full rows held in registers, and
+        // the value computed at its own elements (once per row for a row value).
+        if (!lay || c.ins.length > cg.MAX_IN || (lay.R && c.ins.filter((x) => sz(x) === lay.R * lay.C).length > FORM_CACHED)
+          || expanded(c.body, c.made.get(u.id), lay)) {
+          ok = false;
+          break;
+        }
+        for (const x of own.ins) if (!reads.get(r.id).has(x)) after += sz(x);
+      }
+      const before = own.ins.reduce((acc, x) => acc + sz(x), 0) + sz(u.id) * (1 + readers.length);
+      if (!ok || after > before) continue;
+      formedSet.add(u.id);
+      for (const r of readers) {
+        const set = reads.get(r.id);
+        set.delete(u.id);
+        for (const x of own.ins) set.add(x);
       }
     }
+    for (const id of formedSet) plan.folded.add(id);
   }
+  // The launches that form values, and what every launch reads.
+  const composed = new Map();
+  for (const node of graph.nodes) {
+    if (launched(node) && formedSet.size && baseInputsOf(node).some((id) => formedSet.has(id))) composed.set(node.id, compose(node.id, formedSet));
+  }
+  const inputsOf = (node) => (composed.has(node.id) ? composed.get(node.id).ins : baseInputsOf(node));
   // Last reads (perf lowering): an elementwise or rowwise kernel loads a full-size operand of
   // STREAM_FROM bytes or more non-temporally where no later launch of the list reads
   // that buffer, so data read for the last time streams past the caches instead of
@@ -1017,13 +1119,9 @@ function lowerOnce(graph, opts, noAbsorb) {
     const absorbSig = (a) => [a.pos, prodKey({ prod: a.prod, ppos: a.ppos, prodFolds: a.prodFolds }),
       a.nested ? a.nested.map(absorbSig) : null];
     const absorbKey = absorbs ? absorbs.map(absorbSig) : null;
-    const forms = formed.get(node.id) || null;
-    const rowSig = (rf) => rf.map((f) => [f.pos, graph.nodes[f.red].op, graph.nodes[f.red].attrs,
-      graph.nodes[graph.nodes[f.red].inputs[0]].shape, prodKey(f)]);
-    const formKey = forms ? forms.map((f) => {
-      const u = graph.nodes[f.value];
-      return [f.pos, f.map, u.op, u.attrs, u.shape, u.inputs.map((i) => graph.nodes[i].shape), f.rowFold ? rowSig(f.rowFold) : null];
-    }) : null;
+    // A launch forming values is keyed by the body it runs.
+    const comp = composed.get(node.id) || null;
+    const formKey = comp ? [comp.body.nodes.map((n) => [n.op, n.inputs, n.attrs, n.shape]), comp.output] : null;
     const inputs = inputsOf(node);
     const lastReads = [];
     inputs.forEach((id, pos) => {
@@ -1038,9 +1136,10 @@ function lowerOnce(graph, opts, noAbsorb) {
     let k = cache.get(key);
     if (!k) {
       try {
-        k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs, forms, streamOut.get(node.id));
+        k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs, comp, streamOut.get(node.id));
       } catch (e) {
-        if (e instanceof cg.ParamOverflow && absorbs) e.reader = node.id;
+        if (e instanceof cg.ParamOverflow && comp) e.formed = comp.values;
+        else if (e instanceof cg.ParamOverflow && absorbs) e.reader = node.id;
         throw e;
       }
       cache.set(key, k);
@@ -1051,23 +1150,15 @@ function lowerOnce(graph, opts, noAbsorb) {
       inputs, params: k.params, grid: k.kernels[0].grid, code: k.kernels[0].name,
       kernels: k.kernels, workspace: k.workspace, bytes: algorithmicBytes(graph, node, inputs), flops: k.flops,
     });
-    if (rowFold) {
-      // The reduction folded into this launch, and the launch's own body (for node-local checks).
-      launches[launches.length - 1].rowFolds = rowFold.map((f) => (f.prod === undefined ? { reduction: f.red, pos: f.pos }
-        : { reduction: f.red, pos: f.pos, producer: f.prod, producerPos: f.ppos }));
-    }
-    if (forms) {
-      // The row values this launch forms (for node-local checks): each value, the positions
-      // it stands for, and the reader positions of its operands; a chain's folded reductions.
-      launches[launches.length - 1].formedRows = forms.map((f) => Object.assign({ value: f.value, pos: f.pos, map: f.map },
-        f.rowFold ? { rowFolds: f.rowFold.map((x) => (x.prod === undefined ? { reduction: x.red, pos: x.pos }
-          : { reduction: x.red, pos: x.pos, producer: x.prod, producerPos: x.ppos })) } : {}));
-    }
-    if (absorbs) {
-      // The producers this launch forms in place of loading them (for node-local checks).
-      const record = (a) => Object.assign({ producer: a.prod, pos: a.pos, producerPos: a.ppos },
-        a.nested ? { absorbed: a.nested.map(record) } : {});
-      launches[launches.length - 1].absorbed = absorbs.map(record);
+    // For node-local checks: the reductions folded into this launch, the producers it
+    // forms in place of loading them, and the values it forms (each with its own folds and
+    // absorbed producers, in the order the launch forms them).
+    if (rowFold) launches[launches.length - 1].rowFolds = foldRecords(rowFold);
+    if (absorbs) launches[launches.length - 1].absorbed = absorbs.map(absorbRecord);
+    if (comp) {
+      launches[launches.length - 1].formed = comp.values.map((v) => Object.assign({ value: v },
+        plan.rowFolds.has(v) ? { rowFolds: foldRecords(plan.rowFolds.get(v)) } : {},
+        plan.absorbed.has(v) ? { absorbed: plan.absorbed.get(v).map(absorbRecord) } : {}));
     }
     if (v) {
       // Operands read in place: for each folded slot, the node it stands for and the view of its source.

@@ -197,65 +197,68 @@ def absorb_producers(graph, node_id, absorbed):
     return dict(node, op="fused", attrs=attrs, inputs=inputs), inputs
 
 
-def form_rows(graph, node_id, formed):
-    """A launch of the perf lowering that forms the row values it reads (its record's
-    formedRows: [{value, pos, map, rowFolds?}]): the reader as a fused node whose body
-    computes each value — the value node itself (a last-axis reduction) or, for a
-    row-statistics chain, the chain with its reductions taken in (fold_reductions) — on the
-    reader's own inputs (value operand j read from reader input map[j], reshaped to the
-    value's operand shape), standing for the reader's inputs at `pos` (broadcast to their
-    shape where the reader read the value through a broadcast). The reader's operands at
-    `pos` become the value's first operand (the launch reads no value buffer). Restated
-    here from the lowering's rule."""
-    node = graph["nodes"][node_id]
-    body, out = _producer_body(graph, node)
-    at = {p: f for f in formed for p in f["pos"]}
-    inputs = list(node["inputs"])
-    new, where, input_at = [], {}, {}
-    for bid, b in enumerate(body):
-        if b["op"] == "input" and int(b["attrs"]["name"][1:]) not in at:
-            new.append(dict(b))
-            where[bid] = input_at[int(b["attrs"]["name"][1:])] = len(new) - 1
-    made = {}
-    for f in formed:
-        vnode, vins = fold_reductions(graph, f["value"], f.get("rowFolds"))
-        vbody, vout = _producer_body(graph, vnode)
-        vwhere = {}
-        for vbid, vb in enumerate(vbody):
-            if vb["op"] == "input":
-                j = int(vb["attrs"]["name"][1:])
-                src = input_at[f["map"][j]]
-                if new[src]["shape"] != vb["shape"]:
-                    new.append({"op": "reshape", "inputs": [src], "attrs": {"shape": vb["shape"]}, "shape": vb["shape"]})
-                    src = len(new) - 1
-                vwhere[vbid] = src
+def _reaches(graph, i, values):
+    """Whether node i is one of `values`, or a broadcast or reshape of one."""
+    n = graph["nodes"][i]
+    return i in values or (n["op"] in ("broadcast", "reshape") and _reaches(graph, n["inputs"][0], values))
+
+
+def form_values(graph, node_id, formed, folds=None, absorbed=None):
+    """A launch of the perf lowering that forms values it reads (its record's formed:
+    [{value, rowFolds?, absorbed?}], every value formed inside it): the launch restated
+    without them (with its own row folds or absorbed producers), every operand that is one
+    of those values — directly, or a broadcast or reshape of one — replaced by that value's
+    own launch restated the same way, on its operands in turn (each value once, reshaped to
+    where it is read). The launch's operands are the nodes left to read, in order of first
+    use. Restated here from the lowering's rule, by node ids: a value formed from the
+    wrong operands, or a record naming a value the launch does not read, fails."""
+    nodes = graph["nodes"]
+    recs = {f["value"]: f for f in formed}
+    out, ins, memo = [], [], {}
+
+    def value(i, shape):
+        if i not in memo:
+            n = nodes[i]
+            if i in recs:
+                memo[i] = inline(*restate(graph, i, recs[i].get("rowFolds"), recs[i].get("absorbed")))
+            elif _reaches(graph, i, recs):
+                src = value(n["inputs"][0], nodes[n["inputs"][0]]["shape"])
+                out.append({"op": n["op"], "inputs": [src], "attrs": n["attrs"], "shape": n["shape"]})
+                memo[i] = len(out) - 1
             else:
-                new.append(dict(vb, inputs=[vwhere[i] for i in vb["inputs"]]))
-                vwhere[vbid] = len(new) - 1
-        made[f["value"]] = (vwhere[vout], vins)
-    for bid, b in enumerate(body):
-        if b["op"] == "input" and int(b["attrs"]["name"][1:]) in at:
-            v, _ = made[at[int(b["attrs"]["name"][1:])]["value"]]
-            if new[v]["shape"] != b["shape"]:
-                value_shape = graph["nodes"][at[int(b["attrs"]["name"][1:])]["value"]]["shape"]
-                assert new[v]["shape"] == value_shape
-                new.append({"op": "broadcast", "inputs": [v], "attrs": {"shape": b["shape"]}, "shape": b["shape"]})
-                v = len(new) - 1
-            where[bid] = v
-    for bid, b in enumerate(body):
-        if b["op"] != "input":
-            new.append(dict(b, inputs=[where[i] for i in b["inputs"]]))
-            where[bid] = len(new) - 1
-    for p, f in at.items():
-        inputs[p] = made[f["value"]][1][0]
-    attrs = dict(node["attrs"]) if node["op"] == "fused" else {"kind": "rowwise", "pattern": "rowwise"}
-    attrs = dict(attrs, body={"nodes": new}, output=where[out])
-    return dict(node, op="fused", attrs=attrs, inputs=inputs), inputs
+                out.append({"op": "input", "inputs": [], "attrs": {"name": f"a{len(ins)}", "shape": n["shape"]},
+                            "shape": n["shape"]})
+                ins.append(i)
+                memo[i] = len(out) - 1
+        v = memo[i]
+        if list(out[v]["shape"]) != list(shape):
+            out.append({"op": "reshape", "inputs": [v], "attrs": {"shape": list(shape)}, "shape": list(shape)})
+            v = len(out) - 1
+        return v
+
+    def inline(node, node_ins):
+        body, bout = _producer_body(graph, node)
+        where = {}
+        for bid, b in enumerate(body):
+            if b["op"] == "input":
+                where[bid] = value(node_ins[int(b["attrs"]["name"][1:])], b["shape"])
+            else:
+                out.append(dict(b, inputs=[where[x] for x in b["inputs"]]))
+                where[bid] = len(out) - 1
+        return where[bout]
+
+    node, node_ins = restate(graph, node_id, folds, absorbed)
+    o = inline(node, node_ins)
+    assert set(recs) <= set(memo), (node_id, sorted(set(recs) - set(memo)))
+    attrs = dict(node["attrs"]) if node["op"] == "fused" else {"kind": "elementwise", "pattern": "elementwise"}
+    attrs = dict(attrs, body={"nodes": out}, output=o)
+    return dict(node, op="fused", attrs=attrs, inputs=ins), ins
 
 
 def formed_values(formed):
-    """The row values, and the reductions and producers folded into them, that the launches
-    of {reader: [formedRows records]} form."""
+    """The values that the launches of {reader: [formed records]} form, and the reductions
+    and producers folded into those values' own launches (their row folds and absorbed
+    producers)."""
     values, reductions, producers = set(), set(), set()
     for records in formed.values():
         for f in records:
@@ -264,16 +267,16 @@ def formed_values(formed):
                 reductions.add(x["reduction"])
                 if "producer" in x:
                     producers.add(x["producer"])
+            producers |= absorbed_producers({0: f.get("absorbed") or []})
     return values, reductions, producers
 
 
 def restate(graph, node_id, folds=None, absorbed=None, formed=None):
-    """The launch of node `node_id` as the perf lowering runs it: its row folds, its
-    absorbed producers or the row values it forms restated (a launch has one of them), or
-    the node itself."""
+    """The launch of node `node_id` as the perf lowering runs it: its row folds or its
+    absorbed producers restated (a launch has at most one of them), then the values it
+    forms, or the node itself."""
     if formed:
-        assert not folds and not absorbed
-        return form_rows(graph, node_id, formed)
+        return form_values(graph, node_id, formed, folds, absorbed)
     if absorbed:
         assert not folds
         return absorb_producers(graph, node_id, absorbed)
@@ -322,7 +325,7 @@ def expectations(full, twin, launched, operand, sequences, row_folds=None, absor
     `row_folds` ({node id: [{reduction, pos}]}, a perf lowering's): those launches are the
     chain with its row reductions taken in, on the reductions' operands; `absorbed`
     ({node id: [{producer, pos, producerPos}]}): those launches form their producers;
-    `formed` ({node id: [formedRows records]}): those launches form the row values they read."""
+    `formed` ({node id: [formed records]}): those launches form the values they read."""
     axis = [batch_axis(n["shape"], t["shape"]) for n, t in zip(full["nodes"], twin["nodes"])]
     row_folds = row_folds or {}
     absorbed = absorbed or {}
@@ -364,11 +367,11 @@ def judge_case(fused, fused_vals, gc, arr):
     # operands formed in the same launches, are the other launches it skips.
     folds = {int(k): v for k, v in gc["rowFolds"].items()}
     took = {int(k): v for k, v in gc["absorbed"].items()}
-    rows = {int(k): v for k, v in gc.get("formedRows", {}).items()}
+    rows = {int(k): v for k, v in gc.get("formed", {}).items()}
     reductions = {f["reduction"] for fs in folds.values() for f in fs}
     producers = {f["producer"] for fs in folds.values() for f in fs if "producer" in f}
     producers |= absorbed_producers(took)
-    # Row values formed by their readers, with what their own launches would fold.
+    # Values formed by their readers, with what their own launches would fold or absorb.
     values, value_reductions, value_producers = formed_values(rows)
     assert all(fused["nodes"][i]["op"] not in ("matmul", "input", "const") for i in values)
     reductions |= {i for i in values if fused["nodes"][i]["op"] in ("sum", "max")} | value_reductions

@@ -22,9 +22,9 @@ def test_arena_plans_keep_every_value_until_its_last_use(tool):
         assert r["peak"] <= r["bytes"] <= max(256, r["peak"]) * 1.03 + 4096, r
         assert r["bytes"] <= r["unshared"]
     c5 = next(r for r in res if r["name"] == "transformer-64")
-    # Config 5's step: 1.59 GB of node buffers in 0.80 GB (the values its launches form in
+    # Config 5's step: 1.29 GB of node buffers in 0.80 GB (the values its launches form in
     # place have no buffer at all, so what is left to share is mostly live at once).
-    assert c5["bytes"] < 0.55 * c5["unshared"] and c5["bytes"] < 0.85e9, c5
+    assert c5["bytes"] < 0.65 * c5["unshared"] and c5["bytes"] < 0.85e9, c5
 
 
 def test_a_planted_overlap_is_caught(tool):

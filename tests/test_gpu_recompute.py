@@ -12,9 +12,10 @@ deliberate "fusion loses" measurements:
 - corpus programs 1..100 (200 graphs) fused with recomputation, plain and perf
   lowerings, every surviving node judged the same way and the perf lowering's kept
   outputs equal to the plain lowering's bit for bit.
-The recompute variants of the five workloads launch fewer kernels than their fused
-variants: the option changed the partition (the reference's own check of that is 2
-fused nodes without it and 1 with it, test/m4-fusion.test.js:55-63)."""
+The recompute variants of the five workloads have fewer fused nodes (launches of the
+checked lowering) than their fused variants: the option changed the partition (the
+reference's own check of that is 2 fused nodes without it and 1 with it,
+test/m4-fusion.test.js:55-63)."""
 import sys
 
 import numpy as np
@@ -50,7 +51,10 @@ def test_fusion_loses_workloads_with_recompute(tmp_path, tool):
             print(f"{c['id']} {v}: {r['launches']} launches, surviving nodes worst {jf['worst']:.3g}, outputs worst "
                   f"{j['worst']:.3g}", file=sys.stderr)
             assert jf["pass"] and r["canaryPlain"], (c["id"], v, jf["first"])
-        assert c["variants"]["recompute"]["launches"] < c["variants"]["fused"]["launches"], c["id"]
+        # The partition: one launch per fused node in the checked lowering (the perf
+        # lowering may form a shared value in its readers either way).
+        assert c["variants"]["recompute"]["plainLaunches"] < c["variants"]["fused"]["plainLaunches"], c["id"]
+        assert c["variants"]["recompute"]["launches"] <= c["variants"]["fused"]["launches"], c["id"]
 
 
 def test_corpus_with_recompute(tmp_path, tool):

@@ -61,7 +61,8 @@ def test_c5_full_batch_step_node_local(tmp_path, tool, attention):
         with interp.blas_matmul():
             folds = c["rowFolds"] if variant == "perf" else None
             took = c["absorbed"] if variant == "perf" else None
-            for nid, s, v, e in expectations(full, twin, launched, operand, SEQUENCES, folds, took):
+            formed = c["formed"] if variant == "perf" else None
+            for nid, s, v, e in expectations(full, twin, launched, operand, SEQUENCES, folds, took, formed):
                 ref_v.append(v)
                 ref_e.append(e)
                 gpu.append(b.arr(outs[nid]["whole"] if s is None else outs[nid]["blocks"][s]))
@@ -75,7 +76,8 @@ def test_c5_full_batch_step_node_local(tmp_path, tool, attention):
               f"{j['worst']:.3g} over {j['elements']} elements, unjudgeable {j['unjudgeable']}", file=sys.stderr)
         assert j["pass"], (variant, j["first"], j["unjudged"])
     print(f"C5 B64: split-K launches {c['splitK']}, batched dispatches {c['batches']}, row reductions folded into "
-          f"{len(c['rowFolds'])} chains, producers absorbed by {len(c['absorbed'])} launches", file=sys.stderr)
-    assert len(c["rowFolds"]) > 0 and len(c["absorbed"]) > 0
+          f"{len(c['rowFolds'])} chains, producers absorbed by {len(c['absorbed'])} launches, values formed by "
+          f"{len(c['formed'])} launches", file=sys.stderr)
+    assert len(c["rowFolds"]) > 0 and len(c["absorbed"]) > 0 and len(c["formed"]) > 0
     assert counts["checked"][0] >= 4 * (250 if attention else 300) and counts["checked"][1] >= 40, counts
     assert counts["perf"][0] > 0 and counts["perf"][1] > 0, counts

@@ -155,7 +155,7 @@ def test_c5_full_size_trainer(tool, graph, arena, streams, attention):
     assert r["batches"] >= 12, r["batches"]
     assert r["dispatches"] == (r["kernels"] - r["batchSaves"] if streams == 1 else r["kernels"]), r
     if arena:
-        # With attention fused no [.., T, T] score tensor has a buffer: 1.2 GB of node
-        # buffers instead of 2.3 GB, placed in 0.76 GB.
-        share = 0.7 if attention else 0.55
+        # With attention fused no [.., T, T] score tensor has a buffer: 1.0 GB of node
+        # buffers instead of 1.3 GB, placed in 0.76 GB (what is left is mostly live at once).
+        share = 0.78 if attention else 0.65
         assert r["arena"]["bytes"] < share * r["arena"]["unshared"] and r["arena"]["bytes"] < 0.85e9, r["arena"]

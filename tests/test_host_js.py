@@ -220,10 +220,11 @@ def test_perf_lowering_views_address_the_operands(tool, req):
     reductions = {f["reduction"] for fs in d["rowFolds"].values() for f in fs}
     producers = {f["producer"] for fs in d["rowFolds"].values() for f in fs if "producer" in f}
     absorbed = set()
-    # Row values formed by their readers: a last-axis reduction, or a row-statistics chain
-    # with its reductions (and their producers) folded in, that every live reader forms.
-    formed, formers = set(), {}
-    for reader, records in d["formedRows"].items():
+    # Values formed by their readers: an elementwise, rowwise or row-statistics value or a
+    # last-axis reduction (with what its own launch folds or absorbs) that every launch
+    # reading it forms.
+    formed, formers, value_absorbs = set(), {}, []
+    for reader, records in d["formed"].items():
         for f in records:
             formed.add(f["value"])
             formers.setdefault(f["value"], set()).add(int(reader))
@@ -231,6 +232,8 @@ def test_perf_lowering_views_address_the_operands(tool, req):
                 reductions.add(x["reduction"])
                 if "producer" in x:
                     producers.add(x["producer"])
+            if f.get("absorbed"):
+                value_absorbs.append((f["absorbed"], f["value"]))
 
     takers = {}
 
@@ -251,6 +254,8 @@ def test_perf_lowering_views_address_the_operands(tool, req):
             consumers.setdefault(i, set()).add(n_id)
     for reader, records in d["absorbed"].items():
         walk(records, int(reader))
+    for records, value in value_absorbs:
+        walk(records, value)
     # A producer formed in place is formed by every live reader of it (a launch, or a
     # producer formed in place in turn): nothing reads a buffer it would have written.
     for prod, by in takers.items():
@@ -273,19 +278,25 @@ def test_perf_lowering_views_address_the_operands(tool, req):
             assert named == (l["node"] in readers), (relu, l["node"])
     assert all(nodes[i]["op"] in ("transpose", "broadcast")
                for i in set(d["folded"]) - reductions - producers - absorbed - set(on_load) - formed)
-    # A formed value is kept by nobody, and every live reader of it (directly, or through a
-    # broadcast read in place) forms it.
+    # A formed value is kept by nobody, and formed by exactly the launches that stand for its
+    # live consumers: a launched consumer itself; for one that launches nothing (a
+    # broadcast read in place, a reshape sharing a buffer, a folded reduction or producer,
+    # another formed value), the launches standing for its own consumers.
+    launched = {x["node"] for x in d["launches"]}
+    aliased = {a for a, _ in d["aliases"]}
+
+    def standing(c):
+        if c in launched:
+            return {c}
+        assert c in d["folded"] or c in aliased, c
+        return set().union(*[standing(x) for x in consumers.get(c, set()) - set(d["dead"])])
     for v, by in formers.items():
         assert v not in d["keep"] and (nodes[v]["op"] in ("sum", "max", "fused") or nodes[v]["op"] in ELEMENTWISE)
-        readers = set()
-        for c in consumers[v] - set(d["dead"]):
-            if nodes[c]["op"] == "broadcast" and c in d["folded"]:
-                readers |= consumers[c] - set(d["dead"])
-            else:
-                readers.add(c)
+        assert not any(src == v and a in d["keep"] for a, src in d["aliases"]), v
+        readers = set().union(*[standing(c) for c in consumers[v] - set(d["dead"])])
         assert readers == by, (v, readers, by)
     if req["model"] == "transformer":
-        assert len(formed) >= 18, len(formed)
+        assert len(formed) >= 40, len(formed)
     # A folded broadcast is read by elementwise, rowwise or epilogue bodies only (never
     # by a reduction, a gather or as a matmul operand), through the broadcast's source.
     for chain, fs in d["rowFolds"].items():

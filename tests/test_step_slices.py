@@ -10,8 +10,8 @@ import numpy as np
 import pytest
 
 from oracle import bounds, interp
-from step_slices import (absorb_producers, absorbed_producers, batch_axis, expectations, fold_reductions, form_rows, fused_values,
-                         local, take_block)
+from step_slices import (absorb_producers, absorbed_producers, batch_axis, expectations, fold_reductions, fused_values,
+                         local, restate, take_block)
 
 
 @pytest.mark.parametrize("attention", [False, True])
@@ -76,9 +76,11 @@ def test_folded_row_reductions_are_the_chain_on_the_reduction(tool):
     reduction evaluated first and the chain's own body applied to its value, bit for bit,
     value and bound: the fold changes where the reduction runs, not what is computed. The
     same holds where the launch also forms the reduction's operand from its producer's
-    operands (the producer evaluated first on the unfolded side)."""
+    operands (the producer evaluated first on the unfolded side). Chains run as launches of
+    their own or inside the launches that form them (their records carry the folds)."""
     d = tool("perf-lower", {"model": "transformer", "B": 1})
     graph, folds = d["graph"], {int(k): v for k, v in d["rowFolds"].items()}
+    folds.update({f["value"]: f["rowFolds"] for fs in d["formed"].values() for f in fs if f.get("rowFolds")})
     assert len(folds) >= 20
     reds = {f["reduction"] for fs in folds.values() for f in fs}
     assert reds <= set(d["folded"]) and all(graph["nodes"][r]["op"] in ("sum", "max") for r in reds)
@@ -157,43 +159,70 @@ def test_absorbed_producers_are_formed_as_computed(tool):
         assert np.array_equal(e, re_), k
 
 
-@pytest.mark.parametrize("req", [{"model": "transformer", "B": 1}, {"model": "transformer", "B": 1, "attention": True}])
-def test_formed_row_values_are_the_value_then_the_reader(tool, req):
-    """The perf lowering lets a full-size launch form the row values it reads (LayerNorm's
-    means and its backward's row statistics: a last-axis reduction, or a row-statistics
-    chain with its reductions folded in), from the rows it loads anyway. The checkers'
-    restatement of such a launch (form_rows), evaluated in float64 on the launch's
-    operands, equals the value's own launch evaluated first (fold_reductions) and the
-    reader's body applied to it, bit for bit, value and bound."""
-    d = tool("perf-lower", req)
-    graph, rows = d["graph"], {int(k): v for k, v in d["formedRows"].items()}
-    assert len(rows) >= 18, len(rows)
-    formed = {f["value"] for fs in rows.values() for f in fs}
-    assert formed <= set(d["folded"])
+def _perf_lowered(tool, req):
+    if "c3" not in req:
+        return tool("perf-lower", req)
+    g = tool("config-graphs", {"c3": [{"fn": req["c3"], "R": 8, "C": 16}]})["c3"][0]["gradient"]
+    return tool("perf-lower", {"graph": g["graph"], "keep": g["keep"], "fuse": {}})
+
+
+def _carried(graph, i, carried):
+    """(value, bound) of node i: carried, or a broadcast or reshape of a carried node."""
+    if i in carried:
+        return carried[i]
+    n = graph["nodes"][i]
+    src = n["inputs"][0]
+    v, e = _carried(graph, src, carried)
+    if n["op"] == "broadcast":
+        s0 = graph["nodes"][src]["shape"]
+        return interp.k_broadcast(v, s0, n["shape"]), interp.k_broadcast(e, s0, n["shape"])
+    assert n["op"] == "reshape", n["op"]
+    return v, e
+
+
+def _run_carried(graph, node, ins, carried):
+    if node["op"] == "fused":
+        body, out = node["attrs"]["body"], node["attrs"]["output"]
+    else:
+        body, out = bounds.one_op_graph(graph, node)
+    r = bounds.reference_with_bounds(body, {}, carried={f"a{p}": _carried(graph, i, carried) for p, i in enumerate(ins)})
+    return r["values"][out], r["bounds"][out]
+
+
+@pytest.mark.parametrize("req", [{"model": "transformer", "B": 1}, {"model": "transformer", "B": 1, "attention": True},
+                                 {"model": "mlp"}, {"c3": "softmax"}, {"c3": "logSoftmax"}])
+def test_formed_values_are_the_values_then_the_reader(tool, req):
+    """The perf lowering lets a launch form the values it reads — row values (LayerNorm's
+    means, a backward's row statistics) and full-size values (LayerNorm's centred rows,
+    softmax's exponentials) — from what their own launches would have read, recursively.
+    The checkers' restatement of such a launch (form_values), evaluated in float64 on the
+    launch's operands, equals each value's own launch evaluated first, in the record's
+    order, and the reader's own launch applied to them, bit for bit, value and bound. The
+    formed values launch nothing, and a config-3 gradient is two launches: the forward
+    reading x, the backward reading x and dy."""
+    d = _perf_lowered(tool, req)
+    graph = d["graph"]
+    formed = {int(k): v for k, v in d["formed"].items()}
+    folds = {int(k): v for k, v in d["rowFolds"].items()}
+    took = {int(k): v for k, v in d["absorbed"].items()}
+    values = {f["value"] for fs in formed.values() for f in fs}
+    assert values <= set(d["folded"]) and not values & {x["node"] for x in d["launches"]}
+    if "c3" in req:
+        assert len(d["launches"]) == 2 and len(formed) == 2, d["launches"]
+    elif req["model"] == "transformer":
+        assert len(values) >= 40, len(values)
     rng = np.random.default_rng(5)
-    for k, records in rows.items():
-        node, ins = form_rows(graph, k, records)
+    for k, records in formed.items():
+        node, ins = restate(graph, k, folds.get(k), took.get(k), records)
         ops = [rng.uniform(0.5, 2.0, size=interp.size(graph["nodes"][i]["shape"])).astype(np.float32) for i in ins]
         v, e = local(graph, node, ops)
-        # The unformed way: each value's own launch on its operands (the reader's, at map),
-        # then the reader's body with the value in its place (broadcast where it read one).
-        reader = graph["nodes"][k]
-        carried = {f"a{p}": (o.astype(np.float64), np.zeros(o.size)) for p, o in enumerate(ops)}
+        assert np.all(np.isfinite(v)), k
+        # The unformed way: each value's own launch on the values before it, then the reader.
+        carried = {i: (o.astype(np.float64), np.zeros(o.size)) for i, o in zip(ins, ops)}
         for f in records:
-            vnode, vins = fold_reductions(graph, f["value"], f.get("rowFolds"))
-            vv, ve = local(graph, vnode, [ops[q] for q in f["map"]])
-            for p in f["pos"]:
-                src = graph["nodes"][reader["inputs"][p]]
-                if src["op"] == "broadcast":
-                    vv_, ve_ = interp.k_broadcast(vv, graph["nodes"][f["value"]]["shape"], src["shape"]), \
-                        interp.k_broadcast(ve, graph["nodes"][f["value"]]["shape"], src["shape"])
-                    carried[f"a{p}"] = (vv_, ve_)
-                else:
-                    carried[f"a{p}"] = (vv, ve)
-        if reader["op"] == "fused":
-            body, out = reader["attrs"]["body"], reader["attrs"]["output"]
-        else:
-            body, out = bounds.one_op_graph(graph, reader)
-        r = bounds.reference_with_bounds(body, {}, carried=carried)
-        assert np.array_equal(v, r["values"][out]) and np.all(np.isfinite(v)), k
-        assert np.array_equal(e, r["bounds"][out]), k
+            vnode, vins = restate(graph, f["value"], f.get("rowFolds"), f.get("absorbed"))
+            carried[f["value"]] = _run_carried(graph, vnode, vins, carried)
+        rnode, rins = restate(graph, k, folds.get(k), took.get(k))
+        rv, re_ = _run_carried(graph, rnode, rins, carried)
+        assert np.array_equal(v, rv), k
+        assert np.array_equal(e, re_), k
