@@ -638,7 +638,8 @@ async function gpuWorkloads(req, dir) {
         graph = f.graph;
         keep = m.outputs.map((id) => f.index.get(id));
       }
-      const lp = lowerMI355X(graph, { perf: true, keep });
+      // As the bench lowers each variant: the unfused graph with nothing folded into another launch.
+      const lp = lowerMI355X(graph, Object.assign({ perf: true, keep }, v === 'unfused' ? { rowFolds: false } : {}));
       const r = await runner.run(graph, lp, m.inputs, { canary: true });
       const out = { outputs: keep.map((id) => bundle.put(r.values[id])), canary: r.canaryIntact.every(Boolean),
         launches: lp.launches.length, kinds: lp.launches.map((l) => l.kind) };
@@ -1473,6 +1474,12 @@ async function main() {
         g = fs.graph;
         keep = [fs.loss, fs.logits].concat(Object.values(fs.outputs));
         absorb = true;
+      } else if (req.workload) {
+        // A sweep workload's graph, unfused (as given).
+        const { workloads } = require('../src/builders/workloads');
+        const m = workloads().find((w) => w.id === req.workload).make();
+        g = m.graph;
+        keep = m.outputs;
       } else {
         g = Graph.fromJSON(req.graph);
         keep = req.keep || [];
@@ -1489,6 +1496,7 @@ async function main() {
         launches: l.launches.map((x) => ({ node: x.node, kind: x.kind, inputs: x.inputs, params: x.params.length, views: x.views || null, modes: gemmModes(x),
           split: gemmSplit(x), plainSplit: gemmSplit(plain.get(x.node)) })),
         batches: (l.batches || []).map((b) => ({ start: b.start, count: b.count, joint: !!b.joint, kernels: b.kernels.map((k) => k.name) })) };
+      if (req.sources) out.sources = Object.fromEntries(kernelSources(l));
       break;
     }
     case 'precompile': out = { kernels: precompileGroup(req.group || 'direct', req.arch, req.shard, req.shards) }; break;

@@ -418,6 +418,7 @@ function rowwiseKernel(b, output, opts) {
   const caches = new Map();
   const reduced = new Map();
   const rowLines = [];    // row-tier statements, emitted as they are first needed
+  const rowNames = new Set();
   let em;
   const ROW = { key: 'r', idx: 'r', root: false, row: true, limit: R };
   const elemCtx = () => ({ key: 'e', idx: 'e', root: true, limit: R * C });
@@ -443,8 +444,11 @@ function rowwiseKernel(b, output, opts) {
     },
     load(k, ctx, lines, node) {
       if (ctx.row) {
-        // A row-tier operand at the row index.
-        const v = `R${rowLines.length}_${k}`;
+        // A row-tier operand at the row index. Row lines are taken out per phase and emitted
+        // in the row loop's scope one phase after another, so a name is kept unique by suffix.
+        let v = `R${rowLines.length}_${k}`;
+        if (rowNames.has(v)) v = `${v}_${rowNames.size}`;
+        rowNames.add(v);
         lines.push(`const float ${v} = A.in[${k}][${ctx.idx}];`);
         return v;
       }

@@ -601,3 +601,24 @@ def test_chain_maps_address_random_transpose_reshape_chains(tool):
             idx = idx + _mixed_radix(v.shape[axis], factors).reshape(sh)
         assert np.array_equal(src.reshape(-1)[idx], v), c
     assert mapped >= 150
+
+
+@pytest.mark.parametrize("workload", ["step-V16-B8", "step-V75-B16"])
+def test_formed_kernels_declare_each_name_once(tool, workload):
+    """A rowwise kernel emits its row-tier statements (values computed once per row) phase
+    by phase into the row loop's scope, so a name made from how many such lines are pending
+    can come back in a later phase: the unfused training steps of the workload sweep,
+    lowered with their row values formed by the launches reading them, once declared one
+    row load twice (a compile error on the GPU). Every name a kernel declares is declared
+    once."""
+    import re
+    d = tool("perf-lower", {"workload": workload, "sources": True})
+    assert d["formed"], "the case forms no values"
+    for name, src in d["sources"].items():
+        declared = re.findall(r"\bconst float (\w+) =", src)
+        loops = src.count("for (int s = 0;")
+        # Names inside the element loops repeat per loop (their own scopes); row-tier names
+        # (R...) and reduction results are declared once in the row loop.
+        row = [x for x in declared if x.startswith("R") or x.startswith("red")]
+        assert len(row) == len(set(row)), (name, sorted(x for x in row if row.count(x) > 1))
+        assert loops > 0 or not row
