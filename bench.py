@@ -7,9 +7,13 @@ quoted on first: fused elementwise chains — 8 seeded programs of 8–16 ops ov
 fp32 [8192, 1024] with a [1024] row-vector broadcast, each run forward and as
 its autodiff gradient graph — in algorithmic HBM GB/s (every unique operand of
 a launch read once at its own size, plus its output: the reference's byte
-count, src/fusion/workloads.js:171-172). A step is one run of every fused
-program; K steps are timed between a sync and hipEvents on both sides, with the
-inputs already in HBM.
+count, src/fusion/workloads.js:171-172) of the launches this backend runs. A
+step is one run of every fused program; K steps are timed between a sync and
+hipEvents on both sides, with the inputs already in HBM. The perf lowering
+forms some values inside the launches that read them, so it moves fewer bytes
+than the fusion contract's one launch per fused node would: `config.step_bytes`
+is what it moves (the numerator of `value`), `config.contract_step_bytes` the
+contract's count of the same programs.
 
 Rowwise (config 3) GB/s and matmul (config 4) TFLOP/s are reported beside it,
 with fused-vs-unfused speedups per program. `roofline` is the dominant kernel
@@ -389,7 +393,7 @@ def compose(full: dict) -> dict:
         "dtype": "f32", "data": "synthetic",
         "config": {"workload": "C2 fused elementwise chains fwd+grad, fp32 [8192,1024]",
                    "programs": c2["programs"], "shape": c2["shape"], "step_bytes": c2["stepBytes"],
-                   "streams": c2["schedule"]["streams"]},
+                   "contract_step_bytes": c2.get("contractBytes"), "streams": c2["schedule"]["streams"]},
         "roofline": {"bound": "hbm", "achieved": dom["gbs"], "peak": HBM_PEAK, "unit": "GB/s", "frac": dom["gbs"] / HBM_PEAK,
                      "traffic": traffic, "traffic_source": traffic_src, "kernel": dom["code"], "kernel_avg_us": dom["avgUs"],
                      "bytes_per_launch": dom["bytesPerLaunch"], "timing": timing,

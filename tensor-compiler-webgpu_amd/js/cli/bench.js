@@ -178,12 +178,15 @@ function measureGraph(runner, bench, name, graph, keep, inputs, opts) {
   }
   const bytesF = lf.launches.reduce((s, l) => s + l.bytes, 0);
   const bytesU = lu.launches.reduce((s, l) => s + l.bytes, 0);
+  // The fusion contract's count of the same program: one launch per fused node (the
+  // reference's own accounting of a fused program, workloads.js:155-175).
+  const bytesC = lowerMI355X(f.graph).launches.reduce((s, l) => s + l.bytes, 0);
   const flops = lf.launches.reduce((s, l) => s + (l.flops || 0), 0);
   const groups = launchU ? groupVerdicts(f, launchF, launchU) : [];
   const res = {
     name, launches: { fused: lf.launches.length, unfused: lu.launches.length }, k: t.k,
     fused: t.stats.fused, unfused: t.stats.unfused, verdict: verdict(t.stats.unfused, t.stats.fused),
-    bytes: { fused: bytesF, unfused: bytesU }, flops,
+    bytes: { fused: bytesF, unfused: bytesU, contract: bytesC }, flops,
     gbs: { fused: bytesF / (t.stats.fused.median * 1e3), unfused: bytesU / (t.stats.unfused.median * 1e3) },
     tflops: flops ? { fused: flops / (t.stats.fused.median * 1e6), unfused: flops / (t.stats.unfused.median * 1e6) } : null,
     bitwiseSameOutputs: { same, total }, groups, launchF, launchU,
@@ -306,7 +309,8 @@ function c2(runner, bench, opts) {
         const lf = lowerMI355X(f.graph, { perf: true, keep: v.keep.map((id) => f.index.get(id)) });
         runner.functions(lf);
         programs.push(prepared(runner, f.graph, lf, inputs, arena ? { arena: { keep: v.keep.map((id) => f.index.get(id)) } } : undefined));
-        results.push({ name: `c2-p${s}-${kind}`, bytes: { fused: lf.launches.reduce((q, l) => q + l.bytes, 0) }, launchF: [],
+        results.push({ name: `c2-p${s}-${kind}`, bytes: { fused: lf.launches.reduce((q, l) => q + l.bytes, 0),
+          contract: lowerMI355X(f.graph).launches.reduce((q, l) => q + l.bytes, 0) }, launchF: [],
           launches: launchRecords(lf) });
         continue;
       }
@@ -356,6 +360,7 @@ function c2(runner, bench, opts) {
   const headline = stepOnly ? sequential : timeStepsChecked(() => group.run());
   const ms = headline.msPerStep * K, wallMs = headline.wallMsPerStep * K;
   const stepBytes = results.reduce((s, r) => s + r.bytes.fused, 0);
+  const contractBytes = results.reduce((s, r) => s + r.bytes.contract, 0);
   // The roofline kernel: the fused kernel moving the most algorithmic bytes per step,
   // chosen without timing so a profile of the same step names the same kernel (each
   // fused body is its own kernel, at one size, so its average is well defined). Its
@@ -386,7 +391,8 @@ function c2(runner, bench, opts) {
   const schedule = stepOnly ? { streams: 1 } : { streams: S, bytesPerStream: group.load, sequential };
   const groups = groupSummary([].concat.apply([], results.map((r) => r.groups || [])));
   return { config: 'c2', shape: [R, C], programs: P, steps: K, warmup: W, arena, schedule, msPerStep: ms / K, wallMsPerStep: wallMs / K,
-    stepBytes, gbs: stepBytes / ((ms / K) * 1e6), dominant: dom, groups, results };
+    stepBytes, gbs: stepBytes / ((ms / K) * 1e6), contractBytes, contractGbs: contractBytes / ((ms / K) * 1e6),
+    dominant: dom, groups, results };
 }
 
 /**

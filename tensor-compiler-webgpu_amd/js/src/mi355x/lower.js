@@ -1084,16 +1084,21 @@ function lowerOnce(graph, opts, noAbsorb, noForm) {
   if (opts.perf) for (const node of graph.nodes) if (launched(node)) for (const id of inputsOf(node)) lastRead.set(id, node.id);
   // Output stores (perf lowering), a hint like the last reads: an output the next launch of
   // the list reads is stored through the caches, where that launch finds it (false); one of
-  // STREAM_FROM bytes or more that it does not read is stored non-temporally, so it does not
-  // displace what that launch reads (true). Elementwise kernels store non-temporally unless
-  // false, rowwise kernels only if true.
+  // STREAM_FROM bytes or more that the next launch does not read is stored non-temporally,
+  // so it does not displace what that launch reads (true). The last launch's output is
+  // stored non-temporally where the launch streams two or more such operands, and left to
+  // the kernel otherwise: measured on the rowwise programs of config 3, the gradients'
+  // last launch (reading x and dy) is 11 % faster with non-temporal stores and the
+  // forwards' one launch (reading x) 8 % slower. Elementwise kernels store non-temporally
+  // unless false, rowwise kernels only if true.
   const streamOut = new Map();
   if (opts.perf) {
+    const big = (id) => size(graph.nodes[id].shape) * 4 >= STREAM_FROM;
     const order = graph.nodes.filter(launched);
     order.forEach((node, i) => {
       const next = order[i + 1];
       if (next && inputsOf(next).includes(node.id)) streamOut.set(node.id, false);
-      else if (size(node.shape) * 4 >= STREAM_FROM) streamOut.set(node.id, true);
+      else if (big(node.id) && (next || new Set(inputsOf(node).filter(big)).size >= 2)) streamOut.set(node.id, true);
     });
   }
   for (const node of graph.nodes) {
