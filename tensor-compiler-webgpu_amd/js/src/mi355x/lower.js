@@ -862,35 +862,54 @@ const STREAM_FROM = 1 << 20;
 /** Full rows a launch forming values may hold in registers (its cached operands). */
 const FORM_CACHED = 6;
 /**
- * Element ops a value's readers may repeat between them to form it: (readers - 1) times
- * the ops it computes per element (elementOps). Forming trades the value's write and
- * read-back for that arithmetic; beyond a few ops per element it costs more than the
- * bytes save (the reference's lost-reuse workload: a 16-op chain shared by four readers).
+ * The estimate by which the perf lowering forms values (MI355X): a launch takes its bytes
+ * at EST_BW, plus its vector work at EST_ALU, plus EST_LAUNCH — added, not overlapped: a
+ * config-2 gradient kernel repeating two exp and two tanh per element measured 28.3 us,
+ * its bytes alone 16.8 us and its arithmetic 10.9 us by this count. EST_BW lies
+ * between the measured copy and read ceilings (5.7 and 6.4 TB/s); EST_ALU is 256 CUs of
+ * 4 SIMDs of 16 lanes at 2.4 GHz (a wavefront's instruction over 4 cycles); EST_LAUNCH is
+ * about what a launch adds to a replayed step of small kernels.
  */
-const FORM_OPS = 16;
-
-/** Ops a body computes per element of its widest values (reductions included; shape-only ops not). */
-function elementOps(body) {
-  const widest = Math.max(...body.nodes.map((n) => size(n.shape)));
-  const free = new Set(['input', 'const', 'reshape', 'broadcast', 'transpose', 'stopGradient']);
-  return body.nodes.filter((n) => isReduce(n) || (!free.has(n.op) && size(n.shape) === widest)).length;
-}
+const EST_BW = 6.0e12;
+const EST_ALU = 256 * 4 * 16 * 2.4e9;
+const EST_LAUNCH = 2e-6;
+/**
+ * Vector instructions per element of each op's tcmi:: form: exp, log and the reciprocal
+ * behind div and tanh run on the transcendental unit at a quarter of the rate; tanh
+ * also clamps, takes |x| and restores the sign. Shape-only ops cost nothing here.
+ */
+const OP_COST = { exp: 5, log: 10, tanh: 18, div: 5, sqrt: 5, relu: 2, step: 2, neg: 1, add: 1, sub: 1, mul: 1,
+  stopGradient: 0, copy: 0, reshape: 0, broadcast: 0, transpose: 0, input: 0, const: 0 };
 
 /**
- * Whether the value at node `v` of a reader's body is spread by a broadcast onto more
- * elements than it has (the reader would compute it once per element it is spread to: the
- * reference's broadcast-recompute workload), other than a row value spread along the rows
- * of a rowwise body, which that kernel computes once per row. Reshapes are followed.
+ * Estimated seconds of one launch running `body` (output `output`) over buffers `ins`
+ * (graph `graph` for their sizes). Elementwise bodies compute every node at every
+ * output element (a broadcast's source again at each element it is spread to); rowwise
+ * bodies compute the elements under each reduction and under the output once per element
+ * of the rows, a row value once per row (not counted), and accumulate each reduction once
+ * per element.
  */
-function expanded(body, v, lay) {
-  const consumers = body.nodes.map(() => []);
-  for (const n of body.nodes) for (const i of n.inputs) consumers[i].push(n);
-  const walk = (id) => consumers[id].some((n) => {
-    if (n.op === 'reshape') return walk(n.id);
-    if (n.op !== 'broadcast' || size(n.shape) === size(body.nodes[id].shape)) return false;
-    return !(lay.R && size(body.nodes[id].shape) === lay.R && rowBroadcast(body.nodes[id].shape, n.shape, lay.C));
-  });
-  return walk(v);
+function launchEstimate(graph, body, output, ins) {
+  const lay = rowLayout(body, output);
+  const rowwise = !!(lay && lay.R);
+  const full = rowwise ? lay.R * lay.C : size(body.nodes[output].shape);
+  const rowTier = (n) => rowwise && size(n.shape) === lay.R && lay.R !== full;
+  const roots = [output];
+  let ops = 0;
+  if (rowwise) for (const n of body.nodes) if (isReduce(n)) { roots.push(n.inputs[0]); ops += full; }
+  for (const root of roots) {
+    const seen = new Set();
+    const walk = (id) => {
+      const n = body.nodes[id];
+      if (seen.has(id) || isReduce(n) || (rowTier(n) && n.op !== 'input')) return;
+      seen.add(id);
+      ops += (OP_COST[n.op] === undefined ? 1 : OP_COST[n.op]) * full;
+      for (const i of n.inputs) walk(i);
+    };
+    walk(root);
+  }
+  const bytes = 4 * (ins.reduce((acc, x) => acc + size(graph.nodes[x].shape), 0) + size(body.nodes[output].shape));
+  return bytes / EST_BW + ops / EST_ALU + EST_LAUNCH;
 }
 
 function lowerMI355X(graph, options) {
@@ -966,11 +985,13 @@ function lowerOnce(graph, opts, noAbsorb, noForm) {
   // full or row size: rowLayout), else an elementwise one; the reductions run with the
   // same lanes and order as in the value's own launch (the rowwise kernel's layout depends
   // on the row length and tuning alone), so every bit is the plain lowering's. A value is
-  // formed where that moves no more bytes: the readers reading the value's operands that
-  // they do not read already, against the value's launch reading them and writing it and
-  // each reader reading it back (LayerNorm's centred rows and statistics, softmax's
-  // exponentials and row sums: the backward of a row function then reads x and dy alone).
-  // Values are taken in graph order, so a value's own operands are settled before it.
+  // formed where that takes no longer by launchEstimate: its own launch and its readers as
+  // they are, against the readers forming it. Bytes the readers save (the value's write
+  // and read-backs) weigh against the operands they read instead and the arithmetic they
+  // repeat, priced by op (LayerNorm's centred rows and statistics, softmax's exponentials
+  // and row sums: the backward of a row function then reads x and dy alone; a chain of
+  // transcendental ops shared by several readers stays a launch). Values are taken in
+  // graph order, so a value's own operands are settled before it.
   // Not under a sabotage (the planted kernel runs alone) or with rowwise and row-reduction
   // tunings that differ (the reductions' lanes would).
   const formedSet = new Set();
@@ -1028,22 +1049,21 @@ function lowerOnce(graph, opts, noAbsorb, noForm) {
       const readers = order.filter((r) => r !== u && !formedSet.has(r.id) && reads.get(r.id).has(u.id));
       if (!readers.length || !readers.every((r) => baseBody(r.id))) continue;
       const own = compose(u.id, formedSet);
-      if (!rowLayout(own.body, own.output) || (readers.length - 1) * elementOps(own.body) > FORM_OPS) continue;
+      if (!rowLayout(own.body, own.output)) continue;
+      const est = (c) => launchEstimate(graph, c.body, c.output, c.ins);
       const trial = new Set(formedSet).add(u.id);
-      let ok = true, after = 0;
+      let ok = true, after = 0, before = est(own);
       for (const r of readers) {
         const c = compose(r.id, trial);
         const lay = rowLayout(c.body, c.output);
-        // Within the argument block, at most FORM_CACHED full rows held in registers, and
-        // the value computed at its own elements (once per row for a row value).
-        if (!lay || c.ins.length > cg.MAX_IN || (lay.R && c.ins.filter((x) => sz(x) === lay.R * lay.C).length > FORM_CACHED)
-          || expanded(c.body, c.made.get(u.id), lay)) {
+        // Within the argument block, and at most FORM_CACHED full rows held in registers.
+        if (!lay || c.ins.length > cg.MAX_IN || (lay.R && c.ins.filter((x) => sz(x) === lay.R * lay.C).length > FORM_CACHED)) {
           ok = false;
           break;
         }
-        for (const x of own.ins) if (!reads.get(r.id).has(x)) after += sz(x);
+        after += est(c);
+        before += est(compose(r.id, formedSet));
       }
-      const before = own.ins.reduce((acc, x) => acc + sz(x), 0) + sz(u.id) * (1 + readers.length);
       if (!ok || after > before) continue;
       formedSet.add(u.id);
       for (const r of readers) {
