@@ -76,7 +76,7 @@ function timeLaunches(runner, bench, program, reps) {
     for (const l of members) {
       out.push({ node: l.node, kind: l.kind, pattern: l.pattern || null, code: l.code, bytes: l.bytes, flops: l.flops,
         us: r.stats.one.median / n, minUs: r.stats.one.min / n, maxUs: r.stats.one.max / n, rowFolds: l.rowFolds || null, absorbed: l.absorbed || null,
-        batched: n > 1 ? n : undefined, joint: b && b.joint ? true : undefined });
+        formed: l.formed || null, batched: n > 1 ? n : undefined, joint: b && b.joint ? true : undefined });
     }
     one.destroy();
     i += n;
@@ -91,9 +91,11 @@ function timeLaunches(runner, bench, program, reps) {
  * loses only when the ranges do not overlap (the fused launch's min-max against the
  * members' summed mins and maxes). A launch that also forms the reductions folded into
  * it (the perf lowering's row folds), the producers of their operands formed in the
- * same launch, and the producers an elementwise launch absorbed, does their work as well:
- * the unfused launches of those nodes (of their groups' members, where one is a group's
- * sink) count on its side too (`folded`: their node ids in the unfused graph).
+ * same launch, the producers an elementwise launch absorbed and the values a launch
+ * forms from what their own launches would read, does their work as well: the unfused
+ * launches of those nodes (of their groups' members, where one is a group's sink) count
+ * on its side too (`folded`: their node ids in the unfused graph). A node that several
+ * launches compute counts a 1/k share in each of their k groups.
  */
 function groupVerdicts(f, launchF, launchU) {
   const fusedAt = new Map(launchF.map((l) => [l.node, l]));
@@ -102,40 +104,53 @@ function groupVerdicts(f, launchF, launchU) {
   for (const g of f.groups) if (f.index.has(g.sink)) groupAt.set(f.index.get(g.sink), g);
   const original = new Map();
   for (const [id, fid] of f.index) if (!original.has(fid)) original.set(fid, id);
+  // The fused nodes a launch computes besides its own: reductions and producers folded
+  // into it, producers it absorbed, values it forms (with what their own launches fold
+  // and absorb). Each is keyed by its group's sink (or its original node).
+  const takenBy = (fl, own) => {
+    const fids = [];
+    const absorbed = (records) => { for (const a of records || []) { fids.push(a.producer); absorbed(a.absorbed); } };
+    const folds = (rfs) => { for (const rf of rfs || []) fids.push(...(rf.producer === undefined ? [rf.reduction] : [rf.reduction, rf.producer])); };
+    absorbed(fl.absorbed);
+    folds(fl.rowFolds);
+    for (const v of fl.formed || []) { fids.push(v.value); folds(v.rowFolds); absorbed(v.absorbed); }
+    const keys = new Map();
+    for (const fid of fids) {
+      const g2 = groupAt.get(fid);
+      if (g2 === own) continue;
+      const id = g2 ? g2.sink : original.get(fid);
+      if (id !== undefined) keys.set(id, g2 ? g2.members : [id]);
+    }
+    return keys;
+  };
+  // A node several launches compute (a value formed by each of its readers) counts
+  // a share of its unfused time in each of their groups, so no unfused launch counts twice.
+  const ownerOf = (fl) => groupAt.get(fl.node) || null;
+  const takers = new Map();
+  for (const fl of launchF) for (const id of takenBy(fl, ownerOf(fl)).keys()) takers.set(id, (takers.get(id) || 0) + 1);
   const groups = [];
   for (const g of f.groups) {
     if (!f.index.has(g.sink)) continue;
     const fl = fusedAt.get(f.index.get(g.sink));
     if (!fl) continue;
-    const members = new Set(g.members);
-    const folded = [];
-    const formed = [];
-    const walk = (records) => { for (const a of records || []) { formed.push(a.producer); walk(a.absorbed); } };
-    walk(fl.absorbed);
-    for (const rf of fl.rowFolds || []) formed.push(...(rf.producer === undefined ? [rf.reduction] : [rf.reduction, rf.producer]));
-    for (const fid of formed) {
-      const g2 = groupAt.get(fid);
-      if (g2 === g) continue;
-      const id = g2 ? g2.sink : original.get(fid);
-      if (id === undefined) continue;
-      folded.push(id);
-      if (g2) for (const m of g2.members) members.add(m);
-      else members.add(id);
-    }
+    const weight = new Map(Array.from(g.members, (m) => [m, 1]));
+    const taken = takenBy(fl, g);
+    for (const [id, members] of taken) for (const m of members) if (!weight.has(m)) weight.set(m, 1 / takers.get(id));
     const sum = { median: 0, min: 0, max: 0 };
     let launches = 0;
-    for (const m of members) {
+    for (const [m, w] of weight) {
       const u = unfusedAt.get(m);
       if (!u) continue;
-      sum.median += u.us; sum.min += u.minUs; sum.max += u.maxUs; launches++;
+      sum.median += w * u.us; sum.min += w * u.minUs; sum.max += w * u.maxUs; launches++;
     }
     if (!launches) continue;
     // A group whose launch is one part of a joint launch (an attention gradient's dQ, dK
     // and dV in one kernel) takes the whole launch's time: the group holds all three.
     const whole = fl.joint ? fl.batched : 1;
     const v = verdict(sum, { median: fl.us * whole, min: fl.minUs * whole, max: fl.maxUs * whole });
-    groups.push({ sink: g.sink, kind: g.kind, pattern: g.pattern, members: members.size, unfusedLaunches: launches,
-      fusedUs: fl.us * whole, unfusedUs: sum.median, speedup: v.speedup, verdict: v.verdict, folded: folded.length ? folded : undefined });
+    groups.push({ sink: g.sink, kind: g.kind, pattern: g.pattern, members: weight.size, unfusedLaunches: launches,
+      fusedUs: fl.us * whole, unfusedUs: sum.median, speedup: v.speedup, verdict: v.verdict,
+      folded: taken.size ? Array.from(taken.keys()) : undefined });
   }
   return groups;
 }
@@ -226,20 +241,26 @@ function dominantByBytes(programs) {
   return d ? { code: d.code, kind: d.kind, pattern: d.pattern, count: d.count, bytes: d.bytes, bytesPerLaunch: d.bytes / d.count } : null;
 }
 
+/** Copies a cold launch rotates over: at least 8, and enough to span COLD_SPAN bytes. */
 const COLD_SETS = 8;
+/** Four times the 256 MB last-level cache: a set is long evicted when its turn comes again. */
+const COLD_SPAN = 4 * 256 * 2 ** 20;
 
 /**
- * Launch `l` of program `p` timed cold: COLD_SETS copies of every buffer it reads and
- * writes, the launch issued on set i mod COLD_SETS, k launches back to back between two
- * events, k chosen for >= 4 ms (or `runs` launches untimed, for a profiler). Returns the
- * average µs per launch and the bytes the sets span.
+ * Launch `l` of program `p` timed cold: copies of every buffer it reads and writes (at
+ * least COLD_SETS of them, and enough to span COLD_SPAN bytes), the launch issued on set
+ * i mod the set count, k launches back to back between two events, k chosen for >= 4 ms
+ * (or `runs` launches untimed, for a profiler). Returns the average µs per launch, the
+ * set count and the bytes the sets span.
  */
 function coldLaunch(runner, bench, p, l, runs) {
   const a = runner.a;
   const ids = Array.from(new Set(l.inputs.concat([l.node])));
+  const perSet = ids.reduce((acc, id) => acc + p.n[id] * 4, 0);
+  const COLD = Math.max(COLD_SETS, Math.ceil(COLD_SPAN / perSet));
   const sets = [];
   let span = 0;
-  for (let s = 0; s < COLD_SETS; s++) {
+  for (let s = 0; s < COLD; s++) {
     const bufs = p.bufs.slice();
     const owned = [];
     for (const id of ids) {
@@ -254,20 +275,20 @@ function coldLaunch(runner, bench, p, l, runs) {
     sets.push({ prog, owned });
   }
   a.sync();
-  const issue = (k) => { for (let i = 0; i < k; i++) sets[i % COLD_SETS].prog.run(); };
+  const issue = (k) => { for (let i = 0; i < k; i++) sets[i % COLD].prog.run(); };
   let out;
   if (runs) {
     issue(runs);
     a.sync();
-    out = { runs, sets: COLD_SETS, spanBytes: span };
+    out = { runs, sets: COLD, spanBytes: span };
   } else {
-    issue(2 * COLD_SETS);
+    issue(2 * COLD);
     a.sync();
     a.eventRecord(bench.start);
-    issue(COLD_SETS);
+    issue(COLD);
     a.eventRecord(bench.end);
-    const one = a.eventElapsed(bench.start, bench.end) / COLD_SETS;
-    const k = Math.max(COLD_SETS, Math.ceil(4 / one / COLD_SETS) * COLD_SETS);
+    const one = a.eventElapsed(bench.start, bench.end) / COLD;
+    const k = Math.max(COLD, Math.ceil(4 / one / COLD) * COLD);
     const reps = [];
     bench.region(() => {
       for (let r = 0; r < 9; r++) {
@@ -278,7 +299,7 @@ function coldLaunch(runner, bench, p, l, runs) {
       }
     });
     const st = summarize(reps);
-    out = { avgUs: st.median, minUs: st.min, maxUs: st.max, k, reps: reps.length, sets: COLD_SETS, spanBytes: span };
+    out = { avgUs: st.median, minUs: st.min, maxUs: st.max, k, reps: reps.length, sets: COLD, spanBytes: span };
   }
   for (const s of sets) { s.prog.destroy(); for (const h of s.owned) a.free(h); }
   return out;
@@ -378,10 +399,10 @@ function c2(runner, bench, opts) {
       one.destroy();
       dom.warm = { avgUs: t.stats.one.median, gbs: dom.bytesPerLaunch / (t.stats.one.median * 1e3), reps: 21 };
     }
-    // Cold: the figure `roofline` reports. The launch rotates over COLD_SETS copies of its
-    // operands and output, so between two launches on one set the other sets' bytes
-    // (several times the last-level cache) have passed through it: every launch reads its
-    // operands from HBM.
+    // Cold: the figure `roofline` reports. The launch rotates over copies of its operands
+    // and output spanning at least four times the last-level cache, so between two
+    // launches on one set the other sets' bytes have passed through it: every launch
+    // reads its operands from HBM.
     dom.cold = coldLaunch(runner, bench, p, l, 0);
     dom.avgUs = dom.cold.avgUs;
     dom.gbs = dom.bytesPerLaunch / (dom.avgUs * 1e3);
