@@ -733,7 +733,8 @@ ${producer ? formed : `      const ${T} v = ${ld('x', '(size_t)k * inner + j')};
  * whether its operands are materialised or read through views.
  */
 function gemmTiling(batch, M, N, K, tuning, peers) {
-  const t = tuning || {};
+  // A tuning's `byShape` entry for this product ('batch x M x N x K') overrides it.
+  const t = Object.assign({}, tuning || {}, ((tuning || {}).byShape || {})[`${batch}x${M}x${N}x${K}`] || {});
   // Products of this shape that may share one dispatch (1 if unknown): they share the
   // chip, so the K split aims at its workgroup count over all of them.
   const P = peers || 1;

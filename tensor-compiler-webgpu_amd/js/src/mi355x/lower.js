@@ -119,10 +119,11 @@ function rowFoldBody(graph, node, rowFold) {
 
 /**
  * The body a launch of `node` runs in the perf lowering before it forms any value it reads
- * (lowerNode's elementwise, rowwise, row-statistics-chain and row-reduction kernels), on
- * inputs a{k} at its operand positions: a row-statistics chain with its reductions folded
- * in; a fused elementwise or rowwise body, or one elementwise op, with its broadcast
- * operands widened and its absorbed producers formed; a reduction over the last
+ * (lowerNode's elementwise, gather, rowwise, row-statistics-chain and row-reduction
+ * kernels), on inputs a{k} at its operand positions: a row-statistics chain with its
+ * reductions folded in; a fused elementwise or rowwise body, or one elementwise op or
+ * launched broadcast or transpose, with its broadcast operands widened and its absorbed
+ * producers formed; a reduction over the last
  * non-trivial axis on its operand as [rows, n] rows (its producers formed), reshaped to
  * its own shape. Returns { body, output }, or null for other launches.
  */
@@ -132,7 +133,7 @@ function launchBase(graph, node, folds, rowFold, absorbs) {
     if (node.attrs.kind !== 'elementwise' && node.attrs.kind !== 'rowwise') return null;
     return absorbProducers(graph, widenInputs(bodyOf(node), node.attrs.output, folds), absorbs);
   }
-  if (ELEMENTWISE_OPS.has(node.op)) {
+  if (ELEMENTWISE_OPS.has(node.op) || node.op === 'broadcast' || node.op === 'transpose') {
     const one = oneOpBody(graph, node);
     return absorbProducers(graph, widenInputs(one.body, one.output, folds), absorbs);
   }
