@@ -596,6 +596,9 @@ ${indent(store, '    ')}
  * Every output sums its terms in a fixed order (deterministic). Scalar form
  * (inner % 4 != 0): the same with one column per lane.
  */
+/** Elements up to which a column reduction runs in one launch (256 KB of fp32). */
+const COLRED_ONE_PASS = 1 << 16;
+
 function colreduceKernels(op, outer, n, inner, tuning, producer) {
   const tune = tuning || {};
   const isMax = op === 'max';
@@ -606,7 +609,11 @@ function colreduceKernels(op, outer, n, inner, tuning, producer) {
   const colsPerBlock = 64 * W;
   const colBlocks = Math.ceil(inner / colsPerBlock);
   const want = tune.blocks || 1024;
-  let splits = Math.max(1, Math.min(Math.ceil(want / Math.max(1, colBlocks * outer)), Math.ceil(n / 32)));
+  // Up to COLRED_ONE_PASS elements the rows are not split: one launch, whose workgroups
+  // each sum whole columns, costs less than a second kernel combining chunks (config 1's
+  // bias gradients over 128 rows).
+  let splits = !tune.blocks && outer * n * inner <= COLRED_ONE_PASS ? 1
+    : Math.max(1, Math.min(Math.ceil(want / Math.max(1, colBlocks * outer)), Math.ceil(n / 32)));
   const chunk = Math.ceil(n / splits);
   splits = Math.ceil(n / chunk);
   const T = vec ? 'tcmi::f4' : 'float';
