@@ -1210,10 +1210,12 @@ async function main() {
       break;
     }
     case 'config-graphs': {
-      // Forward and gradient graphs of configs 3 and 4 at the requested sizes.
+      // Forward and gradient graphs of configs 2, 3 and 4 at the requested sizes.
       const cfg = require('../src/builders/configs');
+      const { chainWorkload } = require('../src/builders/chains');
       const one = (v) => ({ graph: v.graph.toJSON(), keep: v.keep });
       out = {
+        c2: (req.c2 || []).map((c) => { const w = chainWorkload(c.seed, c.R, c.C); return { seed: c.seed, R: c.R, C: c.C, forward: one(w.forward), gradient: one(w.gradient) }; }),
         c3: (req.c3 || []).map((c) => { const g = cfg.c3Graphs(c.fn, c.R, c.C); return { fn: c.fn, R: c.R, C: c.C, forward: one(g.forward), gradient: one(g.gradient) }; }),
         c4: (req.c4 || []).map((c) => { const g = cfg.c4Graphs(c.act, c.M, c.K, c.N); return { act: c.act, M: c.M, K: c.K, N: c.N, forward: one(g.forward), gradient: one(g.gradient) }; }),
       };

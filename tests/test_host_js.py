@@ -624,3 +624,36 @@ def test_formed_kernels_declare_each_name_once(tool, workload):
         row = [x for x in declared if x.startswith("R") or x.startswith("red")]
         assert len(row) == len(set(row)), (name, sorted(x for x in row if row.count(x) > 1))
         assert loops > 0 or not row
+
+
+def test_formation_prices_repeated_transcendentals(tool):
+    """The perf lowering forms a value in its readers where its launch estimate (bytes at
+    6 TB/s plus op-priced vector work plus a launch cost, added) does not rise. In config
+    2's program 0 gradient at full size, the forward chain's last value (two exp and two
+    tanh per element) is read by four launches: repeating it in each would cost more than
+    its write and read-backs, so it stays a launch, and the cheaper values before it are
+    formed in the launches that read them. With a flat count of repeated ops instead,
+    all four readers once repeated the chain (28 us for a 100.7 MB kernel on the GPU)."""
+    g = tool("config-graphs", {"c2": [{"seed": 0, "R": 8192, "C": 1024}]})["c2"][0]["gradient"]
+    d = tool("perf-lower", {"graph": g["graph"], "keep": g["keep"], "fuse": {}})
+    nodes = d["graph"]["nodes"]
+    launched = {x["node"] for x in d["launches"]}
+    formed = {f["value"] for fs in d["formed"].values() for f in fs}
+
+    def ops(i):
+        n = nodes[i]
+        return [b["op"] for b in n["attrs"]["body"]["nodes"]] if n["op"] == "fused" else [n["op"]]
+    readers = {}
+    for i, n in enumerate(nodes):
+        for x in n["inputs"]:
+            readers.setdefault(x, set()).add(i)
+    # A launch computes its own body and the values its record says it forms.
+    def tanhs(i):
+        return ops(i).count("tanh") + sum(ops(f["value"]).count("tanh") for f in d["formed"].get(str(i), []))
+    chain = [i for i in launched if tanhs(i) >= 2 and len(readers.get(i, ())) >= 3]
+    assert chain, "the shared transcendental chain is not a launch"
+    assert formed, "nothing formed"
+    # No launch repeats the chain: the launches reading the chain's value read it.
+    for i in chain:
+        assert i not in formed and all(str(r) not in d["formed"] or i not in {f["value"] for f in d["formed"][str(r)]}
+                                       for r in readers[i])
