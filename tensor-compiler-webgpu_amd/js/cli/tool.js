@@ -1385,14 +1385,14 @@ async function main() {
     }
     case 'batch-check': {
       // Batched launches of model steps and corpus programs (perf lowering), checked against
-      // the plain order; with `plant`, the two planted mistakes of batch_check.js as well.
+      // the plain order; with `plant`, the planted mistakes of batch_check.js as well.
       const { checkBatches, plantBatchMistake } = require('../src/testing/batch_check');
       const one = (name, graph, keep) => {
         const plain = lowerMI355X(graph, { perf: true, keep, batch: false, absorb: true });
         const batched = lowerMI355X(graph, { perf: true, keep, absorb: true });
         const res = { name, launches: batched.launches.length, check: checkBatches(plain, batched) };
         if (req.plant) {
-          for (const kind of ['dependent', 'early', 'grid']) {
+          for (const kind of ['dependent', 'early', 'grid', 'body']) {
             const bad = plantBatchMistake(batched, kind);
             if (bad) res[kind] = checkBatches(plain, bad);
           }

@@ -3,8 +3,8 @@
 // batchPlan): the batched launch list must hold the same launches as the plain
 // order, every launch must read only buffers already written (or written by no
 // launch), the members of a batch must be launches of the same kernel texts
-// (or of matmul texts that differ, each member then run by its own case of the
-// batched kernel, which holds exactly its own body) over the same grids (a column
+// (or of matmul or elementwise texts that differ, each member then run by its own case
+// of the batched kernel, which holds exactly its own body) over the same grids (a column
 // sum's text leaves its outer extent to the grid) with no data path between them, or
 // the three parts of one attention gradient in one launch of their joint kernel; each
 // batched kernel's grid must repeat the
@@ -23,19 +23,24 @@ function runsOwnBody(bk, k, x) {
   if (end < at) return false;
   const kase = bk.source.slice(bk.source.indexOf('{', at) + 1, end);
   const m = kase.match(new RegExp(`(${bk.name}_v\\d+)_(?:av|bv|epi)`));
-  if (!m) return false;
-  const structs = (src, prefix) => (src.match(new RegExp(`struct ${prefix}_(?:av|bv|epi) \\{[\\s\\S]*?\\n\\};\\n`, 'g')) || [])
-    .map((t) => t.split(prefix).join('@')).join('');
-  const mine = structs(x.source, x.name);
-  if (!(mine.length > 0 && structs(bk.source, m[1]) === mine)) return false;
+  if (/^tcmi_ew_/.test(x.name)) {
+    // An elementwise member declares no structs: its case is its own statements alone.
+    if (m || /\bstruct\b/.test(x.source)) return false;
+  } else {
+    if (!m) return false;
+    const structs = (src, prefix) => (src.match(new RegExp(`struct ${prefix}_(?:av|bv|epi) \\{[\\s\\S]*?\\n\\};\\n`, 'g')) || [])
+      .map((t) => t.split(prefix).join('@')).join('');
+    const mine = structs(x.source, x.name);
+    if (!(mine.length > 0 && structs(bk.source, m[1]) === mine)) return false;
+  }
   // The member's own statements: its entry point's body, names and z index normalised.
   const sig = `${x.name}(const TcmiArgs A) {`;
   const own = x.source.slice(x.source.indexOf(sig) + sig.length).replace(/\}\s*$/, '');
-  const norm = (t, prefix) => t.split(`${prefix}_`).join('@_')
+  const norm = (t, prefix) => (prefix ? t.split(`${prefix}_`).join('@_') : t)
     .replace(/\((blockIdx\.z|wg\.z) % \d+u\)/g, '$1')
     .replace('const tcmi::Wg wg = tcmi::xcd_grouped();', '')
     .replace(/\s+/g, '');
-  return norm(kase, m[1]) === norm(own, x.name);
+  return norm(kase, m ? m[1] : null) === norm(own, x.name);
 }
 
 function checkBatches(plain, batched) {
@@ -79,9 +84,11 @@ function checkBatches(plain, batched) {
         const y = first.kernels[j];
         if (x.grid.join() !== y.grid.join() || x.block.join() !== y.block.join() || x.lds !== y.lds) return false;
         if (x.name === y.name) return true;
-        // Another matmul text (operand views, load modes, tiling or epilogue differ) over the
-        // same grid and workgroup: the batched kernel must run this member's own body.
-        return /^tcmi_mm_/.test(x.name) && /^tcmi_mm_/.test(y.name) && runsOwnBody(b.kernels[j], k, x);
+        // Another matmul text (operand views, load modes, tiling or epilogue differ), or
+        // another elementwise body, over the same grid and workgroup: the batched kernel
+        // must run this member's own body.
+        const both = (re) => re.test(x.name) && re.test(y.name);
+        return (both(/^tcmi_mm_/) || both(/^tcmi_ew_/)) && runsOwnBody(b.kernels[j], k, x);
       });
       if (!same || l.workspace !== first.workspace) return { ok: false, why: `batch at ${b.start}: member ${k} is not a launch of the same kernels` };
       unitOf[b.start + k] = b.start;
@@ -103,10 +110,22 @@ function checkBatches(plain, batched) {
  * and a later launch of the same kernel that reads its output (placed right after
  * it); `early` moves a launch in front of the launch that writes its first operand;
  * `grid` gives a batch's last member its kernel over twice the z extent (the same
- * text over another grid, as a column sum of another outer extent has).
+ * text over another grid, as a column sum of another outer extent has); `body`
+ * exchanges, in the launch list, the first member of a batch whose members run
+ * different bodies with a member of another kernel (each member's case of the batched
+ * kernel then holds the other's body).
  * Returns the modified lowering, or null when the list has no such pair.
  */
 function plantBatchMistake(lowered, kind) {
+  if (kind === 'body') {
+    const b = (lowered.batches || []).find((x) => x.kernels.length === 1 && x.kernels[0].variants);
+    if (!b) return null;
+    const v = b.kernels[0].variants;
+    const k = v.findIndex((name) => name !== v[0]);
+    const launches = lowered.launches.slice();
+    [launches[b.start], launches[b.start + k]] = [launches[b.start + k], launches[b.start]];
+    return Object.assign({}, lowered, { launches });
+  }
   if (kind === 'grid') {
     const b = (lowered.batches || [])[0];
     if (!b) return null;

@@ -1,10 +1,11 @@
 """Batched launches of the perf lowering (js/src/mi355x/lower.js batchPlan), checked on the
 CPU by js/src/testing/batch_check.js from the launch records alone: the batched list holds
 the plain list's launches, every launch reads only buffers written before it, a batch's
-members are launches of one kernel text with no data path between them, the batched grid
-has one z-slice per member, and launches that share the workspace keep their order. Two
-planted mistakes (a batch whose second member reads the first's output; a launch moved in
-front of its operand's writer) must be refused. The GPU side — batched runs bit for bit the
+members are launches of one kernel text (or of matmul or elementwise texts of one grid,
+each member then run by its own case of the batched kernel) with no data path between them, the batched grid
+has one z-slice per member, and launches that share the workspace keep their order. Planted
+mistakes (a batch whose second member reads the first's output; a launch moved in front of
+its operand's writer; a member over another grid; members' bodies exchanged) must be refused. The GPU side — batched runs bit for bit the
 plain ones — is in test_gpu_train.py (config 5's step) and test_gpu_fuzz.py (corpus programs)."""
 
 MODELS = [{"model": "transformer", "B": 64}, {"model": "transformer", "B": 1}, {"model": "mlp"},
@@ -25,12 +26,14 @@ def test_batched_launch_lists_are_valid_orders(tool):
 
 
 def test_planted_batch_mistakes_are_caught(tool):
-    """Three planted mistakes: a batch whose second member reads the first's output; a
+    """Four planted mistakes: a batch whose second member reads the first's output; a
     launch moved in front of its operand's writer; a member whose kernel has the same
     text over another grid (a column sum's text leaves its outer extent to the grid:
     batching two such launches by name alone once ran one member over the other's grid,
     which the GPU fuzz test caught as a canary overwrite and as perf-lowering
-    differences in 3 of 4000 corpus graphs)."""
+    differences in 3 of 4000 corpus graphs); two members of a batch whose members run
+    different bodies (matmuls, or elementwise chains of one grid) exchanged, so that each
+    member's case of the batched kernel holds the other's body."""
     res = tool("batch-check", {"models": MODELS[:1], "corpus": {"from": 1, "to": 900}, "plant": True})
     dep = [r for r in res if "dependent" in r]
     early = [r for r in res if "early" in r]
@@ -39,6 +42,9 @@ def test_planted_batch_mistakes_are_caught(tool):
     assert all(not r["dependent"]["ok"] for r in dep)
     assert all(not r["early"]["ok"] for r in early)
     assert all(not r["grid"]["ok"] and "member" in r["grid"]["why"] for r in grid), [r["grid"] for r in grid if r["grid"]["ok"]]
+    body = [r for r in res if "body" in r]
+    assert len(body) >= 100 and any(r["name"] == "transformer-64" for r in body)
+    assert all(not r["body"]["ok"] and "member" in r["body"]["why"] for r in body), [r["name"] for r in body if r["body"]["ok"]]
 
 
 def test_same_text_over_another_grid_is_not_batched(tool):
