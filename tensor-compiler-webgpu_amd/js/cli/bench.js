@@ -595,9 +595,10 @@ function trainStep(runner, bench, name, req, opts) {
   // The fused step under the fusion contract alone: the same lowering of the fused graph.
   const fsContract = fusedStep(m.step, { contract: true });
   runner.functions([fs.lowered, lu, fsContract.lowered]);
-  // 40 timed steps after 5 warm-ups: config 1's step is about 50 µs, so fewer steps would
-  // time a few hundred µs of work.
-  const K = Number(arg('train-steps', opts.quick ? 3 : 40)), W = opts.quick ? 2 : 5;
+  // Timed steps after 5 warm-ups: 40 of config 5's 2.2 ms step; 400 of config 1's step of
+  // about 35–70 µs (40 of them, under 3 ms, once read 9.6–10.0k steps/s through train()
+  // where 400 read 15.2–15.3k in the same code).
+  const K = Number(arg('train-steps', opts.quick ? 3 : name === 'c1' ? 400 : 40)), W = opts.quick ? 2 : 5;
   const batch = m.batch(0);
   const graph = !flag('no-trainer-graphs');
   const trainer = new HipTrainer(runner, fs, m.params, m.state, { graph });

@@ -1501,10 +1501,14 @@ const XCD_GROUPED = 'const tcmi::Wg wg = tcmi::xcd_grouped();';
  * epilogue and code are the same, so they can share one dispatch.
  */
 function batchFamily(k) {
-  // Elementwise kernels of one grid and workgroup size, whatever their bodies: each
-  // member runs its own (no LDS, every size baked into its text), so independent
-  // chains share one dispatch and one ramp and drain.
+  // Elementwise kernels, and rowwise kernels that reduce within wavefronts (no LDS), of
+  // one grid and workgroup size, whatever their bodies: each member runs its own (every
+  // size baked into its text), so independent launches share one dispatch and one ramp
+  // and drain.
   if (/^tcmi_ew_[0-9a-f]+$/.test(k.name) && !k.lds && !k.ldsStatic) return `ew@${k.grid.join(',')}/${k.block.join(',')}`;
+  if (/^tcmi_row_[0-9a-f]+$/.test(k.name) && !k.lds && !k.ldsStatic && !/__shared__/.test(k.source)) {
+    return `row@${k.grid.join(',')}/${k.block.join(',')}`;
+  }
   // Matmul tiles take their LDS from a pool shared by instantiations of one size
   // (tcmi::lds_pool); other kernels' views would each add their own LDS: one text a family.
   if (!/^tcmi_mm_[0-9a-f]+$/.test(k.name)) return `${k.name}@${k.grid.join(',')}/${k.block.join(',')}/${k.lds}`;

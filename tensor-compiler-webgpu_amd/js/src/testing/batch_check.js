@@ -3,7 +3,7 @@
 // batchPlan): the batched launch list must hold the same launches as the plain
 // order, every launch must read only buffers already written (or written by no
 // launch), the members of a batch must be launches of the same kernel texts
-// (or of matmul or elementwise texts that differ, each member then run by its own case
+// (or of matmul, elementwise or rowwise texts that differ, each member then run by its own case
 // of the batched kernel, which holds exactly its own body) over the same grids (a column
 // sum's text leaves its outer extent to the grid) with no data path between them, or
 // the three parts of one attention gradient in one launch of their joint kernel; each
@@ -23,8 +23,9 @@ function runsOwnBody(bk, k, x) {
   if (end < at) return false;
   const kase = bk.source.slice(bk.source.indexOf('{', at) + 1, end);
   const m = kase.match(new RegExp(`(${bk.name}_v\\d+)_(?:av|bv|epi)`));
-  if (/^tcmi_ew_/.test(x.name)) {
-    // An elementwise member declares no structs: its case is its own statements alone.
+  if (/^tcmi_(ew|row)_/.test(x.name)) {
+    // An elementwise or rowwise member declares no structs: its case is its own
+    // statements alone.
     if (m || /\bstruct\b/.test(x.source)) return false;
   } else {
     if (!m) return false;
@@ -85,10 +86,10 @@ function checkBatches(plain, batched) {
         if (x.grid.join() !== y.grid.join() || x.block.join() !== y.block.join() || x.lds !== y.lds) return false;
         if (x.name === y.name) return true;
         // Another matmul text (operand views, load modes, tiling or epilogue differ), or
-        // another elementwise body, over the same grid and workgroup: the batched kernel
-        // must run this member's own body.
+        // another elementwise or rowwise body, over the same grid and workgroup: the
+        // batched kernel must run this member's own body.
         const both = (re) => re.test(x.name) && re.test(y.name);
-        return (both(/^tcmi_mm_/) || both(/^tcmi_ew_/)) && runsOwnBody(b.kernels[j], k, x);
+        return (both(/^tcmi_mm_/) || both(/^tcmi_ew_/) || both(/^tcmi_row_/)) && runsOwnBody(b.kernels[j], k, x);
       });
       if (!same || l.workspace !== first.workspace) return { ok: false, why: `batch at ${b.start}: member ${k} is not a launch of the same kernels` };
       unitOf[b.start + k] = b.start;

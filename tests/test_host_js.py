@@ -612,18 +612,20 @@ def test_formed_kernels_declare_each_name_once(tool, workload):
     can come back in a later phase: the unfused training steps of the workload sweep,
     lowered with their row values formed by the launches reading them, once declared one
     row load twice (a compile error on the GPU). Every name a kernel declares is declared
-    once."""
+    once (in a batched kernel whose members run different bodies, once in each member's
+    case, a scope of its own)."""
     import re
     d = tool("perf-lower", {"workload": workload, "sources": True})
     assert d["formed"], "the case forms no values"
-    for name, src in d["sources"].items():
-        declared = re.findall(r"\bconst float (\w+) =", src)
-        loops = src.count("for (int s = 0;")
-        # Names inside the element loops repeat per loop (their own scopes); row-tier names
-        # (R...) and reduction results are declared once in the row loop.
-        row = [x for x in declared if x.startswith("R") or x.startswith("red")]
-        assert len(row) == len(set(row)), (name, sorted(x for x in row if row.count(x) > 1))
-        assert loops > 0 or not row
+    for name, text in d["sources"].items():
+        for src in re.split(r"\n\s*case \d+u: \{", text):
+            declared = re.findall(r"\bconst float (\w+) =", src)
+            loops = src.count("for (int s = 0;")
+            # Names inside the element loops repeat per loop (their own scopes); row-tier
+            # names (R...) and reduction results are declared once in the row loop.
+            row = [x for x in declared if x.startswith("R") or x.startswith("red")]
+            assert len(row) == len(set(row)), (name, sorted(x for x in row if row.count(x) > 1))
+            assert loops > 0 or not row
 
 
 def test_formation_prices_repeated_transcendentals(tool):
