@@ -320,7 +320,7 @@ def compose(full: dict) -> dict:
         extra["ceiling_1GiB_GBs"] = {"copy": _r(ceiling["copy"]["gbs"], 4), "read": _r(ceiling["read"]["gbs"], 4)}
     seq = c2["schedule"].get("sequential")
     dom = c2["dominant"]
-    extra["c2"] = {"GBs_2streams": _r(c2["gbs"], 4), "GBs_sequential": _r(seq["gbs"], 4) if seq else None,
+    extra["c2"] = {"GBs_streams": _r(c2["gbs"], 4), "GBs_sequential": _r(seq["gbs"], 4) if seq else None,
                    "frac_sequential": _r(seq["gbs"] / HBM_PEAK) if seq else None,
                    "roofline_kernel_cold_GBs": _r(dom["gbs"], 4), "roofline_kernel_warm_GBs": _r(dom["warm"]["gbs"], 4),
                    "groups": _groups(c2.get("groups")),

@@ -356,8 +356,8 @@ function c2(runner, bench, opts) {
   }
   // The headline step: every fused program once; W warm-up steps, then K timed steps
   // bracketed by hipEvents. The 16 programs are independent (each its own buffers), so
-  // the step issues them as one concurrent group over --c2-streams streams (default 2:
-  // 1 to 4 measured, 2 fastest), balanced by bytes; the sequential step, every program
+  // the step issues them as one concurrent group over --c2-streams streams (default 3:
+  // 2, 3 and 4 measured, 3 and 4 fastest), balanced by bytes; the sequential step, every program
   // after the previous on one stream (with --graphs: each a replayed HIP graph), is
   // timed beside it.
   const timeSteps = (issue) => {
@@ -376,7 +376,7 @@ function c2(runner, bench, opts) {
   for (const p of programs) if (bench.graphs) p.capture();
   const sequential = timeStepsChecked(() => { for (const p of programs) go(p); });
   // Profiling mode runs the sequential step only, so each kernel's traced duration is its own.
-  const S = Number(arg('c2-streams', 2));
+  const S = Number(arg('c2-streams', 3));
   const group = stepOnly ? null : new Concurrent(runner, programs, S);
   const headline = stepOnly ? sequential : timeStepsChecked(() => group.run());
   const ms = headline.msPerStep * K, wallMs = headline.wallMsPerStep * K;
