@@ -58,8 +58,10 @@ function prepared(runner, graph, lowered, inputs, opts) {
 /**
  * Time every dispatch of `program` alone, as the program issues it: µs per launch
  * (median, min and max of a few repetitions). A batched dispatch is timed whole and
- * its time shared evenly among its member launches (`batched`: the member count), so
- * a member costs what it costs inside its batch, not what it would cost by itself.
+ * its time shared among its member launches (`batched`: the member count) in
+ * proportion to their work (flops where every member has them, else algorithmic bytes:
+ * evenly among identical members; members whose bodies differ may differ in size), so a
+ * member costs what it costs inside its batch, not what it would cost by itself.
  */
 function timeLaunches(runner, bench, program, reps) {
   const out = [];
@@ -73,11 +75,15 @@ function timeLaunches(runner, bench, program, reps) {
     const one = runner.prepare(program.graph, lowered, { buffers: program.bufs });
     const r = bench.time({ one }, { reps: reps || 5, warmup: 1, targetMs: 0.5, direct: true });
     const n = members.length;
-    for (const l of members) {
+    const byFlops = members.every((l) => l.flops > 0);
+    const work = members.map((l) => (byFlops ? l.flops : l.bytes || 0));
+    const total = work.reduce((s, w) => s + w, 0);
+    members.forEach((l, k) => {
+      const share = total > 0 ? work[k] / total : 1 / n;
       out.push({ node: l.node, kind: l.kind, pattern: l.pattern || null, code: l.code, bytes: l.bytes, flops: l.flops,
-        us: r.stats.one.median / n, minUs: r.stats.one.min / n, maxUs: r.stats.one.max / n, rowFolds: l.rowFolds || null, absorbed: l.absorbed || null,
+        us: r.stats.one.median * share, minUs: r.stats.one.min * share, maxUs: r.stats.one.max * share, rowFolds: l.rowFolds || null, absorbed: l.absorbed || null,
         formed: l.formed || null, batched: n > 1 ? n : undefined, joint: b && b.joint ? true : undefined });
-    }
+    });
     one.destroy();
     i += n;
   }
