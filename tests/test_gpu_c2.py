@@ -2,8 +2,9 @@
 all eight programs at their full size [8192, 1024] and at a small row count. Every kept
 output of the fused and of the unfused launch list, each in the plain lowering and in
 the perf lowering the bench times, is within the float32 budget of the float64 oracle
-(streamed, node by node), canaries intact; the fraction of outputs where fused and
-unfused agree bit for bit is reported."""
+(streamed, node by node), canaries intact; each perf lowering's outputs equal its plain
+lowering's bit for bit; the fraction of outputs where fused and unfused agree bit for bit
+is reported."""
 import sys
 
 import numpy as np
@@ -29,6 +30,13 @@ def judge_bundle(b):
                 print(f"{c['name']} {key}: worst {jp['worst']:.3g}, {len(c[key + 'Kernels'])} kernels", file=sys.stderr)
                 assert jp["pass"], (c["name"], key, jp["first"], jp["unjudged"])
                 assert c[key + "Canary"], (c["name"], key, "canary")
+                # The perf lowering forms values inside their readers with the same ops in
+                # the same order, and batches launches whatever their bodies: the same bits
+                # as the plain lowering's launch per node.
+                plain = c["fused"] if key == "fusedPerf" else c["unfused"]
+                for k in c["keep"]:
+                    assert np.array_equal(b.arr(c[key][str(k)]).view(np.uint32), b.arr(plain[str(k)]).view(np.uint32)), \
+                        (c["name"], key, k, "perf lowering differs from the plain one")
         same = sum(int(np.sum(b.arr(c["fused"][str(k)]).view(np.uint32) == b.arr(c["unfused"][str(k)]).view(np.uint32)))
                    for k in c["keep"])
         total = sum(b.arr(c["fused"][str(k)]).size for k in c["keep"])
