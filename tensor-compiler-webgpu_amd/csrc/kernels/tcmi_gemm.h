@@ -487,17 +487,6 @@ __device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict_
   }
 }
 
-// The tile of each workgroup at its launch place (blockIdx.x, blockIdx.y).
-template <int TM, int TN, int BK, int PF, int AMODE, int BMODE, bool SPLIT, class AV, class BV, class Epi, int WN = 2,
-          bool PRIO = false, int KW = 1, class Args = TcmiArgs>
-__device__ __forceinline__ void gemm_f32(const Args& A, const float* __restrict__ a_ptr,
-                                         const float* __restrict__ b_ptr, const uint32_t batch, const uint32_t M,
-                                         const uint32_t K, const uint32_t N, const uint32_t chunks,
-                                         const uint32_t chunkK, const uint32_t zid) {
-  gemm_f32<TM, TN, BK, PF, AMODE, BMODE, SPLIT, AV, BV, Epi, WN, PRIO, KW, Args>(A, a_ptr, b_ptr, batch, M, K, N, chunks,
-                                                                               chunkK, zid, blockIdx.x, blockIdx.y);
-}
-
 // Output element j of a split-K matmul's product: its chunks' partial sums from the
 // workspace, added in chunk order — the value gemm_splitk_reduce forms for j itself.
 // An epilogue that reads the product at another element's index (a recomputed

@@ -59,9 +59,10 @@ function prepared(runner, graph, lowered, inputs, opts) {
  * Time every dispatch of `program` alone, as the program issues it: µs per launch
  * (median, min and max of a few repetitions). A batched dispatch is timed whole and
  * its time shared among its member launches (`batched`: the member count) in
- * proportion to their work (flops where every member has them, else algorithmic bytes:
- * evenly among identical members; members whose bodies differ may differ in size), so a
- * member costs what it costs inside its batch, not what it would cost by itself.
+ * proportion to their work (flops where every member has them, algorithmic bytes where
+ * none has: evenly among identical members; members whose bodies differ may differ in
+ * size), or evenly where products and other kernels share a ragged batch, so a member
+ * costs what it costs inside its batch, not what it would cost by itself.
  */
 function timeLaunches(runner, bench, program, reps) {
   const out = [];
@@ -75,8 +76,8 @@ function timeLaunches(runner, bench, program, reps) {
     const one = runner.prepare(program.graph, lowered, { buffers: program.bufs });
     const r = bench.time({ one }, { reps: reps || 5, warmup: 1, targetMs: 0.5, direct: true });
     const n = members.length;
-    const byFlops = members.every((l) => l.flops > 0);
-    const work = members.map((l) => (byFlops ? l.flops : l.bytes || 0));
+    const byFlops = members.every((l) => l.flops > 0), byBytes = members.every((l) => !(l.flops > 0));
+    const work = members.map((l) => (byFlops ? l.flops : byBytes ? l.bytes || 0 : 1));
     const total = work.reduce((s, w) => s + w, 0);
     members.forEach((l, k) => {
       const share = total > 0 ? work[k] / total : 1 / n;
@@ -449,7 +450,8 @@ function launchRecords(lowered) {
     kernels: l.kernels.map((k) => k.name), bytes: l.bytes, flops: l.flops || 0 }));
   for (const b of lowered.batches || []) {
     const ms = lowered.launches.slice(b.start, b.start + b.count);
-    recs.push({ node: ms[0].node, kind: `batched ${ms[0].kind} x${b.count}`, pattern: ms[0].pattern || null, kernels: b.kernels.map((k) => k.name),
+    const kind = b.ragged ? `ragged x${b.count} (${Array.from(new Set(ms.map((l) => l.kind))).join(', ')})` : `batched ${ms[0].kind} x${b.count}`;
+    recs.push({ node: ms[0].node, kind, pattern: ms[0].pattern || null, kernels: b.kernels.map((k) => k.name),
       bytes: ms.reduce((q, l) => q + l.bytes, 0), flops: ms.reduce((q, l) => q + (l.flops || 0), 0), members: ms.map((l) => l.node) });
   }
   return recs;

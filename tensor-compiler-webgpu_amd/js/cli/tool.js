@@ -327,9 +327,10 @@ function gemmModes(l) {
 
 /** The K split (chunks, chunk length) of a matmul launch's kernel, or null. */
 function gemmSplit(l) {
-  // gemm_f32<...>(A, a, b, batch, M, K, N, chunks, chunkK, zid[, tx, ty]): zid is
-  // blockIdx.z, or wg.z (with wg.x, wg.y) where the tiles take XCD-grouped places.
-  const m = l.kernels[0].source.match(/(\d+)u, (\d+)u, (?:blockIdx\.z|wg\.z, wg\.x, wg\.y)\);/);
+  // gemm_f32<...>(A, a, b, batch, M, K, N, chunks, chunkK, zid, tx, ty): the place is
+  // (blockIdx.z, blockIdx.x, blockIdx.y), or (wg.z, wg.x, wg.y) where the tiles take
+  // XCD-grouped places.
+  const m = l.kernels[0].source.match(/(\d+)u, (\d+)u, (?:blockIdx\.z, blockIdx\.x, blockIdx\.y|wg\.z, wg\.x, wg\.y)\);/);
   return l.flops && m ? [Number(m[1]), Number(m[2])] : null;
 }
 
@@ -1381,6 +1382,36 @@ async function main() {
         kernels.push({ name: k.name, z: l.kernels[0].grid[2], source: src.get(k.name) });
       }
       out = { batches, kernels };
+      break;
+    }
+    case 'ragged-batches': {
+      // The ragged batches of model steps and corpus programs (perf lowering): each batched
+      // kernel's text, grid and workgroup size, and its members' kernel grids in order.
+      const { modelStep } = require('../src/builders/models');
+      const { fusedStep } = require('../src/mi355x/trainer');
+      const lowerings = [];
+      for (const r of req.models || []) {
+        const fs = fusedStep(modelStep(r).step, { attention: !!r.attention });
+        lowerings.push([`${r.model}-${r.B || ''}`, fs.lowered]);
+      }
+      if (req.corpus) {
+        const { corpusGraphs } = require('../src/testing/random_graph');
+        for (let i = req.corpus.from; i <= req.corpus.to; i++) {
+          for (const c of corpusGraphs(i)) {
+            const f = fuse(c.graph, { keep: c.keep });
+            lowerings.push([`corpus-${i}-${c.label}`, lowerMI355X(f.graph, { perf: true, keep: c.keep.map((id) => f.index.get(id)), absorb: true })]);
+          }
+        }
+      }
+      out = [];
+      for (const [name, lo] of lowerings) {
+        for (const b of lo.batches || []) {
+          if (!b.ragged) continue;
+          const k = b.kernels[0];
+          out.push({ name, kernel: k.name, source: k.source, grid: k.grid, block: k.block,
+            members: lo.launches.slice(b.start, b.start + b.count).map((l) => ({ kernel: l.kernels[0].name, grid: l.kernels[0].grid, block: l.kernels[0].block })) });
+        }
+      }
       break;
     }
     case 'batch-check': {

@@ -967,7 +967,9 @@ ${indent(lines, '    ')}
   // A launch split along K places the tiles of each chunk on one XCD (tcmi::xcd_grouped),
   // so they share its L2 for the A and B panels they all read.
   const grouped = tl.chunks > 1;
-  const place = grouped ? ', wg.z, wg.x, wg.y' : ', blockIdx.z';
+  // The tile's place passed explicitly: a ragged batch runs this text with blockIdx
+  // standing for the member's own place (raggedKernel).
+  const place = grouped ? ', wg.z, wg.x, wg.y' : ', blockIdx.z, blockIdx.x, blockIdx.y';
   const main = `extern "C" __global__ void __launch_bounds__(${threads}) __KERNEL__(const TcmiArgs A) {
 ${grouped ? `  ${XCD_GROUPED}
 ` : ''}  tcmi::gemm_f32<${tl.tm}, ${tl.tn}, ${tl.bk}, ${tl.pf}, ${av.mode}, ${bv.mode}, ${split}, __KERNEL___av, __KERNEL___bv, __KERNEL___epi${variant}>(A, A.in[${ia}], A.in[${ib}],
@@ -1585,6 +1587,105 @@ function batchedKernel(members, count) {
     members: count, variants: variants.length > 1 ? variantOf.map((v) => variants[v].name) : undefined };
 }
 
+// ---- ragged batches -----------------------------------------------------------------
+
+// Members of a ragged batch: kernels of at most this many workgroups each (launches that
+// fill less than two workgroups per CU, whose cost is mostly the dispatch), and at most
+// this many bytes of static LDS over all members.
+const RAGGED_MAX_BLOCKS = 512;
+const RAGGED_MAX_LDS = 65536;
+const LDS_TYPE_BYTES = { float: 4, 'tcmi::f4': 16 };
+
+/** Bytes of the static LDS arrays a kernel text declares itself, or null if not known. */
+function textLds(source) {
+  let bytes = 0;
+  const re = /__shared__\s+(?:__attribute__\(\(aligned\(\d+\)\)\)\s+)?([\w:]+)\s+\w+((?:\[\d+\])+);/g;
+  const all = (source.match(/__shared__/g) || []).length;
+  let found = 0;
+  for (let m = re.exec(source); m; m = re.exec(source)) {
+    if (!LDS_TYPE_BYTES[m[1]]) return null;
+    bytes += LDS_TYPE_BYTES[m[1]] * m[2].slice(1, -1).split('][').reduce((q, d) => q * Number(d), 1);
+    found++;
+  }
+  return found === all ? bytes : null;
+}
+
+/**
+ * Whether kernel `k` may join a ragged batch: a one-kernel launch's kernel of the
+ * batchable kinds (no split-K second pass), with no dynamic LDS, static LDS of a known
+ * size, workgroups placed by blockIdx (not XCD-grouped), one entry point, and at most
+ * RAGGED_MAX_BLOCKS workgroups.
+ */
+function raggable(k) {
+  const m = k.name.match(BATCHABLE);
+  if (!m || m[3] || k.needsPad || k.lds || k.ldsStatic || k.joint) return false;
+  if (k.block[1] !== 1 || k.block[2] !== 1 || k.grid[0] * k.grid[1] * k.grid[2] > RAGGED_MAX_BLOCKS) return false;
+  if (k.source.includes(XCD_GROUPED) || textLds(k.source) === null) return false;
+  return k.source.split(`${k.name}(const TcmiArgs A) {`).length === 2;
+}
+
+/** Whether kernels `ks` may share one ragged batch: one workgroup size, LDS within bounds. */
+function raggedFits(ks) {
+  if (!(ks.length >= 1 && ks.length <= MAX_BATCH) || !ks.every(raggable)) return false;
+  if (!ks.every((k) => k.block[0] === ks[0].block[0])) return false;
+  // Matmul tiles share one pool per size (tcmi::lds_pool); each member's own arrays add up.
+  const pools = new Set(ks.filter((k) => k.pool !== undefined).map((k) => k.pool));
+  const lds = Array.from(pools).reduce((q, f) => q + 4 * f, 0) + ks.reduce((q, k) => q + textLds(k.source), 0);
+  return lds <= RAGGED_MAX_LDS;
+}
+
+/**
+ * A ragged batch: independent launches of small kernels whose grids differ (a product's
+ * tile grid, a row reduction's, an elementwise chain's) in one dispatch of their summed
+ * workgroups along x. Workgroup L runs member m, the one whose range [start_m, start_m +
+ * |grid_m|) holds L, uniformly per workgroup: its own body, with `A` bound to member m's
+ * argument block and the names blockIdx and gridDim shadowed in its scope by its own
+ * place (l % gx, (l / gx) % gy, l / (gx·gy)), l = L − start_m, and its own grid, so the
+ * body runs as it does in its own launch (kernel texts read their places and grids
+ * only through those names: a matmul passes its place to tcmi_gemm.h). One workgroup
+ * size for all; their static LDS adds up (raggedFits).
+ */
+function raggedKernel(ks) {
+  if (!(ks.length >= 2 && raggedFits(ks))) throw new Error(`kernels ${ks.map((k) => k.name).join(', ')} cannot share a ragged batch`);
+  const variants = [];
+  const variantOf = ks.map((k) => {
+    let v = variants.findIndex((x) => x.name === k.name);
+    if (v < 0) { v = variants.length; variants.push(k); }
+    return v;
+  });
+  const parts = variants.map((k) => {
+    const [head, body] = k.source.split(`${k.name}(const TcmiArgs A) {`);
+    return { k, head: head.slice(0, head.lastIndexOf('extern "C"')), body };
+  });
+  const includes = Array.from(new Set([].concat(...parts.map((p) => p.head.split('\n').filter((l) => l.startsWith('#include'))))));
+  // Each variant's structs renamed for the batched kernel (v0_, v1_, ...).
+  const own = (t, v) => t.split(`${parts[v].k.name}_`).join(`__KERNEL___v${v}_`);
+  const structs = parts.map((p, v) => own(p.head.split('\n').filter((l) => !l.startsWith('#include')).join('\n'), v));
+  let at = 0;
+  const branches = ks.map((k, m) => {
+    const [gx, gy, gz] = k.grid, count = gx * gy * gz, v = variantOf[m];
+    const stmts = own(parts[v].body, v).replace(/\}\s*$/, '').split('\n').map((l) => (l ? `  ${l}` : l)).join('\n').replace(/\s+$/, '');
+    const text = `  ${m ? '} else ' : ''}if (tcmi_wg_ < ${at + count}u) {   // member ${m}: workgroups [${at}, ${at + count}), its grid ${gx} x ${gy} x ${gz}
+    const uint32_t tcmi_l_ = tcmi_wg_ - ${at}u;
+    const TcmiPtrs& A = B.m[${m}];
+    const uint3 gridDim = make_uint3(${gx}u, ${gy}u, ${gz}u);
+    const uint3 blockIdx = make_uint3(tcmi_l_ % ${gx}u, (tcmi_l_ / ${gx}u) % ${gy}u, tcmi_l_ / ${gx * gy}u);
+${stmts}`;
+    at += count;
+    return text;
+  });
+  const threads = ks[0].block[0];
+  const text = `${includes.join('\n')}${includes.length ? '\n' : ''}${structs.join('')}extern "C" __global__ void __launch_bounds__(${threads}) __KERNEL__(const TcmiBatch<${ks.length}> B) {
+  const uint32_t tcmi_wg_ = blockIdx.x;
+${branches.join('\n')}
+  }
+}
+`;
+  const b = kernelText('rb', text);
+  return { name: b.name, source: b.source, grid: [at, 1, 1], block: [threads, 1, 1], lds: 0, members: ks.length, ragged: ks.map((k) => k.name) };
+}
+
 module.exports = { elementwiseKernel, rowwiseKernel, colreduceKernels, gemmKernel, gemmTiling, attentionKernel, attentionGradKernel,
   gradPart, GRAD_PARTS, classifyGather, gatherStrides,
-  literal, fnv, Emitter, ParamOverflow, WG, MAX_P, MAX_IN, MAX_BATCH, batchable, batchedKernel, batchFamily };
+  literal, fnv, Emitter, ParamOverflow, WG, MAX_P, MAX_IN, MAX_BATCH, batchable, batchedKernel, batchFamily,
+  raggable, raggedFits, raggedKernel, textLds, RAGGED_MAX_BLOCKS, RAGGED_MAX_LDS };

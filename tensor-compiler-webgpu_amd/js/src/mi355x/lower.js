@@ -1280,63 +1280,77 @@ function batchPlan(launches, aliases) {
     for (const j of group) placed[j] = 1;
     units.push(group.map((j) => launches[j]));
   }
-  // Pass 2: group the launches still alone by their windows.
-  for (let changed = true; changed;) {
-    changed = false;
-    const unitOf = new Map();   // buffer owner -> index of the unit writing it
-    units.forEach((u, x) => { for (const l of u) unitOf.set(owner(l.node), x); });
-    const lo = [], hi = [];     // window: after unit lo, before unit hi
-    units.forEach((u) => { lo.push(-1); hi.push(units.length); });
-    units.forEach((u, x) => {
-      for (const l of u) {
-        for (const id of l.inputs) {
-          const w = unitOf.get(owner(id));
-          if (w === undefined) continue;
-          lo[x] = Math.max(lo[x], w);
-          hi[w] = Math.min(hi[w], x);
-        }
-      }
-    });
-    const byKey = new Map();
-    units.forEach((u, x) => {
-      const k = u.length === 1 ? one(u[0]) : null;
-      if (k) { if (!byKey.has(k)) byKey.set(k, []); byKey.get(k).push(x); }
-    });
-    for (const xs of byKey.values()) {
-      if (xs.length < 2) continue;
-      // A lone launch may follow any unit from lo (its operands' last writer) up to,
-      // not including, hi (its output's first reader); grow a group from the
-      // earliest-opening window while the windows still share an anchor.
-      const cand = xs.slice().sort((a, b) => lo[a] - lo[b] || a - b);
-      const group = [cand[0]];
-      let from = lo[cand[0]], to = hi[cand[0]];
-      const reads = (x, y) => units[y][0].inputs.some((id) => unitOf.get(owner(id)) === x);
-      for (const x of cand.slice(1)) {
-        if (group.length >= cg.MAX_BATCH) break;
-        // Anchors a (insert after unit a) with lo <= a < hi, for every member.
-        const f = Math.max(from, lo[x]), t = Math.min(to, hi[x]);
-        if (f >= t) continue;
-        if (group.some((g) => reads(g, x) || reads(x, g))) continue;
-        group.push(x);
-        from = f; to = t;
-      }
-      while (group.length > 1 && !fits(units[group[0]][0], group.length)) group.pop();
-      if (group.length < 2) continue;
-      // Place the group right after unit `from` (the latest writer of any member's
-      // operand): every member's readers come after it, at `to` or later.
-      const members = group.slice().sort((a, b) => a - b).map((x) => units[x][0]);
-      const inGroup = new Set(group);
-      const next = [];
-      if (from < 0) next.push(members);
+  // Passes 2 and 3: group the launches still alone by their windows, those of one key
+  // (keyOf: null for a launch that may not join) while `admits` takes the group so far
+  // and a new member; `mark` tags each new unit.
+  const byWindows = (keyOf, admits, mark, everyStart) => {
+    for (let changed = true; changed;) {
+      changed = false;
+      const unitOf = new Map();   // buffer owner -> index of the unit writing it
+      units.forEach((u, x) => { for (const l of u) unitOf.set(owner(l.node), x); });
+      const lo = [], hi = [];     // window: after unit lo, before unit hi
+      units.forEach((u) => { lo.push(-1); hi.push(units.length); });
       units.forEach((u, x) => {
-        if (!inGroup.has(x)) next.push(u);
-        if (x === from) next.push(members);
+        for (const l of u) {
+          for (const id of l.inputs) {
+            const w = unitOf.get(owner(id));
+            if (w === undefined) continue;
+            lo[x] = Math.max(lo[x], w);
+            hi[w] = Math.min(hi[w], x);
+          }
+        }
       });
-      units = next;
-      changed = true;
-      break;
+      const byKey = new Map();
+      units.forEach((u, x) => {
+        const k = u.length === 1 ? keyOf(u[0]) : null;
+        if (k) { if (!byKey.has(k)) byKey.set(k, []); byKey.get(k).push(x); }
+      });
+      const reads = (x, y) => units[y][0].inputs.some((id) => unitOf.get(owner(id)) === x);
+      for (const xs of byKey.values()) {
+        if (xs.length < 2) continue;
+        // A lone launch may follow any unit from lo (its operands' last writer) up to,
+        // not including, hi (its output's first reader); grow a group from the
+        // earliest-opening window (with `everyStart`, from each in turn until a group
+        // forms) while the windows still share an anchor.
+        const cand = xs.slice().sort((a, b) => lo[a] - lo[b] || a - b);
+        for (let s0 = 0; s0 < (everyStart ? cand.length - 1 : 1) && !changed; s0++) {
+          const group = [cand[s0]];
+          let from = lo[cand[s0]], to = hi[cand[s0]];
+          for (const x of cand.slice(s0 + 1)) {
+            if (group.length >= cg.MAX_BATCH) break;
+            // Anchors a (insert after unit a) with lo <= a < hi, for every member.
+            const f = Math.max(from, lo[x]), t = Math.min(to, hi[x]);
+            if (f >= t) continue;
+            if (group.some((g) => reads(g, x) || reads(x, g))) continue;
+            if (!admits(group.map((g) => units[g][0]), units[x][0])) continue;
+            group.push(x);
+            from = f; to = t;
+          }
+          while (group.length > 1 && !fits(units[group[0]][0], group.length)) group.pop();
+          if (group.length < 2) continue;
+          // Place the group right after unit `from` (the latest writer of any member's
+          // operand): every member's readers come after it, at `to` or later.
+          const members = group.slice().sort((a, b) => a - b).map((x) => units[x][0]);
+          if (mark) mark(members);
+          const inGroup = new Set(group);
+          const next = [];
+          if (from < 0) next.push(members);
+          units.forEach((u, x) => {
+            if (!inGroup.has(x)) next.push(u);
+            if (x === from) next.push(members);
+          });
+          units = next;
+          changed = true;
+        }
+        if (changed) break;
+      }
     }
-  }
+  };
+  byWindows(one, () => true, null, false);
+  // Pass 3 (ragged batches): single-kernel launches of any kernels that may share a
+  // dispatch whose members' grids differ (codegen.js raggedKernel) and still stand alone.
+  const raggedKey = (l) => (l.kernels.length === 1 && !l.workspace && cg.raggable(l.kernels[0]) ? `ragged@${l.kernels[0].block[0]}` : null);
+  byWindows(raggedKey, (group, l) => cg.raggedFits(group.concat([l]).map((m) => m.kernels[0])), (members) => { members.ragged = true; }, true);
   const order = [], batches = [];
   for (const u of units) {
     if (u.joint) {
@@ -1346,7 +1360,9 @@ function batchPlan(launches, aliases) {
       order.push(...u);
       continue;
     }
-    if (u.length > 1) {
+    if (u.length > 1 && u.ragged) {
+      batches.push({ start: order.length, count: u.length, kernels: [cg.raggedKernel(u.map((m) => m.kernels[0]))], wsStride: 0, ragged: true });
+    } else if (u.length > 1) {
       const l = u[0];
       batches.push({ start: order.length, count: u.length, kernels: l.kernels.map((k, j) => cg.batchedKernel(u.map((m) => m.kernels[j]), u.length)),
         wsStride: l.workspace ? Math.ceil(l.workspace / 256) * 256 : 0 });

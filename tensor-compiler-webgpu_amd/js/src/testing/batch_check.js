@@ -6,6 +6,8 @@
 // (or of matmul, elementwise or rowwise texts that differ, each member then run by its own case
 // of the batched kernel, which holds exactly its own body) over the same grids (a column
 // sum's text leaves its outer extent to the grid) with no data path between them, or
+// one-kernel launches over grids that differ, each run by its own branch of a ragged
+// batched kernel over its own range of the dispatch's workgroups, or
 // the three parts of one attention gradient in one launch of their joint kernel; each
 // batched kernel's grid must repeat the
 // member kernel's grid once per member along z, and the members' workspace
@@ -44,6 +46,40 @@ function runsOwnBody(bk, k, x) {
   return norm(kase, m ? m[1] : null) === norm(own, x.name);
 }
 
+// Whether ragged batched kernel `bk` runs, for member k (workgroups [at, at + |grid|) of
+// the dispatch), kernel `x` as its own launch would: the branch of k opens with exactly
+// the range test, the member's argument block, and its own grid and place standing for
+// gridDim and blockIdx (the decomposition of the workgroup's offset l in its range as
+// (l % gx, (l / gx) % gy, l / (gx·gy))), then holds x's own statements, over structs
+// declared as x declares its own.
+function runsOwnRaggedBody(bk, k, x, at) {
+  const [gx, gy, gz] = x.grid, count = gx * gy * gz;
+  const marker = `if (tcmi_wg_ < ${at + count}u) {   // member ${k}: workgroups [${at}, ${at + count}), its grid ${gx} x ${gy} x ${gz}\n`;
+  const start = bk.source.indexOf(marker);
+  if (start < 0) return false;
+  const rest = bk.source.slice(start + marker.length);
+  const next = rest.search(/\n {2}\} else if \(tcmi_wg_ < |\n {2}\}\n\}\n$/);
+  if (next < 0) return false;
+  const branch = rest.slice(0, next);
+  const head = [
+    `const uint32_t tcmi_l_ = tcmi_wg_ - ${at}u;`,
+    `const TcmiPtrs& A = B.m[${k}];`,
+    `const uint3 gridDim = make_uint3(${gx}u, ${gy}u, ${gz}u);`,
+    `const uint3 blockIdx = make_uint3(tcmi_l_ % ${gx}u, (tcmi_l_ / ${gx}u) % ${gy}u, tcmi_l_ / ${gx * gy}u);`,
+  ];
+  const lines = branch.split('\n');
+  if (lines.length < head.length || head.some((h, i) => lines[i].trim() !== h)) return false;
+  const body = lines.slice(head.length).join('\n');
+  const m = body.match(new RegExp(`(${bk.name}_v\\d+)_`));
+  const structs = (src, prefix) => (src.match(new RegExp(`struct ${prefix}_\\w+ \\{[\\s\\S]*?\\n\\};\\n`, 'g')) || [])
+    .map((t) => t.split(prefix).join('@')).join('');
+  if (m ? structs(bk.source, m[1]) !== structs(x.source, x.name) : structs(x.source, x.name) !== '') return false;
+  const sig = `${x.name}(const TcmiArgs A) {`;
+  const own = x.source.slice(x.source.indexOf(sig) + sig.length).replace(/\}\s*$/, '');
+  const norm = (t, prefix) => (prefix ? t.split(`${prefix}_`).join('@_') : t).replace(/\s+/g, '');
+  return norm(body, m ? m[1] : null) === norm(own, x.name);
+}
+
 function checkBatches(plain, batched) {
   const alias = new Map(batched.aliases || []);
   const owner = (id) => (alias.has(id) ? alias.get(id) : id);
@@ -69,6 +105,25 @@ function checkBatches(plain, batched) {
           && l.kernels[0].part === j.parts[k] && l.inputs.join() === first.inputs.join() && !l.workspace);
       if (!ok) return { ok: false, why: `batch at ${b.start}: not the three parts of one attention gradient` };
       for (let k = 0; k < b.count; k++) unitOf[b.start + k] = b.start;
+      continue;
+    }
+    if (b.ragged) {
+      // Members of any one-kernel launches, each over its own grid, in consecutive ranges of
+      // one dispatch's workgroups.
+      const ms = L.slice(b.start, b.start + b.count);
+      if (b.kernels.length !== 1 || b.wsStride || ms.some((l) => l.kernels.length !== 1 || l.workspace)) {
+        return { ok: false, why: `batch at ${b.start}: a ragged batch of launches that are not one kernel each, or use the workspace` };
+      }
+      let at = 0;
+      for (let k = 0; k < b.count; k++) {
+        const x = ms[k].kernels[0];
+        if (x.block.join() !== b.kernels[0].block.join() || x.lds || !runsOwnRaggedBody(b.kernels[0], k, x, at)) {
+          return { ok: false, why: `batch at ${b.start}: member ${k} is not its own kernel over its own workgroups` };
+        }
+        at += x.grid[0] * x.grid[1] * x.grid[2];
+        unitOf[b.start + k] = b.start;
+      }
+      if (b.kernels[0].grid.join() !== [at, 1, 1].join()) return { ok: false, why: `batch at ${b.start}: grid ${b.kernels[0].grid} for ${at} workgroups` };
       continue;
     }
     if (b.kernels.length !== first.kernels.length) return { ok: false, why: `batch at ${b.start}: ${b.kernels.length} batched kernels for ${first.kernels.length}` };
@@ -119,9 +174,9 @@ function checkBatches(plain, batched) {
  */
 function plantBatchMistake(lowered, kind) {
   if (kind === 'body') {
-    const b = (lowered.batches || []).find((x) => x.kernels.length === 1 && x.kernels[0].variants);
+    const b = (lowered.batches || []).find((x) => x.kernels.length === 1 && (x.kernels[0].variants || x.kernels[0].ragged));
     if (!b) return null;
-    const v = b.kernels[0].variants;
+    const v = b.kernels[0].variants || b.kernels[0].ragged;
     const k = v.findIndex((name) => name !== v[0]);
     const launches = lowered.launches.slice();
     [launches[b.start], launches[b.start + k]] = [launches[b.start + k], launches[b.start]];
