@@ -61,23 +61,25 @@ function prepared(runner, graph, lowered, inputs, opts) {
  * its time shared among its member launches (`batched`: the member count) in
  * proportion to their work (flops where every member has them, algorithmic bytes where
  * none has: evenly among identical members; members whose bodies differ may differ in
- * size), or evenly where products and other kernels share a ragged batch, so a member
- * costs what it costs inside its batch, not what it would cost by itself.
+ * size), so a member costs what it costs inside its batch, not what it would cost by
+ * itself. A ragged batch's members are timed each alone.
  */
 function timeLaunches(runner, bench, program, reps) {
   const out = [];
   const L = program.lowered;
   const batchAt = new Map((L.batches || []).map((b) => [b.start, b]));
   for (let i = 0; i < L.launches.length;) {
-    const b = batchAt.get(i);
+    // A ragged batch's members (small kernels of different kinds and grids) are timed
+    // each alone: no share of their dispatch would stand for one of them.
+    const b = batchAt.get(i) && !batchAt.get(i).ragged ? batchAt.get(i) : null;
     const members = L.launches.slice(i, i + (b ? b.count : 1));
     const lowered = { launches: members, workspace: L.workspace };
     if (b) lowered.batches = [Object.assign({}, b, { start: 0 })];
     const one = runner.prepare(program.graph, lowered, { buffers: program.bufs });
     const r = bench.time({ one }, { reps: reps || 5, warmup: 1, targetMs: 0.5, direct: true });
     const n = members.length;
-    const byFlops = members.every((l) => l.flops > 0), byBytes = members.every((l) => !(l.flops > 0));
-    const work = members.map((l) => (byFlops ? l.flops : byBytes ? l.bytes || 0 : 1));
+    const byFlops = members.every((l) => l.flops > 0);
+    const work = members.map((l) => (byFlops ? l.flops : l.bytes || 0));
     const total = work.reduce((s, w) => s + w, 0);
     members.forEach((l, k) => {
       const share = total > 0 ? work[k] / total : 1 / n;
