@@ -77,6 +77,31 @@ def test_node_addon_loads_and_exports():
     assert p.returncode == 0, p.stdout + p.stderr
 
 
+def test_backend_entry_point_exports_what_the_reference_binds():
+    """js/src/mi355x/index.js, the module a reference harness requires in place of
+    src/gpu/runtime.js, lower-fused.js, trainer-fused.js and bench.js: every name the
+    integration binds is there, and what it gives is the backend's own (its lowering of
+    the reference transformer's fused training step holds the same launches as the
+    trainer's, and a launch list the batch checker accepts)."""
+    js = ("const be=require(process.argv[1]);"
+          "const want=['lowerMI355X','kernelSources','HipRunner','Program','precompile','fusedStep','fusedForward','HipTrainer',"
+          "'HipBench','summarize','verdict','fuseAttention','planArena'];"
+          "const miss=want.filter((k)=>typeof be[k]!=='function'); if(miss.length){console.log(miss.join());process.exit(2);}"
+          "const {modelStep}=require(process.argv[2]);const m=modelStep({model:'transformer-ref'});"
+          "const fs=be.fusedStep(m.step);"
+          "const keep=[fs.loss,fs.logits].concat(Object.values(fs.outputs));"
+          "const lo=be.lowerMI355X(fs.graph,{perf:true,keep,absorb:true});"
+          "if(lo.launches.map((l)=>l.node).join()!==fs.lowered.launches.map((l)=>l.node).join())process.exit(3);"
+          "const {checkBatches}=require(process.argv[3]);"
+          "const c=checkBatches(be.lowerMI355X(fs.graph,{perf:true,keep,absorb:true,batch:false}),lo);"
+          "if(!c.ok){console.log(c.why);process.exit(4);}"
+          "if(be.kernelSources(lo).size<10)process.exit(5);")
+    src = PKG / "js" / "src"
+    p = subprocess.run(["node", "-e", js, str(src / "mi355x" / "index.js"), str(src / "builders" / "models.js"),
+                        str(src / "testing" / "batch_check.js")], capture_output=True, text=True)
+    assert p.returncode == 0, (p.returncode, p.stdout + p.stderr)
+
+
 def test_kernel_headers_compile_for_gfx950_offline(tool):
     """The skeletons compile with hiprtc for gfx950 (no GPU): every direct case's kernels as one module."""
     out = tool("precompile", {"group": "direct", "arch": "gfx950"})
