@@ -1,12 +1,15 @@
 """Batched launches of the perf lowering (js/src/mi355x/lower.js batchPlan), checked on the
 CPU by js/src/testing/batch_check.js from the launch records alone: the batched list holds
 the plain list's launches, every launch reads only buffers written before it, a batch's
-members are launches of one kernel text (or of matmul or elementwise texts of one grid,
-each member then run by its own case of the batched kernel) with no data path between them, the batched grid
-has one z-slice per member, and launches that share the workspace keep their order. Planted
+members are launches of one kernel text (or of matmul, elementwise or rowwise texts of one
+grid, each member then run by its own case of the batched kernel) with no data path
+between them, the batched grid has one z-slice per member, and launches that share the
+workspace keep their order. A ragged batch's members (small kernels whose grids differ)
+each run their own branch over their own range of the dispatch's workgroups. Planted
 mistakes (a batch whose second member reads the first's output; a launch moved in front of
-its operand's writer; a member over another grid; members' bodies exchanged) must be refused. The GPU side — batched runs bit for bit the
-plain ones — is in test_gpu_train.py (config 5's step) and test_gpu_fuzz.py (corpus programs)."""
+its operand's writer; a member over another grid; members' bodies exchanged) must be
+refused. The GPU side, batched runs bit for bit the plain ones, is in test_gpu_train.py
+(configs 1 and 5's steps) and test_gpu_fuzz.py (corpus programs)."""
 
 MODELS = [{"model": "transformer", "B": 64}, {"model": "transformer", "B": 1}, {"model": "mlp"},
           {"model": "transformer-ref"}, {"model": "transformer", "B": 64, "attention": True},
