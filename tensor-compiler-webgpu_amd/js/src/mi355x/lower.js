@@ -1207,9 +1207,9 @@ function lowerOnce(graph, opts, noAbsorb, noForm) {
 }
 
 /**
- * Batched launches (perf lowering): launches of one kernel text over the same
- * grids with no data path between them run as one dispatch per kernel of the
- * kernels' batched forms (codegen.js batchedKernel). Two passes over the list:
+ * Batched launches (perf lowering): launches of one kernel family (codegen.js
+ * batchFamily) over the same grids with no data path between them run as one dispatch per kernel of the
+ * kernels' batched forms (codegen.js batchedKernel). Three passes over the list:
  *   1. walking it in order, a batchable launch opens a batch, and every later
  *      launch of the same kernels whose operands are all written by launches
  *      already placed joins it (up to MAX_BATCH); the members are placed
@@ -1219,14 +1219,18 @@ function lowerOnce(graph, opts, noAbsorb, noForm) {
  *      operands and before the first launch reading its output, so launches
  *      whose windows share a point (and none of which reads another's output)
  *      are moved together to the first such point (the bias gradients of every
- *      layer, read only by the parameter updates at the end of a step).
+ *      layer, read only by the parameter updates at the end of a step);
+ *   3. one-kernel launches of small kernels still alone, whatever their kernels and
+ *      grids, are grouped the same way (each window tried in turn as a group's
+ *      first) into ragged batches (codegen.js raggedKernel): one dispatch of their
+ *      summed workgroups, each member over its own range of them.
  * Every launch thus stays after its operands' writers and before its output's
  * readers, so it reads exactly the values it read in graph order, and writes its
  * own node's buffer (a batch's members each their own workspace slice). A batch
  * runs its launches' kernels over all members in turn (all first kernels, then
  * all second kernels), member k with the workspace slice
  * [k·wsStride, (k + 1)·wsStride). Returns { launches (the new order), batches:
- * [{ start, count, kernels, wsStride }] } with each batch's members at
+ * [{ start, count, kernels, wsStride, ragged?, joint? }] } with each batch's members at
  * launches[start .. start + count).
  */
 function batchPlan(launches, aliases) {
