@@ -602,7 +602,7 @@ ${indent(store, '    ')}
 /** Elements up to which a column reduction runs in one launch (256 KB of fp32). */
 const COLRED_ONE_PASS = 1 << 16;
 
-function colreduceKernels(op, outer, n, inner, tuning, producer) {
+function colreduceKernels(op, outer, n, inner, tuning, producer, chain) {
   const tune = tuning || {};
   const isMax = op === 'max';
   const init = isMax ? '(-TCMI_INF)' : '0.f';
@@ -658,6 +658,36 @@ function colreduceKernels(op, outer, n, inner, tuning, producer) {
     formed = [`      const uint32_t g0 = (o * n + k) * inner + j;`, ...lines.map((x) => `      ${x}`),
       `      const ${T} v = ${vec ? `tcmi::f4{${outs.join(', ')}}` : outs[0]};`].join('\n');
   }
+  // A chain applied to each sum before the store (`chain`: { body, output, sumAt }, the
+  // body of the sum's one reader, its inputs at the positions sumAt reading the sum and
+  // every other input loaded at the output's flat index): the launch is that reader's, its
+  // operands the chain's own with the sum's operand at sumAt[0].
+  const xin = chain ? chain.sumAt[0] : 0;
+  if (chain && producer) throw new Error('a column sum folded into its reader forms no producer');
+  // Each lane's chain in a scope of its own (an emitter per lane: the sum it reads is
+  // that lane's); the lowering folds only chains of elementwise ops of one size, which
+  // read every operand, the sum included, at the element they store.
+  const store = (idx, v) => {
+    if (!chain) return st('A.out', idx, v);
+    const parts = [];
+    for (let l = 0; l < W; l++) {
+      const lines = [];
+      const at = l ? `(${idx} + ${l}u)` : `(${idx})`;
+      const em = new Emitter(chain.body, pparams, {
+        load(k, ctx, ls) {
+          if (ctx.idx !== at) throw new Error('a column sum folded into its reader: an operand read at another element');
+          if (chain.sumAt.includes(k)) return vec ? `${v}[${l}]` : v;
+          const x = `C${ls.length}_${k}`;
+          ls.push(`const float ${x} = A.in[${k}][${ctx.idx}];`);
+          return x;
+        },
+      });
+      const out = em.value(chain.output, { key: `c${l}`, idx: at, root: true, lane: l, limit: outer * inner }, lines);
+      parts.push(`{ ${lines.join(' ')} y${l} = ${out}; }`);
+    }
+    const ys = Array.from({ length: W }, (_, l) => `y${l}`);
+    return `{ float ${ys.join(', ')}; ${parts.join(' ')} ${st('A.out', idx, vec ? `tcmi::f4{${ys.join(', ')}}` : 'y0')} }`;
+  };
   const first = `extern "C" __global__ void __launch_bounds__(256) __KERNEL__(const TcmiArgs A) {
   __shared__ ${T} part[4][64];
   const uint32_t n = ${n}u, inner = ${inner}u, splits = ${splits}u, chunk = ${chunk}u;
@@ -668,7 +698,7 @@ function colreduceKernels(op, outer, n, inner, tuning, producer) {
   const uint32_t k1 = min(n, k0 + chunk);
   ${T} acc = ${zero};
   if (j < inner) {
-${producer ? '' : '    const float* __restrict__ x = A.in[0] + (size_t)o * n * inner;\n'}#pragma unroll 8
+${producer ? '' : `    const float* __restrict__ x = A.in[${xin}] + (size_t)o * n * inner;\n`}#pragma unroll 8
     for (uint32_t k = k0 + g; k < k1; k += 4u) {
 ${producer ? formed : `      const ${T} v = ${ld('x', '(size_t)k * inner + j')};`}
       acc = ${combV('acc', 'v')};
@@ -681,7 +711,7 @@ ${producer ? formed : `      const ${T} v = ${ld('x', '(size_t)k * inner + j')};
     r = ${combV('r', 'part[1][lane]')};
     r = ${combV('r', 'part[2][lane]')};
     r = ${combV('r', 'part[3][lane]')};
-    if (splits == 1u) { ${st('A.out', '(size_t)o * inner + j', 'r')} }
+    if (splits == 1u) { ${store('(size_t)o * inner + j', 'r')} }
     else { ${st('A.ws', '((size_t)o * splits + s) * inner + j', 'r')} }
   }
 }
@@ -713,7 +743,7 @@ ${producer ? formed : `      const ${T} v = ${ld('x', '(size_t)k * inner + j')};
     ${T} r = part[0][c];
 #pragma unroll
     for (int q = 1; q < 16; ++q) r = ${combV('r', 'part[q][c]')};
-    ${st('A.out', '(size_t)o * inner + j', 'r')}
+    ${store('(size_t)o * inner + j', 'r')}
   }
 }
 `;
@@ -1688,4 +1718,4 @@ ${branches.join('\n')}
 module.exports = { elementwiseKernel, rowwiseKernel, colreduceKernels, gemmKernel, gemmTiling, attentionKernel, attentionGradKernel,
   gradPart, GRAD_PARTS, classifyGather, gatherStrides,
   literal, fnv, Emitter, ParamOverflow, WG, MAX_P, MAX_IN, MAX_BATCH, batchable, batchedKernel, batchFamily,
-  raggable, raggedFits, raggedKernel, textLds, RAGGED_MAX_BLOCKS, RAGGED_MAX_LDS };
+  raggable, raggedFits, raggedKernel, textLds, RAGGED_MAX_BLOCKS, RAGGED_MAX_LDS, COLRED_ONE_PASS };

@@ -206,7 +206,18 @@ function rowLayout(body, output) {
 }
 
 /** Kernels for one node. */
-function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs, composed, streamOut) {
+function lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs, composed, streamOut, colFold) {
+  if (colFold) {
+    // The chain run as its column sum's kernel: the sum formed as in its own launch, the
+    // chain's body applied to each sum (inputs at `pos`) at the store.
+    const red = graph.nodes[colFold.red];
+    const inShape = graph.nodes[red.inputs[0]].shape;
+    const axis = red.attrs.axis;
+    const chain = node.op === 'fused' ? { body: bodyOf(node), output: node.attrs.output } : oneOpBody(graph, node);
+    const c = cg.colreduceKernels(red.op, size(inShape.slice(0, axis)), inShape[axis], size(inShape.slice(axis + 1)),
+      (opts.tuning || {}).colreduce, null, { body: chain.body, output: chain.output, sumAt: colFold.pos });
+    return { kind: 'colreduce', kernels: c.launches, params: c.params, workspace: c.workspace, flops: 0 };
+  }
   if (composed) {
     // A launch forming values it reads (`composed`: its body with theirs inside, on the
     // buffers left to read): a rowwise kernel where the body reduces rows, with the
@@ -575,7 +586,35 @@ function perfPlan(graph, keep, rowFolding, absorbing, loadOps, noAbsorb) {
     allowed = whole;
   }
   if (loadOps) operandLoadOps(graph, keep, cons, slotOf, dead, folded, views);
-  return { aliases, folded, views, broadcasts, dead, rowFolds, absorbed };
+  // Column sums folded into their one reader: a sum over a non-last axis (a column sum,
+  // such as a bias gradient) that nothing keeps and whose only reader is a kept
+  // elementwise chain of its own size (the bias's update), every operand of which is a
+  // value of that size, launches nothing: the chain runs as the column-sum kernel, which
+  // forms each sum in the order of the sum's own launch and applies the chain's ops to
+  // it at the store, so the same bits as the two launches. Only sums that run in one pass
+  // (up to COLRED_ONE_PASS elements: config 1's biases): a larger one runs a second kernel
+  // combining its row chunks, and its update already shares a dispatch with the others
+  // (config 5's 31), so the fold would save no dispatch. Not where the sum forms its
+  // operand's producer, or the chain reads a broadcast, a view or an absorbed producer.
+  const colFolds = new Map();   // chain id -> { red: the sum's id, pos: its operand positions }
+  for (const r of rowFolding ? graph.nodes : []) {
+    if (r.op !== 'sum' || keep.has(r.id) || dead.has(r.id) || folded.has(r.id) || aliases.has(r.id) || absorbed.has(r.id)) continue;
+    if (size(graph.nodes[r.inputs[0]].shape.slice(r.attrs.axis + 1)) === 1) continue;
+    if (size(graph.nodes[r.inputs[0]].shape) > cg.COLRED_ONE_PASS) continue;
+    const users = Array.from(new Set(cons[r.id]));
+    if (users.length !== 1) continue;
+    const u = graph.nodes[users[0]];
+    if (!keep.has(u.id) || !isChain(u, size(r.shape)) || folded.has(u.id) || dead.has(u.id) || aliases.has(u.id)) continue;
+    // Elementwise ops of one size only (constants and their broadcasts aside, which the
+    // kernel writes as literals): every operand read at the element stored.
+    const bodyNodes = u.op === 'fused' ? u.attrs.body.nodes : [];
+    if (!bodyNodes.every((x) => x.op === 'const' || (x.op === 'broadcast' && bodyNodes[x.inputs[0]].op === 'const')
+      || ((x.op === 'input' || ELEMENTWISE_OPS.has(x.op)) && size(x.shape) === size(r.shape)))) continue;
+    if (rowFolds.has(u.id) || colFolds.has(u.id) || absorbed.has(u.id) || broadcasts.has(u.id) || views.has(u.id)) continue;
+    folded.add(r.id);
+    colFolds.set(u.id, { red: r.id, pos: u.inputs.map((i, k) => (i === r.id ? k : -1)).filter((k) => k >= 0) });
+  }
+  return { aliases, folded, views, broadcasts, dead, rowFolds, absorbed, colFolds };
 }
 
 /** The dense row-major view of an operand of `shape` ([..batch, R, C]). */
@@ -938,7 +977,8 @@ function lowerMI355X(graph, options) {
 function lowerOnce(graph, opts, noAbsorb, noForm) {
   const plan = opts.perf ? perfPlan(graph, new Set(opts.keep), opts.rowFolds !== false, opts.absorb === true && opts.rowFolds !== false,
     opts.loadOps !== false, noAbsorb)
-    : { aliases: new Map(), folded: new Set(), views: new Map(), broadcasts: new Map(), dead: new Set(), rowFolds: new Map(), absorbed: new Map() };
+    : { aliases: new Map(), folded: new Set(), views: new Map(), broadcasts: new Map(), dead: new Set(), rowFolds: new Map(), absorbed: new Map(),
+      colFolds: new Map() };
   const cache = new Map();
   const launches = [];
   let workspace = 0;
@@ -968,6 +1008,8 @@ function lowerOnce(graph, opts, noAbsorb, noForm) {
         f.ppos.forEach((pos, j) => { inputs[pos] = pins[j]; });
       }
     }
+    const colFold = plan.colFolds.get(node.id);
+    if (colFold) for (const pos of colFold.pos) inputs[pos] = resolve(graph.nodes[colFold.red].inputs[0]);
     for (const a of plan.absorbed.get(node.id) || []) {
       // An absorbed producer's operands (its own, with what it absorbed), in its positions.
       const pins = baseInputsOf(graph.nodes[a.prod]);
@@ -1000,7 +1042,7 @@ function lowerOnce(graph, opts, noAbsorb, noForm) {
   const baseBody = (id) => {
     if (!baseOf.has(id)) {
       const node = graph.nodes[id];
-      baseOf.set(id, plan.views.has(id) ? null : launchBase(graph, node, plan.broadcasts.get(id) || null,
+      baseOf.set(id, plan.views.has(id) || plan.colFolds.has(id) ? null : launchBase(graph, node, plan.broadcasts.get(id) || null,
         plan.rowFolds.get(id) || null, plan.absorbed.get(id) || null));
     }
     return baseOf.get(id);
@@ -1141,6 +1183,8 @@ function lowerOnce(graph, opts, noAbsorb, noForm) {
     };
     const rowKey = rowFold ? rowFold.map((f) => [f.pos, graph.nodes[f.red].op, graph.nodes[f.red].attrs,
       graph.nodes[graph.nodes[f.red].inputs[0]].shape, prodKey(f)]) : null;
+    const colFold = plan.colFolds.get(node.id) || null;
+    const colKey = colFold ? [colFold.pos, graph.nodes[colFold.red].attrs, graph.nodes[graph.nodes[colFold.red].inputs[0]].shape] : null;
     const absorbs = plan.absorbed.get(node.id) || null;
     const absorbSig = (a) => [a.pos, prodKey({ prod: a.prod, ppos: a.ppos, prodFolds: a.prodFolds }),
       a.nested ? a.nested.map(absorbSig) : null];
@@ -1158,11 +1202,11 @@ function lowerOnce(graph, opts, noAbsorb, noForm) {
     const peers = peersOf(node);
     const key = JSON.stringify([node.op, node.inputs.map((id) => graph.nodes[id].shape), node.attrs, node.shape,
       node.op === 'fused' ? opts.sabotage : null, opts.tuning || null, mmViews, foldKey, rowKey, lastReads, peers, absorbKey, formKey,
-      streamOut.get(node.id)]);
+      streamOut.get(node.id), colKey]);
     let k = cache.get(key);
     if (!k) {
       try {
-        k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs, comp, streamOut.get(node.id));
+        k = lowerNode(graph, node, opts, mmViews, folds, rowFold, lastReads, peers, absorbs, comp, streamOut.get(node.id), colFold);
       } catch (e) {
         if (e instanceof cg.ParamOverflow && comp) e.formed = comp.values;
         else if (e instanceof cg.ParamOverflow && absorbs) e.reader = node.id;
@@ -1180,6 +1224,8 @@ function lowerOnce(graph, opts, noAbsorb, noForm) {
     // forms in place of loading them, and the values it forms (each with its own folds and
     // absorbed producers, in the order the launch forms them).
     if (rowFold) launches[launches.length - 1].rowFolds = foldRecords(rowFold);
+    // A column sum folded into its reader: recorded as a fold over the sum's own axis.
+    if (colFold) launches[launches.length - 1].rowFolds = [{ reduction: colFold.red, pos: colFold.pos, columns: true }];
     if (absorbs) launches[launches.length - 1].absorbed = absorbs.map(absorbRecord);
     if (comp) {
       launches[launches.length - 1].formed = comp.values.map((v) => Object.assign({ value: v },

@@ -56,7 +56,8 @@ def _producer_body(graph, p):
 def fold_reductions(graph, node_id, folds):
     """A launch of the perf lowering that took row reductions into a chain, fused or a
     single op (its record's rowFolds: [{reduction, pos}], with producer and producerPos
-    where the reduction's operand is formed in the launch too): the chain as a fused node,
+    where the reduction's operand is formed in the launch too, or columns where the
+    reduction is a column sum taken into its one reader): the chain as a fused node,
     each body input at `pos` (the reduction's value) replaced by the reduction itself,
     applied to a new input a{pos[0]} — or to the producer's body on inputs
     a{producerPos[j]} — and the launch's operand node ids (the reduction's operand in
@@ -77,6 +78,14 @@ def fold_reductions(graph, node_id, folds):
         f = at.get(int(b["attrs"]["name"][1:])) if b["op"] == "input" else None
         if f is not None:
             red = graph["nodes"][f["reduction"]]
+            if f["reduction"] not in reduced and f.get("columns"):
+                # A column sum (a sum over a non-last axis) taken into its one reader: the
+                # sum itself, as the graph states it, on a new input of its operand's shape.
+                src = graph["nodes"][red["inputs"][0]]["shape"]
+                assert red["op"] == "sum" and int(np.prod(src[red["attrs"]["axis"] + 1:])) > 1
+                out.append({"op": "input", "inputs": [], "attrs": {"name": f"a{f['pos'][0]}", "shape": src}, "shape": src})
+                out.append({"op": red["op"], "inputs": [len(out) - 1], "attrs": red["attrs"], "shape": red["shape"]})
+                reduced[f["reduction"]] = len(out) - 1
             if f["reduction"] not in reduced:
                 # The operand as [outer, n] rows reduced along them (the reduced axis is the
                 # last non-trivial one), then the reduction's own shape.

@@ -87,7 +87,10 @@ def test_folded_row_reductions_are_the_chain_on_the_reduction(tool):
     rng = np.random.default_rng(3)
     producers = [k for k, fs in folds.items() if any("producer" in f for f in fs)]
     assert len(producers) >= 6
-    for k, fs in list(folds.items())[:12] + [(k, folds[k]) for k in producers[:12]]:
+    # Column sums taken into their one reader (a bias's update), at batch 1 one-pass sums.
+    columns = [k for k, fs in folds.items() if any(f.get("columns") for f in fs)]
+    assert len(columns) >= 6
+    for k, fs in list(folds.items())[:12] + [(k, folds[k]) for k in producers[:12] + columns[:8]]:
         node, ins = fold_reductions(graph, k, fs)
         # Positive operands keep the deviation chains' square roots real.
         ops = [rng.uniform(0.5, 2.0, size=interp.size(graph["nodes"][i]["shape"])).astype(np.float32) for i in ins]
